@@ -1,0 +1,145 @@
+/*
+ * specfold_amd — C ABI of the MI355X (gfx950) kernels for SpecFold's folded
+ * multi-branch verify step.
+ *
+ * Every entry point takes raw device pointers, plain int/float sizes and a HIP
+ * stream (passed as void*), launches asynchronously on that stream, allocates
+ * nothing, and returns an int status (SF_OK or one of the SF_ERR_* codes).
+ * Buffers are caller-owned; scratch comes in as a workspace argument whose size
+ * the matching *_workspace_bytes() function returns.
+ *
+ * Layout conventions (one verify step of B1 branches x N block positions,
+ * BN = B1*N "flat rows", flat row r = b*N + n):
+ *   hidden   bf16 [BN, D]                 layer input, row-major
+ *   q_buf    bf16 [BN+1, H*hd]            roped q per flat row (row BN = trash)
+ *   kv_buf   bf16 [BN+1, 2*Hkv*hd]        roped k heads, then v heads
+ *   o32      fp32 [BN, H*hd]   o_bf bf16 [BN, H*hd]   attention output
+ *   m_tab, z_tab fp32 [BN, H]             softmax row max and sum exp(s - m)
+ *   rows     int32 [bucket]               ascending flat ids of recomputed rows
+ *   prefix K/V cache: element (head h, token t, dim d) lives at
+ *     base + page_table[t / page_size] * page_stride + h * head_stride
+ *          + (t % page_size) * hd + d
+ *   or, with page_table == NULL, at base + h * head_stride + t * hd + d
+ *   (the reference's contiguous [1, Hkv, P, hd] cache is head_stride = P*hd).
+ *
+ * Reference = chungen04/specfold; paths are relative to its root.
+ */
+#ifndef SPECFOLD_AMD_H
+#define SPECFOLD_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SF_OK 0
+#define SF_ERR_SHAPE 1     /* a size outside what the kernels support */
+#define SF_ERR_ARG 2       /* a required pointer is NULL or a value is invalid */
+#define SF_ERR_WORKSPACE 3 /* workspace smaller than *_workspace_bytes() */
+#define SF_ERR_HIP 4       /* a HIP launch failed */
+
+/* Gate precision modes for sf_fold_gate. */
+#define SF_GATE_MODEL_DTYPE 0 /* norms rounded to bf16 as the PyTorch reference
+                                 does (specfold/generate/fastdllm_v2_folded.py:139-141) */
+#define SF_GATE_FP32_SQUARED 1 /* dsq > delta^2 * psq in fp32, as the Triton gate
+                                  (specfold/generate/triton_kernels.py:227-230) */
+#define SF_GATE_ALL 2          /* every row recomputed: the dense block forward
+                                  (specfold/generate/fastdllm_v2_generation.py:151-186) */
+
+const char* sf_status_string(int status);
+int sf_abi_version(void);
+
+/*
+ * (1) Fold gate + deterministic compaction + src resolve + input RMSNorm.
+ * Replaces residual_delta_gate_kernel and src_resolve_kernel
+ * (specfold/generate/triton_kernels.py:199-239 and :18-26), i.e. the per-branch
+ * gate of the reference (specfold/generate/fastdllm_v2_folded.py:136-144) and
+ * the compaction it feeds (:141 nonzero; Triton launch :306-310).
+ *
+ * rec[r]    = 1 if flat row r is recomputed (branch 0 always), else 0
+ * f[r]      = rec ? b : par[b]
+ * src[r]    = nearest recomputing ancestor branch of (b, n) (fixed point of f)
+ * rows      = ascending flat ids of recomputed rows, slots >= count hold BN
+ * count[0]  = number of recomputed rows (may exceed bucket: overflow)
+ * seg[b*N+k], segcnt[b] = the k-th recomputed flat row of branch b, and how many
+ * rstd[r]   = 1 / sqrt(mean(x^2) + eps)
+ * xn[r, :]  = bf16(ln_w * bf16(x * rstd)) for recomputed rows (the
+ *             Qwen2RMSNorm output the QKV projection consumes)
+ * Limits: B1*N <= 1024, B1 <= 64, D % 8 == 0, D <= 8192, 1 <= bucket <= B1*N.
+ */
+int sf_fold_gate(const uint16_t* hidden, const int32_t* par, const uint16_t* ln_w, int B1, int N,
+                 int D, int bucket, float delta, float eps, int gate_mode, int8_t* rec, int32_t* f,
+                 int32_t* src, int32_t* rows, int32_t* count, int32_t* seg, int32_t* segcnt,
+                 float* rstd, uint16_t* xn, void* stream);
+
+/*
+ * (2) QKV projection (bf16 MFMA, fp32 accumulate) + bias + RoPE + scatter for
+ * the compacted rows.  Replaces fused_ln_qkv_rope_scatter_kernel
+ * (specfold/generate/triton_kernels.py:29-87), i.e. the reference's
+ * q/k/v_proj + rotate_half RoPE on recomputed rows
+ * (specfold/generate/fastdllm_v2_folded.py:151-161).  The RMSNorm is applied by
+ * sf_fold_gate (xn).  w_qkv = cat(Wq, Wk, Wv) [(H+2Hkv)*hd, D]
+ * (:77-87 packing); b_qkv may be NULL (NLD: no bias).  cos/sin bf16 [N, hd].
+ * q_scale (optional, fp32 [N]) multiplies roped q by bf16(q_scale[n]) — the
+ * llama-4 attention scale of specfold/generate/nld_folded.py:37-53, 175-176.
+ * Limits: hd == 128, D % 64 == 0, bucket <= 1024.
+ */
+size_t sf_qkv_workspace_bytes(int bucket, int D, int n_qkv);
+int sf_qkv_rope(const uint16_t* xn, const int32_t* rows, const int32_t* count, int bucket, int BN,
+                const uint16_t* w_qkv, const uint16_t* b_qkv, const uint16_t* cos_tab,
+                const uint16_t* sin_tab, const float* q_scale, int N, int D, int H, int Hkv, int hd,
+                uint16_t* q_buf, uint16_t* kv_buf, void* workspace, size_t workspace_bytes,
+                void* stream);
+
+/*
+ * (3) Attention of the recomputed rows over [shared prefix ; own branch block],
+ * keeping the softmax state.  Replaces specfold_flash_attn_gqa_kernel
+ * (specfold/generate/triton_kernels.py:301-361), i.e. the reference's fp32
+ * attention of recomputed rows (specfold/generate/fastdllm_v2_folded.py:164-181).
+ * Block key j of branch b is kv_buf row src[b*N+j]*N + j.  No mask.
+ * Writes o32, o_bf, m_tab, z_tab for the rows listed in rows[0:min(count,bucket)].
+ * Limits: hd == 128, H % Hkv == 0, N <= 64, H/Hkv <= 8.
+ */
+size_t sf_attn_workspace_bytes(int bucket, int H, int P);
+int sf_attn_prefix_block(const uint16_t* q_buf, const uint16_t* kv_buf, const uint16_t* prefix_k,
+                         const uint16_t* prefix_v, const int32_t* page_table, int P, int page_size,
+                         long long page_stride, long long head_stride, const int32_t* src,
+                         const int32_t* rows, const int32_t* count, int bucket, int B1, int N,
+                         int H, int Hkv, int hd, float scaling, float* o32, uint16_t* o_bf,
+                         float* m_tab, float* z_tab, void* workspace, size_t workspace_bytes,
+                         void* stream);
+
+/*
+ * (4) Chain correction of folded rows: start from the state of the nearest
+ * recomputing ancestor and apply the exact rank-|R| softmax update for every
+ * key changed along the ancestor chain.  Replaces
+ * specfold_chain_correction_gqa_kernel (specfold/generate/triton_kernels.py:364-429),
+ * the order-free form of the reference's one-hop correction
+ * (specfold/generate/fastdllm_v2_folded.py:183-204).
+ * Reads o32/m_tab/z_tab of src rows; writes o32, o_bf, m_tab, z_tab of folded rows.
+ * Limits: hd == 128, H/Hkv <= 8, B1*N <= 1024.
+ */
+int sf_chain_correct(const uint16_t* q_buf, const uint16_t* kv_buf, const int32_t* src,
+                     const int32_t* par, const int8_t* rec, const int32_t* seg,
+                     const int32_t* segcnt, int B1, int N, int H, int Hkv, int hd, float scaling,
+                     float* o32, uint16_t* o_bf, float* m_tab, float* z_tab, void* stream);
+
+/*
+ * (5) In-place KV-cache append: copy the k and v heads of n_tok consecutive
+ * kv_buf rows (starting at row0) to cache positions start_pos .. start_pos+n_tok-1.
+ * Replaces the torch.cat growth of the prefix cache inside the block-commit
+ * forward (specfold/model_cache/nemotron_labs_diffusion/modeling_ministral.py:154-162
+ * via DynamicCache.update; called from specfold/generate/fastdllm_v2_generation.py:557-575).
+ * Limits: hd == 128.
+ */
+int sf_kv_append(const uint16_t* kv_buf, int row0, int n_tok, int Hkv, int hd, uint16_t* k_cache,
+                 uint16_t* v_cache, const int32_t* page_table, int page_size,
+                 long long page_stride, long long head_stride, int start_pos, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPECFOLD_AMD_H */

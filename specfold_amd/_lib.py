@@ -1,0 +1,225 @@
+"""ctypes binding of the gfx950 C-ABI library (include/specfold_amd.h).
+
+The library is built in-tree by ``python -m specfold_amd.build``.  There is no
+fallback: if the shared library is missing, every call raises
+``SpecFoldLibraryMissing``.  Wrappers validate dtype, device, contiguity,
+alignment and shape of every tensor before launching, then pass raw device
+pointers and the current HIP stream.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+from typing import Optional
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libspecfold_amd.so"
+
+SF_OK = 0
+SF_GATE_MODEL_DTYPE = 0
+SF_GATE_FP32_SQUARED = 1
+SF_GATE_ALL = 2
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_f = ctypes.c_float
+_ll = ctypes.c_longlong
+_sz = ctypes.c_size_t
+
+# name -> (restype, argtypes); mirrors include/specfold_amd.h
+SIGNATURES = {
+    "sf_status_string": (ctypes.c_char_p, [_i]),
+    "sf_abi_version": (_i, []),
+    "sf_fold_gate": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _f, _f, _i,
+                          _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "sf_qkv_workspace_bytes": (_sz, [_i, _i, _i]),
+    "sf_qkv_rope": (_i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp,
+                         _i, _i, _i, _i, _i, _vp, _vp, _vp, _sz, _vp]),
+    "sf_attn_workspace_bytes": (_sz, [_i, _i, _i]),
+    "sf_attn_prefix_block": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _ll, _ll, _vp, _vp, _vp,
+                                  _i, _i, _i, _i, _i, _i, _f, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "sf_chain_correct": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f,
+                              _vp, _vp, _vp, _vp, _vp]),
+    "sf_kv_append": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp, _i, _ll, _ll, _i, _vp]),
+}
+
+
+class SpecFoldLibraryMissing(RuntimeError):
+    pass
+
+
+class SpecFoldKernelError(RuntimeError):
+    pass
+
+
+_LIB: Optional[ctypes.CDLL] = None
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and type the shared library; raise if it is not built."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not LIB_PATH.exists():
+        raise SpecFoldLibraryMissing(
+            f"{LIB_PATH} is not built; run `python -m specfold_amd.build` "
+            "(the HIP path has no CPU fallback)")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _LIB = lib
+    return lib
+
+
+def _check(status: int, name: str) -> None:
+    if status != SF_OK:
+        msg = load().sf_status_string(status).decode()
+        raise SpecFoldKernelError(f"{name} returned {status}: {msg}")
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(stream=None):
+    s = torch.cuda.current_stream() if stream is None else stream
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def _need(t: torch.Tensor, name: str, dtype: torch.dtype, numel: Optional[int] = None,
+          min_numel: Optional[int] = None, align: int = 16) -> None:
+    if t is None:
+        raise ValueError(f"{name} is required")
+    if t.dtype != dtype:
+        raise TypeError(f"{name}: expected {dtype}, got {t.dtype}")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name}: expected a GPU tensor, got {t.device}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: must be contiguous")
+    if t.data_ptr() % align:
+        raise ValueError(f"{name}: data pointer must be {align}-byte aligned")
+    if numel is not None and t.numel() != numel:
+        raise ValueError(f"{name}: expected {numel} elements, got {t.numel()}")
+    if min_numel is not None and t.numel() < min_numel:
+        raise ValueError(f"{name}: expected at least {min_numel} elements, got {t.numel()}")
+
+
+# ---------------------------------------------------------------------------
+# typed wrappers
+# ---------------------------------------------------------------------------
+
+def fold_gate(hidden, par, ln_w, B1, N, bucket, delta, eps, gate_mode,
+              rec, f, src, rows, count, seg, segcnt, rstd, xn, stream=None) -> None:
+    D = hidden.shape[-1]
+    BN = B1 * N
+    _need(hidden, "hidden", torch.bfloat16, numel=BN * D)
+    _need(par, "par", torch.int32, numel=B1, align=4)
+    _need(ln_w, "ln_w", torch.bfloat16, numel=D)
+    _need(rec, "rec", torch.int8, min_numel=BN, align=4)
+    for nm, t, n in (("f", f, BN), ("src", src, BN), ("rows", rows, bucket), ("count", count, 1),
+                     ("seg", seg, BN), ("segcnt", segcnt, B1)):
+        _need(t, nm, torch.int32, min_numel=n, align=4)
+    _need(rstd, "rstd", torch.float32, min_numel=BN, align=4)
+    _need(xn, "xn", torch.bfloat16, min_numel=BN * D)
+    st = load().sf_fold_gate(_ptr(hidden), _ptr(par), _ptr(ln_w), B1, N, D, bucket, float(delta),
+                             float(eps), int(gate_mode), _ptr(rec), _ptr(f), _ptr(src), _ptr(rows),
+                             _ptr(count), _ptr(seg), _ptr(segcnt), _ptr(rstd), _ptr(xn),
+                             _stream(stream))
+    _check(st, "sf_fold_gate")
+
+
+def qkv_workspace_bytes(bucket: int, D: int, n_qkv: int) -> int:
+    return int(load().sf_qkv_workspace_bytes(bucket, D, n_qkv))
+
+
+def qkv_rope(xn, rows, count, bucket, BN, w_qkv, b_qkv, cos, sin, q_scale, N, D, H, Hkv, hd,
+             q_buf, kv_buf, workspace, stream=None) -> None:
+    nq = (H + 2 * Hkv) * hd
+    _need(xn, "xn", torch.bfloat16, min_numel=BN * D)
+    _need(rows, "rows", torch.int32, min_numel=bucket, align=4)
+    _need(count, "count", torch.int32, min_numel=1, align=4)
+    _need(w_qkv, "w_qkv", torch.bfloat16, numel=nq * D)
+    if b_qkv is not None:
+        _need(b_qkv, "b_qkv", torch.bfloat16, numel=nq, align=4)
+    _need(cos, "cos", torch.bfloat16, numel=N * hd, align=4)
+    _need(sin, "sin", torch.bfloat16, numel=N * hd, align=4)
+    if q_scale is not None:
+        _need(q_scale, "q_scale", torch.float32, numel=N, align=4)
+    _need(q_buf, "q_buf", torch.bfloat16, min_numel=(BN + 1) * H * hd)
+    _need(kv_buf, "kv_buf", torch.bfloat16, min_numel=(BN + 1) * 2 * Hkv * hd)
+    _need(workspace, "workspace", torch.uint8, min_numel=qkv_workspace_bytes(bucket, D, nq),
+          align=256)
+    st = load().sf_qkv_rope(_ptr(xn), _ptr(rows), _ptr(count), bucket, BN, _ptr(w_qkv),
+                            _ptr(b_qkv), _ptr(cos), _ptr(sin), _ptr(q_scale), N, D, H, Hkv, hd,
+                            _ptr(q_buf), _ptr(kv_buf), _ptr(workspace), workspace.numel(),
+                            _stream(stream))
+    _check(st, "sf_qkv_rope")
+
+
+def attn_workspace_bytes(bucket: int, H: int, P: int) -> int:
+    return int(load().sf_attn_workspace_bytes(bucket, H, P))
+
+
+def attn_prefix_block(q_buf, kv_buf, prefix_k, prefix_v, page_table, P, page_size, page_stride,
+                      head_stride, src, rows, count, bucket, B1, N, H, Hkv, hd, scaling,
+                      o32, o_bf, m_tab, z_tab, workspace, stream=None) -> None:
+    BN = B1 * N
+    _need(q_buf, "q_buf", torch.bfloat16, min_numel=(BN + 1) * H * hd)
+    _need(kv_buf, "kv_buf", torch.bfloat16, min_numel=(BN + 1) * 2 * Hkv * hd)
+    if P > 0:
+        _need(prefix_k, "prefix_k", torch.bfloat16)
+        _need(prefix_v, "prefix_v", torch.bfloat16)
+        if page_table is not None:
+            _need(page_table, "page_table", torch.int32, min_numel=(P + page_size - 1) // page_size,
+                  align=4)
+    _need(src, "src", torch.int32, min_numel=BN, align=4)
+    _need(rows, "rows", torch.int32, min_numel=bucket, align=4)
+    _need(count, "count", torch.int32, min_numel=1, align=4)
+    _need(o32, "o32", torch.float32, min_numel=BN * H * hd)
+    _need(o_bf, "o_bf", torch.bfloat16, min_numel=BN * H * hd)
+    _need(m_tab, "m_tab", torch.float32, min_numel=BN * H, align=4)
+    _need(z_tab, "z_tab", torch.float32, min_numel=BN * H, align=4)
+    _need(workspace, "workspace", torch.uint8, min_numel=attn_workspace_bytes(bucket, H, P),
+          align=256)
+    st = load().sf_attn_prefix_block(
+        _ptr(q_buf), _ptr(kv_buf), _ptr(prefix_k) if P > 0 else None,
+        _ptr(prefix_v) if P > 0 else None, _ptr(page_table) if P > 0 else None, P,
+        page_size, page_stride, head_stride, _ptr(src), _ptr(rows), _ptr(count), bucket, B1, N, H,
+        Hkv, hd, float(scaling), _ptr(o32), _ptr(o_bf), _ptr(m_tab), _ptr(z_tab), _ptr(workspace),
+        workspace.numel(), _stream(stream))
+    _check(st, "sf_attn_prefix_block")
+
+
+def chain_correct(q_buf, kv_buf, src, par, rec, seg, segcnt, B1, N, H, Hkv, hd, scaling,
+                  o32, o_bf, m_tab, z_tab, stream=None) -> None:
+    BN = B1 * N
+    _need(q_buf, "q_buf", torch.bfloat16, min_numel=(BN + 1) * H * hd)
+    _need(kv_buf, "kv_buf", torch.bfloat16, min_numel=(BN + 1) * 2 * Hkv * hd)
+    for nm, t, n in (("src", src, BN), ("par", par, B1), ("seg", seg, BN), ("segcnt", segcnt, B1)):
+        _need(t, nm, torch.int32, min_numel=n, align=4)
+    _need(rec, "rec", torch.int8, min_numel=BN, align=4)
+    _need(o32, "o32", torch.float32, min_numel=BN * H * hd)
+    _need(o_bf, "o_bf", torch.bfloat16, min_numel=BN * H * hd)
+    _need(m_tab, "m_tab", torch.float32, min_numel=BN * H, align=4)
+    _need(z_tab, "z_tab", torch.float32, min_numel=BN * H, align=4)
+    st = load().sf_chain_correct(_ptr(q_buf), _ptr(kv_buf), _ptr(src), _ptr(par), _ptr(rec),
+                                 _ptr(seg), _ptr(segcnt), B1, N, H, Hkv, hd, float(scaling),
+                                 _ptr(o32), _ptr(o_bf), _ptr(m_tab), _ptr(z_tab), _stream(stream))
+    _check(st, "sf_chain_correct")
+
+
+def kv_append(kv_buf, row0, n_tok, Hkv, hd, k_cache, v_cache, page_table, page_size,
+              page_stride, head_stride, start_pos, stream=None) -> None:
+    _need(kv_buf, "kv_buf", torch.bfloat16, min_numel=(row0 + n_tok) * 2 * Hkv * hd)
+    _need(k_cache, "k_cache", torch.bfloat16)
+    _need(v_cache, "v_cache", torch.bfloat16)
+    if page_table is not None:
+        _need(page_table, "page_table", torch.int32, align=4)
+    st = load().sf_kv_append(_ptr(kv_buf), row0, n_tok, Hkv, hd, _ptr(k_cache), _ptr(v_cache),
+                             _ptr(page_table), page_size, page_stride, head_stride, start_pos,
+                             _stream(stream))
+    _check(st, "sf_kv_append")

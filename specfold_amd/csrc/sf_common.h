@@ -1,0 +1,76 @@
+// Shared device helpers for the SpecFold gfx950 kernels.
+//
+// Storage type for bf16 is uint16_t (raw bits); arithmetic is done in fp32 and
+// rounded back with round-to-nearest-even, which is what torch's bf16 ops do.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "specfold_amd.h"
+
+#define SF_DEV __device__ __forceinline__
+
+typedef __bf16 sf_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float sf_f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t sf_u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t sf_u32x2 __attribute__((ext_vector_type(2)));
+
+SF_DEV float sf_bf2f(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
+
+// fp32 -> bf16, round to nearest even; NaN stays a quiet NaN.
+SF_DEV uint16_t sf_f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// Round an fp32 value through bf16 (the value a bf16 tensor op would store).
+SF_DEV float sf_rbf(float f) { return sf_bf2f(sf_f2bf(f)); }
+
+// Unpack 8 bf16 held in a 16-byte word.
+SF_DEV void sf_unpack8(const sf_u32x4 w, float out[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = __uint_as_float(w[i] << 16);
+    out[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+
+SF_DEV uint32_t sf_pack2(float lo, float hi) {
+  return (uint32_t)sf_f2bf(lo) | ((uint32_t)sf_f2bf(hi) << 16);
+}
+
+// Full 64-lane butterfly reductions (result valid in every lane).
+SF_DEV float sf_wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+SF_DEV float sf_wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Reinterpret 8 packed bf16 (u32x4) as the MFMA operand vector.
+SF_DEV sf_bf16x8 sf_as_bf16x8(const sf_u32x4 w) {
+  union {
+    sf_u32x4 u;
+    sf_bf16x8 b;
+  } c;
+  c.u = w;
+  return c.b;
+}
+
+SF_DEV sf_f32x4 sf_mfma16x16x32(const sf_bf16x8 a, const sf_bf16x8 b, sf_f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Launch-error check shared by every entry point.
+static inline int sf_launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? SF_OK : SF_ERR_HIP;
+}

@@ -1,0 +1,212 @@
+// Fold gate: per-row relative-residual test, deterministic compaction of the
+// recomputed rows, src resolution and the input RMSNorm of recomputed rows.
+//
+// Reference semantics: specfold/generate/fastdllm_v2_folded.py:136-152
+// (gate against the subset-parent, RMSNorm of recomputed rows) and the Triton
+// gate/src kernels specfold/generate/triton_kernels.py:18-26, 199-239.
+// Unlike the Triton gate (atomic slot order), rows[] is in ascending flat-row
+// order, which equals the concatenation of the reference's per-branch
+// nonzero() lists.
+#include "sf_common.h"
+
+namespace {
+
+constexpr int kGateWaves = 4;  // one wave per flat row, 4 rows per workgroup
+constexpr int kMaxVecPerLane = 16;  // 16 x 8 bf16 x 64 lanes = 8192 columns
+
+// One wave per flat row r = b*N + n: three fp32 sums over D (x^2, residual^2,
+// parent^2), the gate decision, rstd, and the normalized row for recomputed rows.
+template <int VPL>
+__global__ __launch_bounds__(256) void sf_gate_rows_kernel(
+    const uint16_t* __restrict__ hidden, const int32_t* __restrict__ par,
+    const uint16_t* __restrict__ ln_w, int B1, int N, int D, float delta, float eps, int mode,
+    int8_t* __restrict__ rec, float* __restrict__ rstd, uint16_t* __restrict__ xn) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * kGateWaves + (threadIdx.x >> 6);
+  const int BN = B1 * N;
+  if (r >= BN) return;
+  const int b = r / N;
+  const int n = r - b * N;
+  int p = par[b];
+  p = p < 0 ? 0 : (p >= B1 ? B1 - 1 : p);
+  const bool draft = b > 0 && mode != SF_GATE_ALL;
+
+  const int nvec = D >> 3;
+  const sf_u32x4* xrow = reinterpret_cast<const sf_u32x4*>(hidden + (size_t)r * D);
+  const sf_u32x4* prow = reinterpret_cast<const sf_u32x4*>(hidden + (size_t)(p * N + n) * D);
+
+  sf_u32x4 xv[VPL];
+  float ss = 0.f, ds = 0.f, ps = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int idx = lane + i * 64;
+    if (idx < nvec) {
+      xv[i] = xrow[idx];
+      float xf[8];
+      sf_unpack8(xv[i], xf);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss = fmaf(xf[j], xf[j], ss);
+      if (draft) {
+        float pf[8];
+        sf_unpack8(prow[idx], pf);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          float d = xf[j] - pf[j];
+          if (mode == SF_GATE_MODEL_DTYPE) d = sf_rbf(d);  // x - x_par is a bf16 tensor op
+          ds = fmaf(d, d, ds);
+          ps = fmaf(pf[j], pf[j], ps);
+        }
+      }
+    }
+  }
+  ss = sf_wave_sum(ss);
+  ds = sf_wave_sum(ds);
+  ps = sf_wave_sum(ps);
+
+  // Qwen2RMSNorm: x * rsqrt(mean(x^2) + eps) in fp32 (torch CPU rsqrt is 1/sqrt).
+  const float inv = 1.0f / sqrtf(ss / (float)D + eps);
+  bool is_rec = true;
+  if (draft) {
+    if (mode == SF_GATE_MODEL_DTYPE) {
+      // bf16 norms: dn = bf16(|x - xp|), thr = bf16(delta * bf16(|xp|)), dn > thr.
+      const float dn = sf_rbf(sqrtf(ds));
+      const float pn = sf_rbf(sqrtf(ps));
+      const float thr = sf_rbf(delta * pn);
+      is_rec = dn > thr;
+    } else {
+      is_rec = ds > (delta * delta) * ps;
+    }
+  }
+  if (lane == 0) {
+    rec[r] = is_rec ? 1 : 0;
+    rstd[r] = inv;
+  }
+  if (!is_rec) return;
+
+  // normalized row: bf16(w * bf16(x * rstd)), as Qwen2RMSNorm in bf16.
+  const sf_u32x4* wv = reinterpret_cast<const sf_u32x4*>(ln_w);
+  sf_u32x4* out = reinterpret_cast<sf_u32x4*>(xn + (size_t)r * D);
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int idx = lane + i * 64;
+    if (idx < nvec) {
+      float xf[8], wf[8];
+      sf_unpack8(xv[i], xf);
+      sf_unpack8(wv[idx], wf);
+      sf_u32x4 o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float a = sf_rbf(wf[2 * j] * sf_rbf(xf[2 * j] * inv));
+        const float c = sf_rbf(wf[2 * j + 1] * sf_rbf(xf[2 * j + 1] * inv));
+        o[j] = sf_pack2(a, c);
+      }
+      out[idx] = o;
+    }
+  }
+}
+
+// One workgroup of 1024 threads, thread t = flat row t: ballot/popcount scan of
+// the rec flags, ascending compaction, per-branch segments and the src chase.
+__global__ __launch_bounds__(1024) void sf_gate_compact_kernel(
+    const int8_t* __restrict__ rec, const int32_t* __restrict__ par, int B1, int N, int bucket,
+    int32_t* __restrict__ f, int32_t* __restrict__ src, int32_t* __restrict__ rows,
+    int32_t* __restrict__ count, int32_t* __restrict__ seg, int32_t* __restrict__ segcnt) {
+  __shared__ int s_f[1024];
+  __shared__ int s_slot[1024];
+  __shared__ int s_wave_tot[16];
+  const int BN = B1 * N;
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int w = t >> 6;
+  const int flag = (t < BN) ? (rec[t] != 0) : 0;
+  const unsigned long long bal = __ballot(flag);
+  const unsigned long long below = (lane == 0) ? 0ull : (bal & ((~0ull) >> (64 - lane)));
+  const int pre = __popcll(below);
+  if (lane == 0) s_wave_tot[w] = __popcll(bal);
+  __syncthreads();
+  int base = 0, total = 0;
+  for (int i = 0; i < 16; ++i) {
+    const int v = s_wave_tot[i];
+    base += (i < w) ? v : 0;
+    total += v;
+  }
+  const int slot = base + pre;  // exclusive prefix count of recomputed rows before t
+  const int b = (t < BN) ? t / N : 0;
+  const int n = (t < BN) ? t - b * N : 0;
+  if (t < BN) {
+    int p = par[b];
+    p = p < 0 ? 0 : (p >= B1 ? B1 - 1 : p);
+    const int fv = flag ? b : p;
+    s_f[t] = fv;
+    s_slot[t] = slot;
+    f[t] = fv;
+    if (flag && slot < bucket) rows[slot] = t;
+  }
+  for (int s = t; s < bucket; s += blockDim.x)
+    if (s >= total) rows[s] = BN;
+  __syncthreads();
+  if (t < BN) {
+    const int first = s_slot[b * N];
+    if (flag) seg[b * N + (slot - first)] = t;
+    if (n == 0) segcnt[b] = ((b + 1 < B1) ? s_slot[(b + 1) * N] : total) - first;
+    // Chains strictly shorten towards branch 0, so B1 hops reach the fixed point.
+    int s = s_f[t];
+    for (int hop = 0; hop < B1; ++hop) s = s_f[s * N + n];
+    src[t] = s;
+  }
+  if (t == 0) *count = total;
+}
+
+template <int VPL>
+void launch_rows(const uint16_t* hidden, const int32_t* par, const uint16_t* ln_w, int B1, int N,
+                 int D, float delta, float eps, int mode, int8_t* rec, float* rstd, uint16_t* xn,
+                 hipStream_t st) {
+  const int BN = B1 * N;
+  dim3 grid((BN + kGateWaves - 1) / kGateWaves);
+  hipLaunchKernelGGL(sf_gate_rows_kernel<VPL>, grid, dim3(256), 0, st, hidden, par, ln_w, B1, N, D,
+                     delta, eps, mode, rec, rstd, xn);
+}
+
+}  // namespace
+
+extern "C" const char* sf_status_string(int status) {
+  switch (status) {
+    case SF_OK: return "ok";
+    case SF_ERR_SHAPE: return "shape outside kernel limits";
+    case SF_ERR_ARG: return "invalid argument";
+    case SF_ERR_WORKSPACE: return "workspace too small";
+    case SF_ERR_HIP: return "HIP launch failed";
+    default: return "unknown status";
+  }
+}
+
+extern "C" int sf_abi_version(void) { return 1; }
+
+extern "C" int sf_fold_gate(const uint16_t* hidden, const int32_t* par, const uint16_t* ln_w,
+                            int B1, int N, int D, int bucket, float delta, float eps, int gate_mode,
+                            int8_t* rec, int32_t* f, int32_t* src, int32_t* rows, int32_t* count,
+                            int32_t* seg, int32_t* segcnt, float* rstd, uint16_t* xn,
+                            void* stream) {
+  if (!hidden || !par || !ln_w || !rec || !f || !src || !rows || !count || !seg || !segcnt ||
+      !rstd || !xn)
+    return SF_ERR_ARG;
+  if (gate_mode != SF_GATE_MODEL_DTYPE && gate_mode != SF_GATE_FP32_SQUARED &&
+      gate_mode != SF_GATE_ALL)
+    return SF_ERR_ARG;
+  if (B1 < 1 || B1 > 64 || N < 1 || B1 * N > 1024) return SF_ERR_SHAPE;
+  if (D < 8 || D % 8 != 0 || D > 8 * 64 * kMaxVecPerLane) return SF_ERR_SHAPE;
+  if (bucket < 1 || bucket > B1 * N) return SF_ERR_SHAPE;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int vpl = (D / 8 + 63) / 64;
+  if (vpl <= 4)
+    launch_rows<4>(hidden, par, ln_w, B1, N, D, delta, eps, gate_mode, rec, rstd, xn, st);
+  else if (vpl <= 8)
+    launch_rows<8>(hidden, par, ln_w, B1, N, D, delta, eps, gate_mode, rec, rstd, xn, st);
+  else if (vpl <= 12)
+    launch_rows<12>(hidden, par, ln_w, B1, N, D, delta, eps, gate_mode, rec, rstd, xn, st);
+  else
+    launch_rows<16>(hidden, par, ln_w, B1, N, D, delta, eps, gate_mode, rec, rstd, xn, st);
+  hipLaunchKernelGGL(sf_gate_compact_kernel, dim3(1), dim3(1024), 0, st, rec, par, B1, N, bucket,
+                     f, src, rows, count, seg, segcnt);
+  return sf_launch_status();
+}

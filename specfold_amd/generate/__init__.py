@@ -1,0 +1,14 @@
+"""Generator and executor classes with the reference's API (specfold/generate/)."""
+
+from specfold_amd.generate.fastdllm_model_executor import ByteTokenizer, FastDLLMModelExecutor
+from specfold_amd.generate.fastdllm_v2_folded import (SpecFoldHIPFastDLLMV2Generation,
+                                                      SpecFoldTritonFastDLLMV2Generation)
+from specfold_amd.generate.fastdllm_v2_generation import FastDLLMV2SpeculativeGeneration
+
+__all__ = [
+    "ByteTokenizer",
+    "FastDLLMModelExecutor",
+    "FastDLLMV2SpeculativeGeneration",
+    "SpecFoldHIPFastDLLMV2Generation",
+    "SpecFoldTritonFastDLLMV2Generation",
+]

@@ -1,0 +1,86 @@
+"""SpecFold for Fast-dLLM v2 on MI355X: the B+1-branch folded verify step.
+
+``SpecFoldHIPFastDLLMV2Generation`` is the drop-in for the reference's fused
+class ``SpecFoldTritonFastDLLMV2Generation``
+(specfold/generate/fastdllm_v2_folded.py:226-370): same constructor
+(``delta``, ``fold_bucket``), same ``_batched_block_forward(batched_input,
+past_key_values) -> shifted logits [B1, N, V]`` seam, same ``fold_ratio``
+bookkeeping and the same bucket-overflow behaviour (warn, recompute with a
+full bucket — here on the GPU, not through a PyTorch prototype).  The step
+runs the hand-written gfx950 kernels of ``specfold_amd.engine``; there is no
+CPU or PyTorch fallback.
+"""
+
+from __future__ import annotations
+
+import logging
+from typing import List, Optional, Tuple
+
+import torch
+
+from specfold_amd import _lib
+from specfold_amd.engine import FoldedVerifyEngine, StepStats, build_parent_map
+from specfold_amd.generate.fastdllm_v2_generation import FastDLLMV2SpeculativeGeneration
+
+logger = logging.getLogger(__name__)
+
+
+class SpecFoldHIPFastDLLMV2Generation(FastDLLMV2SpeculativeGeneration):
+    """Folded verify step: relative-residual gate per (branch, position) against
+    the subset-parent, QKV/attention/FFN only on recomputed rows, exact chain
+    correction of the attention state of folded rows, residual kept per row."""
+
+    def __init__(self, *args, delta: float = 0.1, fold_bucket: Optional[int] = None,
+                 gate_mode: int = _lib.SF_GATE_MODEL_DTYPE, **kwargs):
+        super().__init__(*args, **kwargs)
+        self.delta = float(delta)
+        self.fold_bucket = None if fold_bucket is None else int(fold_bucket)
+        self.gate_mode = gate_mode
+        self._engine: Optional[FoldedVerifyEngine] = None
+        self._fold_draft_positions = 0
+        self._fold_draft_recomputed = 0
+        self.last_stats: Optional[StepStats] = None
+
+    @property
+    def fold_ratio(self) -> float:
+        tot = self._fold_draft_positions
+        return 1.0 - self._fold_draft_recomputed / tot if tot else float("nan")
+
+    @staticmethod
+    def _build_parent_map(batched_input: torch.Tensor) -> Tuple[List[Optional[int]], List[int]]:
+        return build_parent_map(batched_input)
+
+    def _pack_layer_weights(self, layers=None) -> None:
+        """Pack per-layer QKV weights once (inside the engine)."""
+        ex = self.model_executor
+        eng = getattr(ex, "engine", None)
+        if eng is None or eng.model is not ex.model:
+            eng = FoldedVerifyEngine(ex.model, gate_mode=self.gate_mode)
+        self._engine = eng
+
+    @torch.no_grad()
+    def _batched_block_forward(self, batched_input: torch.Tensor, past_key_values) -> torch.Tensor:
+        B1, N = batched_input.shape
+        if B1 == 1:
+            return FastDLLMV2SpeculativeGeneration._batched_block_forward(
+                self, batched_input, past_key_values)
+        if self._engine is None:
+            self._pack_layer_weights()
+        eng = self._engine
+        bucket = B1 * N if self.fold_bucket is None else min(self.fold_bucket, B1 * N)
+        stats = StepStats()
+        prev_mode, eng.gate_mode = eng.gate_mode, self.gate_mode
+        try:
+            logits = eng.forward(batched_input, past_key_values, delta=self.delta, bucket=bucket,
+                                 stats=stats)
+        finally:
+            eng.gate_mode = prev_mode
+        L = len(stats.counts)
+        self._fold_draft_positions += (B1 - 1) * N * L
+        self._fold_draft_recomputed += sum(stats.counts) - L * N
+        self.last_stats = stats
+        return self._shift_logits(logits)
+
+
+# The reference's fused-path class name, so callers switch without code changes.
+SpecFoldTritonFastDLLMV2Generation = SpecFoldHIPFastDLLMV2Generation

@@ -1,0 +1,271 @@
+"""Block-diffusion decode loop with draft speculation — the caller of the
+verify-step seam ``_batched_block_forward``.
+
+Mirrors ``FastDLLMV2SpeculativeGeneration`` of the reference
+(specfold/generate/fastdllm_v2_generation.py:25-720): the same constructor
+knobs, the same seam, the same draft construction from a calibration graph
+(:387-474), the same unmasking rule (threshold plus the always-committed
+argmax, :666-676) and the same draft-logit cache (:599-651).  The decisions
+are integer logic on the logits; the forward passes go to the model executor
+(dense) or, in the SpecFold subclass, to the HIP folded verify step.
+"""
+
+from __future__ import annotations
+
+import logging
+import time
+from typing import Dict, List, Optional, Tuple
+
+import torch
+
+logger = logging.getLogger(__name__)
+
+
+class FastDLLMV2SpeculativeGeneration:
+    MASK_ID = 151665
+    STOP_TOKEN = 151645
+
+    def __init__(self, block_length: int, model_executor, calibration_graph=None,
+                 temperature: float = 0.0, top_p: float = 0.95, top_k: Optional[int] = None,
+                 mask_id: int = 151665, stop_token: int = 151645, max_length: int = 4096,
+                 max_new_tokens: int = 1024, small_block_size: int = 8, threshold: float = 0.9,
+                 use_block_cache: bool = False, device: str = "cuda", dtype: str = "bfloat16",
+                 prompt_render_mode: str = "preformatted_text", **kwargs):
+        self.__dict__.update(kwargs)
+        self.model_executor = model_executor
+        self.device = getattr(model_executor, "device", torch.device(device))
+        self.dtype = dtype
+        self.target_dtype = {"bfloat16": torch.bfloat16, "float16": torch.float16}.get(
+            dtype, torch.float32)
+        self.block_length = block_length
+        self.calibration_graph = calibration_graph
+        self.temperature = temperature
+        self.top_p = top_p
+        self.top_k = top_k
+        self.mask_id = mask_id
+        self.stop_token = stop_token
+        self.max_length = max_length
+        self.max_new_tokens = max_new_tokens
+        self.small_block_size = small_block_size
+        self.threshold = threshold
+        self.use_block_cache = use_block_cache
+        self.prompt_render_mode = prompt_render_mode
+        self.tokenizer = model_executor.get_tokenizer()
+        # decode statistics of the last generate call
+        self.last_model_calls = 0
+        self.last_commits: List[int] = []
+
+    # -- helpers with the reference's names ------------------------------------------
+    def _shift_logits(self, logits: torch.Tensor) -> torch.Tensor:
+        """Position i gets the logits of position i-1 (:121-126)."""
+        return torch.cat([logits[:, :1, :], logits[:, :-1, :]], dim=1)
+
+    @staticmethod
+    def _kv_seq_length(past_key_values) -> int:
+        return 0 if past_key_values is None else int(past_key_values.get_seq_length())
+
+    def _sample_with_top_p(self, logits, top_p: float = 0.95, temperature: float = 0.0):
+        return self.model_executor.sample_with_top_p(logits, top_p=top_p, temperature=temperature)
+
+    def _prepare_prompt_text(self, prompt: str) -> str:
+        if self.prompt_render_mode == "preformatted_text":
+            if not isinstance(prompt, str):
+                raise TypeError(f"Expected preformatted prompt text, got {type(prompt)}")
+            return prompt
+        if self.prompt_render_mode == "legacy_single_user_chat":
+            return self.tokenizer.apply_chat_template([{"role": "user", "content": prompt}],
+                                                      tokenize=False, add_generation_prompt=True)
+        raise ValueError(f"Unsupported prompt_render_mode: {self.prompt_render_mode}")
+
+    def _init_generation_state(self, prompt: str) -> Tuple[int, torch.Tensor]:
+        ids = self.tokenizer(self._prepare_prompt_text(prompt), return_tensors="pt").input_ids
+        ids = ids.to(self.device)
+        return ids.shape[1], ids
+
+    # -- the seam ---------------------------------------------------------------------
+    def _batched_block_forward(self, batched_input: torch.Tensor, past_key_values) -> torch.Tensor:
+        """Dense B+1-row block forward -> shifted logits [B+1, N, V] (:151-186)."""
+        out = self.model_executor.forward(batched_input, past_key_values=past_key_values,
+                                          use_cache=True, update_past_key_values=False)
+        return self._shift_logits(out.logits)
+
+    # -- drafts -----------------------------------------------------------------------
+    @torch.no_grad()
+    def get_draft_blocks(self, x: torch.Tensor, p: torch.Tensor,
+                         mask_index: Optional[torch.Tensor] = None, start_pos=None, end_pos=None,
+                         small_block_start: Optional[int] = None,
+                         small_block_end: Optional[int] = None, **kwargs) -> List[Dict]:
+        """One draft block per calibration-graph node (:387-474).
+
+        Node ij_set = [(position rank, vocab rank), ...]: take the masked
+        positions of the small block ranked by max softmax probability, and put
+        the vocab_rank-th most likely token at the pos_rank-th position.
+        """
+        if self.calibration_graph is None:
+            return []
+        if small_block_start is not None and small_block_end is not None:
+            small_mask = None if mask_index is None else mask_index[small_block_start:small_block_end]
+            small_logits = p[small_block_start:small_block_end, :]
+            offset = small_block_start
+        else:
+            small_mask, small_logits, offset = mask_index, p, 0
+        if small_mask is None:
+            return []
+        n_masked = int(small_mask.sum().item())
+        if n_masked == 0:
+            return []
+        conf = torch.softmax(small_logits, dim=-1).max(dim=-1).values
+        conf = torch.where(~small_mask, float("-inf"), conf)
+        drafts = []
+        for node in self.calibration_graph.get("selected_nodes", []):
+            ij_set = node.get("ij_set", [])
+            if not ij_set:
+                continue
+            top_rank = max(pr for pr, _ in ij_set)
+            if top_rank >= n_masked:
+                continue
+            positions = torch.topk(conf, k=top_rank + 1).indices
+            block = x.clone()
+            for pos_rank, vocab_rank in ij_set:
+                pos = positions[pos_rank]
+                tok = torch.topk(small_logits[pos], k=vocab_rank + 1).indices[vocab_rank]
+                block[offset + pos] = tok
+            drafts.append({"state": block, "start_pos": start_pos, "end_pos": end_pos,
+                           "node": node})
+        return drafts
+
+    # -- the decode loop ----------------------------------------------------------------
+    def _stop_reached(self, x_t: torch.Tensor, prompt_length: int) -> bool:
+        tail = x_t[:, prompt_length:]
+        hits = (tail == self.stop_token).nonzero()
+        if hits.numel() == 0:
+            return False
+        first = int(hits[0][1])
+        return int((tail[:, :first] == self.mask_id).sum()) == 0
+
+    @torch.no_grad()
+    def generate_with_draft_speculation(self, prompt: str = None, prompt_ids=None,
+                                        max_model_calls: Optional[int] = None, **kwargs):
+        """Decode with draft speculation (:483-720).
+
+        Returns (text, tokens_generated, model_calls, drafts_computed).
+        ``prompt_ids`` ([1, L] token ids) may replace the text prompt;
+        ``max_model_calls`` stops early after that many verify forwards.
+        """
+        t0 = time.time()
+        if prompt_ids is not None:
+            input_ids = prompt_ids.to(self.device)
+        else:
+            _, input_ids = self._init_generation_state(prompt)
+        orig_len = input_ids.shape[1]
+        bl, sbs = self.block_length, self.small_block_size
+        n_blocks = self.max_new_tokens // bl
+        n_small = bl // sbs
+        cache = None
+        model_calls = 0
+        drafts_computed = 0
+        self.last_commits = []
+
+        if input_ids.shape[1] > bl:
+            pre = (input_ids.shape[1] // bl) * bl
+            out = self.model_executor.forward(input_ids[:, :pre], past_key_values=None,
+                                              use_cache=True, update_past_key_values=True)
+            cache = out.past_key_values
+            model_calls += 1
+            if input_ids.shape[1] % bl == 0:
+                input_ids = torch.cat([input_ids, out.logits[:, -1:, :].argmax(dim=-1)], dim=1)
+
+        x_t = input_ids
+        draft_blocks: List[Dict] = []
+        called: List[Tuple[torch.Tensor, torch.Tensor]] = []
+        done = False
+        for _ in range(n_blocks):
+            if done or bool((x_t[:, orig_len:] == self.stop_token).any()):
+                break
+            plen = x_t.shape[1]
+            fill = bl - (plen % bl)
+            x_t = torch.cat([x_t, torch.full((x_t.shape[0], fill), self.mask_id,
+                                             device=self.device, dtype=torch.long)], dim=1)
+            while True:
+                if self._stop_reached(x_t, plen):
+                    break
+                mask_idx = x_t[:, -bl:] == self.mask_id
+                if int(mask_idx.sum()) == 0:
+                    out = self.model_executor.forward(x_t[:, -bl:], past_key_values=cache,
+                                                      use_cache=True, update_past_key_values=True)
+                    cache = out.past_key_values
+                    model_calls += 1
+                    x_t = torch.cat([x_t, out.logits[:, -1:, :].argmax(dim=-1)], dim=1)
+                    draft_blocks, called = [], []
+                    break
+                for sb in range(n_small):
+                    s0, s1 = sb * sbs, sb * sbs + sbs
+                    while True:
+                        if max_model_calls is not None and model_calls >= max_model_calls:
+                            done = True
+                            break
+                        mask_idx = x_t[:, -bl:] == self.mask_id
+                        small_mask = mask_idx[:, s0:s1]
+                        if int(small_mask.sum()) == 0:
+                            break
+                        if self._stop_reached(x_t, plen):
+                            break
+                        hit = -1
+                        if called:
+                            cur = x_t[0, -bl:]
+                            eq = torch.stack([s for s, _ in called]).eq(cur).all(dim=1).tolist()
+                            hit = eq.index(True) if True in eq else -1
+                        if hit >= 0:
+                            _, hit_logits = called.pop(hit)
+                            fx, fp = self._sample_with_top_p(hit_logits, top_p=self.top_p,
+                                                             temperature=self.temperature)
+                            x_1, p_1t = fx[:, s0:s1], fp[:, s0:s1, :]
+                        else:
+                            main_block = x_t[:, -bl:]
+                            if draft_blocks:
+                                states = torch.stack([d["state"] for d in draft_blocks], dim=0)
+                                batched = torch.cat([main_block, states], dim=0)
+                            else:
+                                batched = main_block
+                            logits = self._batched_block_forward(batched, cache)
+                            model_calls += 1
+                            main_logits = logits[0:1]
+                            for i, d in enumerate(draft_blocks):
+                                called.append((d["state"], logits[i + 1:i + 2]))
+                            x_1, p_1t = self._sample_with_top_p(main_logits[:, s0:s1, :],
+                                                                top_p=self.top_p,
+                                                                temperature=self.temperature)
+                            if self.calibration_graph is not None:
+                                draft_blocks = self.get_draft_blocks(
+                                    x_t[0, -bl:], main_logits[0], mask_idx[0],
+                                    start_pos=x_t.shape[1] - bl, end_pos=x_t.shape[1],
+                                    small_block_start=s0, small_block_end=s1)
+                                drafts_computed += len(draft_blocks)
+                        conf = torch.gather(p_1t, -1, x_1.unsqueeze(-1)).squeeze(-1)
+                        conf = torch.where(small_mask, conf, -torch.inf)
+                        unmask = conf > self.threshold
+                        best = conf.argmax(dim=-1)
+                        unmask[torch.arange(x_1.shape[0], device=self.device), best] = True
+                        unmask = unmask & small_mask
+                        self.last_commits.append(int(unmask.sum()))
+                        region = x_t[:, x_t.shape[1] - bl + s0: x_t.shape[1] - bl + s1]
+                        region[unmask] = x_1[unmask]
+                    if done:
+                        break
+                if done:
+                    break
+
+        final_ids = x_t[0, orig_len:]
+        stops = (final_ids == self.stop_token).nonzero()
+        if stops.numel() > 0:
+            final_ids = final_ids[:int(stops[0]) + 1]
+        kept = final_ids[final_ids != self.mask_id]
+        text = self.tokenizer.batch_decode(kept.unsqueeze(0), skip_special_tokens=True)
+        tokens = int(kept.numel())
+        elapsed = time.time() - t0
+        self.last_model_calls = model_calls
+        self.last_cache = cache
+        self.last_tokens = x_t
+        logger.info("Generated %d tokens in %.2fs (%.2f tok/s); model calls %d, drafts %d",
+                    tokens, elapsed, tokens / max(elapsed, 1e-9), model_calls, drafts_computed)
+        return text, tokens, model_calls, drafts_computed
