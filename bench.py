@@ -1,0 +1,301 @@
+"""Benchmark of SpecFold's folded verify step on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--workload cfg3_7b] [--no-cpu-baseline]
+
+Workload (default ``cfg3_7b``): Fast-dLLM-v2-7B shape (hidden 3584, 28/4 heads,
+hd 128, 28 layers, SwiGLU 18944, vocab 152064), bf16, random-init weights
+(seed 2), a 2048-token random prompt prefilled block by block into the paged
+KV cache, B=7 drafts from the fixed synthetic draft graph (depth 4 <= D=8,
+<= S=3 per level), block 32, small block 8, delta 0.1, threshold 0.9, greedy.
+
+A step is one iteration of the decode loop (generate_with_draft_speculation):
+one folded verify step of the 8 branches over the prefix (or a block commit
+/ a draft-cache hit), then sampling, drafting and unmasking.  W untimed steps,
+then exactly K timed steps between two torch.cuda.synchronize() calls.
+``value`` = tokens committed during the K steps / their wall time.
+
+Also reported (same run): the verify step alone (hipEvent median), every HIP
+kernel's average duration from HIP events around back-to-back launches on
+the launch stream with its algorithmic bytes/flops and roofline fraction
+(MI355X peaks: HBM 8 TB/s, dense bf16 MFMA 2.5 PFLOP/s), and the CPU baseline:
+the oracle (CPU restatement of the reference PyTorch step) in fp32 on the
+host cores, one layer timed and scaled to all layers plus the lm_head.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def parse_args(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--workload", default="cfg3_7b")
+    ap.add_argument("--verify-iters", type=int, default=50)
+    ap.add_argument("--kernel-iters", type=int, default=200)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--only-kernels", action="store_true",
+                    help="skip the decode loop; time the verify step and kernels only")
+    return ap.parse_args(argv)
+
+
+def event_time_ms(fn, iters: int) -> float:
+    """Average ms per call of fn() from HIP events on the current stream."""
+    fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(iters):
+        fn()
+    e.record()
+    e.synchronize()
+    return s.elapsed_time(e) / iters
+
+
+def kernel_roofline(name, ms, w, R, B1, N, P):
+    """Algorithmic bytes / flops per launch of each kernel at the measured R."""
+    sh = w.shape
+    D, H, Hkv, hd, e = sh.hidden, sh.heads, sh.kv_heads, sh.head_dim, 2
+    BN = B1 * N
+    F = BN - R
+    nq = (H + 2 * Hkv) * hd
+    if name == "gate":
+        by = BN * D * e + R * D * e + BN * 17 + R * 4
+        fl = 6 * BN * D
+    elif name == "qkv":
+        by = nq * D * e + nq * e + R * D * e + R * nq * e + 2 * N * hd * e
+        fl = 2 * R * D * nq
+    elif name == "attn":
+        by = 2 * Hkv * P * hd * e + BN * 2 * Hkv * hd * e + 2 * R * H * hd * e + 8 * R * H
+        fl = 4 * R * H * (P + N) * hd
+    elif name == "chain":
+        by = F * (2 * H * hd * e + 8 * H)
+        fl = 8 * F * H * hd
+    elif name == "append":
+        by = 2 * (2 * N * Hkv * hd * e)
+        fl = 0
+    else:
+        raise KeyError(name)
+    s = ms * 1e-3
+    t_hbm = by / (HBM_PEAK_GBS * 1e9)
+    t_mfma = fl / (BF16_PEAK_TFLOPS * 1e12)
+    bound = "mfma" if t_mfma > t_hbm else "hbm"
+    if bound == "hbm":
+        ach, peak, unit = by / s / 1e9, HBM_PEAK_GBS, "GB/s"
+    else:
+        ach, peak, unit = fl / s / 1e12, BF16_PEAK_TFLOPS, "TFLOP/s"
+    return {"bound": bound, "achieved": round(ach, 3), "peak": peak, "unit": unit,
+            "frac": round(ach / peak, 5), "traffic": None, "avg_us": round(ms * 1e3, 3),
+            "algorithmic_bytes": int(by), "algorithmic_flops": int(fl),
+            "hbm_gbps": round(by / s / 1e9, 2), "mfma_tflops": round(fl / s / 1e12, 3)}
+
+
+def cpu_baseline(w, batched_cpu, tokens_per_step, seconds):
+    """The oracle (CPU restatement of the reference PyTorch step) in fp32:
+    one decoder layer of the workload's shape on the host cores, scaled to
+    all layers, plus the lm_head GEMM timed on a vocab slice and scaled."""
+    from dataclasses import replace
+
+    from oracle.folded_reference import folded_layer, parent_map, rope_tables, topo_order
+    from specfold_amd.generate.synthetic_model import build_qwen2
+    from specfold_amd.synthetic import random_prefix_kv
+
+    cores = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(cores)
+    sh = replace(w.shape, layers=1, vocab=4096)
+    model = build_qwen2(sh, w.seed, device="cpu", dtype=torch.float32)
+    gen = torch.Generator().manual_seed(w.seed)
+    kv = random_prefix_kv(1, sh.kv_heads, w.prefix, sh.head_dim, gen, dtype=torch.float32)[0]
+    toks = batched_cpu % sh.vocab
+    parent, counts = parent_map(toks)
+    order = topo_order(counts)
+    hidden = torch.randn(toks.shape[0], toks.shape[1], sh.hidden, generator=gen)
+    cos, sin = rope_tables(model, hidden, w.prefix, toks.shape[1])
+    h = [hidden[i:i + 1] for i in range(toks.shape[0])]
+    lyr = model.model.layers[0]
+
+    def one():
+        folded_layer(lyr, h, parent, order, kv, cos, sin, w.delta, sh.heads, sh.kv_heads)
+
+    with torch.no_grad():
+        one()
+        times = []
+        t_end = time.perf_counter() + seconds
+        while len(times) < 2 or time.perf_counter() < t_end:
+            t0 = time.perf_counter()
+            one()
+            times.append(time.perf_counter() - t0)
+        t_layer = statistics.median(times)
+        vs = 8192
+        x = torch.randn(toks.numel(), sh.hidden)
+        wh = torch.randn(vs, sh.hidden)
+        x @ wh.t()
+        t0 = time.perf_counter()
+        for _ in range(3):
+            x @ wh.t()
+        t_head = (time.perf_counter() - t0) / 3 * (w.shape.vocab / vs)
+    t_step = t_layer * w.shape.layers + t_head
+    return {"value": round(tokens_per_step / t_step, 5), "unit": "tokens/s", "cores": cores,
+            "kind": "port",
+            "sample": (f"oracle fp32, 1 of {w.shape.layers} layers timed ({len(times)} runs, "
+                       f"median {t_layer:.3f}s) x{w.shape.layers} + lm_head "
+                       f"({t_head:.3f}s, timed on a {vs}-row vocab slice); "
+                       f"{tokens_per_step:.3f} tokens/step from the GPU decode loop"),
+            "verify_step_s": round(t_step, 4)}
+
+
+def main(argv=None) -> int:
+    args = parse_args(argv)
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: the verify step is a single-GPU path in this build "
+              "(multi-GPU sharding is design-only); run with --gpus 1", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    from specfold_amd.configs import SYNTHETIC_DRAFT_GRAPH, workload
+    from specfold_amd.generate import FastDLLMModelExecutor, SpecFoldHIPFastDLLMV2Generation
+
+    torch.cuda.set_device(0)
+    w = workload(args.workload)
+    t_build = time.time()
+    ex = FastDLLMModelExecutor.synthetic(
+        w.shape, w.seed, device="cuda", block_length=w.block,
+        max_length=w.prefix + w.gen_tokens + 4 * w.block, page_size=w.page_size,
+        page_order="shuffled" if w.shuffled_pages else "sequential", page_seed=w.seed)
+    gen = SpecFoldHIPFastDLLMV2Generation(
+        block_length=w.block, model_executor=ex, calibration_graph=SYNTHETIC_DRAFT_GRAPH,
+        threshold=w.threshold, small_block_size=w.small_block, max_new_tokens=w.gen_tokens,
+        max_length=w.prefix + w.gen_tokens, delta=w.delta)
+    g = torch.Generator().manual_seed(w.seed)
+    prompt = torch.randint(0, w.shape.vocab, (1, w.prefix), generator=g)
+    torch.cuda.synchronize()
+    build_s = time.time() - t_build
+    print(f"[bench] model + engine ready in {build_s:.1f}s", file=sys.stderr, flush=True)
+
+    # decode loop: prefill, W warmup steps, K timed steps
+    steps = gen.decode_steps(prompt)
+    t0 = time.time()
+    ev = next(steps)
+    assert ev["kind"] == "prefill"
+    torch.cuda.synchronize()
+    prefill_s = time.time() - t0
+    print(f"[bench] prefill {w.prefix} tokens in {prefill_s:.2f}s", file=sys.stderr, flush=True)
+    for _ in range(args.warmup):
+        next(steps)
+    kinds = {}
+    committed = 0
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        ev = next(steps)
+        committed += ev["committed"]
+        kinds[ev["kind"]] = kinds.get(ev["kind"], 0) + 1
+    torch.cuda.synchronize()
+    timed_s = time.perf_counter() - t0
+    tps = committed / timed_s
+    n_verify = kinds.get("verify", 0)
+    print(f"[bench] {args.steps} decode steps in {timed_s:.3f}s: {committed} tokens, {kinds}",
+          file=sys.stderr, flush=True)
+
+    # the verify step alone, on the last draft batch at the current prefix
+    cache = gen._state["cache"]
+    x_t = gen._state["x_t"]
+    main_block = x_t[:, -w.block:]
+    from specfold_amd.synthetic import TREE_DIFFS
+    batched = main_block.repeat(len(TREE_DIFFS), 1)
+    gsel = torch.Generator().manual_seed(123)
+    repl = torch.randint(0, w.shape.vocab, (7,), generator=gsel).to(batched.device)
+    for i, d in enumerate(TREE_DIFFS):
+        for k in d:
+            batched[i, k] = repl[k]
+    lat = []
+    for i in range(args.verify_iters + 3):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        gen._batched_block_forward(batched, cache)
+        e.record()
+        e.synchronize()
+        if i >= 3:
+            lat.append(s.elapsed_time(e))
+    verify_ms = statistics.median(lat)
+    counts = gen.last_stats.counts
+    R = round(sum(counts) / len(counts))
+    B1, N = batched.shape
+    fold_ratio_step = 1 - (sum(counts) - len(counts) * N) / ((B1 - 1) * N * len(counts))
+    print(f"[bench] verify step median {verify_ms:.3f} ms, mean R {R}", file=sys.stderr,
+          flush=True)
+
+    # per-kernel timings on the buffers of the last verify step (layer 0 of the view)
+    eng = gen._engine
+    launchers, info = eng.profile_launchers(li=-1)
+    P = info["prefix"]
+    R_last = int(info["count"].item())
+    kernels = {}
+    for name in ("qkv", "attn", "chain", "append", "gate"):
+        if name not in launchers:
+            continue
+        ms = event_time_ms(launchers[name], args.kernel_iters)
+        kernels[name] = kernel_roofline(name, ms, w, R_last, B1, N, P)
+    print(f"[bench] kernels {json.dumps({k: v['avg_us'] for k, v in kernels.items()})}",
+          file=sys.stderr, flush=True)
+
+    tokens_per_step = committed / max(1, args.steps)
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(w, batched.cpu(), tokens_per_step, args.cpu_seconds)
+        print(f"[bench] cpu baseline {cpu}", file=sys.stderr, flush=True)
+
+    out = {
+        "metric": "decode tokens/sec on 1 GPU; folded verify-step latency; attention HBM GB/s",
+        "value": round(tps, 3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(timed_s / args.steps * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init weights, random-token prompt, synthetic draft graph)",
+        "config": {"workload": w.name, "hidden": w.shape.hidden, "layers": w.shape.layers,
+                   "heads": w.shape.heads, "kv_heads": w.shape.kv_heads,
+                   "intermediate": w.shape.intermediate, "vocab": w.shape.vocab,
+                   "prefix": w.prefix, "branches": w.branches, "block": w.block,
+                   "small_block": w.small_block, "delta": w.delta, "threshold": w.threshold,
+                   "parallelism": "none (1 GPU)"},
+        "verify_step_ms": round(verify_ms, 4),
+        "verify_step_prefix": P,
+        "verify_recomputed_rows_mean": R,
+        "verify_fold_ratio": round(fold_ratio_step, 4),
+        "decode_step_kinds": kinds,
+        "tokens_per_step": round(tokens_per_step, 4),
+        "prefill_s": round(prefill_s, 3),
+        "roofline": kernels.get("attn"),
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -28,7 +28,7 @@ import torch
 import torch.nn.functional as F
 
 from specfold_amd import _lib
-from specfold_amd.kv_cache import PagedKVCache, prefix_view
+from specfold_amd.kv_cache import PagedKVCache, cache_length, prefix_view
 
 logger = logging.getLogger(__name__)
 
@@ -180,7 +180,7 @@ class FoldedVerifyEngine:
         par_host = [0] + [int(p) for p in parent[1:]]
         par = torch.tensor(par_host, dtype=torch.int32).to(self.device, non_blocking=True)
 
-        P = int(cache.get_seq_length()) if cache is not None else 0
+        P = cache_length(cache)
         buf = self.buffers(B1, N, bucket, P)
         base = self.model.model
         hidden = base.embed_tokens(batched_input).reshape(BN, self.D)
@@ -252,7 +252,58 @@ class FoldedVerifyEngine:
                                 compute_logits=compute_logits, q_scale=q_scale, trace=trace,
                                 teacher=teacher, stats=stats)
         self.last_hidden = hidden
+        self._last = dict(B1=B1, N=N, bucket=bucket, cache=cache, par=par, cos=cos, sin=sin,
+                          q_scale=q_scale, hidden=hidden, delta=delta)
         if not compute_logits:
             return None
         final = base.norm(hidden.view(B1, N, D))
         return self.model.lm_head(final)
+
+    # ------------------------------------------------------------------------
+    def profile_launchers(self, li: int = -1):
+        """No-argument callables that re-launch each HIP entry point of layer
+        ``li`` on the buffers resident from the last forward (for timing).
+        The gate runs on the last layer's output hidden states, so call it
+        last: it rewrites rows/count/src for the other launchers."""
+        st = self._last
+        B1, N, bucket, cache = st["B1"], st["N"], st["bucket"], st["cache"]
+        BN = B1 * N
+        buf = self._bufs[(B1, N, bucket)]
+        li = li % self.L
+        lyr = self.layers[li]
+        H, Hkv, hd, D = self.H, self.Hkv, self.hd, self.D
+        count = buf.count_slab[li:li + 1]
+        segcnt = buf.segcnt_slab[li * B1:(li + 1) * B1]
+        pv = prefix_view(cache, li)
+        w_qkv, b_qkv = self._packed[li]
+        hidden = st["hidden"]
+
+        def gate():
+            _lib.fold_gate(hidden, st["par"], lyr.input_layernorm.weight, B1, N, bucket, st["delta"],
+                           self.eps, self.gate_mode, buf.rec, buf.f, buf.src, buf.rows, count,
+                           buf.seg, segcnt, buf.rstd, buf.xn)
+
+        def qkv():
+            _lib.qkv_rope(buf.xn, buf.rows, count, bucket, BN, w_qkv, b_qkv, st["cos"], st["sin"],
+                          st["q_scale"], N, D, H, Hkv, hd, buf.q_buf, buf.kv_buf, buf.ws_qkv)
+
+        def attn():
+            _lib.attn_prefix_block(
+                buf.q_buf, buf.kv_buf, pv.k if pv else None, pv.v if pv else None,
+                pv.page_table if pv else None, pv.length if pv else 0,
+                pv.page_size if pv else 1, pv.page_stride if pv else 0,
+                pv.head_stride if pv else 0, buf.src, buf.rows, count, bucket, B1, N, H, Hkv, hd,
+                self.scaling, buf.o32, buf.o_bf, buf.m_tab, buf.z_tab, buf.ws_attn)
+
+        def chain():
+            _lib.chain_correct(buf.q_buf, buf.kv_buf, buf.src, st["par"], buf.rec, buf.seg, segcnt,
+                               B1, N, H, Hkv, hd, self.scaling, buf.o32, buf.o_bf, buf.m_tab,
+                               buf.z_tab)
+
+        out = dict(qkv=qkv, attn=attn, chain=chain, gate=gate)
+        if isinstance(cache, PagedKVCache) and cache.length + N <= cache.capacity:
+            def append():
+                # writes past the logical end of the cache: never read, length unchanged
+                cache.append_rows(li, buf.kv_buf, 0, N, start_pos=cache.length)
+            out["append"] = append
+        return out, dict(count=count, buf=buf, prefix=pv.length if pv else 0)

@@ -144,66 +144,58 @@ class FastDLLMV2SpeculativeGeneration:
         return int((tail[:, :first] == self.mask_id).sum()) == 0
 
     @torch.no_grad()
-    def generate_with_draft_speculation(self, prompt: str = None, prompt_ids=None,
-                                        max_model_calls: Optional[int] = None, **kwargs):
-        """Decode with draft speculation (:483-720).
-
-        Returns (text, tokens_generated, model_calls, drafts_computed).
-        ``prompt_ids`` ([1, L] token ids) may replace the text prompt;
-        ``max_model_calls`` stops early after that many verify forwards.
-        """
-        t0 = time.time()
-        if prompt_ids is not None:
-            input_ids = prompt_ids.to(self.device)
-        else:
-            _, input_ids = self._init_generation_state(prompt)
+    def decode_steps(self, prompt_ids: torch.Tensor):
+        """The decode loop of generate_with_draft_speculation (:483-700) as a
+        generator: yields one event per loop iteration —
+        {"kind": "prefill" | "commit" | "verify" | "hit", "committed": tokens
+        unmasked by the iteration}.  Loop state is on ``self._state``."""
+        input_ids = prompt_ids.to(self.device)
         orig_len = input_ids.shape[1]
         bl, sbs = self.block_length, self.small_block_size
         n_blocks = self.max_new_tokens // bl
         n_small = bl // sbs
-        cache = None
-        model_calls = 0
-        drafts_computed = 0
-        self.last_commits = []
+        st = self._state = dict(cache=None, model_calls=0, drafts_computed=0, x_t=input_ids,
+                                orig_len=orig_len)
 
         if input_ids.shape[1] > bl:
             pre = (input_ids.shape[1] // bl) * bl
             out = self.model_executor.forward(input_ids[:, :pre], past_key_values=None,
                                               use_cache=True, update_past_key_values=True)
-            cache = out.past_key_values
-            model_calls += 1
+            st["cache"] = out.past_key_values
+            st["model_calls"] += 1
             if input_ids.shape[1] % bl == 0:
                 input_ids = torch.cat([input_ids, out.logits[:, -1:, :].argmax(dim=-1)], dim=1)
+            st["x_t"] = input_ids
+            yield {"kind": "prefill", "committed": 0}
 
         x_t = input_ids
         draft_blocks: List[Dict] = []
         called: List[Tuple[torch.Tensor, torch.Tensor]] = []
-        done = False
         for _ in range(n_blocks):
-            if done or bool((x_t[:, orig_len:] == self.stop_token).any()):
+            if bool((x_t[:, orig_len:] == self.stop_token).any()):
                 break
             plen = x_t.shape[1]
             fill = bl - (plen % bl)
             x_t = torch.cat([x_t, torch.full((x_t.shape[0], fill), self.mask_id,
                                              device=self.device, dtype=torch.long)], dim=1)
+            st["x_t"] = x_t
             while True:
                 if self._stop_reached(x_t, plen):
                     break
                 mask_idx = x_t[:, -bl:] == self.mask_id
                 if int(mask_idx.sum()) == 0:
-                    out = self.model_executor.forward(x_t[:, -bl:], past_key_values=cache,
+                    out = self.model_executor.forward(x_t[:, -bl:], past_key_values=st["cache"],
                                                       use_cache=True, update_past_key_values=True)
-                    cache = out.past_key_values
-                    model_calls += 1
+                    st["cache"] = out.past_key_values
+                    st["model_calls"] += 1
                     x_t = torch.cat([x_t, out.logits[:, -1:, :].argmax(dim=-1)], dim=1)
+                    st["x_t"] = x_t
                     draft_blocks, called = [], []
+                    yield {"kind": "commit", "committed": 0}
                     break
                 for sb in range(n_small):
                     s0, s1 = sb * sbs, sb * sbs + sbs
                     while True:
-                        if max_model_calls is not None and model_calls >= max_model_calls:
-                            done = True
-                            break
                         mask_idx = x_t[:, -bl:] == self.mask_id
                         small_mask = mask_idx[:, s0:s1]
                         if int(small_mask.sum()) == 0:
@@ -220,6 +212,7 @@ class FastDLLMV2SpeculativeGeneration:
                             fx, fp = self._sample_with_top_p(hit_logits, top_p=self.top_p,
                                                              temperature=self.temperature)
                             x_1, p_1t = fx[:, s0:s1], fp[:, s0:s1, :]
+                            kind = "hit"
                         else:
                             main_block = x_t[:, -bl:]
                             if draft_blocks:
@@ -227,8 +220,8 @@ class FastDLLMV2SpeculativeGeneration:
                                 batched = torch.cat([main_block, states], dim=0)
                             else:
                                 batched = main_block
-                            logits = self._batched_block_forward(batched, cache)
-                            model_calls += 1
+                            logits = self._batched_block_forward(batched, st["cache"])
+                            st["model_calls"] += 1
                             main_logits = logits[0:1]
                             for i, d in enumerate(draft_blocks):
                                 called.append((d["state"], logits[i + 1:i + 2]))
@@ -240,22 +233,39 @@ class FastDLLMV2SpeculativeGeneration:
                                     x_t[0, -bl:], main_logits[0], mask_idx[0],
                                     start_pos=x_t.shape[1] - bl, end_pos=x_t.shape[1],
                                     small_block_start=s0, small_block_end=s1)
-                                drafts_computed += len(draft_blocks)
+                                st["drafts_computed"] += len(draft_blocks)
+                            kind = "verify"
                         conf = torch.gather(p_1t, -1, x_1.unsqueeze(-1)).squeeze(-1)
                         conf = torch.where(small_mask, conf, -torch.inf)
                         unmask = conf > self.threshold
                         best = conf.argmax(dim=-1)
                         unmask[torch.arange(x_1.shape[0], device=self.device), best] = True
                         unmask = unmask & small_mask
-                        self.last_commits.append(int(unmask.sum()))
                         region = x_t[:, x_t.shape[1] - bl + s0: x_t.shape[1] - bl + s1]
                         region[unmask] = x_1[unmask]
-                    if done:
-                        break
-                if done:
-                    break
+                        n = int(unmask.sum())
+                        self.last_commits.append(n)
+                        yield {"kind": kind, "committed": n}
 
-        final_ids = x_t[0, orig_len:]
+    @torch.no_grad()
+    def generate_with_draft_speculation(self, prompt: str = None, prompt_ids=None,
+                                        max_model_calls: Optional[int] = None, **kwargs):
+        """Decode with draft speculation (:483-720).
+
+        Returns (text, tokens_generated, model_calls, drafts_computed).
+        ``prompt_ids`` ([1, L] token ids) may replace the text prompt;
+        ``max_model_calls`` stops early after that many forwards.
+        """
+        t0 = time.time()
+        if prompt_ids is None:
+            _, prompt_ids = self._init_generation_state(prompt)
+        self.last_commits = []
+        for _ in self.decode_steps(prompt_ids):
+            if max_model_calls is not None and self._state["model_calls"] >= max_model_calls:
+                break
+        st = self._state
+        x_t = st["x_t"]
+        final_ids = x_t[0, st["orig_len"]:]
         stops = (final_ids == self.stop_token).nonzero()
         if stops.numel() > 0:
             final_ids = final_ids[:int(stops[0]) + 1]
@@ -263,9 +273,10 @@ class FastDLLMV2SpeculativeGeneration:
         text = self.tokenizer.batch_decode(kept.unsqueeze(0), skip_special_tokens=True)
         tokens = int(kept.numel())
         elapsed = time.time() - t0
-        self.last_model_calls = model_calls
-        self.last_cache = cache
+        self.last_model_calls = st["model_calls"]
+        self.last_cache = st["cache"]
         self.last_tokens = x_t
         logger.info("Generated %d tokens in %.2fs (%.2f tok/s); model calls %d, drafts %d",
-                    tokens, elapsed, tokens / max(elapsed, 1e-9), model_calls, drafts_computed)
-        return text, tokens, model_calls, drafts_computed
+                    tokens, elapsed, tokens / max(elapsed, 1e-9), st["model_calls"],
+                    st["drafts_computed"])
+        return text, tokens, st["model_calls"], st["drafts_computed"]

@@ -132,6 +132,17 @@ def contiguous_view(k: torch.Tensor, v: torch.Tensor) -> PrefixView:
                       head_stride=P * hd)
 
 
+def cache_length(cache) -> int:
+    """Prefix length of a PagedKVCache, a DynamicCache-like object or a list of (k, v)."""
+    if cache is None:
+        return 0
+    if hasattr(cache, "get_seq_length"):
+        return int(cache.get_seq_length())
+    if len(cache) == 0 or cache[0][0] is None:
+        return 0
+    return int(cache[0][0].shape[-2])
+
+
 def prefix_view(cache, li: int) -> Optional[PrefixView]:
     """Kernel view of layer li of either a PagedKVCache or a reference-style cache."""
     if cache is None:

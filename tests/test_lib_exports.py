@@ -1,0 +1,52 @@
+"""The C-ABI library loads on a machine without a GPU and exports every
+function include/specfold_amd.h declares, with the signatures the ctypes
+binding uses; argument validation rejects bad shapes without launching."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from specfold_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "specfold_amd.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sf_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_entry_points():
+    names = declared_functions()
+    for n in ("sf_fold_gate", "sf_qkv_rope", "sf_attn_prefix_block", "sf_chain_correct",
+              "sf_kv_append", "sf_qkv_workspace_bytes", "sf_attn_workspace_bytes"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_functions()
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signatures out of sync with the header"
+    for n in names:
+        assert isinstance(getattr(lib, n), ctypes._CFuncPtr), n
+
+
+def test_host_side_validation_without_gpu():
+    lib = _lib.load()
+    assert lib.sf_abi_version() == 1
+    assert lib.sf_status_string(1).decode() == "shape outside kernel limits"
+    # NULL pointers and bad shapes are rejected before any launch
+    assert lib.sf_fold_gate(*([None] * 3), 8, 32, 64, 256, 0.1, 1e-6, 0, *([None] * 10)) == 2
+    assert lib.sf_chain_correct(*([None] * 7), 8, 32, 28, 4, 64, 0.1, *([None] * 5)) == 2
+    assert lib.sf_qkv_workspace_bytes(256, 3584, 4608) > 0
+    assert lib.sf_attn_workspace_bytes(256, 28, 0) > 0
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "nope.so")
+    monkeypatch.setattr(_lib, "_LIB", None)
+    with pytest.raises(_lib.SpecFoldLibraryMissing):
+        _lib.load()
