@@ -151,7 +151,10 @@ def prefix_view(cache, li: int) -> Optional[PrefixView]:
         return cache.view(li) if cache.length > 0 else None
     if len(cache) <= li:
         return None
-    k, v = cache[li][0], cache[li][1]
+    if hasattr(cache, "layers") and not hasattr(cache, "__getitem__"):
+        k, v = cache.layers[li].keys, cache.layers[li].values   # transformers>=5 DynamicCache
+    else:
+        k, v = cache[li][0], cache[li][1]
     if k is None or k.shape[-2] == 0:
         return None
     return contiguous_view(k, v)
