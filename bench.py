@@ -57,13 +57,24 @@ def parse_args(argv=None):
 
 
 def event_time_ms(fn, iters: int) -> float:
-    """Average ms per call of fn() from HIP events on the current stream."""
-    fn()
+    """Average ms per call of fn() on the GPU: ``iters`` back-to-back launches
+    captured in one HIP graph, replayed between two HIP events recorded on the
+    stream the kernels run on (no host launch overhead between kernels)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(iters):
+            fn()
+    graph.replay()
     torch.cuda.synchronize()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     s.record()
-    for _ in range(iters):
-        fn()
+    graph.replay()
     e.record()
     e.synchronize()
     return s.elapsed_time(e) / iters
@@ -91,6 +102,27 @@ def kernel_roofline(name, ms, w, R, B1, N, P):
     elif name == "append":
         by = 2 * (2 * N * Hkv * hd * e)
         fl = 0
+    elif name == "o_proj":
+        by = D * H * hd * e + BN * H * hd * e + 2 * BN * D * e
+        fl = 2 * BN * H * hd * D
+    elif name == "post_norm":
+        by = 2 * R * D * e + D * e
+        fl = 4 * R * D
+    elif name == "gate_up":
+        I = sh.intermediate
+        by = 2 * I * D * e + R * D * e + R * I * e
+        fl = 4 * R * D * I
+    elif name == "down":
+        I = sh.intermediate
+        by = D * I * e + R * I * e + R * D * e
+        fl = 2 * R * I * D
+    elif name == "resid":
+        by = 3 * BN * D * e
+        fl = BN * D
+    elif name == "lm_head":
+        V = sh.vocab
+        by = V * D * e + BN * D * e + BN * V * e
+        fl = 2 * BN * D * V
     else:
         raise KeyError(name)
     s = ms * 1e-3
@@ -161,6 +193,7 @@ def cpu_baseline(w, batched_cpu, tokens_per_step, seconds):
             "verify_step_s": round(t_step, 4)}
 
 
+@torch.no_grad()
 def main(argv=None) -> int:
     args = parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -249,7 +282,8 @@ def main(argv=None) -> int:
     P = info["prefix"]
     R_last = int(info["count"].item())
     kernels = {}
-    for name in ("qkv", "attn", "chain", "append", "gate"):
+    for name in ("qkv", "attn", "chain", "o_proj", "post_norm", "gate_up", "down", "resid",
+                 "lm_head", "append", "gate"):
         if name not in launchers:
             continue
         ms = event_time_ms(launchers[name], args.kernel_iters)

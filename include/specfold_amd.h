@@ -84,7 +84,7 @@ int sf_fold_gate(const uint16_t* hidden, const int32_t* par, const uint16_t* ln_
  * (:77-87 packing); b_qkv may be NULL (NLD: no bias).  cos/sin bf16 [N, hd].
  * q_scale (optional, fp32 [N]) multiplies roped q by bf16(q_scale[n]) — the
  * llama-4 attention scale of specfold/generate/nld_folded.py:37-53, 175-176.
- * Limits: hd == 128, D % 64 == 0, bucket <= 1024.
+ * Limits: hd == 128, D % 128 == 0, bucket <= 1024.
  */
 size_t sf_qkv_workspace_bytes(int bucket, int D, int n_qkv);
 int sf_qkv_rope(const uint16_t* xn, const int32_t* rows, const int32_t* count, int bucket, int BN,
@@ -100,16 +100,20 @@ int sf_qkv_rope(const uint16_t* xn, const int32_t* rows, const int32_t* count, i
  * attention of recomputed rows (specfold/generate/fastdllm_v2_folded.py:164-181).
  * Block key j of branch b is kv_buf row src[b*N+j]*N + j.  No mask.
  * Writes o32, o_bf, m_tab, z_tab for the rows listed in rows[0:min(count,bucket)].
- * Limits: hd == 128, H % Hkv == 0, N <= 64, H/Hkv <= 8.
+ * prefix_len (optional, device int32[1]): the prefix length, read on the device;
+ * P is then the capacity the grid and workspace are sized for (so one captured
+ * graph serves a growing cache).  With prefix_len NULL, P is the length.
+ * Limits: hd == 128, H % Hkv == 0, N <= 64, H/Hkv <= 8, P <= 32768, a page size
+ * dividing 128.
  */
 size_t sf_attn_workspace_bytes(int bucket, int H, int P);
 int sf_attn_prefix_block(const uint16_t* q_buf, const uint16_t* kv_buf, const uint16_t* prefix_k,
                          const uint16_t* prefix_v, const int32_t* page_table, int P, int page_size,
                          long long page_stride, long long head_stride, const int32_t* src,
                          const int32_t* rows, const int32_t* count, int bucket, int B1, int N,
-                         int H, int Hkv, int hd, float scaling, float* o32, uint16_t* o_bf,
-                         float* m_tab, float* z_tab, void* workspace, size_t workspace_bytes,
-                         void* stream);
+                         int H, int Hkv, int hd, float scaling, const int32_t* prefix_len,
+                         float* o32, uint16_t* o_bf, float* m_tab, float* z_tab, void* workspace,
+                         size_t workspace_bytes, void* stream);
 
 /*
  * (4) Chain correction of folded rows: start from the state of the nearest
@@ -137,6 +141,39 @@ int sf_chain_correct(const uint16_t* q_buf, const uint16_t* kv_buf, const int32_
 int sf_kv_append(const uint16_t* kv_buf, int row0, int n_tok, int Hkv, int hd, uint16_t* k_cache,
                  uint16_t* v_cache, const int32_t* page_table, int page_size,
                  long long page_stride, long long head_stride, int start_pos, void* stream);
+
+/*
+ * (6) The rest of the layer on the compacted rows (reference:
+ * specfold/generate/fastdllm_v2_folded.py:207-218; Triton
+ * fused_ln_gateup_silu_kernel / fused_down_residual_scatter_kernel,
+ * specfold/generate/triton_kernels.py:102-194, and the torch addmm/index ops of
+ * the fused path, fastdllm_v2_folded.py:351-361).  All GEMMs stream the bf16
+ * weight [N, K] once on bf16 MFMA with fp32 accumulation; split-K partials go to
+ * a caller workspace of sf_gemm_workspace_bytes(M or bucket, N, K) bytes.
+ *
+ * sf_o_proj_residual    hp[r] = bf16(x[r] + bf16(o_bf[r] . Wo^T)), r < M (all rows)
+ * sf_rows_rmsnorm       out[m] = bf16(w * bf16(x[rows[m]] * rstd)), m < count
+ * sf_ffn_gate_up        act[m] = bf16(bf16(silu(bf16(zn[m] . Wg^T))) * bf16(zn[m] . Wu^T))
+ * sf_ffn_down_scatter   ffn[rows[m]] = bf16(act[m] . Wd^T), m < count
+ * sf_residual_gather_add out[r] = bf16(hp[r] + ffn[src[r]*N + r%N]), r < B1*N
+ *                       (folded rows take their nearest recomputing ancestor's FFN)
+ * sf_lm_head            logits[m] = bf16(x[m] . Wlm^T), m < M
+ * Limits: K % 128 == 0, N % 64 == 0, M/bucket <= 1024, D <= 8192.
+ */
+size_t sf_gemm_workspace_bytes(int mcap, int N, int K);
+int sf_o_proj_residual(const uint16_t* o_bf, const uint16_t* x, const uint16_t* wo, int M, int K,
+                       int N, uint16_t* hp, void* workspace, size_t workspace_bytes, void* stream);
+int sf_rows_rmsnorm(const uint16_t* x, const int32_t* rows, const int32_t* count, int bucket,
+                    const uint16_t* w, int D, float eps, uint16_t* out, void* stream);
+int sf_ffn_gate_up(const uint16_t* zn, const int32_t* count, int bucket, const uint16_t* wg,
+                   const uint16_t* wu, int D, int I, uint16_t* act, void* stream);
+int sf_ffn_down_scatter(const uint16_t* act, const int32_t* count, int bucket, const int32_t* rows,
+                        const uint16_t* wd, int I, int D, uint16_t* ffn, void* workspace,
+                        size_t workspace_bytes, void* stream);
+int sf_residual_gather_add(const uint16_t* hp, const uint16_t* ffn, const int32_t* src, int B1,
+                           int N, int D, uint16_t* out, void* stream);
+int sf_lm_head(const uint16_t* x, int M, const uint16_t* w, int D, int V, uint16_t* logits,
+               void* stream);
 
 #ifdef __cplusplus
 }

@@ -39,10 +39,18 @@ SIGNATURES = {
                          _i, _i, _i, _i, _i, _vp, _vp, _vp, _sz, _vp]),
     "sf_attn_workspace_bytes": (_sz, [_i, _i, _i]),
     "sf_attn_prefix_block": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _ll, _ll, _vp, _vp, _vp,
-                                  _i, _i, _i, _i, _i, _i, _f, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+                                  _i, _i, _i, _i, _i, _i, _f, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
+                                  _vp]),
     "sf_chain_correct": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f,
                               _vp, _vp, _vp, _vp, _vp]),
     "sf_kv_append": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp, _i, _ll, _ll, _i, _vp]),
+    "sf_gemm_workspace_bytes": (_sz, [_i, _i, _i]),
+    "sf_o_proj_residual": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _vp, _sz, _vp]),
+    "sf_rows_rmsnorm": (_i, [_vp, _vp, _vp, _i, _vp, _i, _f, _vp, _vp]),
+    "sf_ffn_gate_up": (_i, [_vp, _vp, _i, _vp, _vp, _i, _i, _vp, _vp]),
+    "sf_ffn_down_scatter": (_i, [_vp, _vp, _i, _vp, _vp, _i, _i, _vp, _vp, _sz, _vp]),
+    "sf_residual_gather_add": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _vp]),
+    "sf_lm_head": (_i, [_vp, _i, _vp, _i, _i, _vp, _vp]),
 }
 
 
@@ -166,7 +174,9 @@ def attn_workspace_bytes(bucket: int, H: int, P: int) -> int:
 
 def attn_prefix_block(q_buf, kv_buf, prefix_k, prefix_v, page_table, P, page_size, page_stride,
                       head_stride, src, rows, count, bucket, B1, N, H, Hkv, hd, scaling,
-                      o32, o_bf, m_tab, z_tab, workspace, stream=None) -> None:
+                      o32, o_bf, m_tab, z_tab, workspace, prefix_len=None, stream=None) -> None:
+    """prefix_len: optional device int32[1] holding the prefix length; P is then
+    the capacity (grid / workspace size)."""
     BN = B1 * N
     _need(q_buf, "q_buf", torch.bfloat16, min_numel=(BN + 1) * H * hd)
     _need(kv_buf, "kv_buf", torch.bfloat16, min_numel=(BN + 1) * 2 * Hkv * hd)
@@ -185,12 +195,14 @@ def attn_prefix_block(q_buf, kv_buf, prefix_k, prefix_v, page_table, P, page_siz
     _need(z_tab, "z_tab", torch.float32, min_numel=BN * H, align=4)
     _need(workspace, "workspace", torch.uint8, min_numel=attn_workspace_bytes(bucket, H, P),
           align=256)
+    if prefix_len is not None:
+        _need(prefix_len, "prefix_len", torch.int32, numel=1, align=4)
     st = load().sf_attn_prefix_block(
         _ptr(q_buf), _ptr(kv_buf), _ptr(prefix_k) if P > 0 else None,
         _ptr(prefix_v) if P > 0 else None, _ptr(page_table) if P > 0 else None, P,
         page_size, page_stride, head_stride, _ptr(src), _ptr(rows), _ptr(count), bucket, B1, N, H,
-        Hkv, hd, float(scaling), _ptr(o32), _ptr(o_bf), _ptr(m_tab), _ptr(z_tab), _ptr(workspace),
-        workspace.numel(), _stream(stream))
+        Hkv, hd, float(scaling), _ptr(prefix_len) if P > 0 else None, _ptr(o32), _ptr(o_bf),
+        _ptr(m_tab), _ptr(z_tab), _ptr(workspace), workspace.numel(), _stream(stream))
     _check(st, "sf_attn_prefix_block")
 
 
@@ -223,3 +235,71 @@ def kv_append(kv_buf, row0, n_tok, Hkv, hd, k_cache, v_cache, page_table, page_s
                              _ptr(page_table), page_size, page_stride, head_stride, start_pos,
                              _stream(stream))
     _check(st, "sf_kv_append")
+
+
+def gemm_workspace_bytes(mcap: int, N: int, K: int) -> int:
+    return int(load().sf_gemm_workspace_bytes(mcap, N, K))
+
+
+def o_proj_residual(o_bf, x, wo, M, K, N, hp, workspace, stream=None) -> None:
+    _need(o_bf, "o_bf", torch.bfloat16, min_numel=M * K)
+    _need(x, "x", torch.bfloat16, min_numel=M * N)
+    _need(wo, "wo", torch.bfloat16, numel=N * K)
+    _need(hp, "hp", torch.bfloat16, min_numel=M * N)
+    _need(workspace, "workspace", torch.uint8, min_numel=gemm_workspace_bytes(M, N, K), align=256)
+    st = load().sf_o_proj_residual(_ptr(o_bf), _ptr(x), _ptr(wo), M, K, N, _ptr(hp),
+                                   _ptr(workspace), workspace.numel(), _stream(stream))
+    _check(st, "sf_o_proj_residual")
+
+
+def rows_rmsnorm(x, rows, count, bucket, w, D, eps, out, stream=None) -> None:
+    _need(x, "x", torch.bfloat16)
+    _need(rows, "rows", torch.int32, min_numel=bucket, align=4)
+    _need(count, "count", torch.int32, min_numel=1, align=4)
+    _need(w, "w", torch.bfloat16, numel=D)
+    _need(out, "out", torch.bfloat16, min_numel=bucket * D)
+    st = load().sf_rows_rmsnorm(_ptr(x), _ptr(rows), _ptr(count), bucket, _ptr(w), D, float(eps),
+                                _ptr(out), _stream(stream))
+    _check(st, "sf_rows_rmsnorm")
+
+
+def ffn_gate_up(zn, count, bucket, wg, wu, D, I, act, stream=None) -> None:
+    _need(zn, "zn", torch.bfloat16, min_numel=bucket * D)
+    _need(count, "count", torch.int32, min_numel=1, align=4)
+    _need(wg, "wg", torch.bfloat16, numel=I * D)
+    _need(wu, "wu", torch.bfloat16, numel=I * D)
+    _need(act, "act", torch.bfloat16, min_numel=bucket * I)
+    st = load().sf_ffn_gate_up(_ptr(zn), _ptr(count), bucket, _ptr(wg), _ptr(wu), D, I, _ptr(act),
+                               _stream(stream))
+    _check(st, "sf_ffn_gate_up")
+
+
+def ffn_down_scatter(act, count, bucket, rows, wd, I, D, ffn, workspace, stream=None) -> None:
+    _need(act, "act", torch.bfloat16, min_numel=bucket * I)
+    _need(count, "count", torch.int32, min_numel=1, align=4)
+    _need(rows, "rows", torch.int32, min_numel=bucket, align=4)
+    _need(wd, "wd", torch.bfloat16, numel=D * I)
+    _need(ffn, "ffn", torch.bfloat16)
+    _need(workspace, "workspace", torch.uint8, min_numel=gemm_workspace_bytes(bucket, D, I),
+          align=256)
+    st = load().sf_ffn_down_scatter(_ptr(act), _ptr(count), bucket, _ptr(rows), _ptr(wd), I, D,
+                                    _ptr(ffn), _ptr(workspace), workspace.numel(), _stream(stream))
+    _check(st, "sf_ffn_down_scatter")
+
+
+def residual_gather_add(hp, ffn, src, B1, N, D, out, stream=None) -> None:
+    _need(hp, "hp", torch.bfloat16, min_numel=B1 * N * D)
+    _need(ffn, "ffn", torch.bfloat16, min_numel=B1 * N * D)
+    _need(src, "src", torch.int32, min_numel=B1 * N, align=4)
+    _need(out, "out", torch.bfloat16, min_numel=B1 * N * D)
+    st = load().sf_residual_gather_add(_ptr(hp), _ptr(ffn), _ptr(src), B1, N, D, _ptr(out),
+                                       _stream(stream))
+    _check(st, "sf_residual_gather_add")
+
+
+def lm_head(x, M, w, D, V, logits, stream=None) -> None:
+    _need(x, "x", torch.bfloat16, min_numel=M * D)
+    _need(w, "w", torch.bfloat16, numel=V * D)
+    _need(logits, "logits", torch.bfloat16, min_numel=M * V)
+    st = load().sf_lm_head(_ptr(x), M, _ptr(w), D, V, _ptr(logits), _stream(stream))
+    _check(st, "sf_lm_head")

@@ -10,7 +10,12 @@ fastdllm_v2_folded.py:296-361 for the launch sequence, :117-220 for the math):
   sf_kv_append       optional in-place append (block commit)   (HIP)
   sf_attn_prefix_block  prefix + block attention with (m, Z)   (HIP)
   sf_chain_correct   folded rows' exact softmax update         (HIP)
-  o_proj + residual, FFN on the compacted rows, hidden update  (torch/hipBLASLt)
+  o_proj + residual for every row (M = B1*N)             (torch mm + add, hipBLASLt)
+  sf_rows_rmsnorm     post-attention RMSNorm of recomputed rows  (HIP)
+  sf_ffn_gate_up      gate/up GEMM + SiLU*mul on compacted rows  (HIP)
+  sf_ffn_down_scatter down GEMM, scattered to the per-row FFN table (HIP)
+  sf_residual_gather_add  h = hp + ffn[src] (folded rows reuse)  (HIP)
+and after the last layer the final RMSNorm (HIP) and the lm_head (hipBLASLt).
 
 Nothing here syncs with the host inside the layer loop: ``count`` stays on the
 device and every kernel reads it.  The only host syncs are the parent map
@@ -25,7 +30,6 @@ from dataclasses import dataclass, field
 from typing import Dict, List, Optional, Tuple
 
 import torch
-import torch.nn.functional as F
 
 from specfold_amd import _lib
 from specfold_amd.kv_cache import PagedKVCache, cache_length, prefix_view
@@ -89,8 +93,19 @@ class _Buffers:
         self.z_tab = torch.zeros(BN, H, dtype=torch.float32, device=dev)
         self.hp = torch.zeros(BN + 1, D, dtype=bf, device=dev)      # row BN stays zero (trash)
         self.ffn = torch.zeros(BN + 1, D, dtype=bf, device=dev)
-        self.n_flat = torch.arange(N, device=dev, dtype=torch.int64).repeat(B1)
+        self.zn = torch.zeros(bucket, D, dtype=bf, device=dev)
+        self.act = torch.zeros(bucket, eng.I, dtype=bf, device=dev)
+        self.hid = torch.zeros(2, BN, D, dtype=bf, device=dev)       # layer outputs, ping-pong
+        self.final = torch.zeros(BN, D, dtype=bf, device=dev)
+        self.attn_out = torch.zeros(BN, D, dtype=bf, device=dev)
+        self.cos = torch.zeros(N, hd, dtype=bf, device=dev)    # RoPE tables of the step
+        self.sin = torch.zeros(N, hd, dtype=bf, device=dev)
+        self.all_rows = torch.arange(BN, **i32)
+        self.all_count = torch.full((1,), BN, **i32)
         nq = (H + 2 * Hkv) * hd
+        self.ws_gemm = torch.empty(max(_lib.gemm_workspace_bytes(BN, D, H * hd),
+                                       _lib.gemm_workspace_bytes(bucket, D, eng.I), 256),
+                                   dtype=torch.uint8, device=dev)
         self.ws_qkv = torch.empty(max(_lib.qkv_workspace_bytes(bucket, D, nq), 256),
                                   dtype=torch.uint8, device=dev)
         self.ws_attn = torch.empty(max(_lib.attn_workspace_bytes(bucket, H, P), 256),
@@ -103,6 +118,7 @@ class FoldedVerifyEngine:
     def __init__(self, model, gate_mode: int = _lib.SF_GATE_MODEL_DTYPE,
                  rms_eps: Optional[float] = None, has_qkv_bias: Optional[bool] = None):
         _lib.load()  # fail loudly, before any work, if the HIP library is not built
+        model.requires_grad_(False)
         self.model = model
         base = model.model
         cfg = model.config
@@ -115,6 +131,8 @@ class FoldedVerifyEngine:
         self.hd = attn0.head_dim
         self.scaling = float(attn0.scaling)
         self.D = base.embed_tokens.weight.shape[1]
+        self.I = self.layers[0].mlp.gate_proj.weight.shape[0]
+        self.V = model.lm_head.weight.shape[0]
         self.device = base.embed_tokens.weight.device
         if base.embed_tokens.weight.dtype != torch.bfloat16:
             raise TypeError("the HIP verify step runs bf16 models")
@@ -132,6 +150,10 @@ class FoldedVerifyEngine:
                  if use_bias and a.q_proj.bias is not None else None)
             self._packed.append((w, b))
         self._bufs: Dict[Tuple[int, int, int], _Buffers] = {}
+        # HIP graphs of the layer loop, keyed by shape / prefix / delta / cache
+        self.use_graphs = True
+        self.max_graphs = 4
+        self._graphs: Dict[tuple, tuple] = {}
 
     # ------------------------------------------------------------------------
     def buffers(self, B1: int, N: int, bucket: int, P: int) -> _Buffers:
@@ -181,61 +203,21 @@ class FoldedVerifyEngine:
         par = torch.tensor(par_host, dtype=torch.int32).to(self.device, non_blocking=True)
 
         P = cache_length(cache)
-        buf = self.buffers(B1, N, bucket, P)
+        P_alloc = cache.capacity if isinstance(cache, PagedKVCache) else P
+        buf = self.buffers(B1, N, bucket, P_alloc)
         base = self.model.model
-        hidden = base.embed_tokens(batched_input).reshape(BN, self.D)
-        cos, sin = self.rope_tables(hidden, P, N)
-        H, Hkv, hd, D = self.H, self.Hkv, self.hd, self.D
-        src_flat = None
-
-        for li, lyr in enumerate(self.layers):
-            if teacher is not None and li in teacher:
-                hidden = teacher[li].reshape(BN, D).to(torch.bfloat16).contiguous()
-            hidden = hidden.contiguous()
-            count = buf.count_slab[li:li + 1]
-            segcnt = buf.segcnt_slab[li * B1:(li + 1) * B1]
-            _lib.fold_gate(hidden, par, lyr.input_layernorm.weight, B1, N, bucket, delta, self.eps,
-                           self.gate_mode, buf.rec, buf.f, buf.src, buf.rows, count, buf.seg,
-                           segcnt, buf.rstd, buf.xn)
-            w_qkv, b_qkv = self._packed[li]
-            _lib.qkv_rope(buf.xn, buf.rows, count, bucket, BN, w_qkv, b_qkv, cos, sin, q_scale,
-                          N, D, H, Hkv, hd, buf.q_buf, buf.kv_buf, buf.ws_qkv)
-            if append:
-                cache.append_rows(li, buf.kv_buf, 0, N)
-            pv = prefix_view(cache, li)
-            Pl = pv.length if pv is not None else 0
-            _lib.attn_prefix_block(
-                buf.q_buf, buf.kv_buf, pv.k if pv else None, pv.v if pv else None,
-                pv.page_table if pv else None, Pl, pv.page_size if pv else 1,
-                pv.page_stride if pv else 0, pv.head_stride if pv else 0,
-                buf.src, buf.rows, count, bucket, B1, N, H, Hkv, hd, self.scaling,
-                buf.o32, buf.o_bf, buf.m_tab, buf.z_tab, buf.ws_attn)
-            _lib.chain_correct(buf.q_buf, buf.kv_buf, buf.src, par, buf.rec, buf.seg, segcnt,
-                               B1, N, H, Hkv, hd, self.scaling, buf.o32, buf.o_bf, buf.m_tab,
-                               buf.z_tab)
-
-            # o_proj + residual for every row (fastdllm_v2_folded.py:207-209)
-            attn_out = torch.mm(buf.o_bf, lyr.self_attn.o_proj.weight.t())
-            torch.add(hidden, attn_out, out=buf.hp[:BN])
-            # FFN on the compacted rows; slots past count hold BN -> the zero row
-            rows_l = buf.rows.long()
-            z = lyr.post_attention_layernorm(buf.hp.index_select(0, rows_l))
-            mlp = lyr.mlp
-            act = F.silu(mlp.gate_proj(z)) * mlp.up_proj(z)
-            buf.ffn.index_copy_(0, rows_l, mlp.down_proj(act))
-            # folded rows reuse the FFN output of their nearest recomputing ancestor
-            src_flat = buf.src.long() * N + buf.n_flat
-            new_hidden = buf.hp[:BN] + buf.ffn.index_select(0, src_flat)
-            if trace is not None:
-                trace.append(dict(
-                    h_in=hidden.clone(), rec=buf.rec.clone(), rows=buf.rows.clone(),
-                    count=count.clone(), src=buf.src.clone(), f=buf.f.clone(),
-                    seg=buf.seg.clone(), segcnt=segcnt.clone(), rstd=buf.rstd.clone(),
-                    xn=buf.xn.clone(), q=buf.q_buf.clone(), kv=buf.kv_buf.clone(),
-                    o32=buf.o32.clone(), o_bf=buf.o_bf.clone(), m=buf.m_tab.clone(),
-                    z=buf.z_tab.clone(), hp=buf.hp[:BN].clone(), ffn=buf.ffn.clone(),
-                    h_out=new_hidden.clone()))
-            hidden = new_hidden
+        D = self.D
+        cos, sin = self.rope_tables(base.embed_tokens.weight, P, N)
+        buf.cos.copy_(cos)
+        buf.sin.copy_(sin)
+        graphable = (self.use_graphs and trace is None and teacher is None and not append
+                     and q_scale is None)
+        if graphable:
+            hidden = self._replay(buf, batched_input, par, cache, P, delta, bucket)
+        else:
+            hidden = self._run_layers(buf, batched_input, par, cache, delta, bucket,
+                                      append=append, q_scale=q_scale, trace=trace,
+                                      teacher=teacher)
 
         if append:
             cache.advance(N)
@@ -252,12 +234,133 @@ class FoldedVerifyEngine:
                                 compute_logits=compute_logits, q_scale=q_scale, trace=trace,
                                 teacher=teacher, stats=stats)
         self.last_hidden = hidden
-        self._last = dict(B1=B1, N=N, bucket=bucket, cache=cache, par=par, cos=cos, sin=sin,
-                          q_scale=q_scale, hidden=hidden, delta=delta)
+        self._last = dict(B1=B1, N=N, bucket=bucket, cache=cache, par=par, cos=buf.cos,
+                          sin=buf.sin, q_scale=q_scale, hidden=hidden, delta=delta)
         if not compute_logits:
             return None
-        final = base.norm(hidden.view(B1, N, D))
-        return self.model.lm_head(final)
+        _lib.rows_rmsnorm(hidden, buf.all_rows, buf.all_count, BN, base.norm.weight, D, self.eps,
+                          buf.final)
+        # lm_head over all BN rows (M = BN): hipBLASLt, a fresh tensor per call
+        logits = torch.mm(buf.final, self.model.lm_head.weight.t())
+        return logits.view(B1, N, self.V)
+
+    # ------------------------------------------------------------------------
+    def _run_layers(self, buf: _Buffers, tokens: torch.Tensor, par: torch.Tensor, cache,
+                    delta: float, bucket: int, append: bool = False,
+                    q_scale: Optional[torch.Tensor] = None, trace: Optional[list] = None,
+                    teacher: Optional[Dict[int, torch.Tensor]] = None) -> torch.Tensor:
+        """Embedding and every layer: device launches only (no host sync), so the
+        sequence can be captured in a HIP graph.  RoPE tables come from buf.cos /
+        buf.sin and a paged cache's length from its device copy, so a captured
+        sequence stays valid as the cache grows.  Returns the last hidden state."""
+        B1, N = tokens.shape
+        BN = B1 * N
+        H, Hkv, hd, D = self.H, self.Hkv, self.hd, self.D
+        base = self.model.model
+        hidden = base.embed_tokens(tokens).reshape(BN, D)
+        cos, sin = buf.cos, buf.sin
+        for li, lyr in enumerate(self.layers):
+            if teacher is not None and li in teacher:
+                hidden = teacher[li].reshape(BN, D).to(torch.bfloat16).contiguous()
+            hidden = hidden.contiguous()
+            count = buf.count_slab[li:li + 1]
+            segcnt = buf.segcnt_slab[li * B1:(li + 1) * B1]
+            _lib.fold_gate(hidden, par, lyr.input_layernorm.weight, B1, N, bucket, delta, self.eps,
+                           self.gate_mode, buf.rec, buf.f, buf.src, buf.rows, count, buf.seg,
+                           segcnt, buf.rstd, buf.xn)
+            w_qkv, b_qkv = self._packed[li]
+            _lib.qkv_rope(buf.xn, buf.rows, count, bucket, BN, w_qkv, b_qkv, cos, sin, q_scale,
+                          N, D, H, Hkv, hd, buf.q_buf, buf.kv_buf, buf.ws_qkv)
+            if append:
+                cache.append_rows(li, buf.kv_buf, 0, N)
+            self._attention(buf, cache, li, count, bucket, B1, N)
+            _lib.chain_correct(buf.q_buf, buf.kv_buf, buf.src, par, buf.rec, buf.seg, segcnt,
+                               B1, N, H, Hkv, hd, self.scaling, buf.o32, buf.o_bf, buf.m_tab,
+                               buf.z_tab)
+
+            # o_proj + residual for every row (fastdllm_v2_folded.py:207-209): M = BN is
+            # a regular GEMM shape, where hipBLASLt beats the skinny-M streaming kernel;
+            # mm then add keeps the reference's two bf16 roundings
+            torch.mm(buf.o_bf, lyr.self_attn.o_proj.weight.t(), out=buf.attn_out)
+            torch.add(hidden, buf.attn_out, out=buf.hp[:BN])
+            # FFN on the compacted rows (:211-217)
+            mlp = lyr.mlp
+            _lib.rows_rmsnorm(buf.hp, buf.rows, count, bucket, lyr.post_attention_layernorm.weight,
+                              D, self.eps, buf.zn)
+            _lib.ffn_gate_up(buf.zn, count, bucket, mlp.gate_proj.weight, mlp.up_proj.weight, D,
+                             self.I, buf.act)
+            _lib.ffn_down_scatter(buf.act, count, bucket, buf.rows, mlp.down_proj.weight, self.I, D,
+                                  buf.ffn, buf.ws_gemm)
+            # folded rows reuse the FFN output of their nearest recomputing ancestor (:218)
+            new_hidden = buf.hid[li % 2]
+            _lib.residual_gather_add(buf.hp, buf.ffn, buf.src, B1, N, D, new_hidden)
+            if trace is not None:
+                trace.append(dict(
+                    h_in=hidden.clone(), rec=buf.rec.clone(), rows=buf.rows.clone(),
+                    count=count.clone(), src=buf.src.clone(), f=buf.f.clone(),
+                    seg=buf.seg.clone(), segcnt=segcnt.clone(), rstd=buf.rstd.clone(),
+                    xn=buf.xn.clone(), q=buf.q_buf.clone(), kv=buf.kv_buf.clone(),
+                    o32=buf.o32.clone(), o_bf=buf.o_bf.clone(), m=buf.m_tab.clone(),
+                    z=buf.z_tab.clone(), hp=buf.hp[:BN].clone(), ffn=buf.ffn.clone(),
+                    h_out=new_hidden.clone()))
+            hidden = new_hidden
+        return hidden
+
+    def _attention(self, buf: _Buffers, cache, li: int, count, bucket: int, B1: int, N: int):
+        pv = prefix_view(cache, li)
+        if pv is None:
+            P_arg, plen = 0, None
+        elif pv.length_dev is not None:
+            P_arg, plen = pv.capacity, pv.length_dev
+        else:
+            P_arg, plen = pv.length, None
+        _lib.attn_prefix_block(
+            buf.q_buf, buf.kv_buf, pv.k if pv else None, pv.v if pv else None,
+            pv.page_table if pv else None, P_arg, pv.page_size if pv else 1,
+            pv.page_stride if pv else 0, pv.head_stride if pv else 0,
+            buf.src, buf.rows, count, bucket, B1, N, self.H, self.Hkv, self.hd, self.scaling,
+            buf.o32, buf.o_bf, buf.m_tab, buf.z_tab, buf.ws_attn, prefix_len=plen)
+
+    def _graph_key(self, buf: _Buffers, cache, P: int, delta: float, bucket: int):
+        if isinstance(cache, PagedKVCache):
+            # the prefix length is read on the device: one graph for every length
+            P = -1
+            ck = (id(cache), cache.k_pages.data_ptr(), cache.v_pages.data_ptr(),
+                  cache.page_table.data_ptr(), cache.length_dev.data_ptr(), cache.capacity)
+        elif cache is None:
+            ck = None
+        else:
+            ck = tuple((prefix_view(cache, li).k.data_ptr(), prefix_view(cache, li).v.data_ptr())
+                       if prefix_view(cache, li) is not None else (0, 0)
+                       for li in range(self.L))
+        return (buf.key, id(buf), P, float(delta), bucket, self.gate_mode, ck)
+
+    def _replay(self, buf: _Buffers, tokens: torch.Tensor, par: torch.Tensor, cache, P: int,
+                delta: float, bucket: int):
+        """Run the layers through a captured HIP graph (captured on first use for
+        this shape / prefix length / cache); inputs go through static buffers."""
+        key = self._graph_key(buf, cache, P, delta, bucket)
+        entry = self._graphs.get(key)
+        if entry is None:
+            static_tok = tokens.clone()
+            static_par = par.clone()
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):      # warm-up launch outside the capture
+                self._run_layers(buf, static_tok, static_par, cache, delta, bucket)
+            torch.cuda.current_stream().wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                out = self._run_layers(buf, static_tok, static_par, cache, delta, bucket)
+            entry = (graph, static_tok, static_par, out)
+            while len(self._graphs) >= self.max_graphs:
+                self._graphs.pop(next(iter(self._graphs)))
+            self._graphs[key] = entry
+        graph, static_tok, static_par, out = entry
+        static_tok.copy_(tokens)
+        static_par.copy_(par)
+        graph.replay()
+        return out
 
     # ------------------------------------------------------------------------
     def profile_launchers(self, li: int = -1):
@@ -288,19 +391,43 @@ class FoldedVerifyEngine:
                           st["q_scale"], N, D, H, Hkv, hd, buf.q_buf, buf.kv_buf, buf.ws_qkv)
 
         def attn():
-            _lib.attn_prefix_block(
-                buf.q_buf, buf.kv_buf, pv.k if pv else None, pv.v if pv else None,
-                pv.page_table if pv else None, pv.length if pv else 0,
-                pv.page_size if pv else 1, pv.page_stride if pv else 0,
-                pv.head_stride if pv else 0, buf.src, buf.rows, count, bucket, B1, N, H, Hkv, hd,
-                self.scaling, buf.o32, buf.o_bf, buf.m_tab, buf.z_tab, buf.ws_attn)
+            self._attention(buf, cache, li, count, bucket, B1, N)
 
         def chain():
             _lib.chain_correct(buf.q_buf, buf.kv_buf, buf.src, st["par"], buf.rec, buf.seg, segcnt,
                                B1, N, H, Hkv, hd, self.scaling, buf.o32, buf.o_bf, buf.m_tab,
                                buf.z_tab)
 
-        out = dict(qkv=qkv, attn=attn, chain=chain, gate=gate)
+        mlp = lyr.mlp
+
+        def o_proj():
+            torch.mm(buf.o_bf, lyr.self_attn.o_proj.weight.t(), out=buf.attn_out)
+            torch.add(hidden, buf.attn_out, out=buf.hp[:BN])
+
+        def post_norm():
+            _lib.rows_rmsnorm(buf.hp, buf.rows, count, bucket, lyr.post_attention_layernorm.weight,
+                              D, self.eps, buf.zn)
+
+        def gate_up():
+            _lib.ffn_gate_up(buf.zn, count, bucket, mlp.gate_proj.weight, mlp.up_proj.weight, D,
+                             self.I, buf.act)
+
+        def down():
+            _lib.ffn_down_scatter(buf.act, count, bucket, buf.rows, mlp.down_proj.weight, self.I,
+                                  D, buf.ffn, buf.ws_gemm)
+
+        scratch = torch.empty_like(buf.hid[0])
+
+        def resid():
+            _lib.residual_gather_add(buf.hp, buf.ffn, buf.src, B1, N, D, scratch)
+
+        logits = torch.empty(BN, self.V, dtype=torch.bfloat16, device=self.device)
+
+        def lm_head():
+            torch.mm(buf.final, self.model.lm_head.weight.t(), out=logits)
+
+        out = dict(qkv=qkv, attn=attn, chain=chain, o_proj=o_proj, post_norm=post_norm,
+                   gate_up=gate_up, down=down, resid=resid, lm_head=lm_head, gate=gate)
         if isinstance(cache, PagedKVCache) and cache.length + N <= cache.capacity:
             def append():
                 # writes past the logical end of the cache: never read, length unchanged

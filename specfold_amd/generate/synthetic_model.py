@@ -70,4 +70,5 @@ def build_qwen2(shape: ModelShape, seed: int, device="cpu", dtype=torch.bfloat16
     rot.original_inv_freq = rot.inv_freq.clone()
     rot.attention_scaling = scaling
     model.eval()
+    model.requires_grad_(False)
     return model

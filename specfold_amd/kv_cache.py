@@ -33,6 +33,8 @@ class PrefixView:
     page_size: int
     page_stride: int
     head_stride: int
+    capacity: int = 0                        # grid / workspace size when length_dev is used
+    length_dev: Optional[torch.Tensor] = None  # device int32[1] copy of length
 
 
 class PagedKVCache:
@@ -59,6 +61,8 @@ class PagedKVCache:
         self.page_table_cpu = perm.to(torch.int32)
         self.page_table = self.page_table_cpu.to(self.device)
         self.length = 0
+        # device copy of the length, read by the attention kernel (graph-stable)
+        self.length_dev = torch.zeros(1, dtype=torch.int32, device=self.device)
 
     # -- the reference cache contract ------------------------------------------------
     def get_seq_length(self, layer_idx: int = 0) -> int:
@@ -84,7 +88,8 @@ class PagedKVCache:
         ps, hd = self.page_size, self.hd
         return PrefixView(k=self.k_pages[li], v=self.v_pages[li], page_table=self.page_table,
                           length=self.length, page_size=ps, page_stride=self.Hkv * ps * hd,
-                          head_stride=ps * hd)
+                          head_stride=ps * hd, capacity=self.capacity,
+                          length_dev=self.length_dev)
 
     def append_rows(self, li: int, kv_buf: torch.Tensor, row0: int, n_tok: int,
                     start_pos: Optional[int] = None) -> None:
@@ -100,6 +105,7 @@ class PagedKVCache:
         if self.length + n_tok > self.capacity:
             raise ValueError("KV cache full")
         self.length += n_tok
+        self.length_dev.fill_(self.length)
 
     def load_dense(self, kv: Sequence[Tuple[torch.Tensor, torch.Tensor]]) -> None:
         """Fill from per-layer ([1, Hkv, P, hd], [1, Hkv, P, hd]) tensors (any device)."""
@@ -118,6 +124,7 @@ class PagedKVCache:
                 x = x.reshape(self.Hkv, npg, ps, self.hd).permute(1, 0, 2, 3)
                 dst[li].index_copy_(0, idx, x.contiguous())
         self.length = P
+        self.length_dev.fill_(P)
 
 
 def contiguous_view(k: torch.Tensor, v: torch.Tensor) -> PrefixView:
@@ -148,7 +155,7 @@ def prefix_view(cache, li: int) -> Optional[PrefixView]:
     if cache is None:
         return None
     if isinstance(cache, PagedKVCache):
-        return cache.view(li) if cache.length > 0 else None
+        return cache.view(li)
     if len(cache) <= li:
         return None
     if hasattr(cache, "layers") and not hasattr(cache, "__getitem__"):

@@ -158,3 +158,40 @@ def test_bucket_overflow_recomputes_full():
     full = eng.forward(t, cache, case.delta)
     small = eng.forward(t, cache, case.delta, bucket=8)   # main alone needs 32 rows
     assert torch.equal(full, small)
+
+
+def test_graph_replays_match_eager():
+    """The layer loop replayed from a captured HIP graph equals the eager launch
+    sequence bit for bit, on every replay, with eager work and host syncs in
+    between, and when the prefix grows (a new capture)."""
+    case = make_case(SHAPE_G7, 12, P=130, delta=0.05)
+    model = to_gpu_model(case.model_cpu)
+    eng = FoldedVerifyEngine(model)
+    cache = PagedKVCache(len(case.kv), case.kv[0][0].shape[1], 128, 1024, page_size=16,
+                         device="cuda", page_order="shuffled", seed=1)
+    cache.load_dense(case.kv)
+    t = case.tokens.cuda()
+    gen = torch.Generator().manual_seed(3)
+    others = [t.clone() for _ in range(3)]
+    for o in others:
+        o[1:, 0] = torch.randint(0, SHAPE_G7.vocab, (t.shape[0] - 1,), generator=gen).cuda()
+    eng.use_graphs = False
+    eager = [eng.forward(x, cache, case.delta) for x in [t] + others]
+    eng.use_graphs = True
+    for rep in range(3):
+        for x, ref in zip([t] + others, eager):
+            out = eng.forward(x, cache, case.delta)
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref), f"replay {rep} differs from eager"
+            _ = (out.float() * 2).sum().item()          # unrelated eager work + sync
+    # grow the prefix by one block commit: a new graph for the new length
+    blk = torch.randint(0, SHAPE_G7.vocab, (1, 32), generator=gen).cuda()
+    eng.use_graphs = False
+    from specfold_amd import _lib
+    eng.gate_mode = _lib.SF_GATE_ALL
+    eng.forward(blk, cache, 0.0, append=True)
+    eng.gate_mode = _lib.SF_GATE_MODEL_DTYPE
+    ref2 = eng.forward(t, cache, case.delta)
+    eng.use_graphs = True
+    for _ in range(2):
+        assert torch.equal(eng.forward(t, cache, case.delta), ref2)

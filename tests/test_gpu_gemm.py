@@ -1,0 +1,115 @@
+"""The weight-streaming GEMM entry points against PyTorch references of the same
+ops computed in fp64 on the CPU and rounded at the reference's bf16 rounding
+points.  Tolerance: at most 0.5% of outputs may differ, each by at most one bf16
+ulp (2^-7 relative) of the stated scale — the fp32 accumulation lands on the
+other side of a rounding tie now and then (torch's own fp32 GEMM does too)."""
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from specfold_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+
+def close_bf16(a, b, frac=5e-3, scale=None, atol=None):
+    """scale: magnitude the rounding error is relative to (defaults to |b|; for a
+    residual sum x + y it is |x + y| + |y|: one ulp of y, which survives
+    cancellation, plus the re-rounding of the sum).  atol: absolute slack for
+    fp32 accumulation under cancellation (see acc_bound)."""
+    a = a.float().cpu()
+    b = b.float().cpu()
+    d = (a - b).abs()
+    sc = b.abs() if scale is None else scale.float().cpu().abs()
+    tol = 2 ** -7 * sc + 1e-6
+    if atol is not None:
+        tol = tol + atol.float().cpu()
+    bad = d > tol
+    diff = (d > 0).float().mean().item()
+    assert int(bad.sum()) == 0, f"{int(bad.sum())} elements beyond 2 ulps, max {d.max().item()}"
+    assert diff <= frac, f"{diff:.4f} of elements differ"
+
+
+def mm64(a, w):
+    """a @ w^T in fp64 on the CPU, rounded to bf16 (a bf16 GEMM output)."""
+    return (a.double().cpu() @ w.double().cpu().t()).to(torch.bfloat16)
+
+
+def acc_bound(a, w):
+    """Statistical bound of fp32 accumulation error of a K-term dot product:
+    2 * sqrt(K) * 2^-24 * sum_k |a_k w_k|.  Matters only where the terms cancel
+    (an exact result far below sum |a_k w_k|)."""
+    K = a.shape[-1]
+    return 2 * K ** 0.5 * 2 ** -24 * (a.double().abs().cpu() @ w.double().abs().cpu().t())
+
+
+def rnd(*shape, std=1.0, gen=None):
+    return (std * torch.randn(*shape, generator=gen)).to(torch.bfloat16).cuda()
+
+
+@pytest.mark.parametrize("M", [1, 37, 128, 200, 256])
+def test_o_proj_residual(M):
+    g = torch.Generator().manual_seed(M)
+    K, N = 3584, 3584
+    o, x, w = rnd(M, K, gen=g), rnd(M, N, gen=g), rnd(N, K, std=0.02, gen=g)
+    hp = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    ws = torch.empty(_lib.gemm_workspace_bytes(M, N, K), dtype=torch.uint8, device="cuda")
+    _lib.o_proj_residual(o, x, w, M, K, N, hp, ws)
+    mm = mm64(o, w)
+    ref = (x.float().cpu() + mm.float()).to(torch.bfloat16)
+    close_bf16(hp, ref, scale=ref.float().abs() + mm.float().abs(), atol=acc_bound(o, w))
+
+
+@pytest.mark.parametrize("count", [1, 39, 117, 130, 256])
+def test_ffn_path(count):
+    g = torch.Generator().manual_seed(count)
+    D, I, BN, bucket = 1536, 8960, 256, 256
+    hp = rnd(BN + 1, D, gen=g)
+    perm = torch.randperm(BN, generator=g)[:count].sort().values
+    rows = torch.full((bucket,), BN, dtype=torch.int32)
+    rows[:count] = perm.to(torch.int32)
+    rows, cnt = rows.cuda(), torch.tensor([count], dtype=torch.int32).cuda()
+    lnw = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).cuda()
+    wg, wu, wd = rnd(I, D, std=0.02, gen=g), rnd(I, D, std=0.02, gen=g), rnd(D, I, std=0.02, gen=g)
+    zn = torch.zeros(bucket, D, dtype=torch.bfloat16, device="cuda")
+    act = torch.zeros(bucket, I, dtype=torch.bfloat16, device="cuda")
+    ffn = torch.zeros(BN + 1, D, dtype=torch.bfloat16, device="cuda")
+    ws = torch.empty(_lib.gemm_workspace_bytes(bucket, D, I), dtype=torch.uint8, device="cuda")
+    _lib.rows_rmsnorm(hp, rows, cnt, bucket, lnw, D, 1e-6, zn)
+    _lib.ffn_gate_up(zn, cnt, bucket, wg, wu, D, I, act)
+    _lib.ffn_down_scatter(act, cnt, bucket, rows, wd, I, D, ffn, ws)
+    torch.cuda.synchronize()
+    r = rows[:count].long()
+    x = hp[r].float()
+    z_ref = lnw * (x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6)).to(torch.bfloat16)
+    # two roundings (x*rstd, then *w): a flip of the inner one can show as 2 ulps
+    close_bf16(zn[:count], z_ref, scale=2 * z_ref.float().abs())
+    z = zn[:count]
+    gt = mm64(z, wg)
+    up = mm64(z, wu)
+    act_ref = F.silu(gt) * up
+    # x*sigmoid(x) has condition number |1 + x(1 - sigmoid(x))| <= 1 + |x|: a 1-ulp
+    # change of the gate GEMM output moves act by up to (1 + |g|) ulps
+    close_bf16(act[:count], act_ref, scale=act_ref.float().abs() * (2 + gt.float().abs()),
+               atol=(acc_bound(z, wg) + acc_bound(z, wu)) * (1 + up.double().abs()))
+    close_bf16(ffn[r], mm64(act[:count], wd), atol=acc_bound(act[:count], wd))
+    untouched = torch.ones(BN + 1, dtype=torch.bool)
+    untouched[r.cpu()] = False
+    assert torch.all(ffn[untouched.cuda()] == 0)
+
+
+def test_residual_gather_add_and_lm_head():
+    g = torch.Generator().manual_seed(5)
+    B1, N, D, V = 8, 32, 3584, 152064
+    hp, ffn = rnd(B1 * N, D, gen=g), rnd(B1 * N + 1, D, gen=g)
+    src = torch.randint(0, B1, (B1 * N,), generator=g, dtype=torch.int32).cuda()
+    out = torch.empty(B1 * N, D, dtype=torch.bfloat16, device="cuda")
+    _lib.residual_gather_add(hp, ffn, src, B1, N, D, out)
+    n = torch.arange(N).repeat(B1).cuda()
+    ref = hp + ffn[src.long() * N + n]
+    assert torch.equal(out, ref)
+    w = rnd(V, D, std=0.02, gen=g)
+    logits = torch.empty(B1 * N, V, dtype=torch.bfloat16, device="cuda")
+    _lib.lm_head(out, B1 * N, w, D, V, logits)
+    close_bf16(logits, mm64(out, w), atol=acc_bound(out, w))
