@@ -80,8 +80,14 @@ int sf_fold_gate(const uint16_t* hidden, const int32_t* par, const uint16_t* ln_
  * (specfold/generate/triton_kernels.py:29-87), i.e. the reference's
  * q/k/v_proj + rotate_half RoPE on recomputed rows
  * (specfold/generate/fastdllm_v2_folded.py:151-161).  The RMSNorm is applied by
- * sf_fold_gate (xn).  w_qkv = cat(Wq, Wk, Wv) [(H+2Hkv)*hd, D]
- * (:77-87 packing); b_qkv may be NULL (NLD: no bias).  cos/sin bf16 [N, hd].
+ * sf_fold_gate (xn).  w_qkv = cat(Wq, Wk, Wv) [(H+2Hkv)*hd, D] in the packed
+ * layout of sf_pack_weight (:77-87 packing); b_qkv may be NULL (NLD: no bias).
+ * The workspace (sf_qkv_workspace_bytes) holds the GEMM's fp32 partial slots
+ * (section (6)).  cos/sin bf16: with
+ * pos0 == NULL they are [N, hd] tables of the block; otherwise [table_rows, hd]
+ * tables over absolute positions and block position n uses row *pos0 + n
+ * (pos0 = the device-side prefix length; clamped to the table), so a captured
+ * launch stays valid as the prefix grows.
  * q_scale (optional, fp32 [N]) multiplies roped q by bf16(q_scale[n]) — the
  * llama-4 attention scale of specfold/generate/nld_folded.py:37-53, 175-176.
  * Limits: hd == 128, D % 128 == 0, bucket <= 1024.
@@ -89,7 +95,8 @@ int sf_fold_gate(const uint16_t* hidden, const int32_t* par, const uint16_t* ln_
 size_t sf_qkv_workspace_bytes(int bucket, int D, int n_qkv);
 int sf_qkv_rope(const uint16_t* xn, const int32_t* rows, const int32_t* count, int bucket, int BN,
                 const uint16_t* w_qkv, const uint16_t* b_qkv, const uint16_t* cos_tab,
-                const uint16_t* sin_tab, const float* q_scale, int N, int D, int H, int Hkv, int hd,
+                const uint16_t* sin_tab, const int32_t* pos0, int table_rows,
+                const float* q_scale, int N, int D, int H, int Hkv, int hd,
                 uint16_t* q_buf, uint16_t* kv_buf, void* workspace, size_t workspace_bytes,
                 void* stream);
 
@@ -147,10 +154,23 @@ int sf_kv_append(const uint16_t* kv_buf, int row0, int n_tok, int Hkv, int hd, u
  * specfold/generate/fastdllm_v2_folded.py:207-218; Triton
  * fused_ln_gateup_silu_kernel / fused_down_residual_scatter_kernel,
  * specfold/generate/triton_kernels.py:102-194, and the torch addmm/index ops of
- * the fused path, fastdllm_v2_folded.py:351-361).  All GEMMs stream the bf16
- * weight [N, K] once on bf16 MFMA with fp32 accumulation; split-K partials go to
- * a caller workspace of sf_gemm_workspace_bytes(M or bucket, N, K) bytes.
+ * the fused path, fastdllm_v2_folded.py:351-361).
  *
+ * Weights.  Every GEMM entry point here and sf_qkv_rope take their weight
+ * [N, K] in the PACKED fragment-major layout that sf_pack_weight writes from a
+ * row-major bf16 matrix (16-byte word (t, c, l) = W[16t + l%16][32c + 8(l/16) ..
+ * +8], t < N/16, c < K/32, l < 64): each wave's weight stream is then one
+ * sequential read.  Packing is done once per model (the counterpart of the
+ * reference's _pack_layer_weights, fastdllm_v2_folded.py:77-87).
+ *
+ * Workspace.  The weight is streamed once on bf16 MFMA with fp32 accumulation,
+ * split stream-K over a fixed grid: tiles computed by several workgroups go
+ * through fp32 partial slots in a caller workspace of
+ * sf_gemm_workspace_bytes(M or bucket, N, K) bytes (sf_qkv_workspace_bytes for
+ * sf_qkv_rope), summed in a fixed order by a fix-up kernel (deterministic).
+ * Calls sharing a workspace must not overlap.
+ *
+ * sf_pack_weight        out = packed(w), w row-major [N, K]; N % 16 == 0, K % 128 == 0
  * sf_o_proj_residual    hp[r] = bf16(x[r] + bf16(o_bf[r] . Wo^T)), r < M (all rows)
  * sf_rows_rmsnorm       out[m] = bf16(w * bf16(x[rows[m]] * rstd)), m < count
  * sf_ffn_gate_up        act[m] = bf16(bf16(silu(bf16(zn[m] . Wg^T))) * bf16(zn[m] . Wu^T))
@@ -158,9 +178,10 @@ int sf_kv_append(const uint16_t* kv_buf, int row0, int n_tok, int Hkv, int hd, u
  * sf_residual_gather_add out[r] = bf16(hp[r] + ffn[src[r]*N + r%N]), r < B1*N
  *                       (folded rows take their nearest recomputing ancestor's FFN)
  * sf_lm_head            logits[m] = bf16(x[m] . Wlm^T), m < M
- * Limits: K % 128 == 0, N % 64 == 0, M/bucket <= 1024, D <= 8192.
+ * Limits: K % 128 == 0, N % 64 == 0 (lm_head: V % 128), M/bucket <= 1024, D <= 8192.
  */
 size_t sf_gemm_workspace_bytes(int mcap, int N, int K);
+int sf_pack_weight(const uint16_t* w, int N, int K, uint16_t* out, void* stream);
 int sf_o_proj_residual(const uint16_t* o_bf, const uint16_t* x, const uint16_t* wo, int M, int K,
                        int N, uint16_t* hp, void* workspace, size_t workspace_bytes, void* stream);
 int sf_rows_rmsnorm(const uint16_t* x, const int32_t* rows, const int32_t* count, int bucket,

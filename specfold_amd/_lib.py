@@ -35,7 +35,7 @@ SIGNATURES = {
     "sf_fold_gate": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _f, _f, _i,
                           _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "sf_qkv_workspace_bytes": (_sz, [_i, _i, _i]),
-    "sf_qkv_rope": (_i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp,
+    "sf_qkv_rope": (_i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _i, _vp,
                          _i, _i, _i, _i, _i, _vp, _vp, _vp, _sz, _vp]),
     "sf_attn_workspace_bytes": (_sz, [_i, _i, _i]),
     "sf_attn_prefix_block": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _ll, _ll, _vp, _vp, _vp,
@@ -45,6 +45,7 @@ SIGNATURES = {
                               _vp, _vp, _vp, _vp, _vp]),
     "sf_kv_append": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp, _i, _ll, _ll, _i, _vp]),
     "sf_gemm_workspace_bytes": (_sz, [_i, _i, _i]),
+    "sf_pack_weight": (_i, [_vp, _i, _i, _vp, _vp]),
     "sf_o_proj_residual": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _vp, _sz, _vp]),
     "sf_rows_rmsnorm": (_i, [_vp, _vp, _vp, _i, _vp, _i, _f, _vp, _vp]),
     "sf_ffn_gate_up": (_i, [_vp, _vp, _i, _vp, _vp, _i, _i, _vp, _vp]),
@@ -145,7 +146,9 @@ def qkv_workspace_bytes(bucket: int, D: int, n_qkv: int) -> int:
 
 
 def qkv_rope(xn, rows, count, bucket, BN, w_qkv, b_qkv, cos, sin, q_scale, N, D, H, Hkv, hd,
-             q_buf, kv_buf, workspace, stream=None) -> None:
+             q_buf, kv_buf, workspace, stream=None, pos0=None) -> None:
+    """cos/sin: [N, hd] block tables, or (with ``pos0``, an int32 device scalar
+    holding the block's first position) [T, hd] tables over absolute positions."""
     nq = (H + 2 * Hkv) * hd
     _need(xn, "xn", torch.bfloat16, min_numel=BN * D)
     _need(rows, "rows", torch.int32, min_numel=bucket, align=4)
@@ -153,8 +156,14 @@ def qkv_rope(xn, rows, count, bucket, BN, w_qkv, b_qkv, cos, sin, q_scale, N, D,
     _need(w_qkv, "w_qkv", torch.bfloat16, numel=nq * D)
     if b_qkv is not None:
         _need(b_qkv, "b_qkv", torch.bfloat16, numel=nq, align=4)
-    _need(cos, "cos", torch.bfloat16, numel=N * hd, align=4)
-    _need(sin, "sin", torch.bfloat16, numel=N * hd, align=4)
+    if pos0 is None:
+        _need(cos, "cos", torch.bfloat16, numel=N * hd, align=4)
+        table_rows = N
+    else:
+        _need(pos0, "pos0", torch.int32, min_numel=1, align=4)
+        table_rows = cos.numel() // hd
+        _need(cos, "cos", torch.bfloat16, numel=table_rows * hd, align=4)
+    _need(sin, "sin", torch.bfloat16, numel=cos.numel(), align=4)
     if q_scale is not None:
         _need(q_scale, "q_scale", torch.float32, numel=N, align=4)
     _need(q_buf, "q_buf", torch.bfloat16, min_numel=(BN + 1) * H * hd)
@@ -162,7 +171,8 @@ def qkv_rope(xn, rows, count, bucket, BN, w_qkv, b_qkv, cos, sin, q_scale, N, D,
     _need(workspace, "workspace", torch.uint8, min_numel=qkv_workspace_bytes(bucket, D, nq),
           align=256)
     st = load().sf_qkv_rope(_ptr(xn), _ptr(rows), _ptr(count), bucket, BN, _ptr(w_qkv),
-                            _ptr(b_qkv), _ptr(cos), _ptr(sin), _ptr(q_scale), N, D, H, Hkv, hd,
+                            _ptr(b_qkv), _ptr(cos), _ptr(sin), _ptr(pos0), table_rows,
+                            _ptr(q_scale), N, D, H, Hkv, hd,
                             _ptr(q_buf), _ptr(kv_buf), _ptr(workspace), workspace.numel(),
                             _stream(stream))
     _check(st, "sf_qkv_rope")
@@ -238,7 +248,23 @@ def kv_append(kv_buf, row0, n_tok, Hkv, hd, k_cache, v_cache, page_table, page_s
 
 
 def gemm_workspace_bytes(mcap: int, N: int, K: int) -> int:
+    """Bytes of the GEMM workspace (fp32 partial slots of the stream-K split)."""
     return int(load().sf_gemm_workspace_bytes(mcap, N, K))
+
+
+def pack_weight(w: torch.Tensor, out: Optional[torch.Tensor] = None, stream=None) -> torch.Tensor:
+    """Row-major bf16 [N, K] -> the packed fragment-major layout every GEMM entry
+    point takes (same shape, same bytes, reordered).  Returns ``out``."""
+    if w.dim() != 2:
+        raise ValueError("pack_weight takes a 2-D [N, K] weight")
+    N, K = w.shape
+    _need(w, "w", torch.bfloat16, numel=N * K)
+    if out is None:
+        out = torch.empty_like(w)
+    _need(out, "out", torch.bfloat16, numel=N * K)
+    st = load().sf_pack_weight(_ptr(w), N, K, _ptr(out), _stream(stream))
+    _check(st, "sf_pack_weight")
+    return out
 
 
 def o_proj_residual(o_bf, x, wo, M, K, N, hp, workspace, stream=None) -> None:

@@ -6,23 +6,30 @@
 // no mask) and the Triton kernel specfold/generate/triton_kernels.py:301-361.
 //
 // Two kernels (flash-decoding split over the prefix):
-//  * prefix: grid (query tile, 128-key prefix chunk, kv head).  All recomputed
-//    rows x the G q-heads of one kv head are flattened to queries qi = m*G + g
-//    and tiled 64 per workgroup (16 per wave), so each prefix K/V element is
-//    read by the few query tiles of its chunk instead of once per row.  The
-//    chunk's page ids are read once into LDS, then every K/V load of the chunk
-//    is issued at once (one memory latency per workgroup), K and V^T are staged
-//    in LDS, and two 64-key MFMA stages run from LDS.  Scores are formed
-//    transposed, S^T = K Q^T, so every lane holds 4 keys of ONE query: the
-//    softmax rescale is per lane and P^T feeds the P.V MFMA straight from
-//    registers (the 8 k-slots of a lane are keys {4g..4g+3} of two 16-key
-//    tiles, and V^T is read in that same order).  P is split into bf16 hi + lo
-//    halves (two MFMAs) so P.V keeps ~16 mantissa bits, close to the
-//    reference's fp32 einsum.  Each chunk writes its (m, l, acc) partial.
-//  * block + merge: one 256-thread workgroup per (recomputed row, kv head):
-//    every load (q, the branch's N block keys/values gathered through src, all
-//    chunk partials) is issued up front; block scores, the merged max, Z and O
-//    follow from LDS.
+//  * prefix: a persistent grid walks the active (query tile, 128-key prefix
+//    chunk, kv head) items; the item count follows the device-side row count and
+//    prefix length, so no workgroup is dispatched for an empty tile.  All
+//    recomputed rows x the G q-heads of one kv head are flattened to queries
+//    qi = m*G + g and tiled 64 per item (16 per wave), so each prefix K/V
+//    element is read by the few query tiles of its chunk instead of once per
+//    row.  Items of one chunk are consecutive and go to one XCD (workgroup b runs
+//    on XCD b % 8), so the chunk's later reads hit that XCD's L2.  Per item the
+//    chunk's page ids go to LDS, every K and V load of the chunk is issued at
+//    once, K is staged in LDS and all 128 scores are formed while V is still in
+//    flight; V is then written transposed.  Scores are formed transposed,
+//    S^T = K Q^T, so every lane holds keys of ONE query: the softmax is per lane
+//    and P^T feeds the P.V MFMA straight from registers (the 8 k-slots of a lane
+//    are keys {4g..4g+3} of two 16-key tiles, and V^T is read in that same
+//    order).  P is split into bf16 hi + lo halves (two MFMAs) so P.V keeps ~16
+//    mantissa bits, close to the reference's fp32 einsum.  Each item writes its
+//    (m, l, acc) partial.
+//  * block + merge: one 512-thread workgroup per active (recomputed row, kv
+//    head): every load (q, the branch's N block keys/values gathered through src,
+//    all chunk partials) is issued up front; block scores, the merged max, Z and
+//    O follow from LDS.
+// Softmax exponentials are exp2 of scores pre-scaled by log2(e) (one v_exp_f32
+// each); partial maxima stay in that base-2 domain and the emitted m is converted
+// back, so (m, Z) describe the natural-base softmax the reference computes.
 // The prefix length may come from device memory (p_len), so a captured graph
 // of the verify step stays valid while the cache grows; `P` is then the
 // capacity the grid and the workspace are sized for.
@@ -39,32 +46,18 @@ constexpr int kKStr = 136;   // K tile row stride (bf16)
 constexpr int kVStr = 136;   // V^T tile row stride (bf16): 128 keys + 8 pad
 constexpr int kMaxG = 8;
 constexpr int kMaxN = 64;
+constexpr int kCUs = 256;  // MI355X compute units
 
-SF_DEV uint32_t bf_at(const sf_u32x4& w, int j) {
-  return (w[j >> 1] >> ((j & 1) * 16)) & 0xffffu;
-}
-
-__global__ __launch_bounds__(256) void sf_attn_prefix_kernel(
-    const uint16_t* __restrict__ q_buf, const uint16_t* __restrict__ pk,
-    const uint16_t* __restrict__ pv, const int32_t* __restrict__ page_table, int page_size,
-    long long page_stride, long long head_stride, const int32_t* __restrict__ p_len, int P_host,
-    const int32_t* __restrict__ rows, const int32_t* __restrict__ count_p, int bucket, int H,
-    int Hkv, float scaling, int qmax, float* __restrict__ ws_o, float* __restrict__ ws_ml) {
-  __shared__ __attribute__((aligned(16))) uint16_t sK[kChunk * kKStr];
-  __shared__ __attribute__((aligned(16))) uint16_t sV[kHD * kVStr];
-  __shared__ int s_page[kChunk];
-  const int G = H / Hkv;
-  const int qt = blockIdx.x;
-  const int ci = blockIdx.y;
-  const int h = blockIdx.z;
-  const int nchunks = gridDim.y;
-  const int P = p_len ? *p_len : P_host;
+// One (query tile, chunk, kv head) item of the prefix pass; all 256 threads
+// take part (the LDS barriers are uniform).
+SF_DEV void prefix_item(const uint16_t* __restrict__ q_buf, const uint16_t* __restrict__ pk,
+                        const uint16_t* __restrict__ pv, const int32_t* __restrict__ page_table,
+                        int page_size, long long page_stride, long long head_stride, int P,
+                        const int32_t* __restrict__ rows, int nq, int G, int H, float scale_log2,
+                        int qmax, int nch_cap, int qt, int ci, int h, uint16_t* sK, uint16_t* sV,
+                        int* s_page, float* __restrict__ ws_o, float* __restrict__ ws_ml) {
   const int k_begin = ci * kChunk;
-  if (k_begin >= P) return;
-  const int k_end = min(P, k_begin + kChunk);
-  const int count = min(*count_p, bucket);
-  const int nq = count * G;
-  if (qt * kQT >= nq) return;
+  const int nkeys = min(P - k_begin, kChunk);  // >= 1
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = tid >> 6;
@@ -74,160 +67,140 @@ __global__ __launch_bounds__(256) void sf_attn_prefix_kernel(
   const bool qvalid = qi < nq;
   const long long head_off = (long long)h * head_stride;
 
-  // page ids of the chunk's keys (one per key; pages must not straddle the chunk
-  // unevenly, so page_size divides 128 — checked on the host)
-  if (tid < kChunk) {
-    const int t = k_begin + tid;
-    s_page[tid] = (page_table && t < k_end) ? page_table[t / page_size] : 0;
-  }
-  // Q^T operand: lane holds q[qi][ds*32 + grp*8 .. +8]
+  // Q^T operand: lane holds q[qi][ds*32 + grp*8 .. +8]; a padding query (qi >= nq)
+  // repeats the last real one and its partial is never written
   sf_u32x4 qf[4];
-  if (qvalid) {
-    const int m = qi / G;
-    const int g = qi - m * G;
+  {
+    const int qc = min(qi, nq - 1);
+    const int m = qc / G;
+    const int g = qc - m * G;
     const uint16_t* qp = q_buf + (size_t)rows[m] * H * kHD + (h * G + g) * kHD + grp * 8;
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds) qf[ds] = *reinterpret_cast<const sf_u32x4*>(qp + ds * 32);
-  } else {
-#pragma unroll
-    for (int ds = 0; ds < 4; ++ds) qf[ds] = sf_u32x4{0u, 0u, 0u, 0u};
+  }
+  // page ids of the chunk's keys (page_size divides 128, checked on the host)
+  if (tid < kChunk) {
+    const int t = k_begin + min(tid, nkeys - 1);
+    s_page[tid] = page_table ? page_table[t / page_size] : 0;
   }
   __syncthreads();
 
   auto key_ptr = [&](const uint16_t* base, int kl) -> const uint16_t* {
     const int t = k_begin + kl;
-    if (page_table) {
-      const int off = t % page_size;
-      return base + (long long)s_page[kl] * page_stride + head_off + (long long)off * kHD;
-    }
+    if (page_table)
+      return base + (long long)s_page[kl] * page_stride + head_off +
+             (long long)(t % page_size) * kHD;
     return base + head_off + (long long)t * kHD;
   };
 
-  // all K/V loads of the chunk at once: K thread->(key = (tid>>4) + 16i, seg = tid&15);
-  // V thread->(keys 64p + 4*(tid>>4) + 0..3, seg = tid&15) so 4 consecutive keys pack
-  // into one 8-byte V^T write
-  const sf_u32x4 zero4 = {0u, 0u, 0u, 0u};
+  // every K and V load of the chunk (clamped to the last key, masked later):
+  // K thread->(key = (tid>>4) + 16i, seg = tid&15); V thread->(keys 64p + 4*(tid>>4)
+  // + 0..3, seg = tid&15) so 4 consecutive keys pack into one 8-byte V^T write
   const int sg = tid & 15;
   const int kr = tid >> 4;
   sf_u32x4 kreg[8], vreg[2][4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int kl = kr + 16 * i;
-    kreg[i] = (k_begin + kl < k_end)
-                  ? *reinterpret_cast<const sf_u32x4*>(key_ptr(pk, kl) + sg * 8)
-                  : zero4;
-  }
+  for (int i = 0; i < 8; ++i)
+    kreg[i] = *reinterpret_cast<const sf_u32x4*>(key_ptr(pk, min(kr + 16 * i, nkeys - 1)) + sg * 8);
 #pragma unroll
   for (int p = 0; p < 2; ++p)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int kl = 64 * p + 4 * kr + i;
-      vreg[p][i] = (k_begin + kl < k_end)
-                       ? *reinterpret_cast<const sf_u32x4*>(key_ptr(pv, kl) + sg * 8)
-                       : zero4;
-    }
+    for (int i = 0; i < 4; ++i)
+      vreg[p][i] = *reinterpret_cast<const sf_u32x4*>(
+          key_ptr(pv, min(64 * p + 4 * kr + i, nkeys - 1)) + sg * 8);
 #pragma unroll
   for (int i = 0; i < 8; ++i)
     *reinterpret_cast<sf_u32x4*>(&sK[(kr + 16 * i) * kKStr + sg * 8]) = kreg[i];
+  __syncthreads();
+
+  // S^T = K Q^T for all 8 key tiles of the chunk (V loads still in flight)
+  float s[8][4];
+#pragma unroll
+  for (int kt = 0; kt < 8; ++kt) {
+    sf_f32x4 a = {0.f, 0.f, 0.f, 0.f};
+    const uint16_t* kb = &sK[(kt * 16 + ql) * kKStr + grp * 8];
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) {
+      const sf_u32x4 kf = *reinterpret_cast<const sf_u32x4*>(kb + ds * 32);
+      a = sf_mfma16x16x32(sf_as_bf16x8(kf), sf_as_bf16x8(qf[ds]), a);
+    }
+    const int key0 = kt * 16 + grp * 4;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s[kt][r] = (key0 + r < nkeys) ? a[r] * scale_log2 : -INFINITY;
+  }
+
+  // V^T: dims (2w, 2w+1) of keys (k0, k1) -> one word per dim, by byte permutes
 #pragma unroll
   for (int p = 0; p < 2; ++p)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint64_t packed =
-          (uint64_t)bf_at(vreg[p][0], j) | ((uint64_t)bf_at(vreg[p][1], j) << 16) |
-          ((uint64_t)bf_at(vreg[p][2], j) << 32) | ((uint64_t)bf_at(vreg[p][3], j) << 48);
-      *reinterpret_cast<uint64_t*>(&sV[(sg * 8 + j) * kVStr + 64 * p + 4 * kr]) = packed;
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t x0 = vreg[p][0][w], x1 = vreg[p][1][w];
+      const uint32_t x2 = vreg[p][2][w], x3 = vreg[p][3][w];
+      sf_u32x2 lo, hi;
+      lo[0] = (x0 & 0xffffu) | (x1 << 16);
+      lo[1] = (x2 & 0xffffu) | (x3 << 16);
+      hi[0] = (x0 >> 16) | (x1 & 0xffff0000u);
+      hi[1] = (x2 >> 16) | (x3 & 0xffff0000u);
+      *reinterpret_cast<sf_u32x2*>(&sV[(sg * 8 + 2 * w) * kVStr + 64 * p + 4 * kr]) = lo;
+      *reinterpret_cast<sf_u32x2*>(&sV[(sg * 8 + 2 * w + 1) * kVStr + 64 * p + 4 * kr]) = hi;
     }
+
+  // one max for the whole chunk: the 4 lanes groups of a query hold its 128 keys
+  float mx = -INFINITY;
+#pragma unroll
+  for (int kt = 0; kt < 8; ++kt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kt][r]);
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  float lsum = 0.f;
+#pragma unroll
+  for (int kt = 0; kt < 8; ++kt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      s[kt][r] = __builtin_amdgcn_exp2f(s[kt][r] - mx);
+      lsum += s[kt][r];
+    }
+  lsum += __shfl_xor(lsum, 16, 64);
+  lsum += __shfl_xor(lsum, 32, 64);
   __syncthreads();
 
-  float m_run = -INFINITY;
-  float l_run = 0.f;
   sf_f32x4 acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
-
 #pragma unroll
-  for (int st = 0; st < 2; ++st) {
-    const int kbase = st * 64;
-    if (k_begin + kbase >= k_end) break;
-    float s[4][4];
+  for (int j = 0; j < 4; ++j) {
+    const int kt0 = 2 * j, kt1 = 2 * j + 1;
+    if (kt0 * 16 >= nkeys) break;
+    sf_u32x4 hi, lo;
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      sf_f32x4 a = {0.f, 0.f, 0.f, 0.f};
-      const uint16_t* kb = &sK[(kbase + kt * 16 + ql) * kKStr + grp * 8];
-#pragma unroll
-      for (int ds = 0; ds < 4; ++ds) {
-        const sf_u32x4 kf = *reinterpret_cast<const sf_u32x4*>(kb + ds * 32);
-        a = sf_mfma16x16x32(sf_as_bf16x8(kf), sf_as_bf16x8(qf[ds]), a);
-      }
-      const int key0 = k_begin + kbase + kt * 16 + grp * 4;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) s[kt][r] = (key0 + r < k_end) ? a[r] * scaling : -INFINITY;
+    for (int w2 = 0; w2 < 2; ++w2) {
+      const float a0 = s[kt0][2 * w2], a1 = s[kt0][2 * w2 + 1];
+      const float b0 = s[kt1][2 * w2], b1 = s[kt1][2 * w2 + 1];
+      hi[w2] = sf_pack2(a0, a1);
+      hi[2 + w2] = sf_pack2(b0, b1);
+      lo[w2] = sf_pack2(a0 - sf_rbf(a0), a1 - sf_rbf(a1));
+      lo[2 + w2] = sf_pack2(b0 - sf_rbf(b0), b1 - sf_rbf(b1));
     }
-    float mx = -INFINITY;
+    const sf_bf16x8 bhi = sf_as_bf16x8(hi);
+    const sf_bf16x8 blo = sf_as_bf16x8(lo);
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kt][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = expf(m_run - m_new);
-    float lsum = 0.f;
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        s[kt][r] = expf(s[kt][r] - m_new);
-        lsum += s[kt][r];
-      }
-    l_run = l_run * alpha + lsum;
-    m_run = m_new;
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
-
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int kt0 = 2 * j, kt1 = 2 * j + 1;
-      float ph[8];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        ph[r] = s[kt0][r];
-        ph[4 + r] = s[kt1][r];
-      }
-      sf_u32x4 hi, lo;
-#pragma unroll
-      for (int w2 = 0; w2 < 4; ++w2) {
-        const float a0 = ph[2 * w2], a1 = ph[2 * w2 + 1];
-        hi[w2] = sf_pack2(a0, a1);
-        lo[w2] = sf_pack2(a0 - sf_rbf(a0), a1 - sf_rbf(a1));
-      }
-      const sf_bf16x8 bhi = sf_as_bf16x8(hi);
-      const sf_bf16x8 blo = sf_as_bf16x8(lo);
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const uint16_t* vrow = &sV[(dt * 16 + ql) * kVStr + kbase + grp * 4];
-        const uint64_t a0 = *reinterpret_cast<const uint64_t*>(vrow + kt0 * 16);
-        const uint64_t a1 = *reinterpret_cast<const uint64_t*>(vrow + kt1 * 16);
-        sf_u32x4 vf;
-        vf[0] = (uint32_t)a0;
-        vf[1] = (uint32_t)(a0 >> 32);
-        vf[2] = (uint32_t)a1;
-        vf[3] = (uint32_t)(a1 >> 32);
-        const sf_bf16x8 va = sf_as_bf16x8(vf);
-        acc[dt] = sf_mfma16x16x32(va, bhi, acc[dt]);
-        acc[dt] = sf_mfma16x16x32(va, blo, acc[dt]);
-      }
+    for (int dt = 0; dt < 8; ++dt) {
+      const uint16_t* vrow = &sV[(dt * 16 + ql) * kVStr + grp * 4];
+      const sf_u32x2 a0 = *reinterpret_cast<const sf_u32x2*>(vrow + kt0 * 16);
+      const sf_u32x2 a1 = *reinterpret_cast<const sf_u32x2*>(vrow + kt1 * 16);
+      const sf_u32x4 vf = {a0[0], a0[1], a1[0], a1[1]};
+      const sf_bf16x8 va = sf_as_bf16x8(vf);
+      acc[dt] = sf_mfma16x16x32(va, bhi, acc[dt]);
+      acc[dt] = sf_mfma16x16x32(va, blo, acc[dt]);
     }
   }
 
-  l_run += __shfl_xor(l_run, 16, 64);
-  l_run += __shfl_xor(l_run, 32, 64);
   if (qvalid) {
-    const size_t slot = ((size_t)h * nchunks + ci) * qmax + qi;
+    const size_t slot = ((size_t)h * nch_cap + ci) * qmax + qi;
     if (grp == 0) {
-      ws_ml[slot * 2] = m_run;
-      ws_ml[slot * 2 + 1] = l_run;
+      ws_ml[slot * 2] = mx;
+      ws_ml[slot * 2 + 1] = lsum;
     }
     float* op = ws_o + slot * kHD + grp * 4;
 #pragma unroll
@@ -235,37 +208,76 @@ __global__ __launch_bounds__(256) void sf_attn_prefix_kernel(
   }
 }
 
-// One 512-thread workgroup per (recomputed row m, kv head h); thread t owns the
-// output pair (q-head t/64, dims 2*(t%64) .. +1).
+// gridDim.x is a multiple of 8; XCD x (workgroups b with b % 8 == x) takes the
+// x-th eighth of the item list, so consecutive items (the query tiles of one
+// chunk) share an L2.
+__global__ __launch_bounds__(256) void sf_attn_prefix_kernel(
+    const uint16_t* __restrict__ q_buf, const uint16_t* __restrict__ pk,
+    const uint16_t* __restrict__ pv, const int32_t* __restrict__ page_table, int page_size,
+    long long page_stride, long long head_stride, const int32_t* __restrict__ p_len, int P_cap,
+    const int32_t* __restrict__ rows, const int32_t* __restrict__ count_p, int bucket, int H,
+    int Hkv, float scale_log2, int qmax, int nch_cap, float* __restrict__ ws_o,
+    float* __restrict__ ws_ml) {
+  __shared__ __attribute__((aligned(16))) uint16_t sK[kChunk * kKStr];
+  __shared__ __attribute__((aligned(16))) uint16_t sV[kHD * kVStr];
+  __shared__ int s_page[kChunk];
+  const int G = H / Hkv;
+  const int P = p_len ? min(*p_len, P_cap) : P_cap;
+  const int nq = min(*count_p, bucket) * G;
+  const int n_qt = (nq + kQT - 1) / kQT;
+  const int nch = (P + kChunk - 1) / kChunk;
+  const int items = n_qt * nch * Hkv;
+  const int xcd = blockIdx.x & 7;
+  const int per = gridDim.x >> 3;
+  const int end = (int)(((long long)items * (xcd + 1)) >> 3);
+  for (int it = (int)(((long long)items * xcd) >> 3) + (int)(blockIdx.x >> 3); it < end;
+       it += per) {
+    const int qt = it % n_qt;
+    const int rest = it / n_qt;
+    const int ci = rest % nch;
+    const int h = rest / nch;
+    prefix_item(q_buf, pk, pv, page_table, page_size, page_stride, head_stride, P, rows, nq, G, H,
+                scale_log2, qmax, nch_cap, qt, ci, h, sK, sV, s_page, ws_o, ws_ml);
+    __syncthreads();  // LDS is reused by the next item
+  }
+}
+
+// One 512-thread workgroup per active (recomputed row m, kv head h) item, walked
+// by a persistent grid; thread t owns the output pair (q-head t/64, dims
+// 2*(t%64) .. +1).
 constexpr int kMaxChunks = 256;   // prefix <= 32768 keys
 constexpr int kBatch = 16;        // chunk partials loaded per round
 
-__global__ __launch_bounds__(512) void sf_attn_block_merge_kernel(
-    const uint16_t* __restrict__ q_buf, const uint16_t* __restrict__ kv_buf,
-    const int32_t* __restrict__ src, const int32_t* __restrict__ rows,
-    const int32_t* __restrict__ count_p, int bucket, int N, int H, int Hkv, float scaling,
-    const int32_t* __restrict__ p_len, int P_host, int nchunks_cap, int qmax,
-    const float* __restrict__ ws_o, const float* __restrict__ ws_ml, float* __restrict__ o32,
-    uint16_t* __restrict__ o_bf, float* __restrict__ m_tab, float* __restrict__ z_tab) {
-  __shared__ float sq[kMaxG][kHD];
-  __shared__ __attribute__((aligned(16))) uint16_t sk[kMaxN][kHD];
-  __shared__ __attribute__((aligned(16))) uint16_t sv[kMaxN][kHD];
-  __shared__ float ss[kMaxG][kMaxN];
-  __shared__ float sml[kMaxG][2 * kMaxChunks];   // per q-head: (m, l) of every chunk
-  __shared__ float sM[kMaxG], sZ[kMaxG];
-  const int m = blockIdx.x;
-  const int h = blockIdx.y;
+SF_DEV void merge_item(const uint16_t* __restrict__ q_buf, const uint16_t* __restrict__ kv_buf,
+                       const int32_t* __restrict__ src, const int32_t* __restrict__ rows, int m,
+                       int h, int N, int H, int Hkv, int G, float scale_log2, int nch,
+                       int nchunks_cap, int qmax, const float* __restrict__ ws_o,
+                       const float* __restrict__ ws_ml, float* __restrict__ o32,
+                       uint16_t* __restrict__ o_bf, float* __restrict__ m_tab,
+                       float* __restrict__ z_tab, float (*sq)[kHD], uint16_t (*sk)[kHD],
+                       uint16_t (*sv)[kHD], float (*ss)[kMaxN], float (*sml)[2 * kMaxChunks],
+                       float* sM, float* sZ) {
   const int tid = threadIdx.x;
-  const int count = min(*count_p, bucket);
-  if (m >= count) return;
-  const int G = H / Hkv;
-  const int P = p_len ? *p_len : P_host;
-  const int nch = min((P + kChunk - 1) / kChunk, nchunks_cap);
+  const int my_g = tid >> 6, dp = (tid & 63) * 2;
+  const bool mine = my_g < G;
+  const size_t my_slot0 = (size_t)h * nchunks_cap * qmax + (size_t)m * G + my_g;
+  // --- loads: chunk (m, l) and the first batch of chunk accumulators (independent
+  // of the row id), then q and the branch's block K/V gathered through src --------
+  for (int i = tid; i < G * nch; i += 512) {
+    const int g = i / nch, c = i - g * nch;
+    const size_t sl = ((size_t)h * nchunks_cap + c) * qmax + (size_t)m * G + g;
+    const float2 ml = *reinterpret_cast<const float2*>(ws_ml + sl * 2);
+    sml[g][2 * c] = ml.x;
+    sml[g][2 * c + 1] = ml.y;
+  }
+  float2 accb[kBatch];
+#pragma unroll
+  for (int c = 0; c < kBatch; ++c)
+    if (mine && c < nch)
+      accb[c] = *reinterpret_cast<const float2*>(ws_o + (my_slot0 + (size_t)c * qmax) * kHD + dp);
   const int row = rows[m];
   const int b = row / N;
   const int kvs = 2 * Hkv * kHD;
-
-  // --- loads: q, the branch's block K/V (gathered through src), chunk (m, l) -------
   if (tid < G * 32) {
     const int g = tid >> 5, d = (tid & 31) * 4;
     const sf_u32x2 w = *reinterpret_cast<const sf_u32x2*>(
@@ -278,29 +290,15 @@ __global__ __launch_bounds__(512) void sf_attn_block_merge_kernel(
   for (int i = tid; i < N * 16; i += 512) {
     const int j = i >> 4, sgm = i & 15;
     const size_t kvrow = (size_t)(src[b * N + j] * N + j) * kvs;
-    *reinterpret_cast<sf_u32x4*>(&sk[j][sgm * 8]) =
-        *reinterpret_cast<const sf_u32x4*>(kv_buf + kvrow + h * kHD + sgm * 8);
-    *reinterpret_cast<sf_u32x4*>(&sv[j][sgm * 8]) =
+    const sf_u32x4 kk = *reinterpret_cast<const sf_u32x4*>(kv_buf + kvrow + h * kHD + sgm * 8);
+    const sf_u32x4 vv =
         *reinterpret_cast<const sf_u32x4*>(kv_buf + kvrow + (Hkv + h) * kHD + sgm * 8);
+    *reinterpret_cast<sf_u32x4*>(&sk[j][sgm * 8]) = kk;
+    *reinterpret_cast<sf_u32x4*>(&sv[j][sgm * 8]) = vv;
   }
-  for (int i = tid; i < G * nch; i += 512) {
-    const int g = i / nch, c = i - g * nch;
-    const size_t sl = ((size_t)h * nchunks_cap + c) * qmax + (size_t)m * G + g;
-    sml[g][2 * c] = ws_ml[sl * 2];
-    sml[g][2 * c + 1] = ws_ml[sl * 2 + 1];
-  }
-  // this thread's first batch of chunk accumulators, in flight during the scores
-  const int my_g = tid >> 6, dp = (tid & 63) * 2;
-  const bool mine = my_g < G;
-  const size_t my_slot0 = (size_t)h * nchunks_cap * qmax + (size_t)m * G + my_g;
-  float2 accb[kBatch];
-#pragma unroll
-  for (int c = 0; c < kBatch; ++c)
-    if (mine && c < nch)
-      accb[c] = *reinterpret_cast<const float2*>(ws_o + (my_slot0 + (size_t)c * qmax) * kHD + dp);
   __syncthreads();
 
-  // --- block scores: thread -> (g, j) ----------------------------------------------
+  // --- block scores (base-2 domain): thread -> (g, j) ------------------------------
   for (int i = tid; i < G * N; i += 512) {
     const int g = i / N, j = i - g * N;
     float d = 0.f;
@@ -311,7 +309,7 @@ __global__ __launch_bounds__(512) void sf_attn_block_merge_kernel(
 #pragma unroll
       for (int t = 0; t < 8; ++t) d = fmaf(sq[g][e + t], kf[t], d);
     }
-    ss[g][j] = d * scaling;
+    ss[g][j] = d * scale_log2;
   }
   __syncthreads();
 
@@ -326,12 +324,12 @@ __global__ __launch_bounds__(512) void sf_attn_block_merge_kernel(
       mm = sf_wave_max(mm);
       float z = 0.f;
       for (int j = lane; j < N; j += 64) {
-        const float p = expf(ss[g][j] - mm);
+        const float p = __builtin_amdgcn_exp2f(ss[g][j] - mm);
         ss[g][j] = p;
         z += p;
       }
       for (int c = lane; c < nch; c += 64) {
-        const float wgt = expf(sml[g][2 * c] - mm);
+        const float wgt = __builtin_amdgcn_exp2f(sml[g][2 * c] - mm);
         sml[g][2 * c] = wgt;
         z += sml[g][2 * c + 1] * wgt;
       }
@@ -343,41 +341,67 @@ __global__ __launch_bounds__(512) void sf_attn_block_merge_kernel(
     }
   }
   __syncthreads();
-  if (!mine) return;
 
   // --- O = (sum_j p_j v_j + sum_c w_c acc_c) / Z --------------------------------------
-  float o0 = 0.f, o1 = 0.f;
-  for (int j = 0; j < N; ++j) {
-    const float p = ss[my_g][j];
-    const uint32_t vv = *reinterpret_cast<const uint32_t*>(&sv[j][dp]);
-    o0 = fmaf(p, __uint_as_float(vv << 16), o0);
-    o1 = fmaf(p, __uint_as_float(vv & 0xffff0000u), o1);
-  }
-  for (int cb = 0; cb < nch; cb += kBatch) {
-    if (cb > 0) {
-#pragma unroll
-      for (int c = 0; c < kBatch; ++c)
-        if (cb + c < nch)
-          accb[c] = *reinterpret_cast<const float2*>(
-              ws_o + (my_slot0 + (size_t)(cb + c) * qmax) * kHD + dp);
+  if (mine) {
+    float o0 = 0.f, o1 = 0.f;
+    for (int j = 0; j < N; ++j) {
+      const float p = ss[my_g][j];
+      const uint32_t vv = *reinterpret_cast<const uint32_t*>(&sv[j][dp]);
+      o0 = fmaf(p, __uint_as_float(vv << 16), o0);
+      o1 = fmaf(p, __uint_as_float(vv & 0xffff0000u), o1);
     }
+    for (int cb = 0; cb < nch; cb += kBatch) {
+      if (cb > 0) {
 #pragma unroll
-    for (int c = 0; c < kBatch; ++c) {
-      if (cb + c < nch) {
-        const float wgt = sml[my_g][2 * (cb + c)];
-        o0 = fmaf(wgt, accb[c].x, o0);
-        o1 = fmaf(wgt, accb[c].y, o1);
+        for (int c = 0; c < kBatch; ++c)
+          accb[c] = *reinterpret_cast<const float2*>(
+              ws_o + (my_slot0 + (size_t)min(cb + c, nch - 1) * qmax) * kHD + dp);
+      }
+#pragma unroll
+      for (int c = 0; c < kBatch; ++c) {
+        if (cb + c < nch) {
+          const float wgt = sml[my_g][2 * (cb + c)];
+          o0 = fmaf(wgt, accb[c].x, o0);
+          o1 = fmaf(wgt, accb[c].y, o1);
+        }
       }
     }
+    const float inv = 1.0f / sZ[my_g];
+    const float r0 = o0 * inv, r1 = o1 * inv;
+    const size_t off = (size_t)row * H * kHD + (h * G + my_g) * kHD + dp;
+    *reinterpret_cast<float2*>(o32 + off) = make_float2(r0, r1);
+    *reinterpret_cast<uint32_t*>(o_bf + off) = sf_pack2(r0, r1);
+    if (dp == 0) {
+      // the natural-base max the block scores and chunk maxima were measured from
+      m_tab[(size_t)row * H + h * G + my_g] = sM[my_g] * 0.69314718055994530942f;
+      z_tab[(size_t)row * H + h * G + my_g] = sZ[my_g];
+    }
   }
-  const float inv = 1.0f / sZ[my_g];
-  const float r0 = o0 * inv, r1 = o1 * inv;
-  const size_t off = (size_t)row * H * kHD + (h * G + my_g) * kHD + dp;
-  *reinterpret_cast<float2*>(o32 + off) = make_float2(r0, r1);
-  *reinterpret_cast<uint32_t*>(o_bf + off) = sf_pack2(r0, r1);
-  if (dp == 0) {
-    m_tab[(size_t)row * H + h * G + my_g] = sM[my_g];
-    z_tab[(size_t)row * H + h * G + my_g] = sZ[my_g];
+}
+
+__global__ __launch_bounds__(512) void sf_attn_block_merge_kernel(
+    const uint16_t* __restrict__ q_buf, const uint16_t* __restrict__ kv_buf,
+    const int32_t* __restrict__ src, const int32_t* __restrict__ rows,
+    const int32_t* __restrict__ count_p, int bucket, int N, int H, int Hkv, float scale_log2,
+    const int32_t* __restrict__ p_len, int P_cap, int nchunks_cap, int qmax,
+    const float* __restrict__ ws_o, const float* __restrict__ ws_ml, float* __restrict__ o32,
+    uint16_t* __restrict__ o_bf, float* __restrict__ m_tab, float* __restrict__ z_tab) {
+  __shared__ float sq[kMaxG][kHD];
+  __shared__ __attribute__((aligned(16))) uint16_t sk[kMaxN][kHD];
+  __shared__ __attribute__((aligned(16))) uint16_t sv[kMaxN][kHD];
+  __shared__ float ss[kMaxG][kMaxN];
+  __shared__ float sml[kMaxG][2 * kMaxChunks];   // per q-head: (m, l) of every chunk
+  __shared__ float sM[kMaxG], sZ[kMaxG];
+  const int count = min(*count_p, bucket);
+  const int G = H / Hkv;
+  const int P = p_len ? min(*p_len, P_cap) : P_cap;
+  const int nch = min((P + kChunk - 1) / kChunk, nchunks_cap);
+  for (int it = blockIdx.x; it < count * Hkv; it += gridDim.x) {
+    merge_item(q_buf, kv_buf, src, rows, it / Hkv, it % Hkv, N, H, Hkv, G, scale_log2, nch,
+               nchunks_cap, qmax, ws_o, ws_ml, o32, o_bf, m_tab, z_tab, sq, sk, sv, ss, sml, sM,
+               sZ);
+    __syncthreads();  // LDS is reused by the next item
   }
 }
 
@@ -417,20 +441,23 @@ extern "C" int sf_attn_prefix_block(const uint16_t* q_buf, const uint16_t* kv_bu
   const int G = H / Hkv;
   const int qmax = bucket * G;
   const int nch = P > 0 ? nchunks_for(P) : 0;
+  const float scale_log2 = scaling * 1.44269504088896340736f;
   float* ws_ml = nullptr;
   float* ws_o = nullptr;
   if (P > 0) {
     const size_t nslot = (size_t)nch * qmax * Hkv;
     ws_o = reinterpret_cast<float*>(workspace);
     ws_ml = ws_o + nslot * kHD;
-    dim3 g1((qmax + kQT - 1) / kQT, nch, Hkv);
-    hipLaunchKernelGGL(sf_attn_prefix_kernel, g1, dim3(256), 0, st, q_buf, prefix_k, prefix_v,
-                       page_table, page_size, page_stride, head_stride, prefix_len, P, rows,
-                       count, bucket, H, Hkv, scaling, qmax, ws_o, ws_ml);
+    // persistent grid: at most two 70 KB-LDS workgroups fit a CU; a multiple of 8
+    const int items_cap = ((qmax + kQT - 1) / kQT) * nch * Hkv;
+    const int grid = min(2 * kCUs, ((items_cap + 7) / 8) * 8);
+    hipLaunchKernelGGL(sf_attn_prefix_kernel, dim3(grid), dim3(256), 0, st, q_buf, prefix_k,
+                       prefix_v, page_table, page_size, page_stride, head_stride, prefix_len, P,
+                       rows, count, bucket, H, Hkv, scale_log2, qmax, nch, ws_o, ws_ml);
   }
-  dim3 g2(bucket, Hkv);
-  hipLaunchKernelGGL(sf_attn_block_merge_kernel, g2, dim3(512), 0, st, q_buf, kv_buf, src, rows,
-                     count, bucket, N, H, Hkv, scaling, P > 0 ? prefix_len : nullptr, P, nch, qmax,
-                     ws_o, ws_ml, o32, o_bf, m_tab, z_tab);
+  const int grid2 = min(bucket * Hkv, 2 * kCUs);
+  hipLaunchKernelGGL(sf_attn_block_merge_kernel, dim3(grid2), dim3(512), 0, st, q_buf, kv_buf,
+                     src, rows, count, bucket, N, H, Hkv, scale_log2, P > 0 ? prefix_len : nullptr,
+                     P, nch, qmax, ws_o, ws_ml, o32, o_bf, m_tab, z_tab);
   return sf_launch_status();
 }

@@ -16,7 +16,8 @@
 //
 // One wave per (folded row, kv head); lane = g*8 + c owns dims c*16..c*16+15 of
 // q-head g of that kv head (G <= 8), so the G dot products of an entry reduce
-// over 8 lanes in parallel.
+// over 8 lanes in parallel.  Entries of a chain are visited in hop order
+// (b, par(b), ...) and, within a branch, in ascending position.
 #include <math.h>
 
 #include "sf_common.h"
@@ -40,6 +41,24 @@ SF_DEV float dot16_group8(const float a[16], const float b[16]) {
   return d;
 }
 
+constexpr int kMaxBN = 1024;
+constexpr int kMaxB1 = 64;
+constexpr int kBatch1 = 8;  // chain entries whose new keys are loaded together (pass 1)
+constexpr int kBatch2 = 4;  // chain entries whose old and new K/V are loaded together (pass 2)
+
+SF_DEV void load16w(const uint16_t* p, sf_u32x4 w[2]) {
+  w[0] = *reinterpret_cast<const sf_u32x4*>(p);
+  w[1] = *reinterpret_cast<const sf_u32x4*>(p + 8);
+}
+
+SF_DEV void unpack16(const sf_u32x4 w[2], float out[16]) {
+  sf_unpack8(w[0], out);
+  sf_unpack8(w[1], out + 8);
+}
+
+// The fold tables (src, seg, par, segcnt) are staged in LDS by the whole
+// workgroup in one round of loads; each wave then walks its chain from LDS and
+// loads the K/V of its chain entries in batches (one memory latency per batch).
 __global__ __launch_bounds__(256) void sf_chain_kernel(
     const uint16_t* __restrict__ q_buf, const uint16_t* __restrict__ kv_buf,
     const int32_t* __restrict__ src, const int32_t* __restrict__ par,
@@ -47,13 +66,42 @@ __global__ __launch_bounds__(256) void sf_chain_kernel(
     const int32_t* __restrict__ segcnt, int B1, int N, int H, int Hkv, float scaling,
     float* __restrict__ o32, uint16_t* __restrict__ o_bf, float* __restrict__ m_tab,
     float* __restrict__ z_tab) {
-  const int lane = threadIdx.x & 63;
-  const int idx = blockIdx.x * 4 + (threadIdx.x >> 6);
+  __shared__ int s_src[kMaxBN];
+  __shared__ int s_seg[kMaxBN];
+  __shared__ int s_par[kMaxB1];
+  __shared__ int s_cnt[kMaxB1];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
   const int BN = B1 * N;
-  const int r = idx / Hkv;
+  const int idx = blockIdx.x * 4 + (tid >> 6);
+  const bool item = idx < BN * Hkv;
+  const int r = item ? idx / Hkv : 0;
   const int h = idx - r * Hkv;
-  if (r >= BN) return;
-  if (rec[r]) return;
+
+  int tsrc[kMaxBN / 256], tseg[kMaxBN / 256];
+#pragma unroll
+  for (int k = 0; k < kMaxBN / 256; ++k) {
+    const int i = min(tid + 256 * k, BN - 1);
+    tsrc[k] = src[i];
+    tseg[k] = seg[i];
+  }
+  const int tpar = par[min(tid, B1 - 1)];
+  const int tcnt = segcnt[min(tid, B1 - 1)];
+  const bool folded = rec[r] == 0;
+#pragma unroll
+  for (int k = 0; k < kMaxBN / 256; ++k) {
+    if (tid + 256 * k < BN) {
+      s_src[tid + 256 * k] = tsrc[k];
+      s_seg[tid + 256 * k] = tseg[k];
+    }
+  }
+  if (tid < B1) {
+    s_par[tid] = tpar;
+    s_cnt[tid] = tcnt;
+  }
+  __syncthreads();
+  if (!item || !folded) return;
+
   const int G = H / Hkv;
   const int g = lane >> 3;
   const int c = lane & 7;
@@ -61,9 +109,11 @@ __global__ __launch_bounds__(256) void sf_chain_kernel(
   const int gq = h * G + (gv ? g : 0);
   const int b = r / N;
   const int n = r - b * N;
-  const int s = src[r];
+  const int s = s_src[r];
   const int sflat = s * N + n;
   const int kvs = 2 * Hkv * kHD;
+  const uint16_t* kbase = kv_buf + h * kHD + c * 16;
+  const uint16_t* vbase = kv_buf + (Hkv + h) * kHD + c * 16;
 
   float q[16], o0[16];
   load16(q_buf + (size_t)sflat * H * kHD + gq * kHD + c * 16, q);
@@ -77,14 +127,22 @@ __global__ __launch_bounds__(256) void sf_chain_kernel(
   float mn = m0;
   int cur = b;
   for (int hop = 0; hop < B1 && cur != s; ++hop) {
-    const int cnt = segcnt[cur];
-    for (int j = 0; j < cnt; ++j) {
-      const int rj = seg[cur * N + j];
-      float kn[16];
-      load16(kv_buf + (size_t)rj * kvs + h * kHD + c * 16, kn);
-      mn = fmaxf(mn, dot16_group8(q, kn) * scaling);
+    const int cnt = s_cnt[cur];
+    const int* sg = s_seg + cur * N;
+    for (int j0 = 0; j0 < cnt; j0 += kBatch1) {
+      sf_u32x4 kw[kBatch1][2];
+#pragma unroll
+      for (int u = 0; u < kBatch1; ++u) load16w(kbase + (size_t)sg[min(j0 + u, cnt - 1)] * kvs, kw[u]);
+#pragma unroll
+      for (int u = 0; u < kBatch1; ++u) {
+        if (j0 + u < cnt) {
+          float kn[16];
+          unpack16(kw[u], kn);
+          mn = fmaxf(mn, dot16_group8(q, kn) * scaling);
+        }
+      }
     }
-    cur = par[cur];
+    cur = s_par[cur];
   }
 
   // pass 2: rescale the inherited state, then swap old entries for new ones
@@ -94,22 +152,38 @@ __global__ __launch_bounds__(256) void sf_chain_kernel(
   for (int i = 0; i < 16; ++i) num[i] = o0[i] * z;
   cur = b;
   for (int hop = 0; hop < B1 && cur != s; ++hop) {
-    const int pc = par[cur];
-    const int cnt = segcnt[cur];
-    for (int j = 0; j < cnt; ++j) {
-      const int rj = seg[cur * N + j];
-      const int e = rj % N;
-      const int old = src[pc * N + e] * N + e;
-      float ko[16], vo[16], kn[16], vn[16];
-      load16(kv_buf + (size_t)old * kvs + h * kHD + c * 16, ko);
-      load16(kv_buf + (size_t)old * kvs + (Hkv + h) * kHD + c * 16, vo);
-      load16(kv_buf + (size_t)rj * kvs + h * kHD + c * 16, kn);
-      load16(kv_buf + (size_t)rj * kvs + (Hkv + h) * kHD + c * 16, vn);
-      const float ao = expf(dot16_group8(q, ko) * scaling - mn);
-      const float an = expf(dot16_group8(q, kn) * scaling - mn);
-      z = z - ao + an;
+    const int pc = s_par[cur];
+    const int cnt = s_cnt[cur];
+    const int* sg = s_seg + cur * N;
+    for (int j0 = 0; j0 < cnt; j0 += kBatch2) {
+      sf_u32x4 ko[kBatch2][2], vo[kBatch2][2], kn[kBatch2][2], vn[kBatch2][2];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) num[i] = num[i] - ao * vo[i] + an * vn[i];
+      for (int u = 0; u < kBatch2; ++u) {
+        const int rj = sg[min(j0 + u, cnt - 1)];
+        const int e = rj % N;
+        const size_t old = (size_t)(s_src[pc * N + e] * N + e) * kvs;
+        const size_t nw = (size_t)rj * kvs;
+        load16w(kbase + old, ko[u]);
+        load16w(vbase + old, vo[u]);
+        load16w(kbase + nw, kn[u]);
+        load16w(vbase + nw, vn[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch2; ++u) {
+        if (j0 + u < cnt) {
+          float kof[16], knf[16];
+          unpack16(ko[u], kof);
+          unpack16(kn[u], knf);
+          const float ao = expf(dot16_group8(q, kof) * scaling - mn);
+          const float an = expf(dot16_group8(q, knf) * scaling - mn);
+          z = z - ao + an;
+          float vof[16], vnf[16];
+          unpack16(vo[u], vof);
+          unpack16(vn[u], vnf);
+#pragma unroll
+          for (int i = 0; i < 16; ++i) num[i] = num[i] - ao * vof[i] + an * vnf[i];
+        }
+      }
     }
     cur = pc;
   }

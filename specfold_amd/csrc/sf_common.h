@@ -10,6 +10,7 @@
 #include "specfold_amd.h"
 
 #define SF_DEV __device__ __forceinline__
+#define SF_HD __host__ __device__ __forceinline__
 
 typedef __bf16 sf_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float sf_f32x4 __attribute__((ext_vector_type(4)));
@@ -18,13 +19,12 @@ typedef uint32_t sf_u32x2 __attribute__((ext_vector_type(2)));
 
 SF_DEV float sf_bf2f(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
 
-// fp32 -> bf16, round to nearest even; NaN stays a quiet NaN.
-SF_DEV uint16_t sf_f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
+// fp32 -> bf16, round to nearest even, NaN kept a NaN: gfx950's
+// v_cvt_pk_bf16_f32 (checked bit-for-bit against the integer RNE formula
+// bits + 0x7fff + lsb on all 2^32 inputs).
+typedef __bf16 sf_bf16x2 __attribute__((ext_vector_type(2)));
+
+SF_DEV uint16_t sf_f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
 // Round an fp32 value through bf16 (the value a bf16 tensor op would store).
 SF_DEV float sf_rbf(float f) { return sf_bf2f(sf_f2bf(f)); }
@@ -39,7 +39,10 @@ SF_DEV void sf_unpack8(const sf_u32x4 w, float out[8]) {
 }
 
 SF_DEV uint32_t sf_pack2(float lo, float hi) {
-  return (uint32_t)sf_f2bf(lo) | ((uint32_t)sf_f2bf(hi) << 16);
+  sf_bf16x2 v;
+  v[0] = (__bf16)lo;
+  v[1] = (__bf16)hi;
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 // Full 64-lane butterfly reductions (result valid in every lane).

@@ -18,46 +18,6 @@ namespace {
 
 using namespace sfg;
 
-// hp[r, n] = bf16(x[r, n] + bf16(sum_s part[s, r, n])), 4 columns per thread
-__global__ __launch_bounds__(256) void reduce_residual_kernel(
-    const float* __restrict__ part, int nsplit, int mcap, int M, int N,
-    const uint16_t* __restrict__ x, uint16_t* __restrict__ out) {
-  const size_t q = (size_t)blockIdx.x * 256 + threadIdx.x;
-  const size_t total = (size_t)M * N / 4;
-  if (q >= total) return;
-  const size_t e = q * 4;
-  const size_t r = e / N, n = e - r * N;
-  sf_f32x4 s = *reinterpret_cast<const sf_f32x4*>(part + r * N + n);
-  for (int k = 1; k < nsplit; ++k)
-    s += *reinterpret_cast<const sf_f32x4*>(part + ((size_t)k * mcap + r) * N + n);
-  const sf_u32x2 xv = *reinterpret_cast<const sf_u32x2*>(x + e);
-  const float x0 = __uint_as_float(xv[0] << 16), x1 = __uint_as_float(xv[0] & 0xffff0000u);
-  const float x2 = __uint_as_float(xv[1] << 16), x3 = __uint_as_float(xv[1] & 0xffff0000u);
-  sf_u32x2 o;
-  o[0] = sf_pack2(x0 + sf_rbf(s[0]), x1 + sf_rbf(s[1]));
-  o[1] = sf_pack2(x2 + sf_rbf(s[2]), x3 + sf_rbf(s[3]));
-  *reinterpret_cast<sf_u32x2*>(out + e) = o;
-}
-
-// out[rows[m], n] = bf16(sum_s part[s, m, n]) for m < count
-__global__ __launch_bounds__(256) void reduce_scatter_kernel(
-    const float* __restrict__ part, int nsplit, int mcap, const int32_t* __restrict__ rows,
-    const int32_t* __restrict__ count_p, int N, uint16_t* __restrict__ out) {
-  const int M = min(*count_p, mcap);
-  const size_t q = (size_t)blockIdx.x * 256 + threadIdx.x;
-  const size_t total = (size_t)M * N / 4;
-  if (q >= total) return;
-  const size_t e = q * 4;
-  const size_t m = e / N, n = e - m * N;
-  sf_f32x4 s = *reinterpret_cast<const sf_f32x4*>(part + m * N + n);
-  for (int k = 1; k < nsplit; ++k)
-    s += *reinterpret_cast<const sf_f32x4*>(part + ((size_t)k * mcap + m) * N + n);
-  sf_u32x2 o;
-  o[0] = sf_pack2(s[0], s[1]);
-  o[1] = sf_pack2(s[2], s[3]);
-  *reinterpret_cast<sf_u32x2*>(out + (size_t)rows[m] * N + n) = o;
-}
-
 // Qwen2RMSNorm of compacted rows: out[m] = bf16(w * bf16(x[rows[m]] * rstd)); one wave per row.
 template <int VPL>
 __global__ __launch_bounds__(256) void rows_rmsnorm_kernel(
@@ -70,10 +30,13 @@ __global__ __launch_bounds__(256) void rows_rmsnorm_kernel(
   if (m >= M) return;
   const int nvec = D >> 3;
   const sf_u32x4* xr = reinterpret_cast<const sf_u32x4*>(x + (size_t)rows[m] * D);
-  sf_u32x4 xv[VPL];
+  const sf_u32x4* wr = reinterpret_cast<const sf_u32x4*>(w);
+  // all loads first (clamped addresses, no branches): one memory latency per wave
+  sf_u32x4 xv[VPL], wv[VPL];
 #pragma unroll
-  for (int i = 0; i < VPL; ++i)
-    if (lane + i * 64 < nvec) xv[i] = xr[lane + i * 64];
+  for (int i = 0; i < VPL; ++i) wv[i] = wr[min(lane + i * 64, nvec - 1)];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) xv[i] = xr[min(lane + i * 64, nvec - 1)];
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
@@ -86,7 +49,6 @@ __global__ __launch_bounds__(256) void rows_rmsnorm_kernel(
   }
   ss = sf_wave_sum(ss);
   const float inv = 1.0f / sqrtf(ss / (float)D + eps);
-  const sf_u32x4* wr = reinterpret_cast<const sf_u32x4*>(w);
   sf_u32x4* orow = reinterpret_cast<sf_u32x4*>(out + (size_t)m * D);
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
@@ -94,7 +56,7 @@ __global__ __launch_bounds__(256) void rows_rmsnorm_kernel(
     if (idx < nvec) {
       float f[8], g[8];
       sf_unpack8(xv[i], f);
-      sf_unpack8(wr[idx], g);
+      sf_unpack8(wv[i], g);
       sf_u32x4 o;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
@@ -124,15 +86,68 @@ __global__ __launch_bounds__(256) void residual_gather_add_kernel(
   *reinterpret_cast<sf_u32x4*>(out + (size_t)r * D + c) = o;
 }
 
+// Fix-up of the FFN down GEMM: tiles computed by several stream-K workgroups are
+// summed from their partial slots in slot order and scattered as bf16 rows
+// (tiles of a single workgroup were written by the GEMM itself).  One workgroup
+// per 64-column tile.
+__global__ __launch_bounds__(256) void down_fixup_kernel(const float* __restrict__ part, Plan plan,
+                                                         int mcap, const int32_t* __restrict__ rows,
+                                                         const int32_t* __restrict__ count_p, int N,
+                                                         uint16_t* __restrict__ out) {
+  const int t = blockIdx.x;
+  const int first = tile_first(t, plan);
+  const int nsl = tile_last(t, plan) - first + 1;
+  if (nsl == 1) return;
+  const int M = min(*count_p, mcap);
+  const size_t stride = (size_t)mcap * N;
+  for (int e = threadIdx.x; e < M * 16; e += 256) {
+    const int m = e >> 4, c = t * 64 + (e & 15) * 4;
+    const int row = rows[m];
+    const sf_f32x4 y = sum_slots<sf_f32x4>(part + (size_t)m * N + c, stride, nsl);
+    sf_u32x2 o;
+    o[0] = sf_pack2(y[0], y[1]);
+    o[1] = sf_pack2(y[2], y[3]);
+    *reinterpret_cast<sf_u32x2*>(out + (size_t)row * N + c) = o;
+  }
+}
+
+// Row-major W [N, K] -> the packed fragment-major layout of the GEMM core: 16-byte
+// word (tile t, chunk c, lane l) = W[16t + l%16][32c + 8(l/16) .. +8].  One thread
+// per 16-byte word, reads gathered, writes sequential.
+__global__ __launch_bounds__(256) void pack_weight_kernel(const uint16_t* __restrict__ w, int N,
+                                                          int K, uint16_t* __restrict__ out) {
+  const size_t q = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const size_t nwords = (size_t)N * K / 8;
+  if (q >= nwords) return;
+  const int l = (int)(q & 63);
+  const size_t tc = q >> 6;                 // tile * (K/32) + chunk
+  const int chunks = K / 32;
+  const size_t t = tc / chunks;
+  const int c = (int)(tc - t * chunks);
+  const size_t row = t * 16 + (l & 15);
+  const size_t k = (size_t)c * 32 + (l >> 4) * 8;
+  *reinterpret_cast<sf_u32x4*>(out + q * 8) = *reinterpret_cast<const sf_u32x4*>(w + row * K + k);
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
 
 extern "C" size_t sf_gemm_workspace_bytes(int mcap, int N, int K) {
-  if (mcap < 1 || N < 64 || K < kKC) return 0;
-  const int mblocks = (mcap + kMB - 1) / kMB;
-  const int ns = pick_nsplit(N / 64, K, mblocks);
-  return (size_t)ns * mcap * N * sizeof(float);
+  if (mcap < 1 || N < 64 || N % 64 || K < kKC || K % kKC) return 0;
+  const size_t b = part_bytes(make_plan(N / 64, K / kKC), mcap, N);
+  return b < 256 ? 256 : b;
+}
+
+extern "C" int sf_pack_weight(const uint16_t* w, int N, int K, uint16_t* out, void* stream) {
+  if (!w || !out || w == out) return SF_ERR_ARG;
+  if (N < 16 || N % 16 || K < kKC || K % kKC || !aligned16(w) || !aligned16(out))
+    return SF_ERR_SHAPE;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const size_t words = (size_t)N * K / 8;
+  hipLaunchKernelGGL(pack_weight_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, st, w,
+                     N, K, out);
+  return sf_launch_status();
 }
 
 extern "C" int sf_o_proj_residual(const uint16_t* o_bf, const uint16_t* x, const uint16_t* wo,
@@ -142,15 +157,12 @@ extern "C" int sf_o_proj_residual(const uint16_t* o_bf, const uint16_t* x, const
   if (M < 1 || M > 1024 || K % kKC || N % 64 || !aligned16(o_bf) || !aligned16(wo))
     return SF_ERR_SHAPE;
   if (workspace_bytes < sf_gemm_workspace_bytes(M, N, K)) return SF_ERR_WORKSPACE;
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const int mblocks = (M + kMB - 1) / kMB;
-  const int ns = pick_nsplit(N / 64, K, mblocks);
-  float* part = reinterpret_cast<float*>(workspace);
-  launch_gemm<1, kPartial>(o_bf, nullptr, K, nullptr, M, M, wo, nullptr, K, N, ns, part, nullptr,
-                           0, st);
-  const size_t total = (size_t)M * N / 4;
-  hipLaunchKernelGGL(reduce_residual_kernel, dim3((total + 255) / 256), dim3(256), 0, st, part, ns,
-                     M, M, N, x, hp);
+  Epi ep{};
+  ep.out = hp;
+  ep.ldo = N;
+  ep.res = x;
+  launch_sk<1, kResid>(make_plan_whole(N / 64, K / kKC), o_bf, nullptr, K, nullptr, M, M, wo,
+                       nullptr, K, N, nullptr, ep, reinterpret_cast<hipStream_t>(stream));
   return sf_launch_status();
 }
 
@@ -179,8 +191,12 @@ extern "C" int sf_ffn_gate_up(const uint16_t* zn, const int32_t* count, int buck
                               uint16_t* act, void* stream) {
   if (!zn || !count || !wg || !wu || !act) return SF_ERR_ARG;
   if (bucket < 1 || bucket > 1024 || D % kKC || I % 64) return SF_ERR_SHAPE;
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  launch_gemm<2, kSiluMul>(zn, nullptr, D, count, 0, bucket, wg, wu, D, I, 1, nullptr, act, I, st);
+  Epi ep{};
+  ep.out = act;
+  ep.ldo = I;
+  // one workgroup per 64-column tile (whole K): SiLU*mul straight from registers
+  launch_sk<2, kSilu>(make_plan_whole(I / 64, D / kKC), zn, nullptr, D, count, 0, bucket, wg, wu,
+                      D, I, nullptr, ep, reinterpret_cast<hipStream_t>(stream));
   return sf_launch_status();
 }
 
@@ -192,14 +208,15 @@ extern "C" int sf_ffn_down_scatter(const uint16_t* act, const int32_t* count, in
   if (bucket < 1 || bucket > 1024 || I % kKC || D % 64) return SF_ERR_SHAPE;
   if (workspace_bytes < sf_gemm_workspace_bytes(bucket, D, I)) return SF_ERR_WORKSPACE;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const int mblocks = (bucket + kMB - 1) / kMB;
-  const int ns = pick_nsplit(D / 64, I, mblocks);
+  const Plan p = make_plan(D / 64, I / kKC);
   float* part = reinterpret_cast<float*>(workspace);
-  launch_gemm<1, kPartial>(act, nullptr, I, count, 0, bucket, wd, nullptr, I, D, ns, part,
-                           nullptr, 0, st);
-  const size_t total = (size_t)bucket * D / 4;
-  hipLaunchKernelGGL(reduce_scatter_kernel, dim3((total + 255) / 256), dim3(256), 0, st, part, ns,
-                     bucket, rows, count, D, ffn);
+  Epi ep{};
+  ep.rows = rows;
+  ep.out = ffn;
+  ep.ldo = D;
+  launch_sk<1, kScatter>(p, act, nullptr, I, count, 0, bucket, wd, nullptr, I, D, part, ep, st);
+  hipLaunchKernelGGL(down_fixup_kernel, dim3(p.T), dim3(256), 0, st, part, p, bucket, rows, count,
+                     D, ffn);
   return sf_launch_status();
 }
 
@@ -217,13 +234,11 @@ extern "C" int sf_residual_gather_add(const uint16_t* hp, const uint16_t* ffn, c
 extern "C" int sf_lm_head(const uint16_t* x, int M, const uint16_t* w, int D, int V,
                           uint16_t* logits, void* stream) {
   if (!x || !w || !logits) return SF_ERR_ARG;
-  if (M < 1 || M > 1024 || D % kKC || V % 64) return SF_ERR_SHAPE;
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (V % 128 == 0)
-    launch_gemm<2, kBf16>(x, nullptr, D, nullptr, M, M, w, nullptr, D, V, 1, nullptr, logits, V,
-                          st);
-  else
-    launch_gemm<1, kBf16>(x, nullptr, D, nullptr, M, M, w, nullptr, D, V, 1, nullptr, logits, V,
-                          st);
+  if (M < 1 || M > 1024 || D % kKC || V % 128) return SF_ERR_SHAPE;
+  Epi ep{};
+  ep.out = logits;
+  ep.ldo = V;
+  launch_sk<2, kPlain>(make_plan_whole(V / 128, D / kKC), x, nullptr, D, nullptr, M, M, w,
+                       nullptr, D, V, nullptr, ep, reinterpret_cast<hipStream_t>(stream));
   return sf_launch_status();
 }

@@ -34,29 +34,33 @@ __global__ __launch_bounds__(256) void sf_gate_rows_kernel(
   const int nvec = D >> 3;
   const sf_u32x4* xrow = reinterpret_cast<const sf_u32x4*>(hidden + (size_t)r * D);
   const sf_u32x4* prow = reinterpret_cast<const sf_u32x4*>(hidden + (size_t)(p * N + n) * D);
+  const sf_u32x4* wrow = reinterpret_cast<const sf_u32x4*>(ln_w);
 
-  sf_u32x4 xv[VPL];
+  // Every load of the row, its parent row and the norm weight is issued before
+  // the first use (clamped addresses, no branches), so the wave pays one memory
+  // latency instead of one per vector.
+  sf_u32x4 xv[VPL], pv[VPL], wv[VPL];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) xv[i] = xrow[min(lane + i * 64, nvec - 1)];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) pv[i] = prow[min(lane + i * 64, nvec - 1)];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) wv[i] = wrow[min(lane + i * 64, nvec - 1)];
+
   float ss = 0.f, ds = 0.f, ps = 0.f;
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
-    const int idx = lane + i * 64;
-    if (idx < nvec) {
-      xv[i] = xrow[idx];
-      float xf[8];
-      sf_unpack8(xv[i], xf);
+    if (lane + i * 64 >= nvec) continue;
+    float xf[8], pf[8];
+    sf_unpack8(xv[i], xf);
+    sf_unpack8(pv[i], pf);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) ss = fmaf(xf[j], xf[j], ss);
-      if (draft) {
-        float pf[8];
-        sf_unpack8(prow[idx], pf);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          float d = xf[j] - pf[j];
-          if (mode == SF_GATE_MODEL_DTYPE) d = sf_rbf(d);  // x - x_par is a bf16 tensor op
-          ds = fmaf(d, d, ds);
-          ps = fmaf(pf[j], pf[j], ps);
-        }
-      }
+    for (int j = 0; j < 8; ++j) {
+      ss = fmaf(xf[j], xf[j], ss);
+      float d = xf[j] - pf[j];
+      if (mode == SF_GATE_MODEL_DTYPE) d = sf_rbf(d);  // x - x_par is a bf16 tensor op
+      ds = fmaf(d, d, ds);
+      ps = fmaf(pf[j], pf[j], ps);
     }
   }
   ss = sf_wave_sum(ss);
@@ -84,7 +88,6 @@ __global__ __launch_bounds__(256) void sf_gate_rows_kernel(
   if (!is_rec) return;
 
   // normalized row: bf16(w * bf16(x * rstd)), as Qwen2RMSNorm in bf16.
-  const sf_u32x4* wv = reinterpret_cast<const sf_u32x4*>(ln_w);
   sf_u32x4* out = reinterpret_cast<sf_u32x4*>(xn + (size_t)r * D);
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
@@ -92,7 +95,7 @@ __global__ __launch_bounds__(256) void sf_gate_rows_kernel(
     if (idx < nvec) {
       float xf[8], wf[8];
       sf_unpack8(xv[i], xf);
-      sf_unpack8(wv[idx], wf);
+      sf_unpack8(wv[i], wf);
       sf_u32x4 o;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {

@@ -1,12 +1,14 @@
 // Weight-streaming GEMM core for skinny row blocks:  C[m, n] = sum_k A[arow(m), k] * W[n, k]
 //
 // Shapes on this path: M = recomputed rows (<= 256, often 30-120) or all BN rows,
-// N and K = 1.5k-38k; W (bf16, [N, K], K contiguous) is the big operand and is read
-// once from HBM.  A workgroup is 4 waves; wave w owns WN column tiles of 16; a block
-// of up to 128 rows of A is staged through LDS in 128-wide K stages (double
-// buffered) and shared by the 4 waves; every wave streams its own weight rows
-// straight into VGPRs one stage ahead (WN x 4 x 16 B per lane), so a workgroup keeps
-// 16-32 KB of weight loads in flight.  MFMA: v_mfma_f32_16x16x32_bf16, fp32 acc.
+// N and K = 1.5k-38k; W (bf16, [N, K], packed fragment-major) is the big operand
+// and is read once from HBM.  A workgroup is 4 waves; wave w owns WN column tiles
+// of 16; a block of up to 64 rows of A is staged through LDS in 128-wide K stages
+// (double buffered) and shared by the 4 waves; every wave streams its own weight
+// tiles straight into VGPRs.  Work is split stream-K: a fixed grid of workgroups
+// per m block, each taking an equal share of the (tile, K stage) units; tiles
+// shared by several workgroups are summed by a fix-up kernel.
+// MFMA: v_mfma_f32_16x16x32_bf16, fp32 accumulation.
 //
 // Operand layout of v_mfma_f32_16x16x32_bf16 (64 lanes): A 16x32 — lane l holds
 // A[l%16][8*(l/16) .. +8]; B 32x16 — lane l holds B[8*(l/16) .. +8][l%16];
@@ -31,206 +33,286 @@ struct Smem {
   int rows[kMB];
 };
 
-// Weight prefetch depth: a ring of SFG_PF register slots per wave, so every wave
-// keeps (SFG_PF-1) stages of weight loads (WN x 4 KB each) outstanding.
-#ifndef SFG_PF
-#define SFG_PF 2
+// Prefetch depth: a ring of SFG_RING register slots per wave (A rows and weights
+// of one K stage each), so every wave keeps SFG_RING-1 stages of loads
+// (WN x 4 KB of weights each) outstanding.
+#ifndef SFG_RING
+#define SFG_RING 2
 #endif
 #ifndef SFG_WAVES
 #define SFG_WAVES 2   // waves per SIMD the register allocation targets
 #endif
 
+// Weight layout (fragment-major, "packed"): for each 16-row tile of W [N, K] and
+// each 32-wide K chunk, the 64 lanes' MFMA B fragments (lane l holds
+// W[16t + l%16][32c + 8(l/16) .. +8]) are one contiguous 1 KB block, and the
+// chunks of a tile follow each other, so every wave's weight stream is a
+// sequential read.  sf_pack_weight produces it from row-major W.
+constexpr int kKsStride = 512;     // elements between 32-wide chunks of a tile
+constexpr int kStageElems = 2048;  // elements between 128-wide K stages of a tile
+SF_DEV const uint16_t* weight_lane_ptr(const uint16_t* W, int tile16, int K, int lane) {
+  return W + (size_t)tile16 * (K / 32) * 512 + lane * 8;
+}
+
 // Main loop over stages [s0, s1) of K for NMT m tiles of 16 rows (NMT is a
-// template parameter so the MFMA loop is straight-line).  `wrow[t]` points at
-// W[col_t][kq] for this lane (kq = 8*(lane/16)); `acc[mt][t]` accumulates rows
-// mt*16.., column tile t.
+// template parameter so the MFMA loop is straight-line).  `wrow[t]` is this
+// lane's weight stream for column tile t; `acc[mt][t]` accumulates rows mt*16..,
+// column tile t.
 //
-// Load order matters: a wave's vector-memory loads complete in issue order, so
-// waiting for one waits for every older one.  Each iteration therefore issues
-// the A stage two ahead (s+2) BEFORE the weight stage PF-1 ahead; writing A(s+1)
-// into LDS at the end of iteration s then waits only for loads issued before
-// A(s+1), never for the weights still in flight.  The loop is unrolled by PF
-// (a multiple of 2) so ring slots and LDS buffers are compile-time indices.
+// Stage s's A rows and weights are issued together, SFG_RING-1 stages ahead, into
+// a register ring of SFG_RING slots (A too, not only W).  A wave's vector-memory
+// loads complete in issue order, so waiting for stage s then waits for nothing
+// younger: the SFG_RING-1 later stages stay in flight.  A(s) goes to LDS (double
+// buffered) only at the start of iteration s, followed by the one barrier of the
+// stage.  Loads past the last stage re-read it and rows past mrows re-read the
+// last row (clamped, no branches), which keeps the wait counts exact.
 template <int WN, int NMT>
 SF_DEV void mainloop(const uint16_t* __restrict__ A, int lda, int mrows,
                      const uint16_t* const (&wrow)[WN], int s0, int s1, Smem& sm,
                      sf_f32x4 (&acc)[kMT][WN]) {
-  constexpr int PF = SFG_PF;
-  static_assert(PF % 2 == 0, "ring depth must be even (LDS double buffer parity)");
+  constexpr int R = SFG_RING;
+  static_assert(R % 2 == 0, "ring depth must be even (LDS double buffer parity)");
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int kq = (lane >> 4) * 8;
   const int a_seg = tid & 15;      // 16 x 16 B per 128-wide row stage
   const int a_row0 = tid >> 4;     // 16 rows per pass, NMT passes
-  sf_u32x4 areg[2][NMT];
-  sf_u32x4 w[PF][WN][4];
+  const int slast = s1 - 1;
+  const uint16_t* arow[NMT];
+#pragma unroll
+  for (int p = 0; p < NMT; ++p)
+    arow[p] = A + (size_t)sm.rows[min(a_row0 + p * 16, mrows - 1)] * lda + a_seg * 8;
+  sf_u32x4 areg[R][NMT];
+  sf_u32x4 w[R][WN][4];
 
-  auto load_a = [&](int s, sf_u32x4 (&ar)[NMT]) {
+  auto issue = [&](int s, int slot) {
+    const int sc = min(s, slast);
 #pragma unroll
-    for (int p = 0; p < NMT; ++p) {
-      const int r = a_row0 + p * 16;
-      if (r < mrows)
-        ar[p] = *reinterpret_cast<const sf_u32x4*>(A + (size_t)sm.rows[r] * lda + s * kKC +
-                                                   a_seg * 8);
-    }
-  };
-  auto store_a = [&](int buf, const sf_u32x4 (&ar)[NMT]) {
-#pragma unroll
-    for (int p = 0; p < NMT; ++p) {
-      const int r = a_row0 + p * 16;
-      if (r < mrows)
-        *reinterpret_cast<sf_u32x4*>(&sm.a[buf][r * kLdsStride + a_seg * 8]) = ar[p];
-    }
-  };
-  auto load_w = [&](int s, sf_u32x4 (&ws)[WN][4]) {
+    for (int p = 0; p < NMT; ++p)
+      areg[slot][p] = *reinterpret_cast<const sf_u32x4*>(arow[p] + sc * kKC);
 #pragma unroll
     for (int t = 0; t < WN; ++t)
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks)
-        ws[t][ks] = *reinterpret_cast<const sf_u32x4*>(wrow[t] + s * kKC + ks * 32);
+        w[slot][t][ks] =
+            *reinterpret_cast<const sf_u32x4*>(wrow[t] + (size_t)sc * kStageElems + ks * kKsStride);
   };
 
-  // prologue: A(s0), A(s0+1) first, then weight stages s0 .. s0+PF-2
-  load_a(s0, areg[0]);
-  if (s0 + 1 < s1) load_a(s0 + 1, areg[1]);
 #pragma unroll
-  for (int j = 0; j < PF - 1; ++j)
-    if (s0 + j < s1) load_w(s0 + j, w[j]);
-  store_a(0, areg[0]);
-  __syncthreads();
+  for (int j = 0; j < R - 1; ++j) issue(s0 + j, j);
 
 #pragma unroll 1
-  for (int sb = s0; sb < s1; sb += PF) {
+  for (int sb = s0; sb < s1; sb += R) {
 #pragma unroll
-    for (int j = 0; j < PF; ++j) {
+    for (int j = 0; j < R; ++j) {
       const int s = sb + j;
-      if (s < s1) {
-        // slot parity: stage s's A is in LDS buffer j&1 and A(s+1) in areg[(j+1)&1]
-        if (s + 2 < s1) load_a(s + 2, areg[j & 1]);
-        if (s + PF - 1 < s1) load_w(s + PF - 1, w[(j + PF - 1) % PF]);
-        const uint16_t* abase = &sm.a[j & 1][(lane & 15) * kLdsStride + kq];
+      if (s >= s1) break;
+      issue(s + R - 1, (j + R - 1) % R);
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
+      for (int p = 0; p < NMT; ++p)
+        *reinterpret_cast<sf_u32x4*>(&sm.a[j & 1][(a_row0 + p * 16) * kLdsStride + a_seg * 8]) =
+            areg[j][p];
+      __syncthreads();
+      const uint16_t* abase = &sm.a[j & 1][(lane & 15) * kLdsStride + kq];
 #pragma unroll
-          for (int mt = 0; mt < NMT; ++mt) {
-            const sf_bf16x8 af = sf_as_bf16x8(
-                *reinterpret_cast<const sf_u32x4*>(abase + mt * 16 * kLdsStride + ks * 32));
+      for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
-            for (int t = 0; t < WN; ++t)
-              acc[mt][t] = sf_mfma16x16x32(af, sf_as_bf16x8(w[j][t][ks]), acc[mt][t]);
-          }
+        for (int mt = 0; mt < NMT; ++mt) {
+          const sf_bf16x8 af = sf_as_bf16x8(
+              *reinterpret_cast<const sf_u32x4*>(abase + mt * 16 * kLdsStride + ks * 32));
+#pragma unroll
+          for (int t = 0; t < WN; ++t)
+            acc[mt][t] = sf_mfma16x16x32(af, sf_as_bf16x8(w[j][t][ks]), acc[mt][t]);
         }
-        if (s + 1 < s1) store_a((j + 1) & 1, areg[(j + 1) & 1]);
-        __syncthreads();
       }
     }
   }
 }
 
-// Number of K splits so that (column tiles x splits) covers the 256 CUs with one
-// active M block (the common case: the row count is known only on the device).
-inline int pick_nsplit(int tiles, int K, int /*mblocks*/ = 1) {
-  const int nst = K / kKC;
-  int s = (256 + tiles - 1) / tiles;
-  if (s < 1) s = 1;
-  if (s > nst) s = nst;
-  return s;
+// ---------------------------------------------------------------------------
+// Stream-K schedule.  The output columns are cut into T tiles of TW columns and K
+// into S stages of 128; the T*S (tile, stage) units are dealt out in tile-major
+// order, U consecutive units per workgroup, so every workgroup streams the same
+// number of weight bytes whatever T is (a fixed tile-per-workgroup grid leaves
+// some CUs with twice the work of others).  A workgroup's range may end one tile
+// and start the next.  A tile computed by one workgroup alone gets its epilogue
+// straight from registers; the pieces of a tile shared by several workgroups go
+// to fp32 partial slots (slot j = g - first(t)) that a fix-up kernel sums in slot
+// order after the GEMM — deterministic, and no cross-workgroup synchronisation
+// inside the kernel (an agent-scope fence costs a whole-L2 write-back and
+// invalidate on this multi-XCD part).
+#ifndef SFG_GRID
+#define SFG_GRID 512   // workgroups per m block (MI355X: two per CU)
+#endif
+
+struct Plan {
+  int T;  // column tiles
+  int S;  // K stages
+  int U;  // units per workgroup
+};
+
+// Balanced plan over SFG_GRID workgroups.
+inline Plan make_plan(int T, int S) {
+  const long long units = (long long)T * S;
+  const int U = (int)((units + SFG_GRID - 1) / SFG_GRID);
+  return Plan{T, S, U < 1 ? 1 : U};
+}
+// One workgroup per whole tile: every tile has a single contributor.
+inline Plan make_plan_whole(int T, int S) { return Plan{T, S, S}; }
+inline int plan_grid(const Plan& p) {
+  return (int)(((long long)p.T * p.S + p.U - 1) / p.U);
+}
+// Upper bound of contributors (slots) per tile.
+inline int plan_slots(const Plan& p) { return p.U >= p.S ? 2 : (p.S + p.U - 1) / p.U + 1; }
+
+SF_HD int tile_first(int t, const Plan& p) {
+  return (int)((long long)t * p.S / p.U);
+}
+SF_HD int tile_last(int t, const Plan& p) {
+  return (int)(((long long)(t + 1) * p.S - 1) / p.U);
 }
 
-// Epilogue modes of gemm_rows_kernel.
-enum Mode { kPartial = 0, kSiluMul = 1, kBf16 = 2 };
+// sum_{j < n} p[j * stride .. +T] in slot order (deterministic).  Loads go out four
+// at a time from clamped addresses with no branch in between.
+template <typename T>
+SF_DEV T sum_slots(const float* p, size_t stride, int n) {
+  T acc = *reinterpret_cast<const T*>(p);
+  for (int s0 = 1; s0 < n; s0 += 4) {
+    T v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      v[j] = *reinterpret_cast<const T*>(p + (size_t)min(s0 + j, n - 1) * stride);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (s0 + j < n) acc += v[j];
+  }
+  return acc;
+}
 
+// Output modes.
+enum Mode {
+  kPart = 0,     // every tile piece to its partial slot (QKV: the fix-up adds bias + RoPE)
+  kScatter = 1,  // out[rows[m]][c] = bf16(y); shared tiles to partial slots (FFN down)
+  kSilu = 2,     // out[m][c] = bf16(bf16(silu(bf16 y_gate)) * bf16 y_up); whole tiles only
+  kResid = 3,    // out[m][c] = bf16(res[m][c] + bf16(y)); whole tiles only (o_proj)
+  kPlain = 4,    // out[m][c] = bf16(y); whole tiles only (lm_head)
+};
+
+struct Epi {
+  const int32_t* rows;  // output row of compacted row m (kScatter)
+  uint16_t* out;        // bf16 output, row stride ldo
+  int ldo;
+  const uint16_t* res;  // residual (kResid), row stride ldo
+};
+
+// C = A[rows] . W^T on packed weights, stream-K over (tile, stage) units; WN column
+// tiles of 16 per wave (kSilu: WN = 2 = the gate and the up tile of the same 16
+// output columns).  Grid: (plan_grid, 1, m blocks).  part: fp32 partial slots
+// [slot][mcap][N].
 template <int WN, int MODE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SFG_WAVES, SFG_WAVES)))
-void gemm_rows_kernel(
-    const uint16_t* __restrict__ A, const int32_t* __restrict__ a_rows, int lda,
-    const int32_t* __restrict__ count_p, int m_static, int mcap, const uint16_t* __restrict__ W0,
-    const uint16_t* __restrict__ W1, int K, int N, int nsplit, float* __restrict__ part,
-    uint16_t* __restrict__ out, int ldo) {
+void gemm_sk_kernel(const uint16_t* __restrict__ A, const int32_t* __restrict__ a_rows, int lda,
+                    const int32_t* __restrict__ count_p, int m_static, int mcap,
+                    const uint16_t* __restrict__ W0, const uint16_t* __restrict__ W1, int K, int N,
+                    Plan plan, float* __restrict__ part, Epi ep) {
   __shared__ Smem sm;
   const int M = count_p ? min(*count_p, mcap) : m_static;
   const int m0 = blockIdx.z * kMB;
   if (m0 >= M) return;
   const int mrows = min(kMB, M - m0);
   const int nmt = (mrows + 15) >> 4;
-  const int lane = threadIdx.x & 63;
-  const int wv = threadIdx.x >> 6;
-  for (int i = threadIdx.x; i < mrows; i += 256) sm.rows[i] = a_rows ? a_rows[m0 + i] : m0 + i;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = tid >> 6;
+  if (tid < kMB) {
+    const int r = m0 + min(tid, mrows - 1);
+    sm.rows[tid] = a_rows ? a_rows[r] : r;
+  }
   __syncthreads();
-  const int nst = K / kKC;
-  const int s0 = blockIdx.y * nst / nsplit;
-  const int s1 = (blockIdx.y + 1) * nst / nsplit;
-  const int kq = (lane >> 4) * 8;
-  int col[WN];
-  const uint16_t* wrow[WN];
-  if (MODE == kSiluMul) {
-    // tile 0 = gate rows, tile 1 = up rows, same 16 output columns
-    const int c = blockIdx.x * 64 + wv * 16 + (lane & 15);
+  const size_t stride = (size_t)mcap * N;
+  const int g = blockIdx.x;
+  const int total = plan.T * plan.S;
+  const int u_end = min((g + 1) * plan.U, total);
+  for (int u = g * plan.U; u < u_end;) {
+    const int t = u / plan.S;
+    const int sa = u - t * plan.S;
+    const int sb = min(plan.S, sa + (u_end - u));
+    int col[WN];
+    const uint16_t* wrow[WN];
+    if (MODE == kSilu) {
+      const int c = t * 64 + wv * 16 + (lane & 15);
 #pragma unroll
-    for (int t = 0; t < WN; ++t) col[t] = c;
-    wrow[0] = W0 + (size_t)c * K + kq;
-    wrow[WN - 1] = W1 + (size_t)c * K + kq;
-  } else {
+      for (int tt = 0; tt < WN; ++tt) col[tt] = c;
+      wrow[0] = weight_lane_ptr(W0, c >> 4, K, lane);
+      wrow[WN - 1] = weight_lane_ptr(W1, c >> 4, K, lane);
+    } else {
 #pragma unroll
-    for (int t = 0; t < WN; ++t) {
-      col[t] = blockIdx.x * 64 * WN + wv * 16 * WN + t * 16 + (lane & 15);
-      wrow[t] = W0 + (size_t)col[t] * K + kq;
-    }
-  }
-  sf_f32x4 acc[kMT][WN];
-#pragma unroll
-  for (int mt = 0; mt < kMT; ++mt)
-#pragma unroll
-    for (int t = 0; t < WN; ++t) acc[mt][t] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
-
-  switch (nmt) {
-    case 1: mainloop<WN, 1>(A, lda, mrows, wrow, s0, s1, sm, acc); break;
-    case 2: mainloop<WN, 2>(A, lda, mrows, wrow, s0, s1, sm, acc); break;
-    case 3: mainloop<WN, 3>(A, lda, mrows, wrow, s0, s1, sm, acc); break;
-#if SFG_MB > 64
-    case 4: mainloop<WN, 4>(A, lda, mrows, wrow, s0, s1, sm, acc); break;
-    case 5: mainloop<WN, 5>(A, lda, mrows, wrow, s0, s1, sm, acc); break;
-    case 6: mainloop<WN, 6>(A, lda, mrows, wrow, s0, s1, sm, acc); break;
-    case 7: mainloop<WN, 7>(A, lda, mrows, wrow, s0, s1, sm, acc); break;
-    default: mainloop<WN, kMT>(A, lda, mrows, wrow, s0, s1, sm, acc); break;
-#else
-    default: mainloop<WN, kMT>(A, lda, mrows, wrow, s0, s1, sm, acc); break;
-#endif
-  }
-
-#pragma unroll
-  for (int mt = 0; mt < kMT; ++mt) {
-    if (mt >= nmt) continue;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = mt * 16 + (lane >> 4) * 4 + i;
-      if (m >= mrows) continue;
-      if (MODE == kPartial) {
-        float* p = part + ((size_t)blockIdx.y * mcap + m0 + m) * N;
-#pragma unroll
-        for (int t = 0; t < WN; ++t) p[col[t]] = acc[mt][t][i];
-      } else if (MODE == kBf16) {
-#pragma unroll
-        for (int t = 0; t < WN; ++t) out[(size_t)(m0 + m) * ldo + col[t]] = sf_f2bf(acc[mt][t][i]);
-      } else {
-        const float g = sf_rbf(acc[mt][0][i]);
-        const float u = sf_rbf(acc[mt][WN - 1][i]);
-        const float s = sf_rbf(g / (1.0f + expf(-g)));
-        out[(size_t)(m0 + m) * ldo + col[0]] = sf_f2bf(s * u);
+      for (int tt = 0; tt < WN; ++tt) {
+        col[tt] = t * 64 * WN + wv * 16 * WN + tt * 16 + (lane & 15);
+        wrow[tt] = weight_lane_ptr(W0, col[tt] >> 4, K, lane);
       }
     }
+    sf_f32x4 acc[kMT][WN];
+#pragma unroll
+    for (int mt = 0; mt < kMT; ++mt)
+#pragma unroll
+      for (int tt = 0; tt < WN; ++tt) acc[mt][tt] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
+    switch (nmt) {
+      case 1: mainloop<WN, 1>(A, lda, mrows, wrow, sa, sb, sm, acc); break;
+      case 2: mainloop<WN, 2>(A, lda, mrows, wrow, sa, sb, sm, acc); break;
+      case 3: mainloop<WN, 3>(A, lda, mrows, wrow, sa, sb, sm, acc); break;
+      default: mainloop<WN, kMT>(A, lda, mrows, wrow, sa, sb, sm, acc); break;
+    }
+    const int first = tile_first(t, plan);
+    const bool whole = MODE != kPart && tile_last(t, plan) == first;
+    float* pw = part + (size_t)(g - first) * stride + (size_t)m0 * N;
+#pragma unroll
+    for (int mt = 0; mt < kMT; ++mt) {
+      if (mt >= nmt) continue;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = mt * 16 + (lane >> 4) * 4 + i;
+        if (m >= mrows) continue;
+        if (!whole) {
+#pragma unroll
+          for (int tt = 0; tt < WN; ++tt) pw[(size_t)m * N + col[tt]] = acc[mt][tt][i];
+        } else if (MODE == kSilu) {
+          const float gt = sf_rbf(acc[mt][0][i]);
+          const float r = sf_rbf(gt / (1.0f + expf(-gt))) * sf_rbf(acc[mt][WN - 1][i]);
+          ep.out[(size_t)(m0 + m) * ep.ldo + col[0]] = sf_f2bf(r);
+        } else {
+#pragma unroll
+          for (int tt = 0; tt < WN; ++tt) {
+            const float y = acc[mt][tt][i];
+            if (MODE == kResid) {
+              const size_t o = (size_t)(m0 + m) * ep.ldo + col[tt];
+              ep.out[o] = sf_f2bf(sf_bf2f(ep.res[o]) + sf_rbf(y));
+            } else {
+              const size_t orow = MODE == kScatter ? (size_t)ep.rows[m0 + m] : (size_t)(m0 + m);
+              ep.out[orow * ep.ldo + col[tt]] = sf_f2bf(y);
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();  // the next piece's first A stage reuses LDS buffer 0
+    u += sb - sa;
   }
 }
 
+// Partial slots of a plan: [plan_slots][mcap][N] fp32.
+inline size_t part_bytes(const Plan& p, int mcap, int N) {
+  return (size_t)plan_slots(p) * mcap * N * sizeof(float);
+}
+
 template <int WN, int MODE>
-inline void launch_gemm(const uint16_t* A, const int32_t* a_rows, int lda,
-                        const int32_t* count_p, int m_static, int mcap, const uint16_t* W0,
-                        const uint16_t* W1, int K, int N, int nsplit, float* part, uint16_t* out,
-                        int ldo, hipStream_t st) {
-  const int span = MODE == kSiluMul ? 64 : 64 * WN;
-  dim3 grid(N / span, nsplit, (mcap + kMB - 1) / kMB);
-  hipLaunchKernelGGL((gemm_rows_kernel<WN, MODE>), grid, dim3(256), 0, st, A, a_rows, lda,
-                     count_p, m_static, mcap, W0, W1, K, N, nsplit, part, out, ldo);
+inline void launch_sk(const Plan& p, const uint16_t* A, const int32_t* a_rows, int lda,
+                      const int32_t* count_p, int m_static, int mcap, const uint16_t* W0,
+                      const uint16_t* W1, int K, int N, float* part, const Epi& ep,
+                      hipStream_t st) {
+  dim3 grid(plan_grid(p), 1, (mcap + kMB - 1) / kMB);
+  hipLaunchKernelGGL((gemm_sk_kernel<WN, MODE>), grid, dim3(256), 0, st, A, a_rows, lda, count_p,
+                     m_static, mcap, W0, W1, K, N, p, part, ep);
 }
 
 }  // namespace sfg

@@ -98,13 +98,12 @@ class _Buffers:
         self.hid = torch.zeros(2, BN, D, dtype=bf, device=dev)       # layer outputs, ping-pong
         self.final = torch.zeros(BN, D, dtype=bf, device=dev)
         self.attn_out = torch.zeros(BN, D, dtype=bf, device=dev)
-        self.cos = torch.zeros(N, hd, dtype=bf, device=dev)    # RoPE tables of the step
-        self.sin = torch.zeros(N, hd, dtype=bf, device=dev)
+        self.pos0 = torch.zeros(1, **i32)   # first block position (caches without length_dev)
         self.all_rows = torch.arange(BN, **i32)
         self.all_count = torch.full((1,), BN, **i32)
         nq = (H + 2 * Hkv) * hd
-        self.ws_gemm = torch.empty(max(_lib.gemm_workspace_bytes(BN, D, H * hd),
-                                       _lib.gemm_workspace_bytes(bucket, D, eng.I), 256),
+        # GEMM workspaces: fp32 partial slots of the stream-K split
+        self.ws_gemm = torch.empty(max(_lib.gemm_workspace_bytes(bucket, D, eng.I), 256),
                                    dtype=torch.uint8, device=dev)
         self.ws_qkv = torch.empty(max(_lib.qkv_workspace_bytes(bucket, D, nq), 256),
                                   dtype=torch.uint8, device=dev)
@@ -141,19 +140,30 @@ class FoldedVerifyEngine:
         self.eps = float(rms_eps if rms_eps is not None else
                          getattr(cfg, "rms_norm_eps", 1e-6))
         self.gate_mode = gate_mode
+        # Weights of the HIP GEMMs, packed once into the fragment-major layout the
+        # weight-streaming kernels read (the reference packs W_qkv / W_gu once too,
+        # fastdllm_v2_folded.py:77-87).  The module tree keeps its own tensors.
         self._packed: List[Tuple[torch.Tensor, Optional[torch.Tensor]]] = []
+        self._packed_mlp: List[Tuple[torch.Tensor, torch.Tensor, torch.Tensor]] = []
         for lyr in self.layers:
             a = lyr.self_attn
             w = torch.cat([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight], 0).contiguous()
             use_bias = has_qkv_bias if has_qkv_bias is not None else a.q_proj.bias is not None
             b = (torch.cat([a.q_proj.bias, a.k_proj.bias, a.v_proj.bias], 0).contiguous()
                  if use_bias and a.q_proj.bias is not None else None)
-            self._packed.append((w, b))
+            self._packed.append((_lib.pack_weight(w), b))
+            del w
+            m = lyr.mlp
+            self._packed_mlp.append((_lib.pack_weight(m.gate_proj.weight.contiguous()),
+                                     _lib.pack_weight(m.up_proj.weight.contiguous()),
+                                     _lib.pack_weight(m.down_proj.weight.contiguous())))
         self._bufs: Dict[Tuple[int, int, int], _Buffers] = {}
         # HIP graphs of the layer loop, keyed by shape / prefix / delta / cache
+        # (one per branch count the decode loop visits: B1 = 1..8 plus block commits)
         self.use_graphs = True
-        self.max_graphs = 4
+        self.max_graphs = 16
         self._graphs: Dict[tuple, tuple] = {}
+        self._rope: Optional[Tuple[torch.Tensor, torch.Tensor]] = None
 
     # ------------------------------------------------------------------------
     def buffers(self, B1: int, N: int, bucket: int, P: int) -> _Buffers:
@@ -167,10 +177,21 @@ class FoldedVerifyEngine:
             self._bufs[key] = buf
         return buf
 
-    def rope_tables(self, hidden: torch.Tensor, P: int, N: int):
-        pos = torch.arange(P, P + N, device=self.device).unsqueeze(0)
-        cos, sin = self.model.model.rotary_emb(hidden, pos)
-        return cos[0].contiguous(), sin[0].contiguous()
+    def rope_tables(self, rows_needed: int) -> Tuple[torch.Tensor, torch.Tensor]:
+        """cos/sin [T, hd] over absolute positions 0..T-1 from the model's own
+        rotary embedding (each entry is elementwise in its position, so a row of
+        the full table equals the table of the block alone).  The kernels index it
+        with the device-side prefix length.  Growing it moves the tables, so the
+        captured graphs that point at them are dropped."""
+        if self._rope is None or self._rope[0].shape[0] < rows_needed:
+            T = max(int(rows_needed), int(getattr(self.cfg, "max_position_embeddings", 0) or 0),
+                    4096)
+            base = self.model.model
+            pos = torch.arange(T, device=self.device).unsqueeze(0)
+            cos, sin = base.rotary_emb(base.embed_tokens.weight, pos)
+            self._rope = (cos[0].contiguous(), sin[0].contiguous())
+            self._graphs.clear()
+        return self._rope
 
     # ------------------------------------------------------------------------
     @torch.no_grad()
@@ -207,9 +228,9 @@ class FoldedVerifyEngine:
         buf = self.buffers(B1, N, bucket, P_alloc)
         base = self.model.model
         D = self.D
-        cos, sin = self.rope_tables(base.embed_tokens.weight, P, N)
-        buf.cos.copy_(cos)
-        buf.sin.copy_(sin)
+        self.rope_tables(P + N)
+        if not isinstance(cache, PagedKVCache):
+            buf.pos0.fill_(P)
         graphable = (self.use_graphs and trace is None and teacher is None and not append
                      and q_scale is None)
         if graphable:
@@ -234,8 +255,8 @@ class FoldedVerifyEngine:
                                 compute_logits=compute_logits, q_scale=q_scale, trace=trace,
                                 teacher=teacher, stats=stats)
         self.last_hidden = hidden
-        self._last = dict(B1=B1, N=N, bucket=bucket, cache=cache, par=par, cos=buf.cos,
-                          sin=buf.sin, q_scale=q_scale, hidden=hidden, delta=delta)
+        self._last = dict(B1=B1, N=N, bucket=bucket, cache=cache, par=par, q_scale=q_scale,
+                          hidden=hidden, delta=delta)
         if not compute_logits:
             return None
         _lib.rows_rmsnorm(hidden, buf.all_rows, buf.all_count, BN, base.norm.weight, D, self.eps,
@@ -250,15 +271,17 @@ class FoldedVerifyEngine:
                     q_scale: Optional[torch.Tensor] = None, trace: Optional[list] = None,
                     teacher: Optional[Dict[int, torch.Tensor]] = None) -> torch.Tensor:
         """Embedding and every layer: device launches only (no host sync), so the
-        sequence can be captured in a HIP graph.  RoPE tables come from buf.cos /
-        buf.sin and a paged cache's length from its device copy, so a captured
-        sequence stays valid as the cache grows.  Returns the last hidden state."""
+        sequence can be captured in a HIP graph.  RoPE rows and a paged cache's
+        length come from the cache's device-side length (buf.pos0 for other
+        caches), so a captured sequence stays valid as the cache grows.  Returns
+        the last hidden state."""
         B1, N = tokens.shape
         BN = B1 * N
         H, Hkv, hd, D = self.H, self.Hkv, self.hd, self.D
         base = self.model.model
         hidden = base.embed_tokens(tokens).reshape(BN, D)
-        cos, sin = buf.cos, buf.sin
+        cos, sin = self._rope
+        pos0 = cache.length_dev if isinstance(cache, PagedKVCache) else buf.pos0
         for li, lyr in enumerate(self.layers):
             if teacher is not None and li in teacher:
                 hidden = teacher[li].reshape(BN, D).to(torch.bfloat16).contiguous()
@@ -270,7 +293,7 @@ class FoldedVerifyEngine:
                            segcnt, buf.rstd, buf.xn)
             w_qkv, b_qkv = self._packed[li]
             _lib.qkv_rope(buf.xn, buf.rows, count, bucket, BN, w_qkv, b_qkv, cos, sin, q_scale,
-                          N, D, H, Hkv, hd, buf.q_buf, buf.kv_buf, buf.ws_qkv)
+                          N, D, H, Hkv, hd, buf.q_buf, buf.kv_buf, buf.ws_qkv, pos0=pos0)
             if append:
                 cache.append_rows(li, buf.kv_buf, 0, N)
             self._attention(buf, cache, li, count, bucket, B1, N)
@@ -284,13 +307,12 @@ class FoldedVerifyEngine:
             torch.mm(buf.o_bf, lyr.self_attn.o_proj.weight.t(), out=buf.attn_out)
             torch.add(hidden, buf.attn_out, out=buf.hp[:BN])
             # FFN on the compacted rows (:211-217)
-            mlp = lyr.mlp
             _lib.rows_rmsnorm(buf.hp, buf.rows, count, bucket, lyr.post_attention_layernorm.weight,
                               D, self.eps, buf.zn)
-            _lib.ffn_gate_up(buf.zn, count, bucket, mlp.gate_proj.weight, mlp.up_proj.weight, D,
-                             self.I, buf.act)
-            _lib.ffn_down_scatter(buf.act, count, bucket, buf.rows, mlp.down_proj.weight, self.I, D,
-                                  buf.ffn, buf.ws_gemm)
+            wg, wu, wd = self._packed_mlp[li]
+            _lib.ffn_gate_up(buf.zn, count, bucket, wg, wu, D, self.I, buf.act)
+            _lib.ffn_down_scatter(buf.act, count, bucket, buf.rows, wd, self.I, D, buf.ffn,
+                                  buf.ws_gemm)
             # folded rows reuse the FFN output of their nearest recomputing ancestor (:218)
             new_hidden = buf.hid[li % 2]
             _lib.residual_gather_add(buf.hp, buf.ffn, buf.src, B1, N, D, new_hidden)
@@ -386,9 +408,13 @@ class FoldedVerifyEngine:
                            self.eps, self.gate_mode, buf.rec, buf.f, buf.src, buf.rows, count,
                            buf.seg, segcnt, buf.rstd, buf.xn)
 
+        cos, sin = self._rope
+        pos0 = cache.length_dev if isinstance(cache, PagedKVCache) else buf.pos0
+
         def qkv():
-            _lib.qkv_rope(buf.xn, buf.rows, count, bucket, BN, w_qkv, b_qkv, st["cos"], st["sin"],
-                          st["q_scale"], N, D, H, Hkv, hd, buf.q_buf, buf.kv_buf, buf.ws_qkv)
+            _lib.qkv_rope(buf.xn, buf.rows, count, bucket, BN, w_qkv, b_qkv, cos, sin,
+                          st["q_scale"], N, D, H, Hkv, hd, buf.q_buf, buf.kv_buf, buf.ws_qkv,
+                          pos0=pos0)
 
         def attn():
             self._attention(buf, cache, li, count, bucket, B1, N)
@@ -398,8 +424,6 @@ class FoldedVerifyEngine:
                                B1, N, H, Hkv, hd, self.scaling, buf.o32, buf.o_bf, buf.m_tab,
                                buf.z_tab)
 
-        mlp = lyr.mlp
-
         def o_proj():
             torch.mm(buf.o_bf, lyr.self_attn.o_proj.weight.t(), out=buf.attn_out)
             torch.add(hidden, buf.attn_out, out=buf.hp[:BN])
@@ -408,13 +432,14 @@ class FoldedVerifyEngine:
             _lib.rows_rmsnorm(buf.hp, buf.rows, count, bucket, lyr.post_attention_layernorm.weight,
                               D, self.eps, buf.zn)
 
+        wg, wu, wd = self._packed_mlp[li]
+
         def gate_up():
-            _lib.ffn_gate_up(buf.zn, count, bucket, mlp.gate_proj.weight, mlp.up_proj.weight, D,
-                             self.I, buf.act)
+            _lib.ffn_gate_up(buf.zn, count, bucket, wg, wu, D, self.I, buf.act)
 
         def down():
-            _lib.ffn_down_scatter(buf.act, count, bucket, buf.rows, mlp.down_proj.weight, self.I,
-                                  D, buf.ffn, buf.ws_gemm)
+            _lib.ffn_down_scatter(buf.act, count, bucket, buf.rows, wd, self.I, D, buf.ffn,
+                                  buf.ws_gemm)
 
         scratch = torch.empty_like(buf.hid[0])
 

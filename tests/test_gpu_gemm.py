@@ -2,7 +2,10 @@
 ops computed in fp64 on the CPU and rounded at the reference's bf16 rounding
 points.  Tolerance: at most 0.5% of outputs may differ, each by at most one bf16
 ulp (2^-7 relative) of the stated scale — the fp32 accumulation lands on the
-other side of a rounding tie now and then (torch's own fp32 GEMM does too)."""
+other side of a rounding tie now and then (torch's own fp32 GEMM does too).
+
+Weights go through sf_pack_weight (checked bit-exact against the layout's
+definition); workspaces are reused across calls."""
 
 import pytest
 import torch
@@ -48,14 +51,38 @@ def rnd(*shape, std=1.0, gen=None):
     return (std * torch.randn(*shape, generator=gen)).to(torch.bfloat16).cuda()
 
 
+def packed(w):
+    return _lib.pack_weight(w)
+
+
+def zeros_ws(nbytes):
+    return torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+
+
+@pytest.mark.parametrize("N,K", [(16, 128), (48, 256), (4608, 3584)])
+def test_pack_weight_layout(N, K):
+    """word (t, c, l) = W[16t + l%16][32c + 8(l/16) .. +8], compared bit for bit
+    with the layout written out by index arithmetic on the CPU."""
+    g = torch.Generator().manual_seed(N + K)
+    w = torch.randint(-32768, 32767, (N, K), generator=g, dtype=torch.int16)
+    out = _lib.pack_weight(w.view(torch.bfloat16).cuda()).view(torch.int16).cpu()
+    t = torch.arange(N // 16).view(-1, 1, 1, 1)
+    c = torch.arange(K // 32).view(1, -1, 1, 1)
+    lane = torch.arange(64).view(1, 1, -1, 1)
+    e = torch.arange(8).view(1, 1, 1, -1)
+    ref = w[(16 * t + lane % 16), (32 * c + 8 * (lane // 16) + e)]
+    assert torch.equal(out.view(-1), ref.reshape(-1))
+
+
 @pytest.mark.parametrize("M", [1, 37, 128, 200, 256])
 def test_o_proj_residual(M):
     g = torch.Generator().manual_seed(M)
     K, N = 3584, 3584
     o, x, w = rnd(M, K, gen=g), rnd(M, N, gen=g), rnd(N, K, std=0.02, gen=g)
     hp = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
-    ws = torch.empty(_lib.gemm_workspace_bytes(M, N, K), dtype=torch.uint8, device="cuda")
-    _lib.o_proj_residual(o, x, w, M, K, N, hp, ws)
+    ws = zeros_ws(_lib.gemm_workspace_bytes(M, N, K))
+    wp = packed(w)
+    _lib.o_proj_residual(o, x, wp, M, K, N, hp, ws)
     mm = mm64(o, w)
     ref = (x.float().cpu() + mm.float()).to(torch.bfloat16)
     close_bf16(hp, ref, scale=ref.float().abs() + mm.float().abs(), atol=acc_bound(o, w))
@@ -75,10 +102,11 @@ def test_ffn_path(count):
     zn = torch.zeros(bucket, D, dtype=torch.bfloat16, device="cuda")
     act = torch.zeros(bucket, I, dtype=torch.bfloat16, device="cuda")
     ffn = torch.zeros(BN + 1, D, dtype=torch.bfloat16, device="cuda")
-    ws = torch.empty(_lib.gemm_workspace_bytes(bucket, D, I), dtype=torch.uint8, device="cuda")
+    ws = zeros_ws(_lib.gemm_workspace_bytes(bucket, D, I))
     _lib.rows_rmsnorm(hp, rows, cnt, bucket, lnw, D, 1e-6, zn)
-    _lib.ffn_gate_up(zn, cnt, bucket, wg, wu, D, I, act)
-    _lib.ffn_down_scatter(act, cnt, bucket, rows, wd, I, D, ffn, ws)
+    for _ in range(2):  # twice through one workspace
+        _lib.ffn_gate_up(zn, cnt, bucket, packed(wg), packed(wu), D, I, act)
+        _lib.ffn_down_scatter(act, cnt, bucket, rows, packed(wd), I, D, ffn, ws)
     torch.cuda.synchronize()
     r = rows[:count].long()
     x = hp[r].float()
@@ -111,5 +139,5 @@ def test_residual_gather_add_and_lm_head():
     assert torch.equal(out, ref)
     w = rnd(V, D, std=0.02, gen=g)
     logits = torch.empty(B1 * N, V, dtype=torch.bfloat16, device="cuda")
-    _lib.lm_head(out, B1 * N, w, D, V, logits)
+    _lib.lm_head(out, B1 * N, packed(w), D, V, logits)
     close_bf16(logits, mm64(out, w), atol=acc_bound(out, w))
