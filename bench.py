@@ -88,8 +88,9 @@ def kernel_roofline(name, ms, w, R, B1, N, P):
     F = BN - R
     nq = (H + 2 * Hkv) * hd
     if name == "gate":
-        by = BN * D * e + R * D * e + BN * 17 + R * 4
-        fl = 6 * BN * D
+        # fused residual gate: hp rows + the R distinct ffn rows in, h rows + R xn rows out
+        by = 2 * BN * D * e + 2 * R * D * e + BN * 21 + R * 4
+        fl = 7 * BN * D
     elif name == "qkv":
         by = nq * D * e + nq * e + R * D * e + R * nq * e + 2 * N * hd * e
         fl = 2 * R * D * nq
@@ -103,11 +104,12 @@ def kernel_roofline(name, ms, w, R, B1, N, P):
         by = 2 * (2 * N * Hkv * hd * e)
         fl = 0
     elif name == "o_proj":
-        by = D * H * hd * e + BN * H * hd * e + 2 * BN * D * e
+        by = D * H * hd * e + BN * H * hd * e + BN * D * e
         fl = 2 * BN * H * hd * D
     elif name == "post_norm":
-        by = 2 * R * D * e + D * e
-        fl = 4 * R * D
+        # residual add of every row + RMSNorm of the R recomputed rows
+        by = 3 * BN * D * e + R * D * e + D * e
+        fl = BN * D + 4 * R * D
     elif name == "gate_up":
         I = sh.intermediate
         by = 2 * I * D * e + R * D * e + R * I * e
@@ -116,9 +118,9 @@ def kernel_roofline(name, ms, w, R, B1, N, P):
         I = sh.intermediate
         by = D * I * e + R * I * e + R * D * e
         fl = 2 * R * I * D
-    elif name == "resid":
-        by = 3 * BN * D * e
-        fl = BN * D
+    elif name == "final_norm":
+        by = 3 * BN * D * e + R * D * e + D * e
+        fl = 5 * BN * D
     elif name == "lm_head":
         V = sh.vocab
         by = V * D * e + BN * D * e + BN * V * e
@@ -282,7 +284,7 @@ def main(argv=None) -> int:
     P = info["prefix"]
     R_last = int(info["count"].item())
     kernels = {}
-    for name in ("qkv", "attn", "chain", "o_proj", "post_norm", "gate_up", "down", "resid",
+    for name in ("qkv", "attn", "chain", "o_proj", "post_norm", "gate_up", "down", "final_norm",
                  "lm_head", "append", "gate"):
         if name not in launchers:
             continue

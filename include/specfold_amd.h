@@ -49,6 +49,7 @@ extern "C" {
                                   (specfold/generate/fastdllm_v2_generation.py:151-186) */
 
 const char* sf_status_string(int status);
+/* 2: GEMM weights in the packed layout of sf_pack_weight; fused residual entries. */
 int sf_abi_version(void);
 
 /*
@@ -64,15 +65,34 @@ int sf_abi_version(void);
  * rows      = ascending flat ids of recomputed rows, slots >= count hold BN
  * count[0]  = number of recomputed rows (may exceed bucket: overflow)
  * seg[b*N+k], segcnt[b] = the k-th recomputed flat row of branch b, and how many
+ * slot[r]   = index of row r in rows, or -1 (folded or beyond bucket); may be NULL
  * rstd[r]   = 1 / sqrt(mean(x^2) + eps)
  * xn[r, :]  = bf16(ln_w * bf16(x * rstd)) for recomputed rows (the
  *             Qwen2RMSNorm output the QKV projection consumes)
  * Limits: B1*N <= 1024, B1 <= 64, D % 8 == 0, D <= 8192, 1 <= bucket <= B1*N.
+ *
+ * sf_fold_gate_residual is the same gate for layers after the first, with the
+ * previous layer's folded residual update fused in: the layer input is
+ * x[r] = bf16(hp[r] + ffn[src_prev[r]*N + r%N]) (fastdllm_v2_folded.py:218),
+ * written to hidden_out (which must not alias hp).  src_prev is read before src
+ * is written, so both may be the same buffer.
+ *
+ * sf_residual_rmsnorm, after the last layer: hidden_out[r] = x[r] as above and
+ * out[r] = bf16(w * bf16(x[r] * rstd)) for every row (the final norm, :222).
  */
 int sf_fold_gate(const uint16_t* hidden, const int32_t* par, const uint16_t* ln_w, int B1, int N,
                  int D, int bucket, float delta, float eps, int gate_mode, int8_t* rec, int32_t* f,
                  int32_t* src, int32_t* rows, int32_t* count, int32_t* seg, int32_t* segcnt,
-                 float* rstd, uint16_t* xn, void* stream);
+                 int32_t* slot, float* rstd, uint16_t* xn, void* stream);
+int sf_fold_gate_residual(const uint16_t* hp, const uint16_t* ffn, const int32_t* src_prev,
+                          const int32_t* par, const uint16_t* ln_w, int B1, int N, int D,
+                          int bucket, float delta, float eps, int gate_mode, uint16_t* hidden_out,
+                          int8_t* rec, int32_t* f, int32_t* src, int32_t* rows, int32_t* count,
+                          int32_t* seg, int32_t* segcnt, int32_t* slot, float* rstd, uint16_t* xn,
+                          void* stream);
+int sf_residual_rmsnorm(const uint16_t* hp, const uint16_t* ffn, const int32_t* src,
+                        const uint16_t* w, int B1, int N, int D, float eps, uint16_t* hidden_out,
+                        uint16_t* out, void* stream);
 
 /*
  * (2) QKV projection (bf16 MFMA, fp32 accumulate) + bias + RoPE + scatter for
@@ -172,6 +192,9 @@ int sf_kv_append(const uint16_t* kv_buf, int row0, int n_tok, int Hkv, int hd, u
  *
  * sf_pack_weight        out = packed(w), w row-major [N, K]; N % 16 == 0, K % 128 == 0
  * sf_o_proj_residual    hp[r] = bf16(x[r] + bf16(o_bf[r] . Wo^T)), r < M (all rows)
+ * sf_residual_post_norm hp[r] = bf16(x[r] + y[r]) for r < BN, and for recomputed rows
+ *                       zn[slot[r]] = bf16(w * bf16(hp[r] * rstd)) (y = a bf16 o_proj
+ *                       output computed elsewhere, e.g. by a library GEMM)
  * sf_rows_rmsnorm       out[m] = bf16(w * bf16(x[rows[m]] * rstd)), m < count
  * sf_ffn_gate_up        act[m] = bf16(bf16(silu(bf16(zn[m] . Wg^T))) * bf16(zn[m] . Wu^T))
  * sf_ffn_down_scatter   ffn[rows[m]] = bf16(act[m] . Wd^T), m < count
@@ -184,6 +207,9 @@ size_t sf_gemm_workspace_bytes(int mcap, int N, int K);
 int sf_pack_weight(const uint16_t* w, int N, int K, uint16_t* out, void* stream);
 int sf_o_proj_residual(const uint16_t* o_bf, const uint16_t* x, const uint16_t* wo, int M, int K,
                        int N, uint16_t* hp, void* workspace, size_t workspace_bytes, void* stream);
+int sf_residual_post_norm(const uint16_t* x, const uint16_t* y, const int32_t* slot, int BN,
+                          int D, const uint16_t* w, float eps, uint16_t* hp, uint16_t* zn,
+                          void* stream);
 int sf_rows_rmsnorm(const uint16_t* x, const int32_t* rows, const int32_t* count, int bucket,
                     const uint16_t* w, int D, float eps, uint16_t* out, void* stream);
 int sf_ffn_gate_up(const uint16_t* zn, const int32_t* count, int bucket, const uint16_t* wg,

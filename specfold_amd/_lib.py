@@ -33,7 +33,10 @@ SIGNATURES = {
     "sf_status_string": (ctypes.c_char_p, [_i]),
     "sf_abi_version": (_i, []),
     "sf_fold_gate": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _f, _f, _i,
-                          _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+                          _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "sf_fold_gate_residual": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _f, _f, _i, _vp,
+                                   _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "sf_residual_rmsnorm": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _f, _vp, _vp, _vp]),
     "sf_qkv_workspace_bytes": (_sz, [_i, _i, _i]),
     "sf_qkv_rope": (_i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _i, _vp,
                          _i, _i, _i, _i, _i, _vp, _vp, _vp, _sz, _vp]),
@@ -47,6 +50,7 @@ SIGNATURES = {
     "sf_gemm_workspace_bytes": (_sz, [_i, _i, _i]),
     "sf_pack_weight": (_i, [_vp, _i, _i, _vp, _vp]),
     "sf_o_proj_residual": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _vp, _sz, _vp]),
+    "sf_residual_post_norm": (_i, [_vp, _vp, _vp, _i, _i, _vp, _f, _vp, _vp, _vp]),
     "sf_rows_rmsnorm": (_i, [_vp, _vp, _vp, _i, _vp, _i, _f, _vp, _vp]),
     "sf_ffn_gate_up": (_i, [_vp, _vp, _i, _vp, _vp, _i, _i, _vp, _vp]),
     "sf_ffn_down_scatter": (_i, [_vp, _vp, _i, _vp, _vp, _i, _i, _vp, _vp, _sz, _vp]),
@@ -121,24 +125,66 @@ def _need(t: torch.Tensor, name: str, dtype: torch.dtype, numel: Optional[int] =
 # typed wrappers
 # ---------------------------------------------------------------------------
 
+def _need_gate_outputs(B1, N, bucket, D, rec, f, src, rows, count, seg, segcnt, slot, rstd, xn):
+    BN = B1 * N
+    _need(rec, "rec", torch.int8, min_numel=BN, align=4)
+    for nm, t, n in (("f", f, BN), ("src", src, BN), ("rows", rows, bucket), ("count", count, 1),
+                     ("seg", seg, BN), ("segcnt", segcnt, B1)):
+        _need(t, nm, torch.int32, min_numel=n, align=4)
+    if slot is not None:
+        _need(slot, "slot", torch.int32, min_numel=BN, align=4)
+    _need(rstd, "rstd", torch.float32, min_numel=BN, align=4)
+    _need(xn, "xn", torch.bfloat16, min_numel=BN * D)
+
+
 def fold_gate(hidden, par, ln_w, B1, N, bucket, delta, eps, gate_mode,
-              rec, f, src, rows, count, seg, segcnt, rstd, xn, stream=None) -> None:
+              rec, f, src, rows, count, seg, segcnt, rstd, xn, stream=None, slot=None) -> None:
     D = hidden.shape[-1]
     BN = B1 * N
     _need(hidden, "hidden", torch.bfloat16, numel=BN * D)
     _need(par, "par", torch.int32, numel=B1, align=4)
     _need(ln_w, "ln_w", torch.bfloat16, numel=D)
-    _need(rec, "rec", torch.int8, min_numel=BN, align=4)
-    for nm, t, n in (("f", f, BN), ("src", src, BN), ("rows", rows, bucket), ("count", count, 1),
-                     ("seg", seg, BN), ("segcnt", segcnt, B1)):
-        _need(t, nm, torch.int32, min_numel=n, align=4)
-    _need(rstd, "rstd", torch.float32, min_numel=BN, align=4)
-    _need(xn, "xn", torch.bfloat16, min_numel=BN * D)
+    _need_gate_outputs(B1, N, bucket, D, rec, f, src, rows, count, seg, segcnt, slot, rstd, xn)
     st = load().sf_fold_gate(_ptr(hidden), _ptr(par), _ptr(ln_w), B1, N, D, bucket, float(delta),
                              float(eps), int(gate_mode), _ptr(rec), _ptr(f), _ptr(src), _ptr(rows),
-                             _ptr(count), _ptr(seg), _ptr(segcnt), _ptr(rstd), _ptr(xn),
-                             _stream(stream))
+                             _ptr(count), _ptr(seg), _ptr(segcnt), _ptr(slot), _ptr(rstd),
+                             _ptr(xn), _stream(stream))
     _check(st, "sf_fold_gate")
+
+
+def fold_gate_residual(hp, ffn, src_prev, par, ln_w, B1, N, D, bucket, delta, eps, gate_mode,
+                       hidden_out, rec, f, src, rows, count, seg, segcnt, slot, rstd, xn,
+                       stream=None) -> None:
+    """The gate of a layer after the first, with the previous layer's residual
+    update x = bf16(hp + ffn[src_prev*N + n]) fused in (written to hidden_out)."""
+    BN = B1 * N
+    _need(hp, "hp", torch.bfloat16, min_numel=BN * D)
+    _need(ffn, "ffn", torch.bfloat16, min_numel=BN * D)
+    _need(src_prev, "src_prev", torch.int32, min_numel=BN, align=4)
+    _need(par, "par", torch.int32, numel=B1, align=4)
+    _need(ln_w, "ln_w", torch.bfloat16, numel=D)
+    _need(hidden_out, "hidden_out", torch.bfloat16, min_numel=BN * D)
+    _need_gate_outputs(B1, N, bucket, D, rec, f, src, rows, count, seg, segcnt, slot, rstd, xn)
+    st = load().sf_fold_gate_residual(
+        _ptr(hp), _ptr(ffn), _ptr(src_prev), _ptr(par), _ptr(ln_w), B1, N, D, bucket,
+        float(delta), float(eps), int(gate_mode), _ptr(hidden_out), _ptr(rec), _ptr(f),
+        _ptr(src), _ptr(rows), _ptr(count), _ptr(seg), _ptr(segcnt), _ptr(slot), _ptr(rstd),
+        _ptr(xn), _stream(stream))
+    _check(st, "sf_fold_gate_residual")
+
+
+def residual_rmsnorm(hp, ffn, src, w, B1, N, D, eps, hidden_out, out, stream=None) -> None:
+    """hidden_out = bf16(hp + ffn[src*N + n]) and out = RMSNorm(hidden_out), every row."""
+    BN = B1 * N
+    _need(hp, "hp", torch.bfloat16, min_numel=BN * D)
+    _need(ffn, "ffn", torch.bfloat16, min_numel=BN * D)
+    _need(src, "src", torch.int32, min_numel=BN, align=4)
+    _need(w, "w", torch.bfloat16, numel=D)
+    _need(hidden_out, "hidden_out", torch.bfloat16, min_numel=BN * D)
+    _need(out, "out", torch.bfloat16, min_numel=BN * D)
+    st = load().sf_residual_rmsnorm(_ptr(hp), _ptr(ffn), _ptr(src), _ptr(w), B1, N, D, float(eps),
+                                    _ptr(hidden_out), _ptr(out), _stream(stream))
+    _check(st, "sf_residual_rmsnorm")
 
 
 def qkv_workspace_bytes(bucket: int, D: int, n_qkv: int) -> int:
@@ -276,6 +322,19 @@ def o_proj_residual(o_bf, x, wo, M, K, N, hp, workspace, stream=None) -> None:
     st = load().sf_o_proj_residual(_ptr(o_bf), _ptr(x), _ptr(wo), M, K, N, _ptr(hp),
                                    _ptr(workspace), workspace.numel(), _stream(stream))
     _check(st, "sf_o_proj_residual")
+
+
+def residual_post_norm(x, y, slot, BN, D, w, eps, hp, zn, stream=None) -> None:
+    """hp = bf16(x + y) for every row; zn[slot[r]] = RMSNorm(hp[r]) where slot[r] >= 0."""
+    _need(x, "x", torch.bfloat16, min_numel=BN * D)
+    _need(y, "y", torch.bfloat16, min_numel=BN * D)
+    _need(slot, "slot", torch.int32, min_numel=BN, align=4)
+    _need(w, "w", torch.bfloat16, numel=D)
+    _need(hp, "hp", torch.bfloat16, min_numel=BN * D)
+    _need(zn, "zn", torch.bfloat16)
+    st = load().sf_residual_post_norm(_ptr(x), _ptr(y), _ptr(slot), BN, D, _ptr(w), float(eps),
+                                      _ptr(hp), _ptr(zn), _stream(stream))
+    _check(st, "sf_residual_post_norm")
 
 
 def rows_rmsnorm(x, rows, count, bucket, w, D, eps, out, stream=None) -> None:

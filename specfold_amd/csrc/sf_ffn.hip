@@ -66,6 +66,67 @@ __global__ __launch_bounds__(256) void rows_rmsnorm_kernel(
   }
 }
 
+// One wave per flat row r: hp[r] = bf16(x[r] + y[r]) (the attention residual,
+// fastdllm_v2_folded.py:207-209, with y = bf16(O . Wo^T)), and for a recomputed
+// row (slot[r] >= 0) its post-attention RMSNorm zn[slot[r]] = bf16(w * bf16(hp[r] *
+// rstd)) (:211-212).  All loads are issued before the first use.
+template <int VPL>
+__global__ __launch_bounds__(256) void residual_post_norm_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ y,
+    const int32_t* __restrict__ slot, int BN, int D, const uint16_t* __restrict__ w, float eps,
+    uint16_t* __restrict__ hp, uint16_t* __restrict__ zn) {
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= BN) return;
+  const int nvec = D >> 3;
+  const sf_u32x4* xr = reinterpret_cast<const sf_u32x4*>(x + (size_t)r * D);
+  const sf_u32x4* yr = reinterpret_cast<const sf_u32x4*>(y + (size_t)r * D);
+  const sf_u32x4* wr = reinterpret_cast<const sf_u32x4*>(w);
+  const int sl = slot[r];
+  sf_u32x4 xv[VPL], yv[VPL], wv[VPL];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) xv[i] = xr[min(lane + i * 64, nvec - 1)];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) yv[i] = yr[min(lane + i * 64, nvec - 1)];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) wv[i] = wr[min(lane + i * 64, nvec - 1)];
+  sf_u32x4* hrow = reinterpret_cast<sf_u32x4*>(hp + (size_t)r * D);
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    float a[8], b[8];
+    sf_unpack8(xv[i], a);
+    sf_unpack8(yv[i], b);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) xv[i][j] = sf_pack2(a[2 * j] + b[2 * j], a[2 * j + 1] + b[2 * j + 1]);
+    if (lane + i * 64 < nvec) {
+      hrow[lane + i * 64] = xv[i];
+      float h[8];
+      sf_unpack8(xv[i], h);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss = fmaf(h[j], h[j], ss);
+    }
+  }
+  if (sl < 0) return;  // wave-uniform
+  ss = sf_wave_sum(ss);
+  const float inv = 1.0f / sqrtf(ss / (float)D + eps);
+  sf_u32x4* orow = reinterpret_cast<sf_u32x4*>(zn + (size_t)sl * D);
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int idx = lane + i * 64;
+    if (idx < nvec) {
+      float f[8], g[8];
+      sf_unpack8(xv[i], f);
+      sf_unpack8(wv[i], g);
+      sf_u32x4 o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        o[j] = sf_pack2(g[2 * j] * sf_rbf(f[2 * j] * inv), g[2 * j + 1] * sf_rbf(f[2 * j + 1] * inv));
+      orow[idx] = o;
+    }
+  }
+}
+
 // h[r, :] = bf16(hp[r, :] + ffn[src[r]*N + n, :]); 8 elements per thread
 __global__ __launch_bounds__(256) void residual_gather_add_kernel(
     const uint16_t* __restrict__ hp, const uint16_t* __restrict__ ffn,
@@ -183,6 +244,26 @@ extern "C" int sf_rows_rmsnorm(const uint16_t* x, const int32_t* rows, const int
   else
     hipLaunchKernelGGL(rows_rmsnorm_kernel<16>, grid, dim3(256), 0, st, x, rows, count, bucket, w,
                        D, eps, out);
+  return sf_launch_status();
+}
+
+extern "C" int sf_residual_post_norm(const uint16_t* x, const uint16_t* y, const int32_t* slot,
+                                     int BN, int D, const uint16_t* w, float eps, uint16_t* hp,
+                                     uint16_t* zn, void* stream) {
+  if (!x || !y || !slot || !w || !hp || !zn) return SF_ERR_ARG;
+  if (BN < 1 || BN > 1024 || D % 8 || D > 8192) return SF_ERR_SHAPE;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int vpl = (D / 8 + 63) / 64;
+  dim3 grid((BN + 3) / 4);
+  if (vpl <= 4)
+    hipLaunchKernelGGL(residual_post_norm_kernel<4>, grid, dim3(256), 0, st, x, y, slot, BN, D, w,
+                       eps, hp, zn);
+  else if (vpl <= 8)
+    hipLaunchKernelGGL(residual_post_norm_kernel<8>, grid, dim3(256), 0, st, x, y, slot, BN, D, w,
+                       eps, hp, zn);
+  else
+    hipLaunchKernelGGL(residual_post_norm_kernel<16>, grid, dim3(256), 0, st, x, y, slot, BN, D, w,
+                       eps, hp, zn);
   return sf_launch_status();
 }
 

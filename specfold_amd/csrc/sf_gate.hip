@@ -16,36 +16,72 @@ constexpr int kMaxVecPerLane = 16;  // 16 x 8 bf16 x 64 lanes = 8192 columns
 
 // One wave per flat row r = b*N + n: three fp32 sums over D (x^2, residual^2,
 // parent^2), the gate decision, rstd, and the normalized row for recomputed rows.
-template <int VPL>
+// RESID: the layer input is first formed from the previous layer's outputs,
+// x[r] = bf16(hp[r] + ffn[src_prev[r]*N + n]) (the folded residual update of
+// fastdllm_v2_folded.py:218), for the row and for its parent row, and x[r] is
+// written to hidden_out.  `par` may be NULL (every row its own parent).
+template <int VPL, bool RESID>
 __global__ __launch_bounds__(256) void sf_gate_rows_kernel(
-    const uint16_t* __restrict__ hidden, const int32_t* __restrict__ par,
+    const uint16_t* __restrict__ hidden, const uint16_t* __restrict__ ffn,
+    const int32_t* __restrict__ src_prev, const int32_t* __restrict__ par,
     const uint16_t* __restrict__ ln_w, int B1, int N, int D, float delta, float eps, int mode,
-    int8_t* __restrict__ rec, float* __restrict__ rstd, uint16_t* __restrict__ xn) {
+    uint16_t* __restrict__ hidden_out, int8_t* __restrict__ rec, float* __restrict__ rstd,
+    uint16_t* __restrict__ xn) {
   const int lane = threadIdx.x & 63;
   const int r = blockIdx.x * kGateWaves + (threadIdx.x >> 6);
   const int BN = B1 * N;
   if (r >= BN) return;
   const int b = r / N;
   const int n = r - b * N;
-  int p = par[b];
+  int p = par ? par[b] : b;
   p = p < 0 ? 0 : (p >= B1 ? B1 - 1 : p);
   const bool draft = b > 0 && mode != SF_GATE_ALL;
+  const int pr = p * N + n;
 
   const int nvec = D >> 3;
   const sf_u32x4* xrow = reinterpret_cast<const sf_u32x4*>(hidden + (size_t)r * D);
-  const sf_u32x4* prow = reinterpret_cast<const sf_u32x4*>(hidden + (size_t)(p * N + n) * D);
+  const sf_u32x4* prow = reinterpret_cast<const sf_u32x4*>(hidden + (size_t)pr * D);
   const sf_u32x4* wrow = reinterpret_cast<const sf_u32x4*>(ln_w);
 
-  // Every load of the row, its parent row and the norm weight is issued before
-  // the first use (clamped addresses, no branches), so the wave pays one memory
-  // latency instead of one per vector.
+  // Every load of the rows and the norm weight is issued before the first use
+  // (clamped addresses, no branches), so the wave pays one memory latency per
+  // dependent step instead of one per vector.
   sf_u32x4 xv[VPL], pv[VPL], wv[VPL];
+  sf_u32x4 fx[RESID ? VPL : 1], fp[RESID ? VPL : 1];
+  if (RESID) {
+    const sf_u32x4* fxrow =
+        reinterpret_cast<const sf_u32x4*>(ffn + (size_t)(src_prev[r] * N + n) * D);
+    const sf_u32x4* fprow =
+        reinterpret_cast<const sf_u32x4*>(ffn + (size_t)(src_prev[pr] * N + n) * D);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) fx[i] = fxrow[min(lane + i * 64, nvec - 1)];
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) fp[i] = fprow[min(lane + i * 64, nvec - 1)];
+  }
 #pragma unroll
   for (int i = 0; i < VPL; ++i) xv[i] = xrow[min(lane + i * 64, nvec - 1)];
 #pragma unroll
   for (int i = 0; i < VPL; ++i) pv[i] = prow[min(lane + i * 64, nvec - 1)];
 #pragma unroll
   for (int i = 0; i < VPL; ++i) wv[i] = wrow[min(lane + i * 64, nvec - 1)];
+  if (RESID) {
+    // h = bf16(hp + ffn), the layer input, kept as packed bf16
+    sf_u32x4* hout = reinterpret_cast<sf_u32x4*>(hidden_out + (size_t)r * D);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      float a[8], c[8], e[8], g[8];
+      sf_unpack8(xv[i], a);
+      sf_unpack8(fx[i], c);
+      sf_unpack8(pv[i], e);
+      sf_unpack8(fp[i], g);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        xv[i][j] = sf_pack2(a[2 * j] + c[2 * j], a[2 * j + 1] + c[2 * j + 1]);
+        pv[i][j] = sf_pack2(e[2 * j] + g[2 * j], e[2 * j + 1] + g[2 * j + 1]);
+      }
+      if (lane + i * 64 < nvec) hout[lane + i * 64] = xv[i];
+    }
+  }
 
   float ss = 0.f, ds = 0.f, ps = 0.f;
 #pragma unroll
@@ -82,8 +118,8 @@ __global__ __launch_bounds__(256) void sf_gate_rows_kernel(
     }
   }
   if (lane == 0) {
-    rec[r] = is_rec ? 1 : 0;
-    rstd[r] = inv;
+    if (rec) rec[r] = is_rec ? 1 : 0;
+    if (rstd) rstd[r] = inv;
   }
   if (!is_rec) return;
 
@@ -113,7 +149,8 @@ __global__ __launch_bounds__(256) void sf_gate_rows_kernel(
 __global__ __launch_bounds__(1024) void sf_gate_compact_kernel(
     const int8_t* __restrict__ rec, const int32_t* __restrict__ par, int B1, int N, int bucket,
     int32_t* __restrict__ f, int32_t* __restrict__ src, int32_t* __restrict__ rows,
-    int32_t* __restrict__ count, int32_t* __restrict__ seg, int32_t* __restrict__ segcnt) {
+    int32_t* __restrict__ count, int32_t* __restrict__ seg, int32_t* __restrict__ segcnt,
+    int32_t* __restrict__ slot_out) {
   __shared__ int s_f[1024];
   __shared__ int s_slot[1024];
   __shared__ int s_wave_tot[16];
@@ -144,6 +181,7 @@ __global__ __launch_bounds__(1024) void sf_gate_compact_kernel(
     s_slot[t] = slot;
     f[t] = fv;
     if (flag && slot < bucket) rows[slot] = t;
+    if (slot_out) slot_out[t] = (flag && slot < bucket) ? slot : -1;
   }
   for (int s = t; s < bucket; s += blockDim.x)
     if (s >= total) rows[s] = BN;
@@ -160,14 +198,45 @@ __global__ __launch_bounds__(1024) void sf_gate_compact_kernel(
   if (t == 0) *count = total;
 }
 
-template <int VPL>
-void launch_rows(const uint16_t* hidden, const int32_t* par, const uint16_t* ln_w, int B1, int N,
-                 int D, float delta, float eps, int mode, int8_t* rec, float* rstd, uint16_t* xn,
-                 hipStream_t st) {
+template <int VPL, bool RESID>
+void launch_rows(const uint16_t* hidden, const uint16_t* ffn, const int32_t* src_prev,
+                 const int32_t* par, const uint16_t* ln_w, int B1, int N, int D, float delta,
+                 float eps, int mode, uint16_t* hidden_out, int8_t* rec, float* rstd,
+                 uint16_t* xn, hipStream_t st) {
   const int BN = B1 * N;
   dim3 grid((BN + kGateWaves - 1) / kGateWaves);
-  hipLaunchKernelGGL(sf_gate_rows_kernel<VPL>, grid, dim3(256), 0, st, hidden, par, ln_w, B1, N, D,
-                     delta, eps, mode, rec, rstd, xn);
+  hipLaunchKernelGGL((sf_gate_rows_kernel<VPL, RESID>), grid, dim3(256), 0, st, hidden, ffn,
+                     src_prev, par, ln_w, B1, N, D, delta, eps, mode, hidden_out, rec, rstd, xn);
+}
+
+template <bool RESID>
+void launch_rows_any(int D, const uint16_t* hidden, const uint16_t* ffn, const int32_t* src_prev,
+                     const int32_t* par, const uint16_t* ln_w, int B1, int N, float delta,
+                     float eps, int mode, uint16_t* hidden_out, int8_t* rec, float* rstd,
+                     uint16_t* xn, hipStream_t st) {
+  const int vpl = (D / 8 + 63) / 64;
+  if (vpl <= 4)
+    launch_rows<4, RESID>(hidden, ffn, src_prev, par, ln_w, B1, N, D, delta, eps, mode, hidden_out,
+                          rec, rstd, xn, st);
+  else if (vpl <= 8)
+    launch_rows<8, RESID>(hidden, ffn, src_prev, par, ln_w, B1, N, D, delta, eps, mode,
+                          hidden_out, rec, rstd, xn, st);
+  else if (vpl <= 12)
+    launch_rows<12, RESID>(hidden, ffn, src_prev, par, ln_w, B1, N, D, delta, eps, mode,
+                           hidden_out, rec, rstd, xn, st);
+  else
+    launch_rows<16, RESID>(hidden, ffn, src_prev, par, ln_w, B1, N, D, delta, eps, mode,
+                           hidden_out, rec, rstd, xn, st);
+}
+
+int check_gate_args(int B1, int N, int D, int bucket, int gate_mode) {
+  if (gate_mode != SF_GATE_MODEL_DTYPE && gate_mode != SF_GATE_FP32_SQUARED &&
+      gate_mode != SF_GATE_ALL)
+    return SF_ERR_ARG;
+  if (B1 < 1 || B1 > 64 || N < 1 || B1 * N > 1024) return SF_ERR_SHAPE;
+  if (D < 8 || D % 8 != 0 || D > 8 * 64 * kMaxVecPerLane) return SF_ERR_SHAPE;
+  if (bucket < 1 || bucket > B1 * N) return SF_ERR_SHAPE;
+  return SF_OK;
 }
 
 }  // namespace
@@ -183,33 +252,55 @@ extern "C" const char* sf_status_string(int status) {
   }
 }
 
-extern "C" int sf_abi_version(void) { return 1; }
+extern "C" int sf_abi_version(void) { return 2; }
 
 extern "C" int sf_fold_gate(const uint16_t* hidden, const int32_t* par, const uint16_t* ln_w,
                             int B1, int N, int D, int bucket, float delta, float eps, int gate_mode,
                             int8_t* rec, int32_t* f, int32_t* src, int32_t* rows, int32_t* count,
-                            int32_t* seg, int32_t* segcnt, float* rstd, uint16_t* xn,
+                            int32_t* seg, int32_t* segcnt, int32_t* slot, float* rstd, uint16_t* xn,
                             void* stream) {
   if (!hidden || !par || !ln_w || !rec || !f || !src || !rows || !count || !seg || !segcnt ||
       !rstd || !xn)
     return SF_ERR_ARG;
-  if (gate_mode != SF_GATE_MODEL_DTYPE && gate_mode != SF_GATE_FP32_SQUARED &&
-      gate_mode != SF_GATE_ALL)
-    return SF_ERR_ARG;
-  if (B1 < 1 || B1 > 64 || N < 1 || B1 * N > 1024) return SF_ERR_SHAPE;
-  if (D < 8 || D % 8 != 0 || D > 8 * 64 * kMaxVecPerLane) return SF_ERR_SHAPE;
-  if (bucket < 1 || bucket > B1 * N) return SF_ERR_SHAPE;
+  const int chk = check_gate_args(B1, N, D, bucket, gate_mode);
+  if (chk != SF_OK) return chk;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const int vpl = (D / 8 + 63) / 64;
-  if (vpl <= 4)
-    launch_rows<4>(hidden, par, ln_w, B1, N, D, delta, eps, gate_mode, rec, rstd, xn, st);
-  else if (vpl <= 8)
-    launch_rows<8>(hidden, par, ln_w, B1, N, D, delta, eps, gate_mode, rec, rstd, xn, st);
-  else if (vpl <= 12)
-    launch_rows<12>(hidden, par, ln_w, B1, N, D, delta, eps, gate_mode, rec, rstd, xn, st);
-  else
-    launch_rows<16>(hidden, par, ln_w, B1, N, D, delta, eps, gate_mode, rec, rstd, xn, st);
+  launch_rows_any<false>(D, hidden, nullptr, nullptr, par, ln_w, B1, N, delta, eps, gate_mode,
+                         nullptr, rec, rstd, xn, st);
   hipLaunchKernelGGL(sf_gate_compact_kernel, dim3(1), dim3(1024), 0, st, rec, par, B1, N, bucket,
-                     f, src, rows, count, seg, segcnt);
+                     f, src, rows, count, seg, segcnt, slot);
+  return sf_launch_status();
+}
+
+extern "C" int sf_fold_gate_residual(const uint16_t* hp, const uint16_t* ffn,
+                                     const int32_t* src_prev, const int32_t* par,
+                                     const uint16_t* ln_w, int B1, int N, int D, int bucket,
+                                     float delta, float eps, int gate_mode, uint16_t* hidden_out,
+                                     int8_t* rec, int32_t* f, int32_t* src, int32_t* rows,
+                                     int32_t* count, int32_t* seg, int32_t* segcnt, int32_t* slot,
+                                     float* rstd, uint16_t* xn, void* stream) {
+  if (!hp || !ffn || !src_prev || !par || !ln_w || !hidden_out || !rec || !f || !src || !rows ||
+      !count || !seg || !segcnt || !rstd || !xn)
+    return SF_ERR_ARG;
+  if (hidden_out == hp) return SF_ERR_ARG;
+  const int chk = check_gate_args(B1, N, D, bucket, gate_mode);
+  if (chk != SF_OK) return chk;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  // the row kernel reads src_prev; only the compaction after it writes src
+  launch_rows_any<true>(D, hp, ffn, src_prev, par, ln_w, B1, N, delta, eps, gate_mode, hidden_out,
+                        rec, rstd, xn, st);
+  hipLaunchKernelGGL(sf_gate_compact_kernel, dim3(1), dim3(1024), 0, st, rec, par, B1, N, bucket,
+                     f, src, rows, count, seg, segcnt, slot);
+  return sf_launch_status();
+}
+
+extern "C" int sf_residual_rmsnorm(const uint16_t* hp, const uint16_t* ffn, const int32_t* src,
+                                   const uint16_t* w, int B1, int N, int D, float eps,
+                                   uint16_t* hidden_out, uint16_t* out, void* stream) {
+  if (!hp || !ffn || !src || !w || !hidden_out || !out || hidden_out == hp) return SF_ERR_ARG;
+  const int chk = check_gate_args(B1, N, D, 1, SF_GATE_ALL);
+  if (chk != SF_OK) return chk;
+  launch_rows_any<true>(D, hp, ffn, src, nullptr, w, B1, N, 0.f, eps, SF_GATE_ALL, hidden_out,
+                        nullptr, nullptr, out, reinterpret_cast<hipStream_t>(stream));
   return sf_launch_status();
 }

@@ -82,6 +82,7 @@ class _Buffers:
         self.rows = torch.zeros(bucket, **i32)
         self.count_slab = torch.zeros(L, **i32)
         self.seg = torch.zeros(BN, **i32)
+        self.slot = torch.zeros(BN, **i32)
         self.segcnt_slab = torch.zeros(L * B1, **i32)
         self.rstd = torch.zeros(BN, dtype=torch.float32, device=dev)
         self.xn = torch.zeros(BN, D, dtype=bf, device=dev)
@@ -259,9 +260,8 @@ class FoldedVerifyEngine:
                           hidden=hidden, delta=delta)
         if not compute_logits:
             return None
-        _lib.rows_rmsnorm(hidden, buf.all_rows, buf.all_count, BN, base.norm.weight, D, self.eps,
-                          buf.final)
-        # lm_head over all BN rows (M = BN): hipBLASLt, a fresh tensor per call
+        # lm_head over all BN rows (M = BN) on the final-normed rows: hipBLASLt, a fresh
+        # tensor per call
         logits = torch.mm(buf.final, self.model.lm_head.weight.t())
         return logits.view(B1, N, self.V)
 
@@ -283,14 +283,24 @@ class FoldedVerifyEngine:
         cos, sin = self._rope
         pos0 = cache.length_dev if isinstance(cache, PagedKVCache) else buf.pos0
         for li, lyr in enumerate(self.layers):
-            if teacher is not None and li in teacher:
-                hidden = teacher[li].reshape(BN, D).to(torch.bfloat16).contiguous()
-            hidden = hidden.contiguous()
             count = buf.count_slab[li:li + 1]
             segcnt = buf.segcnt_slab[li * B1:(li + 1) * B1]
-            _lib.fold_gate(hidden, par, lyr.input_layernorm.weight, B1, N, bucket, delta, self.eps,
-                           self.gate_mode, buf.rec, buf.f, buf.src, buf.rows, count, buf.seg,
-                           segcnt, buf.rstd, buf.xn)
+            ln_w = lyr.input_layernorm.weight
+            if teacher is not None and li in teacher:
+                hidden = teacher[li].reshape(BN, D).to(torch.bfloat16).contiguous()
+            if li == 0 or (teacher is not None and li in teacher):
+                hidden = hidden.contiguous()
+                _lib.fold_gate(hidden, par, ln_w, B1, N, bucket, delta, self.eps, self.gate_mode,
+                               buf.rec, buf.f, buf.src, buf.rows, count, buf.seg, segcnt,
+                               buf.rstd, buf.xn, slot=buf.slot)
+            else:
+                # the previous layer's folded residual update (fastdllm_v2_folded.py:218)
+                # fused into this layer's gate: x = bf16(hp + ffn[src*N + n])
+                hidden = buf.hid[li % 2]
+                _lib.fold_gate_residual(buf.hp, buf.ffn, buf.src, par, ln_w, B1, N, D, bucket,
+                                        delta, self.eps, self.gate_mode, hidden, buf.rec, buf.f,
+                                        buf.src, buf.rows, count, buf.seg, segcnt, buf.slot,
+                                        buf.rstd, buf.xn)
             w_qkv, b_qkv = self._packed[li]
             _lib.qkv_rope(buf.xn, buf.rows, count, bucket, BN, w_qkv, b_qkv, cos, sin, q_scale,
                           N, D, H, Hkv, hd, buf.q_buf, buf.kv_buf, buf.ws_qkv, pos0=pos0)
@@ -301,22 +311,24 @@ class FoldedVerifyEngine:
                                B1, N, H, Hkv, hd, self.scaling, buf.o32, buf.o_bf, buf.m_tab,
                                buf.z_tab)
 
-            # o_proj + residual for every row (fastdllm_v2_folded.py:207-209): M = BN is
-            # a regular GEMM shape, where hipBLASLt beats the skinny-M streaming kernel;
-            # mm then add keeps the reference's two bf16 roundings
+            # o_proj for every row (fastdllm_v2_folded.py:207-209): M = BN is a regular
+            # GEMM shape, where hipBLASLt beats the skinny-M streaming kernel; then one
+            # kernel for the residual hp = bf16(x + bf16(O Wo^T)) (two roundings as in
+            # the reference) and the post-attention RMSNorm of the recomputed rows
             torch.mm(buf.o_bf, lyr.self_attn.o_proj.weight.t(), out=buf.attn_out)
-            torch.add(hidden, buf.attn_out, out=buf.hp[:BN])
+            _lib.residual_post_norm(hidden, buf.attn_out, buf.slot, BN, D,
+                                    lyr.post_attention_layernorm.weight, self.eps, buf.hp, buf.zn)
             # FFN on the compacted rows (:211-217)
-            _lib.rows_rmsnorm(buf.hp, buf.rows, count, bucket, lyr.post_attention_layernorm.weight,
-                              D, self.eps, buf.zn)
             wg, wu, wd = self._packed_mlp[li]
             _lib.ffn_gate_up(buf.zn, count, bucket, wg, wu, D, self.I, buf.act)
             _lib.ffn_down_scatter(buf.act, count, bucket, buf.rows, wd, self.I, D, buf.ffn,
                                   buf.ws_gemm)
-            # folded rows reuse the FFN output of their nearest recomputing ancestor (:218)
-            new_hidden = buf.hid[li % 2]
-            _lib.residual_gather_add(buf.hp, buf.ffn, buf.src, B1, N, D, new_hidden)
             if trace is not None:
+                # folded rows reuse the FFN output of their nearest recomputing ancestor
+                # (:218); the fused kernels form this inside the next gate, so the trace
+                # computes it separately
+                h_out = torch.empty(BN, D, dtype=torch.bfloat16, device=self.device)
+                _lib.residual_gather_add(buf.hp, buf.ffn, buf.src, B1, N, D, h_out)
                 trace.append(dict(
                     h_in=hidden.clone(), rec=buf.rec.clone(), rows=buf.rows.clone(),
                     count=count.clone(), src=buf.src.clone(), f=buf.f.clone(),
@@ -324,9 +336,12 @@ class FoldedVerifyEngine:
                     xn=buf.xn.clone(), q=buf.q_buf.clone(), kv=buf.kv_buf.clone(),
                     o32=buf.o32.clone(), o_bf=buf.o_bf.clone(), m=buf.m_tab.clone(),
                     z=buf.z_tab.clone(), hp=buf.hp[:BN].clone(), ffn=buf.ffn.clone(),
-                    h_out=new_hidden.clone()))
-            hidden = new_hidden
-        return hidden
+                    h_out=h_out))
+        # the last layer's residual update and the final norm (:218, :222)
+        last = buf.hid[self.L % 2]
+        _lib.residual_rmsnorm(buf.hp, buf.ffn, buf.src, base.norm.weight, B1, N, D, self.eps,
+                              last, buf.final)
+        return last
 
     def _attention(self, buf: _Buffers, cache, li: int, count, bucket: int, B1: int, N: int):
         pv = prefix_view(cache, li)
@@ -403,10 +418,15 @@ class FoldedVerifyEngine:
         w_qkv, b_qkv = self._packed[li]
         hidden = st["hidden"]
 
+        scratch = torch.empty_like(buf.hid[0])
+        normed = torch.empty_like(buf.hid[0])
+
         def gate():
-            _lib.fold_gate(hidden, st["par"], lyr.input_layernorm.weight, B1, N, bucket, st["delta"],
-                           self.eps, self.gate_mode, buf.rec, buf.f, buf.src, buf.rows, count,
-                           buf.seg, segcnt, buf.rstd, buf.xn)
+            # the fused gate of a layer after the first (residual update + gate + compaction)
+            _lib.fold_gate_residual(buf.hp, buf.ffn, buf.src, st["par"], lyr.input_layernorm.weight,
+                                    B1, N, D, bucket, st["delta"], self.eps, self.gate_mode,
+                                    scratch, buf.rec, buf.f, buf.src, buf.rows, count, buf.seg,
+                                    segcnt, buf.slot, buf.rstd, buf.xn)
 
         cos, sin = self._rope
         pos0 = cache.length_dev if isinstance(cache, PagedKVCache) else buf.pos0
@@ -426,11 +446,10 @@ class FoldedVerifyEngine:
 
         def o_proj():
             torch.mm(buf.o_bf, lyr.self_attn.o_proj.weight.t(), out=buf.attn_out)
-            torch.add(hidden, buf.attn_out, out=buf.hp[:BN])
 
         def post_norm():
-            _lib.rows_rmsnorm(buf.hp, buf.rows, count, bucket, lyr.post_attention_layernorm.weight,
-                              D, self.eps, buf.zn)
+            _lib.residual_post_norm(hidden, buf.attn_out, buf.slot, BN, D,
+                                    lyr.post_attention_layernorm.weight, self.eps, buf.hp, buf.zn)
 
         wg, wu, wd = self._packed_mlp[li]
 
@@ -441,10 +460,9 @@ class FoldedVerifyEngine:
             _lib.ffn_down_scatter(buf.act, count, bucket, buf.rows, wd, self.I, D, buf.ffn,
                                   buf.ws_gemm)
 
-        scratch = torch.empty_like(buf.hid[0])
-
-        def resid():
-            _lib.residual_gather_add(buf.hp, buf.ffn, buf.src, B1, N, D, scratch)
+        def final_norm():
+            _lib.residual_rmsnorm(buf.hp, buf.ffn, buf.src, self.model.model.norm.weight, B1, N, D,
+                                  self.eps, scratch, normed)
 
         logits = torch.empty(BN, self.V, dtype=torch.bfloat16, device=self.device)
 
@@ -452,7 +470,7 @@ class FoldedVerifyEngine:
             torch.mm(buf.final, self.model.lm_head.weight.t(), out=logits)
 
         out = dict(qkv=qkv, attn=attn, chain=chain, o_proj=o_proj, post_norm=post_norm,
-                   gate_up=gate_up, down=down, resid=resid, lm_head=lm_head, gate=gate)
+                   gate_up=gate_up, down=down, final_norm=final_norm, lm_head=lm_head, gate=gate)
         if isinstance(cache, PagedKVCache) and cache.length + N <= cache.capacity:
             def append():
                 # writes past the logical end of the cache: never read, length unchanged

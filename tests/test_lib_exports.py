@@ -36,10 +36,18 @@ def test_library_exports_every_declared_symbol():
 
 def test_host_side_validation_without_gpu():
     lib = _lib.load()
-    assert lib.sf_abi_version() == 1
+    assert lib.sf_abi_version() == 2
     assert lib.sf_status_string(1).decode() == "shape outside kernel limits"
     # NULL pointers and bad shapes are rejected before any launch
-    assert lib.sf_fold_gate(*([None] * 3), 8, 32, 64, 256, 0.1, 1e-6, 0, *([None] * 10)) == 2
+    assert lib.sf_fold_gate(*([None] * 3), 8, 32, 64, 256, 0.1, 1e-6, 0, *([None] * 11)) == 2
+    assert lib.sf_fold_gate_residual(*([None] * 5), 8, 32, 64, 256, 0.1, 1e-6, 0,
+                                     *([None] * 12)) == 2
+    assert lib.sf_residual_rmsnorm(*([None] * 4), 8, 32, 64, 1e-6, *([None] * 3)) == 2
+    assert lib.sf_residual_post_norm(*([None] * 3), 256, 64, None, 1e-6, *([None] * 3)) == 2
+    assert lib.sf_pack_weight(None, 16, 128, None, None) == 2
+    fake = ctypes.c_void_p(256)   # never dereferenced: the shape check comes first
+    assert lib.sf_pack_weight(fake, 15, 128, ctypes.c_void_p(512), None) == 1
+    assert lib.sf_pack_weight(fake, 16, 100, ctypes.c_void_p(512), None) == 1
     assert lib.sf_chain_correct(*([None] * 7), 8, 32, 28, 4, 64, 0.1, *([None] * 5)) == 2
     assert lib.sf_qkv_workspace_bytes(256, 3584, 4608) > 0
     assert lib.sf_attn_workspace_bytes(256, 28, 0) > 0
