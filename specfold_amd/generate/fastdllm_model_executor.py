@@ -109,8 +109,8 @@ class FastDLLMModelExecutor:
             eng.gate_mode = prev_mode
         return SimpleNamespace(logits=logits, past_key_values=past_key_values)
 
-    def sample_with_top_p(self, logits: torch.Tensor, top_p: float = 0.95,
-                          temperature: float = 0.0) -> Tuple[torch.Tensor, torch.Tensor]:
+    @staticmethod
+    def _top_p(logits: torch.Tensor, top_p: float, temperature: float):
         """Top-p filtered sampling (reference fallback, fastdllm_model_executor.py:129-155)."""
         if temperature > 0:
             logits = logits / temperature
@@ -127,6 +127,13 @@ class FastDLLMModelExecutor:
         else:
             tok = torch.argmax(probs, dim=-1)
         return tok, probs
+
+    def sample_with_top_p(self, logits: torch.Tensor, top_p: float = 0.95,
+                          temperature: float = 0.0) -> Tuple[torch.Tensor, torch.Tensor]:
+        """Top-p filtered sampling, eager: replaying torch's sort / scan kernels of
+        this sequence from a captured HIP graph faulted the GPU, so it stays out of
+        graphs."""
+        return self._top_p(logits, top_p, temperature)
 
     def get_tokenizer(self):
         return self.tokenizer

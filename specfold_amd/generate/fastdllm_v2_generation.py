@@ -114,9 +114,7 @@ class FastDLLMV2SpeculativeGeneration:
         n_masked = int(small_mask.sum().item())
         if n_masked == 0:
             return []
-        conf = torch.softmax(small_logits, dim=-1).max(dim=-1).values
-        conf = torch.where(~small_mask, float("-inf"), conf)
-        drafts = []
+        active = []
         for node in self.calibration_graph.get("selected_nodes", []):
             ij_set = node.get("ij_set", [])
             if not ij_set:
@@ -124,15 +122,33 @@ class FastDLLMV2SpeculativeGeneration:
             top_rank = max(pr for pr, _ in ij_set)
             if top_rank >= n_masked:
                 continue
+            active.append((node, tuple((int(pr), int(vr)) for pr, vr in ij_set), top_rank))
+        if not active:
+            return []
+        # eager: torch.topk over a vocabulary row runs rocprim's radix sort, whose
+        # look-back state is initialised by a memset; replayed from a captured HIP
+        # graph it faulted the GPU, so the draft construction stays out of graphs
+        states = self._draft_states(x, small_logits, small_mask, offset, active)
+        return [{"state": states[i], "start_pos": start_pos, "end_pos": end_pos, "node": node}
+                for i, (node, _, _) in enumerate(active)]
+
+    @staticmethod
+    def _draft_states(x, small_logits, small_mask, offset, active) -> torch.Tensor:
+        """The draft blocks of the active nodes, stacked [n, N] (:430-470); device
+        ops only (indices stay on the device), so no host sync per node."""
+        conf = torch.softmax(small_logits, dim=-1).max(dim=-1).values
+        conf = torch.where(~small_mask, float("-inf"), conf)
+        blocks = []
+        for _, ij_set, top_rank in active:
             positions = torch.topk(conf, k=top_rank + 1).indices
             block = x.clone()
             for pos_rank, vocab_rank in ij_set:
-                pos = positions[pos_rank]
-                tok = torch.topk(small_logits[pos], k=vocab_rank + 1).indices[vocab_rank]
-                block[offset + pos] = tok
-            drafts.append({"state": block, "start_pos": start_pos, "end_pos": end_pos,
-                           "node": node})
-        return drafts
+                pos = positions[pos_rank:pos_rank + 1]
+                row = small_logits.index_select(0, pos)[0]
+                tok = torch.topk(row, k=vocab_rank + 1).indices[vocab_rank:vocab_rank + 1]
+                block.index_put_((pos + offset,), tok)
+            blocks.append(block)
+        return torch.stack(blocks)
 
     # -- the decode loop ----------------------------------------------------------------
     def _stop_reached(self, x_t: torch.Tensor, prompt_length: int) -> bool:
@@ -242,7 +258,7 @@ class FastDLLMV2SpeculativeGeneration:
                         unmask[torch.arange(x_1.shape[0], device=self.device), best] = True
                         unmask = unmask & small_mask
                         region = x_t[:, x_t.shape[1] - bl + s0: x_t.shape[1] - bl + s1]
-                        region[unmask] = x_1[unmask]
+                        region.copy_(torch.where(unmask, x_1, region))
                         n = int(unmask.sum())
                         self.last_commits.append(n)
                         yield {"kind": kind, "committed": n}
