@@ -51,25 +51,29 @@ def parse_args(argv=None):
     ap.add_argument("--kernel-iters", type=int, default=200)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--only-kernels", action="store_true",
-                    help="skip the decode loop; time the verify step and kernels only")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also time a plain 256 MiB device copy (counter calibration)")
     return ap.parse_args(argv)
 
 
-def event_time_ms(fn, iters: int) -> float:
-    """Average ms per call of fn() on the GPU: ``iters`` back-to-back launches
-    captured in one HIP graph, replayed between two HIP events recorded on the
-    stream the kernels run on (no host launch overhead between kernels)."""
+def event_time_ms(fns, iters: int) -> float:
+    """Average ms per call on the GPU: ``iters`` back-to-back launches (cycling
+    through ``fns``, e.g. one launcher per layer, so each launch streams another
+    layer's weights as the verify step does) captured in one HIP graph and
+    replayed between two HIP events recorded on the stream the kernels run on
+    (no host launch overhead between kernels)."""
+    fns = fns if isinstance(fns, (list, tuple)) else [fns]
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
-        fn()
+        for fn in fns:
+            fn()
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        for _ in range(iters):
-            fn()
+        for i in range(iters):
+            fns[i % len(fns)]()
     graph.replay()
     torch.cuda.synchronize()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -139,6 +143,42 @@ def kernel_roofline(name, ms, w, R, B1, N, P):
             "frac": round(ach / peak, 5), "traffic": None, "avg_us": round(ms * 1e3, 3),
             "algorithmic_bytes": int(by), "algorithmic_flops": int(fl),
             "hbm_gbps": round(by / s / 1e9, 2), "mfma_tflops": round(fl / s / 1e12, 3)}
+
+
+# kernels launched once per verify step (the others once per layer)
+ONCE_PER_STEP = ("lm_head", "final_norm")
+
+
+def load_traffic(workload: str) -> dict:
+    """HBM bytes per launch measured by rocprofv3 PMC runs (FETCH_SIZE and
+    WRITE_SIZE, scaled by the plain-copy calibration), committed as JSON under
+    profiles/; empty when absent."""
+    path = ROOT / "profiles" / f"traffic_{workload}.json"
+    if not path.exists():
+        return {}
+    data = json.loads(path.read_text())
+    return {k: v.get("bytes_per_launch") for k, v in data.get("kernels", {}).items()}
+
+
+def copy_calibration(mib: int = 256, reps: int = 8) -> dict:
+    """A plain device copy of known size through an ordinary vectorized
+    elementwise kernel (y = 2x in fp32): the reference point for the
+    FETCH_SIZE / WRITE_SIZE counters, and the copy bandwidth this GPU reaches."""
+    n = (mib << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.mul(src, 2.0, out=dst)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        torch.mul(src, 2.0, out=dst)
+    e.record()
+    e.synchronize()
+    us = s.elapsed_time(e) / reps * 1e3
+    nbytes = n * 4
+    return {"kernel": "vectorized_elementwise_kernel (fp32 y = 2x)", "bytes_read": nbytes,
+            "bytes_written": nbytes, "avg_us": round(us, 2), "gbps": round(2 * nbytes / us / 1e3, 1)}
 
 
 def cpu_baseline(w, batched_cpu, tokens_per_step, seconds):
@@ -278,20 +318,33 @@ def main(argv=None) -> int:
     print(f"[bench] verify step median {verify_ms:.3f} ms, mean R {R}", file=sys.stderr,
           flush=True)
 
-    # per-kernel timings on the buffers of the last verify step (layer 0 of the view)
+    # per-kernel timings on the buffers of the last verify step, cycling through the
+    # layers (weights and cache slices) as the step does
     eng = gen._engine
-    launchers, info = eng.profile_launchers(li=-1)
+    shared = {}
+    per_layer = [eng.profile_launchers(li=li, shared=shared) for li in range(eng.L)]
+    info = per_layer[-1][1]
     P = info["prefix"]
     R_last = int(info["count"].item())
     kernels = {}
     for name in ("qkv", "attn", "chain", "o_proj", "post_norm", "gate_up", "down", "final_norm",
                  "lm_head", "append", "gate"):
-        if name not in launchers:
+        if name not in per_layer[-1][0]:
             continue
-        ms = event_time_ms(launchers[name], args.kernel_iters)
+        once = name in ONCE_PER_STEP
+        fns = [per_layer[-1][0][name]] if once else [pl[0][name] for pl in per_layer]
+        ms = event_time_ms(fns, args.kernel_iters if not once else max(4, args.kernel_iters // 10))
         kernels[name] = kernel_roofline(name, ms, w, R_last, B1, N, P)
+        kernels[name]["launches_per_step"] = 1 if once else eng.L
+    traffic = load_traffic(w.name)
+    for name, k in kernels.items():
+        k["traffic"] = traffic.get(name)
     print(f"[bench] kernels {json.dumps({k: v['avg_us'] for k, v in kernels.items()})}",
           file=sys.stderr, flush=True)
+    # the dominant kernel: largest GPU time per verify step
+    dominant = max((n for n in kernels if n != "append"),
+                   key=lambda n: kernels[n]["avg_us"] * kernels[n]["launches_per_step"])
+    copy = copy_calibration() if args.copy_calibration else None
 
     tokens_per_step = committed / max(1, args.steps)
     cpu = None
@@ -325,8 +378,9 @@ def main(argv=None) -> int:
         "decode_step_kinds": kinds,
         "tokens_per_step": round(tokens_per_step, 4),
         "prefill_s": round(prefill_s, 3),
-        "roofline": kernels.get("attn"),
+        "roofline": dict(kernels[dominant], kernel=dominant),
         "kernels": kernels,
+        "copy_calibration": copy,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))

@@ -400,11 +400,13 @@ class FoldedVerifyEngine:
         return out
 
     # ------------------------------------------------------------------------
-    def profile_launchers(self, li: int = -1):
+    def profile_launchers(self, li: int = -1, shared: Optional[dict] = None):
         """No-argument callables that re-launch each HIP entry point of layer
-        ``li`` on the buffers resident from the last forward (for timing).
-        The gate runs on the last layer's output hidden states, so call it
-        last: it rewrites rows/count/src for the other launchers."""
+        ``li`` (its weights, its slice of the cache) on the buffers resident from
+        the last forward (for timing).  The gate runs on the last layer's output
+        hidden states, so call it last: it rewrites rows/count/src for the other
+        launchers.  ``shared`` (a dict) lets the launchers of several layers
+        share their scratch outputs."""
         st = self._last
         B1, N, bucket, cache = st["B1"], st["N"], st["bucket"], st["cache"]
         BN = B1 * N
@@ -418,8 +420,12 @@ class FoldedVerifyEngine:
         w_qkv, b_qkv = self._packed[li]
         hidden = st["hidden"]
 
-        scratch = torch.empty_like(buf.hid[0])
-        normed = torch.empty_like(buf.hid[0])
+        shared = {} if shared is None else shared
+        if "scratch" not in shared:
+            shared["scratch"] = torch.empty_like(buf.hid[0])
+            shared["normed"] = torch.empty_like(buf.hid[0])
+            shared["logits"] = torch.empty(BN, self.V, dtype=torch.bfloat16, device=self.device)
+        scratch, normed, logits = shared["scratch"], shared["normed"], shared["logits"]
 
         def gate():
             # the fused gate of a layer after the first (residual update + gate + compaction)
@@ -463,8 +469,6 @@ class FoldedVerifyEngine:
         def final_norm():
             _lib.residual_rmsnorm(buf.hp, buf.ffn, buf.src, self.model.model.norm.weight, B1, N, D,
                                   self.eps, scratch, normed)
-
-        logits = torch.empty(BN, self.V, dtype=torch.bfloat16, device=self.device)
 
         def lm_head():
             torch.mm(buf.final, self.model.lm_head.weight.t(), out=logits)
