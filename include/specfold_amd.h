@@ -125,7 +125,11 @@ int sf_qkv_rope(const uint16_t* xn, const int32_t* rows, const int32_t* count, i
  * keeping the softmax state.  Replaces specfold_flash_attn_gqa_kernel
  * (specfold/generate/triton_kernels.py:301-361), i.e. the reference's fp32
  * attention of recomputed rows (specfold/generate/fastdllm_v2_folded.py:164-181).
- * Block key j of branch b is kv_buf row src[b*N+j]*N + j.  No mask.
+ * Block key j of branch b is kv_buf row src[b*N+j]*N + j.  No mask, unless
+ * block_causal != 0: then block position n sees the block keys j <= n (and the
+ * whole prefix) — the causal forward the NLD generator commits blocks with
+ * (specfold/generate/nld_generation.py:300-310, use_causal_mask=True); used
+ * with every row recomputed.
  * Writes o32, o_bf, m_tab, z_tab for the rows listed in rows[0:min(count,bucket)].
  * prefix_len (optional, device int32[1]): the prefix length, read on the device;
  * P is then the capacity the grid and workspace are sized for (so one captured
@@ -139,8 +143,8 @@ int sf_attn_prefix_block(const uint16_t* q_buf, const uint16_t* kv_buf, const ui
                          long long page_stride, long long head_stride, const int32_t* src,
                          const int32_t* rows, const int32_t* count, int bucket, int B1, int N,
                          int H, int Hkv, int hd, float scaling, const int32_t* prefix_len,
-                         float* o32, uint16_t* o_bf, float* m_tab, float* z_tab, void* workspace,
-                         size_t workspace_bytes, void* stream);
+                         int block_causal, float* o32, uint16_t* o_bf, float* m_tab,
+                         float* z_tab, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * (4) Chain correction of folded rows: start from the state of the nearest

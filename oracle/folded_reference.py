@@ -7,6 +7,11 @@ trajectory.  Every numbered step below cites the reference line it follows.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this.
 
+The NLD variant (specfold/generate/nld_folded.py:89-237) is the same step with
+the decoder at ``model.encoder`` and the head at ``model.diffusion_head``, no QKV
+bias, the config's RMSNorm eps, no logit shift, and the llama-4 q scale after
+RoPE (``q_scale``; nld_folded.py:37-53, 173-174).
+
 The model argument is any module tree with the Qwen2 layout the reference reads:
 ``model.model.{embed_tokens, rotary_emb, layers[i], norm}``, ``model.lm_head``,
 ``model.config`` and per layer ``input_layernorm``,
@@ -135,11 +140,13 @@ def folded_layer(
     n_kv_heads: int,
     counters: Optional[FoldCounters] = None,
     trace: Optional[LayerTrace] = None,
+    q_scale: Optional[torch.Tensor] = None,
 ) -> List[torch.Tensor]:
     """One decoder layer of the folded verify step for all B1 branches.
 
-    Follows fastdllm_v2_folded.py:117-220.  ``h`` is a list of B1 tensors
-    [1, N, D]; returns the list of next-layer hidden states.
+    Follows fastdllm_v2_folded.py:117-220 (and nld_folded.py:132-232, which adds
+    ``q_scale``).  ``h`` is a list of B1 tensors [1, N, D]; returns the list of
+    next-layer hidden states.
     """
     attn = lyr.self_attn
     hd = attn.head_dim
@@ -209,6 +216,8 @@ def folded_layer(
             s = sin_n[rsel].unsqueeze(0)
             qn = qn * c + rotate_half(qn) * s
             kn = kn * c + rotate_half(kn) * s
+            if q_scale is not None:                               # nld_folded.py:173-174
+                qn = qn * q_scale.to(qn.device)[rsel].view(1, n_rec, 1).to(qn.dtype)
             if p is not None:
                 k_prev = kt[:, rsel].clone()
                 v_prev = vt[:, rsel].clone()
@@ -309,7 +318,7 @@ def rope_tables(model, hidden: torch.Tensor, P: int, N: int) -> Tuple[torch.Tens
     """cos/sin [N, hd] for block positions P..P+N-1, via the model's rotary
     module in the model dtype.  Follows fastdllm_v2_folded.py:112-114."""
     pos = torch.arange(P, P + N, device=hidden.device).unsqueeze(0)
-    cos, sin = model.model.rotary_emb(hidden, pos)
+    cos, sin = decoder_parts(model)[0].rotary_emb(hidden, pos)
     return cos[0], sin[0]
 
 
@@ -317,6 +326,35 @@ def shift_logits(logits: torch.Tensor) -> torch.Tensor:
     """Position i takes the logits of position i-1 (position 0 keeps its own).
     Follows fastdllm_v2_generation.py:121-126."""
     return torch.cat([logits[:, :1], logits[:, :-1]], dim=1)
+
+
+def decoder_parts(model):
+    """(decoder, head): ``model.model`` / ``model.lm_head`` (fastdllm_v2_folded.py:
+    105-108, 222) or ``model.encoder`` / ``model.diffusion_head`` (nld_folded.py:
+    105-108, 237)."""
+    base = getattr(model, "model", None)
+    if base is None or not hasattr(base, "layers"):
+        base = model.encoder
+    head = getattr(model, "lm_head", None)
+    if head is None:
+        head = model.diffusion_head
+    return base, head
+
+
+def llama4_q_scale(cfg, P: int, N: int) -> Optional[torch.Tensor]:
+    """Per-position llama-4 attention scale for block positions [P, P+N), fp32,
+    or None when it is identically 1.  Follows nld_folded.py:37-53 (the scale of
+    modeling_ministral.py:104-106: 1 + beta * log(1 + floor(pos / omax)))."""
+    rp = getattr(cfg, "rope_parameters", None) or {}
+    beta = rp.get("llama_4_scaling_beta")
+    omax = rp.get("original_max_position_embeddings")
+    if beta is None or omax is None:
+        return None
+    pos = torch.arange(P, P + N, dtype=torch.float32)
+    scale = 1.0 + beta * torch.log(1.0 + torch.floor(pos / omax))
+    if bool((scale == 1.0).all()):
+        return None
+    return scale
 
 
 def prefix_length(past_key_values) -> int:
@@ -337,6 +375,7 @@ def folded_verify_step(
     trace: Optional[StepTrace] = None,
     shift: bool = True,
     teacher_hidden: Optional[Dict[int, torch.Tensor]] = None,
+    q_scale: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Folded verify step for B1 >= 2 branches -> logits [B1, N, V].
 
@@ -345,7 +384,7 @@ def folded_verify_step(
     ``dense_verify_step``).  ``teacher_hidden[li]`` (optional) replaces layer
     li's input hidden states, for stage-by-stage comparison.
     """
-    base = model.model
+    base, head = decoder_parts(model)
     cfg = model.config
     B1, N = batched_input.shape
     H = cfg.num_attention_heads
@@ -370,12 +409,12 @@ def folded_verify_step(
             kv = past_key_values[li]
         lt = LayerTrace() if trace is not None else None
         h = folded_layer(lyr, h, parent, order, kv, cos_n, sin_n, float(delta),
-                         H, Hkv, counters=counters, trace=lt)
+                         H, Hkv, counters=counters, trace=lt, q_scale=q_scale)
         if trace is not None:
             trace.layers.append(lt)
 
     final_h = torch.cat(h, dim=0)
-    logits = model.lm_head(base.norm(final_h))                     # :222-223
+    logits = head(base.norm(final_h))                              # :222-223
     if shift:
         logits = shift_logits(logits)
     if trace is not None:
@@ -389,13 +428,16 @@ def folded_verify_step(
 # ---------------------------------------------------------------------------
 
 def dense_layer(lyr, x: torch.Tensor, prefix_kv, cos_n, sin_n, n_heads: int, n_kv_heads: int,
-                return_kv: bool = False):
+                return_kv: bool = False, q_scale: Optional[torch.Tensor] = None,
+                causal: bool = False):
     """Plain (unfolded) decoder layer for a [B, N, D] block that attends to the
     whole prefix and bidirectionally within the block, attention in fp32.
 
     This is what every folded row reduces to when the gate recomputes it, and
     it is the block-diffusion forward the reference's dense seam runs
     (fastdllm_v2_generation.py:151-186) for a block with a prefix cache.
+    ``causal``: block position n sees block positions <= n only (the causal AR
+    forward NLD commits blocks with, nld_generation.py:300-310).
     """
     attn = lyr.self_attn
     hd, scaling = attn.head_dim, attn.scaling
@@ -409,12 +451,18 @@ def dense_layer(lyr, x: torch.Tensor, prefix_kv, cos_n, sin_n, n_heads: int, n_k
     c, s = cos_n[None, None], sin_n[None, None]
     q = q * c + rotate_half(q) * s
     k = k * c + rotate_half(k) * s
+    if q_scale is not None:
+        q = q * q_scale.to(q.device).view(1, 1, N, 1).to(q.dtype)
     kk, vv = expand_kv_heads(k, G), expand_kv_heads(v, G)
     if prefix_kv is not None and prefix_kv[0] is not None:
         pk, pv = prefix_kv
         kk = torch.cat([expand_kv_heads(pk, G).expand(B, -1, -1, -1), kk], dim=2)
         vv = torch.cat([expand_kv_heads(pv, G).expand(B, -1, -1, -1), vv], dim=2)
     sc = torch.einsum("bhnd,bhkd->bhnk", q.float(), kk.float()) * scaling
+    if causal:
+        P = kk.shape[2] - N
+        blk = torch.ones(N, N, dtype=torch.bool, device=sc.device).triu(1)
+        sc[..., P:] = sc[..., P:].masked_fill(blk, float("-inf"))
     w = torch.softmax(sc, dim=-1)
     o = torch.einsum("bhnk,bhkd->bhnd", w, vv.float())
     o = o.transpose(1, 2).reshape(B, N, H * hd).to(x.dtype)
@@ -429,13 +477,14 @@ def dense_layer(lyr, x: torch.Tensor, prefix_kv, cos_n, sin_n, n_heads: int, n_k
 
 @torch.no_grad()
 def dense_verify_step(model, batched_input: torch.Tensor, past_key_values=None, shift: bool = True,
-                      return_new_kv: bool = False):
+                      return_new_kv: bool = False, q_scale: Optional[torch.Tensor] = None,
+                      causal: bool = False):
     """Dense block forward of every branch (no folding) -> logits [B1, N, V].
 
     With ``return_new_kv`` also returns the per-layer (k, v) [B1, Hkv, N, hd]
     of the block, i.e. what a block-commit forward appends to the cache
     (fastdllm_v2_generation.py:557-575)."""
-    base = model.model
+    base, head = decoder_parts(model)
     cfg = model.config
     B1, N = batched_input.shape
     P = prefix_length(past_key_values)
@@ -445,9 +494,10 @@ def dense_verify_step(model, batched_input: torch.Tensor, past_key_values=None, 
     for li, lyr in enumerate(base.layers):
         kv = past_key_values[li] if past_key_values is not None and len(past_key_values) > li else None
         x, kvb = dense_layer(lyr, x, kv, cos_n, sin_n, cfg.num_attention_heads,
-                             cfg.num_key_value_heads, return_kv=True)
+                             cfg.num_key_value_heads, return_kv=True, q_scale=q_scale,
+                             causal=causal)
         new_kv.append(kvb)
-    logits = model.lm_head(base.norm(x))
+    logits = head(base.norm(x))
     if shift:
         logits = shift_logits(logits)
     if return_new_kv:

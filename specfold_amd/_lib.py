@@ -42,8 +42,8 @@ SIGNATURES = {
                          _i, _i, _i, _i, _i, _vp, _vp, _vp, _sz, _vp]),
     "sf_attn_workspace_bytes": (_sz, [_i, _i, _i]),
     "sf_attn_prefix_block": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _ll, _ll, _vp, _vp, _vp,
-                                  _i, _i, _i, _i, _i, _i, _f, _vp, _vp, _vp, _vp, _vp, _vp, _sz,
-                                  _vp]),
+                                  _i, _i, _i, _i, _i, _i, _f, _vp, _i, _vp, _vp, _vp, _vp, _vp,
+                                  _sz, _vp]),
     "sf_chain_correct": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f,
                               _vp, _vp, _vp, _vp, _vp]),
     "sf_kv_append": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp, _i, _ll, _ll, _i, _vp]),
@@ -230,9 +230,11 @@ def attn_workspace_bytes(bucket: int, H: int, P: int) -> int:
 
 def attn_prefix_block(q_buf, kv_buf, prefix_k, prefix_v, page_table, P, page_size, page_stride,
                       head_stride, src, rows, count, bucket, B1, N, H, Hkv, hd, scaling,
-                      o32, o_bf, m_tab, z_tab, workspace, prefix_len=None, stream=None) -> None:
+                      o32, o_bf, m_tab, z_tab, workspace, prefix_len=None, stream=None,
+                      block_causal: bool = False) -> None:
     """prefix_len: optional device int32[1] holding the prefix length; P is then
-    the capacity (grid / workspace size)."""
+    the capacity (grid / workspace size).  block_causal: block position n sees the
+    block keys j <= n only (a causal block commit; every row recomputed)."""
     BN = B1 * N
     _need(q_buf, "q_buf", torch.bfloat16, min_numel=(BN + 1) * H * hd)
     _need(kv_buf, "kv_buf", torch.bfloat16, min_numel=(BN + 1) * 2 * Hkv * hd)
@@ -257,7 +259,8 @@ def attn_prefix_block(q_buf, kv_buf, prefix_k, prefix_v, page_table, P, page_siz
         _ptr(q_buf), _ptr(kv_buf), _ptr(prefix_k) if P > 0 else None,
         _ptr(prefix_v) if P > 0 else None, _ptr(page_table) if P > 0 else None, P,
         page_size, page_stride, head_stride, _ptr(src), _ptr(rows), _ptr(count), bucket, B1, N, H,
-        Hkv, hd, float(scaling), _ptr(prefix_len) if P > 0 else None, _ptr(o32), _ptr(o_bf),
+        Hkv, hd, float(scaling), _ptr(prefix_len) if P > 0 else None, 1 if block_causal else 0,
+        _ptr(o32), _ptr(o_bf),
         _ptr(m_tab), _ptr(z_tab), _ptr(workspace), workspace.numel(), _stream(stream))
     _check(st, "sf_attn_prefix_block")
 

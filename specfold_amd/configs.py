@@ -41,6 +41,11 @@ class Workload:
     def branches(self) -> int:
         return self.budget_B + 1
 
+    @property
+    def family(self) -> str:
+        """"fastdllm" (Qwen2 layout, shifted logits) or "nld" (Llama layout, no shift)."""
+        return "fastdllm" if self.logit_shift else "nld"
+
 
 WORKLOADS: Dict[str, Workload] = {
     # cfg 1: CPU reference, one Qwen2-1.5B-shaped decoder layer, fp32, 512 prefix

@@ -250,7 +250,7 @@ constexpr int kBatch = 16;        // chunk partials loaded per round
 
 SF_DEV void merge_item(const uint16_t* __restrict__ q_buf, const uint16_t* __restrict__ kv_buf,
                        const int32_t* __restrict__ src, const int32_t* __restrict__ rows, int m,
-                       int h, int N, int H, int Hkv, int G, float scale_log2, int nch,
+                       int h, int N, int H, int Hkv, int G, float scale_log2, int causal, int nch,
                        int nchunks_cap, int qmax, const float* __restrict__ ws_o,
                        const float* __restrict__ ws_ml, float* __restrict__ o32,
                        uint16_t* __restrict__ o_bf, float* __restrict__ m_tab,
@@ -309,7 +309,8 @@ SF_DEV void merge_item(const uint16_t* __restrict__ q_buf, const uint16_t* __res
 #pragma unroll
       for (int t = 0; t < 8; ++t) d = fmaf(sq[g][e + t], kf[t], d);
     }
-    ss[g][j] = d * scale_log2;
+    // causal (a block commit of an AR forward): block position n sees keys j <= n
+    ss[g][j] = (causal && j > row - b * N) ? -INFINITY : d * scale_log2;
   }
   __syncthreads();
 
@@ -384,7 +385,7 @@ __global__ __launch_bounds__(512) void sf_attn_block_merge_kernel(
     const uint16_t* __restrict__ q_buf, const uint16_t* __restrict__ kv_buf,
     const int32_t* __restrict__ src, const int32_t* __restrict__ rows,
     const int32_t* __restrict__ count_p, int bucket, int N, int H, int Hkv, float scale_log2,
-    const int32_t* __restrict__ p_len, int P_cap, int nchunks_cap, int qmax,
+    int causal, const int32_t* __restrict__ p_len, int P_cap, int nchunks_cap, int qmax,
     const float* __restrict__ ws_o, const float* __restrict__ ws_ml, float* __restrict__ o32,
     uint16_t* __restrict__ o_bf, float* __restrict__ m_tab, float* __restrict__ z_tab) {
   __shared__ float sq[kMaxG][kHD];
@@ -398,7 +399,7 @@ __global__ __launch_bounds__(512) void sf_attn_block_merge_kernel(
   const int P = p_len ? min(*p_len, P_cap) : P_cap;
   const int nch = min((P + kChunk - 1) / kChunk, nchunks_cap);
   for (int it = blockIdx.x; it < count * Hkv; it += gridDim.x) {
-    merge_item(q_buf, kv_buf, src, rows, it / Hkv, it % Hkv, N, H, Hkv, G, scale_log2, nch,
+    merge_item(q_buf, kv_buf, src, rows, it / Hkv, it % Hkv, N, H, Hkv, G, scale_log2, causal, nch,
                nchunks_cap, qmax, ws_o, ws_ml, o32, o_bf, m_tab, z_tab, sq, sk, sv, ss, sml, sM,
                sZ);
     __syncthreads();  // LDS is reused by the next item
@@ -423,7 +424,8 @@ extern "C" int sf_attn_prefix_block(const uint16_t* q_buf, const uint16_t* kv_bu
                                     long long page_stride, long long head_stride,
                                     const int32_t* src, const int32_t* rows, const int32_t* count,
                                     int bucket, int B1, int N, int H, int Hkv, int hd,
-                                    float scaling, const int32_t* prefix_len, float* o32,
+                                    float scaling, const int32_t* prefix_len, int block_causal,
+                                    float* o32,
                                     uint16_t* o_bf, float* m_tab, float* z_tab, void* workspace,
                                     size_t workspace_bytes, void* stream) {
   if (!q_buf || !kv_buf || !src || !rows || !count || !o32 || !o_bf || !m_tab || !z_tab)
@@ -457,7 +459,8 @@ extern "C" int sf_attn_prefix_block(const uint16_t* q_buf, const uint16_t* kv_bu
   }
   const int grid2 = min(bucket * Hkv, 2 * kCUs);
   hipLaunchKernelGGL(sf_attn_block_merge_kernel, dim3(grid2), dim3(512), 0, st, q_buf, kv_buf,
-                     src, rows, count, bucket, N, H, Hkv, scale_log2, P > 0 ? prefix_len : nullptr,
+                     src, rows, count, bucket, N, H, Hkv, scale_log2, block_causal ? 1 : 0,
+                     P > 0 ? prefix_len : nullptr,
                      P, nch, qmax, ws_o, ws_ml, o32, o_bf, m_tab, z_tab);
   return sf_launch_status();
 }

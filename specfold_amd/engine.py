@@ -66,6 +66,19 @@ class StepStats:
     overflow: bool = False
 
 
+def decoder_parts(model):
+    """(decoder stack, output head) of a causal-LM module tree: ``model.model`` /
+    ``model.lm_head`` (Qwen2, Llama), or ``model.encoder`` / ``model.diffusion_head``
+    (Nemotron-Labs-Diffusion, specfold/generate/nld_folded.py:105-108, 237)."""
+    base = getattr(model, "model", None)
+    if base is None or not hasattr(base, "layers"):
+        base = model.encoder
+    head = getattr(model, "lm_head", None)
+    if head is None:
+        head = model.diffusion_head
+    return base, head
+
+
 class _Buffers:
     """Device buffers for one (B1, N, bucket, P-capacity) shape; reused across steps."""
 
@@ -100,6 +113,7 @@ class _Buffers:
         self.final = torch.zeros(BN, D, dtype=bf, device=dev)
         self.attn_out = torch.zeros(BN, D, dtype=bf, device=dev)
         self.pos0 = torch.zeros(1, **i32)   # first block position (caches without length_dev)
+        self.q_scale = torch.ones(N, dtype=torch.float32, device=dev)  # per-position q scale
         self.all_rows = torch.arange(BN, **i32)
         self.all_count = torch.full((1,), BN, **i32)
         nq = (H + 2 * Hkv) * hd
@@ -120,7 +134,8 @@ class FoldedVerifyEngine:
         _lib.load()  # fail loudly, before any work, if the HIP library is not built
         model.requires_grad_(False)
         self.model = model
-        base = model.model
+        base, head = decoder_parts(model)
+        self.base, self.head = base, head
         cfg = model.config
         self.cfg = cfg
         self.layers = base.layers
@@ -132,7 +147,7 @@ class FoldedVerifyEngine:
         self.scaling = float(attn0.scaling)
         self.D = base.embed_tokens.weight.shape[1]
         self.I = self.layers[0].mlp.gate_proj.weight.shape[0]
-        self.V = model.lm_head.weight.shape[0]
+        self.V = head.weight.shape[0]
         self.device = base.embed_tokens.weight.device
         if base.embed_tokens.weight.dtype != torch.bfloat16:
             raise TypeError("the HIP verify step runs bf16 models")
@@ -187,7 +202,7 @@ class FoldedVerifyEngine:
         if self._rope is None or self._rope[0].shape[0] < rows_needed:
             T = max(int(rows_needed), int(getattr(self.cfg, "max_position_embeddings", 0) or 0),
                     4096)
-            base = self.model.model
+            base = self.base
             pos = torch.arange(T, device=self.device).unsqueeze(0)
             cos, sin = base.rotary_emb(base.embed_tokens.weight, pos)
             self._rope = (cos[0].contiguous(), sin[0].contiguous())
@@ -202,13 +217,18 @@ class FoldedVerifyEngine:
                 q_scale: Optional[torch.Tensor] = None,
                 trace: Optional[list] = None,
                 teacher: Optional[Dict[int, torch.Tensor]] = None,
-                stats: Optional[StepStats] = None) -> Optional[torch.Tensor]:
+                stats: Optional[StepStats] = None,
+                causal: bool = False) -> Optional[torch.Tensor]:
         """Verify step -> logits [B1, N, V] (unshifted), or None if not compute_logits.
 
         batched_input  [B1, N] int64 on the model's device; row 0 = main branch.
         cache          PagedKVCache, a reference-style per-layer (k, v) cache, or None.
         append         also write the block's K/V into ``cache`` at its end and
                        advance it (block-commit forward; requires B1 == 1).
+        q_scale        optional [N] fp32: roped q of block position n is multiplied by
+                       bf16(q_scale[n]) (the llama-4 attention scale of NLD models).
+        causal         block position n attends to block positions <= n only (an AR
+                       forward: NLD's prefill / block commit); every row recomputed.
         trace          list to receive one dict of per-layer device tensors (clones).
         teacher        {layer: hidden [B1, N, D]} replacing that layer's input.
         """
@@ -227,19 +247,23 @@ class FoldedVerifyEngine:
         P = cache_length(cache)
         P_alloc = cache.capacity if isinstance(cache, PagedKVCache) else P
         buf = self.buffers(B1, N, bucket, P_alloc)
-        base = self.model.model
-        D = self.D
+        if causal and self.gate_mode != _lib.SF_GATE_ALL:
+            raise ValueError("a causal forward recomputes every row (gate mode SF_GATE_ALL)")
         self.rope_tables(P + N)
         if not isinstance(cache, PagedKVCache):
             buf.pos0.fill_(P)
-        graphable = (self.use_graphs and trace is None and teacher is None and not append
-                     and q_scale is None)
+        qs = None
+        if q_scale is not None:
+            buf.q_scale.copy_(q_scale.reshape(-1).to(device=self.device, dtype=torch.float32))
+            qs = buf.q_scale
+        graphable = self.use_graphs and trace is None and teacher is None and not append
         if graphable:
-            hidden = self._replay(buf, batched_input, par, cache, P, delta, bucket)
+            hidden = self._replay(buf, batched_input, par, cache, P, delta, bucket,
+                                  qs is not None, causal)
         else:
             hidden = self._run_layers(buf, batched_input, par, cache, delta, bucket,
-                                      append=append, q_scale=q_scale, trace=trace,
-                                      teacher=teacher)
+                                      append=append, q_scale=qs, trace=trace,
+                                      teacher=teacher, causal=causal)
 
         if append:
             cache.advance(N)
@@ -254,22 +278,23 @@ class FoldedVerifyEngine:
                            max(counts), bucket, BN)
             return self.forward(batched_input, cache, delta, bucket=BN, parent=parent,
                                 compute_logits=compute_logits, q_scale=q_scale, trace=trace,
-                                teacher=teacher, stats=stats)
+                                teacher=teacher, stats=stats, causal=causal)
         self.last_hidden = hidden
-        self._last = dict(B1=B1, N=N, bucket=bucket, cache=cache, par=par, q_scale=q_scale,
+        self._last = dict(B1=B1, N=N, bucket=bucket, cache=cache, par=par, q_scale=qs,
                           hidden=hidden, delta=delta)
         if not compute_logits:
             return None
         # lm_head over all BN rows (M = BN) on the final-normed rows: hipBLASLt, a fresh
         # tensor per call
-        logits = torch.mm(buf.final, self.model.lm_head.weight.t())
+        logits = torch.mm(buf.final, self.head.weight.t())
         return logits.view(B1, N, self.V)
 
     # ------------------------------------------------------------------------
     def _run_layers(self, buf: _Buffers, tokens: torch.Tensor, par: torch.Tensor, cache,
                     delta: float, bucket: int, append: bool = False,
                     q_scale: Optional[torch.Tensor] = None, trace: Optional[list] = None,
-                    teacher: Optional[Dict[int, torch.Tensor]] = None) -> torch.Tensor:
+                    teacher: Optional[Dict[int, torch.Tensor]] = None,
+                    causal: bool = False) -> torch.Tensor:
         """Embedding and every layer: device launches only (no host sync), so the
         sequence can be captured in a HIP graph.  RoPE rows and a paged cache's
         length come from the cache's device-side length (buf.pos0 for other
@@ -278,7 +303,7 @@ class FoldedVerifyEngine:
         B1, N = tokens.shape
         BN = B1 * N
         H, Hkv, hd, D = self.H, self.Hkv, self.hd, self.D
-        base = self.model.model
+        base = self.base
         hidden = base.embed_tokens(tokens).reshape(BN, D)
         cos, sin = self._rope
         pos0 = cache.length_dev if isinstance(cache, PagedKVCache) else buf.pos0
@@ -306,7 +331,7 @@ class FoldedVerifyEngine:
                           N, D, H, Hkv, hd, buf.q_buf, buf.kv_buf, buf.ws_qkv, pos0=pos0)
             if append:
                 cache.append_rows(li, buf.kv_buf, 0, N)
-            self._attention(buf, cache, li, count, bucket, B1, N)
+            self._attention(buf, cache, li, count, bucket, B1, N, causal=causal)
             _lib.chain_correct(buf.q_buf, buf.kv_buf, buf.src, par, buf.rec, buf.seg, segcnt,
                                B1, N, H, Hkv, hd, self.scaling, buf.o32, buf.o_bf, buf.m_tab,
                                buf.z_tab)
@@ -343,7 +368,8 @@ class FoldedVerifyEngine:
                               last, buf.final)
         return last
 
-    def _attention(self, buf: _Buffers, cache, li: int, count, bucket: int, B1: int, N: int):
+    def _attention(self, buf: _Buffers, cache, li: int, count, bucket: int, B1: int, N: int,
+                   causal: bool = False):
         pv = prefix_view(cache, li)
         if pv is None:
             P_arg, plen = 0, None
@@ -356,9 +382,11 @@ class FoldedVerifyEngine:
             pv.page_table if pv else None, P_arg, pv.page_size if pv else 1,
             pv.page_stride if pv else 0, pv.head_stride if pv else 0,
             buf.src, buf.rows, count, bucket, B1, N, self.H, self.Hkv, self.hd, self.scaling,
-            buf.o32, buf.o_bf, buf.m_tab, buf.z_tab, buf.ws_attn, prefix_len=plen)
+            buf.o32, buf.o_bf, buf.m_tab, buf.z_tab, buf.ws_attn, prefix_len=plen,
+            block_causal=causal)
 
-    def _graph_key(self, buf: _Buffers, cache, P: int, delta: float, bucket: int):
+    def _graph_key(self, buf: _Buffers, cache, P: int, delta: float, bucket: int,
+                   q_scaled: bool = False, causal: bool = False):
         if isinstance(cache, PagedKVCache):
             # the prefix length is read on the device: one graph for every length
             P = -1
@@ -370,13 +398,15 @@ class FoldedVerifyEngine:
             ck = tuple((prefix_view(cache, li).k.data_ptr(), prefix_view(cache, li).v.data_ptr())
                        if prefix_view(cache, li) is not None else (0, 0)
                        for li in range(self.L))
-        return (buf.key, id(buf), P, float(delta), bucket, self.gate_mode, ck)
+        return (buf.key, id(buf), P, float(delta), bucket, self.gate_mode, ck, q_scaled, causal)
 
     def _replay(self, buf: _Buffers, tokens: torch.Tensor, par: torch.Tensor, cache, P: int,
-                delta: float, bucket: int):
+                delta: float, bucket: int, q_scaled: bool = False, causal: bool = False):
         """Run the layers through a captured HIP graph (captured on first use for
-        this shape / prefix length / cache); inputs go through static buffers."""
-        key = self._graph_key(buf, cache, P, delta, bucket)
+        this shape / prefix length / cache); inputs go through static buffers
+        (tokens, parent map, and buf.q_scale when q_scaled)."""
+        key = self._graph_key(buf, cache, P, delta, bucket, q_scaled, causal)
+        qs = buf.q_scale if q_scaled else None
         entry = self._graphs.get(key)
         if entry is None:
             static_tok = tokens.clone()
@@ -384,11 +414,13 @@ class FoldedVerifyEngine:
             side = torch.cuda.Stream()
             side.wait_stream(torch.cuda.current_stream())
             with torch.cuda.stream(side):      # warm-up launch outside the capture
-                self._run_layers(buf, static_tok, static_par, cache, delta, bucket)
+                self._run_layers(buf, static_tok, static_par, cache, delta, bucket, q_scale=qs,
+                                 causal=causal)
             torch.cuda.current_stream().wait_stream(side)
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
-                out = self._run_layers(buf, static_tok, static_par, cache, delta, bucket)
+                out = self._run_layers(buf, static_tok, static_par, cache, delta, bucket,
+                                       q_scale=qs, causal=causal)
             entry = (graph, static_tok, static_par, out)
             while len(self._graphs) >= self.max_graphs:
                 self._graphs.pop(next(iter(self._graphs)))
@@ -467,11 +499,11 @@ class FoldedVerifyEngine:
                                   buf.ws_gemm)
 
         def final_norm():
-            _lib.residual_rmsnorm(buf.hp, buf.ffn, buf.src, self.model.model.norm.weight, B1, N, D,
+            _lib.residual_rmsnorm(buf.hp, buf.ffn, buf.src, self.base.norm.weight, B1, N, D,
                                   self.eps, scratch, normed)
 
         def lm_head():
-            torch.mm(buf.final, self.model.lm_head.weight.t(), out=logits)
+            torch.mm(buf.final, self.head.weight.t(), out=logits)
 
         out = dict(qkv=qkv, attn=attn, chain=chain, o_proj=o_proj, post_norm=post_norm,
                    gate_up=gate_up, down=down, final_norm=final_norm, lm_head=lm_head, gate=gate)

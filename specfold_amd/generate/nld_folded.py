@@ -1,0 +1,91 @@
+"""SpecFold for Nemotron-Labs-Diffusion on MI355X: the B+1-branch folded verify
+step on the NLD backbone.
+
+``SpecFoldHIPNLDGeneration`` is the drop-in for the reference's fused class
+``SpecFoldTritonNLDGeneration`` (specfold/generate/nld_folded.py:240-394): same
+constructor (``delta``, ``fold_bucket``), same ``_batched_block_forward`` seam
+returning UNSHIFTED logits [B1, N, V] (the diffusion head predicts each
+position's own token, :237), same ``fold_ratio`` and B1 == 1 dense fallback.
+The differences from the Fast-dLLM v2 step are handled by the engine: the
+decoder at ``model.encoder`` and head at ``model.diffusion_head``, no QKV bias,
+the config's RMSNorm eps, and the llama-4 q scale after RoPE (:37-53,
+173-174) — applied by the QKV kernel at every prefix length, where the Triton
+path falls back to the PyTorch reference beyond 16384 positions.
+"""
+
+from __future__ import annotations
+
+import logging
+from typing import List, Optional, Tuple
+
+import torch
+
+from specfold_amd import _lib
+from specfold_amd.engine import FoldedVerifyEngine, StepStats, build_parent_map
+from specfold_amd.generate.nld_generation import NLDDiffusionGeneration
+from specfold_amd.generate.nld_model_executor import llama4_q_scale
+from specfold_amd.kv_cache import cache_length
+
+logger = logging.getLogger(__name__)
+
+
+class SpecFoldHIPNLDGeneration(NLDDiffusionGeneration):
+    """Folded NLD verify step on the gfx950 kernels of ``specfold_amd.engine``."""
+
+    def __init__(self, *args, delta: float = 0.1, fold_bucket: Optional[int] = None,
+                 gate_mode: int = _lib.SF_GATE_MODEL_DTYPE, **kwargs):
+        super().__init__(*args, **kwargs)
+        self.delta = float(delta)
+        self.fold_bucket = None if fold_bucket is None else int(fold_bucket)
+        self.gate_mode = gate_mode
+        self._engine: Optional[FoldedVerifyEngine] = None
+        self._fold_draft_positions = 0
+        self._fold_draft_recomputed = 0
+        self.last_stats: Optional[StepStats] = None
+
+    @property
+    def fold_ratio(self) -> float:
+        tot = self._fold_draft_positions
+        return 1.0 - self._fold_draft_recomputed / tot if tot else float("nan")
+
+    @staticmethod
+    def _build_parent_map(batched_input: torch.Tensor) -> Tuple[List[Optional[int]], List[int]]:
+        return build_parent_map(batched_input)
+
+    def _pack_layer_weights(self, layers=None) -> None:
+        """Share the executor's engine (weights packed once per model)."""
+        ex = self.model_executor
+        eng = getattr(ex, "engine", None)
+        if eng is None or eng.model is not ex.model:
+            eng = FoldedVerifyEngine(ex.model, gate_mode=self.gate_mode)
+        self._engine = eng
+
+    @torch.no_grad()
+    def _batched_block_forward(self, batched_input: torch.Tensor, past_key_values) -> torch.Tensor:
+        B1, N = batched_input.shape
+        if B1 == 1:
+            return NLDDiffusionGeneration._batched_block_forward(self, batched_input,
+                                                                  past_key_values)
+        if self._engine is None:
+            self._pack_layer_weights()
+        eng = self._engine
+        bucket = B1 * N if self.fold_bucket is None else min(self.fold_bucket, B1 * N)
+        q_scale = llama4_q_scale(self.model_executor.model.config, cache_length(past_key_values),
+                                 N, eng.device)
+        stats = StepStats()
+        prev_mode, eng.gate_mode = eng.gate_mode, self.gate_mode
+        try:
+            logits = eng.forward(batched_input, past_key_values, delta=self.delta, bucket=bucket,
+                                 q_scale=q_scale, stats=stats)
+        finally:
+            eng.gate_mode = prev_mode
+        L = len(stats.counts)
+        self._fold_draft_positions += (B1 - 1) * N * L
+        self._fold_draft_recomputed += sum(stats.counts) - L * N
+        self.last_stats = stats
+        return logits
+
+
+# The reference's class names, so callers switch without code changes.
+SpecFoldTritonNLDGeneration = SpecFoldHIPNLDGeneration
+SpecFoldNLDGeneration = SpecFoldHIPNLDGeneration

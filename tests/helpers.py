@@ -8,7 +8,7 @@ from typing import List, Optional
 
 import torch
 
-from specfold_amd.generate.synthetic_model import ModelShape, build_qwen2
+from specfold_amd.generate.synthetic_model import ModelShape, build_nld, build_qwen2
 from specfold_amd.synthetic import draft_tree_block, random_prefix_kv
 
 # hd = 128 shapes the HIP kernels take; small enough for the CPU oracle
@@ -32,6 +32,24 @@ def make_case(shape: ModelShape, seed: int, N: int = 32, P: int = 100, delta: fl
     if tokens is None:
         tokens = draft_tree_block(N, shape.vocab, gen)
     kv = random_prefix_kv(shape.layers, shape.kv_heads, P, shape.head_dim, gen) if P else None
+    return Case(model, tokens, kv, delta)
+
+
+# NLD (Llama-layout) shapes: no QKV bias, eps 1e-5
+SHAPE_N4 = ModelShape(hidden=512, heads=4, kv_heads=1, layers=2, intermediate=1024, vocab=700,
+                      rms_eps=1e-5, qkv_bias=False)
+SHAPE_N8 = ModelShape(hidden=1024, heads=8, kv_heads=2, layers=2, intermediate=1536, vocab=512,
+                      rms_eps=1e-5, qkv_bias=False)
+
+
+def make_nld_case(shape: ModelShape, seed: int, N: int = 32, P: int = 100, delta: float = 0.1,
+                  omax: int = 64, dtype=torch.bfloat16) -> Case:
+    """An NLD-layout model whose llama-4 q scale is active from position ``omax`` on."""
+    model = build_nld(shape, seed, device="cpu", dtype=dtype, original_max_positions=omax)
+    gen = torch.Generator().manual_seed(seed + 91)
+    tokens = draft_tree_block(N, shape.vocab - 1, gen)
+    kv = random_prefix_kv(shape.layers, shape.kv_heads, P, shape.head_dim, gen, dtype=dtype) \
+        if P else None
     return Case(model, tokens, kv, delta)
 
 

@@ -30,10 +30,10 @@ def bf16_close(a, b, rel=2 ** -7, abs_=2 ** -7):
     return int(bad.sum()), err_stats(a, b)
 
 
-def run_pair(case, teacher=True, cache_kind="paged"):
+def run_pair(case, teacher=True, cache_kind="paged", q_scale=None):
     tr = StepTrace()
     ref_logits = folded_verify_step(case.model_cpu, case.tokens, case.kv, case.delta, trace=tr,
-                                    shift=False)
+                                    shift=False, q_scale=q_scale)
     model = to_gpu_model(case.model_cpu)
     eng = FoldedVerifyEngine(model)
     cache = None
@@ -46,7 +46,8 @@ def run_pair(case, teacher=True, cache_kind="paged"):
             cache = [(k.cuda(), v.cuda()) for k, v in case.kv]
     trace = []
     tf = {li: lt.h_in.cuda() for li, lt in enumerate(tr.layers)} if teacher else None
-    logits = eng.forward(case.tokens.cuda(), cache, case.delta, trace=trace, teacher=tf)
+    logits = eng.forward(case.tokens.cuda(), cache, case.delta, trace=trace, teacher=tf,
+                         q_scale=None if q_scale is None else q_scale.cuda())
     torch.cuda.synchronize()
     return tr, ref_logits, trace, logits
 
@@ -63,6 +64,11 @@ CASES = [
 def test_layers_teacher_forced(name, shape, seed, P, delta):
     case = make_case(shape, seed, P=P, delta=delta)
     tr, _, trace, _ = run_pair(case)
+    check_layers(case, shape, tr, trace)
+
+
+def check_layers(case, shape, tr, trace):
+    """Stage-by-stage comparison of a teacher-forced step (tolerances above)."""
     B1, N = case.tokens.shape
     H, Hkv, hd, D = shape.heads, shape.kv_heads, shape.head_dim, shape.hidden
     parent = tr.parent
@@ -110,19 +116,23 @@ def test_layers_teacher_forced(name, shape, seed, P, delta):
 
 @pytest.mark.parametrize("name,shape,seed,P,delta", CASES[:3])
 def test_end_to_end_logits(name, shape, seed, P, delta):
+    check_end_to_end(name, make_case(shape, seed, P=P, delta=delta))
+
+
+def check_end_to_end(name, case, q_scale=None):
     """No teacher forcing.  bf16 turns fp32-level differences in attention into
     1-ulp flips that every following GEMM spreads, so the reference itself,
     evaluated on the GPU instead of the CPU, lands a measurable distance from
     its CPU result.  The HIP path must be no further from the CPU oracle than
     that spread (x2), and within the absolute bound max|d| <= 2e-2*max(1, |ref|)."""
-    case = make_case(shape, seed, P=P, delta=delta)
-    tr, ref_logits, trace, logits = run_pair(case, teacher=False)
+    tr, ref_logits, trace, logits = run_pair(case, teacher=False, q_scale=q_scale)
     B1, N = case.tokens.shape
     flips = sum(int((ht["rec"].cpu().view(B1, N).bool() != lt.rec).sum())
                 for lt, ht in zip(tr.layers, trace))
     model_gpu = to_gpu_model(case.model_cpu)
     kv_gpu = [(k.cuda(), v.cuda()) for k, v in case.kv] if case.kv else None
-    ref_gpu = folded_verify_step(model_gpu, case.tokens.cuda(), kv_gpu, case.delta, shift=False)
+    ref_gpu = folded_verify_step(model_gpu, case.tokens.cuda(), kv_gpu, case.delta, shift=False,
+                                 q_scale=q_scale)
     spread = err_stats(ref_gpu.float(), ref_logits.float())
     st = err_stats(logits.float(), ref_logits.float())
     print(f"{name}: mask flips {flips}\n  hip vs oracle(cpu) {st}\n  oracle(gpu) vs oracle(cpu) {spread}")
