@@ -96,7 +96,8 @@ def kernel_roofline(name, ms, w, R, B1, N, P):
         by = 2 * BN * D * e + 2 * R * D * e + BN * 21 + R * 4
         fl = 7 * BN * D
     elif name == "qkv":
-        by = nq * D * e + nq * e + R * D * e + R * nq * e + 2 * N * hd * e
+        bias = nq * e if sh.qkv_bias else 0
+        by = nq * D * e + bias + R * D * e + R * nq * e + 2 * N * hd * e
         fl = 2 * R * D * nq
     elif name == "attn":
         by = 2 * Hkv * P * hd * e + BN * 2 * Hkv * hd * e + 2 * R * H * hd * e + 8 * R * H
@@ -187,14 +188,19 @@ def cpu_baseline(w, batched_cpu, tokens_per_step, seconds):
     all layers, plus the lm_head GEMM timed on a vocab slice and scaled."""
     from dataclasses import replace
 
-    from oracle.folded_reference import folded_layer, parent_map, rope_tables, topo_order
-    from specfold_amd.generate.synthetic_model import build_qwen2
+    from oracle.folded_reference import (decoder_parts, folded_layer, llama4_q_scale, parent_map,
+                                         rope_tables, topo_order)
+    from specfold_amd.generate.synthetic_model import build_nld, build_qwen2
     from specfold_amd.synthetic import random_prefix_kv
 
     cores = min(16, len(os.sched_getaffinity(0)))
     torch.set_num_threads(cores)
     sh = replace(w.shape, layers=1, vocab=4096)
-    model = build_qwen2(sh, w.seed, device="cpu", dtype=torch.float32)
+    if w.family == "nld":
+        model = build_nld(sh, w.seed, device="cpu", dtype=torch.float32)
+    else:
+        model = build_qwen2(sh, w.seed, device="cpu", dtype=torch.float32)
+    q_scale = llama4_q_scale(model.config, w.prefix, batched_cpu.shape[1])
     gen = torch.Generator().manual_seed(w.seed)
     kv = random_prefix_kv(1, sh.kv_heads, w.prefix, sh.head_dim, gen, dtype=torch.float32)[0]
     toks = batched_cpu % sh.vocab
@@ -203,10 +209,11 @@ def cpu_baseline(w, batched_cpu, tokens_per_step, seconds):
     hidden = torch.randn(toks.shape[0], toks.shape[1], sh.hidden, generator=gen)
     cos, sin = rope_tables(model, hidden, w.prefix, toks.shape[1])
     h = [hidden[i:i + 1] for i in range(toks.shape[0])]
-    lyr = model.model.layers[0]
+    lyr = decoder_parts(model)[0].layers[0]
 
     def one():
-        folded_layer(lyr, h, parent, order, kv, cos, sin, w.delta, sh.heads, sh.kv_heads)
+        folded_layer(lyr, h, parent, order, kv, cos, sin, w.delta, sh.heads, sh.kv_heads,
+                     q_scale=q_scale)
 
     with torch.no_grad():
         one()
@@ -235,6 +242,39 @@ def cpu_baseline(w, batched_cpu, tokens_per_step, seconds):
             "verify_step_s": round(t_step, 4)}
 
 
+def make_decoders(w):
+    """One generator per sequence of the workload (sharing one executor, so the
+    weights and packed weights exist once) and each sequence's random prompt."""
+    from specfold_amd.configs import draft_graph
+    max_len = w.prefix + w.gen_tokens
+    page_order = "shuffled" if w.shuffled_pages else "sequential"
+    graph = draft_graph(w.budget_B)
+    if w.family == "fastdllm":
+        from specfold_amd.generate import FastDLLMModelExecutor, SpecFoldHIPFastDLLMV2Generation
+        if w.batch != 1:
+            raise ValueError("the Fast-dLLM v2 generator decodes one sequence")
+        ex = FastDLLMModelExecutor.synthetic(
+            w.shape, w.seed, device="cuda", block_length=w.block, max_length=max_len + 4 * w.block,
+            page_size=w.page_size, page_order=page_order, page_seed=w.seed)
+        gens = [SpecFoldHIPFastDLLMV2Generation(
+            block_length=w.block, model_executor=ex, calibration_graph=graph,
+            threshold=w.threshold, small_block_size=w.small_block, max_new_tokens=w.gen_tokens,
+            max_length=max_len, delta=w.delta)]
+    else:
+        from specfold_amd.generate import NLDModelExecutor, SpecFoldHIPNLDGeneration
+        ex = NLDModelExecutor.synthetic(
+            w.shape, w.seed, device="cuda", block_length=w.block, max_length=max_len + 4 * w.block,
+            page_size=w.page_size, page_order=page_order, page_seed=w.seed)
+        gens = [SpecFoldHIPNLDGeneration(
+            block_length=w.block, model_executor=ex, calibration_graph=graph,
+            threshold=w.threshold, max_new_tokens=w.gen_tokens, max_length=max_len,
+            delta=w.delta) for _ in range(w.batch)]
+    g = torch.Generator().manual_seed(w.seed)
+    prompts = [torch.randint(0, w.shape.vocab - 1, (1, w.prefix), generator=g)
+               for _ in range(len(gens))]
+    return gens, prompts
+
+
 @torch.no_grad()
 def main(argv=None) -> int:
     args = parse_args(argv)
@@ -245,60 +285,56 @@ def main(argv=None) -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
-    from specfold_amd.configs import SYNTHETIC_DRAFT_GRAPH, workload
-    from specfold_amd.generate import FastDLLMModelExecutor, SpecFoldHIPFastDLLMV2Generation
+    from specfold_amd.configs import workload
 
     torch.cuda.set_device(0)
     w = workload(args.workload)
     t_build = time.time()
-    ex = FastDLLMModelExecutor.synthetic(
-        w.shape, w.seed, device="cuda", block_length=w.block,
-        max_length=w.prefix + w.gen_tokens + 4 * w.block, page_size=w.page_size,
-        page_order="shuffled" if w.shuffled_pages else "sequential", page_seed=w.seed)
-    gen = SpecFoldHIPFastDLLMV2Generation(
-        block_length=w.block, model_executor=ex, calibration_graph=SYNTHETIC_DRAFT_GRAPH,
-        threshold=w.threshold, small_block_size=w.small_block, max_new_tokens=w.gen_tokens,
-        max_length=w.prefix + w.gen_tokens, delta=w.delta)
-    g = torch.Generator().manual_seed(w.seed)
-    prompt = torch.randint(0, w.shape.vocab, (1, w.prefix), generator=g)
+    gens, prompts = make_decoders(w)
     torch.cuda.synchronize()
     build_s = time.time() - t_build
-    print(f"[bench] model + engine ready in {build_s:.1f}s", file=sys.stderr, flush=True)
+    print(f"[bench] model + engine ready in {build_s:.1f}s ({w.family}, {len(gens)} sequence(s))",
+          file=sys.stderr, flush=True)
 
-    # decode loop: prefill, W warmup steps, K timed steps
-    steps = gen.decode_steps(prompt)
+    # decode loops (one per sequence, stepped round-robin): prefill, W warmup
+    # steps, K timed steps
+    loops = [g.decode_steps(p) for g, p in zip(gens, prompts)]
     t0 = time.time()
-    ev = next(steps)
-    assert ev["kind"] == "prefill"
+    for lp in loops:
+        ev = next(lp)
+        assert ev["kind"] == "prefill"
     torch.cuda.synchronize()
     prefill_s = time.time() - t0
-    print(f"[bench] prefill {w.prefix} tokens in {prefill_s:.2f}s", file=sys.stderr, flush=True)
-    for _ in range(args.warmup):
-        next(steps)
+    print(f"[bench] prefill {len(loops)} x {w.prefix} tokens in {prefill_s:.2f}s", file=sys.stderr,
+          flush=True)
+    for i in range(args.warmup):
+        next(loops[i % len(loops)])
     kinds = {}
     committed = 0
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        ev = next(steps)
+    for i in range(args.steps):
+        ev = next(loops[i % len(loops)])
         committed += ev["committed"]
         kinds[ev["kind"]] = kinds.get(ev["kind"], 0) + 1
     torch.cuda.synchronize()
     timed_s = time.perf_counter() - t0
     tps = committed / timed_s
-    n_verify = kinds.get("verify", 0)
     print(f"[bench] {args.steps} decode steps in {timed_s:.3f}s: {committed} tokens, {kinds}",
           file=sys.stderr, flush=True)
 
-    # the verify step alone, on the last draft batch at the current prefix
+    # the verify step alone, on a B+1-branch draft batch of the last block at the
+    # current prefix of sequence 0
+    gen = gens[0]
     cache = gen._state["cache"]
-    x_t = gen._state["x_t"]
-    main_block = x_t[:, -w.block:]
+    x_cur = gen._state["x_t"] if w.family == "fastdllm" else gen._state["x_accum"]
+    main_block = x_cur[:, -w.block:]
     from specfold_amd.synthetic import TREE_DIFFS
-    batched = main_block.repeat(len(TREE_DIFFS), 1)
+    diffs = TREE_DIFFS[:w.branches]
+    batched = main_block.repeat(len(diffs), 1)
     gsel = torch.Generator().manual_seed(123)
-    repl = torch.randint(0, w.shape.vocab, (7,), generator=gsel).to(batched.device)
-    for i, d in enumerate(TREE_DIFFS):
+    repl = torch.randint(0, w.shape.vocab - 1, (7,), generator=gsel).to(batched.device)
+    for i, d in enumerate(diffs):
         for k in d:
             batched[i, k] = repl[k]
     lat = []
@@ -364,12 +400,15 @@ def main(argv=None) -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (random-init weights, random-token prompt, synthetic draft graph)",
+        "data": (f"synthetic (random-init weights, random-token prompt, synthetic draft graph; "
+                 f"{w.batch} independent sequence(s) stepped round-robin)"),
         "config": {"workload": w.name, "hidden": w.shape.hidden, "layers": w.shape.layers,
                    "heads": w.shape.heads, "kv_heads": w.shape.kv_heads,
                    "intermediate": w.shape.intermediate, "vocab": w.shape.vocab,
                    "prefix": w.prefix, "branches": w.branches, "block": w.block,
-                   "small_block": w.small_block, "delta": w.delta, "threshold": w.threshold,
+                   "small_block": w.small_block if w.family == "fastdllm" else None,
+                   "delta": w.delta, "threshold": w.threshold, "batch": w.batch,
+                   "family": w.family, "shuffled_pages": w.shuffled_pages,
                    "parallelism": "none (1 GPU)"},
         "verify_step_ms": round(verify_ms, 4),
         "verify_step_prefix": P,

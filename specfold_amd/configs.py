@@ -99,3 +99,12 @@ SYNTHETIC_DRAFT_GRAPH = {
         {"ij_set": [(0, 0), (1, 0), (4, 0), (6, 0)]},
     ]
 }
+
+
+def draft_graph(budget_B: int) -> dict:
+    """The first ``budget_B`` nodes of the synthetic draft graph (a valid tree:
+    every node's parent precedes it, <= 3 nodes per level)."""
+    nodes = SYNTHETIC_DRAFT_GRAPH["selected_nodes"]
+    if not 1 <= budget_B <= len(nodes):
+        raise ValueError(f"budget_B must be in [1, {len(nodes)}]")
+    return {"selected_nodes": [dict(n) for n in nodes[:budget_B]]}

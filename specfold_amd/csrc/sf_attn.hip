@@ -6,26 +6,28 @@
 // no mask) and the Triton kernel specfold/generate/triton_kernels.py:301-361.
 //
 // Two kernels (flash-decoding split over the prefix):
-//  * prefix: a persistent grid walks the active (query tile, 128-key prefix
-//    chunk, kv head) items; the item count follows the device-side row count and
-//    prefix length, so no workgroup is dispatched for an empty tile.  All
-//    recomputed rows x the G q-heads of one kv head are flattened to queries
+//  * prefix: a persistent grid walks the active (query tile, range of 128-key
+//    prefix chunks, kv head) items; the item count follows the device-side row
+//    count and prefix length, so no workgroup is dispatched for an empty tile.
+//    All recomputed rows x the G q-heads of one kv head are flattened to queries
 //    qi = m*G + g and tiled 64 per item (16 per wave), so each prefix K/V
 //    element is read by the few query tiles of its chunk instead of once per
-//    row.  Items of one chunk are consecutive and go to one XCD (workgroup b runs
-//    on XCD b % 8), so the chunk's later reads hit that XCD's L2.  Per item the
-//    chunk's page ids go to LDS, every K and V load of the chunk is issued at
-//    once, K is staged in LDS and all 128 scores are formed while V is still in
-//    flight; V is then written transposed.  Scores are formed transposed,
-//    S^T = K Q^T, so every lane holds keys of ONE query: the softmax is per lane
-//    and P^T feeds the P.V MFMA straight from registers (the 8 k-slots of a lane
-//    are keys {4g..4g+3} of two 16-key tiles, and V^T is read in that same
-//    order).  P is split into bf16 hi + lo halves (two MFMAs) so P.V keeps ~16
-//    mantissa bits, close to the reference's fp32 einsum.  Each item writes its
-//    (m, l, acc) partial.
+//    row.  Items of one chunk range are consecutive and go to one XCD
+//    (workgroup b runs on XCD b % 8), so the range's later reads hit that XCD's
+//    L2.  A range is one chunk while one-chunk items fill about two rounds of
+//    the grid and grows with the prefix beyond that (long contexts: fewer
+//    partials, and chunk c+1's K/V loads are in flight while chunk c is
+//    computed).  Per chunk, K is staged in LDS and V written transposed; scores
+//    are formed transposed, S^T = K Q^T, so every lane holds keys of ONE query:
+//    the softmax is per lane, rescaled across the range's chunks as in flash
+//    attention, and P^T feeds the P.V MFMA straight from registers (the 8
+//    k-slots of a lane are keys {4g..4g+3} of two 16-key tiles, and V^T is read
+//    in that same order).  P is split into bf16 hi + lo halves (two MFMAs) so
+//    P.V keeps ~16 mantissa bits, close to the reference's fp32 einsum.  Each
+//    item writes its (m, l, acc) partial.
 //  * block + merge: one 512-thread workgroup per active (recomputed row, kv
 //    head): every load (q, the branch's N block keys/values gathered through src,
-//    all chunk partials) is issued up front; block scores, the merged max, Z and
+//    all range partials) is issued up front; block scores, the merged max, Z and
 //    O follow from LDS.
 // Softmax exponentials are exp2 of scores pre-scaled by log2(e) (one v_exp_f32
 // each); partial maxima stay in that base-2 domain and the emitted m is converted
@@ -48,16 +50,40 @@ constexpr int kMaxG = 8;
 constexpr int kMaxN = 64;
 constexpr int kCUs = 256;  // MI355X compute units
 
-// One (query tile, chunk, kv head) item of the prefix pass; all 256 threads
-// take part (the LDS barriers are uniform).
+// V^T tile swizzle: keys of dim row d are stored in 4-key (8-byte) units, unit u
+// at position u ^ vt_swz(d).  The transposing writes (16 lanes per key group
+// hitting rows 8 apart) then spread over every bank, and the P.V reads (16
+// consecutive rows, one unit each) stay conflict-free: vt_swz is constant
+// across the 16 rows one read instruction touches.
+SF_DEV int vt_swz(int d) { return (d >> 3) & 14; }
+
+// Prefix chunks per work item: one while the one-chunk items fill about two
+// rounds of the resident grid, longer ranges beyond (fewer partials to write and
+// merge, and the next chunk's loads overlap this chunk's math).  A pure function
+// of device-side sizes, evaluated identically by the prefix and merge kernels.
+constexpr int kItemsTarget = 1024;
+SF_DEV int prefix_cpi(int nch, int n_qt, int Hkv) {
+  return max(1, min(nch, (nch * n_qt * Hkv) / kItemsTarget));
+}
+
+// Keys of a chunk are held in a permuted slot order: load j (0..7) of thread row
+// r = tid / 16 brings key 16j + r, which occupies slot 64(j/4) + 4r + j%4.  Every
+// load instruction then reads 16 consecutive keys (one 4 KB stretch of a page,
+// whose id is uniform: a scalar load), and the 4 keys a thread transposes into
+// V^T are 4 consecutive slots.  The softmax does not depend on key order; only
+// the mask of a partial last chunk needs the key behind a slot:
+SF_DEV int slot_key(int slot) { return 64 * (slot >> 6) + 16 * (slot & 3) + ((slot >> 2) & 15); }
+
+// One (query tile, range of prefix chunks, kv head) item of the prefix pass; all
+// 256 threads take part (the LDS barriers are uniform).  K/V of chunk c+1 are
+// loaded into registers while chunk c is scored and accumulated; the running
+// (max, sum, acc) is rescaled per chunk as in flash attention.
 SF_DEV void prefix_item(const uint16_t* __restrict__ q_buf, const uint16_t* __restrict__ pk,
                         const uint16_t* __restrict__ pv, const int32_t* __restrict__ page_table,
                         int page_size, long long page_stride, long long head_stride, int P,
                         const int32_t* __restrict__ rows, int nq, int G, int H, float scale_log2,
-                        int qmax, int nch_cap, int qt, int ci, int h, uint16_t* sK, uint16_t* sV,
-                        int* s_page, float* __restrict__ ws_o, float* __restrict__ ws_ml) {
-  const int k_begin = ci * kChunk;
-  const int nkeys = min(P - k_begin, kChunk);  // >= 1
+                        int qmax, int nch_cap, int qt, int r, int c0, int c1, int h, uint16_t* sK,
+                        uint16_t* sV, float* __restrict__ ws_o, float* __restrict__ ws_ml) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = tid >> 6;
@@ -78,129 +104,163 @@ SF_DEV void prefix_item(const uint16_t* __restrict__ q_buf, const uint16_t* __re
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds) qf[ds] = *reinterpret_cast<const sf_u32x4*>(qp + ds * 32);
   }
-  // page ids of the chunk's keys (page_size divides 128, checked on the host)
-  if (tid < kChunk) {
-    const int t = k_begin + min(tid, nkeys - 1);
-    s_page[tid] = page_table ? page_table[t / page_size] : 0;
-  }
-  __syncthreads();
 
-  auto key_ptr = [&](const uint16_t* base, int kl) -> const uint16_t* {
-    const int t = k_begin + kl;
-    if (page_table)
-      return base + (long long)s_page[kl] * page_stride + head_off +
-             (long long)(t % page_size) * kHD;
-    return base + head_off + (long long)t * kHD;
-  };
-
-  // every K and V load of the chunk (clamped to the last key, masked later):
-  // K thread->(key = (tid>>4) + 16i, seg = tid&15); V thread->(keys 64p + 4*(tid>>4)
-  // + 0..3, seg = tid&15) so 4 consecutive keys pack into one 8-byte V^T write
+  // 16-key group j of chunk ci starts at key g0 (groups past the prefix end are
+  // clamped to the last group holding keys, keys past the end to the last key);
+  // with a page size that is a multiple of 16 a group never straddles pages.
+  const int last_g0 = (P - 1) & ~15;
   const int sg = tid & 15;
   const int kr = tid >> 4;
+  auto group_page = [&](int ci, int j) -> int {
+    const int g0 = min(ci * kChunk + 16 * j, last_g0);
+    return page_table ? page_table[g0 / page_size] : 0;
+  };
   sf_u32x4 kreg[8], vreg[2][4];
+  auto load_chunk = [&](int ci, const int* pg) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
-    kreg[i] = *reinterpret_cast<const sf_u32x4*>(key_ptr(pk, min(kr + 16 * i, nkeys - 1)) + sg * 8);
-#pragma unroll
-  for (int p = 0; p < 2; ++p)
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      vreg[p][i] = *reinterpret_cast<const sf_u32x4*>(
-          key_ptr(pv, min(64 * p + 4 * kr + i, nkeys - 1)) + sg * 8);
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-    *reinterpret_cast<sf_u32x4*>(&sK[(kr + 16 * i) * kKStr + sg * 8]) = kreg[i];
-  __syncthreads();
-
-  // S^T = K Q^T for all 8 key tiles of the chunk (V loads still in flight)
-  float s[8][4];
-#pragma unroll
-  for (int kt = 0; kt < 8; ++kt) {
-    sf_f32x4 a = {0.f, 0.f, 0.f, 0.f};
-    const uint16_t* kb = &sK[(kt * 16 + ql) * kKStr + grp * 8];
-#pragma unroll
-    for (int ds = 0; ds < 4; ++ds) {
-      const sf_u32x4 kf = *reinterpret_cast<const sf_u32x4*>(kb + ds * 32);
-      a = sf_mfma16x16x32(sf_as_bf16x8(kf), sf_as_bf16x8(qf[ds]), a);
+    for (int j = 0; j < 8; ++j) {
+      const int g0 = min(ci * kChunk + 16 * j, last_g0);
+      const long long grow = page_table
+          ? (long long)pg[j] * page_stride + (long long)(g0 & (page_size - 1)) * kHD
+          : (long long)g0 * kHD;
+      const int off = min(kr, P - 1 - g0) * kHD + sg * 8;
+      kreg[j] = *reinterpret_cast<const sf_u32x4*>(pk + head_off + grow + off);
+      vreg[j >> 2][j & 3] = *reinterpret_cast<const sf_u32x4*>(pv + head_off + grow + off);
     }
-    const int key0 = kt * 16 + grp * 4;
+  };
+  int pg_next[8];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) s[kt][r] = (key0 + r < nkeys) ? a[r] * scale_log2 : -INFINITY;
+  for (int j = 0; j < 8; ++j) pg_next[j] = group_page(c0, j);
+  load_chunk(c0, pg_next);
+  if (c0 + 1 < c1) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) pg_next[j] = group_page(c0 + 1, j);
   }
 
-  // V^T: dims (2w, 2w+1) of keys (k0, k1) -> one word per dim, by byte permutes
-#pragma unroll
-  for (int p = 0; p < 2; ++p)
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const uint32_t x0 = vreg[p][0][w], x1 = vreg[p][1][w];
-      const uint32_t x2 = vreg[p][2][w], x3 = vreg[p][3][w];
-      sf_u32x2 lo, hi;
-      lo[0] = (x0 & 0xffffu) | (x1 << 16);
-      lo[1] = (x2 & 0xffffu) | (x3 << 16);
-      hi[0] = (x0 >> 16) | (x1 & 0xffff0000u);
-      hi[1] = (x2 >> 16) | (x3 & 0xffff0000u);
-      *reinterpret_cast<sf_u32x2*>(&sV[(sg * 8 + 2 * w) * kVStr + 64 * p + 4 * kr]) = lo;
-      *reinterpret_cast<sf_u32x2*>(&sV[(sg * 8 + 2 * w + 1) * kVStr + 64 * p + 4 * kr]) = hi;
-    }
-
-  // one max for the whole chunk: the 4 lanes groups of a query hold its 128 keys
-  float mx = -INFINITY;
-#pragma unroll
-  for (int kt = 0; kt < 8; ++kt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kt][r]);
-  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-  float lsum = 0.f;
-#pragma unroll
-  for (int kt = 0; kt < 8; ++kt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      s[kt][r] = __builtin_amdgcn_exp2f(s[kt][r] - mx);
-      lsum += s[kt][r];
-    }
-  lsum += __shfl_xor(lsum, 16, 64);
-  lsum += __shfl_xor(lsum, 32, 64);
-  __syncthreads();
-
+  float m_run = -INFINITY, l_run = 0.f;
   sf_f32x4 acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int c = c0; c < c1; ++c) {
+    const int nkeys = min(P - c * kChunk, kChunk);  // >= 1
+    // stage K (slot order) and V^T of chunk c (V^T: dims (2w, 2w+1) of slots
+    // 4kr + 64p .. +3 -> one word per dim, by byte permutes)
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int kt0 = 2 * j, kt1 = 2 * j + 1;
-    if (kt0 * 16 >= nkeys) break;
-    sf_u32x4 hi, lo;
+    for (int j = 0; j < 8; ++j)
+      *reinterpret_cast<sf_u32x4*>(&sK[(64 * (j >> 2) + 4 * kr + (j & 3)) * kKStr + sg * 8]) =
+          kreg[j];
 #pragma unroll
-    for (int w2 = 0; w2 < 2; ++w2) {
-      const float a0 = s[kt0][2 * w2], a1 = s[kt0][2 * w2 + 1];
-      const float b0 = s[kt1][2 * w2], b1 = s[kt1][2 * w2 + 1];
-      hi[w2] = sf_pack2(a0, a1);
-      hi[2 + w2] = sf_pack2(b0, b1);
-      lo[w2] = sf_pack2(a0 - sf_rbf(a0), a1 - sf_rbf(a1));
-      lo[2 + w2] = sf_pack2(b0 - sf_rbf(b0), b1 - sf_rbf(b1));
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t x0 = vreg[p][0][w], x1 = vreg[p][1][w];
+        const uint32_t x2 = vreg[p][2][w], x3 = vreg[p][3][w];
+        sf_u32x2 lo, hi;
+        lo[0] = (x0 & 0xffffu) | (x1 << 16);
+        lo[1] = (x2 & 0xffffu) | (x3 << 16);
+        hi[0] = (x0 >> 16) | (x1 & 0xffff0000u);
+        hi[1] = (x2 >> 16) | (x3 & 0xffff0000u);
+        const int d = sg * 8 + 2 * w;  // d and d + 1 share vt_swz
+        const int col = ((16 * p + kr) ^ vt_swz(d)) * 4;
+        *reinterpret_cast<sf_u32x2*>(&sV[d * kVStr + col]) = lo;
+        *reinterpret_cast<sf_u32x2*>(&sV[(d + 1) * kVStr + col]) = hi;
+      }
+    __syncthreads();
+    if (c + 1 < c1) {
+      load_chunk(c + 1, pg_next);
+      if (c + 2 < c1) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pg_next[j] = group_page(c + 2, j);
+      }
     }
-    const sf_bf16x8 bhi = sf_as_bf16x8(hi);
-    const sf_bf16x8 blo = sf_as_bf16x8(lo);
+
+    // S^T = K Q^T (raw dot products) for the 8 slot tiles of the chunk
+    float s[8][4];
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const uint16_t* vrow = &sV[(dt * 16 + ql) * kVStr + grp * 4];
-      const sf_u32x2 a0 = *reinterpret_cast<const sf_u32x2*>(vrow + kt0 * 16);
-      const sf_u32x2 a1 = *reinterpret_cast<const sf_u32x2*>(vrow + kt1 * 16);
-      const sf_u32x4 vf = {a0[0], a0[1], a1[0], a1[1]};
-      const sf_bf16x8 va = sf_as_bf16x8(vf);
-      acc[dt] = sf_mfma16x16x32(va, bhi, acc[dt]);
-      acc[dt] = sf_mfma16x16x32(va, blo, acc[dt]);
+    for (int kt = 0; kt < 8; ++kt) {
+      sf_f32x4 a = {0.f, 0.f, 0.f, 0.f};
+      const uint16_t* kb = &sK[(kt * 16 + ql) * kKStr + grp * 8];
+#pragma unroll
+      for (int ds = 0; ds < 4; ++ds) {
+        const sf_u32x4 kf = *reinterpret_cast<const sf_u32x4*>(kb + ds * 32);
+        a = sf_mfma16x16x32(sf_as_bf16x8(kf), sf_as_bf16x8(qf[ds]), a);
+      }
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) s[kt][rr] = a[rr];
     }
+    if (nkeys < kChunk) {  // uniform: only a partial last chunk
+#pragma unroll
+      for (int kt = 0; kt < 8; ++kt)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+          if (slot_key(kt * 16 + grp * 4 + rr) >= nkeys) s[kt][rr] = -INFINITY;
+    }
+
+    // the 4 lane groups of a query hold its 128 keys; the max is taken on the raw
+    // dot products (the scale is positive) and probabilities are
+    // exp2(s * scale_log2 - m) with m in the scaled base-2 domain
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) mx = fmaxf(mx, s[kt][rr]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx * scale_log2);
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first chunk
+    float lsum = 0.f;
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        s[kt][rr] = __builtin_amdgcn_exp2f(fmaf(s[kt][rr], scale_log2, -m_new));
+        lsum += s[kt][rr];
+      }
+    lsum += __shfl_xor(lsum, 16, 64);
+    lsum += __shfl_xor(lsum, 32, 64);
+    l_run = l_run * alpha + lsum;
+    m_run = m_new;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = acc[i] * alpha;
+
+    // acc += V^T P^T; P split into bf16 hi + lo
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int kt0 = 2 * j, kt1 = 2 * j + 1;
+      sf_u32x4 hi, lo;
+#pragma unroll
+      for (int w2 = 0; w2 < 2; ++w2) {
+        const float a0 = s[kt0][2 * w2], a1 = s[kt0][2 * w2 + 1];
+        const float b0 = s[kt1][2 * w2], b1 = s[kt1][2 * w2 + 1];
+        hi[w2] = sf_pack2(a0, a1);
+        hi[2 + w2] = sf_pack2(b0, b1);
+        lo[w2] = sf_pack2(a0 - sf_rbf(a0), a1 - sf_rbf(a1));
+        lo[2 + w2] = sf_pack2(b0 - sf_rbf(b0), b1 - sf_rbf(b1));
+      }
+      const sf_bf16x8 bhi = sf_as_bf16x8(hi);
+      const sf_bf16x8 blo = sf_as_bf16x8(lo);
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const int d = dt * 16 + ql;
+        const uint16_t* vrow = &sV[d * kVStr];
+        const int sw = vt_swz(d);
+        const sf_u32x2 a0 = *reinterpret_cast<const sf_u32x2*>(vrow + ((4 * kt0 + grp) ^ sw) * 4);
+        const sf_u32x2 a1 = *reinterpret_cast<const sf_u32x2*>(vrow + ((4 * kt1 + grp) ^ sw) * 4);
+        const sf_u32x4 vf = {a0[0], a0[1], a1[0], a1[1]};
+        const sf_bf16x8 va = sf_as_bf16x8(vf);
+        acc[dt] = sf_mfma16x16x32(va, bhi, acc[dt]);
+        acc[dt] = sf_mfma16x16x32(va, blo, acc[dt]);
+      }
+    }
+    __syncthreads();  // sK / sV are rewritten by the next chunk
   }
 
   if (qvalid) {
-    const size_t slot = ((size_t)h * nch_cap + ci) * qmax + qi;
+    const size_t slot = ((size_t)h * nch_cap + r) * qmax + qi;
     if (grp == 0) {
-      ws_ml[slot * 2] = mx;
-      ws_ml[slot * 2 + 1] = lsum;
+      ws_ml[slot * 2] = m_run;
+      ws_ml[slot * 2 + 1] = l_run;
     }
     float* op = ws_o + slot * kHD + grp * 4;
 #pragma unroll
@@ -210,8 +270,9 @@ SF_DEV void prefix_item(const uint16_t* __restrict__ q_buf, const uint16_t* __re
 
 // gridDim.x is a multiple of 8; XCD x (workgroups b with b % 8 == x) takes the
 // x-th eighth of the item list, so consecutive items (the query tiles of one
-// chunk) share an L2.
-__global__ __launch_bounds__(256) void sf_attn_prefix_kernel(
+// chunk range) share an L2.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+sf_attn_prefix_kernel(
     const uint16_t* __restrict__ q_buf, const uint16_t* __restrict__ pk,
     const uint16_t* __restrict__ pv, const int32_t* __restrict__ page_table, int page_size,
     long long page_stride, long long head_stride, const int32_t* __restrict__ p_len, int P_cap,
@@ -220,13 +281,15 @@ __global__ __launch_bounds__(256) void sf_attn_prefix_kernel(
     float* __restrict__ ws_ml) {
   __shared__ __attribute__((aligned(16))) uint16_t sK[kChunk * kKStr];
   __shared__ __attribute__((aligned(16))) uint16_t sV[kHD * kVStr];
-  __shared__ int s_page[kChunk];
   const int G = H / Hkv;
   const int P = p_len ? min(*p_len, P_cap) : P_cap;
+  if (P <= 0) return;
   const int nq = min(*count_p, bucket) * G;
   const int n_qt = (nq + kQT - 1) / kQT;
   const int nch = (P + kChunk - 1) / kChunk;
-  const int items = n_qt * nch * Hkv;
+  const int cpi = prefix_cpi(nch, n_qt, Hkv);
+  const int nr = (nch + cpi - 1) / cpi;
+  const int items = n_qt * nr * Hkv;
   const int xcd = blockIdx.x & 7;
   const int per = gridDim.x >> 3;
   const int end = (int)(((long long)items * (xcd + 1)) >> 3);
@@ -234,10 +297,11 @@ __global__ __launch_bounds__(256) void sf_attn_prefix_kernel(
        it += per) {
     const int qt = it % n_qt;
     const int rest = it / n_qt;
-    const int ci = rest % nch;
-    const int h = rest / nch;
+    const int r = rest % nr;
+    const int h = rest / nr;
+    const int c0 = r * cpi;
     prefix_item(q_buf, pk, pv, page_table, page_size, page_stride, head_stride, P, rows, nq, G, H,
-                scale_log2, qmax, nch_cap, qt, ci, h, sK, sV, s_page, ws_o, ws_ml);
+                scale_log2, qmax, nch_cap, qt, r, c0, min(nch, c0 + cpi), h, sK, sV, ws_o, ws_ml);
     __syncthreads();  // LDS is reused by the next item
   }
 }
@@ -397,7 +461,11 @@ __global__ __launch_bounds__(512) void sf_attn_block_merge_kernel(
   const int count = min(*count_p, bucket);
   const int G = H / Hkv;
   const int P = p_len ? min(*p_len, P_cap) : P_cap;
-  const int nch = min((P + kChunk - 1) / kChunk, nchunks_cap);
+  // number of prefix partials per query: the prefix kernel's chunk ranges
+  const int nch_all = min((P + kChunk - 1) / kChunk, nchunks_cap);
+  const int n_qt = (count * G + kQT - 1) / kQT;
+  const int cpi = nch_all > 0 ? prefix_cpi(nch_all, n_qt, Hkv) : 1;
+  const int nch = (nch_all + cpi - 1) / cpi;
   for (int it = blockIdx.x; it < count * Hkv; it += gridDim.x) {
     merge_item(q_buf, kv_buf, src, rows, it / Hkv, it % Hkv, N, H, Hkv, G, scale_log2, causal, nch,
                nchunks_cap, qmax, ws_o, ws_ml, o32, o_bf, m_tab, z_tab, sq, sk, sv, ss, sml, sM,
@@ -435,7 +503,8 @@ extern "C" int sf_attn_prefix_block(const uint16_t* q_buf, const uint16_t* kv_bu
   if (P < 0 || nchunks_for(P) > kMaxChunks) return SF_ERR_SHAPE;
   if (P > 0) {
     if (!prefix_k || !prefix_v || !workspace) return SF_ERR_ARG;
-    if (page_table && (page_size < 1 || kChunk % page_size != 0)) return SF_ERR_SHAPE;
+    // a page holds whole 16-key groups and a chunk whole pages: 16, 32, 64 or 128
+    if (page_table && (page_size < 16 || kChunk % page_size != 0)) return SF_ERR_SHAPE;
     if (!page_table && head_stride < (long long)P * kHD) return SF_ERR_SHAPE;
     if (workspace_bytes < sf_attn_workspace_bytes(bucket, H, P)) return SF_ERR_WORKSPACE;
   }

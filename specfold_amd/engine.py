@@ -175,9 +175,10 @@ class FoldedVerifyEngine:
                                      _lib.pack_weight(m.down_proj.weight.contiguous())))
         self._bufs: Dict[Tuple[int, int, int], _Buffers] = {}
         # HIP graphs of the layer loop, keyed by shape / prefix / delta / cache
-        # (one per branch count the decode loop visits: B1 = 1..8 plus block commits)
+        # (one per branch count the decode loop visits, B1 = 1..8, per sequence's
+        # cache: several sequences decoded in turn each keep their own set)
         self.use_graphs = True
-        self.max_graphs = 16
+        self.max_graphs = 48
         self._graphs: Dict[tuple, tuple] = {}
         self._rope: Optional[Tuple[torch.Tensor, torch.Tensor]] = None
 
