@@ -226,6 +226,31 @@ int sf_residual_gather_add(const uint16_t* hp, const uint16_t* ffn, const int32_
 int sf_lm_head(const uint16_t* x, int M, const uint16_t* w, int D, int V, uint16_t* logits,
                void* stream);
 
+/* ---- greedy decoding statistics of logits rows ----------------------------------
+ * Replaces, at temperature 0, the top-p sampler of the reference decode loop
+ * (specfold/generate/fastdllm_model_executor.py:109-155: sort, softmax, cumsum,
+ * scatter, softmax, argmax; called from fastdllm_v2_generation.py:646-676) and the
+ * softmax/topk calls of its draft construction (fastdllm_v2_generation.py:430-470,
+ * nld_generation.py:105-151; nld transfer: modeling_nemotron_labs_diffusion.py:
+ * 835-861).  For each of the M rows of bf16 logits (row stride ld elements), with
+ * e_i = exp(l_i - l_max) (fp32) and Z = sum e_i:
+ *   top_idx/top_val [M, 8]  the 8 largest logits, value descending then index
+ *                           ascending (top_idx[m*8] is torch.argmax's token)
+ *   zfull [M]   Z;   conf_full [M] = bf16(1/Z) (the bf16 softmax maximum)
+ *   znuc  [M]   the top-p nucleus mass: e summed in descending order up to and
+ *               including the first token that carries it past top_p * Z
+ *   greedy_tok [M], conf [M]   the argmax of the bf16 nucleus probabilities
+ *               bf16(e_i / znuc) (lowest index among equal) and bf16(1/znuc)
+ * workspace: sf_logit_stats_workspace_bytes(M) bytes, zero before the first call
+ * (every call leaves it zero).  Limits: V % 8 == 0, ld % 8 == 0, 16-byte aligned
+ * logits, 0 < top_p (top_p >= 1 keeps every token).
+ */
+size_t sf_logit_stats_workspace_bytes(int M);
+int sf_logit_stats(const uint16_t* logits, int M, int V, long long ld, float top_p,
+                   int32_t* top_idx, float* top_val, float* zfull, float* znuc,
+                   int32_t* greedy_tok, float* conf, float* conf_full, void* workspace,
+                   size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -56,6 +56,8 @@ SIGNATURES = {
     "sf_ffn_down_scatter": (_i, [_vp, _vp, _i, _vp, _vp, _i, _i, _vp, _vp, _sz, _vp]),
     "sf_residual_gather_add": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _vp]),
     "sf_lm_head": (_i, [_vp, _i, _vp, _i, _i, _vp, _vp]),
+    "sf_logit_stats_workspace_bytes": (ctypes.c_size_t, [_i]),
+    "sf_logit_stats": (_i, [_vp, _i, _i, _ll, _f] + [_vp] * 7 + [_vp, ctypes.c_size_t, _vp]),
 }
 
 
@@ -391,3 +393,50 @@ def lm_head(x, M, w, D, V, logits, stream=None) -> None:
     _need(logits, "logits", torch.bfloat16, min_numel=M * V)
     st = load().sf_lm_head(_ptr(x), M, _ptr(w), D, V, _ptr(logits), _stream(stream))
     _check(st, "sf_lm_head")
+
+
+class LogitStats:
+    """Per-row greedy decoding statistics (see ``logit_stats``)."""
+
+    __slots__ = ("top_idx", "top_val", "zfull", "znuc", "greedy_tok", "conf", "conf_full")
+
+    def __init__(self, M: int, device):
+        self.top_idx = torch.empty(M, 8, dtype=torch.int32, device=device)
+        self.top_val = torch.empty(M, 8, dtype=torch.float32, device=device)
+        self.zfull = torch.empty(M, dtype=torch.float32, device=device)
+        self.znuc = torch.empty(M, dtype=torch.float32, device=device)
+        self.greedy_tok = torch.empty(M, dtype=torch.int32, device=device)
+        self.conf = torch.empty(M, dtype=torch.float32, device=device)
+        self.conf_full = torch.empty(M, dtype=torch.float32, device=device)
+
+
+_STATS_WS: dict = {}
+
+
+def logit_stats(logits: torch.Tensor, top_p: float = 0.95, stream=None) -> LogitStats:
+    """Greedy statistics of the rows of ``logits`` ([..., V] bf16, rows contiguous
+    along V): top-8 tokens, softmax / nucleus normalisers, greedy token and its
+    bf16 probability (sf_logit_stats)."""
+    if logits.dtype != torch.bfloat16 or not logits.is_cuda:
+        raise TypeError("logits must be a bf16 CUDA tensor")
+    V = logits.shape[-1]
+    x = logits.reshape(-1, V)
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    M, ld = x.shape[0], x.stride(0)
+    if ld % 8 or x.data_ptr() % 16:
+        x = x.contiguous()
+        ld = x.stride(0)
+    need = int(load().sf_logit_stats_workspace_bytes(M))
+    key = (x.device.index, M)
+    ws = _STATS_WS.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.zeros(need, dtype=torch.uint8, device=x.device)  # kept zero by every call
+        _STATS_WS[key] = ws
+    out = LogitStats(M, x.device)
+    st = load().sf_logit_stats(_ptr(x), M, V, ld, float(top_p), _ptr(out.top_idx),
+                               _ptr(out.top_val), _ptr(out.zfull), _ptr(out.znuc),
+                               _ptr(out.greedy_tok), _ptr(out.conf), _ptr(out.conf_full),
+                               _ptr(ws), ws.numel(), _stream(stream))
+    _check(st, "sf_logit_stats")
+    return out

@@ -1,0 +1,364 @@
+// Per-position statistics of logits rows for greedy decoding: the top-8 tokens,
+// the softmax normaliser, the top-p (nucleus) normaliser and the greedy token
+// with its bf16 probability.  They replace the sort, softmax, cumulative-sum and
+// scatter sequence of the reference's top-p sampler
+// (specfold/generate/fastdllm_model_executor.py:129-155) and the softmax + topk
+// calls of its draft construction (fastdllm_v2_generation.py:430-470,
+// nld_generation.py:105-151) at temperature 0.
+//
+// Semantics, with e_i = exp(l_i - l_max) in fp32 and Z = sum_i e_i:
+//  * top-8: (index, logit) ordered by logit descending, then index ascending.
+//  * nucleus: with p_i = bf16(e_i / Z) (the bf16 softmax) in descending order,
+//    keep every token up to and including the first one whose cumulative sum,
+//    rounded to bf16, exceeds top_p (the reference keeps a sorted token while
+//    bf16(cumsum of the probabilities before it) <= top_p); Zn = sum of e over the
+//    kept tokens.  Tokens of equal value are interchangeable, so Zn depends only
+//    on how many tied tokens at the cut are kept, not on which.
+//  * greedy token: the reference's argmax over the bf16 nucleus probabilities
+//    bf16(e_i / Zn): the lowest index whose bf16 probability equals the maximum,
+//    bf16(1 / Zn) (near-equal logits can round to the same bf16 probability).
+//  * conf = bf16(1 / Zn) (the greedy token's probability), conf_full =
+//    bf16(1 / Z) (the maximum of the bf16 softmax).
+//
+// Two kernels.  Slice: many workgroups per row count every token into a
+// 65536-bin histogram of its bf16 bit pattern (integer atomics) and reduce their
+// slice's top-8.  Finish: one workgroup per row merges the slice candidates and
+// walks the histogram in descending value order: masses are count(v) * e(v) and
+// count(v) * p(v), summed in a fixed order (deterministic), which gives Z, the
+// cut and Zn from exact counts; it then clears the histogram for the next call.
+#include <math.h>
+
+#include "sf_common.h"
+
+namespace {
+
+constexpr int kTop = 8;
+constexpr int kSliceThreads = 256;
+constexpr int kFinishThreads = 1024;
+constexpr int kKeys = 65536;
+constexpr int kMaxSlices = 64;
+
+// order key of a bf16 bit pattern: larger value -> larger key
+SF_DEV uint32_t bf16_key(uint32_t b) { return (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u); }
+SF_DEV float key_value(uint32_t k) {
+  const uint32_t b = (k & 0x8000u) ? (k & 0x7fffu) : (~k & 0xffffu);
+  return __uint_as_float(b << 16);
+}
+
+// (value desc, index asc)
+SF_DEV bool better(float v, int i, float w, int j) { return v > w || (v == w && i < j); }
+
+// Block-wide best of one candidate per thread; every thread gets the winner.
+template <int NT>
+SF_DEV void block_best(float& v, int& i, float* s_v, int* s_i) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float w = __shfl_xor(v, o, 64);
+    const int j = __shfl_xor(i, o, 64);
+    if (better(w, j, v, i)) {
+      v = w;
+      i = j;
+    }
+  }
+  if ((threadIdx.x & 63) == 0) {
+    s_v[threadIdx.x >> 6] = v;
+    s_i[threadIdx.x >> 6] = i;
+  }
+  __syncthreads();
+  v = s_v[0];
+  i = s_i[0];
+#pragma unroll
+  for (int w = 1; w < NT / 64; ++w)
+    if (better(s_v[w], s_i[w], v, i)) {
+      v = s_v[w];
+      i = s_i[w];
+    }
+  __syncthreads();
+}
+
+// Top-8 of a block from per-thread lists (8 rounds, each removing the winner).
+template <int NT>
+SF_DEV void block_top8(float (&tv)[kTop], int (&ti)[kTop], float (&bv)[kTop], int (&bi)[kTop],
+                       float* s_v, int* s_i) {
+#pragma unroll
+  for (int r = 0; r < kTop; ++r) {
+    float v = -INFINITY;
+    int i = 0x7fffffff;
+#pragma unroll
+    for (int k = 0; k < kTop; ++k)
+      if (better(tv[k], ti[k], v, i)) {
+        v = tv[k];
+        i = ti[k];
+      }
+    block_best<NT>(v, i, s_v, s_i);
+    bv[r] = v;
+    bi[r] = i;
+#pragma unroll
+    for (int k = 0; k < kTop; ++k)
+      if (ti[k] == i) {
+        tv[k] = -INFINITY;
+        ti[k] = 0x7fffffff;
+      }
+  }
+}
+
+// grid (S, M): slice s of row m counts its tokens into hist[m] and writes its top-8
+__global__ __launch_bounds__(kSliceThreads) void sf_logit_slice_kernel(
+    const uint16_t* __restrict__ logits, long long ld, int V, uint32_t* __restrict__ hist,
+    float* __restrict__ cand_v, int32_t* __restrict__ cand_i) {
+  __shared__ float s_v[kSliceThreads / 64];
+  __shared__ int s_i[kSliceThreads / 64];
+  const int S = gridDim.x, s = blockIdx.x, row = blockIdx.y;
+  const uint16_t* x = logits + (long long)row * ld;
+  uint32_t* h = hist + (size_t)row * kKeys;
+  const int nvec = V >> 3;
+  const int v0 = (int)((long long)nvec * s / S), v1 = (int)((long long)nvec * (s + 1) / S);
+  float tv[kTop];
+  int ti[kTop];
+#pragma unroll
+  for (int k = 0; k < kTop; ++k) {
+    tv[k] = -INFINITY;
+    ti[k] = 0x7fffffff;
+  }
+  float tmin = -INFINITY;
+  int kmin = 0;
+  for (int vi = v0 + threadIdx.x; vi < v1; vi += kSliceThreads) {
+    const sf_u32x4 w = *reinterpret_cast<const sf_u32x4*>(x + (size_t)vi * 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t bits = (e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xffffu);
+      atomicAdd(&h[bf16_key(bits)], 1u);
+      const float f = __uint_as_float(bits << 16);
+      const int idx = vi * 8 + e;
+      // indices ascend within a thread: a strict comparison keeps the lowest index
+      // among equal values (an empty slot, index INT_MAX, always loses)
+      if (better(f, idx, tmin, ti[kmin])) {
+#pragma unroll
+        for (int k = 0; k < kTop; ++k)
+          if (k == kmin) {
+            tv[k] = f;
+            ti[k] = idx;
+          }
+        tmin = tv[0];
+        kmin = 0;
+#pragma unroll
+        for (int k = 1; k < kTop; ++k)
+          if (better(tmin, ti[kmin], tv[k], ti[k])) {
+            tmin = tv[k];
+            kmin = k;
+          }
+      }
+    }
+  }
+  float bv[kTop];
+  int bi[kTop];
+  block_top8<kSliceThreads>(tv, ti, bv, bi, s_v, s_i);
+  if (threadIdx.x == 0) {
+    const size_t o = ((size_t)row * S + s) * kTop;
+#pragma unroll
+    for (int r = 0; r < kTop; ++r) {
+      cand_v[o + r] = bv[r];
+      cand_i[o + r] = bi[r];
+    }
+  }
+}
+
+// one workgroup per row
+__global__ __launch_bounds__(kFinishThreads) void sf_logit_finish_kernel(
+    const uint16_t* __restrict__ logits, long long ld, int V, int S, float top_p,
+    uint32_t* __restrict__ hist, const float* __restrict__ cand_v,
+    const int32_t* __restrict__ cand_i, int32_t* __restrict__ top_idx,
+    float* __restrict__ top_val, float* __restrict__ zfull, float* __restrict__ znuc,
+    int32_t* __restrict__ greedy_tok, float* __restrict__ conf, float* __restrict__ conf_full) {
+  __shared__ float s_v[kFinishThreads / 64];
+  __shared__ int s_i[kFinishThreads / 64];
+  __shared__ float s_part[kFinishThreads];
+  __shared__ float s_cutf[2];  // Z, Zn
+  const int tid = threadIdx.x, row = blockIdx.x;
+  uint32_t* h = hist + (size_t)row * kKeys;
+
+  // ---- merge the slices' top-8 lists (at most 64 x 8 = 512 candidates) -------------
+  float tv[kTop];
+  int ti[kTop];
+#pragma unroll
+  for (int k = 0; k < kTop; ++k) {
+    const int c = tid * kTop + k;
+    const bool ok = tid < S;  // thread t takes slice t's list
+    tv[k] = ok ? cand_v[(size_t)row * S * kTop + c] : -INFINITY;
+    ti[k] = ok ? cand_i[(size_t)row * S * kTop + c] : 0x7fffffff;
+  }
+  float bv[kTop];
+  int bi[kTop];
+  block_top8<kFinishThreads>(tv, ti, bv, bi, s_v, s_i);
+  const float lmax = bv[0];
+
+  // ---- histogram walk: thread t owns keys 65535 - 64t - j, j = 0..63 (descending) --
+  // Two sums per stretch, each taken from the stretch's highest key down: the
+  // softmax mass (e = exp(v - l_max)) and, once Z is known, the bf16 probability
+  // mass the reference accumulates (p = bf16(e / Z): softmax of bf16 logits).
+  const int kb = kKeys - 1 - 64 * tid;
+  const sf_u32x4* hv = reinterpret_cast<const sf_u32x4*>(h + kb - 63);
+  // sum over the stretch, highest key first, of count * f(value)
+  auto stretch_sum = [&](auto f) {
+    float acc = 0.f;
+#pragma unroll
+    for (int q = 15; q >= 0; --q) {
+      const sf_u32x4 w = hv[q];
+#pragma unroll
+      for (int r = 3; r >= 0; --r)
+        if (w[r]) acc += (float)w[r] * f(key_value(kb - 63 + 4 * q + r));
+    }
+    return acc;
+  };
+  const float part = stretch_sum([&](float v) { return expf(v - lmax); });
+  s_part[tid] = part;
+  __syncthreads();
+  // sequential prefix over the stretches (fixed order; Z is its total)
+  if (tid == 0) {
+    float cum = 0.f;
+    for (int t = 0; t < kFinishThreads; ++t) {
+      const float before = cum;
+      cum += s_part[t];
+      s_part[t] = before;
+    }
+    s_cutf[0] = cum;
+  }
+  __syncthreads();
+  const float z = s_cutf[0];
+  const float excl_e = s_part[tid];
+  const float part_p = stretch_sum([&](float v) { return sf_rbf(expf(v - lmax) / z); });
+  __syncthreads();
+  s_part[tid] = part_p;
+  __syncthreads();
+  if (tid == 0) {
+    float cum = 0.f;
+    for (int t = 0; t < kFinishThreads; ++t) {
+      const float before = cum;
+      cum += s_part[t];
+      s_part[t] = before;
+    }
+    s_cutf[1] = z;  // the nucleus mass when nothing is cut
+  }
+  __syncthreads();
+  // The reference drops sorted token i >= 1 when bf16(cumsum_{j<i} p_j) > top_p:
+  // the kept tokens run up to and including the first one whose cumulative
+  // probability crosses.  Exactly one stretch holds the crossing (monotone sums).
+  auto crosses = [&](float cum) { return sf_rbf(cum) > top_p; };
+  const float excl_p = s_part[tid];
+  const float incl_p = tid + 1 < kFinishThreads ? s_part[tid + 1] : excl_p + part_p;
+  if (!crosses(excl_p) && crosses(incl_p)) {
+    float cp = excl_p, ce = excl_e;
+    float zc = -1.f;
+    for (int j = 0; j < 64 && zc < 0.f; ++j) {
+      const uint32_t c = h[kb - j];
+      if (!c) continue;
+      const float e = expf(key_value(kb - j) - lmax);
+      const float pj = sf_rbf(e / z);
+      if (crosses(cp + (float)c * pj)) {
+        // fewest tokens of this value whose cumulative probability crosses
+        uint32_t lo = 1, hi = c;
+        while (lo < hi) {
+          const uint32_t mid = (lo + hi) >> 1;
+          if (crosses(cp + (float)mid * pj)) hi = mid; else lo = mid + 1;
+        }
+        zc = ce + (float)lo * e;
+      }
+      cp += (float)c * pj;
+      ce += (float)c * e;
+    }
+    if (zc < 0.f) zc = ce;  // rounding kept the crossing out of reach: whole stretch
+    s_cutf[1] = zc;
+  }
+  __syncthreads();
+  const float zn = s_cutf[1];
+
+  // ---- greedy token: lowest index whose bf16 probability equals the maximum -------
+  const float cmax = sf_rbf(1.0f / zn);
+  int g = 0x7fffffff;
+  bool all_tied = true;
+#pragma unroll
+  for (int r = 0; r < kTop; ++r) {
+    const bool tied = bv[r] > -INFINITY && sf_rbf(expf(bv[r] - lmax) / zn) == cmax;
+    if (tied) g = min(g, bi[r]);
+    all_tied = all_tied && tied;
+  }
+  if (all_tied) {
+    // more than 8 tokens may share the maximum probability: every token whose
+    // value is at least the smallest tied value is tied; scan the row
+    // (probabilities are monotone in the logit)
+    const float lo = bv[kTop - 1];
+    float vmin = lo;
+    for (uint32_t k = bf16_key(__float_as_uint(lo) >> 16); k > 0; --k) {
+      const float v = key_value(k - 1);
+      if (sf_rbf(expf(v - lmax) / zn) != cmax) break;
+      vmin = v;
+    }
+    const uint16_t* x = logits + (long long)row * ld;
+    int gi = 0x7fffffff;
+    for (int vi = tid; vi < (V >> 3); vi += kFinishThreads) {
+      const sf_u32x4 w = *reinterpret_cast<const sf_u32x4*>(x + (size_t)vi * 8);
+      float f[8];
+      sf_unpack8(w, f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (f[e] >= vmin) gi = min(gi, vi * 8 + e);
+    }
+    float dummy = 0.f;
+    block_best<kFinishThreads>(dummy, gi, s_v, s_i);
+    g = gi;
+  }
+
+  // ---- outputs; clear this row's histogram for the next call ---------------------
+  if (tid == 0) {
+#pragma unroll
+    for (int r = 0; r < kTop; ++r) {
+      top_idx[row * kTop + r] = bi[r];
+      top_val[row * kTop + r] = bv[r];
+    }
+    zfull[row] = z;
+    znuc[row] = zn;
+    greedy_tok[row] = g;
+    conf[row] = cmax;
+    conf_full[row] = sf_rbf(1.0f / z);
+  }
+  {
+    sf_u32x4* hv = reinterpret_cast<sf_u32x4*>(h + kb - 63);
+#pragma unroll
+    for (int q = 0; q < 16; ++q) hv[q] = sf_u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
+int slices_for(int M) { return max(1, min(kMaxSlices, 512 / M)); }
+
+}  // namespace
+
+extern "C" size_t sf_logit_stats_workspace_bytes(int M) {
+  if (M < 1) return 0;
+  const int S = slices_for(M);
+  return (size_t)M * kKeys * 4 + (size_t)M * S * kTop * 8;
+}
+
+extern "C" int sf_logit_stats(const uint16_t* logits, int M, int V, long long ld, float top_p,
+                              int32_t* top_idx, float* top_val, float* zfull, float* znuc,
+                              int32_t* greedy_tok, float* conf, float* conf_full, void* workspace,
+                              size_t workspace_bytes, void* stream) {
+  if (!logits || !top_idx || !top_val || !zfull || !znuc || !greedy_tok || !conf || !conf_full ||
+      !workspace)
+    return SF_ERR_ARG;
+  if (M < 1 || V < kTop || V % 8 != 0 || ld < V || ld % 8 != 0) return SF_ERR_SHAPE;
+  if (reinterpret_cast<uintptr_t>(logits) % 16 != 0 ||
+      reinterpret_cast<uintptr_t>(workspace) % 16 != 0 || !(top_p > 0.0f))
+    return SF_ERR_ARG;
+  if (workspace_bytes < sf_logit_stats_workspace_bytes(M)) return SF_ERR_WORKSPACE;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int S = slices_for(M);
+  uint32_t* hist = reinterpret_cast<uint32_t*>(workspace);
+  float* cand_v = reinterpret_cast<float*>(hist + (size_t)M * kKeys);
+  int32_t* cand_i = reinterpret_cast<int32_t*>(cand_v + (size_t)M * S * kTop);
+  hipLaunchKernelGGL(sf_logit_slice_kernel, dim3(S, M), dim3(kSliceThreads), 0, st, logits, ld, V,
+                     hist, cand_v, cand_i);
+  hipLaunchKernelGGL(sf_logit_finish_kernel, dim3(M), dim3(kFinishThreads), 0, st, logits, ld, V,
+                     S, top_p, hist, cand_v, cand_i, top_idx, top_val, zfull, znuc, greedy_tok,
+                     conf, conf_full);
+  return sf_launch_status();
+}

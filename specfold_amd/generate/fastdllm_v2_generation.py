@@ -18,6 +18,8 @@ from typing import Dict, List, Optional, Tuple
 
 import torch
 
+from specfold_amd.generate import greedy
+
 logger = logging.getLogger(__name__)
 
 
@@ -67,6 +69,20 @@ class FastDLLMV2SpeculativeGeneration:
     def _sample_with_top_p(self, logits, top_p: float = 0.95, temperature: float = 0.0):
         return self.model_executor.sample_with_top_p(logits, top_p=top_p, temperature=temperature)
 
+    def _sample_rows(self, logits: torch.Tensor):
+        """Sampled tokens and their probabilities for logits [1, n, V] ->
+        (x_1 [1, n], conf [1, n], statistics or None).  At temperature 0 on the GPU
+        both come from one pass of sf_logit_stats (whose statistics the draft
+        construction reuses); otherwise from the top-p sampler and a gather
+        (:646-656)."""
+        if greedy.usable(logits, self.temperature):
+            st = greedy.stats(logits[0], self.top_p)
+            x_1, conf = greedy.top_p_greedy(st)
+            return x_1, conf, st
+        x_1, p_1t = self._sample_with_top_p(logits, top_p=self.top_p,
+                                            temperature=self.temperature)
+        return x_1, torch.gather(p_1t, -1, x_1.unsqueeze(-1)).squeeze(-1), None
+
     def _prepare_prompt_text(self, prompt: str) -> str:
         if self.prompt_render_mode == "preformatted_text":
             if not isinstance(prompt, str):
@@ -94,12 +110,16 @@ class FastDLLMV2SpeculativeGeneration:
     def get_draft_blocks(self, x: torch.Tensor, p: torch.Tensor,
                          mask_index: Optional[torch.Tensor] = None, start_pos=None, end_pos=None,
                          small_block_start: Optional[int] = None,
-                         small_block_end: Optional[int] = None, **kwargs) -> List[Dict]:
+                         small_block_end: Optional[int] = None, stats=None,
+                         **kwargs) -> List[Dict]:
         """One draft block per calibration-graph node (:387-474).
 
         Node ij_set = [(position rank, vocab rank), ...]: take the masked
         positions of the small block ranked by max softmax probability, and put
         the vocab_rank-th most likely token at the pos_rank-th position.
+        ``stats``: sf_logit_stats of the small block's rows, when the caller has
+        them (their maximum probabilities and top tokens replace the softmax and
+        the vocabulary topk).
         """
         if self.calibration_graph is None:
             return []
@@ -128,15 +148,18 @@ class FastDLLMV2SpeculativeGeneration:
         # eager: torch.topk over a vocabulary row runs rocprim's radix sort, whose
         # look-back state is initialised by a memset; replayed from a captured HIP
         # graph it faulted the GPU, so the draft construction stays out of graphs
-        states = self._draft_states(x, small_logits, small_mask, offset, active)
+        states = self._draft_states(x, small_logits, small_mask, offset, active, stats)
         return [{"state": states[i], "start_pos": start_pos, "end_pos": end_pos, "node": node}
                 for i, (node, _, _) in enumerate(active)]
 
     @staticmethod
-    def _draft_states(x, small_logits, small_mask, offset, active) -> torch.Tensor:
+    def _draft_states(x, small_logits, small_mask, offset, active, stats=None) -> torch.Tensor:
         """The draft blocks of the active nodes, stacked [n, N] (:430-470); device
         ops only (indices stay on the device), so no host sync per node."""
-        conf = torch.softmax(small_logits, dim=-1).max(dim=-1).values
+        if stats is not None:
+            conf = greedy.max_prob_bf16(stats)
+        else:
+            conf = torch.softmax(small_logits, dim=-1).max(dim=-1).values
         conf = torch.where(~small_mask, float("-inf"), conf)
         blocks = []
         for _, ij_set, top_rank in active:
@@ -144,8 +167,10 @@ class FastDLLMV2SpeculativeGeneration:
             block = x.clone()
             for pos_rank, vocab_rank in ij_set:
                 pos = positions[pos_rank:pos_rank + 1]
-                row = small_logits.index_select(0, pos)[0]
-                tok = torch.topk(row, k=vocab_rank + 1).indices[vocab_rank:vocab_rank + 1]
+                tok = greedy.vocab_rank(stats, pos, vocab_rank) if stats is not None else None
+                if tok is None:
+                    row = small_logits.index_select(0, pos)[0]
+                    tok = torch.topk(row, k=vocab_rank + 1).indices[vocab_rank:vocab_rank + 1]
                 block.index_put_((pos + offset,), tok)
             blocks.append(block)
         return torch.stack(blocks)
@@ -225,9 +250,7 @@ class FastDLLMV2SpeculativeGeneration:
                             hit = eq.index(True) if True in eq else -1
                         if hit >= 0:
                             _, hit_logits = called.pop(hit)
-                            fx, fp = self._sample_with_top_p(hit_logits, top_p=self.top_p,
-                                                             temperature=self.temperature)
-                            x_1, p_1t = fx[:, s0:s1], fp[:, s0:s1, :]
+                            x_1, conf, _ = self._sample_rows(hit_logits[:, s0:s1, :])
                             kind = "hit"
                         else:
                             main_block = x_t[:, -bl:]
@@ -241,17 +264,14 @@ class FastDLLMV2SpeculativeGeneration:
                             main_logits = logits[0:1]
                             for i, d in enumerate(draft_blocks):
                                 called.append((d["state"], logits[i + 1:i + 2]))
-                            x_1, p_1t = self._sample_with_top_p(main_logits[:, s0:s1, :],
-                                                                top_p=self.top_p,
-                                                                temperature=self.temperature)
+                            x_1, conf, stats = self._sample_rows(main_logits[:, s0:s1, :])
                             if self.calibration_graph is not None:
                                 draft_blocks = self.get_draft_blocks(
                                     x_t[0, -bl:], main_logits[0], mask_idx[0],
                                     start_pos=x_t.shape[1] - bl, end_pos=x_t.shape[1],
-                                    small_block_start=s0, small_block_end=s1)
+                                    small_block_start=s0, small_block_end=s1, stats=stats)
                                 st["drafts_computed"] += len(draft_blocks)
                             kind = "verify"
-                        conf = torch.gather(p_1t, -1, x_1.unsqueeze(-1)).squeeze(-1)
                         conf = torch.where(small_mask, conf, -torch.inf)
                         unmask = conf > self.threshold
                         best = conf.argmax(dim=-1)

@@ -8,7 +8,8 @@ token), the same whole-block draft construction (:105-151), the same
 confidence-threshold unmasking with the transfer schedule of the checkpoint's
 ``generate()`` (modeling_nemotron_labs_diffusion.py:814-861), the same
 draft-logit cache, and the causal refresh of the prefix cache after every block
-(:298-316).
+(:298-316).  At temperature 0 the argmax tokens, probabilities and draft tokens
+come from one sf_logit_stats pass over the block's logits.
 """
 
 from __future__ import annotations
@@ -19,6 +20,8 @@ from typing import Dict, List, Optional, Tuple
 
 import torch
 import torch.nn.functional as F
+
+from specfold_amd.generate import greedy
 
 logger = logging.getLogger(__name__)
 
@@ -57,6 +60,21 @@ def get_transfer_index(logits: torch.Tensor, temperature: float, mask_index: tor
     x0 = torch.argmax(logits_with_noise, dim=-1)
     p = F.softmax(logits, dim=-1)
     x0_p = torch.squeeze(torch.gather(p, dim=-1, index=torch.unsqueeze(x0, -1)), -1)
+    return transfer_from(x0, x0_p, mask_index, x, num_transfer_tokens, threshold)
+
+
+def greedy_transfer_index(stats, mask_index: torch.Tensor, x: torch.Tensor,
+                          num_transfer_tokens: torch.Tensor, threshold: Optional[float] = None):
+    """get_transfer_index at temperature 0 from sf_logit_stats of the block's rows:
+    x0 = the argmax token, its probability = the bf16 softmax maximum."""
+    x0 = stats.top_idx[:, 0].long().unsqueeze(0)
+    x0_p = greedy.max_prob_bf16(stats).unsqueeze(0)
+    return transfer_from(x0, x0_p, mask_index, x, num_transfer_tokens, threshold)
+
+
+def transfer_from(x0, x0_p, mask_index, x, num_transfer_tokens, threshold=None):
+    """The selection part of get_transfer_index, given the argmax tokens x0 and
+    their probabilities x0_p."""
     x0 = torch.where(mask_index, x0, x)
     confidence = torch.where(mask_index, x0_p, float("-inf"))
     transfer_index = torch.zeros_like(x0, dtype=torch.bool)
@@ -110,18 +128,22 @@ class NLDDiffusionGeneration:
     # -- drafts -----------------------------------------------------------------------
     @torch.no_grad()
     def get_draft_blocks(self, x_block: torch.Tensor, logits_block: torch.Tensor,
-                         mask_index: torch.Tensor) -> List[Dict]:
+                         mask_index: torch.Tensor, stats=None) -> List[Dict]:
         """One draft block per graph node over the whole block (:105-151): the
         pos_rank-th most confident masked position gets its vocab_rank-th most
-        likely token.  Indices stay on the device (no host sync per node)."""
+        likely token.  Indices stay on the device (no host sync per node).
+        ``stats``: sf_logit_stats of the block's rows (their 1/Z and top tokens
+        replace the fp32 softmax and the vocabulary topk)."""
         nodes = self._graph_nodes()
         if not nodes:
             return []
         num_mask_positions = int(mask_index.sum().item())
         if num_mask_positions == 0:
             return []
-        probs = torch.softmax(logits_block.float(), dim=-1)
-        confidence = probs.max(dim=-1).values
+        if stats is not None:
+            confidence = greedy.max_prob_fp32(stats)
+        else:
+            confidence = torch.softmax(logits_block.float(), dim=-1).max(dim=-1).values
         confidence = torch.where(~mask_index, float("-inf"), confidence)
         drafts: List[Dict] = []
         for node in nodes:
@@ -133,8 +155,10 @@ class NLDDiffusionGeneration:
             draft = x_block.clone()
             for pos_rank, vocab_rank in ij_set:
                 pos = top_positions[pos_rank:pos_rank + 1]
-                row = logits_block.index_select(0, pos)[0]
-                tok = torch.topk(row, k=vocab_rank + 1).indices[vocab_rank:vocab_rank + 1]
+                tok = greedy.vocab_rank(stats, pos, vocab_rank) if stats is not None else None
+                if tok is None:
+                    row = logits_block.index_select(0, pos)[0]
+                    tok = torch.topk(row, k=vocab_rank + 1).indices[vocab_rank:vocab_rank + 1]
                 draft.index_put_((pos,), tok)
             drafts.append({"state": draft, "node": node})
         return drafts
@@ -204,6 +228,7 @@ class NLDDiffusionGeneration:
                     cur = x_accum[0, block_slice]
                     eq = torch.stack([s for s, _ in called]).eq(cur).all(dim=1).tolist()
                     hit = eq.index(True) if True in eq else -1
+                stats = None
                 if hit >= 0:
                     _, logits_block = called.pop(hit)
                     kind = "hit"
@@ -219,14 +244,24 @@ class NLDDiffusionGeneration:
                     logits_block = logits_all[0:1]
                     for k, d in enumerate(draft_blocks):
                         called.append((d["state"], logits_all[k + 1:k + 2]))
+                    if B == 1 and greedy.usable(logits_block, self.temperature):
+                        stats = greedy.stats(logits_block[0])
                     if self._graph_nodes():
                         draft_blocks = self.get_draft_blocks(x_accum[0, block_slice],
-                                                             logits_block[0], mask_block_idx[0])
+                                                             logits_block[0], mask_block_idx[0],
+                                                             stats=stats)
                         st["drafts_computed"] += len(draft_blocks)
                     kind = "verify"
-                x0, transfer = get_transfer_index(
-                    logits_block, self.temperature, mask_block_idx, x_accum[:, block_slice],
-                    num_transfer_tokens=num_transfer_tokens[:, i], threshold=self.threshold)
+                if stats is None and B == 1 and greedy.usable(logits_block, self.temperature):
+                    stats = greedy.stats(logits_block[0])
+                if stats is not None:
+                    x0, transfer = greedy_transfer_index(
+                        stats, mask_block_idx, x_accum[:, block_slice],
+                        num_transfer_tokens[:, i], threshold=self.threshold)
+                else:
+                    x0, transfer = get_transfer_index(
+                        logits_block, self.temperature, mask_block_idx, x_accum[:, block_slice],
+                        num_transfer_tokens=num_transfer_tokens[:, i], threshold=self.threshold)
                 cur = x_accum[:, block_slice].clone()
                 cur = torch.where(transfer, x0, cur)
                 x_accum[:, block_slice] = cur

@@ -51,6 +51,12 @@ def test_host_side_validation_without_gpu():
     assert lib.sf_chain_correct(*([None] * 7), 8, 32, 28, 4, 64, 0.1, *([None] * 5)) == 2
     assert lib.sf_qkv_workspace_bytes(256, 3584, 4608) > 0
     assert lib.sf_attn_workspace_bytes(256, 28, 0) > 0
+    # logit statistics: null outputs, then a vocabulary that is not a multiple of 8
+    assert lib.sf_logit_stats(fake, 8, 152064, 152064, 0.95, *([None] * 7), fake, 1 << 30,
+                              None) == 2
+    outs = [ctypes.c_void_p(4096 * (i + 1)) for i in range(7)]
+    assert lib.sf_logit_stats(fake, 8, 152063, 152064, 0.95, *outs, fake, 1 << 30, None) == 1
+    assert lib.sf_logit_stats_workspace_bytes(8) >= 8 * 65536 * 4
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
