@@ -49,8 +49,20 @@ extern "C" {
                                   (specfold/generate/fastdllm_v2_generation.py:151-186) */
 
 const char* sf_status_string(int status);
-/* 2: GEMM weights in the packed layout of sf_pack_weight; fused residual entries. */
+/* 2: GEMM weights in the packed layout of sf_pack_weight; fused residual entries.
+ * 3: sf_parent_map (the branch parent map on the device); sf_logit_stats. */
 int sf_abi_version(void);
+
+/*
+ * Branch parent map on the device.  Replaces _build_parent_map
+ * (specfold/generate/fastdllm_v2_folded.py:55-75), which computes the same map on
+ * the host after one device-to-host copy.  tokens [B1, N] int64 (row 0 = main);
+ * diff(i) = {n : tokens[i][n] != tokens[0][n]}; par[i] = the lowest j != i with
+ * |diff(j)| = |diff(i)| - 1 and diff(j) a subset of diff(i), else 0 (par[0] = 0);
+ * counts[i] = |diff(i)| (counts may be NULL).  Limits: B1 <= 64, N <= 64.
+ */
+int sf_parent_map(const int64_t* tokens, int B1, int N, int32_t* par, int32_t* counts,
+                  void* stream);
 
 /*
  * (1) Fold gate + deterministic compaction + src resolve + input RMSNorm.

@@ -57,6 +57,7 @@ SIGNATURES = {
     "sf_residual_gather_add": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _vp]),
     "sf_lm_head": (_i, [_vp, _i, _vp, _i, _i, _vp, _vp]),
     "sf_logit_stats_workspace_bytes": (ctypes.c_size_t, [_i]),
+    "sf_parent_map": (_i, [_vp, _i, _i, _vp, _vp, _vp]),
     "sf_logit_stats": (_i, [_vp, _i, _i, _ll, _f] + [_vp] * 7 + [_vp, ctypes.c_size_t, _vp]),
 }
 
@@ -440,3 +441,17 @@ def logit_stats(logits: torch.Tensor, top_p: float = 0.95, stream=None) -> Logit
                                _ptr(ws), ws.numel(), _stream(stream))
     _check(st, "sf_logit_stats")
     return out
+
+
+def parent_map(tokens: torch.Tensor, par: torch.Tensor, counts: Optional[torch.Tensor] = None,
+               stream=None) -> None:
+    """Branch parent map of a token block [B1, N] int64 into par [B1] int32
+    (sf_parent_map)."""
+    B1, N = tokens.shape
+    _need(tokens, "tokens", torch.int64, numel=B1 * N, align=8)
+    _need(par, "par", torch.int32, min_numel=B1, align=4)
+    if counts is not None:
+        _need(counts, "counts", torch.int32, min_numel=B1, align=4)
+    st = load().sf_parent_map(_ptr(tokens), B1, N, _ptr(par),
+                              _ptr(counts) if counts is not None else None, _stream(stream))
+    _check(st, "sf_parent_map")

@@ -252,7 +252,51 @@ extern "C" const char* sf_status_string(int status) {
   }
 }
 
-extern "C" int sf_abi_version(void) { return 2; }
+namespace {
+
+// Parent of every draft branch (specfold/generate/fastdllm_v2_folded.py:55-75):
+// diff(i) = the positions where branch i's token differs from the main row's;
+// parent(i) = the lowest j != i with |diff(j)| = |diff(i)| - 1 and diff(j) a
+// subset of diff(i), else 0 (the main row).  One wave; diff sets as 64-bit masks.
+__global__ __launch_bounds__(64) void sf_parent_map_kernel(const int64_t* __restrict__ tokens,
+                                                           int B1, int N,
+                                                           int32_t* __restrict__ par,
+                                                           int32_t* __restrict__ counts) {
+  __shared__ unsigned long long s_mask[64];
+  __shared__ int s_cnt[64];
+  const int i = threadIdx.x;
+  if (i < B1) {
+    unsigned long long m = 0ull;
+    for (int n = 0; n < N; ++n)
+      if (tokens[(size_t)i * N + n] != tokens[n]) m |= 1ull << n;
+    s_mask[i] = m;
+    s_cnt[i] = __popcll(m);
+  }
+  __syncthreads();
+  if (i < B1) {
+    int p = 0;
+    for (int j = 0; i > 0 && j < B1; ++j)
+      if (j != i && s_cnt[j] == s_cnt[i] - 1 && (s_mask[j] & ~s_mask[i]) == 0ull) {
+        p = j;
+        break;
+      }
+    par[i] = p;
+    if (counts) counts[i] = s_cnt[i];
+  }
+}
+
+}  // namespace
+
+extern "C" int sf_abi_version(void) { return 3; }
+
+extern "C" int sf_parent_map(const int64_t* tokens, int B1, int N, int32_t* par, int32_t* counts,
+                             void* stream) {
+  if (!tokens || !par) return SF_ERR_ARG;
+  if (B1 < 1 || B1 > 64 || N < 1 || N > 64) return SF_ERR_SHAPE;
+  hipLaunchKernelGGL(sf_parent_map_kernel, dim3(1), dim3(64), 0,
+                     reinterpret_cast<hipStream_t>(stream), tokens, B1, N, par, counts);
+  return sf_launch_status();
+}
 
 extern "C" int sf_fold_gate(const uint16_t* hidden, const int32_t* par, const uint16_t* ln_w,
                             int B1, int N, int D, int bucket, float delta, float eps, int gate_mode,

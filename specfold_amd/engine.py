@@ -17,10 +17,11 @@ fastdllm_v2_folded.py:296-361 for the launch sequence, :117-220 for the math):
   sf_residual_gather_add  h = hp + ffn[src] (folded rows reuse)  (HIP)
 and after the last layer the final RMSNorm (HIP) and the lm_head (hipBLASLt).
 
-Nothing here syncs with the host inside the layer loop: ``count`` stays on the
-device and every kernel reads it.  The only host syncs are the parent map
-(one D2H of the tokens, as the reference) and one read of the per-layer counts
-after the last layer (fold statistics and bucket-overflow detection).
+Nothing here syncs with the host: the branch parent map is computed from the
+tokens on the device (sf_parent_map; the reference copies the tokens to the host
+for it), ``count`` stays on the device and every kernel reads it, and the
+per-layer counts are copied to the host only when read (fold statistics), or
+once per step when a bucket below B1*N could overflow.
 """
 
 from __future__ import annotations
@@ -61,9 +62,18 @@ def build_parent_map(batched_input: torch.Tensor) -> Tuple[List[Optional[int]], 
 
 @dataclass
 class StepStats:
-    counts: List[int] = field(default_factory=list)   # recomputed rows per layer
+    """Recomputed rows per layer of one verify step.  ``count_dev`` stays on the
+    device; ``counts`` copies it to the host on first use."""
+    count_dev: Optional[torch.Tensor] = None
     bucket: int = 0
     overflow: bool = False
+    _counts: Optional[List[int]] = None
+
+    @property
+    def counts(self) -> List[int]:
+        if self._counts is None:
+            self._counts = [] if self.count_dev is None else self.count_dev.tolist()
+        return self._counts
 
 
 def decoder_parts(model):
@@ -94,6 +104,7 @@ class _Buffers:
         self.src = torch.zeros(BN, **i32)
         self.rows = torch.zeros(bucket, **i32)
         self.count_slab = torch.zeros(L, **i32)
+        self.par = torch.zeros(B1, **i32)          # branch parents (sf_parent_map)
         self.seg = torch.zeros(BN, **i32)
         self.slot = torch.zeros(BN, **i32)
         self.segcnt_slab = torch.zeros(L * B1, **i32)
@@ -213,8 +224,7 @@ class FoldedVerifyEngine:
     # ------------------------------------------------------------------------
     @torch.no_grad()
     def forward(self, batched_input: torch.Tensor, cache=None, delta: float = 0.1,
-                bucket: Optional[int] = None, parent: Optional[List[Optional[int]]] = None,
-                append: bool = False, compute_logits: bool = True,
+                bucket: Optional[int] = None, append: bool = False, compute_logits: bool = True,
                 q_scale: Optional[torch.Tensor] = None,
                 trace: Optional[list] = None,
                 teacher: Optional[Dict[int, torch.Tensor]] = None,
@@ -240,11 +250,7 @@ class FoldedVerifyEngine:
         bucket = max(1, min(int(bucket), BN))
         if append and (B1 != 1 or not isinstance(cache, PagedKVCache)):
             raise ValueError("append needs B1 == 1 and a PagedKVCache")
-        if parent is None:
-            parent = build_parent_map(batched_input)[0] if B1 > 1 else [None]
-        par_host = [0] + [int(p) for p in parent[1:]]
-        par = torch.tensor(par_host, dtype=torch.int32).to(self.device, non_blocking=True)
-
+        batched_input = batched_input.to(self.device).contiguous()
         P = cache_length(cache)
         P_alloc = cache.capacity if isinstance(cache, PagedKVCache) else P
         buf = self.buffers(B1, N, bucket, P_alloc)
@@ -259,29 +265,32 @@ class FoldedVerifyEngine:
             qs = buf.q_scale
         graphable = self.use_graphs and trace is None and teacher is None and not append
         if graphable:
-            hidden = self._replay(buf, batched_input, par, cache, P, delta, bucket,
+            hidden = self._replay(buf, batched_input, cache, P, delta, bucket,
                                   qs is not None, causal)
         else:
-            hidden = self._run_layers(buf, batched_input, par, cache, delta, bucket,
+            hidden = self._run_layers(buf, batched_input, cache, delta, bucket,
                                       append=append, q_scale=qs, trace=trace,
                                       teacher=teacher, causal=causal)
 
         if append:
             cache.advance(N)
-        counts = buf.count_slab.tolist()       # the one post-loop host sync
-        overflow = max(counts) > bucket
+        overflow = False
+        if bucket < BN:
+            # a bucket below B1*N can overflow: one host sync to check
+            overflow = int(buf.count_slab.max()) > bucket
         if stats is not None:
-            stats.counts, stats.bucket, stats.overflow = counts, bucket, overflow
+            stats.count_dev, stats.bucket, stats.overflow = buf.count_slab.clone(), bucket, overflow
+            stats._counts = None
         if overflow:
             if append:
                 raise RuntimeError("bucket overflow during a block commit")
-            logger.warning("SpecFold bucket overflow (%d > %d); recomputing with bucket=%d",
-                           max(counts), bucket, BN)
-            return self.forward(batched_input, cache, delta, bucket=BN, parent=parent,
+            logger.warning("SpecFold bucket overflow (> %d); recomputing with bucket=%d",
+                           bucket, BN)
+            return self.forward(batched_input, cache, delta, bucket=BN,
                                 compute_logits=compute_logits, q_scale=q_scale, trace=trace,
                                 teacher=teacher, stats=stats, causal=causal)
         self.last_hidden = hidden
-        self._last = dict(B1=B1, N=N, bucket=bucket, cache=cache, par=par, q_scale=qs,
+        self._last = dict(B1=B1, N=N, bucket=bucket, cache=cache, par=buf.par, q_scale=qs,
                           hidden=hidden, delta=delta)
         if not compute_logits:
             return None
@@ -291,7 +300,7 @@ class FoldedVerifyEngine:
         return logits.view(B1, N, self.V)
 
     # ------------------------------------------------------------------------
-    def _run_layers(self, buf: _Buffers, tokens: torch.Tensor, par: torch.Tensor, cache,
+    def _run_layers(self, buf: _Buffers, tokens: torch.Tensor, cache,
                     delta: float, bucket: int, append: bool = False,
                     q_scale: Optional[torch.Tensor] = None, trace: Optional[list] = None,
                     teacher: Optional[Dict[int, torch.Tensor]] = None,
@@ -305,6 +314,8 @@ class FoldedVerifyEngine:
         BN = B1 * N
         H, Hkv, hd, D = self.H, self.Hkv, self.hd, self.D
         base = self.base
+        par = buf.par
+        _lib.parent_map(tokens, par)          # on the device: no host round trip
         hidden = base.embed_tokens(tokens).reshape(BN, D)
         cos, sin = self._rope
         pos0 = cache.length_dev if isinstance(cache, PagedKVCache) else buf.pos0
@@ -401,34 +412,33 @@ class FoldedVerifyEngine:
                        for li in range(self.L))
         return (buf.key, id(buf), P, float(delta), bucket, self.gate_mode, ck, q_scaled, causal)
 
-    def _replay(self, buf: _Buffers, tokens: torch.Tensor, par: torch.Tensor, cache, P: int,
+    def _replay(self, buf: _Buffers, tokens: torch.Tensor, cache, P: int,
                 delta: float, bucket: int, q_scaled: bool = False, causal: bool = False):
         """Run the layers through a captured HIP graph (captured on first use for
         this shape / prefix length / cache); inputs go through static buffers
-        (tokens, parent map, and buf.q_scale when q_scaled)."""
+        (the tokens, and buf.q_scale when q_scaled; the parent map is computed
+        from the tokens inside the graph)."""
         key = self._graph_key(buf, cache, P, delta, bucket, q_scaled, causal)
         qs = buf.q_scale if q_scaled else None
         entry = self._graphs.get(key)
         if entry is None:
             static_tok = tokens.clone()
-            static_par = par.clone()
             side = torch.cuda.Stream()
             side.wait_stream(torch.cuda.current_stream())
             with torch.cuda.stream(side):      # warm-up launch outside the capture
-                self._run_layers(buf, static_tok, static_par, cache, delta, bucket, q_scale=qs,
+                self._run_layers(buf, static_tok, cache, delta, bucket, q_scale=qs,
                                  causal=causal)
             torch.cuda.current_stream().wait_stream(side)
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
-                out = self._run_layers(buf, static_tok, static_par, cache, delta, bucket,
-                                       q_scale=qs, causal=causal)
-            entry = (graph, static_tok, static_par, out)
+                out = self._run_layers(buf, static_tok, cache, delta, bucket, q_scale=qs,
+                                       causal=causal)
+            entry = (graph, static_tok, out)
             while len(self._graphs) >= self.max_graphs:
                 self._graphs.pop(next(iter(self._graphs)))
             self._graphs[key] = entry
-        graph, static_tok, static_par, out = entry
+        graph, static_tok, out = entry
         static_tok.copy_(tokens)
-        static_par.copy_(par)
         graph.replay()
         return out
 

@@ -40,13 +40,15 @@ class SpecFoldHIPNLDGeneration(NLDDiffusionGeneration):
         self.gate_mode = gate_mode
         self._engine: Optional[FoldedVerifyEngine] = None
         self._fold_draft_positions = 0
-        self._fold_draft_recomputed = 0
+        self._fold_draft_recomputed = None  # device scalar: read only by fold_ratio
         self.last_stats: Optional[StepStats] = None
 
     @property
     def fold_ratio(self) -> float:
         tot = self._fold_draft_positions
-        return 1.0 - self._fold_draft_recomputed / tot if tot else float("nan")
+        if not tot:
+            return float("nan")
+        return 1.0 - int(self._fold_draft_recomputed) / tot
 
     @staticmethod
     def _build_parent_map(batched_input: torch.Tensor) -> Tuple[List[Optional[int]], List[int]]:
@@ -79,9 +81,12 @@ class SpecFoldHIPNLDGeneration(NLDDiffusionGeneration):
                                  q_scale=q_scale, stats=stats)
         finally:
             eng.gate_mode = prev_mode
-        L = len(stats.counts)
+        # fold counters stay on the device (no host sync per step)
+        L = eng.L
         self._fold_draft_positions += (B1 - 1) * N * L
-        self._fold_draft_recomputed += sum(stats.counts) - L * N
+        rec = stats.count_dev.sum(dtype=torch.int64) - L * N
+        self._fold_draft_recomputed = rec if self._fold_draft_recomputed is None else \
+            self._fold_draft_recomputed + rec
         self.last_stats = stats
         return logits
 

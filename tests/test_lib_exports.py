@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_host_side_validation_without_gpu():
     lib = _lib.load()
-    assert lib.sf_abi_version() == 2
+    assert lib.sf_abi_version() == 3
     assert lib.sf_status_string(1).decode() == "shape outside kernel limits"
     # NULL pointers and bad shapes are rejected before any launch
     assert lib.sf_fold_gate(*([None] * 3), 8, 32, 64, 256, 0.1, 1e-6, 0, *([None] * 11)) == 2
@@ -57,6 +57,8 @@ def test_host_side_validation_without_gpu():
     outs = [ctypes.c_void_p(4096 * (i + 1)) for i in range(7)]
     assert lib.sf_logit_stats(fake, 8, 152063, 152064, 0.95, *outs, fake, 1 << 30, None) == 1
     assert lib.sf_logit_stats_workspace_bytes(8) >= 8 * 65536 * 4
+    assert lib.sf_parent_map(None, 8, 32, fake, None, None) == 2
+    assert lib.sf_parent_map(fake, 65, 32, fake, None, None) == 1
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
