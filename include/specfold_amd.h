@@ -147,7 +147,8 @@ int sf_qkv_rope(const uint16_t* xn, const int32_t* rows, const int32_t* count, i
  * P is then the capacity the grid and workspace are sized for (so one captured
  * graph serves a growing cache).  With prefix_len NULL, P is the length.
  * Limits: hd == 128, H % Hkv == 0, N <= 64, H/Hkv <= 8, P <= 32768, a page size
- * dividing 128.
+ * of 16, 32, 64 or 128 tokens (a page holds whole 16-key groups; a 128-key chunk
+ * holds whole pages).
  */
 size_t sf_attn_workspace_bytes(int bucket, int H, int P);
 int sf_attn_prefix_block(const uint16_t* q_buf, const uint16_t* kv_buf, const uint16_t* prefix_k,
