@@ -19,6 +19,18 @@ The model argument is any module tree with the Qwen2 layout the reference reads:
 ``post_attention_layernorm`` and ``mlp.{gate,up,down}_proj``.
 ``past_key_values`` is a sequence of per-layer ``(k, v)`` tensors
 ``[1, Hkv, P, hd]`` (or anything with that indexing contract), or None.
+
+How each function is pinned (all CPU tests):
+  folded_verify_step / folded_layer / shift_logits / rope_tables — bit-exact
+      against golden vectors written by the reference class itself
+      (tests/golden, tests/test_oracle_golden.py);
+  dense_layer — transformers' Qwen2DecoderLayer; with causal=True and q_scale,
+      transformers' Ministral3ForCausalLM over [prefix; block] (test_oracle_pins.py,
+      test_oracle_nld.py);
+  folded == dense with every row recomputed (both families);
+  chain-corrected (m, Z, O) — exact_branch_attention, fp64 brute force;
+  parent_map / topo_order — exhaustive small families + hypothesis;
+  llama4_q_scale — its closed form at the window boundaries.
 """
 
 from __future__ import annotations
