@@ -161,6 +161,10 @@ class FastDLLMV2SpeculativeGeneration:
         else:
             conf = torch.softmax(small_logits, dim=-1).max(dim=-1).values
         conf = torch.where(~small_mask, float("-inf"), conf)
+        if stats is not None:
+            states = greedy.draft_states(x, conf, stats, [ij for _, ij, _ in active], offset)
+            if states is not None:
+                return states
         blocks = []
         for _, ij_set, top_rank in active:
             positions = torch.topk(conf, k=top_rank + 1).indices

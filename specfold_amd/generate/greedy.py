@@ -63,3 +63,50 @@ def vocab_rank(st: _lib.LogitStats, pos: torch.Tensor, rank: int) -> Optional[to
     if rank >= TOP_K:
         return None
     return st.top_idx.index_select(0, pos)[:, rank].long()
+
+
+class DraftIndex:
+    """Device index tensors of a fixed list of draft-graph nodes (ij_sets), built
+    once: for the flattened (node, pos_rank, vocab_rank) pairs, the position in
+    the concatenated per-node topk results, the vocabulary rank and the node."""
+
+    def __init__(self, ij_sets, device):
+        self.ks = [max(p for p, _ in ij) + 1 for ij in ij_sets]
+        starts = [sum(self.ks[:n]) for n in range(len(ij_sets))]
+        g, v, node = [], [], []
+        for n, ij in enumerate(ij_sets):
+            for p, r in ij:
+                g.append(starts[n] + p)
+                v.append(r)
+                node.append(n)
+        self.max_rank = max(v)
+        self.g_idx = torch.tensor(g, dtype=torch.long, device=device)
+        self.v_idx = torch.tensor(v, dtype=torch.long, device=device)
+        self.node_idx = torch.tensor(node, dtype=torch.long, device=device)
+        self.n = len(ij_sets)
+
+
+_DRAFT_INDEX: dict = {}
+
+
+def draft_states(x: torch.Tensor, conf: torch.Tensor, st: _lib.LogitStats, ij_sets,
+                 offset: int = 0) -> Optional[torch.Tensor]:
+    """Draft blocks of the given nodes, stacked [n, len(x)]: node n puts, for each
+    (pos_rank, vocab_rank) of its ij_set, the vocab_rank-th most likely token of
+    the pos_rank-th most confident position (positions index the statistics'
+    rows; block position = row + offset).  The positions of each node come from
+    its own torch.topk over ``conf`` with k = its largest rank + 1, as the
+    reference's per-node call; the tokens of all nodes are then gathered and
+    scattered at once.  None when a vocabulary rank exceeds the statistics."""
+    key = (tuple(tuple(tuple(pair) for pair in ij) for ij in ij_sets), x.device)
+    ix = _DRAFT_INDEX.get(key)
+    if ix is None:
+        ix = _DRAFT_INDEX[key] = DraftIndex(ij_sets, x.device)
+    if ix.max_rank >= TOP_K:
+        return None
+    positions = torch.cat([torch.topk(conf, k=k).indices for k in ix.ks])
+    pos = positions.index_select(0, ix.g_idx)
+    toks = st.top_idx.index_select(0, pos).gather(1, ix.v_idx.unsqueeze(1)).squeeze(1).long()
+    states = x.unsqueeze(0).repeat(ix.n, 1)
+    states.index_put_((ix.node_idx, pos + offset), toks)
+    return states

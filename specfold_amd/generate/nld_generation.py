@@ -145,6 +145,13 @@ class NLDDiffusionGeneration:
         else:
             confidence = torch.softmax(logits_block.float(), dim=-1).max(dim=-1).values
         confidence = torch.where(~mask_index, float("-inf"), confidence)
+        if stats is not None:
+            live = [n for n in nodes if max(pr for pr, _ in n["ij_set"]) < num_mask_positions]
+            if not live:
+                return []
+            states = greedy.draft_states(x_block, confidence, stats, [n["ij_set"] for n in live])
+            if states is not None:
+                return [{"state": states[i], "node": n} for i, n in enumerate(live)]
         drafts: List[Dict] = []
         for node in nodes:
             ij_set = node["ij_set"]
