@@ -1,0 +1,199 @@
+"""Both decode loops end to end on the CPU, once with the reference's torch ops
+for every decision and once on the greedy-statistics path (the one the loops
+take on the GPU at temperature 0), with ``sf_logit_stats`` stood in for by the
+reference's own ops: the event streams, the committed tokens and the draft
+counts must be identical.  This covers the plumbing around the statistics (the
+top-p greedy pair, draft construction from the top-8 ranks, NLD's transfer rule)
+that the GPU tests reach only through the kernel.
+
+The model is a deterministic hash of (previous token, own token, absolute
+position) into a bank of logits rows.  Every bank row holds distinct bf16
+values (so no argmax / topk over the vocabulary depends on a library's tie
+order) scaled by a power of two (so the rows range from flat to confident and
+the loops take every branch: several commits per step, single commits, draft
+hits).  The stand-in's 1/Z reproduces the fp32 softmax maximum bit for bit, so
+the positions' confidences, ties included, are the same in both runs."""
+
+import types
+
+import pytest
+import torch
+
+from specfold_amd.configs import SYNTHETIC_DRAFT_GRAPH
+from specfold_amd.generate import greedy
+from specfold_amd.generate.fastdllm_model_executor import ByteTokenizer, FastDLLMModelExecutor
+from specfold_amd.generate.fastdllm_v2_generation import FastDLLMV2SpeculativeGeneration
+from specfold_amd.generate.nld_generation import NLDDiffusionGeneration
+
+V = 512
+N_BANK = 97
+
+
+def _bank(seed, eos=None):
+    """N_BANK rows of V distinct bf16 values, each row scaled by 4, 16, 64 or 256."""
+    g = torch.Generator().manual_seed(seed)
+    bits = torch.arange(0x3D80, 0x4100, dtype=torch.int32)          # 1/16 .. 8
+    pos = bits.to(torch.int16).view(torch.bfloat16).float()
+    pool = torch.cat([pos, -pos])
+    rows = []
+    for r in range(N_BANK):
+        vals = pool[torch.randperm(pool.numel(), generator=g)[:V]]
+        row = vals * float(4 ** (1 + r % 4))
+        if eos is not None and r % 47 == 5:
+            top = int(row.argmax())
+            row[[top, eos]] = row[[eos, top]]
+        rows.append(row)
+    bank = torch.stack(rows).to(torch.bfloat16)
+    assert torch.equal(bank.float(), torch.stack(rows))             # exact in bf16
+    assert all(bank[r].unique().numel() == V for r in range(N_BANK))
+    return bank
+
+
+class Cache:
+    def __init__(self, n, last):
+        self.n, self.last = n, last
+
+    def get_seq_length(self):
+        return self.n
+
+
+def _logits(bank, toks, cache):
+    start = 0 if cache is None else cache.n
+    last = 0 if cache is None else cache.last
+    prev = torch.cat([torch.full_like(toks[:, :1], last), toks[:, :-1]], dim=1)
+    pos = start + torch.arange(toks.shape[1])
+    h = (prev * 1000003 + toks * 7919 + pos * 104729) % N_BANK
+    return bank[h]
+
+
+class FakeFastDLLM:
+    device = torch.device("cpu")
+
+    def __init__(self, bank):
+        self.bank = bank
+
+    def get_tokenizer(self):
+        return ByteTokenizer()
+
+    def forward(self, toks, past_key_values=None, use_cache=True, update_past_key_values=False):
+        out = types.SimpleNamespace(logits=_logits(self.bank, toks, past_key_values),
+                                    past_key_values=past_key_values)
+        if update_past_key_values:
+            n = 0 if past_key_values is None else past_key_values.n
+            out.past_key_values = Cache(n + toks.shape[1], int(toks[0, -1]))
+        return out
+
+    def sample_with_top_p(self, logits, top_p=0.95, temperature=0.0):
+        return FastDLLMModelExecutor._top_p(logits, top_p, temperature)
+
+
+class FakeNLD(FakeFastDLLM):
+    MASK, EOS = 100000, 3
+
+    def __init__(self, bank):
+        super().__init__(bank)
+        self.diffusion = []
+
+    def get_mask_id(self):
+        return self.MASK
+
+    def get_eos_token_id(self):
+        return self.EOS
+
+    def set_diffusion_lm(self, flag):
+        self.diffusion.append(flag)
+
+    def forward(self, toks, past_key_values=None, use_cache=True, use_causal_mask=False):
+        out = types.SimpleNamespace(logits=_logits(self.bank, toks, past_key_values),
+                                    past_key_values=None)
+        if use_cache:
+            n = 0 if past_key_values is None else past_key_values.n
+            out.past_key_values = Cache(n + toks.shape[1], int(toks[0, -1]))
+        return out
+
+
+def cpu_stats(rows, top_p=0.95):
+    """sf_logit_stats' fields from the reference's ops: top-8 in descending order
+    (lowest index first among equal values), the top-p sampler's greedy token and
+    probability, the softmax normaliser (1/Z = the fp32 softmax maximum) and the
+    bf16 softmax maximum."""
+    f = rows.float()
+    order = torch.sort(f, dim=-1, descending=True, stable=True).indices[:, :8]
+    tok, probs = FastDLLMModelExecutor._top_p(rows, top_p, 0.0)
+    cmax = torch.softmax(f, dim=-1).max(-1).values
+    zfull = 1.0 / cmax
+    assert torch.equal(1.0 / zfull, cmax)       # max_prob_fp32 reproduces it exactly
+    return types.SimpleNamespace(
+        top_idx=order.to(torch.int32), top_val=f.gather(1, order), zfull=zfull,
+        znuc=torch.full_like(zfull, float("nan")), greedy_tok=tok.to(torch.int32),
+        conf=probs.gather(-1, tok.unsqueeze(-1)).squeeze(-1).float(),
+        conf_full=torch.softmax(rows, dim=-1).max(-1).values.float())
+
+
+def _run(gen, prompt_ids, monkeypatch, use_stats):
+    calls = []
+    if use_stats:
+        def stats(rows, top_p=0.95):
+            calls.append(rows.shape[0])
+            return cpu_stats(rows, top_p)
+        monkeypatch.setattr(greedy, "usable", lambda logits, t: t == 0
+                            and logits.dtype == torch.bfloat16 and logits.shape[-1] % 8 == 0)
+        monkeypatch.setattr(greedy, "stats", stats)
+    events = list(gen.decode_steps(prompt_ids))
+    monkeypatch.undo()
+    return events, gen._state, list(gen.last_commits), calls
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_fastdllm_loop_same_decisions_with_statistics(seed, monkeypatch):
+    bank = _bank(seed)
+    prompt = torch.randint(0, 256, (1, 40 + 3 * seed), generator=torch.Generator().manual_seed(seed))
+    runs = []
+    for use_stats in (False, True):
+        gen = FastDLLMV2SpeculativeGeneration(
+            block_length=32, model_executor=FakeFastDLLM(bank),
+            calibration_graph=SYNTHETIC_DRAFT_GRAPH, max_new_tokens=96, stop_token=7,
+            device="cpu")
+        gen.last_commits = []
+        runs.append(_run(gen, prompt, monkeypatch, use_stats))
+    (ea, sa, ca, _), (eb, sb, cb, calls) = runs
+    assert calls, "the statistics path was not taken"
+    assert ea == eb and ca == cb
+    assert torch.equal(sa["x_t"], sb["x_t"])
+    assert sa["model_calls"] == sb["model_calls"] and sa["drafts_computed"] == sb["drafts_computed"]
+    kinds = {e["kind"] for e in ea}
+    assert {"verify", "commit"} <= kinds
+
+
+def test_fastdllm_loop_hits_drafts():
+    """The fake model exercises the draft-hit branch on at least one seed."""
+    hits = 0
+    for seed in range(4):
+        gen = FastDLLMV2SpeculativeGeneration(
+            block_length=32, model_executor=FakeFastDLLM(_bank(seed)),
+            calibration_graph=SYNTHETIC_DRAFT_GRAPH, max_new_tokens=96, stop_token=7,
+            device="cpu")
+        gen.last_commits = []
+        prompt = torch.randint(0, 256, (1, 40 + 3 * seed),
+                               generator=torch.Generator().manual_seed(seed))
+        hits += sum(e["kind"] == "hit" for e in gen.decode_steps(prompt))
+    assert hits > 0
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_nld_loop_same_decisions_with_statistics(seed, monkeypatch):
+    bank = _bank(100 + seed, eos=FakeNLD.EOS)
+    prompt = torch.randint(0, 256, (1, 20 + 5 * seed),
+                           generator=torch.Generator().manual_seed(seed))
+    runs = []
+    for use_stats in (False, True):
+        gen = NLDDiffusionGeneration(block_length=32, model_executor=FakeNLD(bank),
+                                     calibration_graph=SYNTHETIC_DRAFT_GRAPH, max_new_tokens=128,
+                                     threshold=0.9, device="cpu")
+        runs.append(_run(gen, prompt, monkeypatch, use_stats))
+    (ea, sa, ca, _), (eb, sb, cb, calls) = runs
+    assert calls, "the statistics path was not taken"
+    assert ea == eb and ca == cb
+    assert torch.equal(sa["x_accum"], sb["x_accum"])
+    assert sa["model_calls"] == sb["model_calls"] and sa["drafts_computed"] == sb["drafts_computed"]
+    assert {"prefill", "verify", "hit", "commit"} <= {e["kind"] for e in ea}
