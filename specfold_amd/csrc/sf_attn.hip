@@ -38,41 +38,35 @@
 #include <math.h>
 
 #include "sf_common.h"
+#include "sf_index.h"
 
 namespace {
 
-constexpr int kHD = 128;
-constexpr int kQT = 64;      // queries per workgroup
-constexpr int kChunk = 128;  // prefix keys per workgroup
+using namespace sfa;  // kHD, kQT, kChunk, kMaxChunks and the index maps
+
 constexpr int kKStr = 136;   // K tile row stride (bf16)
 constexpr int kVStr = 136;   // V^T tile row stride (bf16): 128 keys + 8 pad
 constexpr int kMaxG = 8;
 constexpr int kMaxN = 64;
 constexpr int kCUs = 256;  // MI355X compute units
 
-// V^T tile swizzle: keys of dim row d are stored in 4-key (8-byte) units, unit u
-// at position u ^ vt_swz(d).  The transposing writes (16 lanes per key group
-// hitting rows 8 apart) then spread over every bank, and the P.V reads (16
-// consecutive rows, one unit each) stay conflict-free: vt_swz is constant
+// V^T tile swizzle (vt_swz): keys of dim row d are stored in 4-key (8-byte)
+// units, unit u at position u ^ vt_swz(d).  The transposing writes (16 lanes per
+// key group hitting rows 8 apart) then spread over every bank, and the P.V reads
+// (16 consecutive rows, one unit each) stay conflict-free: vt_swz is constant
 // across the 16 rows one read instruction touches.
-SF_DEV int vt_swz(int d) { return (d >> 3) & 14; }
-
-// Prefix chunks per work item: one while the one-chunk items fill about two
-// rounds of the resident grid, longer ranges beyond (fewer partials to write and
-// merge, and the next chunk's loads overlap this chunk's math).  A pure function
-// of device-side sizes, evaluated identically by the prefix and merge kernels.
-constexpr int kItemsTarget = 1024;
-SF_DEV int prefix_cpi(int nch, int n_qt, int Hkv) {
-  return max(1, min(nch, (nch * n_qt * Hkv) / kItemsTarget));
-}
-
+//
+// Prefix chunks per work item (prefix_cpi): one while the one-chunk items fill
+// about two rounds of the resident grid, longer ranges beyond (fewer partials to
+// write and merge, and the next chunk's loads overlap this chunk's math).
+//
 // Keys of a chunk are held in a permuted slot order: load j (0..7) of thread row
-// r = tid / 16 brings key 16j + r, which occupies slot 64(j/4) + 4r + j%4.  Every
-// load instruction then reads 16 consecutive keys (one 4 KB stretch of a page,
-// whose id is uniform: a scalar load), and the 4 keys a thread transposes into
-// V^T are 4 consecutive slots.  The softmax does not depend on key order; only
-// the mask of a partial last chunk needs the key behind a slot:
-SF_DEV int slot_key(int slot) { return 64 * (slot >> 6) + 16 * (slot & 3) + ((slot >> 2) & 15); }
+// r = tid / 16 brings key 16j + r, which occupies slot key_slot(j, r) =
+// 64(j/4) + 4r + j%4.  Every load instruction then reads 16 consecutive keys
+// (one 4 KB stretch of a page, whose id is uniform: a scalar load), and the 4
+// keys a thread transposes into V^T are 4 consecutive slots.  The softmax does
+// not depend on key order; only the mask of a partial last chunk needs the key
+// behind a slot (slot_key).
 
 // One (query tile, range of prefix chunks, kv head) item of the prefix pass; all
 // 256 threads take part (the LDS barriers are uniform).  K/V of chunk c+1 are
@@ -108,22 +102,22 @@ SF_DEV void prefix_item(const uint16_t* __restrict__ q_buf, const uint16_t* __re
   // 16-key group j of chunk ci starts at key g0 (groups past the prefix end are
   // clamped to the last group holding keys, keys past the end to the last key);
   // with a page size that is a multiple of 16 a group never straddles pages.
-  const int last_g0 = (P - 1) & ~15;
+  const int last_g0 = last_group_g0(P);
   const int sg = tid & 15;
   const int kr = tid >> 4;
   auto group_page = [&](int ci, int j) -> int {
-    const int g0 = min(ci * kChunk + 16 * j, last_g0);
+    const int g0 = chunk_group_g0(ci, j, last_g0);
     return page_table ? page_table[g0 / page_size] : 0;
   };
   sf_u32x4 kreg[8], vreg[2][4];
   auto load_chunk = [&](int ci, const int* pg) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int g0 = min(ci * kChunk + 16 * j, last_g0);
+      const int g0 = chunk_group_g0(ci, j, last_g0);
       const long long grow = page_table
           ? (long long)pg[j] * page_stride + (long long)(g0 & (page_size - 1)) * kHD
           : (long long)g0 * kHD;
-      const int off = min(kr, P - 1 - g0) * kHD + sg * 8;
+      const int off = group_key(kr, g0, P) * kHD + sg * 8;
       kreg[j] = *reinterpret_cast<const sf_u32x4*>(pk + head_off + grow + off);
       vreg[j >> 2][j & 3] = *reinterpret_cast<const sf_u32x4*>(pv + head_off + grow + off);
     }
@@ -148,8 +142,7 @@ SF_DEV void prefix_item(const uint16_t* __restrict__ q_buf, const uint16_t* __re
     // 4kr + 64p .. +3 -> one word per dim, by byte permutes)
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      *reinterpret_cast<sf_u32x4*>(&sK[(64 * (j >> 2) + 4 * kr + (j & 3)) * kKStr + sg * 8]) =
-          kreg[j];
+      *reinterpret_cast<sf_u32x4*>(&sK[key_slot(j, kr) * kKStr + sg * 8]) = kreg[j];
 #pragma unroll
     for (int p = 0; p < 2; ++p)
 #pragma unroll
@@ -257,7 +250,7 @@ SF_DEV void prefix_item(const uint16_t* __restrict__ q_buf, const uint16_t* __re
   }
 
   if (qvalid) {
-    const size_t slot = ((size_t)h * nch_cap + r) * qmax + qi;
+    const size_t slot = attn_slot(h, r, qi, nch_cap, qmax);
     if (grp == 0) {
       ws_ml[slot * 2] = m_run;
       ws_ml[slot * 2 + 1] = l_run;
@@ -285,23 +278,21 @@ sf_attn_prefix_kernel(
   const int P = p_len ? min(*p_len, P_cap) : P_cap;
   if (P <= 0) return;
   const int nq = min(*count_p, bucket) * G;
-  const int n_qt = (nq + kQT - 1) / kQT;
-  const int nch = (P + kChunk - 1) / kChunk;
-  const int cpi = prefix_cpi(nch, n_qt, Hkv);
-  const int nr = (nch + cpi - 1) / cpi;
+  const PrefixGrid pg = prefix_grid(P, nq, Hkv);
+  const int n_qt = pg.n_qt;
+  const int nch = pg.nch;
+  const int cpi = pg.cpi;
+  const int nr = pg.nr;
   const int items = n_qt * nr * Hkv;
   const int xcd = blockIdx.x & 7;
   const int per = gridDim.x >> 3;
-  const int end = (int)(((long long)items * (xcd + 1)) >> 3);
-  for (int it = (int)(((long long)items * xcd) >> 3) + (int)(blockIdx.x >> 3); it < end;
-       it += per) {
-    const int qt = it % n_qt;
-    const int rest = it / n_qt;
-    const int r = rest % nr;
-    const int h = rest / nr;
-    const int c0 = r * cpi;
+  const int end = xcd_begin(items, xcd + 1);
+  for (int it = xcd_begin(items, xcd) + (int)(blockIdx.x >> 3); it < end; it += per) {
+    const AttnItem item = attn_item(it, n_qt, nr);
+    const int c0 = item.r * cpi;
     prefix_item(q_buf, pk, pv, page_table, page_size, page_stride, head_stride, P, rows, nq, G, H,
-                scale_log2, qmax, nch_cap, qt, r, c0, min(nch, c0 + cpi), h, sK, sV, ws_o, ws_ml);
+                scale_log2, qmax, nch_cap, item.qt, item.r, c0, min(nch, c0 + cpi), item.h, sK, sV,
+                ws_o, ws_ml);
     __syncthreads();  // LDS is reused by the next item
   }
 }
@@ -309,7 +300,6 @@ sf_attn_prefix_kernel(
 // One 512-thread workgroup per active (recomputed row m, kv head h) item, walked
 // by a persistent grid; thread t owns the output pair (q-head t/64, dims
 // 2*(t%64) .. +1).
-constexpr int kMaxChunks = 256;   // prefix <= 32768 keys
 constexpr int kBatch = 16;        // chunk partials loaded per round
 
 SF_DEV void merge_item(const uint16_t* __restrict__ q_buf, const uint16_t* __restrict__ kv_buf,
@@ -329,6 +319,8 @@ SF_DEV void merge_item(const uint16_t* __restrict__ q_buf, const uint16_t* __res
   // of the row id), then q and the branch's block K/V gathered through src --------
   for (int i = tid; i < G * nch; i += 512) {
     const int g = i / nch, c = i - g * nch;
+    // attn_slot(h, c, m·G + g, ...) in 64-bit arithmetic (tests/cpp/index_check.cpp
+    // checks that these reads are exactly the prefix pass's writes)
     const size_t sl = ((size_t)h * nchunks_cap + c) * qmax + (size_t)m * G + g;
     const float2 ml = *reinterpret_cast<const float2*>(ws_ml + sl * 2);
     sml[g][2 * c] = ml.x;
@@ -462,10 +454,7 @@ __global__ __launch_bounds__(512) void sf_attn_block_merge_kernel(
   const int G = H / Hkv;
   const int P = p_len ? min(*p_len, P_cap) : P_cap;
   // number of prefix partials per query: the prefix kernel's chunk ranges
-  const int nch_all = min((P + kChunk - 1) / kChunk, nchunks_cap);
-  const int n_qt = (count * G + kQT - 1) / kQT;
-  const int cpi = nch_all > 0 ? prefix_cpi(nch_all, n_qt, Hkv) : 1;
-  const int nch = (nch_all + cpi - 1) / cpi;
+  const int nch = merge_ranges(P, count * G, Hkv, nchunks_cap);
   for (int it = blockIdx.x; it < count * Hkv; it += gridDim.x) {
     merge_item(q_buf, kv_buf, src, rows, it / Hkv, it % Hkv, N, H, Hkv, G, scale_log2, causal, nch,
                nchunks_cap, qmax, ws_o, ws_ml, o32, o_bf, m_tab, z_tab, sq, sk, sv, ss, sml, sM,
@@ -473,8 +462,6 @@ __global__ __launch_bounds__(512) void sf_attn_block_merge_kernel(
     __syncthreads();  // LDS is reused by the next item
   }
 }
-
-int nchunks_for(int P) { return (P + kChunk - 1) / kChunk; }
 
 }  // namespace
 
@@ -520,8 +507,7 @@ extern "C" int sf_attn_prefix_block(const uint16_t* q_buf, const uint16_t* kv_bu
     ws_o = reinterpret_cast<float*>(workspace);
     ws_ml = ws_o + nslot * kHD;
     // persistent grid: at most two 70 KB-LDS workgroups fit a CU; a multiple of 8
-    const int items_cap = ((qmax + kQT - 1) / kQT) * nch * Hkv;
-    const int grid = min(2 * kCUs, ((items_cap + 7) / 8) * 8);
+    const int grid = prefix_launch_grid(qmax, nch, Hkv);
     hipLaunchKernelGGL(sf_attn_prefix_kernel, dim3(grid), dim3(256), 0, st, q_buf, prefix_k,
                        prefix_v, page_table, page_size, page_stride, head_stride, prefix_len, P,
                        rows, count, bucket, H, Hkv, scale_log2, qmax, nch, ws_o, ws_ml);

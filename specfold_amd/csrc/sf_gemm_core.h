@@ -16,6 +16,7 @@
 #pragma once
 
 #include "sf_common.h"
+#include "sf_index.h"
 
 namespace sfg {
 
@@ -43,16 +44,9 @@ struct Smem {
 #define SFG_WAVES 2   // waves per SIMD the register allocation targets
 #endif
 
-// Weight layout (fragment-major, "packed"): for each 16-row tile of W [N, K] and
-// each 32-wide K chunk, the 64 lanes' MFMA B fragments (lane l holds
-// W[16t + l%16][32c + 8(l/16) .. +8]) are one contiguous 1 KB block, and the
-// chunks of a tile follow each other, so every wave's weight stream is a
-// sequential read.  sf_pack_weight produces it from row-major W.
-constexpr int kKsStride = 512;     // elements between 32-wide chunks of a tile
-constexpr int kStageElems = 2048;  // elements between 128-wide K stages of a tile
-SF_DEV const uint16_t* weight_lane_ptr(const uint16_t* W, int tile16, int K, int lane) {
-  return W + (size_t)tile16 * (K / 32) * 512 + lane * 8;
-}
+// Weight layout (fragment-major, "packed"; weight_lane_ptr, kKsStride and
+// kStageElems in sf_index.h): every wave's weight stream is a sequential read.
+// sf_pack_weight produces it from row-major W.
 
 // Main loop over stages [s0, s1) of K for NMT m tiles of 16 rows (NMT is a
 // template parameter so the MFMA loop is straight-line).  `wrow[t]` is this
@@ -141,36 +135,8 @@ SF_DEV void mainloop(const uint16_t* __restrict__ A, int lda, int mrows,
 // order after the GEMM — deterministic, and no cross-workgroup synchronisation
 // inside the kernel (an agent-scope fence costs a whole-L2 write-back and
 // invalidate on this multi-XCD part).
-#ifndef SFG_GRID
-#define SFG_GRID 512   // workgroups per m block (MI355X: two per CU)
-#endif
-
-struct Plan {
-  int T;  // column tiles
-  int S;  // K stages
-  int U;  // units per workgroup
-};
-
-// Balanced plan over SFG_GRID workgroups.
-inline Plan make_plan(int T, int S) {
-  const long long units = (long long)T * S;
-  const int U = (int)((units + SFG_GRID - 1) / SFG_GRID);
-  return Plan{T, S, U < 1 ? 1 : U};
-}
-// One workgroup per whole tile: every tile has a single contributor.
-inline Plan make_plan_whole(int T, int S) { return Plan{T, S, S}; }
-inline int plan_grid(const Plan& p) {
-  return (int)(((long long)p.T * p.S + p.U - 1) / p.U);
-}
-// Upper bound of contributors (slots) per tile.
-inline int plan_slots(const Plan& p) { return p.U >= p.S ? 2 : (p.S + p.U - 1) / p.U + 1; }
-
-SF_HD int tile_first(int t, const Plan& p) {
-  return (int)((long long)t * p.S / p.U);
-}
-SF_HD int tile_last(int t, const Plan& p) {
-  return (int)(((long long)(t + 1) * p.S - 1) / p.U);
-}
+// (Plan, make_plan, make_plan_whole, plan_grid, plan_slots, tile_first,
+// tile_last, plan_range_end, plan_piece and part_bytes: sf_index.h.)
 
 // sum_{j < n} p[j * stride .. +T] in slot order (deterministic).  Loads go out four
 // at a time from clamped addresses with no branch in between.
@@ -231,16 +197,16 @@ void gemm_sk_kernel(const uint16_t* __restrict__ A, const int32_t* __restrict__ 
   __syncthreads();
   const size_t stride = (size_t)mcap * N;
   const int g = blockIdx.x;
-  const int total = plan.T * plan.S;
-  const int u_end = min((g + 1) * plan.U, total);
+  const int u_end = plan_range_end(g, plan);
   for (int u = g * plan.U; u < u_end;) {
-    const int t = u / plan.S;
-    const int sa = u - t * plan.S;
-    const int sb = min(plan.S, sa + (u_end - u));
+    const Piece pc = plan_piece(u, u_end, plan);
+    const int t = pc.t;
+    const int sa = pc.sa;
+    const int sb = pc.sb;
     int col[WN];
     const uint16_t* wrow[WN];
     if (MODE == kSilu) {
-      const int c = t * 64 + wv * 16 + (lane & 15);
+      const int c = gemm_col<WN, true>(t, wv, 0, lane);
 #pragma unroll
       for (int tt = 0; tt < WN; ++tt) col[tt] = c;
       wrow[0] = weight_lane_ptr(W0, c >> 4, K, lane);
@@ -248,7 +214,7 @@ void gemm_sk_kernel(const uint16_t* __restrict__ A, const int32_t* __restrict__ 
     } else {
 #pragma unroll
       for (int tt = 0; tt < WN; ++tt) {
-        col[tt] = t * 64 * WN + wv * 16 * WN + tt * 16 + (lane & 15);
+        col[tt] = gemm_col<WN, false>(t, wv, tt, lane);
         wrow[tt] = weight_lane_ptr(W0, col[tt] >> 4, K, lane);
       }
     }
@@ -298,11 +264,6 @@ void gemm_sk_kernel(const uint16_t* __restrict__ A, const int32_t* __restrict__ 
     __syncthreads();  // the next piece's first A stage reuses LDS buffer 0
     u += sb - sa;
   }
-}
-
-// Partial slots of a plan: [plan_slots][mcap][N] fp32.
-inline size_t part_bytes(const Plan& p, int mcap, int N) {
-  return (size_t)plan_slots(p) * mcap * N * sizeof(float);
 }
 
 template <int WN, int MODE>

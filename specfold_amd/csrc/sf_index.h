@@ -1,0 +1,202 @@
+// Integer index maps of the kernels, shared with their CPU checker.
+//
+// Plain integer functions: the stream-K schedule of the weight-streaming GEMMs
+// and their output-column / packed-weight addressing, and the prefix attention's
+// work decomposition, key-slot permutation, V^T swizzle and page-group
+// addressing.  Under hipcc they are host+device functions used by the kernels
+// and the launchers; under a plain C++ compiler they build on their own, so the
+// CPU test tests/cpp/index_check.cpp walks them over the shapes the entry points
+// accept and checks that every access lands inside its buffer, every unit of
+// work is done exactly once and the kernels that pass work to each other agree
+// on its layout.
+#pragma once
+
+#include <stddef.h>
+
+#if defined(__HIPCC__)
+#define SF_IDX __host__ __device__ __forceinline__
+#else
+#define SF_IDX inline
+#endif
+
+SF_IDX int sf_imin(int a, int b) { return a < b ? a : b; }
+SF_IDX int sf_imax(int a, int b) { return a > b ? a : b; }
+
+// ---------------------------------------------------------------------------
+// Weight-streaming GEMM (sf_gemm_core.h)
+// ---------------------------------------------------------------------------
+namespace sfg {
+
+// Packed ("fragment-major") weights: for each 16-row tile of W [N, K] and each
+// 32-wide K chunk, the 64 lanes' MFMA B fragments (lane l holds
+// W[16t + l%16][32c + 8(l/16) .. +8]) are one contiguous 1 KB block, and the
+// chunks of a tile follow each other.
+constexpr int kKsStride = 512;     // elements between 32-wide chunks of a tile
+constexpr int kStageElems = 2048;  // elements between 128-wide K stages of a tile
+
+// Lane `lane`'s first fragment of 16-row tile `tile16`, from base W (a pointer to
+// the packed weights in the kernels; an integer 0 gives the element offset).
+template <typename P>
+SF_IDX P weight_lane_ptr(P W, int tile16, int K, int lane) {
+  return W + (size_t)tile16 * (K / 32) * 512 + lane * 8;
+}
+
+// Output column held by lane `lane` of wave `wv` in its column tile `tt` of
+// 64·WN-column tile t (WN tiles of 16 per wave).  SILU: the gate and the up tile
+// of one wave cover the same 16 columns of a 64-column tile.
+template <int WN, bool SILU>
+SF_IDX int gemm_col(int t, int wv, int tt, int lane) {
+  return SILU ? t * 64 + wv * 16 + (lane & 15) : t * 64 * WN + wv * 16 * WN + tt * 16 + (lane & 15);
+}
+
+// Stream-K schedule.  The output columns are cut into T tiles and K into S
+// stages of 128; the T*S (tile, stage) units are dealt out in tile-major order,
+// U consecutive units per workgroup.
+#ifndef SFG_GRID
+#define SFG_GRID 512   // workgroups per m block (MI355X: two per CU)
+#endif
+
+struct Plan {
+  int T;  // column tiles
+  int S;  // K stages
+  int U;  // units per workgroup
+};
+
+// Balanced plan over SFG_GRID workgroups.
+inline Plan make_plan(int T, int S) {
+  const long long units = (long long)T * S;
+  const int U = (int)((units + SFG_GRID - 1) / SFG_GRID);
+  return Plan{T, S, U < 1 ? 1 : U};
+}
+// One workgroup per whole tile: every tile has a single contributor.
+inline Plan make_plan_whole(int T, int S) { return Plan{T, S, S}; }
+inline int plan_grid(const Plan& p) {
+  return (int)(((long long)p.T * p.S + p.U - 1) / p.U);
+}
+// Upper bound of contributors (slots) per tile.
+inline int plan_slots(const Plan& p) { return p.U >= p.S ? 2 : (p.S + p.U - 1) / p.U + 1; }
+
+// First and last workgroup holding units of tile t; a piece of tile t computed by
+// workgroup g goes to partial slot g - tile_first(t).
+SF_IDX int tile_first(int t, const Plan& p) {
+  return (int)((long long)t * p.S / p.U);
+}
+SF_IDX int tile_last(int t, const Plan& p) {
+  return (int)(((long long)(t + 1) * p.S - 1) / p.U);
+}
+
+// Workgroup g's units are [g·U, plan_range_end(g)).
+SF_IDX int plan_range_end(int g, const Plan& p) {
+  const int total = p.T * p.S;
+  return sf_imin((g + 1) * p.U, total);
+}
+
+// The piece of a workgroup's range that starts at unit u: tile t, stages [sa, sb).
+struct Piece {
+  int t, sa, sb;
+};
+SF_IDX Piece plan_piece(int u, int u_end, const Plan& p) {
+  const int t = u / p.S;
+  const int sa = u - t * p.S;
+  return Piece{t, sa, sf_imin(p.S, sa + (u_end - u))};
+}
+
+// Partial slots of a plan: [plan_slots][mcap][N] fp32.
+inline size_t part_bytes(const Plan& p, int mcap, int N) {
+  return (size_t)plan_slots(p) * mcap * N * sizeof(float);
+}
+
+}  // namespace sfg
+
+// ---------------------------------------------------------------------------
+// Prefix attention (sf_attn.hip)
+// ---------------------------------------------------------------------------
+namespace sfa {
+
+constexpr int kHD = 128;
+constexpr int kQT = 64;      // queries per work item
+constexpr int kChunk = 128;  // prefix keys per chunk
+constexpr int kMaxChunks = 256;   // prefix <= 32768 keys
+
+// V^T tile swizzle: keys of dim row d are stored in 4-key (8-byte) units, unit u
+// at position u ^ vt_swz(d).
+SF_IDX int vt_swz(int d) { return (d >> 3) & 14; }
+
+// Prefix chunks per work item: one while the one-chunk items fill about two
+// rounds of the resident grid, longer ranges beyond.  A pure function of
+// device-side sizes, evaluated identically by the prefix and merge kernels.
+constexpr int kItemsTarget = 1024;
+SF_IDX int prefix_cpi(int nch, int n_qt, int Hkv) {
+  return sf_imax(1, sf_imin(nch, (nch * n_qt * Hkv) / kItemsTarget));
+}
+
+// Keys of a chunk are held in a permuted slot order: load j (0..7) of thread row
+// r = tid / 16 brings key 16j + r, which occupies slot key_slot(j, r); slot_key
+// is the inverse (the key behind a slot, for the mask of a partial chunk).
+SF_IDX int key_slot(int j, int r) { return 64 * (j >> 2) + 4 * r + (j & 3); }
+SF_IDX int slot_key(int slot) { return 64 * (slot >> 6) + 16 * (slot & 3) + ((slot >> 2) & 15); }
+
+// 16-key group j of chunk ci starts at key chunk_group_g0 (groups past the
+// prefix end are clamped to the last group holding keys, last_group_g0(P));
+// thread row kr of the group reads key g0 + group_key(kr, g0, P) (keys past the
+// end clamped to the last key).  With a page size that is a multiple of 16 a
+// group never straddles pages.
+SF_IDX int last_group_g0(int P) { return (P - 1) & ~15; }
+SF_IDX int chunk_group_g0(int ci, int j, int last_g0) {
+  return sf_imin(ci * kChunk + 16 * j, last_g0);
+}
+SF_IDX int group_key(int kr, int g0, int P) { return sf_imin(kr, P - 1 - g0); }
+
+// Persistent prefix grid (a multiple of 8 workgroups; workgroup b runs on XCD
+// b % 8): XCD x walks items [xcd_begin(items, x), xcd_begin(items, x + 1)).
+SF_IDX int xcd_begin(int items, int xcd) { return (int)(((long long)items * xcd) >> 3); }
+
+// Item it of the prefix pass: query tile qt, chunk range r, kv head h.
+struct AttnItem {
+  int qt, r, h;
+};
+SF_IDX AttnItem attn_item(int it, int n_qt, int nr) {
+  const int qt = it % n_qt;
+  const int rest = it / n_qt;
+  return AttnItem{qt, rest % nr, rest / nr};
+}
+
+// The prefix pass's decomposition for nq active queries per kv head and a prefix
+// of P keys: n_qt query tiles, nch chunks, cpi chunks per range, nr ranges
+// (= partials per query); items = n_qt · nr · Hkv ...
+struct PrefixGrid {
+  int n_qt, nch, cpi, nr;
+};
+SF_IDX PrefixGrid prefix_grid(int P, int nq, int Hkv) {
+  const int n_qt = (nq + kQT - 1) / kQT;
+  const int nch = (P + kChunk - 1) / kChunk;
+  const int cpi = prefix_cpi(nch, n_qt, Hkv);
+  return PrefixGrid{n_qt, nch, cpi, (nch + cpi - 1) / cpi};
+}
+// ... and the partials per query as the merge kernel derives them from its
+// query count nq = rows · G.
+SF_IDX int merge_ranges(int P, int nq, int Hkv, int nchunks_cap) {
+  const int nch_all = sf_imin((P + kChunk - 1) / kChunk, nchunks_cap);
+  const int n_qt = (nq + kQT - 1) / kQT;
+  const int cpi = nch_all > 0 ? prefix_cpi(nch_all, n_qt, Hkv) : 1;
+  return (nch_all + cpi - 1) / cpi;
+}
+
+// Partial slot of query qi of range r, kv head h: the workspace holds
+// [Hkv][nch_cap][qmax] slots of kHD fp32 (acc), then the same count of (m, l).
+SF_IDX size_t attn_slot(int h, int r, int qi, int nch_cap, int qmax) {
+  return ((size_t)h * nch_cap + r) * qmax + qi;
+}
+
+inline int nchunks_for(int P) { return (P + kChunk - 1) / kChunk; }
+
+// Persistent prefix grid for a capacity of qmax queries per kv head and nch
+// chunks: enough workgroups for every item, at most two per CU (256 CUs), a
+// multiple of 8.
+inline int prefix_launch_grid(int qmax, int nch, int Hkv) {
+  const int items_cap = ((qmax + kQT - 1) / kQT) * nch * Hkv;
+  const int g = ((items_cap + 7) / 8) * 8;
+  return g < 512 ? g : 512;
+}
+
+}  // namespace sfa

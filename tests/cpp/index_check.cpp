@@ -1,0 +1,376 @@
+// CPU checker of the kernels' integer index maps (specfold_amd/csrc/sf_index.h),
+// built with a plain C++ compiler and run by tests/test_index_maps.py.
+//
+//   index_check <libspecfold_amd.so>
+//
+// Walks the maps the kernels use over the shapes the entry points accept and
+// checks what the kernels rely on:
+//   * stream-K GEMM plans: every (tile, stage) unit done exactly once, every
+//     workgroup's range non-empty, the partial slot of each piece inside the
+//     plan's slot count and the library's workspace, whole-tile plans single-
+//     contributor; output columns of each mode inside N and covering each tile
+//     once; every packed-weight load inside the N·K weights, and the fragment it
+//     reads (under the packed layout) belonging to the column the lane writes;
+//   * prefix attention: the key-slot permutation and its inverse, the V^T unit
+//     layout, the page-group addressing (every load inside the prefix and inside
+//     its page; every real key loaded exactly once; masked slots are exactly the
+//     clamped loads), the persistent grid's item walk (each item once), the chunk
+//     ranges (a partition of the chunks), and the partial slots (inside the
+//     library's workspace; the merge reads exactly the slots the prefix pass
+//     wrote, with the same range count).
+// Prints one line per family and "OK"; exits 1 at the first failed check.
+#include <dlfcn.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+
+#include <vector>
+
+#include "sf_index.h"
+
+static long long g_checks = 0;
+#define CHECK(cond, ...)                                              \
+  do {                                                                \
+    ++g_checks;                                                       \
+    if (!(cond)) {                                                    \
+      fprintf(stderr, "FAIL %s:%d: %s  ", __FILE__, __LINE__, #cond); \
+      fprintf(stderr, __VA_ARGS__);                                   \
+      fprintf(stderr, "\n");                                          \
+      exit(1);                                                        \
+    }                                                                 \
+  } while (0)
+
+typedef size_t (*ws3_fn)(int, int, int);
+static ws3_fn f_gemm_ws, f_qkv_ws, f_attn_ws;
+
+// ---------------------------------------------------------------------------
+// GEMM plans
+// ---------------------------------------------------------------------------
+// Walks plan p as the GEMM kernel does; returns the largest slot index used.
+static int walk_plan(const sfg::Plan& p, bool whole) {
+  const int grid = sfg::plan_grid(p);
+  const long long total = (long long)p.T * p.S;
+  std::vector<unsigned char> seen((size_t)total, 0);
+  std::vector<int> lo(p.T, 1 << 30), hi(p.T, -1), cnt(p.T, 0);
+  int max_slot = -1;
+  for (int g = 0; g < grid; ++g) {
+    const int u_end = sfg::plan_range_end(g, p);
+    CHECK((long long)g * p.U < u_end, "empty range g=%d T=%d S=%d U=%d", g, p.T, p.S, p.U);
+    int last_t = -1;
+    for (int u = g * p.U; u < u_end;) {
+      const sfg::Piece pc = sfg::plan_piece(u, u_end, p);
+      CHECK(pc.t >= 0 && pc.t < p.T && pc.sa >= 0 && pc.sa < pc.sb && pc.sb <= p.S,
+            "piece t=%d sa=%d sb=%d", pc.t, pc.sa, pc.sb);
+      CHECK(pc.t > last_t, "tile order g=%d", g);
+      last_t = pc.t;
+      for (int s = pc.sa; s < pc.sb; ++s) {
+        const long long unit = (long long)pc.t * p.S + s;
+        CHECK(unit == u + (s - pc.sa), "unit order");
+        CHECK(!seen[unit], "unit %lld twice", unit);
+        seen[unit] = 1;
+      }
+      const int first = sfg::tile_first(pc.t, p), last = sfg::tile_last(pc.t, p);
+      CHECK(first <= g && g <= last, "g=%d outside [%d, %d] of tile %d", g, first, last, pc.t);
+      const int slot = g - first;
+      CHECK(slot < sfg::plan_slots(p), "slot %d >= %d", slot, sfg::plan_slots(p));
+      if (slot > max_slot) max_slot = slot;
+      lo[pc.t] = lo[pc.t] < g ? lo[pc.t] : g;
+      hi[pc.t] = hi[pc.t] > g ? hi[pc.t] : g;
+      ++cnt[pc.t];
+      u += pc.sb - pc.sa;
+    }
+  }
+  for (long long u = 0; u < total; ++u) CHECK(seen[u], "unit %lld never done", u);
+  for (int t = 0; t < p.T; ++t) {
+    // the contributors of a tile are exactly tile_first .. tile_last, one piece each
+    CHECK(lo[t] == sfg::tile_first(t, p) && hi[t] == sfg::tile_last(t, p) &&
+              cnt[t] == hi[t] - lo[t] + 1,
+          "tile %d contributors [%d, %d] x%d vs [%d, %d]", t, lo[t], hi[t], cnt[t],
+          sfg::tile_first(t, p), sfg::tile_last(t, p));
+    if (whole) CHECK(lo[t] == hi[t], "whole plan shares tile %d", t);
+  }
+  return max_slot;
+}
+
+static void check_plans() {
+  long long plans = 0;
+  for (int T = 1; T <= 160; ++T)
+    for (int S = 1; S <= 96; ++S) {
+      const sfg::Plan p = sfg::make_plan(T, S);
+      CHECK(sfg::plan_grid(p) <= SFG_GRID, "grid %d", sfg::plan_grid(p));
+      walk_plan(p, false);
+      const sfg::Plan w = sfg::make_plan_whole(T, S);
+      CHECK(sfg::plan_grid(w) == T, "whole grid");
+      walk_plan(w, true);
+      plans += 2;
+    }
+  // the shapes of the workloads (hidden D, q/k/v width, intermediate I, vocab V)
+  struct Shape { int D, nqkv, I, V; };
+  const Shape shapes[] = {{1536, 2048, 8960, 151936},  {3584, 4608, 18944, 152064},
+                          {4096, 6144, 14336, 131072}, {5120, 7168, 17408, 131072},
+                          {896, 1152, 4864, 151936}};
+  for (const Shape& s : shapes) {
+    for (int mcap : {1, 39, 64, 65, 256, 1024}) {
+      // QKV: 128-column tiles, stream-K, partial slots [slots][bucket][n_qkv]
+      const sfg::Plan q = sfg::make_plan(s.nqkv / 128, s.D / 128);
+      const int qs = walk_plan(q, false);
+      const size_t need_q = (size_t)(qs + 1) * mcap * s.nqkv * sizeof(float);
+      CHECK(f_qkv_ws(mcap, s.D, s.nqkv) >= need_q, "qkv workspace D=%d", s.D);
+      // down: 64-column tiles over D, K = I
+      const sfg::Plan d = sfg::make_plan(s.D / 64, s.I / 128);
+      const int ds = walk_plan(d, false);
+      CHECK(f_gemm_ws(mcap, s.D, s.I) >= (size_t)(ds + 1) * mcap * s.D * sizeof(float),
+            "down workspace D=%d I=%d", s.D, s.I);
+      plans += 2;
+    }
+    walk_plan(sfg::make_plan_whole(s.I / 64, s.D / 128), true);    // gate/up
+    walk_plan(sfg::make_plan_whole(s.D / 64, s.D / 128), true);    // o_proj (H·hd = D)
+    walk_plan(sfg::make_plan_whole(s.V / 128, s.D / 128), true);   // lm_head
+    plans += 3;
+  }
+  printf("gemm plans: %lld plans walked\n", plans);
+}
+
+// Output columns and packed-weight addressing of one GEMM mode: N output
+// columns in T tiles of 64·WN (SILU: 64), K = 128·S.
+template <int WN, bool SILU>
+static void check_columns(int N, int K) {
+  const int tw = SILU ? 64 : 64 * WN;
+  CHECK(N % tw == 0, "N %% tile");
+  const int T = N / tw, S = K / 128;
+  const int ntile = SILU ? 1 : WN;
+  for (int t = 0; t < T; ++t) {
+    std::vector<int> hits(tw, 0);
+    for (int wv = 0; wv < 4; ++wv)
+      for (int tt = 0; tt < ntile; ++tt)
+        for (int lane = 0; lane < 64; ++lane) {
+          const int col = sfg::gemm_col<WN, SILU>(t, wv, tt, lane);
+          CHECK(col >= t * tw && col < (t + 1) * tw && col < N, "col %d of tile %d", col, t);
+          if (lane < 16) ++hits[col - t * tw];
+          // the lane's weight stream: stage sc, 32-wide chunk ks of tile col/16
+          for (int sc = 0; sc < S; ++sc)
+            for (int ks = 0; ks < 4; ++ks) {
+              const size_t off = sfg::weight_lane_ptr<size_t>(0, col >> 4, K, lane) +
+                                 (size_t)sc * sfg::kStageElems + ks * sfg::kKsStride;
+              CHECK(off + 8 <= (size_t)N * K, "weight load past the end");
+              // packed layout: word (tile16 · K/32 + chunk) · 64 + l holds
+              // W[16 tile16 + l%16][32 chunk + 8 (l/16) ..+8]
+              CHECK(off % 8 == 0, "word alignment");
+              const size_t word = off / 8;
+              const size_t l = word & 63, tc = word >> 6;
+              const size_t tile16 = tc / (K / 32), chunk = tc % (K / 32);
+              CHECK(tile16 * 16 + (l & 15) == (size_t)col, "B fragment column");
+              CHECK(chunk * 32 + (l >> 4) * 8 == (size_t)sc * 128 + ks * 32 + (lane >> 4) * 8,
+                    "B fragment k");
+            }
+        }
+    for (int c = 0; c < tw; ++c) CHECK(hits[c] == 1, "column %d of tile %d hit %d times", c, t, hits[c]);
+  }
+}
+
+static void check_gemm_columns() {
+  check_columns<2, false>(4608, 3584);    // QKV, 7B
+  check_columns<2, false>(2048, 1536);    // QKV, 1.5B
+  check_columns<1, false>(3584, 18944);   // down, 7B
+  check_columns<1, false>(5120, 5120);    // o_proj, 14B
+  check_columns<2, true>(18944, 3584);    // gate/up, 7B
+  check_columns<2, true>(17408, 5120);    // gate/up, 14B
+  check_columns<2, false>(1024, 896);     // lm_head-style 128-column tiles
+  printf("gemm columns and weight fragments: ok\n");
+}
+
+// ---------------------------------------------------------------------------
+// Prefix attention
+// ---------------------------------------------------------------------------
+static void check_slots_and_vt() {
+  std::vector<int> used(128, 0);
+  for (int j = 0; j < 8; ++j)
+    for (int kr = 0; kr < 16; ++kr) {
+      const int s = sfa::key_slot(j, kr);
+      CHECK(s >= 0 && s < 128, "slot range");
+      ++used[s];
+      CHECK(sfa::slot_key(s) == 16 * j + kr, "slot_key(key_slot(%d, %d))", j, kr);
+    }
+  for (int s = 0; s < 128; ++s) CHECK(used[s] == 1, "slot %d used %d times", s, used[s]);
+  // a thread's 4 transposed keys (loads 4p..4p+3 of row kr) are V^T unit 16p + kr
+  for (int p = 0; p < 2; ++p)
+    for (int kr = 0; kr < 16; ++kr)
+      for (int i = 0; i < 4; ++i)
+        CHECK(sfa::key_slot(4 * p + i, kr) == 4 * (16 * p + kr) + i, "V^T unit of row %d", kr);
+  // per V^T row the swizzle permutes the 32 units and stays inside the 128 keys
+  for (int d = 0; d < sfa::kHD; ++d) {
+    std::vector<int> pos(32, 0);
+    for (int u = 0; u < 32; ++u) {
+      const int q = u ^ sfa::vt_swz(d);
+      CHECK(q >= 0 && q < 32, "swizzled unit");
+      ++pos[q];
+    }
+    for (int q = 0; q < 32; ++q) CHECK(pos[q] == 1, "swizzle not a permutation");
+    // one P.V read instruction touches rows d0..d0+15 with the same swizzle
+    CHECK(sfa::vt_swz(d) == sfa::vt_swz(d & ~15), "swizzle constant over 16 rows");
+  }
+  printf("key slots and V^T layout: ok\n");
+}
+
+// Loads of chunk ci for prefix length P and page size ps (ps = 0: contiguous).
+static void check_chunk_loads(int P, int ps) {
+  const int nch = sfa::nchunks_for(P);
+  const int last_g0 = sfa::last_group_g0(P);
+  const int npages = ps ? (P + ps - 1) / ps : 0;
+  std::vector<unsigned char> loaded(P, 0);
+  for (int ci = 0; ci < nch; ++ci) {
+    const int nkeys = P - ci * sfa::kChunk < sfa::kChunk ? P - ci * sfa::kChunk : sfa::kChunk;
+    for (int j = 0; j < 8; ++j) {
+      const int g0 = sfa::chunk_group_g0(ci, j, last_g0);
+      CHECK(g0 >= 0 && g0 % 16 == 0 && g0 < P, "group start %d (P=%d)", g0, P);
+      if (ps) CHECK(g0 / ps < npages, "page index %d of %d", g0 / ps, npages);
+      for (int kr = 0; kr < 16; ++kr) {
+        const int kk = sfa::group_key(kr, g0, P);
+        const int key = g0 + kk;
+        CHECK(kk >= 0 && key < P, "key %d (P=%d)", key, P);
+        if (ps) {
+          CHECK((g0 & (ps - 1)) + kk < ps, "row %d past page of %d", (g0 & (ps - 1)) + kk, ps);
+          CHECK(key / ps == g0 / ps, "group straddles pages");
+        }
+        const int slot = sfa::key_slot(j, kr);
+        const bool masked = sfa::slot_key(slot) >= nkeys;
+        if (!masked) {
+          // an unmasked slot holds its own key, loaded once over the whole prefix
+          CHECK(key == ci * sfa::kChunk + sfa::slot_key(slot), "slot holds key %d", key);
+          CHECK(!loaded[key], "key %d loaded twice", key);
+          loaded[key] = 1;
+        } else {
+          CHECK(ci == nch - 1, "masked slot outside the last chunk");
+        }
+      }
+    }
+  }
+  for (int k = 0; k < P; ++k) CHECK(loaded[k], "key %d never loaded (P=%d)", k, P);
+}
+
+static void check_page_addressing() {
+  long long n = 0;
+  for (int P = 1; P <= 2600; ++P)
+    for (int ps : {0, 16, 32, 64, 128}) check_chunk_loads(P, ps), ++n;
+  unsigned seed = 12345;
+  for (int i = 0; i < 60; ++i) {
+    seed = seed * 1103515245u + 12345u;
+    const int P = 2600 + (int)(seed % (32768 - 2600 + 1));
+    for (int ps : {0, 16, 128}) check_chunk_loads(P, ps), ++n;
+  }
+  for (int ps : {16, 32, 64, 128}) check_chunk_loads(32768, ps), ++n;
+  printf("page-group addressing: %lld (P, page size) cases\n", n);
+}
+
+// The persistent prefix grid over one shape, and the merge's reads.
+static void check_decomposition(int P, int P_cap, int count, int bucket, int G, int Hkv) {
+  const int qmax = bucket * G;
+  const int nch_cap = sfa::nchunks_for(P_cap);
+  const int nq = count * G;
+  const sfa::PrefixGrid pg = sfa::prefix_grid(P, nq, Hkv);
+  const int nr_merge = sfa::merge_ranges(P, nq, Hkv, nch_cap);
+  CHECK(pg.nr == nr_merge, "ranges: prefix %d merge %d (P=%d nq=%d Hkv=%d)", pg.nr, nr_merge, P,
+        nq, Hkv);
+  CHECK(nr_merge <= sfa::kMaxChunks, "merge LDS table");
+  // the ranges partition the chunks
+  int next = 0;
+  for (int r = 0; r < pg.nr; ++r) {
+    const int c0 = r * pg.cpi;
+    const int c1 = pg.nch < c0 + pg.cpi ? pg.nch : c0 + pg.cpi;
+    CHECK(c0 == next && c1 > c0, "range %d = [%d, %d)", r, c0, c1);
+    next = c1;
+  }
+  CHECK(next == pg.nch, "ranges end at %d of %d chunks", next, pg.nch);
+  // the grid the host launches for the capacity walks every item once
+  const int grid = sfa::prefix_launch_grid(qmax, nch_cap, Hkv);
+  CHECK(grid >= 8 && grid % 8 == 0 && grid <= 512, "grid %d", grid);
+  const int items = pg.n_qt * pg.nr * Hkv;
+  std::vector<unsigned char> item_seen(items, 0);
+  const size_t nslot = (size_t)nch_cap * qmax * Hkv;
+  std::vector<unsigned char> written(nslot, 0);
+  size_t n_written = 0;
+  for (int b = 0; b < grid; ++b) {
+    const int xcd = b & 7, per = grid >> 3;
+    const int end = sfa::xcd_begin(items, xcd + 1);
+    for (int it = sfa::xcd_begin(items, xcd) + (b >> 3); it < end; it += per) {
+      CHECK(it >= 0 && it < items && !item_seen[it], "item %d", it);
+      item_seen[it] = 1;
+      const sfa::AttnItem a = sfa::attn_item(it, pg.n_qt, pg.nr);
+      CHECK(a.qt < pg.n_qt && a.r < pg.nr && a.h < Hkv, "item decode");
+      for (int qi = a.qt * sfa::kQT; qi < (a.qt + 1) * sfa::kQT && qi < nq; ++qi) {
+        const size_t s = sfa::attn_slot(a.h, a.r, qi, nch_cap, qmax);
+        CHECK(s < nslot, "slot %zu >= %zu", s, nslot);
+        CHECK(!written[s], "slot written twice");
+        written[s] = 1;
+        ++n_written;
+      }
+    }
+  }
+  for (int it = 0; it < items; ++it) CHECK(item_seen[it], "item %d not walked", it);
+  // the merge reads (row m, q-head g, range c) at h·nch_cap·qmax + c·qmax + m·G + g:
+  // every read slot was written by the prefix pass, and nothing else was
+  size_t reads = 0;
+  for (int h = 0; h < Hkv; ++h)
+    for (int m = 0; m < count; ++m)
+      for (int g = 0; g < G; ++g)
+        for (int c = 0; c < nr_merge; ++c) {
+          const size_t s = ((size_t)h * nch_cap + c) * qmax + (size_t)m * G + g;
+          CHECK(s < nslot && written[s], "merge reads unwritten slot (h=%d m=%d g=%d c=%d)", h, m, g, c);
+          ++reads;
+        }
+  CHECK(reads == n_written, "prefix wrote %zu slots, merge reads %zu", n_written, reads);
+  // (acc, then (m, l)) fit the library's workspace for this capacity
+  const size_t need = nslot * (sfa::kHD + 2) * sizeof(float);
+  CHECK(f_attn_ws(bucket, G * Hkv, P_cap) >= need, "attention workspace");
+}
+
+static void check_attention_grid() {
+  long long n = 0;
+  const int GH[][2] = {{1, 1}, {5, 8}, {7, 4}, {8, 8}, {6, 2}, {4, 8}};
+  for (auto gh : GH) {
+    const int G = gh[0], Hkv = gh[1];
+    for (int bucket : {1, 8, 39, 64, 256}) {
+      for (int count : {1, bucket / 2 + 1, bucket}) {
+        if (count < 1 || count > bucket) continue;
+        for (int P = 1; P <= 1100; P += 37) check_decomposition(P, P, count, bucket, G, Hkv), ++n;
+        for (int P : {2047, 2048, 2112, 4096, 8191, 16384, 16448, 32768})
+          check_decomposition(P, P, count, bucket, G, Hkv), ++n;
+        // device length below the capacity the grid and workspace are sized for
+        for (int P : {1, 100, 2049, 9000}) check_decomposition(P, 16448, count, bucket, G, Hkv), ++n;
+      }
+    }
+  }
+  // every chunk count with the north-star and the long-context heads
+  for (int nch = 1; nch <= sfa::kMaxChunks; ++nch)
+    for (int count : {1, 39, 256}) {
+      check_decomposition(nch * 128, nch * 128, count, 256, 7, 4), ++n;
+      check_decomposition(nch * 128 - 5, nch * 128, count, 256, 5, 8), ++n;
+    }
+  printf("attention grids: %lld shapes\n", n);
+}
+
+int main(int argc, char** argv) {
+  if (argc != 2) {
+    fprintf(stderr, "usage: index_check <libspecfold_amd.so>\n");
+    return 2;
+  }
+  void* lib = dlopen(argv[1], RTLD_NOW | RTLD_LOCAL);
+  if (!lib) {
+    fprintf(stderr, "dlopen: %s\n", dlerror());
+    return 2;
+  }
+  f_gemm_ws = (ws3_fn)dlsym(lib, "sf_gemm_workspace_bytes");
+  f_qkv_ws = (ws3_fn)dlsym(lib, "sf_qkv_workspace_bytes");
+  f_attn_ws = (ws3_fn)dlsym(lib, "sf_attn_workspace_bytes");
+  if (!f_gemm_ws || !f_qkv_ws || !f_attn_ws) {
+    fprintf(stderr, "missing workspace queries\n");
+    return 2;
+  }
+  check_plans();
+  check_gemm_columns();
+  check_slots_and_vt();
+  check_page_addressing();
+  check_attention_grid();
+  printf("OK (%lld checks)\n", g_checks);
+  return 0;
+}
