@@ -1,0 +1,128 @@
+// Runs the attention entry point sf_attn_prefix_block (kernel source given by
+// KERNEL_SRC, compiled for the CPU SIMT simulator) on random inputs and checks O,
+// m and Z against a float64 restatement of the attention the kernels compute:
+// for each recomputed row, every q-head attends over the P prefix keys (paged,
+// shuffled pages) and its branch's N block keys (gathered through src; causal
+// within the block when asked), with scores scaled by `scaling`.
+//
+//   attn_sim P page_size B1 N H Hkv R causal seed
+// Prints the error summary; exits 1 when beyond tolerance.
+#include <stdio.h>
+#include <stdlib.h>
+
+#include <algorithm>
+#include <cmath>
+#include <random>
+#include <vector>
+
+#include KERNEL_SRC
+
+static uint16_t bf(float f) { return sim_f_to_bf16(f); }
+static double fb(uint16_t b) { return (double)sim_bf16_to_f(b); }
+
+int main(int argc, char** argv) {
+  if (argc != 10) {
+    fprintf(stderr, "usage: attn_sim P page_size B1 N H Hkv R causal seed\n");
+    return 2;
+  }
+  const int P = atoi(argv[1]), ps = atoi(argv[2]), B1 = atoi(argv[3]), N = atoi(argv[4]);
+  const int H = atoi(argv[5]), Hkv = atoi(argv[6]), R = atoi(argv[7]), causal = atoi(argv[8]);
+  const unsigned seed = (unsigned)atoi(argv[9]);
+  const int hd = 128, G = H / Hkv, BN = B1 * N, bucket = BN;
+  const float scaling = 1.0f / std::sqrt((float)hd);
+  std::mt19937 rng(seed);
+  std::normal_distribution<float> nd(0.f, 1.f);
+
+  std::vector<uint16_t> q((size_t)BN * H * hd), kv((size_t)BN * 2 * Hkv * hd);
+  for (auto& x : q) x = bf(nd(rng));
+  for (auto& x : kv) x = bf(nd(rng));
+  // recomputed rows: R distinct flat rows, ascending; the rest padded with the last
+  std::vector<int> all(BN);
+  for (int i = 0; i < BN; ++i) all[i] = i;
+  std::shuffle(all.begin(), all.end(), rng);
+  std::vector<int32_t> rows(all.begin(), all.begin() + R);
+  std::sort(rows.begin(), rows.end());
+  rows.resize(bucket, rows.back());
+  // src: block position j of branch b reads branch src[b*N + j]'s K/V row (<= b)
+  std::vector<int32_t> src(BN);
+  for (int b = 0; b < B1; ++b)
+    for (int j = 0; j < N; ++j) src[b * N + j] = b == 0 ? 0 : (int)(rng() % (b + 1));
+  int32_t count = R, plen = P;
+
+  // prefix: pages of ps keys, [page][Hkv][ps][hd], page table shuffled
+  const int npages = std::max(1, (P + ps - 1) / ps);
+  const long long head_stride = (long long)ps * hd, page_stride = (long long)Hkv * ps * hd;
+  std::vector<uint16_t> pk((size_t)npages * page_stride + 64), pv(pk.size());
+  for (auto& x : pk) x = bf(nd(rng));
+  for (auto& x : pv) x = bf(nd(rng));
+  std::vector<int32_t> table(npages);
+  for (int i = 0; i < npages; ++i) table[i] = i;
+  std::shuffle(table.begin(), table.end(), rng);
+  auto pkey = [&](const std::vector<uint16_t>& a, int h, int p, int d) {
+    return fb(a[(size_t)table[p / ps] * page_stride + (size_t)h * head_stride + (size_t)(p % ps) * hd + d]);
+  };
+
+  std::vector<float> o32((size_t)BN * H * hd, NAN), mt((size_t)BN * H, NAN), zt((size_t)BN * H, NAN);
+  std::vector<uint16_t> obf((size_t)BN * H * hd);
+  const size_t wsb = sf_attn_workspace_bytes(bucket, H, P);
+  std::vector<float> ws(wsb / 4 + 16);
+  const int st = sf_attn_prefix_block(q.data(), kv.data(), pk.data(), pv.data(), table.data(), P, ps,
+                                      page_stride, head_stride, src.data(), rows.data(), &count,
+                                      bucket, B1, N, H, Hkv, hd, scaling, &plen, causal, o32.data(),
+                                      obf.data(), mt.data(), zt.data(), ws.data(), wsb, nullptr);
+  if (st != 0) {
+    fprintf(stderr, "sf_attn_prefix_block returned %d\n", st);
+    return 1;
+  }
+
+  double max_o = 0, err_o = 0, err_m = 0, err_z = 0, ref_o = 0;
+  const int kvs = 2 * Hkv * hd;
+  for (int m = 0; m < R; ++m) {
+    const int row = rows[m], b = row / N, n = row % N;
+    for (int hq = 0; hq < H; ++hq) {
+      const int h = hq / G;
+      std::vector<double> s, w;
+      std::vector<const void*> vsrc;
+      std::vector<double> vrow;
+      std::vector<std::vector<double>> vals;
+      for (int p = 0; p < P; ++p) {
+        double d = 0;
+        for (int e = 0; e < hd; ++e) d += fb(q[((size_t)row * H + hq) * hd + e]) * pkey(pk, h, p, e);
+        s.push_back(d * scaling);
+        std::vector<double> v(hd);
+        for (int e = 0; e < hd; ++e) v[e] = pkey(pv, h, p, e);
+        vals.push_back(v);
+      }
+      for (int j = 0; j < N; ++j) {
+        if (causal && j > n) continue;
+        const size_t kr = (size_t)(src[b * N + j] * N + j) * kvs;
+        double d = 0;
+        for (int e = 0; e < hd; ++e) d += fb(q[((size_t)row * H + hq) * hd + e]) * fb(kv[kr + h * hd + e]);
+        s.push_back(d * scaling);
+        std::vector<double> v(hd);
+        for (int e = 0; e < hd; ++e) v[e] = fb(kv[kr + (Hkv + h) * hd + e]);
+        vals.push_back(v);
+      }
+      const double mx = *std::max_element(s.begin(), s.end());
+      double z = 0;
+      for (double x : s) z += std::exp(x - mx);
+      for (int e = 0; e < hd; ++e) {
+        double o = 0;
+        for (size_t i = 0; i < s.size(); ++i) o += std::exp(s[i] - mx) * vals[i][e];
+        o /= z;
+        const double got = o32[((size_t)row * H + hq) * hd + e];
+        err_o = std::max(err_o, std::fabs(got - o));
+        ref_o = std::max(ref_o, std::fabs(o));
+      }
+      err_m = std::max(err_m, std::fabs(mt[(size_t)row * H + hq] - mx));
+      err_z = std::max(err_z, std::fabs(zt[(size_t)row * H + hq] - z) / z);
+      max_o = ref_o;
+    }
+  }
+  printf("P=%d ps=%d B1=%d N=%d H=%d/%d R=%d causal=%d: O max abs err %.3g (|O| max %.3g), "
+         "m %.3g, Z rel %.3g\n", P, ps, B1, N, H, Hkv, R, causal, err_o, max_o, err_m, err_z);
+  const bool ok = err_o <= 2e-4 * std::max(1.0, max_o) && err_m <= 1e-4 && err_z <= 1e-4 &&
+                  std::isfinite(err_o) && std::isfinite(err_m) && std::isfinite(err_z);
+  if (!ok) printf("FAIL\n");
+  return ok ? 0 : 1;
+}

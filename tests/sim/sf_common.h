@@ -1,0 +1,50 @@
+// Host stand-in for specfold_amd/csrc/sf_common.h in the CPU SIMT simulation
+// (tests/sim/simt.h): the same names and semantics, built on the simulator.  The
+// kernel sources are compiled unchanged against it (a copy of the kernel file is
+// placed next to this header so its quoted include resolves here).
+#pragma once
+
+#include <stdint.h>
+
+#include "simt.h"
+#include "specfold_amd.h"
+
+#define SF_DEV inline
+#define SF_HD inline
+
+typedef uint16_t sf_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float sf_f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t sf_u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t sf_u32x2 __attribute__((ext_vector_type(2)));
+
+SF_DEV float sf_bf2f(uint16_t b) { return sim_bf16_to_f(b); }
+SF_DEV uint16_t sf_f2bf(float f) { return sim_f_to_bf16(f); }
+SF_DEV float sf_rbf(float f) { return sf_bf2f(sf_f2bf(f)); }
+
+SF_DEV void sf_unpack8(const sf_u32x4 w, float out[8]) {
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = __uint_as_float(w[i] << 16);
+    out[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+
+SF_DEV uint32_t sf_pack2(float lo, float hi) {
+  return (uint32_t)sf_f2bf(lo) | ((uint32_t)sf_f2bf(hi) << 16);
+}
+
+SF_DEV float sf_wave_sum(float v) {
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+SF_DEV float sf_wave_max(float v) {
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+SF_DEV sf_bf16x8 sf_as_bf16x8(const sf_u32x4 w) { return __builtin_bit_cast(sf_bf16x8, w); }
+
+SF_DEV sf_f32x4 sf_mfma16x16x32(const sf_bf16x8 a, const sf_bf16x8 b, sf_f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+static inline int sf_launch_status() { return hipGetLastError() == hipSuccess ? SF_OK : SF_ERR_HIP; }

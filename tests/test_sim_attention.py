@@ -1,0 +1,62 @@
+"""The attention kernels' own source (specfold_amd/csrc/sf_attn.hip) run on the
+CPU through the SIMT simulator of tests/sim (fibers per work-item, barriers,
+wave-collective MFMA and shuffles from the documented operand layouts), called
+through the library's entry point sf_attn_prefix_block with its host checks and
+launch arithmetic, and checked against a float64 restatement of the attention.
+
+This pins the kernels' data movement and indexing (paged and shuffled prefix
+pages, permuted key slots, swizzled V^T, chunk ranges with the flash rescale,
+persistent-grid walk, partial slots, merge, causal block) on machines without a
+GPU; the GPU tests pin the same kernels on the hardware."""
+
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+SIM = ROOT / "tests" / "sim"
+CSRC = ROOT / "specfold_amd" / "csrc"
+CLANG = Path("/opt/rocm/llvm/bin/clang++")
+
+
+@pytest.fixture(scope="module")
+def attn_sim(tmp_path_factory):
+    cxx = str(CLANG) if CLANG.exists() else shutil.which("clang++")
+    if cxx is None:
+        pytest.skip("no clang++ (the simulator needs clang's vector extensions)")
+    d = tmp_path_factory.mktemp("attn_sim")
+    # a copy of the kernel file, so its quoted include of sf_common.h resolves to the
+    # simulator's host header (tests/sim) instead of the HIP one next to the original
+    src = d / "sf_attn.hip"
+    src.write_text((CSRC / "sf_attn.hip").read_text())
+    exe = d / "attn_sim"
+    r = subprocess.run([cxx, "-std=c++20", "-O2", "-Wno-unknown-attributes", f"-I{SIM}",
+                        f"-I{ROOT / 'include'}", f"-I{CSRC}", f'-DKERNEL_SRC="{src}"',
+                        str(SIM / "attn_sim.cpp"), "-o", str(exe), "-lpthread"],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-4000:]
+    return exe
+
+
+CASES = [
+    # P, page size, B1, N, H, Hkv, R, causal, seed
+    (1, 16, 2, 8, 4, 2, 5, 0, 1),        # one prefix key
+    (17, 16, 3, 8, 4, 2, 9, 0, 2),       # two pages, partial last
+    (130, 32, 2, 16, 6, 2, 11, 1, 3),    # partial second chunk, causal block
+    (300, 16, 3, 8, 8, 1, 7, 0, 4),      # G = 8
+    (257, 128, 2, 8, 4, 4, 16, 0, 5),    # G = 1, 128-key pages
+    (0, 16, 2, 8, 4, 2, 6, 1, 6),        # no prefix: block keys only
+    (2112, 16, 8, 32, 28, 4, 39, 0, 11),  # the 7B verify shape
+    (4096, 16, 8, 32, 16, 8, 256, 0, 12),  # two chunks per work item (flash rescale)
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "P%d_ps%d_H%d-%d_R%d_c%d" % (
+    c[0], c[1], c[4], c[5], c[6], c[7]))
+def test_attention_kernels_in_simulator(attn_sim, case):
+    r = subprocess.run([str(attn_sim), *map(str, case)], capture_output=True, text=True,
+                       timeout=600)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
