@@ -1,0 +1,206 @@
+// Runs the weight-streaming GEMM entry points (kernel sources compiled for the
+// CPU SIMT simulator in separate objects) on random bf16 inputs and checks them
+// against float64 dot products rounded as each epilogue specifies:
+//   sf_pack_weight      the packed layout word (t, c, l) = W[16t + l%16][32c + 8(l/16) .. +8]
+//   sf_ffn_gate_up      act[m] = bf16(bf16(silu(bf16 g)) * bf16 u), m < count (whole tiles)
+//   sf_ffn_down_scatter ffn[rows[m]] = bf16(act[m] . Wd^T), m < count (stream-K, fix-up);
+//                       rows not in `rows` stay untouched
+//   sf_o_proj_residual  hp[r] = bf16(x[r] + bf16(o[r] . Wo^T)), r < M (static M)
+//   sf_lm_head          logits[m] = bf16(x[m] . W^T), m < M
+// A result may differ from the rounded float64 value where the fp32 sum (another
+// summation order) lies next to a rounding boundary, or where the sum cancels:
+// the check allows two bf16 steps plus 1e-6 of the sum of the terms' magnitudes
+// (plus one step of bf16(y) where a rounded product feeds a residual sum), on at
+// most 2% of the outputs; everything else must match exactly.
+//
+//   gemm_sim D I count bucket M seed
+#include <stdio.h>
+#include <stdlib.h>
+
+#include <algorithm>
+#include <cmath>
+#include <random>
+#include <vector>
+
+#include "sf_common.h"
+
+static uint16_t bf(double f) { return sim_f_to_bf16((float)f); }
+static double fb(uint16_t b) { return (double)sim_bf16_to_f(b); }
+
+struct Checker {
+  const char* name;
+  long n = 0, near = 0, bad = 0;
+  // want: the float64 value before the final bf16 rounding; mag: sum of |terms|
+  void add(uint16_t got, double want, double mag, double extra = 0) {
+    const uint16_t w = bf(want);
+    ++n;
+    if (got == w) return;
+    const double ulp = std::ldexp(1.0, std::ilogb(std::fabs(fb(w)) + 1e-30) - 7);
+    if (std::fabs(fb(got) - want) <= 2 * ulp + 1e-6 * mag + extra) {
+      ++near;
+      return;
+    }
+    if (++bad <= 5) fprintf(stderr, "%s: got %g want %g (mag %g)\n", name, fb(got), want, mag);
+  }
+  bool report() {
+    printf("  %-22s %7ld outputs: %ld within rounding, %ld wrong\n", name, n, near, bad);
+    return bad == 0 && near * 50 <= n;
+  }
+};
+
+static std::vector<uint16_t> pack(const std::vector<uint16_t>& w, int N, int K) {
+  std::vector<uint16_t> out((size_t)N * K);
+  if (const int st = sf_pack_weight(w.data(), N, K, out.data(), nullptr)) {
+    fprintf(stderr, "sf_pack_weight(N=%d, K=%d) returned %d\n", N, K, st);
+    exit(1);
+  }
+  return out;
+}
+
+int main(int argc, char** argv) {
+  if (argc != 7) {
+    fprintf(stderr, "usage: gemm_sim D I count bucket M seed\n");
+    return 2;
+  }
+  const int D = atoi(argv[1]), I = atoi(argv[2]), count = atoi(argv[3]), bucket = atoi(argv[4]);
+  const int M = atoi(argv[5]);
+  std::mt19937 rng((unsigned)atoi(argv[6]));
+  std::normal_distribution<float> nd(0.f, 1.f);
+  auto rnd = [&](size_t n, float sd) {
+    std::vector<uint16_t> v(n);
+    for (auto& x : v) x = bf(sd * nd(rng));
+    return v;
+  };
+  bool ok = true;
+
+  // ---- packing ----------------------------------------------------------------------
+  {
+    const int N = 64, K = 256;
+    auto w = rnd((size_t)N * K, 1.f);
+    auto p = pack(w, N, K);
+    long bad = 0;
+    for (int t = 0; t < N / 16; ++t)
+      for (int c = 0; c < K / 32; ++c)
+        for (int l = 0; l < 64; ++l)
+          for (int e = 0; e < 8; ++e)
+            bad += p[(((size_t)t * (K / 32) + c) * 64 + l) * 8 + e] !=
+                   w[(size_t)(16 * t + l % 16) * K + 32 * c + 8 * (l / 16) + e];
+    printf("  %-22s %s\n", "pack layout", bad ? "WRONG" : "exact");
+    ok &= bad == 0;
+  }
+
+  // ---- gate/up and down over the recomputed rows ----------------------------------------
+  {
+    auto zn = rnd((size_t)bucket * D, 1.f);
+    auto wg = rnd((size_t)I * D, 0.05f), wu = rnd((size_t)I * D, 0.05f);
+    auto wd = rnd((size_t)D * I, 0.05f);
+    const auto pg = pack(wg, I, D), pu = pack(wu, I, D), pd = pack(wd, D, I);
+    std::vector<uint16_t> act((size_t)bucket * I, 0x7fc0);
+    int32_t cnt = count;
+    if (sf_ffn_gate_up(zn.data(), &cnt, bucket, pg.data(), pu.data(), D, I, act.data(), nullptr)) {
+      fprintf(stderr, "sf_ffn_gate_up failed\n");
+      return 1;
+    }
+    Checker cg{"ffn gate/up"};
+    for (int m = 0; m < count; ++m)
+      for (int c = 0; c < I; ++c) {
+        double g = 0, u = 0, mg = 0, mu = 0;
+        for (int k = 0; k < D; ++k) {
+          g += fb(zn[(size_t)m * D + k]) * fb(wg[(size_t)c * D + k]);
+          u += fb(zn[(size_t)m * D + k]) * fb(wu[(size_t)c * D + k]);
+          mg += std::fabs(fb(zn[(size_t)m * D + k]) * fb(wg[(size_t)c * D + k]));
+          mu += std::fabs(fb(zn[(size_t)m * D + k]) * fb(wu[(size_t)c * D + k]));
+        }
+        const double gt = fb(bf(g));
+        const double s = fb(bf((float)gt / (1.0f + expf(-(float)gt))));
+        cg.add(act[(size_t)m * I + c], (double)(float)(s * fb(bf(u))), mg + mu);
+      }
+    ok &= cg.report();
+
+    // down: rows[m] = a permutation of flat rows; act rows as computed above
+    const int BN = bucket + 7;
+    std::vector<int32_t> rows(bucket);
+    {  // distinct destination rows in a scrambled order
+      std::vector<int32_t> perm(BN);
+      for (int i = 0; i < BN; ++i) perm[i] = i;
+      std::shuffle(perm.begin(), perm.end(), rng);
+      for (int m = 0; m < bucket; ++m) rows[m] = perm[m];
+    }
+    std::vector<uint16_t> ffn((size_t)BN * D, 0x1234);
+    auto act_in = rnd((size_t)bucket * I, 1.f);
+    std::vector<float> ws(sf_gemm_workspace_bytes(bucket, D, I) / 4 + 16);
+    if (sf_ffn_down_scatter(act_in.data(), &cnt, bucket, rows.data(), pd.data(), I, D, ffn.data(),
+                            ws.data(), ws.size() * 4, nullptr)) {
+      fprintf(stderr, "sf_ffn_down_scatter failed\n");
+      return 1;
+    }
+    Checker cd{"ffn down + scatter"};
+    std::vector<char> written(BN, 0);
+    for (int m = 0; m < count; ++m) {
+      written[rows[m]] = 1;
+      for (int c = 0; c < D; ++c) {
+        double y = 0, mag = 0;
+        for (int k = 0; k < I; ++k) {
+          y += fb(act_in[(size_t)m * I + k]) * fb(wd[(size_t)c * I + k]);
+          mag += std::fabs(fb(act_in[(size_t)m * I + k]) * fb(wd[(size_t)c * I + k]));
+        }
+        cd.add(ffn[(size_t)rows[m] * D + c], y, mag);
+      }
+    }
+    long touched = 0;
+    for (int r = 0; r < BN; ++r)
+      if (!written[r])
+        for (int c = 0; c < D; ++c) touched += ffn[(size_t)r * D + c] != 0x1234;
+    printf("  %-22s %s\n", "down: other rows", touched ? "OVERWRITTEN" : "untouched");
+    ok &= cd.report() && touched == 0;
+  }
+
+  // ---- o_proj + residual and lm_head over M static rows -----------------------------------
+  {
+    auto o = rnd((size_t)M * D, 1.f), x = rnd((size_t)M * D, 1.f);
+    auto wo = rnd((size_t)D * D, 0.05f);
+    const auto po = pack(wo, D, D);
+    std::vector<uint16_t> hp((size_t)M * D);
+    std::vector<float> ws(sf_gemm_workspace_bytes(M, D, D) / 4 + 16);
+    if (sf_o_proj_residual(o.data(), x.data(), po.data(), M, D, D, hp.data(), ws.data(),
+                           ws.size() * 4, nullptr)) {
+      fprintf(stderr, "sf_o_proj_residual failed\n");
+      return 1;
+    }
+    Checker co{"o_proj + residual"};
+    for (int r = 0; r < M; ++r)
+      for (int c = 0; c < D; ++c) {
+        double y = 0, mag = 0;
+        for (int k = 0; k < D; ++k) {
+          y += fb(o[(size_t)r * D + k]) * fb(wo[(size_t)c * D + k]);
+          mag += std::fabs(fb(o[(size_t)r * D + k]) * fb(wo[(size_t)c * D + k]));
+        }
+        // a one-step flip of bf16(y) carries through the residual sum
+        const double uy = std::ldexp(1.0, std::ilogb(std::fabs(y) + 1e-30) - 7);
+        co.add(hp[(size_t)r * D + c], (double)(float)(fb(x[(size_t)r * D + c]) + fb(bf(y))), mag, uy);
+      }
+    ok &= co.report();
+
+    const int V = 256;
+    auto wl = rnd((size_t)V * D, 0.05f);
+    const auto pl = pack(wl, V, D);
+    std::vector<uint16_t> logits((size_t)M * V);
+    if (sf_lm_head(x.data(), M, pl.data(), D, V, logits.data(), nullptr)) {
+      fprintf(stderr, "sf_lm_head failed\n");
+      return 1;
+    }
+    Checker cl{"lm_head"};
+    for (int m = 0; m < M; ++m)
+      for (int v = 0; v < V; ++v) {
+        double y = 0, mag = 0;
+        for (int k = 0; k < D; ++k) {
+          y += fb(x[(size_t)m * D + k]) * fb(wl[(size_t)v * D + k]);
+          mag += std::fabs(fb(x[(size_t)m * D + k]) * fb(wl[(size_t)v * D + k]));
+        }
+        cl.add(logits[(size_t)m * V + v], y, mag);
+      }
+    ok &= cl.report();
+  }
+  printf("D=%d I=%d count=%d bucket=%d M=%d: %s\n", D, I, count, bucket, M, ok ? "OK" : "FAIL");
+  return ok ? 0 : 1;
+}

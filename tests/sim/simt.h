@@ -120,6 +120,26 @@ inline long long min(long long a, long long b) { return a < b ? a : b; }
 inline float sim_exp2f(float x) { return std::exp2(x); }
 #define __builtin_amdgcn_exp2f(x) sim_exp2f(x)
 
+// fp32 -> fp16 rounded toward zero (v_cvt_pkrtz_f16_f32), two at a time
+typedef _Float16 sim_half2 __attribute__((ext_vector_type(2)));
+inline uint16_t sim_f_to_f16_rtz(float f) {
+  const uint32_t u = __float_as_uint(f), s = (u >> 16) & 0x8000u;
+  const int e = (int)((u >> 23) & 255) - 127 + 15;
+  const uint32_t m = u & 0x7fffffu;
+  if (((u >> 23) & 255) == 255) return (uint16_t)(s | 0x7c00u | (m ? 0x200u : 0));
+  if (e >= 31) return (uint16_t)(s | 0x7bffu);                  // toward zero: largest finite
+  if (e <= 0) {                                                  // subnormal or zero
+    if (e < -10) return (uint16_t)s;
+    return (uint16_t)(s | ((m | 0x800000u) >> (14 - e)));
+  }
+  return (uint16_t)(s | (e << 10) | (m >> 13));
+}
+inline sim_half2 sim_cvt_pkrtz(float a, float b) {
+  const uint32_t w = (uint32_t)sim_f_to_f16_rtz(a) | ((uint32_t)sim_f_to_f16_rtz(b) << 16);
+  return __builtin_bit_cast(sim_half2, w);
+}
+#define __builtin_amdgcn_cvt_pkrtz(a, b) sim_cvt_pkrtz(a, b)
+
 // ---- MFMA ----------------------------------------------------------------------------
 // Operands are 8 16-bit values per lane (bf16 or fp16 bit patterns).
 typedef uint16_t sim_h8 __attribute__((ext_vector_type(8)));

@@ -1,5 +1,8 @@
-"""The attention kernels' own source (specfold_amd/csrc/sf_attn.hip) run on the
-CPU through the SIMT simulator of tests/sim (fibers per work-item, barriers,
+"""Kernel sources run on the CPU through the SIMT simulator of tests/sim: the
+attention kernels (specfold_amd/csrc/sf_attn.hip) here, the GEMM kernels in
+test_sim_gemm.py.
+
+The attention kernels' own source runs in the simulator (fibers per work-item, barriers,
 wave-collective MFMA and shuffles from the documented operand layouts), called
 through the library's entry point sf_attn_prefix_block with its host checks and
 launch arithmetic, and checked against a float64 restatement of the attention.
