@@ -7,6 +7,8 @@
 //                       rows not in `rows` stay untouched
 //   sf_o_proj_residual  hp[r] = bf16(x[r] + bf16(o[r] . Wo^T)), r < M (static M)
 //   sf_lm_head          logits[m] = bf16(x[m] . W^T), m < M
+//   sf_qkv_rope         q / k / v of the recomputed rows: bias, RoPE from absolute
+//                       position tables, the optional q scale, scatter by flat row
 // A result may differ from the rounded float64 value where the fp32 sum (another
 // summation order) lies next to a rounding boundary, or where the sum cancels:
 // the check allows two bf16 steps plus 1e-6 of the sum of the terms' magnitudes
@@ -200,6 +202,95 @@ int main(int argc, char** argv) {
         cl.add(logits[(size_t)m * V + v], y, mag);
       }
     ok &= cl.report();
+  }
+  // ---- QKV projection + bias + RoPE (+ q scale) + scatter ----------------------------------
+  // the reference's op sequence (fastdllm_v2_folded.py:151-161, nld_folded.py:173-174):
+  // y = bf16(x . W^T + b); rope: bf16(bf16(y * cos) + bf16(rotate_half(y) * sin)) for q
+  // and k heads, rotate_half(y)[d] = -y[d + 64] (d < 64), y[d - 64] (d >= 64); then
+  // for q heads bf16(q * bf16(q_scale[n])); written to row `row` of q_buf / kv_buf
+  for (int with_scale = 0; with_scale < 2; ++with_scale) {
+    const int H = 4, Hkv = 2, hd = 128, N = 16, nq = (H + 2 * Hkv) * hd;
+    const int BNq = std::max(bucket, count) + 5;
+    auto xn = rnd((size_t)BNq * D, 1.f);
+    auto w = rnd((size_t)nq * D, 0.05f), bias = rnd(nq, 0.5f);
+    const auto pw = pack(w, nq, D);
+    const int table_rows = 300;
+    std::vector<uint16_t> cs((size_t)table_rows * hd), sn((size_t)table_rows * hd);
+    for (int t = 0; t < table_rows; ++t)
+      for (int d = 0; d < hd; ++d) {
+        const double ang = t / std::pow(10000.0, (2.0 * (d % 64)) / hd);
+        cs[(size_t)t * hd + d] = bf(std::cos(ang));
+        sn[(size_t)t * hd + d] = bf(std::sin(ang));
+      }
+    std::vector<int32_t> rows(bucket);
+    {
+      std::vector<int32_t> perm(BNq);
+      for (int i = 0; i < BNq; ++i) perm[i] = i;
+      std::shuffle(perm.begin(), perm.end(), rng);
+      std::sort(perm.begin(), perm.begin() + count);
+      for (int m = 0; m < bucket; ++m) rows[m] = m < count ? perm[m] : BNq;
+    }
+    std::vector<float> qs(N);
+    for (int n = 0; n < N; ++n) qs[n] = 1.0f + 0.03f * n;
+    int32_t cnt = count, pos0 = 117;
+    std::vector<uint16_t> qb((size_t)(BNq + 1) * H * hd, 0x1234), kvb((size_t)(BNq + 1) * 2 * Hkv * hd, 0x1234);
+    std::vector<float> ws(sf_qkv_workspace_bytes(bucket, D, nq) / 4 + 16);
+    const int st = sf_qkv_rope(xn.data(), rows.data(), &cnt, bucket, BNq, pw.data(), bias.data(),
+                               cs.data(), sn.data(), &pos0, table_rows,
+                               with_scale ? qs.data() : nullptr, N, D, H, Hkv, hd, qb.data(),
+                               kvb.data(), ws.data(), ws.size() * 4, nullptr);
+    if (st) {
+      fprintf(stderr, "sf_qkv_rope returned %d\n", st);
+      return 1;
+    }
+    Checker cq{with_scale ? "qkv + rope + q scale" : "qkv + rope"};
+    std::vector<char> written(BNq + 1, 0);
+    for (int m = 0; m < count; ++m) {
+      const int row = rows[m], n = row % N, tr = std::min(pos0 + n, table_rows - 1);
+      written[row] = 1;
+      std::vector<double> y(nq), mag(nq);
+      for (int c = 0; c < nq; ++c) {
+        double a = 0, g = 0;
+        for (int k = 0; k < D; ++k) {
+          a += fb(xn[(size_t)row * D + k]) * fb(w[(size_t)c * D + k]);
+          g += std::fabs(fb(xn[(size_t)row * D + k]) * fb(w[(size_t)c * D + k]));
+        }
+        y[c] = a + fb(bias[c]);
+        mag[c] = g;
+      }
+      for (int hh = 0; hh < H + 2 * Hkv; ++hh)
+        for (int d = 0; d < hd; ++d) {
+          const int c = hh * hd + d;
+          const double yb = fb(bf(y[c]));
+          double out = yb;
+          double slack = 0;
+          if (hh < H + Hkv) {
+            const double rot = d < 64 ? -fb(bf(y[c + 64])) : fb(bf(y[c - 64]));
+            const double a1 = fb(bf((float)(yb * fb(cs[(size_t)tr * hd + d]))));
+            const double a2 = fb(bf((float)(rot * fb(sn[(size_t)tr * hd + d]))));
+            out = (double)(float)(a1 + a2);
+            // a one-step flip of either rounded input carries through the rope sum
+            slack = std::ldexp(1.0, std::ilogb(std::fabs(a1) + 1e-30) - 7) +
+                    std::ldexp(1.0, std::ilogb(std::fabs(a2) + 1e-30) - 7);
+            if (hh < H && with_scale) {
+              const double q = fb(bf(out));
+              out = (double)(float)(q * fb(bf(qs[n])));
+              slack *= 2;
+            }
+          }
+          const uint16_t got = hh < H ? qb[((size_t)row * H + hh) * hd + d]
+                                      : kvb[((size_t)row * 2 * Hkv + (hh - H)) * hd + d];
+          cq.add(got, out, mag[c], slack);
+        }
+    }
+    long touched = 0;
+    for (int r = 0; r <= BNq; ++r)
+      if (!written[r]) {
+        for (int e = 0; e < H * hd; ++e) touched += qb[(size_t)r * H * hd + e] != 0x1234;
+        for (int e = 0; e < 2 * Hkv * hd; ++e) touched += kvb[(size_t)r * 2 * Hkv * hd + e] != 0x1234;
+      }
+    printf("  %-22s %s\n", "qkv: other rows", touched ? "OVERWRITTEN" : "untouched");
+    ok &= cq.report() && touched == 0;
   }
   printf("D=%d I=%d count=%d bucket=%d M=%d: %s\n", D, I, count, bucket, M, ok ? "OK" : "FAIL");
   return ok ? 0 : 1;

@@ -2,8 +2,9 @@
 sf_qkv.hip, sf_gemm_core.h) run on the CPU through the SIMT simulator of
 tests/sim, called through the library's entry points: weight packing, FFN
 gate/up (whole tiles, SiLU epilogue), FFN down (stream-K with partial slots,
-fix-up, row scatter), o_proj + residual and lm_head (static row counts), over one
-to four 64-row blocks, against float64 dot products rounded as each epilogue
+fix-up, row scatter), o_proj + residual and lm_head (static row counts), and the
+QKV projection with bias, RoPE from absolute-position tables, the optional q
+scale and the scatter by flat row, over one to four 64-row blocks, against float64 dot products rounded as each epilogue
 specifies (tests/sim/gemm_sim.cpp states the tolerance)."""
 
 import shutil
