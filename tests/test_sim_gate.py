@@ -1,0 +1,140 @@
+"""The integer core of the folded verify step, on the CPU: the kernels' own
+sources for the delta gate and fold compaction (sf_fold_gate, with the
+previous layer's residual fused in: sf_fold_gate_residual) and the branch parent
+map (sf_parent_map), built for the SIMT simulator of tests/sim and driven through
+the library's own Python wrappers (tests/simlib.py), against the same CPU
+restatements of the reference the GPU tests use (recompute mask, compacted rows,
+src, one-hop parents, segments: bit-exact; rstd and normalized rows: rounding)."""
+
+import pytest
+import torch
+
+from oracle.folded_reference import parent_map
+from specfold_amd import _lib
+from specfold_amd.engine import build_parent_map
+from specfold_amd.synthetic import TREE_PARENTS, draft_tree_block, perturbed_hidden
+from tests.simlib import build_sim_library, compiler, use_sim_library
+from tests.test_gpu_gate import check_outputs, ref_mask
+
+
+@pytest.fixture(scope="module")
+def sim(tmp_path_factory):
+    if compiler() is None:
+        pytest.skip("no clang++ (the simulator needs clang's vector extensions)")
+    path = build_sim_library(tmp_path_factory.mktemp("simlib"))
+    with use_sim_library(path) as lib:
+        yield lib
+
+
+def gate_outputs(B1, N, D, bucket):
+    BN = B1 * N
+    i32 = dict(dtype=torch.int32)
+    return dict(rec=torch.zeros(BN, dtype=torch.int8), f=torch.zeros(BN, **i32),
+                src=torch.zeros(BN, **i32), rows=torch.full((bucket,), -7, **i32),
+                count=torch.zeros(1, **i32), seg=torch.full((BN,), -1, **i32),
+                segcnt=torch.zeros(B1, **i32), rstd=torch.zeros(BN, dtype=torch.float32),
+                xn=torch.zeros(BN, D, dtype=torch.bfloat16))
+
+
+def run_gate(lib, hidden, parent, ln_w, delta, mode, bucket=None, eps=1e-6):
+    B1, N, D = hidden.shape
+    bucket = B1 * N if bucket is None else bucket
+    par = torch.tensor([0] + [int(p) for p in parent[1:]], dtype=torch.int32)
+    out = gate_outputs(B1, N, D, bucket)
+    lib.fold_gate(hidden.reshape(B1 * N, D).contiguous(), par, ln_w, B1, N, bucket, delta, eps,
+                  mode, out["rec"], out["f"], out["src"], out["rows"], out["count"], out["seg"],
+                  out["segcnt"], out["rstd"], out["xn"])
+    return out
+
+
+@pytest.mark.parametrize("mode", [_lib.SF_GATE_MODEL_DTYPE, _lib.SF_GATE_FP32_SQUARED])
+def test_gate_tree(sim, mode):
+    gen = torch.Generator().manual_seed(11 + mode)
+    parents = list(TREE_PARENTS)
+    hidden = perturbed_hidden(parents, 32, 1536, gen)
+    ln_w = (1 + 0.1 * torch.randn(1536, generator=gen)).to(torch.bfloat16)
+    rec = ref_mask(hidden, parents, 0.1, mode)
+    out = run_gate(sim, hidden, parents, ln_w, 0.1, mode)
+    check_outputs(out, hidden, parents, rec, ln_w)
+    assert 0.3 < 1 - rec[1:].float().mean() < 0.9   # both outcomes occur
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_gate_random_forests_and_bucket(sim, seed):
+    gen = torch.Generator().manual_seed(200 + seed)
+    B1 = int(torch.randint(2, 17, (1,), generator=gen))
+    N = int(torch.randint(4, 64, (1,), generator=gen))
+    main = torch.randint(0, 5, (N,), generator=gen)
+    toks = main.repeat(B1, 1)
+    for i in range(1, B1):
+        m = torch.rand(N, generator=gen) < 0.15
+        toks[i][m] = torch.randint(5, 9, (int(m.sum()),), generator=gen)
+    parents = build_parent_map(toks)[0]
+    D = 256
+    hidden = torch.zeros(B1, N, D)
+    hidden[0] = torch.randn(N, D, generator=gen)
+    for i in range(1, B1):
+        hidden[i] = hidden[parents[i]] + 0.2 * torch.rand(N, 1, generator=gen) * \
+            torch.randn(N, D, generator=gen)
+    hidden = hidden.to(torch.bfloat16)
+    ln_w = torch.ones(D, dtype=torch.bfloat16)
+    delta = float(torch.rand(1, generator=gen)) * 0.2
+    rec = ref_mask(hidden, parents, delta, _lib.SF_GATE_MODEL_DTYPE)
+    bucket = max(1, int(rec.sum()) - 3) if seed == 2 else None   # last: an overflowing bucket
+    out = run_gate(sim, hidden, parents, ln_w, delta, _lib.SF_GATE_MODEL_DTYPE, bucket=bucket)
+    check_outputs(out, hidden, parents, rec, ln_w, bucket=bucket)
+
+
+def test_gate_residual_fused(sim):
+    """Layer > 0: the input x = bf16(hp + ffn[src_prev*N + n]) is formed inside the
+    gate (written to hidden_out) and then gated exactly like sf_fold_gate's input."""
+    gen = torch.Generator().manual_seed(5)
+    parents = list(TREE_PARENTS)
+    B1, N, D = len(parents), 32, 512
+    x = perturbed_hidden(parents, N, D, gen)
+    hp = (x.float() * 0.5).to(torch.bfloat16)
+    src_prev = torch.randint(0, B1, (B1 * N,), generator=gen, dtype=torch.int32)
+    src_prev[:N] = 0
+    ffn = torch.randn(B1 * N, D, generator=gen).to(torch.bfloat16) * 0.01
+    # the residual rows the kernel forms, and the gate they must then produce
+    r = torch.arange(B1 * N)
+    xin = (hp.reshape(B1 * N, D).float() + ffn[(src_prev.long() * N + r % N)].float())
+    xin = xin.to(torch.bfloat16).view(B1, N, D)
+    ln_w = torch.ones(D, dtype=torch.bfloat16)
+    rec = ref_mask(xin, parents, 0.1, _lib.SF_GATE_MODEL_DTYPE)
+    out = gate_outputs(B1, N, D, B1 * N)
+    par = torch.tensor([0] + [int(p) for p in parents[1:]], dtype=torch.int32)
+    hidden_out = torch.zeros(B1 * N, D, dtype=torch.bfloat16)
+    sim.fold_gate_residual(hp.reshape(B1 * N, D), ffn, src_prev, par, ln_w, B1, N, D, B1 * N, 0.1,
+                           1e-6, _lib.SF_GATE_MODEL_DTYPE, hidden_out, out["rec"], out["f"],
+                           out["src"], out["rows"], out["count"], out["seg"], out["segcnt"],
+                           None, out["rstd"], out["xn"])
+    assert torch.equal(hidden_out.view(B1, N, D), xin)
+    check_outputs(out, xin, parents, rec, ln_w)
+
+
+def device_map(lib, tokens):
+    B1 = tokens.shape[0]
+    par = torch.full((B1,), -1, dtype=torch.int32)
+    cnt = torch.full((B1,), -1, dtype=torch.int32)
+    lib.parent_map(tokens.contiguous(), par, cnt)
+    return par.tolist(), cnt.tolist()
+
+
+def oracle_map(tokens):
+    parent, counts = parent_map(tokens)
+    return [0] + [int(p) for p in parent[1:]], [int(c) for c in counts]
+
+
+def test_parent_map(sim):
+    g = torch.Generator().manual_seed(9)
+    for _ in range(3):
+        tokens = draft_tree_block(32, 151936, g)
+        assert device_map(sim, tokens) == oracle_map(tokens)
+    for B1, N, vocab in [(8, 32, 3), (64, 64, 2), (17, 7, 3), (1, 32, 10)]:
+        for _ in range(4):
+            main = torch.randint(0, vocab, (1, N), generator=g)
+            flips = torch.rand(B1, N, generator=g) < 0.15
+            tokens = torch.where(flips, torch.randint(0, vocab, (B1, N), generator=g), main)
+            tokens[0] = main[0]
+            assert device_map(sim, tokens) == oracle_map(tokens)
