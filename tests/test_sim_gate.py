@@ -1,10 +1,13 @@
-"""The integer core of the folded verify step, on the CPU: the kernels' own
-sources for the delta gate and fold compaction (sf_fold_gate, with the
-previous layer's residual fused in: sf_fold_gate_residual) and the branch parent
-map (sf_parent_map), built for the SIMT simulator of tests/sim and driven through
-the library's own Python wrappers (tests/simlib.py), against the same CPU
-restatements of the reference the GPU tests use (recompute mask, compacted rows,
-src, one-hop parents, segments: bit-exact; rstd and normalized rows: rounding)."""
+"""The integer core of the folded verify step and the attention of folded rows,
+on the CPU: the kernels' own sources for the delta gate and fold compaction
+(sf_fold_gate, with the previous layer's residual fused in:
+sf_fold_gate_residual), the branch parent map (sf_parent_map) and the chain
+correction (sf_chain_correct, after sf_attn_prefix_block), built for the SIMT
+simulator of tests/sim and driven through the library's own Python wrappers
+(tests/simlib.py).  Against the same CPU restatements of the reference the GPU
+tests use (recompute mask, compacted rows, src, one-hop parents, segments:
+bit-exact; rstd and normalized rows: rounding) and, for attention, float64
+attention of every row of the folded step."""
 
 import pytest
 import torch
@@ -138,3 +141,76 @@ def test_parent_map(sim):
             tokens = torch.where(flips, torch.randint(0, vocab, (B1, N), generator=g), main)
             tokens[0] = main[0]
             assert device_map(sim, tokens) == oracle_map(tokens)
+
+
+@pytest.mark.parametrize("P,seed", [(0, 1), (70, 2), (300, 3)])
+def test_gate_attention_chain(sim, P, seed):
+    """Gate -> attention of the recomputed rows -> chain correction of the folded
+    rows, every row then checked against float64 attention of the folded step:
+    row (b, n) attends with the query of its source row src[b*N+n]*N + n over the
+    prefix and the block keys src[b*N+j]*N + j (the nearest recomputing ancestor's
+    K/V at every block position).  A folded row may keep an upper bound of its
+    row maximum (the ancestor's, when a changed key held it), so (m, Z) is checked
+    through the log-sum-exp m + log Z."""
+    gen = torch.Generator().manual_seed(seed)
+    parents = list(TREE_PARENTS)
+    B1, N, D, H, Hkv, hd = len(parents), 16, 256, 4, 2, 128
+    BN = B1 * N
+    hidden = perturbed_hidden(parents, N, D, gen)
+    ln_w = torch.ones(D, dtype=torch.bfloat16)
+    g = run_gate(sim, hidden, parents, ln_w, 0.1, _lib.SF_GATE_MODEL_DTYPE)
+    rec = g["rec"].view(B1, N).bool()
+    assert 0 < int((~rec).sum()) and int(rec[1:].sum()) > 0
+    q = torch.randn((BN + 1) * H * hd, generator=gen).to(torch.bfloat16)
+    kv = torch.randn((BN + 1) * 2 * Hkv * hd, generator=gen).to(torch.bfloat16)
+    ps = 16
+    npages = max(1, (P + ps - 1) // ps)
+    pk = torch.randn(npages * Hkv * ps * hd, generator=gen).to(torch.bfloat16)
+    pv = torch.randn(npages * Hkv * ps * hd, generator=gen).to(torch.bfloat16)
+    table = torch.randperm(npages, generator=gen).to(torch.int32)
+    o32 = torch.full((BN * H * hd,), float("nan"))
+    obf = torch.zeros(BN * H * hd, dtype=torch.bfloat16)
+    mt = torch.full((BN * H,), float("nan"))
+    zt = torch.full((BN * H,), float("nan"))
+    nws = max(sim.attn_workspace_bytes(BN, H, P), 256)
+    raw = torch.zeros(nws + 256, dtype=torch.uint8)          # a 256-byte aligned view
+    off = (-raw.data_ptr()) % 256
+    ws = raw[off:off + nws]
+    scaling = hd ** -0.5
+    par = torch.tensor([0] + [int(p) for p in parents[1:]], dtype=torch.int32)
+    sim.attn_prefix_block(q, kv, pk, pv, table, P, ps, Hkv * ps * hd, ps * hd, g["src"], g["rows"],
+                          g["count"], BN, B1, N, H, Hkv, hd, scaling, o32, obf, mt, zt, ws)
+    sim.chain_correct(q, kv, g["src"], par, g["rec"], g["seg"], g["segcnt"], B1, N, H, Hkv, hd,
+                      scaling, o32, obf, mt, zt)
+    G = H // Hkv
+    qv = q.double().view(BN + 1, H, hd)
+    kvv = kv.double().view(BN + 1, 2, Hkv, hd)
+    src = g["src"].long()
+
+    def prefix(t, h):
+        rows = [t.view(npages, Hkv, ps, hd)[int(table[p // ps]), h, p % ps] for p in range(P)]
+        return torch.stack(rows).double() if rows else torch.zeros(0, hd, dtype=torch.float64)
+    pref = [(prefix(pk, h), prefix(pv, h)) for h in range(Hkv)]
+    worst_o = worst_lse = 0.0
+    for b in range(B1):
+        blk = src[b * N:(b + 1) * N] * N + torch.arange(N)
+        for n in range(N):
+            r = b * N + n
+            qrow = int(src[r]) * N + n
+            for hq in range(H):
+                h = hq // G
+                keys = torch.cat([pref[h][0], kvv[blk, 0, h]])
+                vals = torch.cat([pref[h][1], kvv[blk, 1, h]])
+                s = keys @ qv[qrow, hq] * scaling
+                m = float(s.max())
+                p = torch.exp(s - m)
+                z = float(p.sum())
+                o = (p @ vals) / z
+                got_o = o32.view(BN, H, hd)[r, hq].double()
+                worst_o = max(worst_o, float((got_o - o).abs().max()) / max(1.0, float(o.abs().max())))
+                lse_got = float(mt.view(BN, H)[r, hq]) + float(torch.log(zt.view(BN, H)[r, hq].double()))
+                worst_lse = max(worst_lse, abs(lse_got - (m + float(torch.log(torch.tensor(z, dtype=torch.float64))))))
+                assert float(mt.view(BN, H)[r, hq]) >= m - 1e-4
+    print(f"P={P}: O max err {worst_o:.3g}, lse max err {worst_lse:.3g}, "
+          f"folded rows {int((~rec).sum())}")
+    assert worst_o <= 2e-5 and worst_lse <= 2e-5
