@@ -162,8 +162,7 @@ class FoldedVerifyEngine:
         self.device = base.embed_tokens.weight.device
         if base.embed_tokens.weight.dtype != torch.bfloat16:
             raise TypeError("the HIP verify step runs bf16 models")
-        if self.device.type != "cuda":
-            raise ValueError("the HIP verify step needs the model on a GPU")
+        self._check_device(self.device)
         self.eps = float(rms_eps if rms_eps is not None else
                          getattr(cfg, "rms_norm_eps", 1e-6))
         self.gate_mode = gate_mode
@@ -192,6 +191,12 @@ class FoldedVerifyEngine:
         self.max_graphs = 48
         self._graphs: Dict[tuple, tuple] = {}
         self._rope: Optional[Tuple[torch.Tensor, torch.Tensor]] = None
+
+    @staticmethod
+    def _check_device(device: torch.device) -> None:
+        """The kernels run on the GPU only; there is no CPU path."""
+        if device.type != "cuda":
+            raise ValueError("the HIP verify step needs the model on a GPU")
 
     # ------------------------------------------------------------------------
     def buffers(self, B1: int, N: int, bucket: int, P: int) -> _Buffers:

@@ -99,6 +99,24 @@ inline float __shfl_xor(float v, int mask, int width = 64) {
   return out;
 }
 
+inline unsigned long long __ballot(int pred) {
+  const int mine = pred != 0;
+  unsigned long long m = 0;
+  sim_wave_exchange(&mine, 4, [&](const uint8_t* b) {
+    for (int l = 0; l < 64; ++l) {
+      int v;
+      memcpy(&v, b + l * 128, 4);
+      if (v) m |= 1ull << l;
+    }
+  });
+  return m;
+}
+inline int __popcll(unsigned long long x) { return __builtin_popcountll(x); }
+
+// device-scope atomics: workgroups run concurrently on the pool threads
+inline unsigned atomicAdd(unsigned* p, unsigned v) { return __atomic_fetch_add(p, v, __ATOMIC_RELAXED); }
+inline int atomicAdd(int* p, int v) { return __atomic_fetch_add(p, v, __ATOMIC_RELAXED); }
+
 // ---- scalar helpers ------------------------------------------------------------------
 inline float __uint_as_float(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
 inline uint32_t __float_as_uint(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
@@ -220,7 +238,10 @@ inline float2 make_float2(float x, float y) { return float2{x, y}; }
 #define __host__
 #define __forceinline__ inline
 #define __launch_bounds__(...)
-#define __shared__ static thread_local
+// LDS objects start 16-byte aligned on the GPU (a kernel's first object at offset
+// 0); the simulator gives its thread_local stand-ins the same alignment, which the
+// host's 16-byte vector loads and stores need.
+#define __shared__ static thread_local __attribute__((aligned(16)))
 typedef void* hipStream_t;
 typedef int hipError_t;
 #define hipSuccess 0
