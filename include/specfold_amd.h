@@ -254,9 +254,11 @@ int sf_lm_head(const uint16_t* x, int M, const uint16_t* w, int D, int V, uint16
  *               including the first token that carries it past top_p * Z
  *   greedy_tok [M], conf [M]   the argmax of the bf16 nucleus probabilities
  *               bf16(e_i / znuc) (lowest index among equal) and bf16(1/znuc)
- * workspace: sf_logit_stats_workspace_bytes(M) bytes, zero before the first call
- * (every call leaves it zero).  Limits: V % 8 == 0, ld % 8 == 0, 16-byte aligned
- * logits, 0 < top_p (top_p >= 1 keeps every token).
+ * workspace: sf_logit_stats_workspace_bytes(M) bytes, zero before the first call:
+ * its first M * 65536 32-bit counters are value histograms that every call leaves
+ * zero again; the rest is scratch each call overwrites before reading.
+ * Limits: V % 8 == 0, ld % 8 == 0, 16-byte aligned logits, 0 < top_p (top_p >= 1
+ * keeps every token).
  */
 size_t sf_logit_stats_workspace_bytes(int M);
 int sf_logit_stats(const uint16_t* logits, int M, int V, long long ld, float top_p,

@@ -214,3 +214,72 @@ def test_gate_attention_chain(sim, P, seed):
     print(f"P={P}: O max err {worst_o:.3g}, lse max err {worst_lse:.3g}, "
           f"folded rows {int((~rec).sum())}")
     assert worst_o <= 2e-5 and worst_lse <= 2e-5
+
+
+# -- greedy decode statistics (sf_logit_stats) and the paged KV append ------------------
+
+def sim_logit_stats(lib, logits, top_p, ws=None):
+    """sf_logit_stats on CPU rows, with the wrapper's argument layout (the wrapper
+    itself accepts GPU tensors only)."""
+    M, V = logits.shape
+    x = logits.contiguous()
+    need = int(lib._LIB.sf_logit_stats_workspace_bytes(M))
+    ws = torch.zeros(need, dtype=torch.uint8) if ws is None else ws
+    out = lib.LogitStats(M, "cpu")
+    st = lib._LIB.sf_logit_stats(lib._ptr(x), M, V, V, float(top_p), lib._ptr(out.top_idx),
+                                 lib._ptr(out.top_val), lib._ptr(out.zfull), lib._ptr(out.znuc),
+                                 lib._ptr(out.greedy_tok), lib._ptr(out.conf),
+                                 lib._ptr(out.conf_full), lib._ptr(ws), ws.numel(), None)
+    assert st == 0
+    return out, ws
+
+
+@pytest.mark.parametrize("M,V,scale,top_p", [(4, 152064, 1.0, 0.95), (3, 20000, 3.0, 0.5),
+                                             (2, 131072, 0.3, 1.0)])
+def test_logit_stats(sim, M, V, scale, top_p):
+    """Against the reference sampler's torch sequence on the CPU and the softmax /
+    topk statistics (the checks of the GPU test, tests/test_gpu_logit_stats.py)."""
+    from tests.test_gpu_logit_stats import nucleus_mass64, reference_greedy, ulp_bf16
+    g = torch.Generator().manual_seed(M * 31 + V)
+    logits = (torch.randn(M, V, generator=g) * scale).to(torch.bfloat16)
+    logits[0, 17] = logits[0].max() + 2.0           # a clear winner in one row
+    st, ws = sim_logit_stats(sim, logits, top_p)
+    assert torch.equal(st.top_idx[:, 0].long(), torch.argmax(logits, dim=-1))
+    assert torch.equal(st.top_val, torch.topk(logits.float(), 8, dim=-1).values)
+    zn64, z64 = nucleus_mass64(logits, top_p)
+    assert torch.allclose(st.zfull.double(), z64, rtol=1e-5)
+    assert bool(((st.znuc.double() - zn64).abs() <= 1e-5 * z64 + 2.0).all())
+    tok, conf = reference_greedy(logits, top_p)
+    same = st.conf == conf.float()
+    assert bool(((st.conf - conf.float()).abs() <= ulp_bf16(conf)).all())
+    assert torch.equal(st.greedy_tok[same].long(), tok[same])
+    cfull = torch.softmax(logits, dim=-1).max(dim=-1).values
+    assert bool(((st.conf_full - cfull.float()).abs() <= ulp_bf16(cfull)).all())
+    # the histograms (the workspace's first M x 65536 counters) are left zero; the
+    # per-slice candidates after them are overwritten by every call; a second call
+    # on the same workspace gives the same statistics
+    assert int(ws[:M * 65536 * 4].count_nonzero()) == 0
+    st2, _ = sim_logit_stats(sim, logits, top_p, ws)
+    for f in ("top_idx", "top_val", "zfull", "znuc", "greedy_tok", "conf", "conf_full"):
+        assert torch.equal(getattr(st, f), getattr(st2, f)), f
+
+
+def test_kv_append_paged(sim):
+    """The block's K/V rows land at positions start .. start+n_tok of a paged cache
+    (shuffled pages), every other cache element untouched."""
+    g = torch.Generator().manual_seed(4)
+    Hkv, hd, ps, npages, n_tok, start, row0 = 2, 128, 16, 9, 32, 37, 5
+    kv = torch.randn((row0 + n_tok + 2) * 2 * Hkv * hd, generator=g).to(torch.bfloat16)
+    kc = torch.full((npages * Hkv * ps * hd,), 7.0).to(torch.bfloat16)
+    vc = kc.clone()
+    table = torch.randperm(npages, generator=g).to(torch.int32)
+    sim.kv_append(kv, row0, n_tok, Hkv, hd, kc, vc, table, ps, Hkv * ps * hd, ps * hd, start)
+    kvv = kv.view(-1, 2, Hkv, hd)
+    expect_k, expect_v = torch.full_like(kc, 7.0).view(npages, Hkv, ps, hd), \
+        torch.full_like(vc, 7.0).view(npages, Hkv, ps, hd)
+    for t in range(n_tok):
+        p = start + t
+        expect_k[int(table[p // ps]), :, p % ps] = kvv[row0 + t, 0]
+        expect_v[int(table[p // ps]), :, p % ps] = kvv[row0 + t, 1]
+    assert torch.equal(kc.view_as(expect_k), expect_k)
+    assert torch.equal(vc.view_as(expect_v), expect_v)
