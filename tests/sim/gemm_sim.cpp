@@ -115,7 +115,14 @@ int main(int argc, char** argv) {
         }
         const double gt = fb(bf(g));
         const double s = fb(bf((float)gt / (1.0f + expf(-(float)gt))));
-        cg.add(act[(size_t)m * I + c], (double)(float)(s * fb(bf(u))), mg + mu);
+        // a one-step flip of bf16(g) or bf16(u) (their fp32 sums next to a rounding
+        // boundary) carries through silu and the product
+        const double sig = 1.0 / (1.0 + std::exp(-gt));
+        const double dsilu = std::fabs(sig * (1.0 + gt * (1.0 - sig)));
+        const double ug = std::ldexp(1.0, std::ilogb(std::fabs(gt) + 1e-30) - 7);
+        const double uu = std::ldexp(1.0, std::ilogb(std::fabs(u) + 1e-30) - 7);
+        const double flip = dsilu * ug * std::fabs(u) + std::fabs(s) * uu;
+        cg.add(act[(size_t)m * I + c], (double)(float)(s * fb(bf(u))), mg + mu, flip);
       }
     ok &= cg.report();
 

@@ -48,6 +48,7 @@ def gemm_sim(tmp_path_factory):
 @pytest.mark.parametrize("case", [
     (256, 384, 39, 64, 40, 1),      # D, I, count, bucket, M, seed: one row block
     (384, 512, 100, 128, 70, 2),    # two row blocks
+    (384, 512, 117, 128, 117, 7),   # the recomputed-row count of a trained 7B model
     (512, 640, 130, 256, 130, 3),   # three of four row blocks in use
     (256, 384, 1, 256, 1, 4),       # a single row
     (640, 768, 200, 256, 256, 5),   # four full row blocks for the static-M GEMMs
