@@ -47,10 +47,17 @@ extern "C" {
                                   (specfold/generate/triton_kernels.py:227-230) */
 #define SF_GATE_ALL 2          /* every row recomputed: the dense block forward
                                   (specfold/generate/fastdllm_v2_generation.py:151-186) */
+/* Flag OR-ed into a gate mode: the always-recomputed root branches are those that
+   are their own parent (par[b] == b) instead of branch 0 alone, so one call gates
+   several sequences' branch trees laid out one after another (a batched verify
+   step; each sequence's main branch has par[b] == b).  No counterpart in the
+   reference, whose verify step takes one sequence. */
+#define SF_GATE_ROOTS_BY_PARENT 16
 
 const char* sf_status_string(int status);
 /* 2: GEMM weights in the packed layout of sf_pack_weight; fused residual entries.
- * 3: sf_parent_map (the branch parent map on the device); sf_logit_stats. */
+ * 3: sf_parent_map (the branch parent map on the device); sf_logit_stats.
+ * 4: batched verify steps: SF_GATE_ROOTS_BY_PARENT, sf_qkv_rope_branches. */
 int sf_abi_version(void);
 
 /*
@@ -131,6 +138,20 @@ int sf_qkv_rope(const uint16_t* xn, const int32_t* rows, const int32_t* count, i
                 const float* q_scale, int N, int D, int H, int Hkv, int hd,
                 uint16_t* q_buf, uint16_t* kv_buf, void* workspace, size_t workspace_bytes,
                 void* stream);
+/* sf_qkv_rope for a batched verify step: the branch trees of several sequences
+ * laid out one after another (BN = total branches * N), each sequence at its own
+ * prefix length.  pos0_branch: int32 [BN/N], the first absolute position of each
+ * branch's block (its sequence's prefix length), required; cos/sin [table_rows, hd]
+ * over absolute positions; q_scale_rows: optional fp32 [BN], the scale of each flat
+ * row.  Same GEMM, workspace and limits as sf_qkv_rope, plus BN % N == 0.  No
+ * counterpart in the reference (its verify step takes one sequence); a batch of
+ * one sequence gives the results of sf_qkv_rope. */
+int sf_qkv_rope_branches(const uint16_t* xn, const int32_t* rows, const int32_t* count, int bucket,
+                         int BN, const uint16_t* w_qkv, const uint16_t* b_qkv,
+                         const uint16_t* cos_tab, const uint16_t* sin_tab,
+                         const int32_t* pos0_branch, int table_rows, const float* q_scale_rows,
+                         int N, int D, int H, int Hkv, int hd, uint16_t* q_buf, uint16_t* kv_buf,
+                         void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * (3) Attention of the recomputed rows over [shared prefix ; own branch block],

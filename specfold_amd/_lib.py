@@ -21,6 +21,7 @@ SF_OK = 0
 SF_GATE_MODEL_DTYPE = 0
 SF_GATE_FP32_SQUARED = 1
 SF_GATE_ALL = 2
+SF_GATE_ROOTS_BY_PARENT = 16  # flag: roots are the branches with par[b] == b
 
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
@@ -40,6 +41,8 @@ SIGNATURES = {
     "sf_qkv_workspace_bytes": (_sz, [_i, _i, _i]),
     "sf_qkv_rope": (_i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _i, _vp,
                          _i, _i, _i, _i, _i, _vp, _vp, _vp, _sz, _vp]),
+    "sf_qkv_rope_branches": (_i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _i, _vp,
+                                  _i, _i, _i, _i, _i, _vp, _vp, _vp, _sz, _vp]),
     "sf_attn_workspace_bytes": (_sz, [_i, _i, _i]),
     "sf_attn_prefix_block": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _ll, _ll, _vp, _vp, _vp,
                                   _i, _i, _i, _i, _i, _i, _f, _vp, _i, _vp, _vp, _vp, _vp, _vp,
@@ -225,6 +228,38 @@ def qkv_rope(xn, rows, count, bucket, BN, w_qkv, b_qkv, cos, sin, q_scale, N, D,
                             _ptr(q_buf), _ptr(kv_buf), _ptr(workspace), workspace.numel(),
                             _stream(stream))
     _check(st, "sf_qkv_rope")
+
+
+def qkv_rope_branches(xn, rows, count, bucket, BN, w_qkv, b_qkv, cos, sin, q_scale_rows, N, D,
+                      H, Hkv, hd, q_buf, kv_buf, workspace, pos0_branch, stream=None) -> None:
+    """qkv_rope over a batched step's branches: ``pos0_branch`` int32 [BN/N] (each
+    branch's first absolute position), cos/sin [T, hd] tables over absolute
+    positions, ``q_scale_rows`` optional fp32 [BN]."""
+    nq = (H + 2 * Hkv) * hd
+    if BN % N:
+        raise ValueError(f"BN={BN} is not a multiple of N={N}")
+    _need(xn, "xn", torch.bfloat16, min_numel=BN * D)
+    _need(rows, "rows", torch.int32, min_numel=bucket, align=4)
+    _need(count, "count", torch.int32, min_numel=1, align=4)
+    _need(w_qkv, "w_qkv", torch.bfloat16, numel=nq * D)
+    if b_qkv is not None:
+        _need(b_qkv, "b_qkv", torch.bfloat16, numel=nq, align=4)
+    _need(pos0_branch, "pos0_branch", torch.int32, numel=BN // N, align=4)
+    table_rows = cos.numel() // hd
+    _need(cos, "cos", torch.bfloat16, numel=table_rows * hd, align=4)
+    _need(sin, "sin", torch.bfloat16, numel=cos.numel(), align=4)
+    if q_scale_rows is not None:
+        _need(q_scale_rows, "q_scale_rows", torch.float32, numel=BN, align=4)
+    _need(q_buf, "q_buf", torch.bfloat16, min_numel=(BN + 1) * H * hd)
+    _need(kv_buf, "kv_buf", torch.bfloat16, min_numel=(BN + 1) * 2 * Hkv * hd)
+    _need(workspace, "workspace", torch.uint8, min_numel=qkv_workspace_bytes(bucket, D, nq),
+          align=256)
+    st = load().sf_qkv_rope_branches(_ptr(xn), _ptr(rows), _ptr(count), bucket, BN, _ptr(w_qkv),
+                                     _ptr(b_qkv), _ptr(cos), _ptr(sin), _ptr(pos0_branch),
+                                     table_rows, _ptr(q_scale_rows), N, D, H, Hkv, hd,
+                                     _ptr(q_buf), _ptr(kv_buf), _ptr(workspace),
+                                     workspace.numel(), _stream(stream))
+    _check(st, "sf_qkv_rope_branches")
 
 
 def attn_workspace_bytes(bucket: int, H: int, P: int) -> int:

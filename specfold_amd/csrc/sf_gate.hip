@@ -20,7 +20,7 @@ constexpr int kMaxVecPerLane = 16;  // 16 x 8 bf16 x 64 lanes = 8192 columns
 // x[r] = bf16(hp[r] + ffn[src_prev[r]*N + n]) (the folded residual update of
 // fastdllm_v2_folded.py:218), for the row and for its parent row, and x[r] is
 // written to hidden_out.  `par` may be NULL (every row its own parent).
-template <int VPL, bool RESID>
+template <int VPL, bool RESID, bool ROOTS>
 __global__ __launch_bounds__(256) void sf_gate_rows_kernel(
     const uint16_t* __restrict__ hidden, const uint16_t* __restrict__ ffn,
     const int32_t* __restrict__ src_prev, const int32_t* __restrict__ par,
@@ -35,7 +35,10 @@ __global__ __launch_bounds__(256) void sf_gate_rows_kernel(
   const int n = r - b * N;
   int p = par ? par[b] : b;
   p = p < 0 ? 0 : (p >= B1 ? B1 - 1 : p);
-  const bool draft = b > 0 && mode != SF_GATE_ALL;
+  // a draft row is gated against its parent's; the root branch (branch 0, or with
+  // ROOTS every branch that is its own parent: the main branch of each sequence
+  // of a batched step) is always recomputed
+  const bool draft = (ROOTS ? p != b : b > 0) && mode != SF_GATE_ALL;
   const int pr = p * N + n;
 
   const int nvec = D >> 3;
@@ -198,40 +201,54 @@ __global__ __launch_bounds__(1024) void sf_gate_compact_kernel(
   if (t == 0) *count = total;
 }
 
-template <int VPL, bool RESID>
+template <int VPL, bool RESID, bool ROOTS>
 void launch_rows(const uint16_t* hidden, const uint16_t* ffn, const int32_t* src_prev,
                  const int32_t* par, const uint16_t* ln_w, int B1, int N, int D, float delta,
                  float eps, int mode, uint16_t* hidden_out, int8_t* rec, float* rstd,
                  uint16_t* xn, hipStream_t st) {
   const int BN = B1 * N;
   dim3 grid((BN + kGateWaves - 1) / kGateWaves);
-  hipLaunchKernelGGL((sf_gate_rows_kernel<VPL, RESID>), grid, dim3(256), 0, st, hidden, ffn,
+  hipLaunchKernelGGL((sf_gate_rows_kernel<VPL, RESID, ROOTS>), grid, dim3(256), 0, st, hidden, ffn,
                      src_prev, par, ln_w, B1, N, D, delta, eps, mode, hidden_out, rec, rstd, xn);
 }
 
-template <bool RESID>
+template <bool RESID, bool ROOTS>
 void launch_rows_any(int D, const uint16_t* hidden, const uint16_t* ffn, const int32_t* src_prev,
                      const int32_t* par, const uint16_t* ln_w, int B1, int N, float delta,
                      float eps, int mode, uint16_t* hidden_out, int8_t* rec, float* rstd,
                      uint16_t* xn, hipStream_t st) {
   const int vpl = (D / 8 + 63) / 64;
   if (vpl <= 4)
-    launch_rows<4, RESID>(hidden, ffn, src_prev, par, ln_w, B1, N, D, delta, eps, mode, hidden_out,
+    launch_rows<4, RESID, ROOTS>(hidden, ffn, src_prev, par, ln_w, B1, N, D, delta, eps, mode, hidden_out,
                           rec, rstd, xn, st);
   else if (vpl <= 8)
-    launch_rows<8, RESID>(hidden, ffn, src_prev, par, ln_w, B1, N, D, delta, eps, mode,
+    launch_rows<8, RESID, ROOTS>(hidden, ffn, src_prev, par, ln_w, B1, N, D, delta, eps, mode,
                           hidden_out, rec, rstd, xn, st);
   else if (vpl <= 12)
-    launch_rows<12, RESID>(hidden, ffn, src_prev, par, ln_w, B1, N, D, delta, eps, mode,
+    launch_rows<12, RESID, ROOTS>(hidden, ffn, src_prev, par, ln_w, B1, N, D, delta, eps, mode,
                            hidden_out, rec, rstd, xn, st);
   else
-    launch_rows<16, RESID>(hidden, ffn, src_prev, par, ln_w, B1, N, D, delta, eps, mode,
+    launch_rows<16, RESID, ROOTS>(hidden, ffn, src_prev, par, ln_w, B1, N, D, delta, eps, mode,
                            hidden_out, rec, rstd, xn, st);
 }
 
+template <bool RESID>
+void launch_rows_mode(int D, const uint16_t* hidden, const uint16_t* ffn, const int32_t* src_prev,
+                      const int32_t* par, const uint16_t* ln_w, int B1, int N, float delta,
+                      float eps, int gate_mode, uint16_t* hidden_out, int8_t* rec, float* rstd,
+                      uint16_t* xn, hipStream_t st) {
+  const int mode = gate_mode & ~SF_GATE_ROOTS_BY_PARENT;
+  if (gate_mode & SF_GATE_ROOTS_BY_PARENT)
+    launch_rows_any<RESID, true>(D, hidden, ffn, src_prev, par, ln_w, B1, N, delta, eps, mode,
+                                 hidden_out, rec, rstd, xn, st);
+  else
+    launch_rows_any<RESID, false>(D, hidden, ffn, src_prev, par, ln_w, B1, N, delta, eps, mode,
+                                  hidden_out, rec, rstd, xn, st);
+}
+
 int check_gate_args(int B1, int N, int D, int bucket, int gate_mode) {
-  if (gate_mode != SF_GATE_MODEL_DTYPE && gate_mode != SF_GATE_FP32_SQUARED &&
-      gate_mode != SF_GATE_ALL)
+  const int mode = gate_mode & ~SF_GATE_ROOTS_BY_PARENT;
+  if (mode != SF_GATE_MODEL_DTYPE && mode != SF_GATE_FP32_SQUARED && mode != SF_GATE_ALL)
     return SF_ERR_ARG;
   if (B1 < 1 || B1 > 64 || N < 1 || B1 * N > 1024) return SF_ERR_SHAPE;
   if (D < 8 || D % 8 != 0 || D > 8 * 64 * kMaxVecPerLane) return SF_ERR_SHAPE;
@@ -287,7 +304,7 @@ __global__ __launch_bounds__(64) void sf_parent_map_kernel(const int64_t* __rest
 
 }  // namespace
 
-extern "C" int sf_abi_version(void) { return 3; }
+extern "C" int sf_abi_version(void) { return 4; }
 
 extern "C" int sf_parent_map(const int64_t* tokens, int B1, int N, int32_t* par, int32_t* counts,
                              void* stream) {
@@ -309,7 +326,7 @@ extern "C" int sf_fold_gate(const uint16_t* hidden, const int32_t* par, const ui
   const int chk = check_gate_args(B1, N, D, bucket, gate_mode);
   if (chk != SF_OK) return chk;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  launch_rows_any<false>(D, hidden, nullptr, nullptr, par, ln_w, B1, N, delta, eps, gate_mode,
+  launch_rows_mode<false>(D, hidden, nullptr, nullptr, par, ln_w, B1, N, delta, eps, gate_mode,
                          nullptr, rec, rstd, xn, st);
   hipLaunchKernelGGL(sf_gate_compact_kernel, dim3(1), dim3(1024), 0, st, rec, par, B1, N, bucket,
                      f, src, rows, count, seg, segcnt, slot);
@@ -331,7 +348,7 @@ extern "C" int sf_fold_gate_residual(const uint16_t* hp, const uint16_t* ffn,
   if (chk != SF_OK) return chk;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   // the row kernel reads src_prev; only the compaction after it writes src
-  launch_rows_any<true>(D, hp, ffn, src_prev, par, ln_w, B1, N, delta, eps, gate_mode, hidden_out,
+  launch_rows_mode<true>(D, hp, ffn, src_prev, par, ln_w, B1, N, delta, eps, gate_mode, hidden_out,
                         rec, rstd, xn, st);
   hipLaunchKernelGGL(sf_gate_compact_kernel, dim3(1), dim3(1024), 0, st, rec, par, B1, N, bucket,
                      f, src, rows, count, seg, segcnt, slot);
@@ -344,7 +361,8 @@ extern "C" int sf_residual_rmsnorm(const uint16_t* hp, const uint16_t* ffn, cons
   if (!hp || !ffn || !src || !w || !hidden_out || !out || hidden_out == hp) return SF_ERR_ARG;
   const int chk = check_gate_args(B1, N, D, 1, SF_GATE_ALL);
   if (chk != SF_OK) return chk;
-  launch_rows_any<true>(D, hp, ffn, src, nullptr, w, B1, N, 0.f, eps, SF_GATE_ALL, hidden_out,
-                        nullptr, nullptr, out, reinterpret_cast<hipStream_t>(stream));
+  launch_rows_any<true, false>(D, hp, ffn, src, nullptr, w, B1, N, 0.f, eps, SF_GATE_ALL,
+                               hidden_out, nullptr, nullptr, out,
+                               reinterpret_cast<hipStream_t>(stream));
   return sf_launch_status();
 }

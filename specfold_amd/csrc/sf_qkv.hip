@@ -18,7 +18,10 @@ namespace {
 
 // Wave w of workgroup (x, y) handles head 4y + w of compacted rows
 // m = x, x + gridDim.x, ... < count; lane t owns dims t and t+64, exactly the pair
-// rotate_half mixes.
+// rotate_half mixes.  BRANCHES: the first absolute position is pos0[branch] and
+// the q scale q_scale[flat row] (a batched step: each sequence's branches at its
+// own prefix length); otherwise *pos0 and q_scale[n] for every row.
+template <bool BRANCHES>
 __global__ __launch_bounds__(256) void sf_qkv_epilogue_kernel(
     const float* __restrict__ part, Plan plan, int bucket, int n_qkv,
     const int32_t* __restrict__ rows, const int32_t* __restrict__ count_p,
@@ -36,13 +39,14 @@ __global__ __launch_bounds__(256) void sf_qkv_epilogue_kernel(
   const float b0 = bias ? sf_bf2f(bias[c0]) : 0.f;
   const float b1 = bias ? sf_bf2f(bias[c1]) : 0.f;
   const int count = min(*count_p, bucket);
-  const int p0 = pos0 ? *pos0 : 0;
+  const int p0 = (!BRANCHES && pos0) ? *pos0 : 0;
   for (int m = blockIdx.x; m < count; m += gridDim.x) {
     const int row = rows[m];
     const float* ps = part + (size_t)m * n_qkv;
     float y0 = sum_slots<float>(ps + c0, stride, nsl);
     float y1 = sum_slots<float>(ps + c1, stride, nsl);
     const int n = row % N;
+    const int pb = BRANCHES ? pos0[row / N] : p0;
     if (bias) {  // (without a bias, a -0 sum stays -0 as in torch)
       y0 += b0;
       y1 += b1;
@@ -50,7 +54,7 @@ __global__ __launch_bounds__(256) void sf_qkv_epilogue_kernel(
     y0 = sf_rbf(y0);  // nn.Linear output is a bf16 tensor
     y1 = sf_rbf(y1);
     if (head < H + Hkv) {
-      const size_t tr = (size_t)min(max(p0 + n, 0), table_rows - 1) * 128;
+      const size_t tr = (size_t)min(max(pb + n, 0), table_rows - 1) * 128;
       const float cs0 = sf_bf2f(cos_tab[tr + t]);
       const float cs1 = sf_bf2f(cos_tab[tr + t + 64]);
       const float sn0 = sf_bf2f(sin_tab[tr + t]);
@@ -61,7 +65,7 @@ __global__ __launch_bounds__(256) void sf_qkv_epilogue_kernel(
       y0 = o0;
       y1 = o1;
       if (head < H && q_scale) {
-        const float qs = sf_rbf(q_scale[n]);
+        const float qs = sf_rbf(q_scale[BRANCHES ? row : n]);
         y0 = sf_rbf(y0 * qs);
         y1 = sf_rbf(y1 * qs);
       }
@@ -103,8 +107,42 @@ extern "C" int sf_qkv_rope(const uint16_t* xn, const int32_t* rows, const int32_
   float* part = reinterpret_cast<float*>(workspace);
   launch_sk<2, kPart>(p, xn, rows, D, count, 0, bucket, w_qkv, nullptr, D, n_qkv, part, Epi{}, st);
   dim3 g2(min(bucket, 128), (H + 2 * Hkv + 3) / 4);
-  hipLaunchKernelGGL(sf_qkv_epilogue_kernel, g2, dim3(256), 0, st, part, p, bucket, n_qkv, rows,
+  hipLaunchKernelGGL(sf_qkv_epilogue_kernel<false>, g2, dim3(256), 0, st, part, p, bucket, n_qkv, rows,
                      count, b_qkv, cos_tab, sin_tab, pos0, table_rows, q_scale, N, H, Hkv, q_buf,
                      kv_buf);
+  return sf_launch_status();
+}
+
+// The batched-step variant: one GEMM over the recomputed rows of several
+// sequences laid out one after another, the rope and q scale of each branch at its
+// own sequence's positions.  pos0_branch: int32 [BN / N], the first absolute
+// position of each branch (its sequence's prefix length); q_scale_rows: fp32 [BN]
+// or NULL.  No counterpart in the reference (one sequence per verify step).
+extern "C" int sf_qkv_rope_branches(const uint16_t* xn, const int32_t* rows,
+                                    const int32_t* count, int bucket, int BN,
+                                    const uint16_t* w_qkv, const uint16_t* b_qkv,
+                                    const uint16_t* cos_tab, const uint16_t* sin_tab,
+                                    const int32_t* pos0_branch, int table_rows,
+                                    const float* q_scale_rows, int N, int D, int H, int Hkv,
+                                    int hd, uint16_t* q_buf, uint16_t* kv_buf, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
+  if (!xn || !rows || !count || !w_qkv || !cos_tab || !sin_tab || !pos0_branch || !q_buf ||
+      !kv_buf || !workspace)
+    return SF_ERR_ARG;
+  if (hd != 128 || H < 1 || Hkv < 1 || H % Hkv != 0) return SF_ERR_SHAPE;
+  if (D < kKC || D % kKC != 0) return SF_ERR_SHAPE;
+  if (N < 1 || BN < 1 || BN % N != 0 || bucket < 1 || bucket > BN || bucket > 1024)
+    return SF_ERR_SHAPE;
+  if (table_rows < N) return SF_ERR_SHAPE;
+  const int n_qkv = (H + 2 * Hkv) * hd;
+  if (workspace_bytes < sf_qkv_workspace_bytes(bucket, D, n_qkv)) return SF_ERR_WORKSPACE;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const Plan p = make_plan(n_qkv / 128, D / kKC);
+  float* part = reinterpret_cast<float*>(workspace);
+  launch_sk<2, kPart>(p, xn, rows, D, count, 0, bucket, w_qkv, nullptr, D, n_qkv, part, Epi{}, st);
+  dim3 g2(min(bucket, 128), (H + 2 * Hkv + 3) / 4);
+  hipLaunchKernelGGL(sf_qkv_epilogue_kernel<true>, g2, dim3(256), 0, st, part, p, bucket, n_qkv,
+                     rows, count, b_qkv, cos_tab, sin_tab, pos0_branch, table_rows, q_scale_rows,
+                     N, H, Hkv, q_buf, kv_buf);
   return sf_launch_status();
 }

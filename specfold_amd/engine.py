@@ -137,6 +137,44 @@ class _Buffers:
                                    dtype=torch.uint8, device=dev)
 
 
+class _Batch:
+    """Several sequences' branch trees stacked into one verify step: sequence s
+    owns branches offsets[s] .. offsets[s] + sizes[s] - 1 (its main branch first)
+    and its own prefix cache.  The per-branch first positions and per-row q scales
+    are device tensors built once per call."""
+
+    def __init__(self, eng: "FoldedVerifyEngine", sizes: List[int], caches: list, N: int,
+                 q_scales: Optional[list]):
+        dev = eng.device
+        self.sizes = list(sizes)
+        self.offsets = [sum(self.sizes[:i]) for i in range(len(self.sizes))]
+        self.caches = list(caches)
+        B1 = sum(self.sizes)
+        i32 = dict(dtype=torch.int32, device=dev)
+        self.pos0_branch = torch.cat([
+            c.length_dev.expand(b) if c is not None else torch.zeros(b, **i32)
+            for c, b in zip(self.caches, self.sizes)]).contiguous()
+        self.q_scale_rows = None
+        if q_scales is not None and any(q is not None for q in q_scales):
+            ones = torch.ones(N, dtype=torch.float32, device=dev)
+            self.q_scale_rows = torch.cat([
+                (ones if q is None else q.reshape(-1).to(device=dev, dtype=torch.float32))
+                .repeat(b) for q, b in zip(q_scales, self.sizes)]).contiguous()
+        self.bounds = torch.tensor([o * N for o in self.offsets] + [B1 * N], **i32)
+        self.idx = torch.arange(B1 * N, **i32)
+
+    def split_rows(self, rows: torch.Tensor, count: torch.Tensor, bucket: int, N: int):
+        """Per-sequence runs of the ascending compacted rows: (rows_s [S, bucket],
+        count_s [S]) on the device, without a host sync."""
+        idx = self.idx[:bucket]
+        valid = idx < count
+        below = (valid.unsqueeze(0) & (rows[:bucket].unsqueeze(0) < self.bounds.unsqueeze(1))
+                 ).sum(1, dtype=torch.int32)
+        gather = (below[:-1].unsqueeze(1) + idx.unsqueeze(0)).clamp_(max=bucket - 1)
+        rows_s = rows[gather.long()].contiguous()
+        return rows_s, (below[1:] - below[:-1]).contiguous()
+
+
 class FoldedVerifyEngine:
     """Runs the folded verify step of a Qwen2-layout model through the HIP kernels."""
 
@@ -304,23 +342,86 @@ class FoldedVerifyEngine:
         logits = torch.mm(buf.final, self.head.weight.t())
         return logits.view(B1, N, self.V)
 
+    @torch.no_grad()
+    def forward_batched(self, blocks: List[torch.Tensor], caches: list, delta: float = 0.1,
+                        bucket: Optional[int] = None,
+                        q_scales: Optional[List[Optional[torch.Tensor]]] = None,
+                        stats: Optional[StepStats] = None,
+                        compute_logits: bool = True) -> Optional[List[torch.Tensor]]:
+        """One verify step over several independent sequences -> per-sequence logits
+        [B1_s, N, V] (unshifted).
+
+        blocks[s]  [B1_s, N] int64, sequence s's branches (row 0 = its main branch);
+        caches[s]  its PagedKVCache (or None: no prefix); q_scales[s] optional [N].
+        The sequences' branches are stacked into one step of sum(B1_s) branches:
+        the gate, compaction, GEMMs and chain correction run once over all of them
+        (the main branch of every sequence is a root: SF_GATE_ROOTS_BY_PARENT), the
+        QKV epilogue ropes each branch at its sequence's positions, and attention
+        runs per sequence over its own prefix.  Each sequence's result is that of
+        ``forward`` on it alone.  No counterpart in the reference, whose verify step
+        takes one sequence; runs eagerly (no HIP graph)."""
+        if not blocks or len(blocks) != len(caches):
+            raise ValueError("forward_batched needs one cache (or None) per token block")
+        if q_scales is not None and len(q_scales) != len(blocks):
+            raise ValueError("forward_batched needs one q scale (or None) per token block")
+        N = blocks[0].shape[-1]
+        for b in blocks:
+            if b.dim() != 2 or b.shape[1] != N:
+                raise ValueError("every token block must be [B1_s, N] with the same N")
+        for c in caches:
+            if c is not None and not isinstance(c, PagedKVCache):
+                raise TypeError("forward_batched takes PagedKVCache prefixes (or None)")
+        sizes = [int(b.shape[0]) for b in blocks]
+        tokens = torch.cat([b.to(self.device) for b in blocks]).contiguous()
+        B1 = tokens.shape[0]
+        BN = B1 * N
+        bucket = BN if bucket is None else max(1, min(int(bucket), BN))
+        P_alloc = max([c.capacity for c in caches if c is not None], default=0)
+        buf = self.buffers(B1, N, bucket, P_alloc)
+        self.rope_tables(max(cache_length(c) for c in caches) + N)
+        batch = _Batch(self, sizes, caches, N, q_scales)
+        hidden = self._run_layers(buf, tokens, None, delta, bucket, batch=batch)
+        overflow = bucket < BN and int(buf.count_slab.max()) > bucket
+        if stats is not None:
+            stats.count_dev, stats.bucket, stats.overflow = buf.count_slab.clone(), bucket, overflow
+            stats._counts = None
+        if overflow:
+            logger.warning("SpecFold bucket overflow (> %d); recomputing with bucket=%d",
+                           bucket, BN)
+            return self.forward_batched(blocks, caches, delta, bucket=BN, q_scales=q_scales,
+                                        stats=stats, compute_logits=compute_logits)
+        self.last_hidden = hidden
+        if not compute_logits:
+            return None
+        logits = torch.mm(buf.final, self.head.weight.t()).view(B1, N, self.V)
+        return list(logits.split(sizes, 0))
+
     # ------------------------------------------------------------------------
     def _run_layers(self, buf: _Buffers, tokens: torch.Tensor, cache,
                     delta: float, bucket: int, append: bool = False,
                     q_scale: Optional[torch.Tensor] = None, trace: Optional[list] = None,
                     teacher: Optional[Dict[int, torch.Tensor]] = None,
-                    causal: bool = False) -> torch.Tensor:
+                    causal: bool = False, batch: Optional["_Batch"] = None) -> torch.Tensor:
         """Embedding and every layer: device launches only (no host sync), so the
         sequence can be captured in a HIP graph.  RoPE rows and a paged cache's
         length come from the cache's device-side length (buf.pos0 for other
         caches), so a captured sequence stays valid as the cache grows.  Returns
-        the last hidden state."""
+        the last hidden state.  ``batch``: the branch trees of several sequences
+        stacked in ``tokens`` (forward_batched)."""
         B1, N = tokens.shape
         BN = B1 * N
         H, Hkv, hd, D = self.H, self.Hkv, self.hd, self.D
         base = self.base
         par = buf.par
-        _lib.parent_map(tokens, par)          # on the device: no host round trip
+        gate_mode = self.gate_mode
+        if batch is None:
+            _lib.parent_map(tokens, par)          # on the device: no host round trip
+        else:
+            for o, b in zip(batch.offsets, batch.sizes):
+                _lib.parent_map(tokens[o:o + b], par[o:o + b])
+                if o:
+                    par[o:o + b] += o
+            gate_mode |= _lib.SF_GATE_ROOTS_BY_PARENT
         hidden = base.embed_tokens(tokens).reshape(BN, D)
         cos, sin = self._rope
         pos0 = cache.length_dev if isinstance(cache, PagedKVCache) else buf.pos0
@@ -332,7 +433,7 @@ class FoldedVerifyEngine:
                 hidden = teacher[li].reshape(BN, D).to(torch.bfloat16).contiguous()
             if li == 0 or (teacher is not None and li in teacher):
                 hidden = hidden.contiguous()
-                _lib.fold_gate(hidden, par, ln_w, B1, N, bucket, delta, self.eps, self.gate_mode,
+                _lib.fold_gate(hidden, par, ln_w, B1, N, bucket, delta, self.eps, gate_mode,
                                buf.rec, buf.f, buf.src, buf.rows, count, buf.seg, segcnt,
                                buf.rstd, buf.xn, slot=buf.slot)
             else:
@@ -340,15 +441,29 @@ class FoldedVerifyEngine:
                 # fused into this layer's gate: x = bf16(hp + ffn[src*N + n])
                 hidden = buf.hid[li % 2]
                 _lib.fold_gate_residual(buf.hp, buf.ffn, buf.src, par, ln_w, B1, N, D, bucket,
-                                        delta, self.eps, self.gate_mode, hidden, buf.rec, buf.f,
+                                        delta, self.eps, gate_mode, hidden, buf.rec, buf.f,
                                         buf.src, buf.rows, count, buf.seg, segcnt, buf.slot,
                                         buf.rstd, buf.xn)
             w_qkv, b_qkv = self._packed[li]
-            _lib.qkv_rope(buf.xn, buf.rows, count, bucket, BN, w_qkv, b_qkv, cos, sin, q_scale,
-                          N, D, H, Hkv, hd, buf.q_buf, buf.kv_buf, buf.ws_qkv, pos0=pos0)
+            if batch is None:
+                _lib.qkv_rope(buf.xn, buf.rows, count, bucket, BN, w_qkv, b_qkv, cos, sin,
+                              q_scale, N, D, H, Hkv, hd, buf.q_buf, buf.kv_buf, buf.ws_qkv,
+                              pos0=pos0)
+            else:
+                _lib.qkv_rope_branches(buf.xn, buf.rows, count, bucket, BN, w_qkv, b_qkv, cos,
+                                       sin, batch.q_scale_rows, N, D, H, Hkv, hd, buf.q_buf,
+                                       buf.kv_buf, buf.ws_qkv, batch.pos0_branch)
             if append:
                 cache.append_rows(li, buf.kv_buf, 0, N)
-            self._attention(buf, cache, li, count, bucket, B1, N, causal=causal)
+            if batch is None:
+                self._attention(buf, cache, li, count, bucket, B1, N, causal=causal)
+            else:
+                # each sequence's recomputed rows over its own prefix: the compacted
+                # rows are ascending, so sequence s owns a contiguous run of them
+                rows_s, count_s = batch.split_rows(buf.rows, count, bucket, N)
+                for si, c in enumerate(batch.caches):
+                    self._attention(buf, c, li, count_s[si:si + 1], bucket, B1, N,
+                                    rows=rows_s[si])
             _lib.chain_correct(buf.q_buf, buf.kv_buf, buf.src, par, buf.rec, buf.seg, segcnt,
                                B1, N, H, Hkv, hd, self.scaling, buf.o32, buf.o_bf, buf.m_tab,
                                buf.z_tab)
@@ -386,7 +501,7 @@ class FoldedVerifyEngine:
         return last
 
     def _attention(self, buf: _Buffers, cache, li: int, count, bucket: int, B1: int, N: int,
-                   causal: bool = False):
+                   causal: bool = False, rows: Optional[torch.Tensor] = None):
         pv = prefix_view(cache, li)
         if pv is None:
             P_arg, plen = 0, None
@@ -398,9 +513,9 @@ class FoldedVerifyEngine:
             buf.q_buf, buf.kv_buf, pv.k if pv else None, pv.v if pv else None,
             pv.page_table if pv else None, P_arg, pv.page_size if pv else 1,
             pv.page_stride if pv else 0, pv.head_stride if pv else 0,
-            buf.src, buf.rows, count, bucket, B1, N, self.H, self.Hkv, self.hd, self.scaling,
-            buf.o32, buf.o_bf, buf.m_tab, buf.z_tab, buf.ws_attn, prefix_len=plen,
-            block_causal=causal)
+            buf.src, buf.rows if rows is None else rows, count, bucket, B1, N, self.H, self.Hkv,
+            self.hd, self.scaling, buf.o32, buf.o_bf, buf.m_tab, buf.z_tab, buf.ws_attn,
+            prefix_len=plen, block_causal=causal)
 
     def _graph_key(self, buf: _Buffers, cache, P: int, delta: float, bucket: int,
                    q_scaled: bool = False, causal: bool = False):

@@ -78,3 +78,69 @@ def test_nld_layers_teacher_forced(sim, name, shape, seed, P, delta, omax):
     assert (qs is not None) == (P + case.tokens.shape[1] > omax)
     tr, ref_logits, trace, logits = run(case, q_scale=qs)
     check_layers(case, shape, tr, trace)
+
+
+def _paged(kv):
+    if kv is None:
+        return None
+    cache = PagedKVCache(len(kv), kv[0][0].shape[1], 128, 512, page_size=16, device="cpu",
+                         page_order="shuffled", seed=5)
+    cache.load_dense(kv)
+    return cache
+
+
+def _batched_vs_single(model, seqs, delta, q_scales=None):
+    """forward_batched over `seqs` [(tokens, kv)] against forward on each alone:
+    every sequence's logits and per-layer recomputed-row counts identical."""
+    from specfold_amd.engine import StepStats
+    q_scales = q_scales or [None] * len(seqs)
+    eng = SimEngine(model)
+    eng.use_graphs = False
+    single, counts = [], []
+    for (tok, kv), qs in zip(seqs, q_scales):
+        st = StepStats()
+        single.append(eng.forward(tok, _paged(kv), delta, q_scale=qs, stats=st))
+        counts.append(st.counts)
+    stb = StepStats()
+    batched = eng.forward_batched([t for t, _ in seqs], [_paged(kv) for _, kv in seqs], delta,
+                                  q_scales=q_scales, stats=stb)
+    assert len(batched) == len(seqs)
+    for s, (a, b) in enumerate(zip(batched, single)):
+        assert a.shape == b.shape
+        assert torch.equal(a, b), (s, err_stats(a.float(), b.float()))
+    assert stb.counts == [sum(c) for c in zip(*counts)], (stb.counts, counts)
+    return counts
+
+
+def test_batched_step_equals_single_steps(sim):
+    """Three Fast-dLLM sequences (prefix 100 / none / 37; 8, 1 and 5 branches) in one
+    verify step give each sequence's own verify step, bit for bit."""
+    from tests.helpers import draft_tree_block, random_prefix_kv
+    shape = SHAPE_G2
+    model = make_case(shape, 1, P=0).model_cpu
+    seqs = []
+    for P, k, seed in ((100, 8, 11), (0, 1, 12), (37, 5, 13)):
+        gen = torch.Generator().manual_seed(seed)
+        tok = draft_tree_block(32, shape.vocab, gen)[:k].contiguous()
+        kv = random_prefix_kv(shape.layers, shape.kv_heads, P, shape.head_dim, gen) if P else None
+        seqs.append((tok, kv))
+    counts = _batched_vs_single(model, seqs, 0.1)
+    assert counts[1] == [32] * shape.layers        # a lone main branch: every row recomputed
+    assert any(c < 8 * 32 for c in counts[0])      # some rows of the 8-branch tree folded
+
+
+def test_batched_nld_step_with_q_scales(sim):
+    """NLD sequences, the llama-4 q scale active for one (prefix 70 + block > 64) and
+    not for the other (no prefix)."""
+    from tests.helpers import draft_tree_block, random_prefix_kv
+    shape = SHAPE_N4
+    model = make_nld_case(shape, 1, P=0, omax=64).model_cpu
+    seqs, qss = [], []
+    for P, k, seed in ((70, 6, 21), (0, 4, 22)):
+        gen = torch.Generator().manual_seed(seed)
+        tok = draft_tree_block(32, shape.vocab - 1, gen)[:k].contiguous()
+        kv = random_prefix_kv(shape.layers, shape.kv_heads, P, shape.head_dim, gen) if P else None
+        seqs.append((tok, kv))
+        qss.append(llama4_q_scale(model.config, P, 32))
+    assert qss[0] is not None and qss[1] is None
+    _batched_vs_single(model, seqs, 0.1, q_scales=qss)

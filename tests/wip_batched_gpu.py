@@ -1,0 +1,63 @@
+"""GPU check of FoldedVerifyEngine.forward_batched (sf_qkv_rope_branches and the
+SF_GATE_ROOTS_BY_PARENT gate): several sequences in one verify step against each
+sequence's own forward.  Integer outputs (per-layer recomputed-row counts) must
+be identical; logits within the parity tolerance (o_proj and lm_head run on
+hipBLASLt, whose kernel choice may change with M = total rows).
+
+Not collected by pytest until it has passed on the GPU; run it by naming it:
+python -m pytest tests/wip_batched_gpu.py -m gpu."""
+
+import pytest
+import torch
+
+from oracle.folded_reference import llama4_q_scale
+from specfold_amd.engine import FoldedVerifyEngine, StepStats
+from specfold_amd.kv_cache import PagedKVCache
+from tests.helpers import (SHAPE_G2, SHAPE_N4, draft_tree_block, err_stats, make_case,
+                           make_nld_case, random_prefix_kv, to_gpu_model)
+
+pytestmark = pytest.mark.gpu
+
+
+def _paged(kv):
+    if kv is None:
+        return None
+    cache = PagedKVCache(len(kv), kv[0][0].shape[1], 128, 512, page_size=16, device="cuda",
+                         page_order="shuffled", seed=5)
+    cache.load_dense([(k.cuda(), v.cuda()) for k, v in kv])
+    return cache
+
+
+@pytest.mark.parametrize("family", ["fastdllm", "nld"])
+def test_batched_step_gpu(family):
+    if family == "fastdllm":
+        shape, specs = SHAPE_G2, ((100, 8, 11), (0, 1, 12), (37, 5, 13))
+        model = to_gpu_model(make_case(shape, 1, P=0).model_cpu)
+        vocab = shape.vocab
+    else:
+        shape, specs = SHAPE_N4, ((70, 6, 21), (0, 4, 22))
+        model = to_gpu_model(make_nld_case(shape, 1, P=0, omax=64).model_cpu)
+        vocab = shape.vocab - 1
+    seqs, qss = [], []
+    for P, k, seed in specs:
+        gen = torch.Generator().manual_seed(seed)
+        tok = draft_tree_block(32, vocab, gen)[:k].contiguous()
+        kv = random_prefix_kv(shape.layers, shape.kv_heads, P, shape.head_dim, gen) if P else None
+        seqs.append((tok.cuda(), kv))
+        qs = llama4_q_scale(model.config, P, 32) if family == "nld" else None
+        qss.append(qs.cuda() if qs is not None else None)
+    print(f"[wip_batched_gpu] {family} specs={specs}", flush=True)
+    eng = FoldedVerifyEngine(model)
+    single, counts = [], []
+    for (tok, kv), qs in zip(seqs, qss):
+        st = StepStats()
+        single.append(eng.forward(tok, _paged(kv), 0.1, q_scale=qs, stats=st))
+        counts.append(st.counts)
+    stb = StepStats()
+    batched = eng.forward_batched([t for t, _ in seqs], [_paged(kv) for _, kv in seqs], 0.1,
+                                  q_scales=qss, stats=stb)
+    torch.cuda.synchronize()
+    assert stb.counts == [sum(c) for c in zip(*counts)]
+    for a, b in zip(batched, single):
+        st = err_stats(a.float(), b.float())
+        assert st["max_abs"] <= 2e-2 * max(1.0, st["ref_absmax"]), st
