@@ -51,6 +51,9 @@ def parse_args(argv=None):
     ap.add_argument("--kernel-iters", type=int, default=200)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--lockstep", action="store_true",
+                    help="a multi-sequence workload (cfg4) decodes its sequences in lockstep, "
+                         "one batched verify step per round (a step = one round)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also time a plain 256 MiB device copy (counter calibration)")
     return ap.parse_args(argv)
@@ -296,27 +299,51 @@ def main(argv=None) -> int:
     print(f"[bench] model + engine ready in {build_s:.1f}s ({w.family}, {len(gens)} sequence(s))",
           file=sys.stderr, flush=True)
 
-    # decode loops (one per sequence, stepped round-robin): prefill, W warmup
+    # decode loops (one per sequence, stepped round-robin; or, with --lockstep, all
+    # sequences per round with their verify steps batched): prefill, W warmup
     # steps, K timed steps
-    loops = [g.decode_steps(p) for g, p in zip(gens, prompts)]
+    lockstep = args.lockstep and len(gens) > 1
+    if args.lockstep and not lockstep:
+        print("--lockstep needs a multi-sequence workload", file=sys.stderr)
+        return 2
     t0 = time.time()
-    for lp in loops:
-        ev = next(lp)
-        assert ev["kind"] == "prefill"
+    if lockstep:
+        from specfold_amd.generate.lockstep import LockstepDecoder
+        rounds = LockstepDecoder(gens).rounds(prompts)
+        first = next(rounds)      # every sequence's prefill, then the first batched step
+        assert [e["kind"] for _, e in first["events"]] == ["prefill"] * len(gens)
+
+        def advance(i):
+            try:
+                r = next(rounds)
+            except StopIteration:
+                raise SystemExit("the decode loops ended before the timed steps did: "
+                                 "lower --steps / --warmup") from None
+            return r["committed"], [e["kind"] for _, e in r["events"]]
+    else:
+        loops = [g.decode_steps(p) for g, p in zip(gens, prompts)]
+        for lp in loops:
+            ev = next(lp)
+            assert ev["kind"] == "prefill"
+
+        def advance(i):
+            ev = next(loops[i % len(loops)])
+            return ev["committed"], [ev["kind"]]
     torch.cuda.synchronize()
     prefill_s = time.time() - t0
-    print(f"[bench] prefill {len(loops)} x {w.prefix} tokens in {prefill_s:.2f}s", file=sys.stderr,
+    print(f"[bench] prefill {len(gens)} x {w.prefix} tokens in {prefill_s:.2f}s", file=sys.stderr,
           flush=True)
     for i in range(args.warmup):
-        next(loops[i % len(loops)])
+        advance(i)
     kinds = {}
     committed = 0
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        ev = next(loops[i % len(loops)])
-        committed += ev["committed"]
-        kinds[ev["kind"]] = kinds.get(ev["kind"], 0) + 1
+        c, ks = advance(i)
+        committed += c
+        for k in ks:
+            kinds[k] = kinds.get(k, 0) + 1
     torch.cuda.synchronize()
     timed_s = time.perf_counter() - t0
     tps = committed / timed_s
@@ -382,7 +409,8 @@ def main(argv=None) -> int:
                    key=lambda n: kernels[n]["avg_us"] * kernels[n]["launches_per_step"])
     copy = copy_calibration() if args.copy_calibration else None
 
-    tokens_per_step = committed / max(1, args.steps)
+    # tokens per sequence's decode step (a lockstep round steps every sequence)
+    tokens_per_step = committed / max(1, args.steps * (len(gens) if lockstep else 1))
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(w, batched.cpu(), tokens_per_step, args.cpu_seconds)
@@ -401,7 +429,9 @@ def main(argv=None) -> int:
         "vs_baseline": None,
         "dtype": "bf16",
         "data": (f"synthetic (random-init weights, random-token prompt, synthetic draft graph; "
-                 f"{w.batch} independent sequence(s) stepped round-robin)"),
+                 f"{w.batch} independent sequence(s) "
+                 + ("decoded in lockstep, one batched verify step per round; a step = one "
+                    "round)" if lockstep else "stepped round-robin)")),
         "config": {"workload": w.name, "hidden": w.shape.hidden, "layers": w.shape.layers,
                    "heads": w.shape.heads, "kv_heads": w.shape.kv_heads,
                    "intermediate": w.shape.intermediate, "vocab": w.shape.vocab,
@@ -409,6 +439,7 @@ def main(argv=None) -> int:
                    "small_block": w.small_block if w.family == "fastdllm" else None,
                    "delta": w.delta, "threshold": w.threshold, "batch": w.batch,
                    "family": w.family, "shuffled_pages": w.shuffled_pages,
+                   "lockstep": lockstep,
                    "parallelism": "none (1 GPU)"},
         "verify_step_ms": round(verify_ms, 4),
         "verify_step_prefix": P,

@@ -1,0 +1,118 @@
+"""Several independent sequences decoded in lockstep, their verify steps merged.
+
+The NLD decode loop (NLDDiffusionGeneration.decode_steps) runs one sequence; a
+batch of B sequences stepped one after another streams every weight matrix B
+times per round of verify steps.  LockstepDecoder runs each sequence's loop with
+``defer_forward=True``: in each round every live sequence advances to its next
+verify forward, and the forwards of all of them run as ONE verify step over the
+stacked branch trees (FoldedVerifyEngine.forward_batched), so the weights are
+streamed once per round.  Prefill and block commits (cache writes) stay per
+sequence.  Each sequence's tokens are those its own loop would produce with its
+verify steps computed by the engine (forward_batched gives every sequence the
+result of FoldedVerifyEngine.forward on it alone).
+
+No counterpart in the reference, whose generators decode one sequence per call.
+"""
+
+from __future__ import annotations
+
+from typing import Callable, Dict, List, Optional, Sequence
+
+import torch
+
+from specfold_amd.engine import StepStats
+from specfold_amd.generate.nld_model_executor import llama4_q_scale
+from specfold_amd.kv_cache import cache_length
+
+# [(batched [B1_s, N], prefix cache)] -> [logits [B1_s, N, V]]
+ForwardMany = Callable[[List[tuple]], List[torch.Tensor]]
+
+
+class LockstepDecoder:
+    """Drives the decode loops of ``gens`` (NLD generators, one per sequence) in
+    lockstep.  ``forward_many`` computes a round's verify forwards; the default is
+    one batched verify step on the engine of the first generator (a
+    SpecFoldHIPNLDGeneration; every generator shares its delta and bucket)."""
+
+    def __init__(self, gens: Sequence, forward_many: Optional[ForwardMany] = None):
+        if not gens:
+            raise ValueError("LockstepDecoder needs at least one generator")
+        self.gens = list(gens)
+        self.forward_many = forward_many or self._engine_forward_many
+        self.rounds_run = 0
+        self.batched_steps = 0
+        self.draft_positions = 0
+        self._recomputed: Optional[torch.Tensor] = None   # device scalar
+        self.last_stats: Optional[StepStats] = None
+
+    @property
+    def fold_ratio(self) -> float:
+        """Share of draft rows folded over every batched step (one host read)."""
+        if not self.draft_positions:
+            return float("nan")
+        return 1.0 - int(self._recomputed) / self.draft_positions
+
+    def _engine_forward_many(self, requests: List[tuple]) -> List[torch.Tensor]:
+        g0 = self.gens[0]
+        if g0._engine is None:
+            g0._pack_layer_weights()
+        eng = g0._engine
+        N = requests[0][0].shape[1]
+        total = sum(b.shape[0] for b, _ in requests) * N
+        bucket = total if g0.fold_bucket is None else min(g0.fold_bucket, total)
+        cfg = g0.model_executor.model.config
+        q_scales = [llama4_q_scale(cfg, cache_length(c), N, eng.device) for _, c in requests]
+        stats = StepStats()
+        prev_mode, eng.gate_mode = eng.gate_mode, g0.gate_mode
+        try:
+            logits = eng.forward_batched([b for b, _ in requests], [c for _, c in requests],
+                                         delta=g0.delta, bucket=bucket, q_scales=q_scales,
+                                         stats=stats)
+        finally:
+            eng.gate_mode = prev_mode
+        # fold counters stay on the device: every sequence's main branch is a root
+        L = eng.L
+        self.draft_positions += (total - len(requests) * N) * L
+        rec = stats.count_dev.sum(dtype=torch.int64) - L * N * len(requests)
+        self._recomputed = rec if self._recomputed is None else self._recomputed + rec
+        self.last_stats = stats
+        return logits
+
+    def rounds(self, prompts: Sequence[torch.Tensor]):
+        """Generator: one event per round, {"kind": "round", "committed": tokens
+        unmasked in the round (all sequences), "forwards": sequences in the round's
+        batched verify step, "events": [(sequence, loop event), ...]}.  The first
+        round holds the prefills.  Ends when every loop has ended; states stay on
+        each generator's ``_state``."""
+        if len(prompts) != len(self.gens):
+            raise ValueError("one prompt per generator")
+        loops = [g.decode_steps(p, defer_forward=True) for g, p in zip(self.gens, prompts)]
+        reply: Dict[int, Optional[torch.Tensor]] = {i: None for i in range(len(loops))}
+        started = [False] * len(loops)
+        live = list(range(len(loops)))
+        while live:
+            events, requests, still = [], [], []
+            for i in live:
+                lp = loops[i]
+                try:
+                    ev = lp.send(reply[i]) if started[i] else next(lp)
+                    started[i] = True
+                    reply[i] = None
+                    while ev["kind"] != "forward":
+                        events.append((i, ev))
+                        ev = next(lp)
+                except StopIteration:
+                    continue
+                requests.append((i, ev))
+                still.append(i)
+            live = still
+            if requests:
+                outs = self.forward_many([(ev["batched"], ev["cache"]) for _, ev in requests])
+                if len(outs) != len(requests):
+                    raise RuntimeError("forward_many returned the wrong number of results")
+                for (i, _), out in zip(requests, outs):
+                    reply[i] = out
+                self.batched_steps += 1
+            self.rounds_run += 1
+            yield {"kind": "round", "committed": sum(e["committed"] for _, e in events),
+                   "forwards": len(requests), "events": events}

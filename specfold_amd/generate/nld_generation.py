@@ -178,11 +178,17 @@ class NLDDiffusionGeneration:
 
     # -- the decode loop ----------------------------------------------------------------
     @torch.no_grad()
-    def decode_steps(self, prompt_ids: torch.Tensor):
+    def decode_steps(self, prompt_ids: torch.Tensor, defer_forward: bool = False):
         """The decode loop of generate_with_draft_speculation (:153-316) as a
         generator: one event per iteration — {"kind": "prefill" | "verify" |
         "hit" | "commit", "committed": tokens unmasked by it}.  State on
-        ``self._state``."""
+        ``self._state``.
+
+        defer_forward: instead of calling ``_batched_block_forward`` the loop yields
+        {"kind": "forward", "batched": [B1, N] tokens, "cache": prefix cache,
+        "committed": 0} and continues with the logits [B1, N, V] passed back by
+        ``send`` (a driver that batches several sequences' verify steps into one,
+        specfold_amd.generate.lockstep)."""
         executor = self.model_executor
         mask_id, eos_id = self.mask_id, self.stop_token
         prompt_ids = prompt_ids.to(self.device)
@@ -246,7 +252,13 @@ class NLDDiffusionGeneration:
                         batched = torch.cat([main_block, states], dim=0)
                     else:
                         batched = main_block
-                    logits_all = self._batched_block_forward(batched, past_key_values)
+                    if defer_forward:
+                        logits_all = yield {"kind": "forward", "batched": batched,
+                                            "cache": past_key_values, "committed": 0}
+                        if logits_all is None:
+                            raise RuntimeError("a deferred forward needs its logits via send()")
+                    else:
+                        logits_all = self._batched_block_forward(batched, past_key_values)
                     st["model_calls"] += 1
                     logits_block = logits_all[0:1]
                     for k, d in enumerate(draft_blocks):

@@ -197,3 +197,47 @@ def test_nld_loop_same_decisions_with_statistics(seed, monkeypatch):
     assert torch.equal(sa["x_accum"], sb["x_accum"])
     assert sa["model_calls"] == sb["model_calls"] and sa["drafts_computed"] == sb["drafts_computed"]
     assert {"prefill", "verify", "hit", "commit"} <= {e["kind"] for e in ea}
+
+
+@pytest.mark.parametrize("seeds", [(0, 1, 2), (3, 5)])
+def test_nld_lockstep_same_tokens_as_separate_loops(seeds):
+    """LockstepDecoder over several NLD loops (deferred forwards, one merged call
+    per round) gives every sequence the events, tokens and counters of its own
+    loop run alone; each round's call carries one request per live sequence."""
+    from specfold_amd.generate.lockstep import LockstepDecoder
+
+    def make(seed):
+        bank = _bank(100 + seed, eos=FakeNLD.EOS)
+        prompt = torch.randint(0, 256, (1, 20 + 5 * seed),
+                               generator=torch.Generator().manual_seed(seed))
+        gen = NLDDiffusionGeneration(block_length=32, model_executor=FakeNLD(bank),
+                                     calibration_graph=SYNTHETIC_DRAFT_GRAPH,
+                                     max_new_tokens=64 + 32 * (seed % 2), threshold=0.9,
+                                     device="cpu")
+        return gen, prompt
+
+    alone = []
+    for seed in seeds:
+        gen, prompt = make(seed)
+        alone.append((list(gen.decode_steps(prompt)), gen._state))
+    pairs = [make(seed) for seed in seeds]
+    gens = [g for g, _ in pairs]
+    sizes = []
+
+    def forward_many(requests):
+        sizes.append(len(requests))
+        # each sequence's own forward (the fake models differ per sequence)
+        return [gens[[id(g._state["cache"]) if g._state["cache"] is not None else None
+                      for g in gens].index(id(c) if c is not None else None)]
+                ._batched_block_forward(b, c) for b, c in requests]
+
+    dec = LockstepDecoder(gens, forward_many=forward_many)
+    per_seq = [[] for _ in seeds]
+    for rnd in dec.rounds([p for _, p in pairs]):
+        for i, ev in rnd["events"]:
+            per_seq[i].append(ev)
+    for i, (ev_alone, st_alone) in enumerate(alone):
+        assert per_seq[i] == ev_alone
+        assert torch.equal(gens[i]._state["x_accum"], st_alone["x_accum"])
+        assert gens[i]._state["model_calls"] == st_alone["model_calls"]
+    assert max(sizes) == len(seeds) and dec.batched_steps == len(sizes)

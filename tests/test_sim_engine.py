@@ -144,3 +144,45 @@ def test_batched_nld_step_with_q_scales(sim):
         qss.append(llama4_q_scale(model.config, P, 32))
     assert qss[0] is not None and qss[1] is None
     _batched_vs_single(model, seqs, 0.1, q_scales=qss)
+
+
+def test_nld_lockstep_decode_matches_separate_decodes(sim, monkeypatch):
+    """Two NLD sequences decoded in lockstep (LockstepDecoder: one forward_batched
+    per round) produce the tokens and events of the same generators decoding each
+    sequence alone (engine forward per verify step), prefill and block commits
+    included, all on the simulated kernels."""
+    from specfold_amd.configs import SYNTHETIC_DRAFT_GRAPH
+    from specfold_amd.generate import nld_model_executor as nme
+    from specfold_amd.generate.lockstep import LockstepDecoder
+    from specfold_amd.generate.nld_folded import SpecFoldHIPNLDGeneration
+
+    monkeypatch.setattr(nme, "FoldedVerifyEngine", SimEngine)
+    shape = SHAPE_N4
+    ex = nme.NLDModelExecutor(make_nld_case(shape, 1, P=0, omax=64).model_cpu, device="cpu",
+                              block_length=8, max_length=128, page_order="shuffled", page_seed=3)
+    ex.engine.use_graphs = False
+    g = torch.Generator().manual_seed(9)
+    prompts = [torch.randint(0, shape.vocab - 2, (1, n), generator=g) for n in (12, 21)]
+    budgets = (16, 8)       # two blocks (a commit mid-run) / one: the loops end apart
+
+    def make():
+        return [SpecFoldHIPNLDGeneration(block_length=8, model_executor=ex,
+                                         calibration_graph=SYNTHETIC_DRAFT_GRAPH,
+                                         threshold=0.9, max_new_tokens=b, max_length=128,
+                                         delta=0.1, device="cpu") for b in budgets]
+
+    alone = []
+    for gen, p in zip(make(), prompts):
+        alone.append((list(gen.decode_steps(p)), gen._state["x_accum"].clone()))
+    gens = make()
+    dec = LockstepDecoder(gens)
+    per_seq = [[] for _ in prompts]
+    for rnd in dec.rounds(prompts):
+        for i, ev in rnd["events"]:
+            per_seq[i].append(ev)
+    for i, (ev, x) in enumerate(alone):
+        assert per_seq[i] == ev, i
+        assert torch.equal(gens[i]._state["x_accum"], x), i
+    assert dec.batched_steps > 0 and dec.draft_positions > 0
+    print(f"rounds {dec.rounds_run}, batched steps {dec.batched_steps}, "
+          f"fold ratio {dec.fold_ratio:.3f}")
