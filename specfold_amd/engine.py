@@ -140,36 +140,51 @@ class _Buffers:
 class _Batch:
     """Several sequences' branch trees stacked into one verify step: sequence s
     owns branches offsets[s] .. offsets[s] + sizes[s] - 1 (its main branch first)
-    and its own prefix cache.  The per-branch first positions and per-row q scales
-    are device tensors built once per call."""
+    and its own prefix cache.  Static device tensors, so a captured step replays
+    with new values: the per-branch first positions are re-read from the caches'
+    device-side lengths inside the step (refresh_positions), the per-row q scales
+    are copied into q_scale_rows before each run."""
 
     def __init__(self, eng: "FoldedVerifyEngine", sizes: List[int], caches: list, N: int,
-                 q_scales: Optional[list]):
+                 q_scaled: bool):
         dev = eng.device
         self.sizes = list(sizes)
         self.offsets = [sum(self.sizes[:i]) for i in range(len(self.sizes))]
         self.caches = list(caches)
         B1 = sum(self.sizes)
         i32 = dict(dtype=torch.int32, device=dev)
-        self.pos0_branch = torch.cat([
-            c.length_dev.expand(b) if c is not None else torch.zeros(b, **i32)
-            for c, b in zip(self.caches, self.sizes)]).contiguous()
-        self.q_scale_rows = None
-        if q_scales is not None and any(q is not None for q in q_scales):
-            ones = torch.ones(N, dtype=torch.float32, device=dev)
-            self.q_scale_rows = torch.cat([
-                (ones if q is None else q.reshape(-1).to(device=dev, dtype=torch.float32))
-                .repeat(b) for q, b in zip(q_scales, self.sizes)]).contiguous()
+        self.pos0_branch = torch.zeros(B1, **i32)
+        self._zeros = torch.zeros(max(self.sizes), **i32)
+        self.q_scale_rows = torch.ones(B1 * N, dtype=torch.float32, device=dev) \
+            if q_scaled else None
         self.bounds = torch.tensor([o * N for o in self.offsets] + [B1 * N], **i32)
         self.idx = torch.arange(B1 * N, **i32)
+        self.masked = torch.zeros(B1 * N, **i32)
+
+    def set_q_scales(self, q_scales: Optional[list], N: int) -> None:
+        if self.q_scale_rows is None:
+            return
+        for o, b, q in zip(self.offsets, self.sizes, q_scales):
+            dst = self.q_scale_rows[o * N:(o + b) * N].view(b, N)
+            if q is None:
+                dst.fill_(1.0)
+            else:
+                dst.copy_(q.reshape(1, N).to(dtype=torch.float32).expand(b, N))
+
+    def refresh_positions(self) -> None:
+        """pos0_branch[b] = its sequence's prefix length, read on the device."""
+        torch.cat([c.length_dev.expand(b) if c is not None else self._zeros[:b]
+                   for c, b in zip(self.caches, self.sizes)], out=self.pos0_branch)
 
     def split_rows(self, rows: torch.Tensor, count: torch.Tensor, bucket: int, N: int):
         """Per-sequence runs of the ascending compacted rows: (rows_s [S, bucket],
-        count_s [S]) on the device, without a host sync."""
+        count_s [S]) on the device, without a host sync (a binary search of the
+        sequences' first rows; no reduction kernel)."""
         idx = self.idx[:bucket]
-        valid = idx < count
-        below = (valid.unsqueeze(0) & (rows[:bucket].unsqueeze(0) < self.bounds.unsqueeze(1))
-                 ).sum(1, dtype=torch.int32)
+        masked = self.masked[:bucket]
+        # rows past the count -> B1*N, so the first `count` rows stay a sorted prefix
+        torch.where(idx < count, rows[:bucket], self.bounds[-1], out=masked)
+        below = torch.searchsorted(masked, self.bounds, out_int32=True)
         gather = (below[:-1].unsqueeze(1) + idx.unsqueeze(0)).clamp_(max=bucket - 1)
         rows_s = rows[gather.long()].contiguous()
         return rows_s, (below[1:] - below[:-1]).contiguous()
@@ -346,20 +361,24 @@ class FoldedVerifyEngine:
     def forward_batched(self, blocks: List[torch.Tensor], caches: list, delta: float = 0.1,
                         bucket: Optional[int] = None,
                         q_scales: Optional[List[Optional[torch.Tensor]]] = None,
-                        stats: Optional[StepStats] = None,
-                        compute_logits: bool = True) -> Optional[List[torch.Tensor]]:
+                        stats: Optional[StepStats] = None, compute_logits: bool = True,
+                        pad_to: Optional[int] = None) -> Optional[List[torch.Tensor]]:
         """One verify step over several independent sequences -> per-sequence logits
         [B1_s, N, V] (unshifted).
 
         blocks[s]  [B1_s, N] int64, sequence s's branches (row 0 = its main branch);
         caches[s]  its PagedKVCache (or None: no prefix); q_scales[s] optional [N].
+        pad_to     pad every sequence to this many branches with copies of its main
+                   branch (they gate as folded at every layer: no GEMM rows, no
+                   attention), so the step's shape, and its captured HIP graph,
+                   depend on the number of sequences only.
         The sequences' branches are stacked into one step of sum(B1_s) branches:
         the gate, compaction, GEMMs and chain correction run once over all of them
         (the main branch of every sequence is a root: SF_GATE_ROOTS_BY_PARENT), the
         QKV epilogue ropes each branch at its sequence's positions, and attention
         runs per sequence over its own prefix.  Each sequence's result is that of
         ``forward`` on it alone.  No counterpart in the reference, whose verify step
-        takes one sequence; runs eagerly (no HIP graph)."""
+        takes one sequence.  ``stats`` counts padded rows among the folded ones."""
         if not blocks or len(blocks) != len(caches):
             raise ValueError("forward_batched needs one cache (or None) per token block")
         if q_scales is not None and len(q_scales) != len(blocks):
@@ -371,6 +390,14 @@ class FoldedVerifyEngine:
         for c in caches:
             if c is not None and not isinstance(c, PagedKVCache):
                 raise TypeError("forward_batched takes PagedKVCache prefixes (or None)")
+        real = [int(b.shape[0]) for b in blocks]
+        orig_blocks = blocks
+        if pad_to is not None:
+            if max(real) > pad_to:
+                raise ValueError(f"a sequence has {max(real)} branches > pad_to={pad_to}")
+            blocks = [b if b.shape[0] == pad_to else
+                      torch.cat([b, b[0:1].expand(pad_to - b.shape[0], N)])
+                      for b in (x.to(self.device) for x in blocks)]
         sizes = [int(b.shape[0]) for b in blocks]
         tokens = torch.cat([b.to(self.device) for b in blocks]).contiguous()
         B1 = tokens.shape[0]
@@ -379,8 +406,14 @@ class FoldedVerifyEngine:
         P_alloc = max([c.capacity for c in caches if c is not None], default=0)
         buf = self.buffers(B1, N, bucket, P_alloc)
         self.rope_tables(max(cache_length(c) for c in caches) + N)
-        batch = _Batch(self, sizes, caches, N, q_scales)
-        hidden = self._run_layers(buf, tokens, None, delta, bucket, batch=batch)
+        q_scaled = q_scales is not None and any(q is not None for q in q_scales)
+        if self.use_graphs:
+            hidden = self._replay_batched(buf, tokens, sizes, caches, N, delta, bucket,
+                                          q_scales if q_scaled else None)
+        else:
+            batch = _Batch(self, sizes, caches, N, q_scaled)
+            batch.set_q_scales(q_scales, N)
+            hidden = self._run_layers(buf, tokens, None, delta, bucket, batch=batch)
         overflow = bucket < BN and int(buf.count_slab.max()) > bucket
         if stats is not None:
             stats.count_dev, stats.bucket, stats.overflow = buf.count_slab.clone(), bucket, overflow
@@ -388,13 +421,46 @@ class FoldedVerifyEngine:
         if overflow:
             logger.warning("SpecFold bucket overflow (> %d); recomputing with bucket=%d",
                            bucket, BN)
-            return self.forward_batched(blocks, caches, delta, bucket=BN, q_scales=q_scales,
-                                        stats=stats, compute_logits=compute_logits)
+            return self.forward_batched(orig_blocks, caches, delta, bucket=BN, q_scales=q_scales,
+                                        stats=stats, compute_logits=compute_logits,
+                                        pad_to=pad_to)
         self.last_hidden = hidden
         if not compute_logits:
             return None
         logits = torch.mm(buf.final, self.head.weight.t()).view(B1, N, self.V)
-        return list(logits.split(sizes, 0))
+        return [x[:r] for x, r in zip(logits.split(sizes, 0), real)]
+
+    def _replay_batched(self, buf: _Buffers, tokens: torch.Tensor, sizes: List[int],
+                        caches: list, N: int, delta: float, bucket: int,
+                        q_scales: Optional[list]):
+        """forward_batched's layers through a captured HIP graph, one per (branch
+        counts, caches, delta, bucket): the tokens and q scales go through static
+        buffers, the prefix lengths are read on the device inside the graph."""
+        key = ("batched", buf.key, id(buf), tuple(sizes),
+               tuple(self._cache_key(c) for c in caches), float(delta), bucket,
+               self.gate_mode, q_scales is not None)
+        entry = self._graphs.get(key)
+        if entry is None:
+            batch = _Batch(self, sizes, caches, N, q_scales is not None)
+            batch.set_q_scales(q_scales, N)
+            static_tok = tokens.clone()
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):      # warm-up launch outside the capture
+                self._run_layers(buf, static_tok, None, delta, bucket, batch=batch)
+            torch.cuda.current_stream().wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                out = self._run_layers(buf, static_tok, None, delta, bucket, batch=batch)
+            entry = (graph, static_tok, out, batch)
+            while len(self._graphs) >= self.max_graphs:
+                self._graphs.pop(next(iter(self._graphs)))
+            self._graphs[key] = entry
+        graph, static_tok, out, batch = entry
+        static_tok.copy_(tokens)
+        batch.set_q_scales(q_scales, N)
+        graph.replay()
+        return out
 
     # ------------------------------------------------------------------------
     def _run_layers(self, buf: _Buffers, tokens: torch.Tensor, cache,
@@ -422,6 +488,7 @@ class FoldedVerifyEngine:
                 if o:
                     par[o:o + b] += o
             gate_mode |= _lib.SF_GATE_ROOTS_BY_PARENT
+            batch.refresh_positions()
         hidden = base.embed_tokens(tokens).reshape(BN, D)
         cos, sin = self._rope
         pos0 = cache.length_dev if isinstance(cache, PagedKVCache) else buf.pos0
@@ -517,13 +584,20 @@ class FoldedVerifyEngine:
             self.hd, self.scaling, buf.o32, buf.o_bf, buf.m_tab, buf.z_tab, buf.ws_attn,
             prefix_len=plen, block_causal=causal)
 
+    @staticmethod
+    def _cache_key(cache):
+        """A paged cache's identity for a captured graph (its buffers' addresses)."""
+        if cache is None:
+            return None
+        return (id(cache), cache.k_pages.data_ptr(), cache.v_pages.data_ptr(),
+                cache.page_table.data_ptr(), cache.length_dev.data_ptr(), cache.capacity)
+
     def _graph_key(self, buf: _Buffers, cache, P: int, delta: float, bucket: int,
                    q_scaled: bool = False, causal: bool = False):
         if isinstance(cache, PagedKVCache):
             # the prefix length is read on the device: one graph for every length
             P = -1
-            ck = (id(cache), cache.k_pages.data_ptr(), cache.v_pages.data_ptr(),
-                  cache.page_table.data_ptr(), cache.length_dev.data_ptr(), cache.capacity)
+            ck = self._cache_key(cache)
         elif cache is None:
             ck = None
         else:

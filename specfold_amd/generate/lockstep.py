@@ -34,10 +34,15 @@ class LockstepDecoder:
     one batched verify step on the engine of the first generator (a
     SpecFoldHIPNLDGeneration; every generator shares its delta and bucket)."""
 
-    def __init__(self, gens: Sequence, forward_many: Optional[ForwardMany] = None):
+    def __init__(self, gens: Sequence, forward_many: Optional[ForwardMany] = None,
+                 pad: bool = True):
         if not gens:
             raise ValueError("LockstepDecoder needs at least one generator")
         self.gens = list(gens)
+        # every sequence padded to the most branches a step can have (main + one per
+        # draft-graph node), so a round's shape depends on the live sequences only
+        # and its captured graph is reused
+        self.pad_to = 1 + len(self.gens[0]._graph_nodes()) if pad else None
         self.forward_many = forward_many or self._engine_forward_many
         self.rounds_run = 0
         self.batched_steps = 0
@@ -58,8 +63,8 @@ class LockstepDecoder:
             g0._pack_layer_weights()
         eng = g0._engine
         N = requests[0][0].shape[1]
-        total = sum(b.shape[0] for b, _ in requests) * N
-        bucket = total if g0.fold_bucket is None else min(g0.fold_bucket, total)
+        total = sum(b.shape[0] for b, _ in requests) * N      # real (unpadded) rows
+        bucket = g0.fold_bucket      # None: every (padded) row
         cfg = g0.model_executor.model.config
         q_scales = [llama4_q_scale(cfg, cache_length(c), N, eng.device) for _, c in requests]
         stats = StepStats()
@@ -67,7 +72,7 @@ class LockstepDecoder:
         try:
             logits = eng.forward_batched([b for b, _ in requests], [c for _, c in requests],
                                          delta=g0.delta, bucket=bucket, q_scales=q_scales,
-                                         stats=stats)
+                                         stats=stats, pad_to=self.pad_to)
         finally:
             eng.gate_mode = prev_mode
         # fold counters stay on the device: every sequence's main branch is a root

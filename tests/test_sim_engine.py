@@ -101,14 +101,17 @@ def _batched_vs_single(model, seqs, delta, q_scales=None):
         st = StepStats()
         single.append(eng.forward(tok, _paged(kv), delta, q_scale=qs, stats=st))
         counts.append(st.counts)
-    stb = StepStats()
-    batched = eng.forward_batched([t for t, _ in seqs], [_paged(kv) for _, kv in seqs], delta,
-                                  q_scales=q_scales, stats=stb)
-    assert len(batched) == len(seqs)
-    for s, (a, b) in enumerate(zip(batched, single)):
-        assert a.shape == b.shape
-        assert torch.equal(a, b), (s, err_stats(a.float(), b.float()))
-    assert stb.counts == [sum(c) for c in zip(*counts)], (stb.counts, counts)
+    # unpadded, and every sequence padded with copies of its main branch (they fold
+    # at every layer, so the recomputed-row counts are unchanged too)
+    for pad_to in (None, max(t.shape[0] for t, _ in seqs) + 2):
+        stb = StepStats()
+        batched = eng.forward_batched([t for t, _ in seqs], [_paged(kv) for _, kv in seqs],
+                                      delta, q_scales=q_scales, stats=stb, pad_to=pad_to)
+        assert len(batched) == len(seqs)
+        for s, (a, b) in enumerate(zip(batched, single)):
+            assert a.shape == b.shape
+            assert torch.equal(a, b), (pad_to, s, err_stats(a.float(), b.float()))
+        assert stb.counts == [sum(c) for c in zip(*counts)], (pad_to, stb.counts, counts)
     return counts
 
 

@@ -12,6 +12,7 @@ import torch
 
 from oracle.folded_reference import llama4_q_scale
 from specfold_amd.engine import FoldedVerifyEngine, StepStats
+from specfold_amd.generate.nld_model_executor import llama4_q_scale as q_scale_dev
 from specfold_amd.kv_cache import PagedKVCache
 from tests.helpers import (SHAPE_G2, SHAPE_N4, draft_tree_block, err_stats, make_case,
                            make_nld_case, random_prefix_kv, to_gpu_model)
@@ -61,3 +62,39 @@ def test_batched_step_gpu(family):
     for a, b in zip(batched, single):
         st = err_stats(a.float(), b.float())
         assert st["max_abs"] <= 2e-2 * max(1.0, st["ref_absmax"]), st
+
+
+def test_batched_graph_replays_gpu():
+    """forward_batched through its captured HIP graph (padded shape) against the
+    eager run, three times, each sequence's cache grown by a committed block
+    between replays (the graph must re-read every prefix length and take the new
+    q scales), with eager work in between."""
+    shape = SHAPE_N4
+    model = to_gpu_model(make_nld_case(shape, 1, P=0, omax=64).model_cpu)
+    blocks, caches = [], []
+    for P, k, seed in ((40, 5, 31), (0, 3, 32), (17, 1, 33)):
+        gen = torch.Generator().manual_seed(seed)
+        blocks.append(draft_tree_block(32, shape.vocab - 1, gen)[:k].contiguous().cuda())
+        kv = random_prefix_kv(shape.layers, shape.kv_heads, P, shape.head_dim, gen) if P else None
+        c = _paged(kv)
+        if c is None:
+            c = PagedKVCache(shape.layers, shape.kv_heads, 128, 512, page_size=16,
+                             device="cuda", page_order="shuffled", seed=5)
+        caches.append(c)
+    eng = FoldedVerifyEngine(model)
+    for rep in range(3):
+        qss = [q_scale_dev(model.config, c.length, 32, "cuda") for c in caches]
+        print(f"[wip_batched_gpu] graph replay {rep} lengths={[c.length for c in caches]}",
+              flush=True)
+        eng.use_graphs = False
+        ref = eng.forward_batched(blocks, caches, 0.1, q_scales=qss, pad_to=6)
+        eng.use_graphs = True
+        got = eng.forward_batched(blocks, caches, 0.1, q_scales=qss, pad_to=6)
+        torch.cuda.synchronize()
+        for a, b in zip(got, ref):
+            assert torch.equal(a, b), err_stats(a.float(), b.float())
+        for c, b in zip(caches, blocks):      # commit each main branch: the prefixes grow
+            eng.use_graphs = False
+            eng.forward(b[0:1], c, 0.0, append=True,
+                        q_scale=q_scale_dev(model.config, c.length, 32, "cuda"))
+        torch.cuda.synchronize()
