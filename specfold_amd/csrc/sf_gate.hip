@@ -219,17 +219,17 @@ void launch_rows_any(int D, const uint16_t* hidden, const uint16_t* ffn, const i
                      uint16_t* xn, hipStream_t st) {
   const int vpl = (D / 8 + 63) / 64;
   if (vpl <= 4)
-    launch_rows<4, RESID, ROOTS>(hidden, ffn, src_prev, par, ln_w, B1, N, D, delta, eps, mode, hidden_out,
-                          rec, rstd, xn, st);
+    launch_rows<4, RESID, ROOTS>(hidden, ffn, src_prev, par, ln_w, B1, N, D, delta, eps, mode,
+                                 hidden_out, rec, rstd, xn, st);
   else if (vpl <= 8)
     launch_rows<8, RESID, ROOTS>(hidden, ffn, src_prev, par, ln_w, B1, N, D, delta, eps, mode,
-                          hidden_out, rec, rstd, xn, st);
+                                 hidden_out, rec, rstd, xn, st);
   else if (vpl <= 12)
     launch_rows<12, RESID, ROOTS>(hidden, ffn, src_prev, par, ln_w, B1, N, D, delta, eps, mode,
-                           hidden_out, rec, rstd, xn, st);
+                                  hidden_out, rec, rstd, xn, st);
   else
     launch_rows<16, RESID, ROOTS>(hidden, ffn, src_prev, par, ln_w, B1, N, D, delta, eps, mode,
-                           hidden_out, rec, rstd, xn, st);
+                                  hidden_out, rec, rstd, xn, st);
 }
 
 template <bool RESID>
