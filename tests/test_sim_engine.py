@@ -189,3 +189,23 @@ def test_nld_lockstep_decode_matches_separate_decodes(sim, monkeypatch):
     assert dec.batched_steps > 0 and dec.draft_positions > 0
     print(f"rounds {dec.rounds_run}, batched steps {dec.batched_steps}, "
           f"fold ratio {dec.fold_ratio:.3f}")
+
+
+def test_batched_step_rejects_bad_arguments(sim):
+    """forward_batched's host checks, before any launch."""
+    shape = SHAPE_G2
+    eng = SimEngine(make_case(shape, 1, P=0).model_cpu)
+    eng.use_graphs = False
+    a = torch.zeros(3, 32, dtype=torch.int64)
+    with pytest.raises(ValueError, match="one cache"):
+        eng.forward_batched([a, a], [None])
+    with pytest.raises(ValueError, match="one q scale"):
+        eng.forward_batched([a], [None], q_scales=[None, None])
+    with pytest.raises(ValueError, match="same N"):
+        eng.forward_batched([a, torch.zeros(2, 16, dtype=torch.int64)], [None, None])
+    with pytest.raises(TypeError, match="PagedKVCache"):
+        eng.forward_batched([a], [[(torch.zeros(1), torch.zeros(1))]])
+    with pytest.raises(ValueError, match="pad_to"):
+        eng.forward_batched([a], [None], pad_to=2)
+    with pytest.raises(ValueError, match="one cache"):
+        eng.forward_batched([], [])
