@@ -283,3 +283,39 @@ def test_kv_append_paged(sim):
         expect_v[int(table[p // ps]), :, p % ps] = kvv[row0 + t, 1]
     assert torch.equal(kc.view_as(expect_k), expect_k)
     assert torch.equal(vc.view_as(expect_v), expect_v)
+
+
+@pytest.mark.parametrize("mode", [_lib.SF_GATE_MODEL_DTYPE, _lib.SF_GATE_FP32_SQUARED])
+def test_gate_stacked_sequences(sim, mode):
+    """SF_GATE_ROOTS_BY_PARENT: three sequences' branch trees stacked in one call
+    (each root its own parent) give each tree's gate and compaction alone, indices
+    shifted by the tree's offset: recompute mask, count, compacted rows, src and
+    per-branch segment counts exactly, the normalized rows bit for bit."""
+    gen = torch.Generator().manual_seed(40 + mode)
+    N, D = 32, 512
+    ln_w = (1 + 0.1 * torch.randn(D, generator=gen)).to(torch.bfloat16)
+    trees = [list(TREE_PARENTS), [None], list(TREE_PARENTS[:5])]
+    hid = [perturbed_hidden(p, N, D, gen) for p in trees]
+    alone = [run_gate(sim, h, p, ln_w, 0.1, mode) for h, p in zip(hid, trees)]
+    sizes = [len(p) for p in trees]
+    offs = [sum(sizes[:i]) for i in range(len(sizes))]
+    B1 = sum(sizes)
+    par = torch.tensor([o + (0 if q is None else int(q)) for p, o in zip(trees, offs) for q in p],
+                       dtype=torch.int32)
+    out = gate_outputs(B1, N, D, B1 * N)
+    sim.fold_gate(torch.cat(hid).reshape(B1 * N, D).contiguous(), par, ln_w, B1, N, B1 * N, 0.1,
+                  1e-6, mode | _lib.SF_GATE_ROOTS_BY_PARENT, out["rec"], out["f"], out["src"],
+                  out["rows"], out["count"], out["seg"], out["segcnt"], out["rstd"], out["xn"])
+    assert torch.equal(out["rec"], torch.cat([a["rec"] for a in alone]))
+    counts = [int(a["count"]) for a in alone]
+    assert int(out["count"]) == sum(counts)
+    assert torch.equal(out["rows"][:sum(counts)],
+                       torch.cat([a["rows"][:c] + o * N for a, c, o in zip(alone, counts, offs)]))
+    assert torch.equal(out["src"], torch.cat([a["src"] + o for a, o in zip(alone, offs)]))
+    assert torch.equal(out["segcnt"], torch.cat([a["segcnt"] for a in alone]))
+    rows = out["rows"][:sum(counts)].long()
+    xn_alone = torch.cat([a["xn"] for a in alone])
+    rstd_alone = torch.cat([a["rstd"] for a in alone])
+    assert torch.equal(out["xn"][rows], xn_alone[rows])
+    assert torch.equal(out["rstd"][rows], rstd_alone[rows])
+    assert 0 < sum(counts) < B1 * N
