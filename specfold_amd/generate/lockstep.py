@@ -121,3 +121,15 @@ class LockstepDecoder:
             self.rounds_run += 1
             yield {"kind": "round", "committed": sum(e["committed"] for _, e in events),
                    "forwards": len(requests), "events": events}
+
+    def generate(self, prompts: Sequence) -> List[tuple]:
+        """Each sequence's ``generate_with_draft_speculation`` result (texts,
+        tokens_generated, model_calls, drafts_computed), the sequences decoded in
+        lockstep.  prompts: strings or [1, L] token ids, one per generator."""
+        ids = [g.tokenizer(p, return_tensors="pt").input_ids if isinstance(p, str) else p
+               for g, p in zip(self.gens, prompts)]
+        for g in self.gens:
+            g.last_commits = []
+        for _ in self.rounds(ids):
+            pass
+        return [g._result() for g in self.gens]

@@ -323,6 +323,16 @@ class NLDDiffusionGeneration:
         for _ in self.decode_steps(prompt_ids):
             if max_model_calls is not None and self._state["model_calls"] >= max_model_calls:
                 break
+        result = self._result()
+        elapsed = time.time() - t0
+        logger.info("Generated %d tokens in %.2fs (%.2f tok/s)", result[1], elapsed,
+                    result[1] / max(elapsed, 1e-9))
+        return result
+
+    def _result(self):
+        """(texts, tokens_generated, model_calls, drafts_computed) of the decode
+        state on ``self._state``: the generated ids up to the first EOS, masks
+        dropped (:300-316)."""
         st = self._state
         final_ids = st["x_accum"][0, st["prompt_len"]:]
         eos_id = self.stop_token
@@ -331,9 +341,5 @@ class NLDDiffusionGeneration:
             final_ids = final_ids[:int(stops[0]) + 1]
         kept = final_ids[final_ids != self.mask_id]
         text = self.tokenizer.batch_decode(kept.unsqueeze(0), skip_special_tokens=True)
-        tokens = int(kept.numel())
-        elapsed = time.time() - t0
         self.last_model_calls = st["model_calls"]
-        logger.info("Generated %d tokens in %.2fs (%.2f tok/s)", tokens, elapsed,
-                    tokens / max(elapsed, 1e-9))
-        return text, tokens, st["model_calls"], st["drafts_computed"]
+        return text, int(kept.numel()), st["model_calls"], st["drafts_computed"]

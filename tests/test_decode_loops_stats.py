@@ -241,3 +241,34 @@ def test_nld_lockstep_same_tokens_as_separate_loops(seeds):
         assert torch.equal(gens[i]._state["x_accum"], st_alone["x_accum"])
         assert gens[i]._state["model_calls"] == st_alone["model_calls"]
     assert max(sizes) == len(seeds) and dec.batched_steps == len(sizes)
+
+
+def test_nld_lockstep_generate_same_results():
+    """LockstepDecoder.generate returns, per sequence, what that generator's
+    generate_with_draft_speculation returns alone (texts, tokens, model calls,
+    drafts)."""
+    from specfold_amd.generate.lockstep import LockstepDecoder
+
+    def make(seed):
+        return NLDDiffusionGeneration(block_length=32, model_executor=FakeNLD(_bank(100 + seed,
+                                                                                  eos=FakeNLD.EOS)),
+                                      calibration_graph=SYNTHETIC_DRAFT_GRAPH,
+                                      max_new_tokens=64 + 32 * (seed % 2), threshold=0.9,
+                                      device="cpu")
+
+    seeds = (0, 1, 3)
+    prompts = ["lockstep %d" % s * (1 + s) for s in seeds]
+    alone = [make(s).generate_with_draft_speculation(prompt=p) for s, p in zip(seeds, prompts)]
+    gens = [make(s) for s in seeds]
+
+    def forward_many(requests):
+        # each request through its own generator's forward (the fake models differ)
+        out = []
+        for b, c in requests:
+            g = next(g for g in gens if g._state["cache"] is c)
+            out.append(g._batched_block_forward(b, c))
+        return out
+
+    got = LockstepDecoder(gens, forward_many=forward_many).generate(prompts)
+    assert got == alone
+    assert all(r[1] > 0 for r in got)
