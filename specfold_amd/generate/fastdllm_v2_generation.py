@@ -189,11 +189,16 @@ class FastDLLMV2SpeculativeGeneration:
         return int((tail[:, :first] == self.mask_id).sum()) == 0
 
     @torch.no_grad()
-    def decode_steps(self, prompt_ids: torch.Tensor):
+    def decode_steps(self, prompt_ids: torch.Tensor, defer_forward: bool = False):
         """The decode loop of generate_with_draft_speculation (:483-700) as a
         generator: yields one event per loop iteration —
         {"kind": "prefill" | "commit" | "verify" | "hit", "committed": tokens
-        unmasked by the iteration}.  Loop state is on ``self._state``."""
+        unmasked by the iteration}.  Loop state is on ``self._state``.
+
+        defer_forward: instead of calling ``_batched_block_forward`` the loop yields
+        {"kind": "forward", "batched": [B1, N] tokens, "cache": prefix cache,
+        "committed": 0} and continues with the shifted logits [B1, N, V] passed
+        back by ``send`` (specfold_amd.generate.lockstep)."""
         input_ids = prompt_ids.to(self.device)
         orig_len = input_ids.shape[1]
         bl, sbs = self.block_length, self.small_block_size
@@ -263,7 +268,14 @@ class FastDLLMV2SpeculativeGeneration:
                                 batched = torch.cat([main_block, states], dim=0)
                             else:
                                 batched = main_block
-                            logits = self._batched_block_forward(batched, st["cache"])
+                            if defer_forward:
+                                logits = yield {"kind": "forward", "batched": batched,
+                                                "cache": st["cache"], "committed": 0}
+                                if logits is None:
+                                    raise RuntimeError(
+                                        "a deferred forward needs its logits via send()")
+                            else:
+                                logits = self._batched_block_forward(batched, st["cache"])
                             st["model_calls"] += 1
                             main_logits = logits[0:1]
                             for i, d in enumerate(draft_blocks):
@@ -303,6 +315,16 @@ class FastDLLMV2SpeculativeGeneration:
         for _ in self.decode_steps(prompt_ids):
             if max_model_calls is not None and self._state["model_calls"] >= max_model_calls:
                 break
+        result = self._result()
+        elapsed = time.time() - t0
+        logger.info("Generated %d tokens in %.2fs (%.2f tok/s); model calls %d, drafts %d",
+                    result[1], elapsed, result[1] / max(elapsed, 1e-9), result[2], result[3])
+        return result
+
+    def _result(self):
+        """(text, tokens_generated, model_calls, drafts_computed) of the decode state
+        on ``self._state``: the generated ids up to the first stop token, masks
+        dropped (:700-720)."""
         st = self._state
         x_t = st["x_t"]
         final_ids = x_t[0, st["orig_len"]:]
@@ -311,12 +333,7 @@ class FastDLLMV2SpeculativeGeneration:
             final_ids = final_ids[:int(stops[0]) + 1]
         kept = final_ids[final_ids != self.mask_id]
         text = self.tokenizer.batch_decode(kept.unsqueeze(0), skip_special_tokens=True)
-        tokens = int(kept.numel())
-        elapsed = time.time() - t0
         self.last_model_calls = st["model_calls"]
         self.last_cache = st["cache"]
         self.last_tokens = x_t
-        logger.info("Generated %d tokens in %.2fs (%.2f tok/s); model calls %d, drafts %d",
-                    tokens, elapsed, tokens / max(elapsed, 1e-9), st["model_calls"],
-                    st["drafts_computed"])
-        return text, tokens, st["model_calls"], st["drafts_computed"]
+        return text, int(kept.numel()), st["model_calls"], st["drafts_computed"]

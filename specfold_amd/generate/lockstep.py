@@ -1,6 +1,7 @@
 """Several independent sequences decoded in lockstep, their verify steps merged.
 
-The NLD decode loop (NLDDiffusionGeneration.decode_steps) runs one sequence; a
+The decode loops (NLDDiffusionGeneration.decode_steps and
+FastDLLMV2SpeculativeGeneration.decode_steps) run one sequence each; a
 batch of B sequences stepped one after another streams every weight matrix B
 times per round of verify steps.  LockstepDecoder runs each sequence's loop with
 ``defer_forward=True``: in each round every live sequence advances to its next
@@ -21,7 +22,6 @@ from typing import Callable, Dict, List, Optional, Sequence
 import torch
 
 from specfold_amd.engine import StepStats
-from specfold_amd.generate.nld_model_executor import llama4_q_scale
 from specfold_amd.kv_cache import cache_length
 
 # [(batched [B1_s, N], prefix cache)] -> [logits [B1_s, N, V]]
@@ -29,10 +29,13 @@ ForwardMany = Callable[[List[tuple]], List[torch.Tensor]]
 
 
 class LockstepDecoder:
-    """Drives the decode loops of ``gens`` (NLD generators, one per sequence) in
-    lockstep.  ``forward_many`` computes a round's verify forwards; the default is
-    one batched verify step on the engine of the first generator (a
-    SpecFoldHIPNLDGeneration; every generator shares its delta and bucket)."""
+    """Drives the decode loops of ``gens`` (generators of one family, one per
+    sequence) in lockstep.  ``forward_many`` computes a round's verify forwards;
+    the default is one batched verify step on the engine of the first generator
+    (a SpecFoldHIPNLDGeneration or SpecFoldHIPFastDLLMV2Generation; every
+    generator shares its delta and bucket), with the executor's per-position q
+    scale where it has one (NLD) and the generator's logit shift where it has
+    one (Fast-dLLM)."""
 
     def __init__(self, gens: Sequence, forward_many: Optional[ForwardMany] = None,
                  pad: bool = True):
@@ -42,7 +45,9 @@ class LockstepDecoder:
         # every sequence padded to the most branches a step can have (main + one per
         # draft-graph node), so a round's shape depends on the live sequences only
         # and its captured graph is reused
-        self.pad_to = 1 + len(self.gens[0]._graph_nodes()) if pad else None
+        graph = getattr(self.gens[0], "calibration_graph", None) or {}
+        drafts = sum(1 for n in graph.get("selected_nodes", []) if n.get("ij_set"))
+        self.pad_to = 1 + drafts if pad else None
         self.forward_many = forward_many or self._engine_forward_many
         self.rounds_run = 0
         self.batched_steps = 0
@@ -65,8 +70,9 @@ class LockstepDecoder:
         N = requests[0][0].shape[1]
         total = sum(b.shape[0] for b, _ in requests) * N      # real (unpadded) rows
         bucket = g0.fold_bucket      # None: every (padded) row
-        cfg = g0.model_executor.model.config
-        q_scales = [llama4_q_scale(cfg, cache_length(c), N, eng.device) for _, c in requests]
+        q_scale = getattr(g0.model_executor, "q_scale", None)
+        q_scales = [q_scale(cache_length(c), N) if q_scale is not None else None
+                    for _, c in requests]
         stats = StepStats()
         prev_mode, eng.gate_mode = eng.gate_mode, g0.gate_mode
         try:
@@ -81,7 +87,8 @@ class LockstepDecoder:
         rec = stats.count_dev.sum(dtype=torch.int64) - L * N * len(requests)
         self._recomputed = rec if self._recomputed is None else self._recomputed + rec
         self.last_stats = stats
-        return logits
+        shift = getattr(g0, "_shift_logits", None)
+        return [shift(x) for x in logits] if shift is not None else logits
 
     def rounds(self, prompts: Sequence[torch.Tensor]):
         """Generator: one event per round, {"kind": "round", "committed": tokens
@@ -126,8 +133,14 @@ class LockstepDecoder:
         """Each sequence's ``generate_with_draft_speculation`` result (texts,
         tokens_generated, model_calls, drafts_computed), the sequences decoded in
         lockstep.  prompts: strings or [1, L] token ids, one per generator."""
-        ids = [g.tokenizer(p, return_tensors="pt").input_ids if isinstance(p, str) else p
-               for g, p in zip(self.gens, prompts)]
+        def prompt_ids(g, p):
+            if not isinstance(p, str):
+                return p
+            if hasattr(g, "_init_generation_state"):     # Fast-dLLM: its prompt template
+                return g._init_generation_state(p)[1]
+            return g.tokenizer(p, return_tensors="pt").input_ids
+
+        ids = [prompt_ids(g, p) for g, p in zip(self.gens, prompts)]
         for g in self.gens:
             g.last_commits = []
         for _ in self.rounds(ids):

@@ -272,3 +272,109 @@ def test_nld_lockstep_generate_same_results():
     got = LockstepDecoder(gens, forward_many=forward_many).generate(prompts)
     assert got == alone
     assert all(r[1] > 0 for r in got)
+
+
+def test_fastdllm_lockstep_same_results():
+    """Fast-dLLM loops in lockstep (deferred forwards) reproduce each sequence's
+    own loop: events, final tokens, and generate_with_draft_speculation's
+    results."""
+    from specfold_amd.generate.lockstep import LockstepDecoder
+
+    def make(seed):
+        g = FastDLLMV2SpeculativeGeneration(
+            block_length=32, model_executor=FakeFastDLLM(_bank(seed)),
+            calibration_graph=SYNTHETIC_DRAFT_GRAPH, max_new_tokens=64 + 32 * (seed % 2),
+            stop_token=7, device="cpu")
+        g.last_commits = []
+        return g
+
+    seeds = (0, 1, 2)
+
+    def forward_many_for(gens):
+        def forward_many(requests):
+            out = []
+            for b, c in requests:
+                g = next(g for g in gens if g._state["cache"] is c)
+                out.append(g._batched_block_forward(b, c))     # shifted, as the seam
+            return out
+        return forward_many
+
+    prompts = [torch.randint(0, 256, (1, 40 + 3 * s), generator=torch.Generator().manual_seed(s))
+               for s in seeds]
+    alone = []
+    for s, p in zip(seeds, prompts):
+        g = make(s)
+        alone.append((list(g.decode_steps(p)), g._state["x_t"].clone()))
+    gens = [make(s) for s in seeds]
+    per_seq = [[] for _ in seeds]
+    for rnd in LockstepDecoder(gens, forward_many=forward_many_for(gens)).rounds(prompts):
+        for i, ev in rnd["events"]:
+            per_seq[i].append(ev)
+    for i, (ev, x) in enumerate(alone):
+        assert per_seq[i] == ev
+        assert torch.equal(gens[i]._state["x_t"], x)
+    assert any(e["kind"] == "hit" for evs in per_seq for e in evs)
+
+    texts = ["lockstep fast-dllm %d" % s * (1 + s) for s in seeds]
+    want = [make(s).generate_with_draft_speculation(prompt=t) for s, t in zip(seeds, texts)]
+    gens = [make(s) for s in seeds]
+    got = LockstepDecoder(gens, forward_many=forward_many_for(gens)).generate(texts)
+    assert got == want
+
+
+def test_lockstep_engine_glue():
+    """The default batched forward of LockstepDecoder: one forward_batched call
+    with every request, the executor's q scale per sequence where it has one,
+    padding to the draft graph's width, the generator's logit shift applied per
+    sequence, and the fold counters over real draft rows only."""
+    from specfold_amd.generate.lockstep import LockstepDecoder
+
+    class Cache:
+        def __init__(self, n):
+            self.length = n
+
+        def get_seq_length(self):
+            return self.length
+
+    calls = []
+
+    class Eng:
+        L, gate_mode, device = 2, 0, torch.device("cpu")
+
+        def forward_batched(self, blocks, caches, delta, bucket, q_scales, stats, pad_to):
+            calls.append(dict(blocks=blocks, caches=caches, delta=delta, bucket=bucket,
+                              q_scales=q_scales, pad_to=pad_to))
+            stats.count_dev = torch.tensor([40, 36], dtype=torch.int32)
+            return [torch.arange(b.shape[0] * b.shape[1] * 3, dtype=torch.float32)
+                    .view(b.shape[0], b.shape[1], 3) for b in blocks]
+
+    def gen(executor, shift):
+        g = types.SimpleNamespace(_engine=Eng(), gate_mode=0, delta=0.2, fold_bucket=None,
+                                  model_executor=executor,
+                                  calibration_graph=SYNTHETIC_DRAFT_GRAPH)
+        if shift:
+            g._shift_logits = FastDLLMV2SpeculativeGeneration._shift_logits.__get__(g)
+        return g
+
+    n_drafts = sum(1 for n in SYNTHETIC_DRAFT_GRAPH["selected_nodes"] if n.get("ij_set"))
+    blocks = [torch.zeros(3, 8, dtype=torch.int64), torch.zeros(1, 8, dtype=torch.int64)]
+    caches = [Cache(5), Cache(70)]
+
+    # NLD-like: executor q scale, no shift
+    ex = types.SimpleNamespace(q_scale=lambda P, N: torch.full((N,), float(P)))
+    dec = LockstepDecoder([gen(ex, False), gen(ex, False)])
+    out = dec.forward_many(list(zip(blocks, caches)))
+    c = calls[-1]
+    assert c["pad_to"] == 1 + n_drafts and c["delta"] == 0.2 and c["bucket"] is None
+    assert [float(q[0]) for q in c["q_scales"]] == [5.0, 70.0]
+    assert torch.equal(out[0], torch.arange(72, dtype=torch.float32).view(3, 8, 3))
+    assert dec.draft_positions == (4 - 2) * 8 * 2
+    assert int(dec._recomputed) == 76 - 2 * 8 * 2
+
+    # Fast-dLLM-like: no q scale, logits shifted by one position per sequence
+    ex2 = types.SimpleNamespace()
+    dec2 = LockstepDecoder([gen(ex2, True), gen(ex2, True)])
+    out2 = dec2.forward_many(list(zip(blocks, caches)))
+    assert calls[-1]["q_scales"] == [None, None]
+    raw = torch.arange(72, dtype=torch.float32).view(3, 8, 3)
+    assert torch.equal(out2[0], torch.cat([raw[:, :1], raw[:, :-1]], dim=1))
