@@ -309,7 +309,8 @@ def main(argv=None) -> int:
     t0 = time.time()
     if lockstep:
         from specfold_amd.generate.lockstep import LockstepDecoder
-        rounds = LockstepDecoder(gens).rounds(prompts)
+        dec = LockstepDecoder(gens)
+        rounds = dec.rounds(prompts)
         first = next(rounds)      # every sequence's prefill, then the first batched step
         assert [e["kind"] for _, e in first["events"]] == ["prefill"] * len(gens)
 
@@ -355,15 +356,20 @@ def main(argv=None) -> int:
     gen = gens[0]
     cache = gen._state["cache"]
     x_cur = gen._state["x_t"] if w.family == "fastdllm" else gen._state["x_accum"]
-    main_block = x_cur[:, -w.block:]
     from specfold_amd.synthetic import TREE_DIFFS
     diffs = TREE_DIFFS[:w.branches]
-    batched = main_block.repeat(len(diffs), 1)
     gsel = torch.Generator().manual_seed(123)
-    repl = torch.randint(0, w.shape.vocab - 1, (7,), generator=gsel).to(batched.device)
-    for i, d in enumerate(diffs):
-        for k in d:
-            batched[i, k] = repl[k]
+    repl = torch.randint(0, w.shape.vocab - 1, (7,), generator=gsel).to(x_cur.device)
+
+    def tree_batch(x):
+        """The draft tree's B+1 branches over the last block of token state x."""
+        b = x[:, -w.block:].repeat(len(diffs), 1)
+        for i, d in enumerate(diffs):
+            for k in d:
+                b[i, k] = repl[k]
+        return b
+
+    batched = tree_batch(x_cur)
     lat = []
     for i in range(args.verify_iters + 3):
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -380,6 +386,27 @@ def main(argv=None) -> int:
     fold_ratio_step = 1 - (sum(counts) - len(counts) * N) / ((B1 - 1) * N * len(counts))
     print(f"[bench] verify step median {verify_ms:.3f} ms, mean R {R}", file=sys.stderr,
           flush=True)
+    batched_step = None
+    if lockstep:
+        # the batched verify step alone: every sequence's B+1-branch batch at its own
+        # prefix, in one step (as a lockstep round runs it)
+        reqs = [(tree_batch(g._state["x_t"] if w.family == "fastdllm" else g._state["x_accum"]),
+                 g._state["cache"]) for g in gens]
+        lat_b = []
+        for i in range(args.verify_iters + 3):
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            dec.forward_many(reqs)
+            e.record()
+            e.synchronize()
+            if i >= 3:
+                lat_b.append(s.elapsed_time(e))
+        ms_b = statistics.median(lat_b)
+        batched_step = {"ms": round(ms_b, 4), "sequences": len(reqs),
+                        "branches_each": len(diffs), "pad_to": dec.pad_to,
+                        "ms_per_sequence": round(ms_b / len(reqs), 4)}
+        print(f"[bench] batched verify step ({len(reqs)} sequences) median {ms_b:.3f} ms",
+              file=sys.stderr, flush=True)
 
     # per-kernel timings on the buffers of the last verify step, cycling through the
     # layers (weights and cache slices) as the step does
@@ -442,6 +469,7 @@ def main(argv=None) -> int:
                    "lockstep": lockstep,
                    "parallelism": "none (1 GPU)"},
         "verify_step_ms": round(verify_ms, 4),
+        "verify_step_batched": batched_step,
         "verify_step_prefix": P,
         "verify_recomputed_rows_mean": R,
         "verify_fold_ratio": round(fold_ratio_step, 4),
