@@ -209,3 +209,29 @@ def test_batched_step_rejects_bad_arguments(sim):
         eng.forward_batched([a], [None], pad_to=2)
     with pytest.raises(ValueError, match="one cache"):
         eng.forward_batched([], [])
+
+
+def test_batched_step_bucket_overflow_retry(sim):
+    """A bucket below the recomputed count overflows; forward_batched then redoes
+    the step with every row (padding kept), and its logits equal the unbucketed
+    step's."""
+    from specfold_amd.engine import StepStats
+    from tests.helpers import draft_tree_block, random_prefix_kv
+    shape = SHAPE_G2
+    model = make_case(shape, 1, P=0).model_cpu
+    eng = SimEngine(model)
+    eng.use_graphs = False
+    blocks, kvs = [], []
+    for P, k, seed in ((50, 4, 41), (0, 2, 42)):
+        gen = torch.Generator().manual_seed(seed)
+        blocks.append(draft_tree_block(32, shape.vocab, gen)[:k].contiguous())
+        kvs.append(random_prefix_kv(shape.layers, shape.kv_heads, P, shape.head_dim, gen)
+                   if P else None)
+    ref = eng.forward_batched(blocks, [_paged(kv) for kv in kvs], 0.1, pad_to=5)
+    st = StepStats()
+    got = eng.forward_batched(blocks, [_paged(kv) for kv in kvs], 0.1, bucket=40, pad_to=5,
+                              stats=st)
+    assert st.overflow is False and st.bucket == 10 * 32     # the retry's stats
+    assert [g.shape[0] for g in got] == [4, 2]
+    for a, b in zip(got, ref):
+        assert torch.equal(a, b)
