@@ -23,16 +23,18 @@ namespace sfg {
 #ifndef SFG_MB
 #define SFG_MB 64
 #endif
-constexpr int kMB = SFG_MB;       // rows of A per workgroup
+constexpr int kMB = SFG_MB;       // rows of A per workgroup (default of every kernel)
 constexpr int kKC = 128;          // K per LDS stage
 constexpr int kLdsStride = 136;   // bf16 per LDS row (128 + 8 pad: 272 B, spreads banks)
 constexpr int kMT = kMB / 16;     // max m tiles per workgroup
 
-// Shared memory of one workgroup: two A stages + the row index table.
-struct Smem {
-  uint16_t a[2][kMB * kLdsStride];
-  int rows[kMB];
+// Shared memory of one workgroup of MB rows: two A stages + the row index table.
+template <int MB>
+struct SmemT {
+  uint16_t a[2][MB * kLdsStride];
+  int rows[MB];
 };
+using Smem = SmemT<kMB>;
 
 // Prefetch depth: a ring of SFG_RING register slots per wave (A rows and weights
 // of one K stage each), so every wave keeps SFG_RING-1 stages of loads
@@ -60,10 +62,10 @@ struct Smem {
 // buffered) only at the start of iteration s, followed by the one barrier of the
 // stage.  Loads past the last stage re-read it and rows past mrows re-read the
 // last row (clamped, no branches), which keeps the wait counts exact.
-template <int WN, int NMT>
+template <int WN, int NMT, int MB = kMB>
 SF_DEV void mainloop(const uint16_t* __restrict__ A, int lda, int mrows,
-                     const uint16_t* const (&wrow)[WN], int s0, int s1, Smem& sm,
-                     sf_f32x4 (&acc)[kMT][WN]) {
+                     const uint16_t* const (&wrow)[WN], int s0, int s1, SmemT<MB>& sm,
+                     sf_f32x4 (&acc)[MB / 16][WN]) {
   constexpr int R = SFG_RING;
   static_assert(R % 2 == 0, "ring depth must be even (LDS double buffer parity)");
   const int tid = threadIdx.x;
@@ -175,22 +177,23 @@ struct Epi {
 // tiles of 16 per wave (kSilu: WN = 2 = the gate and the up tile of the same 16
 // output columns).  Grid: (plan_grid, 1, m blocks).  part: fp32 partial slots
 // [slot][mcap][N].
-template <int WN, int MODE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(SFG_WAVES, SFG_WAVES)))
+template <int WN, int MODE, int MB = kMB, int WAVES = SFG_WAVES>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES, WAVES)))
 void gemm_sk_kernel(const uint16_t* __restrict__ A, const int32_t* __restrict__ a_rows, int lda,
                     const int32_t* __restrict__ count_p, int m_static, int mcap,
                     const uint16_t* __restrict__ W0, const uint16_t* __restrict__ W1, int K, int N,
                     Plan plan, float* __restrict__ part, Epi ep) {
-  __shared__ Smem sm;
+  constexpr int kMT = MB / 16;    // max m tiles of this kernel's row block
+  __shared__ SmemT<MB> sm;
   const int M = count_p ? min(*count_p, mcap) : m_static;
-  const int m0 = blockIdx.z * kMB;
+  const int m0 = blockIdx.z * MB;
   if (m0 >= M) return;
-  const int mrows = min(kMB, M - m0);
+  const int mrows = min(MB, M - m0);
   const int nmt = (mrows + 15) >> 4;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = tid >> 6;
-  if (tid < kMB) {
+  if (tid < MB) {
     const int r = m0 + min(tid, mrows - 1);
     sm.rows[tid] = a_rows ? a_rows[r] : r;
   }
@@ -224,10 +227,10 @@ void gemm_sk_kernel(const uint16_t* __restrict__ A, const int32_t* __restrict__ 
 #pragma unroll
       for (int tt = 0; tt < WN; ++tt) acc[mt][tt] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
     switch (nmt) {
-      case 1: mainloop<WN, 1>(A, lda, mrows, wrow, sa, sb, sm, acc); break;
-      case 2: mainloop<WN, 2>(A, lda, mrows, wrow, sa, sb, sm, acc); break;
-      case 3: mainloop<WN, 3>(A, lda, mrows, wrow, sa, sb, sm, acc); break;
-      default: mainloop<WN, kMT>(A, lda, mrows, wrow, sa, sb, sm, acc); break;
+      case 1: mainloop<WN, 1, MB>(A, lda, mrows, wrow, sa, sb, sm, acc); break;
+      case 2: mainloop<WN, 2, MB>(A, lda, mrows, wrow, sa, sb, sm, acc); break;
+      case 3: mainloop<WN, 3, MB>(A, lda, mrows, wrow, sa, sb, sm, acc); break;
+      default: mainloop<WN, kMT, MB>(A, lda, mrows, wrow, sa, sb, sm, acc); break;
     }
     const int first = tile_first(t, plan);
     const bool whole = MODE != kPart && tile_last(t, plan) == first;
@@ -266,14 +269,17 @@ void gemm_sk_kernel(const uint16_t* __restrict__ A, const int32_t* __restrict__ 
   }
 }
 
-template <int WN, int MODE>
+// MB rows per workgroup (grid z = row blocks), register allocation for WAVES
+// waves per SIMD; every launch here uses the defaults.
+template <int WN, int MODE, int MB = kMB, int WAVES = SFG_WAVES>
 inline void launch_sk(const Plan& p, const uint16_t* A, const int32_t* a_rows, int lda,
                       const int32_t* count_p, int m_static, int mcap, const uint16_t* W0,
                       const uint16_t* W1, int K, int N, float* part, const Epi& ep,
                       hipStream_t st) {
-  dim3 grid(plan_grid(p), 1, (mcap + kMB - 1) / kMB);
-  hipLaunchKernelGGL((gemm_sk_kernel<WN, MODE>), grid, dim3(256), 0, st, A, a_rows, lda, count_p,
-                     m_static, mcap, W0, W1, K, N, p, part, ep);
+  static_assert(MB % 16 == 0 && MB >= 16 && MB <= 256, "row block: 16..256 rows, whole m tiles");
+  dim3 grid(plan_grid(p), 1, (mcap + MB - 1) / MB);
+  hipLaunchKernelGGL((gemm_sk_kernel<WN, MODE, MB, WAVES>), grid, dim3(256), 0, st, A, a_rows,
+                     lda, count_p, m_static, mcap, W0, W1, K, N, p, part, ep);
 }
 
 }  // namespace sfg
