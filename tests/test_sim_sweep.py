@@ -2,9 +2,10 @@
 shapes the fixed cases of test_sim_attention.py, test_sim_gemm.py and
 test_sim_gate.py do not name: attention (prefix length, page size, branches,
 block length, head grouping, recomputed rows, causal block), the GEMMs (D, I,
-recomputed rows, bucket, static M) and the gate with compaction (forests of up
+recomputed rows, bucket, static M), the gate with compaction (forests of up
 to 32 branches, block lengths, widths, all three gate modes, buckets below, at
-and above the recomputed count).  Same checks as the fixed cases.
+and above the recomputed count) and gate -> attention -> chain correction at
+random prefix lengths and inputs.  Same checks as the fixed cases.
 
 SF_SIM_SWEEP=<n> sets the number of attention and GEMM shapes (default 4 each;
 the gate takes 8x as many cases); SF_SIM_SWEEP_SEED picks another sweep."""
@@ -20,6 +21,7 @@ from specfold_amd import _lib
 from specfold_amd.engine import build_parent_map
 from tests.test_gpu_gate import check_outputs, ref_mask
 from tests.test_sim_attention import attn_sim  # noqa: F401  (fixture)
+import tests.test_sim_gate as sim_gate
 from tests.test_sim_gate import run_gate, sim  # noqa: F401  (fixture)
 from tests.test_sim_gemm import gemm_sim  # noqa: F401  (fixture)
 
@@ -99,3 +101,13 @@ def test_gate_sweep(sim):  # noqa: F811
         except AssertionError as e:
             raise AssertionError(f"seed={seed} B1={B1} N={N} D={D} mode={mode} "
                                  f"delta={delta} bucket={bucket}: {e}") from None
+
+
+def chain_cases():
+    rng = random.Random(SEED + 3)
+    return [(rng.randint(0, 600), rng.randint(10, 10**6)) for _ in range(max(1, COUNT // 2))]
+
+
+@pytest.mark.parametrize("P,seed", chain_cases())
+def test_chain_sweep(sim, P, seed):  # noqa: F811
+    sim_gate.test_gate_attention_chain(sim, P, seed)
