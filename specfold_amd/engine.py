@@ -399,9 +399,12 @@ class FoldedVerifyEngine:
                       torch.cat([b, b[0:1].expand(pad_to - b.shape[0], N)])
                       for b in (x.to(self.device) for x in blocks)]
         sizes = [int(b.shape[0]) for b in blocks]
-        tokens = torch.cat([b.to(self.device) for b in blocks]).contiguous()
-        B1 = tokens.shape[0]
+        B1 = sum(sizes)
         BN = B1 * N
+        if B1 > 64 or BN > 1024:
+            raise ValueError(f"a batched step holds at most 64 branches and 1024 rows: "
+                             f"{len(sizes)} sequences of {sizes} branches x {N} = {BN} rows")
+        tokens = torch.cat([b.to(self.device) for b in blocks]).contiguous()
         bucket = BN if bucket is None else max(1, min(int(bucket), BN))
         P_alloc = max([c.capacity for c in caches if c is not None], default=0)
         buf = self.buffers(B1, N, bucket, P_alloc)

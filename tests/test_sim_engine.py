@@ -209,6 +209,8 @@ def test_batched_step_rejects_bad_arguments(sim):
         eng.forward_batched([a], [None], pad_to=2)
     with pytest.raises(ValueError, match="one cache"):
         eng.forward_batched([], [])
+    with pytest.raises(ValueError, match="at most 64 branches and 1024 rows"):
+        eng.forward_batched([a] * 4, [None] * 4, pad_to=9)      # 4 x 9 x 32 = 1152 rows
 
 
 def test_batched_step_bucket_overflow_retry(sim):
