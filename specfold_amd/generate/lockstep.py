@@ -73,20 +73,38 @@ class LockstepDecoder:
         q_scale = getattr(g0.model_executor, "q_scale", None)
         q_scales = [q_scale(cache_length(c), N) if q_scale is not None else None
                     for _, c in requests]
-        stats = StepStats()
+        # a batched step holds at most 64 branches and 1024 rows: split the round
+        # into as few steps as fit
+        chunks, cur, cur_b = [], [], 0
+        for i, (b, _) in enumerate(requests):
+            nb = self.pad_to or b.shape[0]
+            if cur and (cur_b + nb > 64 or (cur_b + nb) * N > 1024):
+                chunks.append(cur)
+                cur, cur_b = [], 0
+            cur.append(i)
+            cur_b += nb
+        chunks.append(cur)
+        logits = [None] * len(requests)
+        rec = None
         prev_mode, eng.gate_mode = eng.gate_mode, g0.gate_mode
         try:
-            logits = eng.forward_batched([b for b, _ in requests], [c for _, c in requests],
-                                         delta=g0.delta, bucket=bucket, q_scales=q_scales,
-                                         stats=stats, pad_to=self.pad_to)
+            for idx in chunks:
+                stats = StepStats()
+                out = eng.forward_batched([requests[i][0] for i in idx],
+                                          [requests[i][1] for i in idx], delta=g0.delta,
+                                          bucket=bucket, q_scales=[q_scales[i] for i in idx],
+                                          stats=stats, pad_to=self.pad_to)
+                for i, x in zip(idx, out):
+                    logits[i] = x
+                # fold counters stay on the device: every sequence's main branch is a root
+                r = stats.count_dev.sum(dtype=torch.int64) - eng.L * N * len(idx)
+                rec = r if rec is None else rec + r
+                self.last_stats = stats
         finally:
             eng.gate_mode = prev_mode
-        # fold counters stay on the device: every sequence's main branch is a root
-        L = eng.L
-        self.draft_positions += (total - len(requests) * N) * L
-        rec = stats.count_dev.sum(dtype=torch.int64) - L * N * len(requests)
+        self.batched_steps += len(chunks) - 1      # rounds() counts one step per round
+        self.draft_positions += (total - len(requests) * N) * eng.L
         self._recomputed = rec if self._recomputed is None else self._recomputed + rec
-        self.last_stats = stats
         shift = getattr(g0, "_shift_logits", None)
         return [shift(x) for x in logits] if shift is not None else logits
 

@@ -378,3 +378,13 @@ def test_lockstep_engine_glue():
     assert calls[-1]["q_scales"] == [None, None]
     raw = torch.arange(72, dtype=torch.float32).view(3, 8, 3)
     assert torch.equal(out2[0], torch.cat([raw[:, :1], raw[:, :-1]], dim=1))
+
+    # a round beyond 1024 rows is split: 5 sequences padded to 9 branches x 32 rows
+    dec3 = LockstepDecoder([gen(ex2, False)] * 5)
+    dec3.pad_to = 9
+    n0 = len(calls)
+    big = [(torch.zeros(2, 32, dtype=torch.int64), Cache(3)) for _ in range(5)]
+    out3 = dec3.forward_many(big)
+    split = [len(c["blocks"]) for c in calls[n0:]]
+    assert split == [3, 2] and len(out3) == 5 and dec3.batched_steps == 1
+    assert int(dec3._recomputed) == 2 * 76 - 5 * 32 * 2
