@@ -369,16 +369,21 @@ class FoldedVerifyEngine:
         blocks[s]  [B1_s, N] int64, sequence s's branches (row 0 = its main branch);
         caches[s]  its PagedKVCache (or None: no prefix); q_scales[s] optional [N].
         pad_to     pad every sequence to this many branches with copies of its main
-                   branch (they gate as folded at every layer: no GEMM rows, no
-                   attention), so the step's shape, and its captured HIP graph,
-                   depend on the number of sequences only.
+                   branch, so the step's shape, and its captured HIP graph, depend
+                   on the number of sequences only.  A copy is no branch's parent
+                   and leaves every other row's result unchanged; it gates as
+                   folded (no GEMM rows, no attention) wherever delta > 0.  At
+                   delta = 0 a copy's chain-corrected attention output, which may
+                   round one bf16 step away from its main branch's, can make it
+                   recompute at later layers: extra rows, same results.
         The sequences' branches are stacked into one step of sum(B1_s) branches:
         the gate, compaction, GEMMs and chain correction run once over all of them
         (the main branch of every sequence is a root: SF_GATE_ROOTS_BY_PARENT), the
         QKV epilogue ropes each branch at its sequence's positions, and attention
         runs per sequence over its own prefix.  Each sequence's result is that of
         ``forward`` on it alone.  No counterpart in the reference, whose verify step
-        takes one sequence.  ``stats`` counts padded rows among the folded ones."""
+        takes one sequence.  ``stats`` counts every recomputed row, padded ones
+        included."""
         if not blocks or len(blocks) != len(caches):
             raise ValueError("forward_batched needs one cache (or None) per token block")
         if q_scales is not None and len(q_scales) != len(blocks):

@@ -57,7 +57,9 @@ class LockstepDecoder:
 
     @property
     def fold_ratio(self) -> float:
-        """Share of draft rows folded over every batched step (one host read)."""
+        """Share of draft rows folded over every batched step (one host read).  At
+        delta = 0 a padding branch recomputed at a later layer counts as a
+        recomputed draft row (see FoldedVerifyEngine.forward_batched)."""
         if not self.draft_positions:
             return float("nan")
         return 1.0 - int(self._recomputed) / self.draft_positions
