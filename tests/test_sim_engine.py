@@ -237,3 +237,36 @@ def test_batched_step_bucket_overflow_retry(sim):
     assert [g.shape[0] for g in got] == [4, 2]
     for a, b in zip(got, ref):
         assert torch.equal(a, b)
+
+
+def test_batched_padding_at_delta_zero(sim):
+    """At delta = 0 a padding copy of a main branch can be recomputed at a later
+    layer (its chain-corrected attention output rounds one bf16 step off its main
+    branch's); every real sequence's logits stay those of its own step.  The
+    case an engine-level random sweep found: NLD, four sequences padded to 7."""
+    from specfold_amd.engine import StepStats
+    from tests.helpers import draft_tree_block, random_prefix_kv
+    shape = SHAPE_N4
+    model = make_nld_case(shape, 1, P=0, omax=64).model_cpu
+    eng = SimEngine(model)
+    eng.use_graphs = False
+    seqs, qss = [], []
+    for k, P, seed in ((2, 6, 470481935), (7, 60, 166478675), (1, 129, 143982545),
+                       (2, 97, 416689676)):
+        g = torch.Generator().manual_seed(seed)
+        tok = draft_tree_block(32, shape.vocab - 1, g)[:k].contiguous()
+        kv = random_prefix_kv(shape.layers, shape.kv_heads, P, shape.head_dim, g) if P else None
+        seqs.append((tok, kv))
+        qss.append(llama4_q_scale(model.config, P, 32))
+    single, counts = [], []
+    for (t, kv), q in zip(seqs, qss):
+        st = StepStats()
+        single.append(eng.forward(t, _paged(kv), 0.0, q_scale=q, stats=st))
+        counts.append(st.counts)
+    st = StepStats()
+    got = eng.forward_batched([t for t, _ in seqs], [_paged(kv) for _, kv in seqs], 0.0,
+                              q_scales=qss, stats=st, pad_to=7)
+    for a, b in zip(got, single):
+        assert torch.equal(a, b)
+    real = [sum(c) for c in zip(*counts)]
+    assert all(b >= r for b, r in zip(st.counts, real)) and st.counts[0] == real[0]
