@@ -2,10 +2,7 @@
 SF_GATE_ROOTS_BY_PARENT gate): several sequences in one verify step against each
 sequence's own forward.  Integer outputs (per-layer recomputed-row counts) must
 be identical; logits within the parity tolerance (o_proj and lm_head run on
-hipBLASLt, whose kernel choice may change with M = total rows).
-
-Not collected by pytest until it has passed on the GPU; run it by naming it:
-python -m pytest tests/wip_batched_gpu.py -m gpu."""
+hipBLASLt, whose kernel choice may change with M = total rows)."""
 
 import pytest
 import torch
@@ -47,7 +44,7 @@ def test_batched_step_gpu(family):
         seqs.append((tok.cuda(), kv))
         qs = llama4_q_scale(model.config, P, 32) if family == "nld" else None
         qss.append(qs.cuda() if qs is not None else None)
-    print(f"[wip_batched_gpu] {family} specs={specs}", flush=True)
+    print(f"[batched_gpu] {family} specs={specs}", flush=True)
     eng = FoldedVerifyEngine(model)
     single, counts = [], []
     for (tok, kv), qs in zip(seqs, qss):
@@ -84,7 +81,7 @@ def test_batched_graph_replays_gpu():
     eng = FoldedVerifyEngine(model)
     for rep in range(3):
         qss = [q_scale_dev(model.config, c.length, 32, "cuda") for c in caches]
-        print(f"[wip_batched_gpu] graph replay {rep} lengths={[c.length for c in caches]}",
+        print(f"[batched_gpu] graph replay {rep} lengths={[c.length for c in caches]}",
               flush=True)
         eng.use_graphs = False
         ref = eng.forward_batched(blocks, caches, 0.1, q_scales=qss, pad_to=6)
