@@ -139,6 +139,23 @@ class FoldCounters:
 # one layer
 # ---------------------------------------------------------------------------
 
+def delta_gate(x: torch.Tensor, x_par: torch.Tensor, delta: float) -> torch.Tensor:
+    """Recompute mask [N] of a draft branch: relative L2 residual against its
+    parent's hidden states, both norms taken in the model dtype.  Follows
+    fastdllm_v2_folded.py:136-141 (``(x - xp).norm(-1) > delta * xp.norm(-1)``).
+    ``x``, ``x_par``: [1, N, D]."""
+    resid_norm = (x[0] - x_par[0]).norm(dim=-1)
+    par_norm = x_par[0].norm(dim=-1)
+    return resid_norm > delta * par_norm
+
+
+def gate_margin(x: torch.Tensor, x_par: torch.Tensor, delta: float) -> torch.Tensor:
+    """fp64 distance of each position from the gate's threshold,
+    ||x - x_par|| / ||x_par|| - delta (diagnostic for a mask disagreement)."""
+    xd, pd = x[0].double(), x_par[0].double()
+    return (xd - pd).norm(dim=-1) / pd.norm(dim=-1).clamp_min(1e-300) - delta
+
+
 def folded_layer(
     lyr,
     h: List[torch.Tensor],
@@ -200,9 +217,7 @@ def folded_layer(
         if p is None:
             rsel = torch.arange(N, device=dev)
         else:
-            resid_norm = (x[0] - h[p][0]).norm(dim=-1)
-            par_norm = h[p][0].norm(dim=-1)
-            rsel = (resid_norm > delta * par_norm).nonzero(as_tuple=True)[0]
+            rsel = delta_gate(x, h[p], delta).nonzero(as_tuple=True)[0]
             if counters is not None:
                 counters.draft_positions += N
                 counters.draft_recomputed += int(rsel.numel())

@@ -217,21 +217,26 @@ SF_DEV void prefix_item(const uint16_t* __restrict__ q_buf, const uint16_t* __re
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = acc[i] * alpha;
 
-    // acc += V^T P^T; P split into bf16 hi + lo
+    // acc += V^T P^T; P split into three bf16 parts hi + mid + lo (24 bits: the
+    // products P*V are those of the reference's fp32 einsum)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int kt0 = 2 * j, kt1 = 2 * j + 1;
-      sf_u32x4 hi, lo;
+      sf_u32x4 hi, mid, lo;
 #pragma unroll
       for (int w2 = 0; w2 < 2; ++w2) {
-        const float a0 = s[kt0][2 * w2], a1 = s[kt0][2 * w2 + 1];
-        const float b0 = s[kt1][2 * w2], b1 = s[kt1][2 * w2 + 1];
-        hi[w2] = sf_pack2(a0, a1);
-        hi[2 + w2] = sf_pack2(b0, b1);
-        lo[w2] = sf_pack2(a0 - sf_rbf(a0), a1 - sf_rbf(a1));
-        lo[2 + w2] = sf_pack2(b0 - sf_rbf(b0), b1 - sf_rbf(b1));
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int kt = t ? kt1 : kt0;
+          const float a0 = s[kt][2 * w2], a1 = s[kt][2 * w2 + 1];
+          const float r0 = a0 - sf_rbf(a0), r1 = a1 - sf_rbf(a1);
+          hi[2 * t + w2] = sf_pack2(a0, a1);
+          mid[2 * t + w2] = sf_pack2(r0, r1);
+          lo[2 * t + w2] = sf_pack2(r0 - sf_rbf(r0), r1 - sf_rbf(r1));
+        }
       }
       const sf_bf16x8 bhi = sf_as_bf16x8(hi);
+      const sf_bf16x8 bmid = sf_as_bf16x8(mid);
       const sf_bf16x8 blo = sf_as_bf16x8(lo);
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
@@ -242,8 +247,9 @@ SF_DEV void prefix_item(const uint16_t* __restrict__ q_buf, const uint16_t* __re
         const sf_u32x2 a1 = *reinterpret_cast<const sf_u32x2*>(vrow + ((4 * kt1 + grp) ^ sw) * 4);
         const sf_u32x4 vf = {a0[0], a0[1], a1[0], a1[1]};
         const sf_bf16x8 va = sf_as_bf16x8(vf);
-        acc[dt] = sf_mfma16x16x32(va, bhi, acc[dt]);
         acc[dt] = sf_mfma16x16x32(va, blo, acc[dt]);
+        acc[dt] = sf_mfma16x16x32(va, bmid, acc[dt]);
+        acc[dt] = sf_mfma16x16x32(va, bhi, acc[dt]);
       }
     }
     __syncthreads();  // sK / sV are rewritten by the next chunk

@@ -297,7 +297,10 @@ class FastDLLMV2SpeculativeGeneration:
                         region.copy_(torch.where(unmask, x_1, region))
                         n = int(unmask.sum())
                         self.last_commits.append(n)
-                        yield {"kind": kind, "committed": n}
+                        # the decision itself rides along (device tensors, no sync):
+                        # sampled tokens, maskable positions and the committed ones
+                        yield {"kind": kind, "committed": n, "tokens": x_1,
+                               "maskable": small_mask, "unmask": unmask}
 
     @torch.no_grad()
     def generate_with_draft_speculation(self, prompt: str = None, prompt_ids=None,

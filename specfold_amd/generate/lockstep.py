@@ -71,7 +71,6 @@ class LockstepDecoder:
         eng = g0._engine
         N = requests[0][0].shape[1]
         total = sum(b.shape[0] for b, _ in requests) * N      # real (unpadded) rows
-        bucket = g0.fold_bucket      # None: every (padded) row
         q_scale = getattr(g0.model_executor, "q_scale", None)
         q_scales = [q_scale(cache_length(c), N) if q_scale is not None else None
                     for _, c in requests]
@@ -92,6 +91,11 @@ class LockstepDecoder:
         try:
             for idx in chunks:
                 stats = StepStats()
+                # fold_bucket bounds one sequence's recomputed rows: a stacked step
+                # holds the sum of its sequences' bounds (each at most its rows)
+                bucket = None if g0.fold_bucket is None else sum(
+                    min(int(g0.fold_bucket), (self.pad_to or requests[i][0].shape[0]) * N)
+                    for i in idx)
                 out = eng.forward_batched([requests[i][0] for i in idx],
                                           [requests[i][1] for i in idx], delta=g0.delta,
                                           bucket=bucket, q_scales=[q_scales[i] for i in idx],

@@ -27,14 +27,13 @@ logger = logging.getLogger(__name__)
 
 
 def add_gumbel_noise(logits: torch.Tensor, temperature: float) -> torch.Tensor:
-    """Gumbel-max sampling noise in float64; identity at temperature 0
-    (modeling_nemotron_labs_diffusion.py:814-821)."""
+    """Scores whose argmax is a Gumbel-max sample at ``temperature``: exp(l) * E^-T
+    with E = -ln U, U ~ U(0, 1), all in float64; the logits themselves at
+    temperature 0 (the rule of modeling_nemotron_labs_diffusion.py:814-821)."""
     if temperature == 0:
         return logits
-    logits = logits.to(torch.float64)
-    noise = torch.rand_like(logits, dtype=torch.float64)
-    gumbel_noise = (-torch.log(noise)) ** temperature
-    return logits.exp() / gumbel_noise
+    u = torch.rand(logits.shape, dtype=torch.float64, device=logits.device)
+    return torch.exp(logits.double()) * torch.pow(-torch.log(u), -float(temperature))
 
 
 def get_num_transfer_tokens(mask_index: torch.Tensor, steps: int) -> torch.Tensor:
@@ -170,11 +169,13 @@ class NLDDiffusionGeneration:
             drafts.append({"state": draft, "node": node})
         return drafts
 
-    def _sample_token(self, last_logit: torch.Tensor) -> torch.Tensor:
-        if self.temperature > 0:
-            probs = torch.softmax(last_logit / self.temperature, dim=-1)
-            return torch.multinomial(probs, num_samples=1)
-        return torch.argmax(last_logit, dim=-1, keepdim=True)
+    def _next_ar_token(self, last_logit: torch.Tensor) -> torch.Tensor:
+        """Next token [B, 1] of the autoregressive fallback: the argmax at
+        temperature 0, else one draw from softmax(logits / T) (nld_generation.py:
+        321-326)."""
+        if self.temperature <= 0:
+            return last_logit.argmax(dim=-1, keepdim=True)
+        return torch.multinomial(torch.softmax(last_logit / self.temperature, dim=-1), 1)
 
     # -- the decode loop ----------------------------------------------------------------
     @torch.no_grad()
@@ -213,7 +214,7 @@ class NLDDiffusionGeneration:
             executor.set_diffusion_lm(True)
         next_token = None
         if self.causal_context:
-            next_token = self._sample_token(output.logits[:, -1, :])
+            next_token = self._next_ar_token(output.logits[:, -1, :])
         yield {"kind": "prefill", "committed": 0}
 
         steps_per_block = self.block_length
@@ -305,7 +306,7 @@ class NLDDiffusionGeneration:
             st["model_calls"] += 1
             if self.causal_context:
                 executor.set_diffusion_lm(True)
-                next_token = self._sample_token(output.logits[:, -1, :])
+                next_token = self._next_ar_token(output.logits[:, -1, :])
             yield {"kind": "commit", "committed": 0}
             if eos_id is not None and bool((x_accum[:, prompt_len:] == eos_id).any(dim=1).all()):
                 break

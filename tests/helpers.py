@@ -79,3 +79,10 @@ def src_from_mask(parent: List[Optional[int]], rec: torch.Tensor) -> torch.Tenso
                 c = parent[c] if parent[c] is not None else 0
             out[b, n] = c
     return out
+
+
+def plain_events(events) -> list:
+    """Decode-loop events with their tensor fields (the Fast-dLLM loop's decision
+    tensors) turned into lists, so that event streams compare with ==."""
+    return [{k: (v.tolist() if isinstance(v, torch.Tensor) else v) for k, v in e.items()}
+            for e in events]

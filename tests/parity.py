@@ -1,0 +1,263 @@
+"""Stage-by-stage comparison of one layer of the HIP verify step with the oracle.
+
+Two kinds of forcing:
+
+* layer-input forcing: the oracle runs the layer on the HIP path's own layer
+  input; every stage up to the attention residual ``hp`` is compared there.
+* stage forcing for the FFN: the HIP FFN kernels (post-attention RMSNorm of the
+  recomputed rows, gate/up + SiLU, down + scatter) run on the oracle's own
+  ``hp``, so the FFN output and ``h_out = hp + ffn`` are compared on identical
+  inputs.  This matters because the FFN amplifies any 1-ulp change of ``hp``:
+  a ~2% fraction of ``hp`` elements rounding the other way (fp32 summation
+  order in attention and o_proj — the oracle itself run on the GPU differs
+  from its CPU result this way) turns about half of the FFN outputs one ulp
+  off.  The layer-input-forced ``h_out`` is compared too, against both the
+  CPU oracle and the oracle run in torch on the same GPU, to the bound below.
+
+Tolerances (per quantity; the same everywhere they are used):
+  recompute mask, rows, count, src          bit-exact
+  q/k/v, hp, ffn, h_out (stage-forced)      |hip - ref| <= 2^-7 * (|ref| + 2 rms(ref row)
+                                            + the operands of a rounded sum) per
+                                            element (row_close: ~2 bf16 ulps of the
+                                            element, two of its row's RMS, one of the
+                                            operands of hp = x + attn, h = hp + ffn), and
+                                            the north star's max abs <= 2e-2 * max(1,
+                                            max|ref|), mean rel <= 1e-3
+  O (fp32), m, Z                            max |hip - ref| <= 2e-3 * max|ref|
+  h_out (layer-input forced)                max abs <= 2e-2 * max(1, max|ref|) and mean rel
+                                            <= H_OUT_MEAN_REL_MAX against the CPU oracle;
+                                            the oracle's own GPU-vs-CPU spread and HIP vs
+                                            the oracle on the GPU are reported beside it.
+
+Why the layer-input-forced h_out is further than 1e-3: the QKV GEMM's fp32
+summation order rounds ~1e-4 of q elements the other way (as the oracle's own
+GEMMs do between CPU and GPU); one flipped q element moves that head's attention
+output by ~4e-6 relative, enough to round ~1% of the o_proj inputs the other
+way, and the FFN spreads the resulting hp flips.  Given the oracle's own q, the
+attention output is within ~2e-7 of fp64 attention; given the oracle's own hp,
+the FFN output and h_out meet the north-star bound (the stage-forced rows).
+"""
+
+from __future__ import annotations
+
+import copy
+from typing import List, Optional
+
+import torch
+
+from oracle.folded_reference import (LayerTrace, delta_gate, folded_layer, gate_margin,
+                                     topo_order)
+from tests.helpers import err_stats, src_from_mask
+
+NS_MAX_ABS = 2e-2       # north star: hidden states and logits, max abs (x max(1, |ref|))
+NS_MEAN_REL = 1e-3      # north star: hidden states and logits, mean relative
+H_OUT_MEAN_REL_MAX = 4e-3   # layer-input-forced h_out, whatever the oracle's own spread
+
+
+def bf16_close(a, b, rel=2 ** -7, abs_=2 ** -7):
+    a = a.detach().float().cpu()
+    b = b.detach().float().cpu()
+    bad = (a - b).abs() > rel * b.abs() + abs_
+    return int(bad.sum()), err_stats(a, b)
+
+
+def row_close(a, b, *operands, rel=2 ** -7):
+    """Per element |a - b| <= rel * (|b| + 2 rms(b's row) + sum_i |operand_i|):
+    about 2 bf16 ulps of the element, plus two of its row's RMS (a GEMM output
+    that cancels to a small value moves by the rounding of its inputs, which is
+    absolute, at the scale of the row), plus one ulp of the largest operand of a
+    rounded sum (``operands``, elementwise: a sum that cancels moves by an
+    operand's ulp).  Returns (elements off, err_stats)."""
+    a = a.detach().float().cpu()
+    b = b.detach().float().cpu()
+    tol = b.abs() + 2 * b.pow(2).mean(-1, keepdim=True).sqrt()
+    for o in operands:
+        tol = tol + o.detach().float().cpu().abs().reshape(b.shape)
+    ratio = (a - b).abs() / (rel * tol).clamp_min(1e-30)
+    st = err_stats(a, b)
+    if ratio.numel():
+        k = int(ratio.flatten().argmax())
+        st["worst"] = dict(index=k, hip=float(a.flatten()[k]), ref=float(b.flatten()[k]),
+                           tol=float(rel * tol.flatten()[k]), ratio=float(ratio.flatten()[k]))
+    return int((ratio > 1).sum()), st
+
+
+def max_ulps(a: torch.Tensor, b: torch.Tensor, mag: Optional[torch.Tensor] = None) -> float:
+    """Largest |a - b| in units of the bf16 ulp 2^(floor(log2 m) - 7) of the
+    magnitude m = ``mag`` (per element; default |b|).  For a rounded sum such as
+    h_out = bf16(hp + ffn) pass the largest operand magnitude: where the sum
+    cancels, one ulp of an operand is many ulps of the result.  Magnitudes below
+    2^-8 of the largest are measured at that floor."""
+    a = a.detach().float().cpu()
+    b = b.detach().float().cpu()
+    m = b.abs() if mag is None else mag.detach().float().cpu().abs()
+    floor = max(float(m.max()) * 2.0 ** -8, 2.0 ** -126) if m.numel() else 1.0
+    ulp = torch.exp2(torch.floor(torch.log2(m.clamp_min(floor))) - 7)
+    d = (a - b).abs() / ulp
+    return float(d.max()) if d.numel() else 0.0
+
+
+def ns_ok(st: dict) -> bool:
+    """The north star's bound on hidden states / logits."""
+    return st["max_abs"] <= NS_MAX_ABS * max(1.0, st["ref_absmax"]) and \
+        st["mean_rel"] <= NS_MEAN_REL
+
+
+def oracle_layer(lyr, h_in: torch.Tensor, parent, counts, kv, cos_n, sin_n, delta: float,
+                 H: int, Hkv: int, q_scale: Optional[torch.Tensor] = None,
+                 device: str = "cpu") -> LayerTrace:
+    """The oracle's folded layer on ``device`` for layer inputs ``h_in``
+    [B1, N, D] (any device); the layer module ``lyr`` is copied there when it
+    lives elsewhere.  kv = (k, v) [1, Hkv, P, hd] or None; cos_n/sin_n [N, hd]
+    of the block positions.  The trace comes back on the CPU."""
+    dev = torch.device(device)
+    on_dev = next(lyr.parameters()).device == dev
+    lyr_d = lyr if on_dev else copy.deepcopy(lyr).to(dev)
+    h = h_in.detach().to(dev)
+    hs = [h[i:i + 1] for i in range(h.shape[0])]
+    lt = LayerTrace()
+    kv_d = None if kv is None else (kv[0].to(dev), kv[1].to(dev))
+    with torch.no_grad():
+        folded_layer(lyr_d, hs, parent, topo_order(counts), kv_d, cos_n.to(dev), sin_n.to(dev),
+                     float(delta), H, Hkv, trace=lt,
+                     q_scale=None if q_scale is None else q_scale.to(dev))
+    if not on_dev:
+        del lyr_d
+    return lt
+
+
+def gate_flips(h_in: torch.Tensor, rec_hip: torch.Tensor, parent, delta: float) -> List[tuple]:
+    """(branch, position, margin) of every position where the HIP recompute
+    mask differs from the oracle's gate on the same layer input h_in [B1, N, D]
+    (main branch: always recomputed)."""
+    h = h_in.detach().to("cpu")
+    rec = rec_hip.detach().to("cpu").bool()
+    out = []
+    B1, N = rec.shape
+    if not bool(rec[0].all()):
+        out += [(0, n, None) for n in range(N) if not bool(rec[0, n])]
+    for i in range(1, B1):
+        p = parent[i] if parent[i] is not None else 0
+        ref = delta_gate(h[i:i + 1], h[p:p + 1], delta)
+        bad = (ref != rec[i]).nonzero().flatten().tolist()
+        if bad:
+            marg = gate_margin(h[i:i + 1], h[p:p + 1], delta)
+            out += [(i, n, float(marg[n])) for n in bad]
+    return out
+
+
+def hip_ffn(eng, li: int, hp: torch.Tensor, rows: torch.Tensor) -> torch.Tensor:
+    """The HIP FFN of layer ``li`` for the rows ``rows`` of ``hp`` [BN, D] (the
+    verify step's kernels: post-attention RMSNorm of the recomputed rows, gate/up
+    + SiLU, down + scatter) -> ffn [BN, D] (rows not listed stay zero)."""
+    from specfold_amd import _lib
+    BN, D = hp.shape
+    dev = eng.device
+    R = int(rows.numel())
+    lyr = eng.layers[li]
+    hp_d = hp.to(dev, torch.bfloat16).contiguous()
+    rows_d = torch.full((BN,), BN, dtype=torch.int32, device=dev)
+    rows_d[:R] = rows.to(dev, torch.int32)
+    count = torch.tensor([R], dtype=torch.int32, device=dev)
+    zn = torch.zeros(BN, D, dtype=torch.bfloat16, device=dev)
+    act = torch.zeros(BN, eng.I, dtype=torch.bfloat16, device=dev)
+    ffn = torch.zeros(BN + 1, D, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(max(_lib.gemm_workspace_bytes(BN, D, eng.I), 256), dtype=torch.uint8,
+                     device=dev)
+    wg, wu, wd = eng._packed_mlp[li]
+    _lib.rows_rmsnorm(hp_d, rows_d, count, BN, lyr.post_attention_layernorm.weight, D, eng.eps, zn)
+    _lib.ffn_gate_up(zn, count, BN, wg, wu, D, eng.I, act)
+    _lib.ffn_down_scatter(act, count, BN, rows_d, wd, eng.I, D, ffn, ws)
+    return ffn[:BN]
+
+
+def compare_layer(li: int, lt: LayerTrace, ht: dict, parent, B1: int, N: int, H: int, Hkv: int,
+                  hd: int, D: int, eng=None, lt_gpu: Optional[LayerTrace] = None,
+                  verbose: bool = True) -> dict:
+    """Assert one HIP layer (``ht``, from FoldedVerifyEngine.forward(trace=...))
+    equals the oracle's (``lt``, run on the same layer input) to the tolerances
+    above.  ``eng`` enables the stage-forced FFN check; ``lt_gpu`` (the oracle
+    run in torch on the GPU on the same input) the same-device comparison of
+    h_out.  Prints every statistic before asserting; returns them."""
+    out, fails = {}, []
+    rec_ref = lt.rec
+    rec_hip = ht["rec"].cpu().view(B1, N).bool()
+    assert torch.equal(rec_hip, rec_ref), f"layer {li}: recompute mask differs"
+    cnt = int(ht["count"].item())
+    assert cnt == int(rec_ref.sum())
+    rows_ref = rec_ref.flatten().nonzero().flatten().to(torch.int32)
+    assert torch.equal(ht["rows"].cpu()[:cnt], rows_ref)
+    assert torch.all(ht["rows"].cpu()[cnt:] == B1 * N)
+    src_ref = src_from_mask(parent, rec_ref)
+    assert torch.equal(ht["src"].cpu().view(B1, N).long(), src_ref)
+
+    r = rows_ref.long()
+    bb, nn = r // N, r % N
+    q_hip = ht["q"].cpu().view(-1, H, hd)[r]
+    kv = ht["kv"].cpu().view(-1, 2, Hkv, hd)[r]
+    for nm, a, b in (("q", q_hip, lt.q[bb, :, nn, :]), ("k", kv[:, 0], lt.k[bb, :, nn, :]),
+                     ("v", kv[:, 1], lt.v[bb, :, nn, :])):
+        nbad, st = row_close(a, b)
+        out[nm] = st
+        if nbad:
+            fails.append(f"{nm}: {nbad} elements off")
+
+    st = err_stats(ht["o32"].cpu().view(B1, N, H, hd), lt.O.permute(0, 2, 1, 3))
+    out["O"] = st
+    if st["max_abs"] > 2e-3 * max(st["ref_absmax"], 1e-6):
+        fails.append("O")
+    for nm, a, b in (("m", ht["m"].cpu().view(B1, N, H), lt.m.permute(0, 2, 1)),
+                     ("Z", ht["z"].cpu().view(B1, N, H), lt.Z.permute(0, 2, 1))):
+        st = err_stats(a, b)
+        out[nm] = st
+        if st["max_abs"] > 2e-3 * max(st["ref_absmax"], 1.0):
+            fails.append(nm)
+
+    hp_hip = ht["hp"].cpu().view(B1, N, D)
+    # hp = bf16(x + attn_out): operands x and attn_out = hp - x
+    x_in = lt.h_in.float()
+    nbad, st = row_close(hp_hip, lt.hp, x_in, lt.hp.float() - x_in)
+    out["hp"] = st
+    if nbad or not ns_ok(st):
+        fails.append(f"hp: {nbad} elements off / north-star bound")
+
+    if eng is not None:
+        # FFN forced with the oracle's hp: ffn rows and h_out = hp + ffn[src]
+        BN = B1 * N
+        ffn = hip_ffn(eng, li, lt.hp.reshape(BN, D), r).cpu()
+        nbad, st = row_close(ffn[r], lt.ffn.reshape(BN, D)[r])
+        out["ffn|hp"] = st
+        if nbad or not ns_ok(st):
+            fails.append(f"ffn|hp: {nbad} elements off / north-star bound ({st})")
+        srow = (src_ref * N + torch.arange(N).view(1, N)).flatten()
+        hp_o = lt.hp.reshape(BN, D).float()
+        h2 = (hp_o + ffn[srow].float()).to(torch.bfloat16)
+        nbad, st = row_close(h2, lt.h_out.reshape(BN, D), hp_o, lt.ffn.reshape(BN, D)[srow])
+        out["h_out|hp"] = st
+        if nbad or not ns_ok(st):
+            fails.append(f"h_out|hp: {nbad} elements off / north-star bound")
+
+    h_hip = ht["h_out"].cpu().view(B1, N, D)
+    st = err_stats(h_hip, lt.h_out)
+    srow = (src_ref * N + torch.arange(N).view(1, N)).flatten()
+    ffn_res = lt.ffn.reshape(B1 * N, D)[srow].view(B1, N, D)
+    mag = torch.maximum(torch.maximum(lt.hp.float().abs(), ffn_res.float().abs()),
+                        lt.h_out.float().abs())
+    st["max_ulps"] = max_ulps(h_hip, lt.h_out, mag)
+    out["h_out"] = st
+    spread = None
+    if lt_gpu is not None:
+        spread = err_stats(lt_gpu.h_out, lt.h_out)
+        out["h_out oracle(gpu)-oracle(cpu)"] = spread
+        out["h_out hip-oracle(gpu)"] = err_stats(h_hip, lt_gpu.h_out)
+    if st["max_abs"] > NS_MAX_ABS * max(1.0, st["ref_absmax"]) or \
+            st["mean_rel"] > H_OUT_MEAN_REL_MAX:
+        fails.append("h_out (layer-input forced)")
+    if verbose:
+        print(f"layer {li}: count {cnt}", flush=True)
+        for k, v in out.items():
+            extra = f" ulps {v['max_ulps']:.2f}" if "max_ulps" in v else ""
+            print(f"    {k:32s} max {v['max_abs']:.3g} mean_rel {v['mean_rel']:.2e} "
+                  f"diff {v['frac_diff']:.4f} |ref| {v['ref_absmax']:.3g}{extra}", flush=True)
+    assert not fails, f"layer {li}: {fails}"
+    return out

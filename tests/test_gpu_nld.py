@@ -18,7 +18,8 @@ from specfold_amd.generate.nld_folded import SpecFoldHIPNLDGeneration
 from specfold_amd.generate.nld_generation import NLDDiffusionGeneration
 from specfold_amd.generate.nld_model_executor import NLDModelExecutor
 from tests.helpers import SHAPE_N4, SHAPE_N8, err_stats, make_nld_case, to_gpu_model
-from tests.test_gpu_engine_parity import bf16_close, check_end_to_end, check_layers, run_pair
+from tests.parity import bf16_close
+from tests.test_gpu_engine_parity import check_end_to_end, check_layers, run_pair
 
 pytestmark = pytest.mark.gpu
 
@@ -38,8 +39,8 @@ def test_nld_layers_teacher_forced(name, shape, seed, P, delta, omax):
     case = make_nld_case(shape, seed, P=P, delta=delta, omax=omax)
     qs = _q_scale(case, P, case.tokens.shape[1])
     assert (qs is not None) == (P + case.tokens.shape[1] > omax)
-    tr, _, trace, _ = run_pair(case, q_scale=qs)
-    check_layers(case, shape, tr, trace)
+    tr, _, trace, _, eng = run_pair(case, q_scale=qs)
+    check_layers(case, shape, tr, trace, eng, q_scale=qs)
 
 
 @pytest.mark.parametrize("name,shape,seed,P,delta,omax", CASES[:2])
