@@ -221,14 +221,15 @@ int sf_kv_append(const uint16_t* kv_buf, int row0, int n_tok, int Hkv, int hd, u
  * sequential read.  Packing is done once per model (the counterpart of the
  * reference's _pack_layer_weights, fastdllm_v2_folded.py:77-87).
  *
- * Workspace.  The weight is streamed once on bf16 MFMA with fp32 accumulation,
- * split stream-K over a fixed grid: tiles computed by several workgroups go
- * through fp32 partial slots in a caller workspace of
- * sf_gemm_workspace_bytes(M or bucket, N, K) bytes (sf_qkv_workspace_bytes for
+ * Workspace.  The weight is streamed once on bf16 MFMA with fp32 accumulation
+ * for every row (up to 256 rows per pass), split stream-K over one workgroup per
+ * CU: tiles computed by several workgroups go through fp32 partial slots in a
+ * caller workspace of sf_gemm_workspace_bytes(M or bucket, N, K) bytes
+ * (sf_ffn_gate_up_workspace_bytes for sf_ffn_gate_up, sf_qkv_workspace_bytes for
  * sf_qkv_rope), summed in a fixed order by a fix-up kernel (deterministic).
  * Calls sharing a workspace must not overlap.
  *
- * sf_pack_weight        out = packed(w), w row-major [N, K]; N % 16 == 0, K % 128 == 0
+ * sf_pack_weight        out = packed(w), w row-major [N, K]; N % 16 == 0, K % 64 == 0
  * sf_o_proj_residual    hp[r] = bf16(x[r] + bf16(o_bf[r] . Wo^T)), r < M (all rows)
  * sf_residual_post_norm hp[r] = bf16(x[r] + y[r]) for r < BN, and for recomputed rows
  *                       zn[slot[r]] = bf16(w * bf16(hp[r] * rstd)) (y = a bf16 o_proj
@@ -239,9 +240,11 @@ int sf_kv_append(const uint16_t* kv_buf, int row0, int n_tok, int Hkv, int hd, u
  * sf_residual_gather_add out[r] = bf16(hp[r] + ffn[src[r]*N + r%N]), r < B1*N
  *                       (folded rows take their nearest recomputing ancestor's FFN)
  * sf_lm_head            logits[m] = bf16(x[m] . Wlm^T), m < M
- * Limits: K % 128 == 0, N % 64 == 0 (lm_head: V % 128), M/bucket <= 1024, D <= 8192.
+ * Limits: K % 64 == 0, N % 128 == 0 (gate/up: I % 128, lm_head: V % 128), M/bucket
+ * <= 1024, D <= 8192.
  */
 size_t sf_gemm_workspace_bytes(int mcap, int N, int K);
+size_t sf_ffn_gate_up_workspace_bytes(int bucket, int D, int I);
 int sf_pack_weight(const uint16_t* w, int N, int K, uint16_t* out, void* stream);
 int sf_o_proj_residual(const uint16_t* o_bf, const uint16_t* x, const uint16_t* wo, int M, int K,
                        int N, uint16_t* hp, void* workspace, size_t workspace_bytes, void* stream);
@@ -251,7 +254,8 @@ int sf_residual_post_norm(const uint16_t* x, const uint16_t* y, const int32_t* s
 int sf_rows_rmsnorm(const uint16_t* x, const int32_t* rows, const int32_t* count, int bucket,
                     const uint16_t* w, int D, float eps, uint16_t* out, void* stream);
 int sf_ffn_gate_up(const uint16_t* zn, const int32_t* count, int bucket, const uint16_t* wg,
-                   const uint16_t* wu, int D, int I, uint16_t* act, void* stream);
+                   const uint16_t* wu, int D, int I, uint16_t* act, void* workspace,
+                   size_t workspace_bytes, void* stream);
 int sf_ffn_down_scatter(const uint16_t* act, const int32_t* count, int bucket, const int32_t* rows,
                         const uint16_t* wd, int I, int D, uint16_t* ffn, void* workspace,
                         size_t workspace_bytes, void* stream);

@@ -51,11 +51,12 @@ SIGNATURES = {
                               _vp, _vp, _vp, _vp, _vp]),
     "sf_kv_append": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp, _i, _ll, _ll, _i, _vp]),
     "sf_gemm_workspace_bytes": (_sz, [_i, _i, _i]),
+    "sf_ffn_gate_up_workspace_bytes": (_sz, [_i, _i, _i]),
     "sf_pack_weight": (_i, [_vp, _i, _i, _vp, _vp]),
     "sf_o_proj_residual": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _vp, _sz, _vp]),
     "sf_residual_post_norm": (_i, [_vp, _vp, _vp, _i, _i, _vp, _f, _vp, _vp, _vp]),
     "sf_rows_rmsnorm": (_i, [_vp, _vp, _vp, _i, _vp, _i, _f, _vp, _vp]),
-    "sf_ffn_gate_up": (_i, [_vp, _vp, _i, _vp, _vp, _i, _i, _vp, _vp]),
+    "sf_ffn_gate_up": (_i, [_vp, _vp, _i, _vp, _vp, _i, _i, _vp, _vp, _sz, _vp]),
     "sf_ffn_down_scatter": (_i, [_vp, _vp, _i, _vp, _vp, _i, _i, _vp, _vp, _sz, _vp]),
     "sf_residual_gather_add": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _vp]),
     "sf_lm_head": (_i, [_vp, _i, _vp, _i, _i, _vp, _vp]),
@@ -389,14 +390,21 @@ def rows_rmsnorm(x, rows, count, bucket, w, D, eps, out, stream=None) -> None:
     _check(st, "sf_rows_rmsnorm")
 
 
-def ffn_gate_up(zn, count, bucket, wg, wu, D, I, act, stream=None) -> None:
+def gate_up_workspace_bytes(bucket: int, D: int, I: int) -> int:
+    """Bytes of the gate/up GEMM's partial-slot workspace (0 for invalid shapes)."""
+    return int(load().sf_ffn_gate_up_workspace_bytes(bucket, D, I))
+
+
+def ffn_gate_up(zn, count, bucket, wg, wu, D, I, act, workspace, stream=None) -> None:
     _need(zn, "zn", torch.bfloat16, min_numel=bucket * D)
     _need(count, "count", torch.int32, min_numel=1, align=4)
     _need(wg, "wg", torch.bfloat16, numel=I * D)
     _need(wu, "wu", torch.bfloat16, numel=I * D)
     _need(act, "act", torch.bfloat16, min_numel=bucket * I)
+    _need(workspace, "workspace", torch.uint8, min_numel=gate_up_workspace_bytes(bucket, D, I),
+          align=256)
     st = load().sf_ffn_gate_up(_ptr(zn), _ptr(count), bucket, _ptr(wg), _ptr(wu), D, I, _ptr(act),
-                               _stream(stream))
+                               _ptr(workspace), workspace.numel(), _stream(stream))
     _check(st, "sf_ffn_gate_up")
 
 

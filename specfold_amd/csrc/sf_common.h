@@ -72,6 +72,53 @@ SF_DEV sf_f32x4 sf_mfma16x16x32(const sf_bf16x8 a, const sf_bf16x8 b, sf_f32x4 c
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+// ---- direct global -> LDS loads (gfx950 global_load_lds_dwordx4) -------------------
+// Every lane copies 16 bytes from its own global address `src` to LDS at
+// lds_base + 16 * lane (lds_base: wave-uniform, 16-byte aligned).  The copy counts
+// in the issuing wave's vmcnt like any load; the data may be read (by any wave)
+// after that count has come down past it and a workgroup barrier.
+typedef __attribute__((address_space(3))) void sf_lds_void;
+SF_DEV void sf_lds_dma16(const void* src, void* lds_base) {
+  __builtin_amdgcn_global_load_lds(const_cast<void*>(src), (sf_lds_void*)lds_base, 16, 0, 0);
+}
+
+// Wait until at most N vector-memory loads of this wave are outstanding (they
+// complete in issue order) and all of its LDS accesses have completed, then a
+// workgroup barrier: after it, every wave's loads older than its last N are in
+// LDS / registers and no wave still reads LDS it read before the barrier.  No
+// memory fence is implied; the signal fences keep the compiler from moving
+// memory accesses across the pair.
+template <int N>
+SF_DEV void sf_wait_vm_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// LDS fragment reads the compiler does not track: 16 bytes at byte address
+// `addr` + OFF of LDS into a register, no wait; sf_lds_reads_done makes the values
+// usable (s_waitcnt lgkmcnt(0), with every value passed through it so that no use
+// is scheduled above the wait).  Used where the compiler would otherwise wait for
+// every direct global -> LDS copy in flight before any LDS read.
+typedef uint32_t sf_lds_off;  // an LDS byte address
+template <int OFF>
+SF_DEV sf_u32x4 sf_lds_read16(sf_lds_off addr) {
+  sf_u32x4 v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+  return v;
+}
+template <int N>
+SF_DEV void sf_lds_reads_done(sf_u32x4 (&v)[N]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+v"(v[i]));
+}
+SF_DEV sf_lds_off sf_lds_addr(const void* p) {
+  return (sf_lds_off)(uintptr_t)(const sf_lds_void*)p;
+}
+
 // Launch-error check shared by every entry point.
 static inline int sf_launch_status() {
   hipError_t e = hipGetLastError();

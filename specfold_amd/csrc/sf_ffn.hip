@@ -150,7 +150,8 @@ __global__ __launch_bounds__(256) void residual_gather_add_kernel(
 // Fix-up of the FFN down GEMM: tiles computed by several stream-K workgroups are
 // summed from their partial slots in slot order and scattered as bf16 rows
 // (tiles of a single workgroup were written by the GEMM itself).  One workgroup
-// per 64-column tile.
+// per TW-column tile.
+template <int TW>
 __global__ __launch_bounds__(256) void down_fixup_kernel(const float* __restrict__ part, Plan plan,
                                                          int mcap, const int32_t* __restrict__ rows,
                                                          const int32_t* __restrict__ count_p, int N,
@@ -161,14 +162,45 @@ __global__ __launch_bounds__(256) void down_fixup_kernel(const float* __restrict
   if (nsl == 1) return;
   const int M = min(*count_p, mcap);
   const size_t stride = (size_t)mcap * N;
-  for (int e = threadIdx.x; e < M * 16; e += 256) {
-    const int m = e >> 4, c = t * 64 + (e & 15) * 4;
+  for (int e = threadIdx.x; e < M * (TW / 4); e += 256) {
+    const int m = e / (TW / 4), c = t * TW + (e % (TW / 4)) * 4;
     const int row = rows[m];
     const sf_f32x4 y = sum_slots<sf_f32x4>(part + (size_t)m * N + c, stride, nsl);
     sf_u32x2 o;
     o[0] = sf_pack2(y[0], y[1]);
     o[1] = sf_pack2(y[2], y[3]);
     *reinterpret_cast<sf_u32x2*>(out + (size_t)row * N + c) = o;
+  }
+}
+
+// Fix-up of the gate/up GEMM: a 128-column tile computed by several workgroups has
+// its gate and up sums in partial slot rows of 2I columns (gate, then up); they
+// are summed in slot order and the SiLU*mul epilogue applied, with the same three
+// bf16 roundings as the GEMM's own epilogue.  One workgroup per tile.
+__global__ __launch_bounds__(256) void silu_fixup_kernel(const float* __restrict__ part, Plan plan,
+                                                         int mcap, const int32_t* __restrict__ count_p,
+                                                         int I, uint16_t* __restrict__ act) {
+  const int t = blockIdx.x;
+  const int first = tile_first(t, plan);
+  const int nsl = tile_last(t, plan) - first + 1;
+  if (nsl == 1) return;
+  const int M = min(*count_p, mcap);
+  const size_t stride = (size_t)mcap * 2 * I;
+  for (int e = threadIdx.x; e < M * 32; e += 256) {
+    const int m = e >> 5, c = t * 128 + (e & 31) * 4;
+    const float* p = part + (size_t)m * 2 * I + c;
+    const sf_f32x4 g = sum_slots<sf_f32x4>(p, stride, nsl);
+    const sf_f32x4 u = sum_slots<sf_f32x4>(p + I, stride, nsl);
+    float r[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float gt = sf_rbf(g[i]);
+      r[i] = sf_rbf(gt / (1.0f + expf(-gt))) * sf_rbf(u[i]);
+    }
+    sf_u32x2 o;
+    o[0] = sf_pack2(r[0], r[1]);
+    o[1] = sf_pack2(r[2], r[3]);
+    *reinterpret_cast<sf_u32x2*>(act + (size_t)m * I + c) = o;
   }
 }
 
@@ -195,8 +227,14 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 }  // namespace
 
 extern "C" size_t sf_gemm_workspace_bytes(int mcap, int N, int K) {
-  if (mcap < 1 || N < 64 || N % 64 || K < kKC || K % kKC) return 0;
-  const size_t b = part_bytes(make_plan(N / 64, K / kKC), mcap, N);
+  if (mcap < 1 || N < 128 || N % 128 || K < kKC || K % kKC) return 0;
+  const size_t b = part_bytes(make_plan(N / 128, K / kKC), mcap, N);
+  return b < 256 ? 256 : b;
+}
+
+extern "C" size_t sf_ffn_gate_up_workspace_bytes(int bucket, int D, int I) {
+  if (bucket < 1 || I < 128 || I % 128 || D < kKC || D % kKC) return 0;
+  const size_t b = part_bytes(make_plan(I / 128, D / kKC), bucket, 2 * I);
   return b < 256 ? 256 : b;
 }
 
@@ -215,14 +253,14 @@ extern "C" int sf_o_proj_residual(const uint16_t* o_bf, const uint16_t* x, const
                                   int M, int K, int N, uint16_t* hp, void* workspace,
                                   size_t workspace_bytes, void* stream) {
   if (!o_bf || !x || !wo || !hp || !workspace) return SF_ERR_ARG;
-  if (M < 1 || M > 1024 || K % kKC || N % 64 || !aligned16(o_bf) || !aligned16(wo))
+  if (M < 1 || M > 1024 || K % kKC || N % 128 || !aligned16(o_bf) || !aligned16(wo))
     return SF_ERR_SHAPE;
   if (workspace_bytes < sf_gemm_workspace_bytes(M, N, K)) return SF_ERR_WORKSPACE;
   Epi ep{};
   ep.out = hp;
   ep.ldo = N;
   ep.res = x;
-  launch_sk<1, kResid>(make_plan_whole(N / 64, K / kKC), o_bf, nullptr, K, nullptr, M, M, wo,
+  launch_sk<1, kResid>(make_plan_whole(N / 128, K / kKC), o_bf, nullptr, K, nullptr, M, M, wo,
                        nullptr, K, N, nullptr, ep, reinterpret_cast<hipStream_t>(stream));
   return sf_launch_status();
 }
@@ -269,15 +307,21 @@ extern "C" int sf_residual_post_norm(const uint16_t* x, const uint16_t* y, const
 
 extern "C" int sf_ffn_gate_up(const uint16_t* zn, const int32_t* count, int bucket,
                               const uint16_t* wg, const uint16_t* wu, int D, int I,
-                              uint16_t* act, void* stream) {
-  if (!zn || !count || !wg || !wu || !act) return SF_ERR_ARG;
-  if (bucket < 1 || bucket > 1024 || D % kKC || I % 64) return SF_ERR_SHAPE;
+                              uint16_t* act, void* workspace, size_t workspace_bytes,
+                              void* stream) {
+  if (!zn || !count || !wg || !wu || !act || !workspace) return SF_ERR_ARG;
+  if (bucket < 1 || bucket > 1024 || D % kKC || I % 128) return SF_ERR_SHAPE;
+  if (workspace_bytes < sf_ffn_gate_up_workspace_bytes(bucket, D, I)) return SF_ERR_WORKSPACE;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const Plan p = make_plan(I / 128, D / kKC);
+  float* part = reinterpret_cast<float*>(workspace);
   Epi ep{};
   ep.out = act;
   ep.ldo = I;
-  // one workgroup per 64-column tile (whole K): SiLU*mul straight from registers
-  launch_sk<2, kSilu>(make_plan_whole(I / 64, D / kKC), zn, nullptr, D, count, 0, bucket, wg, wu,
-                      D, I, nullptr, ep, reinterpret_cast<hipStream_t>(stream));
+  // whole tiles get SiLU*mul straight from registers, shared tiles in the fix-up
+  launch_sk<2, kSilu>(p, zn, nullptr, D, count, 0, bucket, wg, wu, D, I, part, ep, st);
+  hipLaunchKernelGGL(silu_fixup_kernel, dim3(p.T), dim3(256), 0, st, part, p, bucket, count, I,
+                     act);
   return sf_launch_status();
 }
 
@@ -286,18 +330,18 @@ extern "C" int sf_ffn_down_scatter(const uint16_t* act, const int32_t* count, in
                                    uint16_t* ffn, void* workspace, size_t workspace_bytes,
                                    void* stream) {
   if (!act || !count || !rows || !wd || !ffn || !workspace) return SF_ERR_ARG;
-  if (bucket < 1 || bucket > 1024 || I % kKC || D % 64) return SF_ERR_SHAPE;
+  if (bucket < 1 || bucket > 1024 || I % kKC || D % 128) return SF_ERR_SHAPE;
   if (workspace_bytes < sf_gemm_workspace_bytes(bucket, D, I)) return SF_ERR_WORKSPACE;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const Plan p = make_plan(D / 64, I / kKC);
+  const Plan p = make_plan(D / 128, I / kKC);
   float* part = reinterpret_cast<float*>(workspace);
   Epi ep{};
   ep.rows = rows;
   ep.out = ffn;
   ep.ldo = D;
   launch_sk<1, kScatter>(p, act, nullptr, I, count, 0, bucket, wd, nullptr, I, D, part, ep, st);
-  hipLaunchKernelGGL(down_fixup_kernel, dim3(p.T), dim3(256), 0, st, part, p, bucket, rows, count,
-                     D, ffn);
+  hipLaunchKernelGGL(down_fixup_kernel<128>, dim3(p.T), dim3(256), 0, st, part, p, bucket, rows,
+                     count, D, ffn);
   return sf_launch_status();
 }
 
@@ -319,7 +363,7 @@ extern "C" int sf_lm_head(const uint16_t* x, int M, const uint16_t* w, int D, in
   Epi ep{};
   ep.out = logits;
   ep.ldo = V;
-  launch_sk<2, kPlain>(make_plan_whole(V / 128, D / kKC), x, nullptr, D, nullptr, M, M, w,
+  launch_sk<1, kPlain>(make_plan_whole(V / 128, D / kKC), x, nullptr, D, nullptr, M, M, w,
                        nullptr, D, V, nullptr, ep, reinterpret_cast<hipStream_t>(stream));
   return sf_launch_status();
 }

@@ -1,14 +1,16 @@
 // Weight-streaming GEMM core for skinny row blocks:  C[m, n] = sum_k A[arow(m), k] * W[n, k]
 //
 // Shapes on this path: M = recomputed rows (<= 256, often 30-120) or all BN rows,
-// N and K = 1.5k-38k; W (bf16, [N, K], packed fragment-major) is the big operand
-// and is read once from HBM.  A workgroup is 4 waves; wave w owns WN column tiles
-// of 16; a block of up to 64 rows of A is staged through LDS in 128-wide K stages
-// (double buffered) and shared by the 4 waves; every wave streams its own weight
-// tiles straight into VGPRs.  Work is split stream-K: a fixed grid of workgroups
-// per m block, each taking an equal share of the (tile, K stage) units; tiles
-// shared by several workgroups are summed by a fix-up kernel.
-// MFMA: v_mfma_f32_16x16x32_bf16, fp32 accumulation.
+// N and K = 1.5k-152k; W (bf16, [N, K], packed fragment-major) is the big operand
+// and is read once from HBM.  One workgroup of 8 waves per CU; wave w owns WN
+// column tiles of 16 (column group w), so the workgroup covers 128*WN columns.
+// ALL rows of A (up to MB = 64 or 128 per pass: one pass over the weights for
+// every row up to 128) are staged through a ring of LDS buffers, 64 K at a time,
+// and shared by the 8 waves; the weights go to LDS too, each wave's own
+// fragments.  Work is split stream-K: a grid of one workgroup per CU, each taking
+// an equal share of the (tile, K stage) units; tiles shared by several workgroups
+// are summed by a fix-up
+// kernel.  MFMA: v_mfma_f32_16x16x32_bf16, fp32 accumulation.
 //
 // Operand layout of v_mfma_f32_16x16x32_bf16 (64 lanes): A 16x32 — lane l holds
 // A[l%16][8*(l/16) .. +8]; B 32x16 — lane l holds B[8*(l/16) .. +8][l%16];
@@ -20,123 +22,183 @@
 
 namespace sfg {
 
-#ifndef SFG_MB
-#define SFG_MB 64
+constexpr int kKC = 64;       // K per stage: two MFMA K chunks, one per wave of a pair
+constexpr int kThreads = 512; // 8 waves
+constexpr int kLdsBudget = 152 * 1024;
+#ifndef SFG_RING_MAX
+#define SFG_RING_MAX 6
 #endif
-constexpr int kMB = SFG_MB;       // rows of A per workgroup (default of every kernel)
-constexpr int kKC = 128;          // K per LDS stage
-constexpr int kLdsStride = 136;   // bf16 per LDS row (128 + 8 pad: 272 B, spreads banks)
-constexpr int kMT = kMB / 16;     // max m tiles per workgroup
 
-// Shared memory of one workgroup of MB rows: two A stages + the row index table.
-template <int MB>
-struct SmemT {
-  uint16_t a[2][MB * kLdsStride];
-  int rows[MB];
+// One ring stage of a workgroup of up to MB rows and WN weight tiles per wave:
+// the two 32-K chunks of the MB/16 A m tiles (1 KB per (chunk, m tile)), then
+// every wave's WN weight fragments of its chunk (1 KB each, in lane order: the
+// packed layout).  Sizes in 16-byte words.  The ring holds as many stages as fit
+// kLdsBudget, at most 8.
+template <int MB, int WN>
+struct Stage {
+  static constexpr int kA = 2 * (MB / 16) * 64;   // words of A per stage
+  static constexpr int kW = 8 * WN * 2 * 64;      // words of weights per stage
+  static constexpr int kWords = kA + kW;
+  static constexpr int kRing =
+      kLdsBudget / (kWords * 16) < SFG_RING_MAX ? kLdsBudget / (kWords * 16) : SFG_RING_MAX;
 };
-using Smem = SmemT<kMB>;
 
-// Prefetch depth: a ring of SFG_RING register slots per wave (A rows and weights
-// of one K stage each), so every wave keeps SFG_RING-1 stages of loads
-// (WN x 4 KB of weights each) outstanding.
-#ifndef SFG_RING
-#define SFG_RING 2
-#endif
-#ifndef SFG_WAVES
-#define SFG_WAVES 2   // waves per SIMD the register allocation targets
-#endif
+// The fragments are read from the ring by sf_lds_read16, which the compiler does
+// not track, so it adds no wait for the copies in flight (the waits are
+// sf_wait_vm_barrier's and sf_lds_reads_done's).  A rows are 64 bytes per
+// tile row, whose four 16-byte units are XOR-swizzled — unit u of tile row r
+// sits at position u ^ a_swz(r), so the 16 lanes of a fragment read that share
+// a unit hit distinct banks.
+template <int MB, int WN>
+struct Ring {
+  sf_u32x4* slot[8];
+};
 
-// Weight layout (fragment-major, "packed"; weight_lane_ptr, kKsStride and
-// kStageElems in sf_index.h): every wave's weight stream is a sequential read.
-// sf_pack_weight produces it from row-major W.
+// Rows handled by one workgroup of a launch whose row count is at most mcap.
+inline int row_block(int mcap) { return mcap <= 64 ? 64 : 128; }
 
-// Main loop over stages [s0, s1) of K for NMT m tiles of 16 rows (NMT is a
-// template parameter so the MFMA loop is straight-line).  `wrow[t]` is this
-// lane's weight stream for column tile t; `acc[mt][t]` accumulates rows mt*16..,
-// column tile t.
+// The A fragments (NMT m tiles, 1 KB apart) and weight fragments (WN tiles, 2 KB
+// apart) of K chunk C of a stage, read from LDS without waiting (sf_lds_read16
+// with compile-time offsets).
+template <int NMT, int WN, int I = 0>
+SF_DEV void lds_fragments(sf_u32x4 (&f)[NMT + WN], sf_lds_off a_addr, sf_lds_off w_addr) {
+  if constexpr (I < NMT) {
+    f[I] = sf_lds_read16<I * 1024>(a_addr);
+    lds_fragments<NMT, WN, I + 1>(f, a_addr, w_addr);
+  } else if constexpr (I < NMT + WN) {
+    f[I] = sf_lds_read16<(I - NMT) * 2048>(w_addr);
+    lds_fragments<NMT, WN, I + 1>(f, a_addr, w_addr);
+  }
+}
+
+// Main loop over stages [s0, s1) of K (64 each: two 32-wide MFMA chunks) for NMT
+// m tiles of 16 rows.  `wsrc[t]` is this lane's weight stream for column tile t;
+// `acc[mt][t]` accumulates rows mt*16.., column tile t; `rows` the workgroup's
+// row table in LDS.
 //
-// Stage s's A rows and weights are issued together, SFG_RING-1 stages ahead, into
-// a register ring of SFG_RING slots (A too, not only W).  A wave's vector-memory
-// loads complete in issue order, so waiting for stage s then waits for nothing
-// younger: the SFG_RING-1 later stages stay in flight.  A(s) goes to LDS (double
-// buffered) only at the start of iteration s, followed by the one barrier of the
-// stage.  Loads past the last stage re-read it and rows past mrows re-read the
-// last row (clamped, no branches), which keeps the wait counts exact.
-template <int WN, int NMT, int MB = kMB>
-SF_DEV void mainloop(const uint16_t* __restrict__ A, int lda, int mrows,
-                     const uint16_t* const (&wrow)[WN], int s0, int s1, SmemT<MB>& sm,
+// Every operand goes to LDS by direct copies (global_load_lds, 16 bytes per lane,
+// 1 KB per instruction): per stage the 2*NMT A tile copies (chunk, m tile) dealt
+// out over the 8 waves (copy q to wave q % 8; a wave with fewer real copies
+// repeats the last one — the same bytes to the same place — so every wave issues
+// DPW per stage), and each wave's own 2*WN weight fragments (two chunks per
+// tile).  Stage s + R - 1 is issued while stage s is computed; a wave's loads
+// complete in issue order, so waiting for stage s (vmcnt <= (R - 2) * copies per
+// stage) leaves the younger stages in flight.  Stage s + R - 1 goes into the slot
+// of stage s - 1 after the barrier of stage s, when no wave reads that slot any
+// more.  Copies past the last stage re-read it (clamped) and rows past mrows
+// re-read the last row, which keeps every count exact; the loop drains them at
+// its end.
+template <int WN, int NMT, int MB>
+SF_DEV void mainloop(const uint16_t* __restrict__ A, int lda, int mrows, const int* rows,
+                     const uint16_t* const (&wsrc)[WN], int s0, int s1, const Ring<MB, WN>& rg,
                      sf_f32x4 (&acc)[MB / 16][WN]) {
-  constexpr int R = SFG_RING;
-  static_assert(R % 2 == 0, "ring depth must be even (LDS double buffer parity)");
+  using St = Stage<MB, WN>;
+  constexpr int R = St::kRing;
+  static_assert(R >= 3, "the ring needs three stages");
+  constexpr int kMT = MB / 16;
+  constexpr int DPW = (2 * NMT + 7) / 8;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int kq = (lane >> 4) * 8;
-  const int a_seg = tid & 15;      // 16 x 16 B per 128-wide row stage
-  const int a_row0 = tid >> 4;     // 16 rows per pass, NMT passes
+  const int wv = tid >> 6;
   const int slast = s1 - 1;
-  const uint16_t* arow[NMT];
+  // this lane's part of each A tile copy: tile row lane/4, stored unit lane%4
+  // holding A unit a_copy_unit(lane) of the copy's 32-K chunk
+  const uint16_t* asrc[DPW];
+  int adst[DPW];   // first word of the copy in a slot
 #pragma unroll
-  for (int p = 0; p < NMT; ++p)
-    arow[p] = A + (size_t)sm.rows[min(a_row0 + p * 16, mrows - 1)] * lda + a_seg * 8;
-  sf_u32x4 areg[R][NMT];
-  sf_u32x4 w[R][WN][4];
-
-  auto issue = [&](int s, int slot) {
-    const int sc = min(s, slast);
+  for (int j = 0; j < DPW; ++j) {
+    const int q = a_copy(wv, j, NMT);
+    const int ch = q / NMT, mt = q - ch * NMT;
+    const int r = sf_imin(mt * 16 + (lane >> 2), mrows - 1);
+    asrc[j] = A + (size_t)rows[r] * lda + ch * 32 + a_copy_unit(lane) * 8;
+    adst[j] = (ch * kMT + mt) * 64;
+  }
+  const int wdst = St::kA + wv * WN * 128;   // this wave's weights: [tile][chunk][1 KB]
+  auto issue = [&](int s, sf_u32x4* slot) {
+    const int sc = sf_imin(s, slast);
 #pragma unroll
-    for (int p = 0; p < NMT; ++p)
-      areg[slot][p] = *reinterpret_cast<const sf_u32x4*>(arow[p] + sc * kKC);
+    for (int j = 0; j < DPW; ++j) sf_lds_dma16(asrc[j] + sc * kKC, slot + adst[j]);
 #pragma unroll
     for (int t = 0; t < WN; ++t)
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-        w[slot][t][ks] =
-            *reinterpret_cast<const sf_u32x4*>(wrow[t] + (size_t)sc * kStageElems + ks * kKsStride);
+      for (int c = 0; c < 2; ++c)
+        sf_lds_dma16(wsrc[t] + (size_t)weight_chunk(sc, c) * kKsStride,
+                     slot + wdst + (t * 2 + c) * 64);
   };
-
 #pragma unroll
-  for (int j = 0; j < R - 1; ++j) issue(s0 + j, j);
+  for (int j = 0; j < R - 1; ++j) issue(s0 + j, rg.slot[j]);
 
+  // this lane's A fragment in chunk c of a stage: word a_read_word(lane) of tile
+  // (c, mt); its weight fragment: word `lane` of block (tile t, chunk c)
+  const sf_lds_off a_byte = (sf_lds_off)a_read_word(lane) * 16;
+  const sf_lds_off w_byte = (sf_lds_off)(wdst + lane) * 16;
 #pragma unroll 1
   for (int sb = s0; sb < s1; sb += R) {
 #pragma unroll
     for (int j = 0; j < R; ++j) {
-      const int s = sb + j;
-      if (s >= s1) break;
-      issue(s + R - 1, (j + R - 1) % R);
+      if (sb + j < s1) {  // wave-uniform; no break, so the ring indices stay static
+        sf_wait_vm_barrier<(R - 2) * (DPW + 2 * WN)>();
+        issue(sb + j + R - 1, rg.slot[(j + R - 1) % R]);
+        const sf_lds_off base = sf_lds_addr(rg.slot[j]);
 #pragma unroll
-      for (int p = 0; p < NMT; ++p)
-        *reinterpret_cast<sf_u32x4*>(&sm.a[j & 1][(a_row0 + p * 16) * kLdsStride + a_seg * 8]) =
-            areg[j][p];
-      __syncthreads();
-      const uint16_t* abase = &sm.a[j & 1][(lane & 15) * kLdsStride + kq];
+        for (int c = 0; c < 2; ++c) {
+          sf_u32x4 f[NMT + WN];
+          lds_fragments<NMT, WN>(f, base + a_byte + c * kMT * 1024, base + w_byte + c * 1024);
+          sf_lds_reads_done(f);
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
+          for (int mt = 0; mt < NMT; ++mt)
 #pragma unroll
-        for (int mt = 0; mt < NMT; ++mt) {
-          const sf_bf16x8 af = sf_as_bf16x8(
-              *reinterpret_cast<const sf_u32x4*>(abase + mt * 16 * kLdsStride + ks * 32));
-#pragma unroll
-          for (int t = 0; t < WN; ++t)
-            acc[mt][t] = sf_mfma16x16x32(af, sf_as_bf16x8(w[j][t][ks]), acc[mt][t]);
+            for (int t = 0; t < WN; ++t)
+              acc[mt][t] =
+                  sf_mfma16x16x32(sf_as_bf16x8(f[mt]), sf_as_bf16x8(f[NMT + t]), acc[mt][t]);
         }
       }
+    }
+  }
+  // drain the clamped re-issues past the last stage before the LDS is reused
+  sf_wait_vm_barrier<0>();
+}
+
+// The finished piece goes to LDS as an fp32 tile [MB][TW] (after the main loop's
+// drain, in the ring's memory).  Column of (wave w, tile t, lane): 16*(WN*w + t)
+// + lane%16; for kSilu (TW = 256) the gate tile at w*16 + lane%16 and the up tile
+// at 128 + w*16 + lane%16.
+template <int WN, int MB, bool SILU>
+struct TileLds {
+  static constexpr int kTW = SILU ? 256 : 128 * WN;   // columns of a tile in LDS
+  static constexpr int kFloats = MB * kTW;
+};
+template <int WN, int MB, bool SILU>
+SF_DEV void tile_to_lds(float* x, const sf_f32x4 (&acc)[MB / 16][WN], int nmt) {
+  constexpr int kMT = MB / 16;
+  constexpr int kTW = TileLds<WN, MB, SILU>::kTW;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = tid >> 6;
+#pragma unroll
+  for (int mt = 0; mt < kMT; ++mt) {
+    if (mt >= nmt) continue;
+#pragma unroll
+    for (int t = 0; t < WN; ++t) {
+      const int c = SILU ? t * 128 + wv * 16 + (lane & 15) : 16 * (WN * wv + t) + (lane & 15);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[(mt * 16 + (lane >> 4) * 4 + i) * kTW + c] = acc[mt][t][i];
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-// Stream-K schedule.  The output columns are cut into T tiles of TW columns and K
-// into S stages of 128; the T*S (tile, stage) units are dealt out in tile-major
-// order, U consecutive units per workgroup, so every workgroup streams the same
-// number of weight bytes whatever T is (a fixed tile-per-workgroup grid leaves
-// some CUs with twice the work of others).  A workgroup's range may end one tile
-// and start the next.  A tile computed by one workgroup alone gets its epilogue
-// straight from registers; the pieces of a tile shared by several workgroups go
-// to fp32 partial slots (slot j = g - first(t)) that a fix-up kernel sums in slot
-// order after the GEMM — deterministic, and no cross-workgroup synchronisation
-// inside the kernel (an agent-scope fence costs a whole-L2 write-back and
-// invalidate on this multi-XCD part).
+// Stream-K schedule.  The output columns are cut into T tiles of 64·WN columns
+// and K into S stages of 64; the T*S (tile, stage) units are dealt out in
+// tile-major order, U consecutive units per workgroup, so every workgroup streams
+// the same number of weight bytes whatever T is (a fixed tile-per-workgroup grid
+// leaves some CUs with twice the work of others).  A workgroup's range may end
+// one tile and start the next.  A tile computed by one workgroup alone gets its
+// epilogue straight from registers; the pieces of a tile shared by several
+// workgroups go to fp32 partial slots (slot j = g - first(t)) that a fix-up kernel
+// sums in slot order after the GEMM — deterministic, and no cross-workgroup
+// synchronisation inside the kernel (an agent-scope fence costs a whole-L2
+// write-back and invalidate on this multi-XCD part).
 // (Plan, make_plan, make_plan_whole, plan_grid, plan_slots, tile_first,
 // tile_last, plan_range_end, plan_piece and part_bytes: sf_index.h.)
 
@@ -161,7 +223,8 @@ SF_DEV T sum_slots(const float* p, size_t stride, int n) {
 enum Mode {
   kPart = 0,     // every tile piece to its partial slot (QKV: the fix-up adds bias + RoPE)
   kScatter = 1,  // out[rows[m]][c] = bf16(y); shared tiles to partial slots (FFN down)
-  kSilu = 2,     // out[m][c] = bf16(bf16(silu(bf16 y_gate)) * bf16 y_up); whole tiles only
+  kSilu = 2,     // out[m][c] = bf16(bf16(silu(bf16 y_gate)) * bf16 y_up); shared tiles to
+                 // partial slots of 2N columns (gate, then up) for the fix-up
   kResid = 3,    // out[m][c] = bf16(res[m][c] + bf16(y)); whole tiles only (o_proj)
   kPlain = 4,    // out[m][c] = bf16(y); whole tiles only (lm_head)
 };
@@ -175,41 +238,50 @@ struct Epi {
 
 // C = A[rows] . W^T on packed weights, stream-K over (tile, stage) units; WN column
 // tiles of 16 per wave (kSilu: WN = 2 = the gate and the up tile of the same 16
-// output columns).  Grid: (plan_grid, 1, m blocks).  part: fp32 partial slots
-// [slot][mcap][N].
-template <int WN, int MODE, int MB = kMB, int WAVES = SFG_WAVES>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES, WAVES)))
+// output columns).  All M <= MB rows in one pass over the weights (more rows:
+// one pass per MB rows).  Grid: plan_grid workgroups.
+// part: fp32 partial slots [slot][mcap][N] ([slot][mcap][2N] for kSilu).
+template <int WN, int MODE, int MB>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void gemm_sk_kernel(const uint16_t* __restrict__ A, const int32_t* __restrict__ a_rows, int lda,
                     const int32_t* __restrict__ count_p, int m_static, int mcap,
                     const uint16_t* __restrict__ W0, const uint16_t* __restrict__ W1, int K, int N,
                     Plan plan, float* __restrict__ part, Epi ep) {
-  constexpr int kMT = MB / 16;    // max m tiles of this kernel's row block
-  __shared__ SmemT<MB> sm;
-  const int M = count_p ? min(*count_p, mcap) : m_static;
-  const int m0 = blockIdx.z * MB;
-  if (m0 >= M) return;
-  const int mrows = min(MB, M - m0);
-  const int nmt = (mrows + 15) >> 4;
+  constexpr int kMT = MB / 16;    // max m tiles of this kernel
+  using St = Stage<MB, WN>;
+  constexpr int R = St::kRing;
+  __shared__ sf_u32x4 ring[R * St::kWords];
+  __shared__ int rows_s[MB];
+  Ring<MB, WN> rg;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) rg.slot[j] = ring + (j < R ? j : 0) * St::kWords;
+  const int M = count_p ? sf_imin(*count_p, mcap) : m_static;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = tid >> 6;
-  if (tid < MB) {
-    const int r = m0 + min(tid, mrows - 1);
-    sm.rows[tid] = a_rows ? a_rows[r] : r;
-  }
-  __syncthreads();
   const size_t stride = (size_t)mcap * N;
   const int g = blockIdx.x;
   const int u_end = plan_range_end(g, plan);
+  // rows beyond MB (a launch whose mcap exceeds 256) take further passes
+  for (int m0 = 0; m0 < M; m0 += MB) {
+  const int mrows = sf_imin(MB, M - m0);
+  const int nmt = (mrows + 15) >> 4;
+  __syncthreads();  // the previous pass's last readers of the row table are done
+  if (tid < MB) {
+    const int r = m0 + sf_imin(tid, mrows - 1);
+    rows_s[tid] = a_rows ? a_rows[r] : r;
+  }
+  __syncthreads();
   for (int u = g * plan.U; u < u_end;) {
     const Piece pc = plan_piece(u, u_end, plan);
     const int t = pc.t;
     const int sa = pc.sa;
     const int sb = pc.sb;
+    const int cg = wv;  // column group
     int col[WN];
-    const uint16_t* wrow[WN];
+    const uint16_t* wrow[WN];  // this lane's weight stream of each column tile
     if (MODE == kSilu) {
-      const int c = gemm_col<WN, true>(t, wv, 0, lane);
+      const int c = gemm_col<WN, true>(t, cg, 0, lane);
 #pragma unroll
       for (int tt = 0; tt < WN; ++tt) col[tt] = c;
       wrow[0] = weight_lane_ptr(W0, c >> 4, K, lane);
@@ -217,7 +289,7 @@ void gemm_sk_kernel(const uint16_t* __restrict__ A, const int32_t* __restrict__ 
     } else {
 #pragma unroll
       for (int tt = 0; tt < WN; ++tt) {
-        col[tt] = gemm_col<WN, false>(t, wv, tt, lane);
+        col[tt] = gemm_col<WN, false>(t, cg, tt, lane);
         wrow[tt] = weight_lane_ptr(W0, col[tt] >> 4, K, lane);
       }
     }
@@ -226,60 +298,95 @@ void gemm_sk_kernel(const uint16_t* __restrict__ A, const int32_t* __restrict__ 
     for (int mt = 0; mt < kMT; ++mt)
 #pragma unroll
       for (int tt = 0; tt < WN; ++tt) acc[mt][tt] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
-    switch (nmt) {
-      case 1: mainloop<WN, 1, MB>(A, lda, mrows, wrow, sa, sb, sm, acc); break;
-      case 2: mainloop<WN, 2, MB>(A, lda, mrows, wrow, sa, sb, sm, acc); break;
-      case 3: mainloop<WN, 3, MB>(A, lda, mrows, wrow, sa, sb, sm, acc); break;
-      default: mainloop<WN, kMT, MB>(A, lda, mrows, wrow, sa, sb, sm, acc); break;
-    }
+    // m tiles rounded up to 2, 4 or 8 (fewer instantiations; the extra tiles
+    // re-read the last row and their results are dropped)
+    if (nmt <= 2)
+      mainloop<WN, 2, MB>(A, lda, mrows, rows_s, wrow, sa, sb, rg, acc);
+    else if (nmt <= 4 || kMT < 8)
+      mainloop<WN, (kMT < 4 ? kMT : 4), MB>(A, lda, mrows, rows_s, wrow, sa, sb, rg, acc);
+    else
+      mainloop<WN, (kMT < 8 ? kMT : 8), MB>(A, lda, mrows, rows_s, wrow, sa, sb, rg, acc);
+    // the tile to LDS (the ring's memory), then every thread takes 4 consecutive
+    // columns of a row: epilogue, vector stores
+    constexpr bool kS = MODE == kSilu;
+    float* tl = reinterpret_cast<float*>(ring);
+    static_assert(TileLds<WN, MB, kS>::kFloats * 4 <= R * St::kWords * 16, "tile LDS");
+    tile_to_lds<WN, MB, kS>(tl, acc, nmt);
+    __syncthreads();
+    u += sb - sa;
     const int first = tile_first(t, plan);
     const bool whole = MODE != kPart && tile_last(t, plan) == first;
-    float* pw = part + (size_t)(g - first) * stride + (size_t)m0 * N;
+    constexpr int kTW = TileLds<WN, MB, kS>::kTW;
+    // partial slot rows: N columns (kSilu: 2N, the gate sums then the up sums)
+    constexpr int kPW = kS ? 2 : 1;
+    float* pw = part + ((size_t)(g - first) * stride + (size_t)m0 * N) * kPW;
+    const int c0 = kS ? t * 128 : t * kTW;   // first output column of the tile
+    for (int e = tid; e < mrows * (kTW / 4); e += kThreads) {
+      const int m = e / (kTW / 4);
+      const int c = (e - m * (kTW / 4)) * 4;          // column in the LDS tile
+      const sf_f32x4 y = *reinterpret_cast<const sf_f32x4*>(tl + m * kTW + c);
+      if (!whole) {
+        // kSilu: LDS columns [0, 128) are gate sums -> pw[.. + c0 + c], [128, 256)
+        // up sums -> pw[.. + N + c0 + c - 128]
+        const size_t pc = kS ? (c < 128 ? (size_t)c0 + c : (size_t)N + c0 + c - 128)
+                             : (size_t)c0 + c;
+        *reinterpret_cast<sf_f32x4*>(pw + (size_t)m * N * kPW + pc) = y;
+      } else if (kS) {
+        if (c < 128) {
+          const sf_f32x4 up = *reinterpret_cast<const sf_f32x4*>(tl + m * kTW + 128 + c);
+          float r[4];
 #pragma unroll
-    for (int mt = 0; mt < kMT; ++mt) {
-      if (mt >= nmt) continue;
+          for (int i = 0; i < 4; ++i) {
+            const float gt = sf_rbf(y[i]);
+            r[i] = sf_rbf(gt / (1.0f + expf(-gt))) * sf_rbf(up[i]);
+          }
+          sf_u32x2 o;
+          o[0] = sf_pack2(r[0], r[1]);
+          o[1] = sf_pack2(r[2], r[3]);
+          *reinterpret_cast<sf_u32x2*>(ep.out + (size_t)(m0 + m) * ep.ldo + c0 + c) = o;
+        }
+      } else {
+        float r[4];
+        const size_t orow = MODE == kScatter ? (size_t)ep.rows[m0 + m] : (size_t)(m0 + m);
+        const size_t o = orow * ep.ldo + c0 + c;
+        if (MODE == kResid) {
+          float x[4];
+          const sf_u32x2 rv = *reinterpret_cast<const sf_u32x2*>(ep.res + o);
+          x[0] = __uint_as_float(rv[0] << 16);
+          x[1] = __uint_as_float(rv[0] & 0xffff0000u);
+          x[2] = __uint_as_float(rv[1] << 16);
+          x[3] = __uint_as_float(rv[1] & 0xffff0000u);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = mt * 16 + (lane >> 4) * 4 + i;
-        if (m >= mrows) continue;
-        if (!whole) {
-#pragma unroll
-          for (int tt = 0; tt < WN; ++tt) pw[(size_t)m * N + col[tt]] = acc[mt][tt][i];
-        } else if (MODE == kSilu) {
-          const float gt = sf_rbf(acc[mt][0][i]);
-          const float r = sf_rbf(gt / (1.0f + expf(-gt))) * sf_rbf(acc[mt][WN - 1][i]);
-          ep.out[(size_t)(m0 + m) * ep.ldo + col[0]] = sf_f2bf(r);
+          for (int i = 0; i < 4; ++i) r[i] = x[i] + sf_rbf(y[i]);
         } else {
 #pragma unroll
-          for (int tt = 0; tt < WN; ++tt) {
-            const float y = acc[mt][tt][i];
-            if (MODE == kResid) {
-              const size_t o = (size_t)(m0 + m) * ep.ldo + col[tt];
-              ep.out[o] = sf_f2bf(sf_bf2f(ep.res[o]) + sf_rbf(y));
-            } else {
-              const size_t orow = MODE == kScatter ? (size_t)ep.rows[m0 + m] : (size_t)(m0 + m);
-              ep.out[orow * ep.ldo + col[tt]] = sf_f2bf(y);
-            }
-          }
+          for (int i = 0; i < 4; ++i) r[i] = y[i];
         }
+        sf_u32x2 ov;
+        ov[0] = sf_pack2(r[0], r[1]);
+        ov[1] = sf_pack2(r[2], r[3]);
+        *reinterpret_cast<sf_u32x2*>(ep.out + o) = ov;
       }
     }
-    __syncthreads();  // the next piece's first A stage reuses LDS buffer 0
-    u += sb - sa;
+    __syncthreads();  // the tile LDS is the next piece's ring
   }
+  }  // row passes
 }
 
-// MB rows per workgroup (grid z = row blocks), register allocation for WAVES
-// waves per SIMD; every launch here uses the defaults.
-template <int WN, int MODE, int MB = kMB, int WAVES = SFG_WAVES>
+// One pass over the weights for every row: the row block MB is the smallest of
+// 64 / 128 / 256 that holds mcap rows (A ring 8 / 8 / 4 stages, 64 / 128 / 128 KB).
+template <int WN, int MODE>
 inline void launch_sk(const Plan& p, const uint16_t* A, const int32_t* a_rows, int lda,
                       const int32_t* count_p, int m_static, int mcap, const uint16_t* W0,
                       const uint16_t* W1, int K, int N, float* part, const Epi& ep,
                       hipStream_t st) {
-  static_assert(MB % 16 == 0 && MB >= 16 && MB <= 256, "row block: 16..256 rows, whole m tiles");
-  dim3 grid(plan_grid(p), 1, (mcap + MB - 1) / MB);
-  hipLaunchKernelGGL((gemm_sk_kernel<WN, MODE, MB, WAVES>), grid, dim3(256), 0, st, A, a_rows,
-                     lda, count_p, m_static, mcap, W0, W1, K, N, p, part, ep);
+  const dim3 grid(plan_grid(p));
+  if (row_block(mcap) == 64)
+    hipLaunchKernelGGL((gemm_sk_kernel<WN, MODE, 64>), grid, dim3(kThreads), 0, st, A, a_rows, lda,
+                       count_p, m_static, mcap, W0, W1, K, N, p, part, ep);
+  else
+    hipLaunchKernelGGL((gemm_sk_kernel<WN, MODE, 128>), grid, dim3(kThreads), 0, st, A, a_rows,
+                       lda, count_p, m_static, mcap, W0, W1, K, N, p, part, ep);
 }
 
 }  // namespace sfg

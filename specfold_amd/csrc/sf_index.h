@@ -32,7 +32,6 @@ namespace sfg {
 // W[16t + l%16][32c + 8(l/16) .. +8]) are one contiguous 1 KB block, and the
 // chunks of a tile follow each other.
 constexpr int kKsStride = 512;     // elements between 32-wide chunks of a tile
-constexpr int kStageElems = 2048;  // elements between 128-wide K stages of a tile
 
 // Lane `lane`'s first fragment of 16-row tile `tile16`, from base W (a pointer to
 // the packed weights in the kernels; an integer 0 gives the element offset).
@@ -41,19 +40,34 @@ SF_IDX P weight_lane_ptr(P W, int tile16, int K, int lane) {
   return W + (size_t)tile16 * (K / 32) * 512 + lane * 8;
 }
 
-// Output column held by lane `lane` of wave `wv` in its column tile `tt` of
-// 64·WN-column tile t (WN tiles of 16 per wave).  SILU: the gate and the up tile
-// of one wave cover the same 16 columns of a 64-column tile.
+// A stage of the GEMM core is 64 K, two 32-wide MFMA chunks; chunk c of stage sc:
+SF_IDX int weight_chunk(int sc, int c) { return 2 * sc + c; }
+
+// A operand in LDS: per (chunk, m tile) a 1 KB tile of 16 rows x 64 bytes whose
+// four 16-byte units are XOR-swizzled (unit u of row r at position u ^ a_swz(r)).
+// Direct copy j of wave wv brings (chunk, m tile) q = a_copy(wv, j, NMT) = ch*NMT
+// + mt (waves with fewer real copies repeat the last one); its lane L writes word
+// L of the tile (row L/4, position L%4) with A unit a_copy_unit(L) of that row.
+// The MFMA reader lane l (row l%16, unit l/16) reads word a_read_word(l).
+SF_IDX int a_swz(int r) { return (r >> 1) & 3; }
+SF_IDX int a_copy(int wv, int j, int NMT) { return sf_imin(wv + 8 * j, 2 * NMT - 1); }
+SF_IDX int a_copy_unit(int L) { return (L & 3) ^ a_swz(L >> 2); }
+SF_IDX int a_read_word(int l) { return (l & 15) * 4 + ((l >> 4) ^ a_swz(l & 15)); }
+
+// Output column held by lane `lane` of wave `wv` (its column group) in its column
+// tile `tt` of 128·WN-column tile t (WN tiles of 16 per wave).  SILU: the gate and
+// the up tile of one wave cover the same 16 columns of a 128-column tile.
 template <int WN, bool SILU>
 SF_IDX int gemm_col(int t, int wv, int tt, int lane) {
-  return SILU ? t * 64 + wv * 16 + (lane & 15) : t * 64 * WN + wv * 16 * WN + tt * 16 + (lane & 15);
+  return SILU ? t * 128 + wv * 16 + (lane & 15)
+              : t * 128 * WN + wv * 16 * WN + tt * 16 + (lane & 15);
 }
 
 // Stream-K schedule.  The output columns are cut into T tiles and K into S
-// stages of 128; the T*S (tile, stage) units are dealt out in tile-major order,
+// stages of 64; the T*S (tile, stage) units are dealt out in tile-major order,
 // U consecutive units per workgroup.
 #ifndef SFG_GRID
-#define SFG_GRID 512   // workgroups per m block (MI355X: two per CU)
+#define SFG_GRID 256   // workgroups (MI355X: one 8-wave workgroup per CU)
 #endif
 
 struct Plan {

@@ -105,7 +105,7 @@ extern "C" int sf_qkv_rope(const uint16_t* xn, const int32_t* rows, const int32_
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const Plan p = make_plan(n_qkv / 128, D / kKC);
   float* part = reinterpret_cast<float*>(workspace);
-  launch_sk<2, kPart>(p, xn, rows, D, count, 0, bucket, w_qkv, nullptr, D, n_qkv, part, Epi{}, st);
+  launch_sk<1, kPart>(p, xn, rows, D, count, 0, bucket, w_qkv, nullptr, D, n_qkv, part, Epi{}, st);
   dim3 g2(min(bucket, 128), (H + 2 * Hkv + 3) / 4);
   hipLaunchKernelGGL(sf_qkv_epilogue_kernel<false>, g2, dim3(256), 0, st, part, p, bucket, n_qkv, rows,
                      count, b_qkv, cos_tab, sin_tab, pos0, table_rows, q_scale, N, H, Hkv, q_buf,
@@ -139,7 +139,7 @@ extern "C" int sf_qkv_rope_branches(const uint16_t* xn, const int32_t* rows,
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const Plan p = make_plan(n_qkv / 128, D / kKC);
   float* part = reinterpret_cast<float*>(workspace);
-  launch_sk<2, kPart>(p, xn, rows, D, count, 0, bucket, w_qkv, nullptr, D, n_qkv, part, Epi{}, st);
+  launch_sk<1, kPart>(p, xn, rows, D, count, 0, bucket, w_qkv, nullptr, D, n_qkv, part, Epi{}, st);
   dim3 g2(min(bucket, 128), (H + 2 * Hkv + 3) / 4);
   hipLaunchKernelGGL(sf_qkv_epilogue_kernel<true>, g2, dim3(256), 0, st, part, p, bucket, n_qkv,
                      rows, count, b_qkv, cos_tab, sin_tab, pos0_branch, table_rows, q_scale_rows,

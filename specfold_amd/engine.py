@@ -128,8 +128,10 @@ class _Buffers:
         self.all_rows = torch.arange(BN, **i32)
         self.all_count = torch.full((1,), BN, **i32)
         nq = (H + 2 * Hkv) * hd
-        # GEMM workspaces: fp32 partial slots of the stream-K split
-        self.ws_gemm = torch.empty(max(_lib.gemm_workspace_bytes(bucket, D, eng.I), 256),
+        # GEMM workspaces: fp32 partial slots of the stream-K split (gate/up and down
+        # run one after the other on one stream and share theirs)
+        self.ws_gemm = torch.empty(max(_lib.gemm_workspace_bytes(bucket, D, eng.I),
+                                       _lib.gate_up_workspace_bytes(bucket, D, eng.I), 256),
                                    dtype=torch.uint8, device=dev)
         self.ws_qkv = torch.empty(max(_lib.qkv_workspace_bytes(bucket, D, nq), 256),
                                   dtype=torch.uint8, device=dev)
@@ -552,7 +554,7 @@ class FoldedVerifyEngine:
                                     lyr.post_attention_layernorm.weight, self.eps, buf.hp, buf.zn)
             # FFN on the compacted rows (:211-217)
             wg, wu, wd = self._packed_mlp[li]
-            _lib.ffn_gate_up(buf.zn, count, bucket, wg, wu, D, self.I, buf.act)
+            _lib.ffn_gate_up(buf.zn, count, bucket, wg, wu, D, self.I, buf.act, buf.ws_gemm)
             _lib.ffn_down_scatter(buf.act, count, bucket, buf.rows, wd, self.I, D, buf.ffn,
                                   buf.ws_gemm)
             if trace is not None:
@@ -705,7 +707,7 @@ class FoldedVerifyEngine:
         wg, wu, wd = self._packed_mlp[li]
 
         def gate_up():
-            _lib.ffn_gate_up(buf.zn, count, bucket, wg, wu, D, self.I, buf.act)
+            _lib.ffn_gate_up(buf.zn, count, bucket, wg, wu, D, self.I, buf.act, buf.ws_gemm)
 
         def down():
             _lib.ffn_down_scatter(buf.act, count, bucket, buf.rows, wd, self.I, D, buf.ffn,

@@ -41,7 +41,7 @@ static long long g_checks = 0;
   } while (0)
 
 typedef size_t (*ws3_fn)(int, int, int);
-static ws3_fn f_gemm_ws, f_qkv_ws, f_attn_ws;
+static ws3_fn f_gemm_ws, f_qkv_ws, f_attn_ws, f_gu_ws;
 
 // ---------------------------------------------------------------------------
 // GEMM plans
@@ -94,8 +94,11 @@ static int walk_plan(const sfg::Plan& p, bool whole) {
 
 static void check_plans() {
   long long plans = 0;
+  std::vector<int> Ss;
+  for (int S = 1; S <= 96; ++S) Ss.push_back(S);
+  for (int S = 97; S <= 640; S += 13) Ss.push_back(S);
   for (int T = 1; T <= 160; ++T)
-    for (int S = 1; S <= 96; ++S) {
+    for (int S : Ss) {
       const sfg::Plan p = sfg::make_plan(T, S);
       CHECK(sfg::plan_grid(p) <= SFG_GRID, "grid %d", sfg::plan_grid(p));
       walk_plan(p, false);
@@ -110,48 +113,53 @@ static void check_plans() {
                           {4096, 6144, 14336, 131072}, {5120, 7168, 17408, 131072},
                           {896, 1152, 4864, 151936}};
   for (const Shape& s : shapes) {
-    for (int mcap : {1, 39, 64, 65, 256, 1024}) {
-      // QKV: 128-column tiles, stream-K, partial slots [slots][bucket][n_qkv]
-      const sfg::Plan q = sfg::make_plan(s.nqkv / 128, s.D / 128);
+    for (int mcap : {1, 39, 64, 65, 128, 129, 256, 1024}) {
+      // QKV: 128-column tiles, 64-K stages, stream-K, partial slots [slots][bucket][n_qkv]
+      const sfg::Plan q = sfg::make_plan(s.nqkv / 128, s.D / 64);
       const int qs = walk_plan(q, false);
       const size_t need_q = (size_t)(qs + 1) * mcap * s.nqkv * sizeof(float);
       CHECK(f_qkv_ws(mcap, s.D, s.nqkv) >= need_q, "qkv workspace D=%d", s.D);
-      // down: 64-column tiles over D, K = I
-      const sfg::Plan d = sfg::make_plan(s.D / 64, s.I / 128);
+      // down: 128-column tiles over D, K = I
+      const sfg::Plan d = sfg::make_plan(s.D / 128, s.I / 64);
       const int ds = walk_plan(d, false);
       CHECK(f_gemm_ws(mcap, s.D, s.I) >= (size_t)(ds + 1) * mcap * s.D * sizeof(float),
             "down workspace D=%d I=%d", s.D, s.I);
-      plans += 2;
+      // gate/up: 128 output columns per tile, partial rows of 2I (gate, then up)
+      const sfg::Plan gu = sfg::make_plan(s.I / 128, s.D / 64);
+      const int gs = walk_plan(gu, false);
+      CHECK(f_gu_ws(mcap, s.D, s.I) >= (size_t)(gs + 1) * mcap * 2 * s.I * sizeof(float),
+            "gate/up workspace D=%d I=%d", s.D, s.I);
+      plans += 3;
     }
-    walk_plan(sfg::make_plan_whole(s.I / 64, s.D / 128), true);    // gate/up
-    walk_plan(sfg::make_plan_whole(s.D / 64, s.D / 128), true);    // o_proj (H·hd = D)
-    walk_plan(sfg::make_plan_whole(s.V / 128, s.D / 128), true);   // lm_head
-    plans += 3;
+    walk_plan(sfg::make_plan_whole(s.D / 128, s.D / 64), true);    // o_proj (H·hd = D)
+    walk_plan(sfg::make_plan_whole(s.V / 128, s.D / 64), true);    // lm_head
+    plans += 2;
   }
   printf("gemm plans: %lld plans walked\n", plans);
 }
 
 // Output columns and packed-weight addressing of one GEMM mode: N output
-// columns in T tiles of 64·WN (SILU: 64), K = 128·S.
+// columns in T tiles of 128·WN (SILU: 128), K = 64·S; each of the 8 waves owns
+// one column group and takes both 32-K chunks of every stage.
 template <int WN, bool SILU>
 static void check_columns(int N, int K) {
-  const int tw = SILU ? 64 : 64 * WN;
+  const int tw = SILU ? 128 : 128 * WN;
   CHECK(N % tw == 0, "N %% tile");
-  const int T = N / tw, S = K / 128;
+  const int T = N / tw, S = K / 64;
   const int ntile = SILU ? 1 : WN;
   for (int t = 0; t < T; ++t) {
     std::vector<int> hits(tw, 0);
-    for (int wv = 0; wv < 4; ++wv)
+    for (int wv = 0; wv < 8; ++wv)
       for (int tt = 0; tt < ntile; ++tt)
         for (int lane = 0; lane < 64; ++lane) {
           const int col = sfg::gemm_col<WN, SILU>(t, wv, tt, lane);
           CHECK(col >= t * tw && col < (t + 1) * tw && col < N, "col %d of tile %d", col, t);
           if (lane < 16) ++hits[col - t * tw];
-          // the lane's weight stream: stage sc, 32-wide chunk ks of tile col/16
+          // the lane's weight stream: chunks weight_chunk(sc, c) of tile col/16
           for (int sc = 0; sc < S; ++sc)
-            for (int ks = 0; ks < 4; ++ks) {
+            for (int c = 0; c < 2; ++c) {
               const size_t off = sfg::weight_lane_ptr<size_t>(0, col >> 4, K, lane) +
-                                 (size_t)sc * sfg::kStageElems + ks * sfg::kKsStride;
+                                 (size_t)sfg::weight_chunk(sc, c) * sfg::kKsStride;
               CHECK(off + 8 <= (size_t)N * K, "weight load past the end");
               // packed layout: word (tile16 · K/32 + chunk) · 64 + l holds
               // W[16 tile16 + l%16][32 chunk + 8 (l/16) ..+8]
@@ -159,8 +167,9 @@ static void check_columns(int N, int K) {
               const size_t word = off / 8;
               const size_t l = word & 63, tc = word >> 6;
               const size_t tile16 = tc / (K / 32), chunk = tc % (K / 32);
+              CHECK(l == (size_t)lane, "a weight fragment is word `lane` of its 1 KB block");
               CHECK(tile16 * 16 + (l & 15) == (size_t)col, "B fragment column");
-              CHECK(chunk * 32 + (l >> 4) * 8 == (size_t)sc * 128 + ks * 32 + (lane >> 4) * 8,
+              CHECK(chunk * 32 + (l >> 4) * 8 == (size_t)sc * 64 + c * 32 + (lane >> 4) * 8,
                     "B fragment k");
             }
         }
@@ -168,14 +177,53 @@ static void check_columns(int N, int K) {
   }
 }
 
+// The A operand's LDS tiles: the copies of a stage cover every (chunk, m tile)
+// (extra copies only repeat the last), and the MFMA reader of every lane finds
+// the A unit its fragment needs.
+static void check_a_tiles() {
+  for (int NMT : {1, 2, 3, 4, 5, 8, 16}) {
+    const int DPW = (2 * NMT + 7) / 8;
+    std::vector<int> got(2 * NMT, 0);
+    for (int wv = 0; wv < 8; ++wv)
+      for (int j = 0; j < DPW; ++j) {
+        const int q = sfg::a_copy(wv, j, NMT);
+        CHECK(q >= 0 && q < 2 * NMT, "copy %d out of range", q);
+        ++got[q];
+      }
+    for (int q = 0; q < 2 * NMT - 1; ++q) CHECK(got[q] == 1, "tile %d copied %d times", q, got[q]);
+    CHECK(got[2 * NMT - 1] >= 1, "last tile never copied");
+  }
+  // word w of a tile holds unit a_copy_unit(w) of row w/4
+  int unit_at[64], row_at[64];
+  std::vector<int> seen(64, 0);
+  for (int L = 0; L < 64; ++L) {
+    unit_at[L] = sfg::a_copy_unit(L);
+    row_at[L] = L >> 2;
+    ++seen[row_at[L] * 4 + unit_at[L]];
+  }
+  for (int i = 0; i < 64; ++i) CHECK(seen[i] == 1, "(row, unit) %d stored %d times", i, seen[i]);
+  for (int l = 0; l < 64; ++l) {
+    const int w = sfg::a_read_word(l);
+    CHECK(w >= 0 && w < 64, "read word");
+    CHECK(row_at[w] == (l & 15) && unit_at[w] == (l >> 4), "lane %d reads the wrong unit", l);
+  }
+  // the 8 lanes of each quarter-wave read distinct 16-byte bank groups
+  for (int g = 0; g < 8; ++g) {
+    int mask = 0;
+    for (int l = 8 * g; l < 8 * g + 8; ++l) mask |= 1 << (sfg::a_read_word(l) & 7);
+    CHECK(mask == 0xff, "bank groups of lanes %d..%d", 8 * g, 8 * g + 7);
+  }
+}
+
 static void check_gemm_columns() {
-  check_columns<2, false>(4608, 3584);    // QKV, 7B
-  check_columns<2, false>(2048, 1536);    // QKV, 1.5B
+  check_columns<1, false>(4608, 3584);    // QKV, 7B
+  check_columns<1, false>(2048, 1536);    // QKV, 1.5B
   check_columns<1, false>(3584, 18944);   // down, 7B
   check_columns<1, false>(5120, 5120);    // o_proj, 14B
   check_columns<2, true>(18944, 3584);    // gate/up, 7B
   check_columns<2, true>(17408, 5120);    // gate/up, 14B
-  check_columns<2, false>(1024, 896);     // lm_head-style 128-column tiles
+  check_columns<1, false>(1024, 896);     // lm_head-style 128-column tiles
+  check_a_tiles();
   printf("gemm columns and weight fragments: ok\n");
 }
 
@@ -362,7 +410,8 @@ int main(int argc, char** argv) {
   f_gemm_ws = (ws3_fn)dlsym(lib, "sf_gemm_workspace_bytes");
   f_qkv_ws = (ws3_fn)dlsym(lib, "sf_qkv_workspace_bytes");
   f_attn_ws = (ws3_fn)dlsym(lib, "sf_attn_workspace_bytes");
-  if (!f_gemm_ws || !f_qkv_ws || !f_attn_ws) {
+  f_gu_ws = (ws3_fn)dlsym(lib, "sf_ffn_gate_up_workspace_bytes");
+  if (!f_gemm_ws || !f_qkv_ws || !f_attn_ws || !f_gu_ws) {
     fprintf(stderr, "missing workspace queries\n");
     return 2;
   }

@@ -162,11 +162,12 @@ def hip_ffn(eng, li: int, hp: torch.Tensor, rows: torch.Tensor) -> torch.Tensor:
     zn = torch.zeros(BN, D, dtype=torch.bfloat16, device=dev)
     act = torch.zeros(BN, eng.I, dtype=torch.bfloat16, device=dev)
     ffn = torch.zeros(BN + 1, D, dtype=torch.bfloat16, device=dev)
-    ws = torch.empty(max(_lib.gemm_workspace_bytes(BN, D, eng.I), 256), dtype=torch.uint8,
+    ws = torch.empty(max(_lib.gemm_workspace_bytes(BN, D, eng.I),
+                         _lib.gate_up_workspace_bytes(BN, D, eng.I), 256), dtype=torch.uint8,
                      device=dev)
     wg, wu, wd = eng._packed_mlp[li]
     _lib.rows_rmsnorm(hp_d, rows_d, count, BN, lyr.post_attention_layernorm.weight, D, eng.eps, zn)
-    _lib.ffn_gate_up(zn, count, BN, wg, wu, D, eng.I, act)
+    _lib.ffn_gate_up(zn, count, BN, wg, wu, D, eng.I, act, ws)
     _lib.ffn_down_scatter(act, count, BN, rows_d, wd, eng.I, D, ffn, ws)
     return ffn[:BN]
 

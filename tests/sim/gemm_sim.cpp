@@ -2,7 +2,7 @@
 // CPU SIMT simulator in separate objects) on random bf16 inputs and checks them
 // against float64 dot products rounded as each epilogue specifies:
 //   sf_pack_weight      the packed layout word (t, c, l) = W[16t + l%16][32c + 8(l/16) .. +8]
-//   sf_ffn_gate_up      act[m] = bf16(bf16(silu(bf16 g)) * bf16 u), m < count (whole tiles)
+//   sf_ffn_gate_up      act[m] = bf16(bf16(silu(bf16 g)) * bf16 u), m < count (stream-K, fix-up)
 //   sf_ffn_down_scatter ffn[rows[m]] = bf16(act[m] . Wd^T), m < count (stream-K, fix-up);
 //                       rows not in `rows` stay untouched
 //   sf_o_proj_residual  hp[r] = bf16(x[r] + bf16(o[r] . Wo^T)), r < M (static M)
@@ -99,7 +99,9 @@ int main(int argc, char** argv) {
     const auto pg = pack(wg, I, D), pu = pack(wu, I, D), pd = pack(wd, D, I);
     std::vector<uint16_t> act((size_t)bucket * I, 0x7fc0);
     int32_t cnt = count;
-    if (sf_ffn_gate_up(zn.data(), &cnt, bucket, pg.data(), pu.data(), D, I, act.data(), nullptr)) {
+    std::vector<float> gws(sf_ffn_gate_up_workspace_bytes(bucket, D, I) / 4 + 16);
+    if (sf_ffn_gate_up(zn.data(), &cnt, bucket, pg.data(), pu.data(), D, I, act.data(), gws.data(),
+                       gws.size() * 4, nullptr)) {
       fprintf(stderr, "sf_ffn_gate_up failed\n");
       return 1;
     }

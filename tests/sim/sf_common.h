@@ -48,3 +48,27 @@ SF_DEV sf_f32x4 sf_mfma16x16x32(const sf_bf16x8 a, const sf_bf16x8 b, sf_f32x4 c
 }
 
 static inline int sf_launch_status() { return hipGetLastError() == hipSuccess ? SF_OK : SF_ERR_HIP; }
+
+// Direct global -> LDS copies: done at issue in the simulation (the waits that
+// order them on the GPU are no-ops here; the barrier is a workgroup barrier).
+typedef void sf_lds_void;
+SF_DEV void sf_lds_dma16(const void* src, void* lds_base) {
+  memcpy(static_cast<char*>(lds_base) + 16 * sim_lane(), src, 16);
+}
+template <int N>
+SF_DEV void sf_wait_vm_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __syncthreads();
+}
+
+// LDS fragment reads (the GPU issues them untracked and waits once): plain reads.
+typedef uintptr_t sf_lds_off;
+template <int OFF>
+SF_DEV sf_u32x4 sf_lds_read16(sf_lds_off addr) {
+  sf_u32x4 v;
+  memcpy(&v, reinterpret_cast<const void*>(addr + OFF), 16);
+  return v;
+}
+template <int N>
+SF_DEV void sf_lds_reads_done(sf_u32x4 (&)[N]) {}
+SF_DEV sf_lds_off sf_lds_addr(const void* p) { return reinterpret_cast<uintptr_t>(p); }

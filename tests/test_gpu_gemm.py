@@ -88,10 +88,16 @@ def test_o_proj_residual(M):
     close_bf16(hp, ref, scale=ref.float().abs() + mm.float().abs(), atol=acc_bound(o, w))
 
 
-@pytest.mark.parametrize("count", [1, 39, 117, 130, 256])
-def test_ffn_path(count):
-    g = torch.Generator().manual_seed(count)
-    D, I, BN, bucket = 1536, 8960, 256, 256
+@pytest.mark.parametrize("count,D,I,bucket", [(1, 1536, 8960, 256), (39, 1536, 8960, 256),
+                                               (117, 1536, 8960, 256), (130, 1536, 8960, 256),
+                                               (256, 1536, 8960, 256), (39, 3584, 18944, 256),
+                                               (117, 3584, 18944, 128), (300, 1536, 8960, 512),
+                                               (64, 1536, 8960, 64)])
+def test_ffn_path(count, D, I, bucket):
+    """Row counts across the row blocks (64 / 128 / 256 rows per pass, and two
+    passes beyond 256), the 1.5B and 7B FFN shapes."""
+    g = torch.Generator().manual_seed(count + D)
+    BN = max(256, bucket)
     hp = rnd(BN + 1, D, gen=g)
     perm = torch.randperm(BN, generator=g)[:count].sort().values
     rows = torch.full((bucket,), BN, dtype=torch.int32)
@@ -102,10 +108,11 @@ def test_ffn_path(count):
     zn = torch.zeros(bucket, D, dtype=torch.bfloat16, device="cuda")
     act = torch.zeros(bucket, I, dtype=torch.bfloat16, device="cuda")
     ffn = torch.zeros(BN + 1, D, dtype=torch.bfloat16, device="cuda")
-    ws = zeros_ws(_lib.gemm_workspace_bytes(bucket, D, I))
+    ws = zeros_ws(max(_lib.gemm_workspace_bytes(bucket, D, I),
+                      _lib.gate_up_workspace_bytes(bucket, D, I)))
     _lib.rows_rmsnorm(hp, rows, cnt, bucket, lnw, D, 1e-6, zn)
     for _ in range(2):  # twice through one workspace
-        _lib.ffn_gate_up(zn, cnt, bucket, packed(wg), packed(wu), D, I, act)
+        _lib.ffn_gate_up(zn, cnt, bucket, packed(wg), packed(wu), D, I, act, ws)
         _lib.ffn_down_scatter(act, cnt, bucket, rows, packed(wd), I, D, ffn, ws)
     torch.cuda.synchronize()
     r = rows[:count].long()

@@ -1,11 +1,13 @@
 """The weight-streaming GEMM kernels' own source (specfold_amd/csrc/sf_ffn.hip,
 sf_qkv.hip, sf_gemm_core.h) run on the CPU through the SIMT simulator of
 tests/sim, called through the library's entry points: weight packing, FFN
-gate/up (whole tiles, SiLU epilogue), FFN down (stream-K with partial slots,
-fix-up, row scatter), o_proj + residual and lm_head (static row counts), and the
-QKV projection with bias, RoPE from absolute-position tables, the optional q
-scale and the scatter by flat row, over one to four 64-row blocks, against float64 dot products rounded as each epilogue
-specifies (tests/sim/gemm_sim.cpp states the tolerance)."""
+gate/up (stream-K, SiLU epilogue from registers or in the fix-up), FFN down
+(stream-K with partial slots, fix-up, row scatter), o_proj + residual and
+lm_head (static row counts), and the QKV projection with bias, RoPE from
+absolute-position tables, the optional q scale and the scatter by flat row, for
+row counts of one row up to two passes of 128 rows, against float64 dot products
+rounded as each epilogue specifies (tests/sim/gemm_sim.cpp states the
+tolerance)."""
 
 import shutil
 import subprocess
