@@ -39,6 +39,7 @@ extern "C" {
 #define SF_ERR_ARG 2       /* a required pointer is NULL or a value is invalid */
 #define SF_ERR_WORKSPACE 3 /* workspace smaller than *_workspace_bytes() */
 #define SF_ERR_HIP 4       /* a HIP launch failed */
+#define SF_ERR_SCRATCH 5   /* larger than the fixed scratch of an allocation-free entry point */
 
 /* Gate precision modes for sf_fold_gate. */
 #define SF_GATE_MODEL_DTYPE 0 /* norms rounded to bf16 as the PyTorch reference
@@ -57,7 +58,9 @@ extern "C" {
 const char* sf_status_string(int status);
 /* 2: GEMM weights in the packed layout of sf_pack_weight; fused residual entries.
  * 3: sf_parent_map (the branch parent map on the device); sf_logit_stats.
- * 4: batched verify steps: SF_GATE_ROOTS_BY_PARENT, sf_qkv_rope_branches. */
+ * 4: batched verify steps: SF_GATE_ROOTS_BY_PARENT, sf_qkv_rope_branches.
+ * 5: GEMMs on 64-wide K chunks (K % 64, N % 128); sf_ffn_gate_up takes a workspace.
+ * 6: sf_logit_stats_noalloc, SF_ERR_SCRATCH. */
 int sf_abi_version(void);
 
 /*
@@ -290,6 +293,24 @@ int sf_logit_stats(const uint16_t* logits, int M, int V, long long ld, float top
                    int32_t* top_idx, float* top_val, float* zfull, float* znuc,
                    int32_t* greedy_tok, float* conf, float* conf_full, void* workspace,
                    size_t workspace_bytes, void* stream);
+
+/*
+ * sf_logit_stats without a workspace argument: the same kernels and outputs
+ * (bit-identical), with the histograms and candidates in a fixed array in device
+ * memory that the library holds on each GPU it runs on until the process ends
+ * (16 MiB + 32 KiB per GPU).  No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  It calls no allocating
+ * routine; the first call on a device looks the array up and clears it on
+ * `stream` (the current device must be the stream's).
+ * Limit: M <= sf_logit_stats_noalloc_max_rows() (64), else SF_ERR_SCRATCH.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (other streams, other host threads) race and must be ordered by the caller.
+ */
+int sf_logit_stats_noalloc_max_rows(void);
+int sf_logit_stats_noalloc(const uint16_t* logits, int M, int V, long long ld, float top_p,
+                           int32_t* top_idx, float* top_val, float* zfull, float* znuc,
+                           int32_t* greedy_tok, float* conf, float* conf_full, void* stream);
 
 #ifdef __cplusplus
 }

@@ -63,6 +63,8 @@ SIGNATURES = {
     "sf_logit_stats_workspace_bytes": (ctypes.c_size_t, [_i]),
     "sf_parent_map": (_i, [_vp, _i, _i, _vp, _vp, _vp]),
     "sf_logit_stats": (_i, [_vp, _i, _i, _ll, _f] + [_vp] * 7 + [_vp, ctypes.c_size_t, _vp]),
+    "sf_logit_stats_noalloc_max_rows": (_i, []),
+    "sf_logit_stats_noalloc": (_i, [_vp, _i, _i, _ll, _f] + [_vp] * 7 + [_vp]),
 }
 
 
@@ -457,20 +459,23 @@ class LogitStats:
 _STATS_WS: dict = {}
 
 
-def logit_stats(logits: torch.Tensor, top_p: float = 0.95, stream=None) -> LogitStats:
-    """Greedy statistics of the rows of ``logits`` ([..., V] bf16, rows contiguous
-    along V): top-8 tokens, softmax / nucleus normalisers, greedy token and its
-    bf16 probability (sf_logit_stats)."""
+def _stats_rows(logits: torch.Tensor):
     if logits.dtype != torch.bfloat16 or not logits.is_cuda:
         raise TypeError("logits must be a bf16 CUDA tensor")
     V = logits.shape[-1]
     x = logits.reshape(-1, V)
     if x.stride(1) != 1:
         x = x.contiguous()
-    M, ld = x.shape[0], x.stride(0)
-    if ld % 8 or x.data_ptr() % 16:
+    if x.stride(0) % 8 or x.data_ptr() % 16:
         x = x.contiguous()
-        ld = x.stride(0)
+    return x, x.shape[0], V, x.stride(0)
+
+
+def logit_stats(logits: torch.Tensor, top_p: float = 0.95, stream=None) -> LogitStats:
+    """Greedy statistics of the rows of ``logits`` ([..., V] bf16, rows contiguous
+    along V): top-8 tokens, softmax / nucleus normalisers, greedy token and its
+    bf16 probability (sf_logit_stats)."""
+    x, M, V, ld = _stats_rows(logits)
     need = int(load().sf_logit_stats_workspace_bytes(M))
     key = (x.device.index, M)
     ws = _STATS_WS.get(key)
@@ -483,6 +488,31 @@ def logit_stats(logits: torch.Tensor, top_p: float = 0.95, stream=None) -> Logit
                                _ptr(out.greedy_tok), _ptr(out.conf), _ptr(out.conf_full),
                                _ptr(ws), ws.numel(), _stream(stream))
     _check(st, "sf_logit_stats")
+    return out
+
+
+def logit_stats_noalloc(logits: torch.Tensor, out: LogitStats, top_p: float = 0.95,
+                        stream=None) -> LogitStats:
+    """``logit_stats`` into caller-owned outputs with no workspace: the library's
+    fixed per-GPU scratch (sf_logit_stats_noalloc; at most
+    sf_logit_stats_noalloc_max_rows() rows; calls that overlap on one GPU race).
+    ``logits`` must already be bf16 with rows contiguous, 8-element aligned."""
+    if logits.dtype != torch.bfloat16 or not logits.is_cuda:
+        raise TypeError("logits must be a bf16 CUDA tensor")
+    V = logits.shape[-1]
+    x = logits.reshape(-1, V)
+    M, ld = x.shape[0], x.stride(0)
+    if x.stride(1) != 1 or ld % 8 or x.data_ptr() % 16:
+        raise ValueError("logits rows must be contiguous, 16-byte aligned, stride % 8 == 0")
+    for name in LogitStats.__slots__:
+        t = getattr(out, name)
+        if t.device != x.device or t.shape[0] < M or not t.is_contiguous():
+            raise ValueError(f"out.{name} must hold {M} rows on {x.device}")
+    st = load().sf_logit_stats_noalloc(_ptr(x), M, V, ld, float(top_p), _ptr(out.top_idx),
+                                       _ptr(out.top_val), _ptr(out.zfull), _ptr(out.znuc),
+                                       _ptr(out.greedy_tok), _ptr(out.conf), _ptr(out.conf_full),
+                                       _stream(stream))
+    _check(st, "sf_logit_stats_noalloc")
     return out
 
 

@@ -265,6 +265,7 @@ extern "C" const char* sf_status_string(int status) {
     case SF_ERR_ARG: return "invalid argument";
     case SF_ERR_WORKSPACE: return "workspace too small";
     case SF_ERR_HIP: return "HIP launch failed";
+    case SF_ERR_SCRATCH: return "size beyond the fixed scratch of an allocation-free entry point";
     default: return "unknown status";
   }
 }
@@ -304,7 +305,7 @@ __global__ __launch_bounds__(64) void sf_parent_map_kernel(const int64_t* __rest
 
 }  // namespace
 
-extern "C" int sf_abi_version(void) { return 5; }
+extern "C" int sf_abi_version(void) { return 6; }
 
 extern "C" int sf_parent_map(const int64_t* tokens, int B1, int N, int32_t* par, int32_t* counts,
                              void* stream) {

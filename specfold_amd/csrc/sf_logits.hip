@@ -28,6 +28,8 @@
 // cut and Zn from exact counts; it then clears the histogram for the next call.
 #include <math.h>
 
+#include <mutex>
+
 #include "sf_common.h"
 
 namespace {
@@ -330,6 +332,76 @@ __global__ __launch_bounds__(kFinishThreads) void sf_logit_finish_kernel(
 
 int slices_for(int M) { return max(1, min(kMaxSlices, 512 / M)); }
 
+// Rows the allocation-free entry point takes; with S = slices_for(M) slices per
+// row, M * S <= 512 for every M <= 64, so the candidates fit in 512 * 8 pairs.
+constexpr int kNoAllocMaxRows = 64;
+constexpr size_t kNoAllocHistBytes = (size_t)kNoAllocMaxRows * kKeys * 4;
+constexpr size_t kNoAllocBytes = kNoAllocHistBytes + (size_t)512 * kTop * 8;
+
+__global__ __launch_bounds__(256) void sf_zero_kernel(sf_u32x4* __restrict__ p, size_t n16) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (size_t)gridDim.x * 256)
+    p[i] = sf_u32x4{0u, 0u, 0u, 0u};
+}
+
+int launch_stats(const uint16_t* logits, int M, int V, long long ld, float top_p, int32_t* top_idx,
+                 float* top_val, float* zfull, float* znuc, int32_t* greedy_tok, float* conf,
+                 float* conf_full, uint32_t* hist, void* cand, hipStream_t st) {
+  const int S = slices_for(M);
+  float* cand_v = reinterpret_cast<float*>(cand);
+  int32_t* cand_i = reinterpret_cast<int32_t*>(cand_v + (size_t)M * S * kTop);
+  hipLaunchKernelGGL(sf_logit_slice_kernel, dim3(S, M), dim3(kSliceThreads), 0, st, logits, ld, V,
+                     hist, cand_v, cand_i);
+  hipLaunchKernelGGL(sf_logit_finish_kernel, dim3(M), dim3(kFinishThreads), 0, st, logits, ld, V,
+                     S, top_p, hist, cand_v, cand_i, top_idx, top_val, zfull, znuc, greedy_tok,
+                     conf, conf_full);
+  return sf_launch_status();
+}
+
+int check_stats_args(const uint16_t* logits, int M, int V, long long ld, float top_p,
+                     const int32_t* top_idx, const float* top_val, const float* zfull,
+                     const float* znuc, const int32_t* greedy_tok, const float* conf,
+                     const float* conf_full) {
+  if (!logits || !top_idx || !top_val || !zfull || !znuc || !greedy_tok || !conf || !conf_full)
+    return SF_ERR_ARG;
+  if (M < 1 || V < kTop || V % 8 != 0 || ld < V || ld % 8 != 0) return SF_ERR_SHAPE;
+  if (reinterpret_cast<uintptr_t>(logits) % 16 != 0 || !(top_p > 0.0f)) return SF_ERR_ARG;
+  return SF_OK;
+}
+
+}  // namespace
+
+// The allocation-free entry point's workspace: the histograms of kNoAllocMaxRows
+// rows (zero between calls), then the slice candidates (scratch).  Each GPU holds its own copy
+// for the life of the process.  Host code never uses this name as an address (on
+// the host it is only a stand-in for the symbol): it takes the device address
+// from hipGetSymbolAddress, once per device.
+static __device__ __align__(256) uint8_t scratch[kNoAllocBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];  // scratch's device address per device; null until set up
+
+// The current device's copy of scratch.  The first call on a device looks its
+// address up and clears the histograms (a fill kernel on `st`, so that it also
+// works under stream capture); every call leaves them zero again after that.
+int scratch_for_current_device(hipStream_t st, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return SF_ERR_HIP;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return SF_ERR_HIP;
+    hipLaunchKernelGGL(sf_zero_kernel, dim3(1024), dim3(256), 0, st,
+                       reinterpret_cast<sf_u32x4*>(p), kNoAllocHistBytes / 16);
+    if (sf_launch_status() != SF_OK) return SF_ERR_HIP;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return SF_OK;
+}
+
 }  // namespace
 
 extern "C" size_t sf_logit_stats_workspace_bytes(int M) {
@@ -342,23 +414,36 @@ extern "C" int sf_logit_stats(const uint16_t* logits, int M, int V, long long ld
                               int32_t* top_idx, float* top_val, float* zfull, float* znuc,
                               int32_t* greedy_tok, float* conf, float* conf_full, void* workspace,
                               size_t workspace_bytes, void* stream) {
-  if (!logits || !top_idx || !top_val || !zfull || !znuc || !greedy_tok || !conf || !conf_full ||
-      !workspace)
-    return SF_ERR_ARG;
-  if (M < 1 || V < kTop || V % 8 != 0 || ld < V || ld % 8 != 0) return SF_ERR_SHAPE;
-  if (reinterpret_cast<uintptr_t>(logits) % 16 != 0 ||
-      reinterpret_cast<uintptr_t>(workspace) % 16 != 0 || !(top_p > 0.0f))
-    return SF_ERR_ARG;
+  const int a = check_stats_args(logits, M, V, ld, top_p, top_idx, top_val, zfull, znuc,
+                                 greedy_tok, conf, conf_full);
+  if (a != SF_OK) return a;
+  if (!workspace || reinterpret_cast<uintptr_t>(workspace) % 16 != 0) return SF_ERR_ARG;
   if (workspace_bytes < sf_logit_stats_workspace_bytes(M)) return SF_ERR_WORKSPACE;
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const int S = slices_for(M);
   uint32_t* hist = reinterpret_cast<uint32_t*>(workspace);
-  float* cand_v = reinterpret_cast<float*>(hist + (size_t)M * kKeys);
-  int32_t* cand_i = reinterpret_cast<int32_t*>(cand_v + (size_t)M * S * kTop);
-  hipLaunchKernelGGL(sf_logit_slice_kernel, dim3(S, M), dim3(kSliceThreads), 0, st, logits, ld, V,
-                     hist, cand_v, cand_i);
-  hipLaunchKernelGGL(sf_logit_finish_kernel, dim3(M), dim3(kFinishThreads), 0, st, logits, ld, V,
-                     S, top_p, hist, cand_v, cand_i, top_idx, top_val, zfull, znuc, greedy_tok,
-                     conf, conf_full);
-  return sf_launch_status();
+  return launch_stats(logits, M, V, ld, top_p, top_idx, top_val, zfull, znuc, greedy_tok, conf,
+                      conf_full, hist, hist + (size_t)M * kKeys,
+                      reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int sf_logit_stats_noalloc_max_rows(void) { return kNoAllocMaxRows; }
+
+extern "C" int sf_logit_stats_noalloc(const uint16_t* logits, int M, int V, long long ld,
+                                      float top_p, int32_t* top_idx, float* top_val, float* zfull,
+                                      float* znuc, int32_t* greedy_tok, float* conf,
+                                      float* conf_full, void* stream) {
+  const int a = check_stats_args(logits, M, V, ld, top_p, top_idx, top_val, zfull, znuc,
+                                 greedy_tok, conf, conf_full);
+  if (a != SF_OK) return a;
+  if (M > kNoAllocMaxRows || (size_t)M * slices_for(M) * kTop * 8 > kNoAllocBytes - kNoAllocHistBytes)
+    return SF_ERR_SCRATCH;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  void* ws = nullptr;
+  const int s = scratch_for_current_device(st, &ws);
+  if (s != SF_OK) return s;
+  // fixed layout whatever M is: the histograms of every row the array can take,
+  // then the candidates, so that no call writes candidates over a histogram that
+  // a later call with more rows counts into
+  uint8_t* base = reinterpret_cast<uint8_t*>(ws);
+  return launch_stats(logits, M, V, ld, top_p, top_idx, top_val, zfull, znuc, greedy_tok, conf,
+                      conf_full, reinterpret_cast<uint32_t*>(base), base + kNoAllocHistBytes, st);
 }

@@ -247,6 +247,15 @@ typedef int hipError_t;
 #define hipSuccess 0
 inline int sim_launch_error = 0;
 inline hipError_t hipGetLastError() { int e = sim_launch_error; sim_launch_error = 0; return e; }
+// Device globals are ordinary host arrays here: one "device", whose symbol
+// address is the array's own.
+#define __align__(n) __attribute__((aligned(n)))
+#define HIP_SYMBOL(sym) (&(sym))
+inline hipError_t hipGetDevice(int* d) { *d = 0; return hipSuccess; }
+inline hipError_t hipGetSymbolAddress(void** p, const void* sym) {
+  *p = const_cast<void*>(sym);
+  return hipSuccess;
+}
 
 // Runs grid x block work-items: the workgroups are shared out over a pool of OS
 // threads; a workgroup runs as blockDim fibers on one of them (its __shared__

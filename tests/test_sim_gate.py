@@ -264,6 +264,30 @@ def test_logit_stats(sim, M, V, scale, top_p):
         assert torch.equal(getattr(st, f), getattr(st2, f)), f
 
 
+def test_logit_stats_noalloc_sequence(sim):
+    """sf_logit_stats_noalloc over calls of changing row count (more, fewer, more
+    again) gives exactly the workspace entry point's statistics every time: its
+    fixed scratch keeps the histograms at the same place whatever M is, and a call
+    with fewer rows writes nothing where a later, larger call counts."""
+    g = torch.Generator().manual_seed(12)
+    for i, M in enumerate([9, 2, 9, 1]):
+        logits = (torch.randn(M, 4096, generator=g) * 2.0).to(torch.bfloat16)
+        ref, _ = sim_logit_stats(sim, logits, 0.9)
+        out = sim.LogitStats(M, "cpu")
+        st = sim._LIB.sf_logit_stats_noalloc(
+            sim._ptr(logits), M, 4096, 4096, 0.9, sim._ptr(out.top_idx), sim._ptr(out.top_val),
+            sim._ptr(out.zfull), sim._ptr(out.znuc), sim._ptr(out.greedy_tok), sim._ptr(out.conf),
+            sim._ptr(out.conf_full), None)
+        assert st == 0
+        for f in sim.LogitStats.__slots__:
+            assert torch.equal(getattr(out, f), getattr(ref, f)), (i, M, f)
+    big = sim._LIB.sf_logit_stats_noalloc_max_rows() + 1
+    x = torch.zeros(big, 64, dtype=torch.bfloat16)
+    out = sim.LogitStats(big, "cpu")
+    p = [sim._ptr(getattr(out, f)) for f in sim.LogitStats.__slots__]
+    assert sim._LIB.sf_logit_stats_noalloc(sim._ptr(x), big, 64, 64, 0.9, *p, None) == 5
+
+
 def test_kv_append_paged(sim):
     """The block's K/V rows land at positions start .. start+n_tok of a paged cache
     (shuffled pages), every other cache element untouched."""
