@@ -42,263 +42,372 @@
 
 namespace {
 
-using namespace sfa;  // kHD, kQT, kChunk, kMaxChunks and the index maps
+using namespace sfa;  // kHD, kQT, kChunk, kMaxRanges and the index maps
 
-constexpr int kKStr = 136;   // K tile row stride (bf16)
-constexpr int kVStr = 136;   // V^T tile row stride (bf16): 128 keys + 8 pad
 constexpr int kMaxG = 8;
 constexpr int kMaxN = 64;
 constexpr int kCUs = 256;  // MI355X compute units
 
-// V^T tile swizzle (vt_swz): keys of dim row d are stored in 4-key (8-byte)
-// units, unit u at position u ^ vt_swz(d).  The transposing writes (16 lanes per
-// key group hitting rows 8 apart) then spread over every bank, and the P.V reads
-// (16 consecutive rows, one unit each) stay conflict-free: vt_swz is constant
-// across the 16 rows one read instruction touches.
+// ---- prefix pass ---------------------------------------------------------------------
+// Work item = (query tile of 128 queries, range of 64-key prefix chunks, kv head),
+// one 512-thread workgroup per CU walking items.  Wave w takes the 32 queries
+// (w & 3) * 32 .. +32 of the tile (two 16-query MFMA tiles) against keys
+// (w >> 2) * 32 .. +32 of every chunk, so the 8 waves share each staged chunk and
+// each wave keeps its own running softmax state; the two key halves of a query
+// are combined when the range is done.
 //
-// Prefix chunks per work item (prefix_cpi): one while the one-chunk items fill
-// about two rounds of the resident grid, longer ranges beyond (fewer partials to
-// write and merge, and the next chunk's loads overlap this chunk's math).
-//
-// Keys of a chunk are held in a permuted slot order: load j (0..7) of thread row
-// r = tid / 16 brings key 16j + r, which occupies slot key_slot(j, r) =
-// 64(j/4) + 4r + j%4.  Every load instruction then reads 16 consecutive keys
-// (one 4 KB stretch of a page, whose id is uniform: a scalar load), and the 4
-// keys a thread transposes into V^T are 4 consecutive slots.  The softmax does
-// not depend on key order; only the mask of a partial last chunk needs the key
-// behind a slot (slot_key).
+// Staging: K and V rows of a chunk go straight from the cache to an LDS ring of
+// kRing chunks (global_load_lds, 16 bytes per lane, 1 KB per instruction; rows
+// swizzled by k_unit / v_unit on the copy side), kRing - 1 chunks ahead of the
+// one being computed.  Waves 0-3 copy the K rows, waves 4-7 the V rows, wave w
+// the 16-key group w & 3 (one page: a scalar page-table read per chunk).
+// Scores are formed transposed, S^T = K Q^T (K fragments: one 16-byte read of a
+// key row per lane; Q^T stays in registers), so each lane holds 4 keys of one
+// query per 16-key tile: the softmax max / sum reduce over the 4 lane groups.
+// P^T then feeds O^T += V^T P^T as the B operand straight from registers; the
+// V^T operand comes from the row-major V rows by two transposing reads
+// (ds_read_b64_tr_b16) per 32 keys x 16 dims.
+// P is split into kPParts bf16 parts (hi, then the rounding residuals) so the
+// products P.V keep 8 * kPParts mantissa bits.
+#ifndef SFA_P_PARTS
+#define SFA_P_PARTS 2
+#endif
+constexpr int kPParts = SFA_P_PARTS;
+constexpr int kRing = 4;                          // chunks in the LDS ring
+constexpr int kSlotBytes = 2 * kHalfBytes;        // K then V rows: 32 KB
+constexpr int kPrefixThreads = 512;
+constexpr int kCopiesPerChunk = 4;                // DMA instructions per wave per chunk
 
-// One (query tile, range of prefix chunks, kv head) item of the prefix pass; all
-// 256 threads take part (the LDS barriers are uniform).  K/V of chunk c+1 are
-// loaded into registers while chunk c is scored and accumulated; the running
-// (max, sum, acc) is rescaled per chunk as in flash attention.
+// softmax-weighted accumulation of one chunk for one wave (two query tiles)
+template <int NP>
+SF_DEV void pv_parts(const float (&p)[2][4], sf_bf16x8 (&b)[NP]) {
+  // element j of the B operand: key 4*group + j of tile 0 (j < 4), of tile 1 (j >= 4)
+  sf_u32x4 w[NP];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const float a0 = p[u >> 1][2 * (u & 1)], a1 = p[u >> 1][2 * (u & 1) + 1];
+    w[0][u] = sf_pack2(a0, a1);
+    if (NP > 1) {
+      const float r0 = a0 - sf_rbf(a0), r1 = a1 - sf_rbf(a1);
+      w[NP > 1 ? 1 : 0][u] = sf_pack2(r0, r1);
+      if (NP > 2) w[NP > 2 ? 2 : 0][u] = sf_pack2(r0 - sf_rbf(r0), r1 - sf_rbf(r1));
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NP; ++i) b[i] = sf_as_bf16x8(w[i]);
+}
+
 SF_DEV void prefix_item(const uint16_t* __restrict__ q_buf, const uint16_t* __restrict__ pk,
                         const uint16_t* __restrict__ pv, const int32_t* __restrict__ page_table,
                         int page_size, long long page_stride, long long head_stride, int P,
                         const int32_t* __restrict__ rows, int nq, int G, int H, float scale_log2,
-                        int qmax, int nch_cap, int qt, int r, int c0, int c1, int h, uint16_t* sK,
-                        uint16_t* sV, float* __restrict__ ws_o, float* __restrict__ ws_ml) {
+                        int qmax, int nr_cap, int qt, int r, int c0, int c1, int h,
+                        uint8_t* ring, int* s_pg, float* __restrict__ ws_o,
+                        float* __restrict__ ws_ml) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = tid >> 6;
   const int grp = lane >> 4;  // 0..3
   const int ql = lane & 15;
-  const int qi = qt * kQT + wv * 16 + ql;
-  const bool qvalid = qi < nq;
+  const int qg = wv & 3;      // query group
+  const int kh = wv >> 2;     // key half of every chunk
   const long long head_off = (long long)h * head_stride;
 
-  // Q^T operand: lane holds q[qi][ds*32 + grp*8 .. +8]; a padding query (qi >= nq)
-  // repeats the last real one and its partial is never written
-  sf_u32x4 qf[4];
-  {
-    const int qc = min(qi, nq - 1);
-    const int m = qc / G;
-    const int g = qc - m * G;
-    const uint16_t* qp = q_buf + (size_t)rows[m] * H * kHD + (h * G + g) * kHD + grp * 8;
-#pragma unroll
-    for (int ds = 0; ds < 4; ++ds) qf[ds] = *reinterpret_cast<const sf_u32x4*>(qp + ds * 32);
-  }
-
-  // 16-key group j of chunk ci starts at key g0 (groups past the prefix end are
-  // clamped to the last group holding keys, keys past the end to the last key);
-  // with a page size that is a multiple of 16 a group never straddles pages.
+  // ---- item set-up, in two rounds of loads: (1) the query rows and the range's
+  // page ids (to LDS); (2) the first kRing - 1 chunk copies, then q -------------------
+  const int jg = wv & 3;
+  const bool is_v = wv >= 4;
   const int last_g0 = last_group_g0(P);
-  const int sg = tid & 15;
-  const int kr = tid >> 4;
-  auto group_page = [&](int ci, int j) -> int {
-    const int g0 = chunk_group_g0(ci, j, last_g0);
-    return page_table ? page_table[g0 / page_size] : 0;
-  };
-  sf_u32x4 kreg[8], vreg[2][4];
-  auto load_chunk = [&](int ci, const int* pg) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int g0 = chunk_group_g0(ci, j, last_g0);
-      const long long grow = page_table
-          ? (long long)pg[j] * page_stride + (long long)(g0 & (page_size - 1)) * kHD
-          : (long long)g0 * kHD;
-      const int off = group_key(kr, g0, P) * kHD + sg * 8;
-      kreg[j] = *reinterpret_cast<const sf_u32x4*>(pk + head_off + grow + off);
-      vreg[j >> 2][j & 3] = *reinterpret_cast<const sf_u32x4*>(pv + head_off + grow + off);
-    }
-  };
-  int pg_next[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) pg_next[j] = group_page(c0, j);
-  load_chunk(c0, pg_next);
-  if (c0 + 1 < c1) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) pg_next[j] = group_page(c0 + 1, j);
+  const int ngroups = 4 * (c1 - c0);
+  if (page_table) {
+    for (int i = tid; i < ngroups; i += kPrefixThreads)
+      s_pg[i] = page_table[chunk_group_g0(c0 + (i >> 2), i & 3, last_g0) / page_size];
   }
+  int qrow[2], qhead[2];
+#pragma unroll
+  for (int qs = 0; qs < 2; ++qs) {
+    // a padding query (qi >= nq) repeats the last real one; its partial is not written
+    const int qc = min(qt * kQT + qg * 32 + qs * 16 + ql, nq - 1);
+    const int m = qc / G;
+    qrow[qs] = rows[m];
+    qhead[qs] = h * G + (qc - m * G);
+  }
+  sf_wait_vm_loads();
+  // the q rows' addresses, formed before any copy is in flight
+  long long qoff[2];  // element offsets (a pinned pointer would lose its address space)
+#pragma unroll
+  for (int qs = 0; qs < 2; ++qs) {
+    sf_pin(qrow[qs]);
+    qoff[qs] = (long long)qrow[qs] * H * kHD + qhead[qs] * kHD + grp * 8;
+    sf_pin(qoff[qs]);
+  }
+  __syncthreads();  // s_pg
 
-  float m_run = -INFINITY, l_run = 0.f;
-  sf_f32x4 acc[8];
+  // copies: wave w fills rows 16(w&3) .. +16 of K (w < 4) or V (w >= 4) of a chunk;
+  // the wave's 16-key group of chunk ci (past the range end: its last chunk again)
+  // lies in one page
+  const uint16_t* src_base = (is_v ? pv : pk) + head_off;
+  int unit_off[kCopiesPerChunk];  // element offset of the logical unit this lane copies
 #pragma unroll
-  for (int i = 0; i < 8; ++i) acc[i] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < kCopiesPerChunk; ++i) {
+    const int row = 16 * jg + 4 * i + (lane >> 4);
+    const int p = lane & 15;
+    unit_off[i] = (is_v ? v_unit(row, p) : k_unit(row, p)) * 8;
+  }
+  const int dst0 = (is_v ? kHalfBytes : 0) + 16 * jg * kRowBytes;
+  const sf_lds_off pg_addr = sf_lds_addr(s_pg) + 4 * jg;
+  auto issue = [&](int ci, uint8_t* slot) {
+    const int cc = min(ci, c1 - 1);
+    const int g0 = __builtin_amdgcn_readfirstlane(chunk_group_g0(cc, jg, last_g0));
+    long long grow = (long long)g0 * kHD;
+    if (page_table) {
+      const int pg = __builtin_amdgcn_readfirstlane(
+          (int)sf_lds_read4_now(pg_addr + 16 * (uint32_t)(cc - c0)));
+      grow = (long long)pg * page_stride + (long long)(g0 & (page_size - 1)) * kHD;
+    }
+    const uint16_t* gsrc = src_base + grow;
+#pragma unroll
+    for (int i = 0; i < kCopiesPerChunk; ++i) {
+      const int kr = group_key(4 * i + (lane >> 4), g0, P);
+      sf_lds_dma16(gsrc + (size_t)kr * kHD + unit_off[i], slot + dst0 + 4 * i * kRowBytes);
+    }
+  };
+#pragma unroll
+  for (int j = 0; j < kRing - 1; ++j) issue(c0 + j, ring + j * kSlotBytes);
 
-  for (int c = c0; c < c1; ++c) {
-    const int nkeys = min(P - c * kChunk, kChunk);  // >= 1
-    // stage K (slot order) and V^T of chunk c (V^T: dims (2w, 2w+1) of slots
-    // 4kr + 64p .. +3 -> one word per dim, by byte permutes)
+  // Q^T operands: lane holds q[query][ds*32 + grp*8 .. +8] of its query in each of
+  // the two 16-query tiles.  They complete (with the first copies) before the loop,
+  // so its wait counts cover the copies alone.
+  sf_u32x4 qf[2][4];
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      *reinterpret_cast<sf_u32x4*>(&sK[key_slot(j, kr) * kKStr + sg * 8]) = kreg[j];
+  for (int qs = 0; qs < 2; ++qs)
 #pragma unroll
-    for (int p = 0; p < 2; ++p)
+    for (int ds = 0; ds < 4; ++ds)
+      qf[qs][ds] = *reinterpret_cast<const sf_u32x4*>(q_buf + qoff[qs] + ds * 32);
+  sf_wait_vm_loads();
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const uint32_t x0 = vreg[p][0][w], x1 = vreg[p][1][w];
-        const uint32_t x2 = vreg[p][2][w], x3 = vreg[p][3][w];
-        sf_u32x2 lo, hi;
-        lo[0] = (x0 & 0xffffu) | (x1 << 16);
-        lo[1] = (x2 & 0xffffu) | (x3 << 16);
-        hi[0] = (x0 >> 16) | (x1 & 0xffff0000u);
-        hi[1] = (x2 >> 16) | (x3 & 0xffff0000u);
-        const int d = sg * 8 + 2 * w;  // d and d + 1 share vt_swz
-        const int col = ((16 * p + kr) ^ vt_swz(d)) * 4;
-        *reinterpret_cast<sf_u32x2*>(&sV[d * kVStr + col]) = lo;
-        *reinterpret_cast<sf_u32x2*>(&sV[(d + 1) * kVStr + col]) = hi;
+  for (int qs = 0; qs < 2; ++qs)
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) sf_pin(qf[qs][ds]);
+
+  // ---- LDS read addresses (this lane, relative to a slot) ----------------------------
+  // this wave's keys start at row 32 * kh of the chunk (a multiple of 16 rows: the
+  // swizzles are unchanged)
+  uint32_t koff[4];
+#pragma unroll
+  for (int ds = 0; ds < 4; ++ds) koff[ds] = (uint32_t)(k_frag_off(lane, ds) + 32 * kh * kRowBytes);
+  // v_tr_off(lane, dt) = v_tr_off(lane, 0) + 32 * ((dt ^ vsw) - vsw) with vsw the
+  // row's v_unit term: the dim tile enters through v_unit's XOR only
+  const int vrow = 4 * grp + (ql >> 2);
+  const int vsw = vrow & 7;
+  const uint32_t vlane = (uint32_t)(v_tr_off(lane, 0) - 32 * vsw + 32 * kh * kRowBytes);
+
+  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+  sf_f32x4 acc[2][8];
+#pragma unroll
+  for (int qs = 0; qs < 2; ++qs)
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) acc[qs][dt] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int c, const uint8_t* slot) {
+    const sf_lds_off base = sf_lds_addr(slot);
+    sf_u32x4 kf[8];   // [t * 4 + ds]
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) {
+      kf[ds] = sf_lds_read16<0>(base + koff[ds]);
+      kf[4 + ds] = sf_lds_read16<16 * kRowBytes>(base + koff[ds]);
+    }
+    sf_lds_reads_done(kf);
+
+    // S^T tiles [t][qs] (raw dot products)
+    float s[2][2][4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int qs = 0; qs < 2; ++qs) {
+        sf_f32x4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ds = 0; ds < 4; ++ds)
+          a = sf_mfma16x16x32(sf_as_bf16x8(kf[t * 4 + ds]), sf_as_bf16x8(qf[qs][ds]), a);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[t][qs][i] = a[i];
       }
-    __syncthreads();
-    if (c + 1 < c1) {
-      load_chunk(c + 1, pg_next);
-      if (c + 2 < c1) {
+    const int kbase = c * kChunk + kh * 32 + grp * 4;  // key of s[0][.][0] of this lane
+    if (kbase + 16 + 3 >= P) {  // a partial last chunk: keys past the prefix
 #pragma unroll
-        for (int j = 0; j < 8; ++j) pg_next[j] = group_page(c + 2, j);
-      }
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int qs = 0; qs < 2; ++qs)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (kbase + 16 * t + i >= P) s[t][qs][i] = -INFINITY;
     }
 
-    // S^T = K Q^T (raw dot products) for the 8 slot tiles of the chunk
-    float s[8][4];
+    // online softmax per query (base 2, scores pre-scaled by log2(e) * scaling):
+    // the max over the 4 lane groups first (lane shuffles go through the LDS
+    // pipe), then the V^T operand reads, whose latency the exponentials cover
+    float m_use[2], alpha[2];
 #pragma unroll
-    for (int kt = 0; kt < 8; ++kt) {
-      sf_f32x4 a = {0.f, 0.f, 0.f, 0.f};
-      const uint16_t* kb = &sK[(kt * 16 + ql) * kKStr + grp * 8];
+    for (int qs = 0; qs < 2; ++qs) {
+      float mx = -INFINITY;
 #pragma unroll
-      for (int ds = 0; ds < 4; ++ds) {
-        const sf_u32x4 kf = *reinterpret_cast<const sf_u32x4*>(kb + ds * 32);
-        a = sf_mfma16x16x32(sf_as_bf16x8(kf), sf_as_bf16x8(qf[ds]), a);
-      }
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) s[kt][rr] = a[rr];
+        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[t][qs][i]);
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m_run[qs], mx * scale_log2);
+      // a key half with no key yet (only past a short prefix's end) stays empty
+      m_use[qs] = m_new == -INFINITY ? 0.f : m_new;
+      alpha[qs] = __builtin_amdgcn_exp2f(m_run[qs] - m_use[qs]);
+      m_run[qs] = m_new;
     }
-    if (nkeys < kChunk) {  // uniform: only a partial last chunk
+    sf_u32x2 vf[16];  // [dt * 2 + t]
 #pragma unroll
-      for (int kt = 0; kt < 8; ++kt)
+    for (int dt = 0; dt < 8; ++dt) {
+      const sf_lds_off va = base + vlane + (uint32_t)(((dt ^ vsw) & 7) * 32);
+      vf[2 * dt] = sf_lds_read8_tr<0>(va);
+      vf[2 * dt + 1] = sf_lds_read8_tr<16 * kRowBytes>(va);
+    }
+    float lsum[2] = {0.f, 0.f};
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
-          if (slot_key(kt * 16 + grp * 4 + rr) >= nkeys) s[kt][rr] = -INFINITY;
+    for (int qs = 0; qs < 2; ++qs) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          s[t][qs][i] = __builtin_amdgcn_exp2f(fmaf(s[t][qs][i], scale_log2, -m_use[qs]));
+          lsum[qs] += s[t][qs][i];
+        }
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) acc[qs][dt] = acc[qs][dt] * alpha[qs];
+    }
+    // the exponentials and rescales are done before the wait for the V^T reads
+    // (an empty asm that takes them in keeps the compiler from sinking them past it)
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sf_pin(s[t][qs][i]);
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) sf_pin(acc[qs][dt]);
+    }
+    sf_lds_reads_done(vf);
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) {
+      lsum[qs] += __shfl_xor(lsum[qs], 16, 64);
+      lsum[qs] += __shfl_xor(lsum[qs], 32, 64);
+      l_run[qs] = l_run[qs] * alpha[qs] + lsum[qs];
     }
 
-    // the 4 lane groups of a query hold its 128 keys; the max is taken on the raw
-    // dot products (the scale is positive) and probabilities are
-    // exp2(s * scale_log2 - m) with m in the scaled base-2 domain
-    float mx = -INFINITY;
+    // O^T += V^T P^T over the wave's 32 keys (smallest P part first)
+    sf_bf16x8 pb[2][kPParts];
 #pragma unroll
-    for (int kt = 0; kt < 8; ++kt)
+    for (int qs = 0; qs < 2; ++qs) {
+      float p2[2][4];
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) mx = fmaxf(mx, s[kt][rr]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx * scale_log2);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first chunk
-    float lsum = 0.f;
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int kt = 0; kt < 8; ++kt)
+        for (int i = 0; i < 4; ++i) p2[t][i] = s[t][qs][i];
+      pv_parts<kPParts>(p2, pb[qs]);
+    }
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        s[kt][rr] = __builtin_amdgcn_exp2f(fmaf(s[kt][rr], scale_log2, -m_new));
-        lsum += s[kt][rr];
-      }
-    lsum += __shfl_xor(lsum, 16, 64);
-    lsum += __shfl_xor(lsum, 32, 64);
-    l_run = l_run * alpha + lsum;
-    m_run = m_new;
+    for (int dt = 0; dt < 8; ++dt) {
+      const sf_u32x4 vw = {vf[2 * dt][0], vf[2 * dt][1], vf[2 * dt + 1][0], vf[2 * dt + 1][1]};
+      const sf_bf16x8 va = sf_as_bf16x8(vw);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = acc[i] * alpha;
+      for (int qs = 0; qs < 2; ++qs)
+#pragma unroll
+        for (int pp = kPParts - 1; pp >= 0; --pp)
+          acc[qs][dt] = sf_mfma16x16x32(va, pb[qs][pp], acc[qs][dt]);
+    }
+  };
 
-    // acc += V^T P^T; P split into three bf16 parts hi + mid + lo (24 bits: the
-    // products P*V are those of the reference's fp32 einsum)
+  // ---- the ring: chunk k of the range in slot k % kRing --------------------------------
+  const int nck = c1 - c0;
+#pragma unroll 1
+  for (int k = 0; k < nck; ++k) {
+    // chunk k has landed (each wave's copies complete in issue order), and every
+    // wave is done with the slot the next issue overwrites (chunk k - 1's)
+    sf_wait_vm_barrier<(kRing - 2) * kCopiesPerChunk>();
+    issue(c0 + k + kRing - 1, ring + ((k + kRing - 1) % kRing) * kSlotBytes);
+    compute(c0 + k, ring + (k % kRing) * kSlotBytes);
+  }
+  // drain the clamped re-issues past the range end before the ring is reused
+  sf_wait_vm_barrier<0>();
+
+  // ---- combine the two key halves of each query, write the partial -----------------
+  float* xo = reinterpret_cast<float*>(ring);            // [qg][qs][dt][lane] x 4
+  float* xml = xo + 4 * 2 * 8 * 64 * 4;                   // [qg][qs][ql] x (m, l)
+  if (kh == 1) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int kt0 = 2 * j, kt1 = 2 * j + 1;
-      sf_u32x4 hi, mid, lo;
+    for (int qs = 0; qs < 2; ++qs) {
 #pragma unroll
-      for (int w2 = 0; w2 < 2; ++w2) {
+      for (int dt = 0; dt < 8; ++dt)
+        *reinterpret_cast<sf_f32x4*>(xo + (((qg * 2 + qs) * 8 + dt) * 64 + lane) * 4) = acc[qs][dt];
+      if (grp == 0) {
+        xml[((qg * 2 + qs) * 16 + ql) * 2] = m_run[qs];
+        xml[((qg * 2 + qs) * 16 + ql) * 2 + 1] = l_run[qs];
+      }
+    }
+  }
+  __syncthreads();
+  if (kh == 0) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const int kt = t ? kt1 : kt0;
-          const float a0 = s[kt][2 * w2], a1 = s[kt][2 * w2 + 1];
-          const float r0 = a0 - sf_rbf(a0), r1 = a1 - sf_rbf(a1);
-          hi[2 * t + w2] = sf_pack2(a0, a1);
-          mid[2 * t + w2] = sf_pack2(r0, r1);
-          lo[2 * t + w2] = sf_pack2(r0 - sf_rbf(r0), r1 - sf_rbf(r1));
+    for (int qs = 0; qs < 2; ++qs) {
+      const int qi = qt * kQT + qg * 32 + qs * 16 + ql;
+      const float m1 = xml[((qg * 2 + qs) * 16 + ql) * 2];
+      const float l1 = xml[((qg * 2 + qs) * 16 + ql) * 2 + 1];
+      const float mm = fmaxf(m_run[qs], m1);  // finite: half 0 holds the range's first key
+      const float w0 = __builtin_amdgcn_exp2f(m_run[qs] - mm);
+      const float w1 = __builtin_amdgcn_exp2f(m1 - mm);
+      if (qi < nq) {
+        const size_t slot = attn_slot(h, r, qi, nr_cap, qmax);
+        if (grp == 0) {
+          ws_ml[slot * 2] = mm;
+          ws_ml[slot * 2 + 1] = l_run[qs] * w0 + l1 * w1;
+        }
+        float* op = ws_o + slot * kHD + grp * 4;
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+          const sf_f32x4 a1 =
+              *reinterpret_cast<const sf_f32x4*>(xo + (((qg * 2 + qs) * 8 + dt) * 64 + lane) * 4);
+          *reinterpret_cast<sf_f32x4*>(op + dt * 16) = acc[qs][dt] * w0 + a1 * w1;
         }
       }
-      const sf_bf16x8 bhi = sf_as_bf16x8(hi);
-      const sf_bf16x8 bmid = sf_as_bf16x8(mid);
-      const sf_bf16x8 blo = sf_as_bf16x8(lo);
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const int d = dt * 16 + ql;
-        const uint16_t* vrow = &sV[d * kVStr];
-        const int sw = vt_swz(d);
-        const sf_u32x2 a0 = *reinterpret_cast<const sf_u32x2*>(vrow + ((4 * kt0 + grp) ^ sw) * 4);
-        const sf_u32x2 a1 = *reinterpret_cast<const sf_u32x2*>(vrow + ((4 * kt1 + grp) ^ sw) * 4);
-        const sf_u32x4 vf = {a0[0], a0[1], a1[0], a1[1]};
-        const sf_bf16x8 va = sf_as_bf16x8(vf);
-        acc[dt] = sf_mfma16x16x32(va, blo, acc[dt]);
-        acc[dt] = sf_mfma16x16x32(va, bmid, acc[dt]);
-        acc[dt] = sf_mfma16x16x32(va, bhi, acc[dt]);
-      }
     }
-    __syncthreads();  // sK / sV are rewritten by the next chunk
-  }
-
-  if (qvalid) {
-    const size_t slot = attn_slot(h, r, qi, nch_cap, qmax);
-    if (grp == 0) {
-      ws_ml[slot * 2] = m_run;
-      ws_ml[slot * 2 + 1] = l_run;
-    }
-    float* op = ws_o + slot * kHD + grp * 4;
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<sf_f32x4*>(op + dt * 16) = acc[dt];
   }
 }
 
 // gridDim.x is a multiple of 8; XCD x (workgroups b with b % 8 == x) takes the
 // x-th eighth of the item list, so consecutive items (the query tiles of one
 // chunk range) share an L2.
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+__global__ __launch_bounds__(kPrefixThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 sf_attn_prefix_kernel(
     const uint16_t* __restrict__ q_buf, const uint16_t* __restrict__ pk,
     const uint16_t* __restrict__ pv, const int32_t* __restrict__ page_table, int page_size,
     long long page_stride, long long head_stride, const int32_t* __restrict__ p_len, int P_cap,
     const int32_t* __restrict__ rows, const int32_t* __restrict__ count_p, int bucket, int H,
-    int Hkv, float scale_log2, int qmax, int nch_cap, float* __restrict__ ws_o,
+    int Hkv, float scale_log2, int qmax, int nr_cap, float* __restrict__ ws_o,
     float* __restrict__ ws_ml) {
-  __shared__ __attribute__((aligned(16))) uint16_t sK[kChunk * kKStr];
-  __shared__ __attribute__((aligned(16))) uint16_t sV[kHD * kVStr];
+  __shared__ __attribute__((aligned(16))) uint8_t ring[kRing * kSlotBytes];
+  __shared__ int s_pg[4 * kMaxChunks];  // page of each 16-key group of the item's range
   const int G = H / Hkv;
   const int P = p_len ? min(*p_len, P_cap) : P_cap;
   if (P <= 0) return;
   const int nq = min(*count_p, bucket) * G;
   const PrefixGrid pg = prefix_grid(P, nq, Hkv);
-  const int n_qt = pg.n_qt;
-  const int nch = pg.nch;
-  const int cpi = pg.cpi;
-  const int nr = pg.nr;
-  const int items = n_qt * nr * Hkv;
+  const int items = pg.n_qt * pg.nr * Hkv;
   const int xcd = blockIdx.x & 7;
   const int per = gridDim.x >> 3;
   const int end = xcd_begin(items, xcd + 1);
   for (int it = xcd_begin(items, xcd) + (int)(blockIdx.x >> 3); it < end; it += per) {
-    const AttnItem item = attn_item(it, n_qt, nr);
-    const int c0 = item.r * cpi;
+    const AttnItem item = attn_item(it, pg.n_qt, pg.nr);
+    const int c0 = item.r * pg.cpi;
     prefix_item(q_buf, pk, pv, page_table, page_size, page_stride, head_stride, P, rows, nq, G, H,
-                scale_log2, qmax, nch_cap, item.qt, item.r, c0, min(nch, c0 + cpi), item.h, sK, sV,
-                ws_o, ws_ml);
+                scale_log2, qmax, nr_cap, item.qt, item.r, c0, min(pg.nch, c0 + pg.cpi), item.h,
+                ring, s_pg, ws_o, ws_ml);
     __syncthreads();  // LDS is reused by the next item
   }
 }
@@ -315,7 +424,7 @@ SF_DEV void merge_item(const uint16_t* __restrict__ q_buf, const uint16_t* __res
                        const float* __restrict__ ws_ml, float* __restrict__ o32,
                        uint16_t* __restrict__ o_bf, float* __restrict__ m_tab,
                        float* __restrict__ z_tab, float (*sq)[kHD], uint16_t (*sk)[kHD],
-                       uint16_t (*sv)[kHD], float (*ss)[kMaxN], float (*sml)[2 * kMaxChunks],
+                       uint16_t (*sv)[kHD], float (*ss)[kMaxN], float (*sml)[2 * kMaxRanges],
                        float* sM, float* sZ) {
   const int tid = threadIdx.x;
   const int my_g = tid >> 6, dp = (tid & 63) * 2;
@@ -454,13 +563,13 @@ __global__ __launch_bounds__(512) void sf_attn_block_merge_kernel(
   __shared__ __attribute__((aligned(16))) uint16_t sk[kMaxN][kHD];
   __shared__ __attribute__((aligned(16))) uint16_t sv[kMaxN][kHD];
   __shared__ float ss[kMaxG][kMaxN];
-  __shared__ float sml[kMaxG][2 * kMaxChunks];   // per q-head: (m, l) of every chunk
+  __shared__ float sml[kMaxG][2 * kMaxRanges];   // per q-head: (m, l) of every range
   __shared__ float sM[kMaxG], sZ[kMaxG];
   const int count = min(*count_p, bucket);
   const int G = H / Hkv;
   const int P = p_len ? min(*p_len, P_cap) : P_cap;
   // number of prefix partials per query: the prefix kernel's chunk ranges
-  const int nch = merge_ranges(P, count * G, Hkv, nchunks_cap);
+  const int nch = merge_ranges(P, count * G, Hkv);
   for (int it = blockIdx.x; it < count * Hkv; it += gridDim.x) {
     merge_item(q_buf, kv_buf, src, rows, it / Hkv, it % Hkv, N, H, Hkv, G, scale_log2, causal, nch,
                nchunks_cap, qmax, ws_o, ws_ml, o32, o_bf, m_tab, z_tab, sq, sk, sv, ss, sml, sM,
@@ -474,9 +583,9 @@ __global__ __launch_bounds__(512) void sf_attn_block_merge_kernel(
 extern "C" size_t sf_attn_workspace_bytes(int bucket, int H, int P) {
   if (bucket < 1 || H < 1 || P < 0) return 0;
   if (P == 0) return 16;
-  // per (kv head, chunk, query): 128 fp32 acc + (m, l); queries per kv head = bucket*G,
-  // so the total over kv heads is nchunks * bucket * H slots.
-  return (size_t)nchunks_for(P) * bucket * H * (kHD + 2) * sizeof(float);
+  // per (kv head, chunk range, query): 128 fp32 acc + (m, l); queries per kv head =
+  // bucket*G, so the total over kv heads is ranges * bucket * H slots.
+  return (size_t)ranges_cap(P) * bucket * H * (kHD + 2) * sizeof(float);
 }
 
 extern "C" int sf_attn_prefix_block(const uint16_t* q_buf, const uint16_t* kv_buf,
@@ -496,8 +605,9 @@ extern "C" int sf_attn_prefix_block(const uint16_t* q_buf, const uint16_t* kv_bu
   if (P < 0 || nchunks_for(P) > kMaxChunks) return SF_ERR_SHAPE;
   if (P > 0) {
     if (!prefix_k || !prefix_v || !workspace) return SF_ERR_ARG;
-    // a page holds whole 16-key groups and a chunk whole pages: 16, 32, 64 or 128
-    if (page_table && (page_size < 16 || kChunk % page_size != 0)) return SF_ERR_SHAPE;
+    // a page holds whole 16-key groups: 16, 32, 64 or 128 keys
+    if (page_table && (page_size < 16 || page_size > 128 || (page_size & (page_size - 1))))
+      return SF_ERR_SHAPE;
     if (!page_table && head_stride < (long long)P * kHD) return SF_ERR_SHAPE;
     if (workspace_bytes < sf_attn_workspace_bytes(bucket, H, P)) return SF_ERR_WORKSPACE;
   }
@@ -505,23 +615,25 @@ extern "C" int sf_attn_prefix_block(const uint16_t* q_buf, const uint16_t* kv_bu
   const int G = H / Hkv;
   const int qmax = bucket * G;
   const int nch = P > 0 ? nchunks_for(P) : 0;
+  const int nr_cap = P > 0 ? ranges_cap(P) : 0;
   const float scale_log2 = scaling * 1.44269504088896340736f;
   float* ws_ml = nullptr;
   float* ws_o = nullptr;
   if (P > 0) {
-    const size_t nslot = (size_t)nch * qmax * Hkv;
+    const size_t nslot = (size_t)nr_cap * qmax * Hkv;
     ws_o = reinterpret_cast<float*>(workspace);
     ws_ml = ws_o + nslot * kHD;
-    // persistent grid: at most two 70 KB-LDS workgroups fit a CU; a multiple of 8
+    // persistent grid: one 128 KB-LDS workgroup per CU; a multiple of 8
     const int grid = prefix_launch_grid(qmax, nch, Hkv);
-    hipLaunchKernelGGL(sf_attn_prefix_kernel, dim3(grid), dim3(256), 0, st, q_buf, prefix_k,
-                       prefix_v, page_table, page_size, page_stride, head_stride, prefix_len, P,
-                       rows, count, bucket, H, Hkv, scale_log2, qmax, nch, ws_o, ws_ml);
+    hipLaunchKernelGGL(sf_attn_prefix_kernel, dim3(grid), dim3(kPrefixThreads), 0, st, q_buf,
+                       prefix_k, prefix_v, page_table, page_size, page_stride, head_stride,
+                       prefix_len, P, rows, count, bucket, H, Hkv, scale_log2, qmax, nr_cap, ws_o,
+                       ws_ml);
   }
   const int grid2 = min(bucket * Hkv, 2 * kCUs);
   hipLaunchKernelGGL(sf_attn_block_merge_kernel, dim3(grid2), dim3(512), 0, st, q_buf, kv_buf,
                      src, rows, count, bucket, N, H, Hkv, scale_log2, block_causal ? 1 : 0,
                      P > 0 ? prefix_len : nullptr,
-                     P, nch, qmax, ws_o, ws_ml, o32, o_bf, m_tab, z_tab);
+                     P, nr_cap, qmax, ws_o, ws_ml, o32, o_bf, m_tab, z_tab);
   return sf_launch_status();
 }

@@ -115,6 +115,41 @@ SF_DEV void sf_lds_reads_done(sf_u32x4 (&v)[N]) {
 #pragma unroll
   for (int i = 0; i < N; ++i) asm volatile("" : "+v"(v[i]));
 }
+// Transposing LDS read (ds_read_b64_tr_b16), untracked like sf_lds_read16: within
+// each group of 16 lanes, lane i receives the 4 16-bit elements
+//   out[i][k] = (8 bytes at the address of lane 4k + i/4)[i % 4],   k = 0..3,
+// i.e. if lane L of the group points at 4 consecutive elements of row L/4,
+// starting at column 4(L%4), lane i gets column i of rows 0..3: a 4x16 block
+// read column-wise (layout checked on gfx950).
+template <int OFF>
+SF_DEV sf_u32x2 sf_lds_read8_tr(sf_lds_off addr) {
+  sf_u32x2 v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+  return v;
+}
+template <int N>
+SF_DEV void sf_lds_reads_done(sf_u32x2 (&v)[N]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+v"(v[i]));
+}
+// One 32-bit LDS read, completed before the function returns (untracked by the
+// compiler like sf_lds_read16; for tables read between direct copies).
+SF_DEV uint32_t sf_lds_read4_now(sf_lds_off addr) {
+  uint32_t v;
+  asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
+  return v;
+}
+
+// Scheduling pins: sf_pin(x) makes x an input and output of an empty volatile asm,
+// so whatever computes x stays before the next volatile asm (such as a wait) and
+// whatever uses x stays after it.  sf_wait_vm_loads() waits for every vector
+// memory load of the wave (s_waitcnt vmcnt(0)).
+template <typename T>
+SF_DEV void sf_pin(T& x) {
+  asm volatile("" : "+v"(x));
+}
+SF_DEV void sf_wait_vm_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 SF_DEV sf_lds_off sf_lds_addr(const void* p) {
   return (sf_lds_off)(uintptr_t)(const sf_lds_void*)p;
 }

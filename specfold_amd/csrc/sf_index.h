@@ -128,33 +128,64 @@ inline size_t part_bytes(const Plan& p, int mcap, int N) {
 namespace sfa {
 
 constexpr int kHD = 128;
-constexpr int kQT = 64;      // queries per work item
-constexpr int kChunk = 128;  // prefix keys per chunk
-constexpr int kMaxChunks = 256;   // prefix <= 32768 keys
+constexpr int kQT = 128;       // queries per work item: 4 query groups of 32
+constexpr int kChunk = 64;     // prefix keys per chunk (one LDS ring stage)
+constexpr int kMaxChunks = 512;   // prefix <= 32768 keys
+constexpr int kMaxRanges = 64;    // prefix partials per query at most
+#ifndef SFA_ITEMS_TARGET
+#define SFA_ITEMS_TARGET 256
+#endif
+constexpr int kItemsTarget = SFA_ITEMS_TARGET;
 
-// V^T tile swizzle: keys of dim row d are stored in 4-key (8-byte) units, unit u
-// at position u ^ vt_swz(d).
-SF_IDX int vt_swz(int d) { return (d >> 3) & 14; }
+// LDS layout of a staged chunk: key rows of 256 bytes (16 units of 16 bytes =
+// 8 dims each), K rows then V rows.  Unit u of key row r sits at unit
+//  k_unit(r, u) = u ^ (r & 15)      in K: the 16 consecutive rows one MFMA
+//                                   operand read takes at one unit hit 16
+//                                   distinct units;
+//  v_unit(r, u) = u ^ 2 * (r & 7)   in V: a transposing read takes 16
+//                                   consecutive rows x one aligned unit pair;
+//                                   rows 0-7 land on 8 distinct pairs, rows 8-15
+//                                   on the same 8 (the read's second pass).
+// Both are involutions, so the copy that fills physical unit p of row r reads
+// logical unit k_unit(r, p) / v_unit(r, p).
+SF_IDX int k_unit(int r, int u) { return u ^ (r & 15); }
+SF_IDX int v_unit(int r, int u) { return u ^ (2 * (r & 7)); }
+constexpr int kRowBytes = kHD * 2;               // one key row in LDS
+constexpr int kHalfBytes = kChunk * kRowBytes;   // the K (or V) rows of a chunk
 
-// Prefix chunks per work item: one while the one-chunk items fill about two
-// rounds of the resident grid, longer ranges beyond.  A pure function of
-// device-side sizes, evaluated identically by the prefix and merge kernels.
-constexpr int kItemsTarget = 1024;
-SF_IDX int prefix_cpi(int nch, int n_qt, int Hkv) {
-  return sf_imax(1, sf_imin(nch, (nch * n_qt * Hkv) / kItemsTarget));
+// Operand reads of a staged chunk, byte offsets from the chunk's K rows:
+// * K fragment of MFMA A = K (16 keys of tile 0 x 32 dims ds*32..): lane l reads
+//   key row l%16, logical unit ds*4 + l/16 (16 bytes); tile t adds 16 rows.
+SF_IDX int k_frag_off(int lane, int ds) {
+  const int row = lane & 15;
+  return row * kRowBytes + k_unit(row, ds * 4 + (lane >> 4)) * 16;
+}
+// * V^T fragment of MFMA A = V^T (16 dims dt*16.. x 32 keys) by two transposing
+//   reads (keys 4g..4g+3 of tiles 0 and 1, g = l/16): lane L of group g points at
+//   row 4g + L/4, dims dt*16 + 4(L%4) .. +4 (8 bytes); tile 1 adds 16 rows.
+SF_IDX int v_tr_off(int lane, int dt) {
+  const int L = lane & 15;
+  const int row = 4 * (lane >> 4) + (L >> 2);
+  const int col = dt * 16 + 4 * (L & 3);  // first dim
+  return kHalfBytes + row * kRowBytes + v_unit(row, col >> 3) * 16 + (col & 7) * 2;
 }
 
-// Keys of a chunk are held in a permuted slot order: load j (0..7) of thread row
-// r = tid / 16 brings key 16j + r, which occupies slot key_slot(j, r); slot_key
-// is the inverse (the key behind a slot, for the mask of a partial chunk).
-SF_IDX int key_slot(int j, int r) { return 64 * (j >> 2) + 4 * r + (j & 3); }
-SF_IDX int slot_key(int slot) { return 64 * (slot >> 6) + 16 * (slot & 3) + ((slot >> 2) & 15); }
+// Chunks per work item: enough that the items fill about one round of the
+// resident grid (longer ranges write fewer partials) and no query has more
+// than kMaxRanges partials.  A pure function of device-side sizes, evaluated
+// identically by the prefix and merge kernels.
+SF_IDX int prefix_cpi(int nch, int n_qt, int Hkv) {
+  const long long work = (long long)nch * n_qt * Hkv;
+  int c = (int)((work + kItemsTarget - 1) / kItemsTarget);
+  c = sf_imax(c, (nch + kMaxRanges - 1) / kMaxRanges);
+  return sf_imax(1, sf_imin(c, nch));
+}
 
-// 16-key group j of chunk ci starts at key chunk_group_g0 (groups past the
-// prefix end are clamped to the last group holding keys, last_group_g0(P));
-// thread row kr of the group reads key g0 + group_key(kr, g0, P) (keys past the
-// end clamped to the last key).  With a page size that is a multiple of 16 a
-// group never straddles pages.
+// 16-key group j (0..3) of chunk ci starts at key chunk_group_g0 (groups past
+// the prefix end are clamped to the last group holding keys, last_group_g0(P));
+// row kr of the group holds key g0 + group_key(kr, g0, P) (keys past the end
+// clamped to the last key).  With a page size that is a multiple of 16 a group
+// never straddles pages.
 SF_IDX int last_group_g0(int P) { return (P - 1) & ~15; }
 SF_IDX int chunk_group_g0(int ci, int j, int last_g0) {
   return sf_imin(ci * kChunk + 16 * j, last_g0);
@@ -165,7 +196,8 @@ SF_IDX int group_key(int kr, int g0, int P) { return sf_imin(kr, P - 1 - g0); }
 // b % 8): XCD x walks items [xcd_begin(items, x), xcd_begin(items, x + 1)).
 SF_IDX int xcd_begin(int items, int xcd) { return (int)(((long long)items * xcd) >> 3); }
 
-// Item it of the prefix pass: query tile qt, chunk range r, kv head h.
+// Item it of the prefix pass: query tile qt, chunk range r, kv head h (the
+// query tiles of one (range, head) are consecutive: one XCD, one L2).
 struct AttnItem {
   int qt, r, h;
 };
@@ -189,28 +221,28 @@ SF_IDX PrefixGrid prefix_grid(int P, int nq, int Hkv) {
 }
 // ... and the partials per query as the merge kernel derives them from its
 // query count nq = rows · G.
-SF_IDX int merge_ranges(int P, int nq, int Hkv, int nchunks_cap) {
-  const int nch_all = sf_imin((P + kChunk - 1) / kChunk, nchunks_cap);
-  const int n_qt = (nq + kQT - 1) / kQT;
-  const int cpi = nch_all > 0 ? prefix_cpi(nch_all, n_qt, Hkv) : 1;
-  return (nch_all + cpi - 1) / cpi;
-}
-
-// Partial slot of query qi of range r, kv head h: the workspace holds
-// [Hkv][nch_cap][qmax] slots of kHD fp32 (acc), then the same count of (m, l).
-SF_IDX size_t attn_slot(int h, int r, int qi, int nch_cap, int qmax) {
-  return ((size_t)h * nch_cap + r) * qmax + qi;
+SF_IDX int merge_ranges(int P, int nq, int Hkv) {
+  return P > 0 ? prefix_grid(P, nq, Hkv).nr : 0;
 }
 
 inline int nchunks_for(int P) { return (P + kChunk - 1) / kChunk; }
+// Range slots the workspace holds per (kv head, query) for a prefix capacity P.
+inline int ranges_cap(int P) { return nchunks_for(P) < kMaxRanges ? nchunks_for(P) : kMaxRanges; }
 
-// Persistent prefix grid for a capacity of qmax queries per kv head and nch
-// chunks: enough workgroups for every item, at most two per CU (256 CUs), a
-// multiple of 8.
+// Partial slot of query qi of range r, kv head h: the workspace holds
+// [Hkv][nr_cap][qmax] slots of kHD fp32 (acc), then the same count of (m, l).
+SF_IDX size_t attn_slot(int h, int r, int qi, int nr_cap, int qmax) {
+  return ((size_t)h * nr_cap + r) * qmax + qi;
+}
+
+// Persistent prefix grid for a capacity of qmax queries per kv head and a prefix
+// capacity of nch chunks: enough workgroups for every item, at most one per CU
+// (256 CUs), a multiple of 8.
 inline int prefix_launch_grid(int qmax, int nch, int Hkv) {
-  const int items_cap = ((qmax + kQT - 1) / kQT) * nch * Hkv;
-  const int g = ((items_cap + 7) / 8) * 8;
-  return g < 512 ? g : 512;
+  const int nr = nch < kMaxRanges ? nch : kMaxRanges;
+  const long long items_cap = (long long)((qmax + kQT - 1) / kQT) * nr * Hkv;
+  const long long g = ((items_cap + 7) / 8) * 8;
+  return g < 256 ? (int)g : 256;
 }
 
 }  // namespace sfa

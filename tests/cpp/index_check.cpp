@@ -11,10 +11,13 @@
 //     contributor; output columns of each mode inside N and covering each tile
 //     once; every packed-weight load inside the N·K weights, and the fragment it
 //     reads (under the packed layout) belonging to the column the lane writes;
-//   * prefix attention: the key-slot permutation and its inverse, the V^T unit
-//     layout, the page-group addressing (every load inside the prefix and inside
-//     its page; every real key loaded exactly once; masked slots are exactly the
-//     clamped loads), the persistent grid's item walk (each item once), the chunk
+//   * prefix attention: a staged chunk's LDS layout (the copies fill every cell
+//     once; the K fragment and transposing V^T reads, emulated element by
+//     element, deliver the operands the MFMAs expect; K reads bank-conflict free
+//     per quarter-wave, V^T reads on distinct 32-byte pairs per 8 rows), the
+//     page-group addressing (every load inside the prefix and inside its page;
+//     every real key loaded exactly once; masked rows are exactly the clamped
+//     loads), the persistent grid's item walk (each item once), the chunk
 //     ranges (a partition of the chunks), and the partial slots (inside the
 //     library's workspace; the merge reads exactly the slots the prefix pass
 //     wrote, with the same range count).
@@ -230,45 +233,93 @@ static void check_gemm_columns() {
 // ---------------------------------------------------------------------------
 // Prefix attention
 // ---------------------------------------------------------------------------
-static void check_slots_and_vt() {
-  std::vector<int> used(128, 0);
-  for (int j = 0; j < 8; ++j)
-    for (int kr = 0; kr < 16; ++kr) {
-      const int s = sfa::key_slot(j, kr);
-      CHECK(s >= 0 && s < 128, "slot range");
-      ++used[s];
-      CHECK(sfa::slot_key(s) == 16 * j + kr, "slot_key(key_slot(%d, %d))", j, kr);
+// The LDS data path of one staged chunk: the copies (wave w fills rows 16(w&3)..
+// of K for w < 4, of V for w >= 4; lane L of copy i writes 16 bytes at row
+// 16(w&3) + 4i + L/16, physical unit L%16, reading logical unit k_unit / v_unit),
+// then the K fragment reads and the transposing V^T reads of every wave,
+// emulated element by element (the transposing read's layout: lane i of a
+// 16-lane group gets element i%4 of the 8 bytes lane 4k + i/4 points at, k = 0..3).
+static void check_lds_paths() {
+  const int R = sfa::kChunk, D = sfa::kHD;
+  auto logical = [&](int v, int row, int dim) { return (v ? 100000 : 0) + row * 1000 + dim; };
+  std::vector<int> lds(2 * R * D, -1);  // element-granular model of the K then V rows
+  for (int w = 0; w < 8; ++w)
+    for (int i = 0; i < 4; ++i)
+      for (int lane = 0; lane < 64; ++lane) {
+        const int jg = w & 3, v = w >= 4;
+        const int row = 16 * jg + 4 * i + lane / 16, p = lane & 15;
+        const int u = v ? sfa::v_unit(row, p) : sfa::k_unit(row, p);
+        CHECK((v ? sfa::v_unit(row, u) : sfa::k_unit(row, u)) == p, "unit map not an involution");
+        for (int e = 0; e < 8; ++e) {
+          int& cell = lds[(v * R + row) * D + p * 8 + e];
+          CHECK(cell == -1, "LDS cell written twice");
+          cell = logical(v, row, u * 8 + e);
+        }
+      }
+  for (int c : lds) CHECK(c != -1, "LDS cell never written");
+  auto at_byte = [&](int byte) {
+    CHECK(byte >= 0 && byte % 2 == 0 && byte < 2 * sfa::kHalfBytes, "LDS byte %d", byte);
+    return lds[byte / 2];
+  };
+  for (int kh = 0; kh < 2; ++kh)
+    for (int t = 0; t < 2; ++t) {
+      const int rows0 = 32 * kh + 16 * t;  // first key row of the 16-key tile
+      for (int ds = 0; ds < 4; ++ds) {
+        std::vector<int> units(64);
+        for (int lane = 0; lane < 64; ++lane) {
+          const int off = sfa::k_frag_off(lane, ds) + rows0 * sfa::kRowBytes;
+          CHECK(off % 16 == 0, "K read alignment");
+          units[lane] = (off % sfa::kRowBytes) / 16;
+          for (int e = 0; e < 8; ++e)
+            CHECK(at_byte(off + 2 * e) == logical(0, rows0 + lane % 16, ds * 32 + 8 * (lane / 16) + e),
+                  "K fragment (kh=%d t=%d ds=%d lane=%d)", kh, t, ds, lane);
+        }
+        // 16 lanes of a quarter-wave read 16 distinct 16-byte units: no bank conflict
+        for (int g = 0; g < 4; ++g) {
+          std::vector<int> seen(16, 0);
+          for (int i = 0; i < 16; ++i) ++seen[units[16 * g + i]];
+          for (int u = 0; u < 16; ++u) CHECK(seen[u] == 1, "K read conflict");
+        }
+      }
+      for (int dt = 0; dt < 8; ++dt) {
+        std::vector<int> off(64);
+        for (int lane = 0; lane < 64; ++lane) {
+          off[lane] = sfa::v_tr_off(lane, dt) + rows0 * sfa::kRowBytes;
+          CHECK(off[lane] % 8 == 0, "V^T read alignment");
+        }
+        for (int lane = 0; lane < 64; ++lane) {
+          const int grp = lane / 16, i = lane % 16;
+          for (int k = 0; k < 4; ++k) {
+            const int srcl = 16 * grp + 4 * k + i / 4;
+            const int got = at_byte(off[srcl] + 2 * (i % 4));
+            // MFMA A operand element (dim row i, key 8*grp + k of the 32-key block):
+            // key 4*grp + k of the tile
+            CHECK(got == logical(1, rows0 + 4 * grp + k, dt * 16 + i),
+                  "V^T fragment (kh=%d t=%d dt=%d lane=%d k=%d)", kh, t, dt, lane, k);
+          }
+        }
+        // the 64 lanes' 8-byte pieces: 16 rows x 32 bytes; rows 0-7 of the tile on
+        // 8 distinct aligned 32-byte pairs, rows 8-15 on the same 8 pairs
+        std::vector<int> pairs(16, 0);
+        for (int lane = 0; lane < 64; ++lane) {
+          const int b = off[lane] - sfa::kHalfBytes - rows0 * sfa::kRowBytes;
+          const int row = b / sfa::kRowBytes;
+          if ((lane & 3) == 0) ++pairs[((b % sfa::kRowBytes) / 32) + 8 * (row >= 8)];
+        }
+        for (int q = 0; q < 16; ++q) CHECK(pairs[q] == 1, "V^T read pair %d used %d times", q, pairs[q]);
+      }
     }
-  for (int s = 0; s < 128; ++s) CHECK(used[s] == 1, "slot %d used %d times", s, used[s]);
-  // a thread's 4 transposed keys (loads 4p..4p+3 of row kr) are V^T unit 16p + kr
-  for (int p = 0; p < 2; ++p)
-    for (int kr = 0; kr < 16; ++kr)
-      for (int i = 0; i < 4; ++i)
-        CHECK(sfa::key_slot(4 * p + i, kr) == 4 * (16 * p + kr) + i, "V^T unit of row %d", kr);
-  // per V^T row the swizzle permutes the 32 units and stays inside the 128 keys
-  for (int d = 0; d < sfa::kHD; ++d) {
-    std::vector<int> pos(32, 0);
-    for (int u = 0; u < 32; ++u) {
-      const int q = u ^ sfa::vt_swz(d);
-      CHECK(q >= 0 && q < 32, "swizzled unit");
-      ++pos[q];
-    }
-    for (int q = 0; q < 32; ++q) CHECK(pos[q] == 1, "swizzle not a permutation");
-    // one P.V read instruction touches rows d0..d0+15 with the same swizzle
-    CHECK(sfa::vt_swz(d) == sfa::vt_swz(d & ~15), "swizzle constant over 16 rows");
-  }
-  printf("key slots and V^T layout: ok\n");
+  printf("chunk LDS layout, K and V^T operand reads: ok\n");
 }
 
-// Loads of chunk ci for prefix length P and page size ps (ps = 0: contiguous).
+// Copies of chunk ci for prefix length P and page size ps (ps = 0: contiguous).
 static void check_chunk_loads(int P, int ps) {
   const int nch = sfa::nchunks_for(P);
   const int last_g0 = sfa::last_group_g0(P);
   const int npages = ps ? (P + ps - 1) / ps : 0;
   std::vector<unsigned char> loaded(P, 0);
   for (int ci = 0; ci < nch; ++ci) {
-    const int nkeys = P - ci * sfa::kChunk < sfa::kChunk ? P - ci * sfa::kChunk : sfa::kChunk;
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < 4; ++j) {
       const int g0 = sfa::chunk_group_g0(ci, j, last_g0);
       CHECK(g0 >= 0 && g0 % 16 == 0 && g0 < P, "group start %d (P=%d)", g0, P);
       if (ps) CHECK(g0 / ps < npages, "page index %d of %d", g0 / ps, npages);
@@ -280,15 +331,14 @@ static void check_chunk_loads(int P, int ps) {
           CHECK((g0 & (ps - 1)) + kk < ps, "row %d past page of %d", (g0 & (ps - 1)) + kk, ps);
           CHECK(key / ps == g0 / ps, "group straddles pages");
         }
-        const int slot = sfa::key_slot(j, kr);
-        const bool masked = sfa::slot_key(slot) >= nkeys;
-        if (!masked) {
-          // an unmasked slot holds its own key, loaded once over the whole prefix
-          CHECK(key == ci * sfa::kChunk + sfa::slot_key(slot), "slot holds key %d", key);
+        // row 16j + kr of the chunk: the key the kernel's mask takes it for
+        const int want = ci * sfa::kChunk + 16 * j + kr;
+        if (want < P) {
+          CHECK(key == want, "row holds key %d, not %d", key, want);
           CHECK(!loaded[key], "key %d loaded twice", key);
           loaded[key] = 1;
         } else {
-          CHECK(ci == nch - 1, "masked slot outside the last chunk");
+          CHECK(ci == nch - 1, "masked row outside the last chunk");
         }
       }
     }
@@ -314,12 +364,13 @@ static void check_page_addressing() {
 static void check_decomposition(int P, int P_cap, int count, int bucket, int G, int Hkv) {
   const int qmax = bucket * G;
   const int nch_cap = sfa::nchunks_for(P_cap);
+  const int nr_cap = sfa::ranges_cap(P_cap);
   const int nq = count * G;
   const sfa::PrefixGrid pg = sfa::prefix_grid(P, nq, Hkv);
-  const int nr_merge = sfa::merge_ranges(P, nq, Hkv, nch_cap);
+  const int nr_merge = sfa::merge_ranges(P, nq, Hkv);
   CHECK(pg.nr == nr_merge, "ranges: prefix %d merge %d (P=%d nq=%d Hkv=%d)", pg.nr, nr_merge, P,
         nq, Hkv);
-  CHECK(nr_merge <= sfa::kMaxChunks, "merge LDS table");
+  CHECK(nr_merge <= nr_cap && nr_cap <= sfa::kMaxRanges, "ranges %d > slots %d", nr_merge, nr_cap);
   // the ranges partition the chunks
   int next = 0;
   for (int r = 0; r < pg.nr; ++r) {
@@ -331,10 +382,10 @@ static void check_decomposition(int P, int P_cap, int count, int bucket, int G, 
   CHECK(next == pg.nch, "ranges end at %d of %d chunks", next, pg.nch);
   // the grid the host launches for the capacity walks every item once
   const int grid = sfa::prefix_launch_grid(qmax, nch_cap, Hkv);
-  CHECK(grid >= 8 && grid % 8 == 0 && grid <= 512, "grid %d", grid);
+  CHECK(grid >= 8 && grid % 8 == 0 && grid <= 256, "grid %d", grid);
   const int items = pg.n_qt * pg.nr * Hkv;
   std::vector<unsigned char> item_seen(items, 0);
-  const size_t nslot = (size_t)nch_cap * qmax * Hkv;
+  const size_t nslot = (size_t)nr_cap * qmax * Hkv;
   std::vector<unsigned char> written(nslot, 0);
   size_t n_written = 0;
   for (int b = 0; b < grid; ++b) {
@@ -346,7 +397,7 @@ static void check_decomposition(int P, int P_cap, int count, int bucket, int G, 
       const sfa::AttnItem a = sfa::attn_item(it, pg.n_qt, pg.nr);
       CHECK(a.qt < pg.n_qt && a.r < pg.nr && a.h < Hkv, "item decode");
       for (int qi = a.qt * sfa::kQT; qi < (a.qt + 1) * sfa::kQT && qi < nq; ++qi) {
-        const size_t s = sfa::attn_slot(a.h, a.r, qi, nch_cap, qmax);
+        const size_t s = sfa::attn_slot(a.h, a.r, qi, nr_cap, qmax);
         CHECK(s < nslot, "slot %zu >= %zu", s, nslot);
         CHECK(!written[s], "slot written twice");
         written[s] = 1;
@@ -355,14 +406,14 @@ static void check_decomposition(int P, int P_cap, int count, int bucket, int G, 
     }
   }
   for (int it = 0; it < items; ++it) CHECK(item_seen[it], "item %d not walked", it);
-  // the merge reads (row m, q-head g, range c) at h·nch_cap·qmax + c·qmax + m·G + g:
+  // the merge reads (row m, q-head g, range c) at h·nr_cap·qmax + c·qmax + m·G + g:
   // every read slot was written by the prefix pass, and nothing else was
   size_t reads = 0;
   for (int h = 0; h < Hkv; ++h)
     for (int m = 0; m < count; ++m)
       for (int g = 0; g < G; ++g)
         for (int c = 0; c < nr_merge; ++c) {
-          const size_t s = ((size_t)h * nch_cap + c) * qmax + (size_t)m * G + g;
+          const size_t s = ((size_t)h * nr_cap + c) * qmax + (size_t)m * G + g;
           CHECK(s < nslot && written[s], "merge reads unwritten slot (h=%d m=%d g=%d c=%d)", h, m, g, c);
           ++reads;
         }
@@ -391,8 +442,8 @@ static void check_attention_grid() {
   // every chunk count with the north-star and the long-context heads
   for (int nch = 1; nch <= sfa::kMaxChunks; ++nch)
     for (int count : {1, 39, 256}) {
-      check_decomposition(nch * 128, nch * 128, count, 256, 7, 4), ++n;
-      check_decomposition(nch * 128 - 5, nch * 128, count, 256, 5, 8), ++n;
+      check_decomposition(nch * sfa::kChunk, nch * sfa::kChunk, count, 256, 7, 4), ++n;
+      check_decomposition(nch * sfa::kChunk - 5, nch * sfa::kChunk, count, 256, 5, 8), ++n;
     }
   printf("attention grids: %lld shapes\n", n);
 }
@@ -417,7 +468,7 @@ int main(int argc, char** argv) {
   }
   check_plans();
   check_gemm_columns();
-  check_slots_and_vt();
+  check_lds_paths();
   check_page_addressing();
   check_attention_grid();
   printf("OK (%lld checks)\n", g_checks);

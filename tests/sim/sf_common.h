@@ -72,3 +72,33 @@ SF_DEV sf_u32x4 sf_lds_read16(sf_lds_off addr) {
 template <int N>
 SF_DEV void sf_lds_reads_done(sf_u32x4 (&)[N]) {}
 SF_DEV sf_lds_off sf_lds_addr(const void* p) { return reinterpret_cast<uintptr_t>(p); }
+SF_DEV uint32_t sf_lds_read4_now(sf_lds_off addr) {
+  uint32_t v;
+  memcpy(&v, reinterpret_cast<const void*>(addr), 4);
+  return v;
+}
+// scheduling pins and waits: nothing to order in the simulation
+template <typename T>
+SF_DEV void sf_pin(T&) {}
+SF_DEV void sf_wait_vm_loads() {}
+// ds_read_b64_tr_b16: lane i of each 16-lane group gets element i % 4 of the
+// 8 bytes lane 4k + i/4 points at, k = 0..3 (the layout measured on gfx950).
+template <int OFF>
+SF_DEV sf_u32x2 sf_lds_read8_tr(sf_lds_off addr) {
+  uint16_t mine[4];
+  memcpy(mine, reinterpret_cast<const void*>(addr + OFF), 8);
+  uint16_t got[4];
+  sim_wave_exchange(mine, 8, [&](const uint8_t* buf) {
+    const int l = sim_lane(), grp = l & ~15, i = l & 15;
+    for (int k = 0; k < 4; ++k) {
+      uint16_t e[4];
+      memcpy(e, buf + (grp + 4 * k + i / 4) * 128, 8);
+      got[k] = e[i % 4];
+    }
+  });
+  sf_u32x2 v;
+  memcpy(&v, got, 8);
+  return v;
+}
+template <int N>
+SF_DEV void sf_lds_reads_done(sf_u32x2 (&)[N]) {}

@@ -92,6 +92,14 @@ inline void sim_wave_exchange(const void* mine, size_t bytes, F use) {
   sim_arrive(sim_blk->wave[w]);
 }
 
+// v_readfirstlane: the value of the wave's first lane (every lane is active here)
+inline int sim_readfirstlane(int v) {
+  int out;
+  sim_wave_exchange(&v, 4, [&](const uint8_t* b) { memcpy(&out, b, 4); });
+  return out;
+}
+#define __builtin_amdgcn_readfirstlane(x) sim_readfirstlane(x)
+
 inline float __shfl_xor(float v, int mask, int width = 64) {
   (void)width;
   float out;

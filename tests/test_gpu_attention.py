@@ -105,14 +105,16 @@ def run_case(P, B1, N, H, Hkv, count, seed, causal=False, P_cap=None, page_size=
     assert torch.equal(o_bf[r], o32[r].to(torch.bfloat16))
 
 
-# (P, B1, N, H, Hkv, count): the chunks per work item follow
-# max(1, nch * n_qt * Hkv // 1024) with nch = ceil(P/128), n_qt = ceil(count*G/64)
+# (P, B1, N, H, Hkv, count): the prefix pass takes chunks of 64 keys, query tiles of
+# 128 (n_qt = ceil(count*G/128)) and cpi = max(ceil(nch*n_qt*Hkv/256), ceil(nch/64))
+# chunks per work item, nch = ceil(P/64)
 CASES = [
-    (16384, 8, 32, 40, 8, 39),      # 4 chunks per item (32 ranges)
-    (16389, 8, 32, 40, 8, 39),      # ragged last chunk (5 keys) in a 1-chunk last range
-    (32768, 8, 32, 8, 8, 256),      # 8 chunks per item, G = 1, every row
-    (3000, 8, 32, 28, 4, 100),      # one chunk per item
-    (700, 2, 32, 16, 2, 5),         # short prefix, few rows
+    (16384, 8, 32, 40, 8, 39),      # 16 chunks per item, 16 ranges
+    (16389, 8, 32, 40, 8, 39),      # 17 per item; ragged last chunk (5 keys) in a 2-chunk range
+    (32768, 8, 32, 8, 8, 256),      # 32 per item, G = 1, every row
+    (3000, 8, 32, 28, 4, 100),      # 5 per item, 6 query tiles
+    (700, 2, 32, 16, 2, 5),         # one chunk per item, short prefix, few rows
+    (20, 2, 32, 16, 2, 7),          # one 20-key chunk: the second key half of every wave empty
 ]
 
 

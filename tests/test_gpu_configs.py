@@ -118,7 +118,8 @@ def check_step(w, model, eng, tokens, cache, q_scale, layers_checked, teacher=No
                           q_scale=q_scale)
         lt_gpu = oracle_layer(eng.layers[li], h_in, parent, counts, kv, cos_n, sin_n, w.delta, H,
                               Hkv, q_scale=q_scale, device="cuda")
-        compare_layer(li, lt, trace[li], parent, B1, N, H, Hkv, hd, D, eng=eng, lt_gpu=lt_gpu)
+        compare_layer(li, lt, trace[li], parent, B1, N, H, Hkv, hd, D, eng=eng, lt_gpu=lt_gpu,
+                      prefix_kv=kv)
         del lt, lt_gpu
     # the head on the same GPU from the HIP final hidden state
     base, head = eng.base, eng.head

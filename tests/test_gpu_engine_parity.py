@@ -73,7 +73,7 @@ def check_layers(case, shape, tr, trace, eng, q_scale=None):
             lt_gpu = oracle_layer(eng.layers[li], lt.h_in, parent, tr.counts, kv, cos[P:P + N],
                                   sin[P:P + N], case.delta, H, Hkv, q_scale=q_scale,
                                   device="cuda")
-        compare_layer(li, lt, ht, parent, B1, N, H, Hkv, hd, D, eng=eng, lt_gpu=lt_gpu)
+        compare_layer(li, lt, ht, parent, B1, N, H, Hkv, hd, D, eng=eng, lt_gpu=lt_gpu, prefix_kv=kv)
 
 
 @pytest.mark.parametrize("name,shape,seed,P,delta", CASES[:3])

@@ -2,9 +2,10 @@
 CPU: tests/cpp/index_check.cpp is compiled with the host C++ compiler against the
 same header the HIP kernels include and run against the built library (for its
 workspace-size queries).  It walks the stream-K GEMM plans, the GEMM output
-columns and packed-weight fragments, the prefix attention's key slots, V^T
-layout, page-group addressing, persistent-grid item walk, chunk ranges and
-partial slots over the shapes the entry points accept (see the checker's header
+columns and packed-weight fragments, the prefix attention's staged-chunk LDS
+layout with its K and transposed V^T operand reads (emulated element by element,
+with the bank-conflict properties of the swizzles), page-group addressing,
+persistent-grid item walk, chunk ranges and partial slots over the shapes the entry points accept (see the checker's header
 for the list of properties)."""
 
 import shutil
@@ -37,7 +38,7 @@ def test_index_maps(checker):
     r = subprocess.run([str(checker), str(lib)], capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stdout + r.stderr
     out = r.stdout
-    for family in ("gemm plans", "gemm columns", "key slots", "page-group", "attention grids"):
+    for family in ("gemm plans", "gemm columns", "operand reads", "page-group", "attention grids"):
         assert family in out, out
     assert out.strip().splitlines()[-1].startswith("OK"), out
 
