@@ -147,11 +147,14 @@ __global__ __launch_bounds__(256) void residual_gather_add_kernel(
   *reinterpret_cast<sf_u32x4*>(out + (size_t)r * D + c) = o;
 }
 
+// The fix-ups below take 8 rows x 128 columns per workgroup (one 4-column group
+// per thread): grid (column tiles, ceil(mcap / 8)); row blocks past the device-side
+// row count exit at once.
+constexpr int kFixRows = 8;
+
 // Fix-up of the FFN down GEMM: tiles computed by several stream-K workgroups are
 // summed from their partial slots in slot order and scattered as bf16 rows
-// (tiles of a single workgroup were written by the GEMM itself).  One workgroup
-// per TW-column tile.
-template <int TW>
+// (tiles of a single workgroup were written by the GEMM itself).
 __global__ __launch_bounds__(256) void down_fixup_kernel(const float* __restrict__ part, Plan plan,
                                                          int mcap, const int32_t* __restrict__ rows,
                                                          const int32_t* __restrict__ count_p, int N,
@@ -161,22 +164,22 @@ __global__ __launch_bounds__(256) void down_fixup_kernel(const float* __restrict
   const int nsl = tile_last(t, plan) - first + 1;
   if (nsl == 1) return;
   const int M = min(*count_p, mcap);
+  const int m = blockIdx.y * kFixRows + (threadIdx.x >> 5);
+  if (m >= M) return;
   const size_t stride = (size_t)mcap * N;
-  for (int e = threadIdx.x; e < M * (TW / 4); e += 256) {
-    const int m = e / (TW / 4), c = t * TW + (e % (TW / 4)) * 4;
-    const int row = rows[m];
-    const sf_f32x4 y = sum_slots<sf_f32x4>(part + (size_t)m * N + c, stride, nsl);
-    sf_u32x2 o;
-    o[0] = sf_pack2(y[0], y[1]);
-    o[1] = sf_pack2(y[2], y[3]);
-    *reinterpret_cast<sf_u32x2*>(out + (size_t)row * N + c) = o;
-  }
+  const int c = t * 128 + (threadIdx.x & 31) * 4;
+  const int row = rows[m];
+  const sf_f32x4 y = sum_slots<sf_f32x4>(part + (size_t)m * N + c, stride, nsl);
+  sf_u32x2 o;
+  o[0] = sf_pack2(y[0], y[1]);
+  o[1] = sf_pack2(y[2], y[3]);
+  *reinterpret_cast<sf_u32x2*>(out + (size_t)row * N + c) = o;
 }
 
 // Fix-up of the gate/up GEMM: a 128-column tile computed by several workgroups has
 // its gate and up sums in partial slot rows of 2I columns (gate, then up); they
 // are summed in slot order and the SiLU*mul epilogue applied, with the same three
-// bf16 roundings as the GEMM's own epilogue.  One workgroup per tile.
+// bf16 roundings as the GEMM's own epilogue.
 __global__ __launch_bounds__(256) void silu_fixup_kernel(const float* __restrict__ part, Plan plan,
                                                          int mcap, const int32_t* __restrict__ count_p,
                                                          int I, uint16_t* __restrict__ act) {
@@ -186,8 +189,10 @@ __global__ __launch_bounds__(256) void silu_fixup_kernel(const float* __restrict
   if (nsl == 1) return;
   const int M = min(*count_p, mcap);
   const size_t stride = (size_t)mcap * 2 * I;
-  for (int e = threadIdx.x; e < M * 32; e += 256) {
-    const int m = e >> 5, c = t * 128 + (e & 31) * 4;
+  {
+    const int m = blockIdx.y * kFixRows + (threadIdx.x >> 5);
+    if (m >= M) return;
+    const int c = t * 128 + (threadIdx.x & 31) * 4;
     const float* p = part + (size_t)m * 2 * I + c;
     const sf_f32x4 g = sum_slots<sf_f32x4>(p, stride, nsl);
     const sf_f32x4 u = sum_slots<sf_f32x4>(p + I, stride, nsl);
@@ -320,8 +325,8 @@ extern "C" int sf_ffn_gate_up(const uint16_t* zn, const int32_t* count, int buck
   ep.ldo = I;
   // whole tiles get SiLU*mul straight from registers, shared tiles in the fix-up
   launch_sk<2, kSilu>(p, zn, nullptr, D, count, 0, bucket, wg, wu, D, I, part, ep, st);
-  hipLaunchKernelGGL(silu_fixup_kernel, dim3(p.T), dim3(256), 0, st, part, p, bucket, count, I,
-                     act);
+  hipLaunchKernelGGL(silu_fixup_kernel, dim3(p.T, (bucket + kFixRows - 1) / kFixRows), dim3(256), 0,
+                     st, part, p, bucket, count, I, act);
   return sf_launch_status();
 }
 
@@ -340,8 +345,8 @@ extern "C" int sf_ffn_down_scatter(const uint16_t* act, const int32_t* count, in
   ep.out = ffn;
   ep.ldo = D;
   launch_sk<1, kScatter>(p, act, nullptr, I, count, 0, bucket, wd, nullptr, I, D, part, ep, st);
-  hipLaunchKernelGGL(down_fixup_kernel<128>, dim3(p.T), dim3(256), 0, st, part, p, bucket, rows,
-                     count, D, ffn);
+  hipLaunchKernelGGL(down_fixup_kernel, dim3(p.T, (bucket + kFixRows - 1) / kFixRows), dim3(256), 0,
+                     st, part, p, bucket, rows, count, D, ffn);
   return sf_launch_status();
 }
 
