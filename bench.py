@@ -51,6 +51,9 @@ def parse_args(argv=None):
     ap.add_argument("--kernel-iters", type=int, default=200)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--mode-b", action="store_true",
+                    help="also measure the verify step at a fold ratio near 0.62 (synthetic "
+                         "layer inputs; reported under 'mode_b')")
     ap.add_argument("--lockstep", action="store_true",
                     help="a multi-sequence workload (cfg4) decodes its sequences in lockstep, "
                          "one batched verify step per round (a step = one round)")
@@ -185,41 +188,73 @@ def copy_calibration(mib: int = 256, reps: int = 8) -> dict:
             "bytes_written": nbytes, "avg_us": round(us, 2), "gbps": round(2 * nbytes / us / 1e3, 1)}
 
 
-def cpu_baseline(w, batched_cpu, tokens_per_step, seconds):
-    """The oracle (CPU restatement of the reference PyTorch step) in fp32:
-    one decoder layer of the workload's shape on the host cores, scaled to
-    all layers, plus the lm_head GEMM timed on a vocab slice and scaled."""
-    from dataclasses import replace
+def host_cores() -> dict:
+    """The host cores this process may use: the affinity set, capped by a cgroup
+    CPU quota when one is set, and the CPU model (lscpu's "Model name", read from
+    /proc/cpuinfo)."""
+    aff = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        q, per = Path("/sys/fs/cgroup/cpu.max").read_text().split()[:2]
+        if q != "max":
+            quota = max(1, int(int(q) / int(per)))
+    except (OSError, ValueError):
+        pass
+    model = None
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"threads": min(aff, quota) if quota else aff, "affinity": aff, "cgroup_quota": quota,
+            "model": model}
 
-    from oracle.folded_reference import (decoder_parts, folded_layer, llama4_q_scale, parent_map,
-                                         rope_tables, topo_order)
-    from specfold_amd.generate.synthetic_model import build_nld, build_qwen2
-    from specfold_amd.synthetic import random_prefix_kv
 
-    cores = min(16, len(os.sched_getaffinity(0)))
-    torch.set_num_threads(cores)
-    sh = replace(w.shape, layers=1, vocab=4096)
-    if w.family == "nld":
-        model = build_nld(sh, w.seed, device="cpu", dtype=torch.float32)
-    else:
-        model = build_qwen2(sh, w.seed, device="cpu", dtype=torch.float32)
-    q_scale = llama4_q_scale(model.config, w.prefix, batched_cpu.shape[1])
-    gen = torch.Generator().manual_seed(w.seed)
-    kv = random_prefix_kv(1, sh.kv_heads, w.prefix, sh.head_dim, gen, dtype=torch.float32)[0]
-    toks = batched_cpu % sh.vocab
+def cpu_baseline(w, gen, batched, gpu_counts, tokens_per_step, seconds):
+    """The oracle (oracle/folded_reference.py: the CPU restatement of the
+    reference's PyTorch folded verify step) on the host cores, replaying the GPU
+    step's own work: layer 0 of the GPU model (its bf16 weights copied to the
+    host: the reference's model dtype), the step's own batched tokens and their
+    embedding, and the cache's layer-0 prefix, so the CPU gate recomputes the
+    rows the GPU step recomputed at layer 0 (both counts are reported).  One
+    layer is timed and scaled by the layer count, plus the lm_head timed on a
+    vocabulary slice and scaled ("extrapolated": true)."""
+    import copy
+
+    from oracle.folded_reference import FoldCounters, folded_layer, parent_map, topo_order
+
+    host = host_cores()
+    torch.set_num_threads(host["threads"])
+    eng = gen._engine
+    cache = gen._state["cache"]
+    P = cache.length
+    B1, N = batched.shape
+    sh = w.shape
+    toks = batched.cpu()
     parent, counts = parent_map(toks)
     order = topo_order(counts)
-    hidden = torch.randn(toks.shape[0], toks.shape[1], sh.hidden, generator=gen)
-    cos, sin = rope_tables(model, hidden, w.prefix, toks.shape[1])
-    h = [hidden[i:i + 1] for i in range(toks.shape[0])]
-    lyr = decoder_parts(model)[0].layers[0]
+    h0 = eng.base.embed_tokens(batched).to("cpu")
+    h = [h0[i:i + 1] for i in range(B1)]
+    lyr = copy.deepcopy(eng.layers[0]).to("cpu")
+    kv = tuple(t.to("cpu") for t in cache[0])
+    cos, sin = eng.rope_tables(P + N)
+    cos, sin = cos[P:P + N].to("cpu"), sin[P:P + N].to("cpu")
+    q_scale = None
+    qfn = getattr(gen.model_executor, "q_scale", None)
+    if qfn is not None:
+        qs = qfn(P, N)
+        q_scale = None if qs is None else qs.to("cpu")
+    cnt = FoldCounters()
 
-    def one():
+    def one(counters=None):
         folded_layer(lyr, h, parent, order, kv, cos, sin, w.delta, sh.heads, sh.kv_heads,
-                     q_scale=q_scale)
+                     counters=counters, q_scale=q_scale)
 
     with torch.no_grad():
-        one()
+        one(cnt)
+        r_cpu = N + cnt.draft_recomputed          # branch 0 always, plus the recomputed drafts
         times = []
         t_end = time.perf_counter() + seconds
         while len(times) < 2 or time.perf_counter() < t_end:
@@ -228,21 +263,87 @@ def cpu_baseline(w, batched_cpu, tokens_per_step, seconds):
             times.append(time.perf_counter() - t0)
         t_layer = statistics.median(times)
         vs = 8192
-        x = torch.randn(toks.numel(), sh.hidden)
-        wh = torch.randn(vs, sh.hidden)
+        x = torch.randn(B1 * N, sh.hidden, dtype=torch.bfloat16)
+        wh = eng.head.weight[:vs].to("cpu")
         x @ wh.t()
         t0 = time.perf_counter()
         for _ in range(3):
             x @ wh.t()
-        t_head = (time.perf_counter() - t0) / 3 * (w.shape.vocab / vs)
-    t_step = t_layer * w.shape.layers + t_head
-    return {"value": round(tokens_per_step / t_step, 5), "unit": "tokens/s", "cores": cores,
-            "kind": "port",
-            "sample": (f"oracle fp32, 1 of {w.shape.layers} layers timed ({len(times)} runs, "
-                       f"median {t_layer:.3f}s) x{w.shape.layers} + lm_head "
-                       f"({t_head:.3f}s, timed on a {vs}-row vocab slice); "
-                       f"{tokens_per_step:.3f} tokens/step from the GPU decode loop"),
+        t_head = (time.perf_counter() - t0) / 3 * (sh.vocab / vs)
+    t_step = t_layer * sh.layers + t_head
+    return {"value": round(tokens_per_step / t_step, 5), "unit": "tokens/s",
+            "cores": host["threads"], "kind": "port", "extrapolated": True,
+            "cpu_model": host["model"], "affinity_cores": host["affinity"],
+            "cgroup_quota_cores": host["cgroup_quota"], "dtype": str(h0.dtype).replace("torch.", ""),
+            "recomputed_rows_layer0": {"cpu": r_cpu, "gpu": int(gpu_counts[0])},
+            "sample": (f"the oracle on the GPU step's own layer-0 input (tokens, embedding, "
+                       f"weights, {P}-key prefix): 1 of {sh.layers} layers timed ({len(times)} "
+                       f"runs, median {t_layer:.3f}s) x{sh.layers} + lm_head ({t_head:.3f}s, "
+                       f"timed on a {vs}-row vocab slice and scaled); {tokens_per_step:.3f} "
+                       f"tokens/step from the GPU decode loop"),
             "verify_step_s": round(t_step, 4)}
+
+
+def kernel_table(w, eng, B1, N, kernel_iters):
+    """Every entry point's average duration (HIP events around a graph of
+    back-to-back launches on the buffers of the engine's last verify step, one
+    launcher per layer in turn) with its algorithmic bytes / flops at that step's
+    recomputed-row count; returns (kernels, prefix, rows)."""
+    shared = {}
+    per_layer = [eng.profile_launchers(li=li, shared=shared) for li in range(eng.L)]
+    info = per_layer[-1][1]
+    P = info["prefix"]
+    R = int(info["count"].item())
+    kernels = {}
+    for name in ("qkv", "attn", "chain", "o_proj", "post_norm", "gate_up", "down", "final_norm",
+                 "lm_head", "append", "gate"):
+        if name not in per_layer[-1][0]:
+            continue
+        once = name in ONCE_PER_STEP
+        fns = [per_layer[-1][0][name]] if once else [pl[0][name] for pl in per_layer]
+        ms = event_time_ms(fns, kernel_iters if not once else max(4, kernel_iters // 10))
+        kernels[name] = kernel_roofline(name, ms, w, R, B1, N, P)
+        kernels[name]["launches_per_step"] = 1 if once else eng.L
+    return kernels, P, R
+
+
+def mode_b(w, gen, batched, iters, kernel_iters):
+    """The verify step at the reference's fold regime: every layer's input is
+    replaced by synthetic hidden states in which branch i = its parent's +
+    sigma * N(0, 1) per position, sigma 0.2 on a seeded 38% of positions and 0.05
+    elsewhere (relative L2 ~ sigma, so at delta 0.1 about 38% of the draft
+    positions are recomputed: fold ratio ~0.62, the reference's end-to-end figure,
+    README.md:55-59).  The step runs eagerly (a replaced layer input leaves the
+    captured graph); its per-kernel table is measured like the main one."""
+    from specfold_amd.engine import StepStats, build_parent_map
+    from specfold_amd.synthetic import perturbed_hidden
+    eng = gen._engine
+    cache = gen._state["cache"]
+    B1, N = batched.shape
+    parents, _ = build_parent_map(batched)
+    g = torch.Generator().manual_seed(w.seed + 1000)
+    teacher = {li: perturbed_hidden(parents, N, w.shape.hidden, g).to(eng.device)
+               for li in range(eng.L)}
+    qfn = getattr(gen.model_executor, "q_scale", None)
+    qs = qfn(cache.length, N) if qfn is not None else None
+    st = StepStats()
+    lat = []
+    for i in range(iters + 2):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        eng.forward(batched, cache, w.delta, teacher=teacher, stats=st, q_scale=qs)
+        e.record()
+        e.synchronize()
+        if i >= 2:
+            lat.append(s.elapsed_time(e))
+    counts = st.counts
+    R = sum(counts) / len(counts)
+    kernels, P, R_last = kernel_table(w, eng, B1, N, kernel_iters)
+    fold = 1 - (sum(counts) - len(counts) * N) / ((B1 - 1) * N * len(counts))
+    return {"verify_step_ms_eager": round(statistics.median(lat), 4),
+            "recomputed_rows_mean": round(R, 2), "recomputed_rows_last_layer": R_last,
+            "fold_ratio": round(fold, 4), "prefix": P, "kernels": kernels,
+            "data": "synthetic layer inputs (branch = parent + sigma N(0,1)), every layer"}
 
 
 def make_decoders(w):
@@ -411,21 +512,7 @@ def main(argv=None) -> int:
     # per-kernel timings on the buffers of the last verify step, cycling through the
     # layers (weights and cache slices) as the step does
     eng = gen._engine
-    shared = {}
-    per_layer = [eng.profile_launchers(li=li, shared=shared) for li in range(eng.L)]
-    info = per_layer[-1][1]
-    P = info["prefix"]
-    R_last = int(info["count"].item())
-    kernels = {}
-    for name in ("qkv", "attn", "chain", "o_proj", "post_norm", "gate_up", "down", "final_norm",
-                 "lm_head", "append", "gate"):
-        if name not in per_layer[-1][0]:
-            continue
-        once = name in ONCE_PER_STEP
-        fns = [per_layer[-1][0][name]] if once else [pl[0][name] for pl in per_layer]
-        ms = event_time_ms(fns, args.kernel_iters if not once else max(4, args.kernel_iters // 10))
-        kernels[name] = kernel_roofline(name, ms, w, R_last, B1, N, P)
-        kernels[name]["launches_per_step"] = 1 if once else eng.L
+    kernels, P, R_last = kernel_table(w, eng, B1, N, args.kernel_iters)
     traffic = load_traffic(w.name)
     for name, k in kernels.items():
         k["traffic"] = traffic.get(name)
@@ -440,8 +527,15 @@ def main(argv=None) -> int:
     tokens_per_step = committed / max(1, args.steps * (len(gens) if lockstep else 1))
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(w, batched.cpu(), tokens_per_step, args.cpu_seconds)
+        cpu = cpu_baseline(w, gen, batched, counts, tokens_per_step, args.cpu_seconds)
         print(f"[bench] cpu baseline {cpu}", file=sys.stderr, flush=True)
+
+    mb = None
+    if args.mode_b:
+        mb = mode_b(w, gen, batched, max(3, args.verify_iters // 5), args.kernel_iters)
+        print(f"[bench] mode B: R {mb['recomputed_rows_mean']}, kernels "
+              f"{json.dumps({k: v['avg_us'] for k, v in mb['kernels'].items()})}",
+              file=sys.stderr, flush=True)
 
     out = {
         "metric": "decode tokens/sec on 1 GPU; folded verify-step latency; attention HBM GB/s",
@@ -480,6 +574,7 @@ def main(argv=None) -> int:
         "kernels": kernels,
         "copy_calibration": copy,
         "cpu_baseline": cpu,
+        "mode_b": mb,
     }
     print(json.dumps(out))
     return 0
