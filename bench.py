@@ -95,7 +95,6 @@ def kernel_roofline(name, ms, w, R, B1, N, P):
     sh = w.shape
     D, H, Hkv, hd, e = sh.hidden, sh.heads, sh.kv_heads, sh.head_dim, 2
     BN = B1 * N
-    F = BN - R
     nq = (H + 2 * Hkv) * hd
     if name == "gate":
         # fused residual gate: hp rows + the R distinct ffn rows in, h rows + R xn rows out
@@ -106,11 +105,11 @@ def kernel_roofline(name, ms, w, R, B1, N, P):
         by = nq * D * e + bias + R * D * e + R * nq * e + 2 * N * hd * e
         fl = 2 * R * D * nq
     elif name == "attn":
-        by = 2 * Hkv * P * hd * e + BN * 2 * Hkv * hd * e + 2 * R * H * hd * e + 8 * R * H
-        fl = 4 * R * H * (P + N) * hd
-    elif name == "chain":
-        by = F * (2 * H * hd * e + 8 * H)
-        fl = 8 * F * H * hd
+        # prefix K/V once, the block K/V rows, the recomputed rows' q; O (fp32 + bf16)
+        # and (m, Z) of every row (folded rows included)
+        by = (2 * Hkv * P * hd * e + BN * 2 * Hkv * hd * e + R * H * hd * e
+              + BN * H * hd * (4 + e) + 8 * BN * H)
+        fl = 4 * R * H * P * hd + 4 * BN * H * N * hd
     elif name == "append":
         by = 2 * (2 * N * Hkv * hd * e)
         fl = 0
@@ -295,7 +294,7 @@ def kernel_table(w, eng, B1, N, kernel_iters):
     P = info["prefix"]
     R = int(info["count"].item())
     kernels = {}
-    for name in ("qkv", "attn", "chain", "o_proj", "post_norm", "gate_up", "down", "final_norm",
+    for name in ("qkv", "attn", "o_proj", "post_norm", "gate_up", "down", "final_norm",
                  "lm_head", "append", "gate"):
         if name not in per_layer[-1][0]:
             continue

@@ -60,7 +60,8 @@ const char* sf_status_string(int status);
  * 3: sf_parent_map (the branch parent map on the device); sf_logit_stats.
  * 4: batched verify steps: SF_GATE_ROOTS_BY_PARENT, sf_qkv_rope_branches.
  * 5: GEMMs on 64-wide K chunks (K % 64, N % 128); sf_ffn_gate_up takes a workspace.
- * 6: sf_logit_stats_noalloc, SF_ERR_SCRATCH. */
+ * 6: sf_logit_stats_noalloc, SF_ERR_SCRATCH.
+ * 7: sf_attn_rows; the attention workspace holds the merged prefix states. */
 int sf_abi_version(void);
 
 /*
@@ -170,9 +171,9 @@ int sf_qkv_rope_branches(const uint16_t* xn, const int32_t* rows, const int32_t*
  * prefix_len (optional, device int32[1]): the prefix length, read on the device;
  * P is then the capacity the grid and workspace are sized for (so one captured
  * graph serves a growing cache).  With prefix_len NULL, P is the length.
+ * workspace: sf_attn_workspace_bytes(bucket, H, P) bytes, 16-byte aligned (scratch).
  * Limits: hd == 128, H % Hkv == 0, N <= 64, H/Hkv <= 8, P <= 32768, a page size
- * of 16, 32, 64 or 128 tokens (a page holds whole 16-key groups; a 128-key chunk
- * holds whole pages).
+ * of 16, 32, 64 or 128 tokens (a page holds whole 16-key groups).
  */
 size_t sf_attn_workspace_bytes(int bucket, int H, int P);
 int sf_attn_prefix_block(const uint16_t* q_buf, const uint16_t* kv_buf, const uint16_t* prefix_k,
@@ -182,6 +183,28 @@ int sf_attn_prefix_block(const uint16_t* q_buf, const uint16_t* kv_buf, const ui
                          int H, int Hkv, int hd, float scaling, const int32_t* prefix_len,
                          int block_causal, float* o32, uint16_t* o_bf, float* m_tab,
                          float* z_tab, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * (3)+(4) Attention of every row of branches [b_first, b_first + b_count): the
+ * recomputed rows as sf_attn_prefix_block computes them, and each folded row
+ * (b, n) from the query of its source row s = src[b*N+n]*N + n over the prefix
+ * (s's merged prefix state) and branch b's own block keys -- the exact softmax
+ * over the branch's keys that the reference's chain correction reaches
+ * incrementally (specfold/generate/fastdllm_v2_folded.py:164-204; Triton
+ * specfold_flash_attn_gqa_kernel + specfold_chain_correction_gqa_kernel,
+ * specfold/generate/triton_kernels.py:301-429), so one call replaces
+ * sf_attn_prefix_block + sf_chain_correct.  rows / count: the recomputed rows of
+ * those branches (ascending; every folded row's source row among them).  A batched
+ * step calls it once per sequence with that sequence's branch range and rows.
+ * Same workspace and limits as sf_attn_prefix_block; no causal mode.
+ */
+int sf_attn_rows(const uint16_t* q_buf, const uint16_t* kv_buf, const uint16_t* prefix_k,
+                 const uint16_t* prefix_v, const int32_t* page_table, int P, int page_size,
+                 long long page_stride, long long head_stride, const int32_t* src,
+                 const int32_t* rows, const int32_t* count, int bucket, int B1, int N,
+                 int b_first, int b_count, int H, int Hkv, int hd, float scaling,
+                 const int32_t* prefix_len, float* o32, uint16_t* o_bf, float* m_tab,
+                 float* z_tab, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * (4) Chain correction of folded rows: start from the state of the nearest

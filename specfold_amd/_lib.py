@@ -47,6 +47,9 @@ SIGNATURES = {
     "sf_attn_prefix_block": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _ll, _ll, _vp, _vp, _vp,
                                   _i, _i, _i, _i, _i, _i, _f, _vp, _i, _vp, _vp, _vp, _vp, _vp,
                                   _sz, _vp]),
+    "sf_attn_rows": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _ll, _ll, _vp, _vp, _vp,
+                          _i, _i, _i, _i, _i, _i, _i, _i, _f, _vp, _vp, _vp, _vp, _vp, _vp,
+                          _sz, _vp]),
     "sf_chain_correct": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _f,
                               _vp, _vp, _vp, _vp, _vp]),
     "sf_kv_append": (_i, [_vp, _i, _i, _i, _i, _vp, _vp, _vp, _i, _ll, _ll, _i, _vp]),
@@ -304,6 +307,43 @@ def attn_prefix_block(q_buf, kv_buf, prefix_k, prefix_v, page_table, P, page_siz
         _ptr(o32), _ptr(o_bf),
         _ptr(m_tab), _ptr(z_tab), _ptr(workspace), workspace.numel(), _stream(stream))
     _check(st, "sf_attn_prefix_block")
+
+
+def attn_rows(q_buf, kv_buf, prefix_k, prefix_v, page_table, P, page_size, page_stride,
+              head_stride, src, rows, count, bucket, B1, N, b_first, b_count, H, Hkv, hd,
+              scaling, o32, o_bf, m_tab, z_tab, workspace, prefix_len=None, stream=None) -> None:
+    """Attention of every row of branches [b_first, b_first + b_count): recomputed
+    rows as attn_prefix_block, folded rows from their source row's query over the
+    prefix and their own branch's block keys (sf_attn_rows: attention + chain
+    correction in one call)."""
+    BN = B1 * N
+    _need(q_buf, "q_buf", torch.bfloat16, min_numel=(BN + 1) * H * hd)
+    _need(kv_buf, "kv_buf", torch.bfloat16, min_numel=(BN + 1) * 2 * Hkv * hd)
+    if P > 0:
+        _need(prefix_k, "prefix_k", torch.bfloat16)
+        _need(prefix_v, "prefix_v", torch.bfloat16)
+        if page_table is not None:
+            _need(page_table, "page_table", torch.int32, min_numel=(P + page_size - 1) // page_size,
+                  align=4)
+    _need(src, "src", torch.int32, min_numel=BN, align=4)
+    _need(rows, "rows", torch.int32, min_numel=bucket, align=4)
+    _need(count, "count", torch.int32, min_numel=1, align=4)
+    _need(o32, "o32", torch.float32, min_numel=BN * H * hd)
+    _need(o_bf, "o_bf", torch.bfloat16, min_numel=BN * H * hd)
+    _need(m_tab, "m_tab", torch.float32, min_numel=BN * H, align=4)
+    _need(z_tab, "z_tab", torch.float32, min_numel=BN * H, align=4)
+    _need(workspace, "workspace", torch.uint8, min_numel=attn_workspace_bytes(bucket, H, P),
+          align=256)
+    if prefix_len is not None:
+        _need(prefix_len, "prefix_len", torch.int32, numel=1, align=4)
+    st = load().sf_attn_rows(
+        _ptr(q_buf), _ptr(kv_buf), _ptr(prefix_k) if P > 0 else None,
+        _ptr(prefix_v) if P > 0 else None, _ptr(page_table) if P > 0 else None, P,
+        page_size, page_stride, head_stride, _ptr(src), _ptr(rows), _ptr(count), bucket, B1, N,
+        b_first, b_count, H, Hkv, hd, float(scaling), _ptr(prefix_len) if P > 0 else None,
+        _ptr(o32), _ptr(o_bf), _ptr(m_tab), _ptr(z_tab), _ptr(workspace), workspace.numel(),
+        _stream(stream))
+    _check(st, "sf_attn_rows")
 
 
 def chain_correct(q_buf, kv_buf, src, par, rec, seg, segcnt, B1, N, H, Hkv, hd, scaling,

@@ -412,170 +412,321 @@ sf_attn_prefix_kernel(
   }
 }
 
-// One 512-thread workgroup per active (recomputed row m, kv head h) item, walked
-// by a persistent grid; thread t owns the output pair (q-head t/64, dims
-// 2*(t%64) .. +1).
-constexpr int kBatch = 16;        // chunk partials loaded per round
+// ---- prefix merge ----------------------------------------------------------------------
+// One wave per (recomputed row m, q-head): the nr range partials of its query are
+// combined into one prefix state {acc[128], m, l} (m in the scaled base-2 domain of
+// the partials) at state[m][q-head] (132 floats).  Lane l takes dims 2l, 2l+1 and
+// the (m, l) of range l (nr <= 64).
+constexpr int kStateFloats = kHD + 4;
 
-SF_DEV void merge_item(const uint16_t* __restrict__ q_buf, const uint16_t* __restrict__ kv_buf,
-                       const int32_t* __restrict__ src, const int32_t* __restrict__ rows, int m,
-                       int h, int N, int H, int Hkv, int G, float scale_log2, int causal, int nch,
-                       int nchunks_cap, int qmax, const float* __restrict__ ws_o,
-                       const float* __restrict__ ws_ml, float* __restrict__ o32,
-                       uint16_t* __restrict__ o_bf, float* __restrict__ m_tab,
-                       float* __restrict__ z_tab, float (*sq)[kHD], uint16_t (*sk)[kHD],
-                       uint16_t (*sv)[kHD], float (*ss)[kMaxN], float (*sml)[2 * kMaxRanges],
-                       float* sM, float* sZ) {
+__global__ __launch_bounds__(256) void sf_attn_prefix_merge_kernel(
+    const int32_t* __restrict__ count_p, int bucket, int H, int Hkv,
+    const int32_t* __restrict__ p_len, int P_cap, int nr_cap, int qmax,
+    const float* __restrict__ ws_o, const float* __restrict__ ws_ml, float* __restrict__ state) {
+  const int lane = threadIdx.x & 63;
+  const int it = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int count = min(*count_p, bucket);
+  if (it >= count * H) return;
+  const int G = H / Hkv;
+  const int m = it / H, hq = it - m * H;
+  const int h = hq / G, g = hq - h * G;
+  const int P = p_len ? min(*p_len, P_cap) : P_cap;
+  const int nr = merge_ranges(P, count * G, Hkv);
+  const int qi = m * G + g;
+  constexpr int kB = 16;  // range partials loaded per round (clamped addresses)
+  float2 a[kB];
+  const float2 ml = lane < nr ? *reinterpret_cast<const float2*>(ws_ml + attn_slot(h, lane, qi, nr_cap, qmax) * 2)
+                              : make_float2(-INFINITY, 0.f);
+#pragma unroll
+  for (int u = 0; u < kB; ++u)
+    a[u] = *reinterpret_cast<const float2*>(
+        ws_o + attn_slot(h, min(u, max(nr - 1, 0)), qi, nr_cap, qmax) * kHD + 2 * lane);
+  const float mm = sf_wave_max(ml.x);  // -inf only with no prefix key at all
+  const float w = (lane < nr && mm > -INFINITY) ? __builtin_amdgcn_exp2f(ml.x - mm) : 0.f;
+  const float l = sf_wave_sum(ml.y * w);
+  float2 acc = make_float2(0.f, 0.f);
+  for (int r0 = 0; r0 < nr; r0 += kB) {
+    if (r0 > 0) {
+#pragma unroll
+      for (int u = 0; u < kB; ++u)
+        a[u] = *reinterpret_cast<const float2*>(
+            ws_o + attn_slot(h, min(r0 + u, nr - 1), qi, nr_cap, qmax) * kHD + 2 * lane);
+    }
+#pragma unroll
+    for (int u = 0; u < kB; ++u) {
+      const float wr = __shfl(w, min(r0 + u, 63), 64);   // 0 past nr
+      acc.x = fmaf(wr, a[u].x, acc.x);
+      acc.y = fmaf(wr, a[u].y, acc.y);
+    }
+  }
+  float* st = state + ((size_t)m * H + hq) * kStateFloats;
+  *reinterpret_cast<float2*>(st + 2 * lane) = acc;
+  if (lane == 0) *reinterpret_cast<float2*>(st + kHD) = make_float2(mm, l);
+}
+
+// ---- finalize --------------------------------------------------------------------------
+// One 256-thread workgroup per (branch b, kv head h, 8 block positions): a row (b, n)
+// listed among the compacted rows takes its own query; any other (folded) row the
+// query of its source row s = src[b*N + n]*N + n (its nearest recomputing
+// ancestor's, which is listed).  Either attends over the prefix -- that query's
+// merged prefix state -- and branch b's own N block keys (kv rows
+// src[b*N + j]*N + j).  For a folded row this is the
+// softmax over its own keys that the reference reaches by chain correction
+// (fastdllm_v2_folded.py:183-204: the old keys' terms swapped for the new ones);
+// here it is formed directly, with the branch's block K/V staged once in LDS for all
+// its rows.  The 8 positions x G q-heads (<= 64 queries) are 4 tiles of 16, one per
+// wave; block scores S^T = K Q^T and O^T += V^T P^T on MFMA as in the prefix pass.
+// FOLDED = false computes the listed rows only.
+constexpr int kFinRows = 8;
+constexpr int kMaxBucket = 1024;  // compacted rows (B1 * N <= 1024)
+
+template <bool FOLDED>
+__global__ __launch_bounds__(256) void sf_attn_finalize_kernel(
+    const uint16_t* __restrict__ q_buf, const uint16_t* __restrict__ kv_buf,
+    const int32_t* __restrict__ src, const int32_t* __restrict__ rows,
+    const int32_t* __restrict__ count_p, int bucket, int N, int b_first, int H, int Hkv,
+    float scale_log2, int causal, int has_prefix, const float* __restrict__ state,
+    float* __restrict__ o32, uint16_t* __restrict__ o_bf, float* __restrict__ m_tab,
+    float* __restrict__ z_tab) {
+  __shared__ __attribute__((aligned(16))) uint8_t sKV[2 * kMaxN * kRowBytes];  // K rows, V rows
+  __shared__ int sRows[kMaxBucket];
   const int tid = threadIdx.x;
-  const int my_g = tid >> 6, dp = (tid & 63) * 2;
-  const bool mine = my_g < G;
-  const size_t my_slot0 = (size_t)h * nchunks_cap * qmax + (size_t)m * G + my_g;
-  // --- loads: chunk (m, l) and the first batch of chunk accumulators (independent
-  // of the row id), then q and the branch's block K/V gathered through src --------
-  for (int i = tid; i < G * nch; i += 512) {
-    const int g = i / nch, c = i - g * nch;
-    // attn_slot(h, c, m·G + g, ...) in 64-bit arithmetic (tests/cpp/index_check.cpp
-    // checks that these reads are exactly the prefix pass's writes)
-    const size_t sl = ((size_t)h * nchunks_cap + c) * qmax + (size_t)m * G + g;
-    const float2 ml = *reinterpret_cast<const float2*>(ws_ml + sl * 2);
-    sml[g][2 * c] = ml.x;
-    sml[g][2 * c + 1] = ml.y;
-  }
-  float2 accb[kBatch];
-#pragma unroll
-  for (int c = 0; c < kBatch; ++c)
-    if (mine && c < nch)
-      accb[c] = *reinterpret_cast<const float2*>(ws_o + (my_slot0 + (size_t)c * qmax) * kHD + dp);
-  const int row = rows[m];
-  const int b = row / N;
+  const int lane = tid & 63;
+  const int wv = tid >> 6;
+  const int grp = lane >> 4;
+  const int ql = lane & 15;
+  const int G = H / Hkv;
+  const int ngr = (N + kFinRows - 1) / kFinRows;
+  const int item = blockIdx.x;
+  const int h = item % Hkv;
+  const int b = b_first + (item / Hkv) / ngr;
+  const int n0 = ((item / Hkv) % ngr) * kFinRows;
+  const int count = min(*count_p, bucket);
   const int kvs = 2 * Hkv * kHD;
-  if (tid < G * 32) {
-    const int g = tid >> 5, d = (tid & 31) * 4;
-    const sf_u32x2 w = *reinterpret_cast<const sf_u32x2*>(
-        q_buf + (size_t)row * H * kHD + (h * G + g) * kHD + d);
-    sq[g][d] = __uint_as_float(w[0] << 16);
-    sq[g][d + 1] = __uint_as_float(w[0] & 0xffff0000u);
-    sq[g][d + 2] = __uint_as_float(w[1] << 16);
-    sq[g][d + 3] = __uint_as_float(w[1] & 0xffff0000u);
-  }
-  for (int i = tid; i < N * 16; i += 512) {
-    const int j = i >> 4, sgm = i & 15;
-    const size_t kvrow = (size_t)(src[b * N + j] * N + j) * kvs;
-    const sf_u32x4 kk = *reinterpret_cast<const sf_u32x4*>(kv_buf + kvrow + h * kHD + sgm * 8);
-    const sf_u32x4 vv =
-        *reinterpret_cast<const sf_u32x4*>(kv_buf + kvrow + (Hkv + h) * kHD + sgm * 8);
-    *reinterpret_cast<sf_u32x4*>(&sk[j][sgm * 8]) = kk;
-    *reinterpret_cast<sf_u32x4*>(&sv[j][sgm * 8]) = vv;
-  }
-  __syncthreads();
+  const int nkt = (N + 15) >> 4;  // 16-key tiles of the block
 
-  // --- block scores (base-2 domain): thread -> (g, j) ------------------------------
-  for (int i = tid; i < G * N; i += 512) {
-    const int g = i / N, j = i - g * N;
-    float d = 0.f;
-#pragma unroll 4
-    for (int e = 0; e < kHD; e += 8) {
-      float kf[8];
-      sf_unpack8(*reinterpret_cast<const sf_u32x4*>(&sk[j][e]), kf);
-#pragma unroll
-      for (int t = 0; t < 8; ++t) d = fmaf(sq[g][e + t], kf[t], d);
-    }
-    // causal (a block commit of an AR forward): block position n sees keys j <= n
-    ss[g][j] = (causal && j > row - b * N) ? -INFINITY : d * scale_log2;
-  }
-  __syncthreads();
-
-  // --- per q-head: merged max, block probabilities, chunk weights, Z (wave w: head w)
+  // ---- branch b's block K/V of head h to LDS, whole 32-key blocks (rows past N repeat
+  // row N-1: finite values under the zero weights of masked keys) -------------------------
   {
-    const int lane = tid & 63, w = tid >> 6;
-    if (w < G) {
-      const int g = w;
-      float mm = -INFINITY;
-      for (int j = lane; j < N; j += 64) mm = fmaxf(mm, ss[g][j]);
-      for (int c = lane; c < nch; c += 64) mm = fmaxf(mm, sml[g][2 * c]);
-      mm = sf_wave_max(mm);
-      float z = 0.f;
-      for (int j = lane; j < N; j += 64) {
-        const float p = __builtin_amdgcn_exp2f(ss[g][j] - mm);
-        ss[g][j] = p;
-        z += p;
+    const int nunits = ((nkt + 1) / 2) * 32 * 16;  // (row, 16-byte unit) pairs per K or V
+    for (int i = tid; i < 2 * nunits; i += 256) {
+      const int v = i >= nunits;
+      const int ii = i - v * nunits;
+      const int row = ii >> 4, p = ii & 15;
+      const int j = min(row, N - 1);
+      const size_t kvrow = (size_t)(src[b * N + j] * N + j) * kvs;
+      const int u = v ? v_unit(row, p) : k_unit(row, p);
+      *reinterpret_cast<sf_u32x4*>(sKV + v * kMaxN * kRowBytes + row * kRowBytes + p * 16) =
+          *reinterpret_cast<const sf_u32x4*>(kv_buf + kvrow + (v ? Hkv + h : h) * kHD + u * 8);
+    }
+  }
+
+  // the compacted rows, for lookups
+  for (int i = tid; i < count; i += 256) sRows[i] = rows[i];
+  __syncthreads();
+  auto find = [&](int row) {  // first index with sRows[i] >= row (ascending rows)
+    int lo = 0, hi = count;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (sRows[mid] < row) lo = mid + 1; else hi = mid;
+    }
+    return min(lo, max(count - 1, 0));
+  };
+
+  // ---- this lane's query (tile wv, column ql) ------------------------------------------
+  const int qloc = wv * 16 + ql;         // query = position n0 + qloc / G, q-head qloc % G
+  const int nl = qloc / G;
+  const int g = qloc - nl * G;
+  const int n = n0 + nl;
+  const bool qvalid = nl < kFinRows && n < N;
+  const int r = b * N + min(n, N - 1);
+  // a listed (recomputed) row takes its own query and prefix state; an unlisted one
+  // (folded) those of its source row, which is listed
+  int sidx = find(r);
+  const bool listed = count > 0 && sRows[sidx] == r;
+  const int srow = listed ? r : src[r] * N + min(n, N - 1);
+  if (!listed) sidx = find(srow);
+  const bool compute = qvalid && (FOLDED || listed);
+  const int hq = h * G + min(g, G - 1);
+  sf_u32x4 qf[4];
+  {
+    const uint16_t* qp = q_buf + (size_t)srow * H * kHD + hq * kHD + grp * 8;
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) qf[ds] = *reinterpret_cast<const sf_u32x4*>(qp + ds * 32);
+  }
+  // the source row's merged prefix state: its index among the ascending compacted rows
+  float m_run = -INFINITY, l_run = 0.f;
+  sf_f32x4 acc[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) acc[dt] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
+  if (has_prefix) {
+    const float* st = state + ((size_t)sidx * H + hq) * kStateFloats;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) acc[dt] = *reinterpret_cast<const sf_f32x4*>(st + dt * 16 + grp * 4);
+    const float2 ml = *reinterpret_cast<const float2*>(st + kHD);
+    m_run = ml.x;
+    l_run = ml.y;
+  }
+  __syncthreads();  // sKV
+
+  // ---- block scores S^T = K Q^T ----------------------------------------------------------
+  float s_t[4][4];  // [key tile][i]: key 16t + 4*grp + i of this lane's query
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    sf_f32x4 a = {0.f, 0.f, 0.f, 0.f};
+    if (t < nkt) {  // uniform
+      sf_u32x4 kf[4];
+#pragma unroll
+      for (int ds = 0; ds < 4; ++ds)
+        kf[ds] = *reinterpret_cast<const sf_u32x4*>(sKV + t * 16 * kRowBytes + k_frag_off(lane, ds));
+#pragma unroll
+      for (int ds = 0; ds < 4; ++ds) a = sf_mfma16x16x32(sf_as_bf16x8(kf[ds]), sf_as_bf16x8(qf[ds]), a);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = 16 * t + 4 * grp + i;
+      const bool keep = t < nkt && j < N && !(causal && j > n);
+      s_t[t][i] = keep ? a[i] : -INFINITY;   // exp2 gives 0
+    }
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s_t[t][i]);
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  const float m_new = fmaxf(m_run, mx * scale_log2);   // finite: key 0 is never masked
+  const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+  float lsum = 0.f;
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      s_t[t][i] = __builtin_amdgcn_exp2f(fmaf(s_t[t][i], scale_log2, -m_new));
+      lsum += s_t[t][i];
+    }
+  lsum += __shfl_xor(lsum, 16, 64);
+  lsum += __shfl_xor(lsum, 32, 64);
+  const float l_new = l_run * alpha + lsum;
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) acc[dt] = acc[dt] * alpha;
+
+  // ---- O^T += V^T P^T over 32-key blocks ---------------------------------------------------
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+    if (2 * kb < nkt) {  // uniform
+      float p2[2][4];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) p2[t][i] = s_t[2 * kb + t][i];   // 0 past the last tile
+      sf_bf16x8 pb[kPParts];
+      pv_parts<kPParts>(p2, pb);
+      sf_u32x2 vf[16];
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const sf_lds_off va = sf_lds_addr(sKV) + (uint32_t)(v_tr_off(lane, dt) + 32 * kb * kRowBytes);
+        vf[2 * dt] = sf_lds_read8_tr<0>(va);
+        vf[2 * dt + 1] = sf_lds_read8_tr<16 * kRowBytes>(va);
       }
-      for (int c = lane; c < nch; c += 64) {
-        const float wgt = __builtin_amdgcn_exp2f(sml[g][2 * c] - mm);
-        sml[g][2 * c] = wgt;
-        z += sml[g][2 * c + 1] * wgt;
-      }
-      z = sf_wave_sum(z);
-      if (lane == 0) {
-        sM[g] = mm;
-        sZ[g] = z;
+      sf_lds_reads_done(vf);
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const sf_u32x4 vw = {vf[2 * dt][0], vf[2 * dt][1], vf[2 * dt + 1][0], vf[2 * dt + 1][1]};
+        const sf_bf16x8 va = sf_as_bf16x8(vw);
+#pragma unroll
+        for (int pp = kPParts - 1; pp >= 0; --pp) acc[dt] = sf_mfma16x16x32(va, pb[pp], acc[dt]);
       }
     }
   }
-  __syncthreads();
 
-  // --- O = (sum_j p_j v_j + sum_c w_c acc_c) / Z --------------------------------------
-  if (mine) {
-    float o0 = 0.f, o1 = 0.f;
-    for (int j = 0; j < N; ++j) {
-      const float p = ss[my_g][j];
-      const uint32_t vv = *reinterpret_cast<const uint32_t*>(&sv[j][dp]);
-      o0 = fmaf(p, __uint_as_float(vv << 16), o0);
-      o1 = fmaf(p, __uint_as_float(vv & 0xffff0000u), o1);
-    }
-    for (int cb = 0; cb < nch; cb += kBatch) {
-      if (cb > 0) {
+  // ---- outputs ------------------------------------------------------------------------------
+  if (compute) {
+    const float inv = 1.0f / l_new;
+    const size_t off = (size_t)r * H * kHD + hq * kHD + grp * 4;
 #pragma unroll
-        for (int c = 0; c < kBatch; ++c)
-          accb[c] = *reinterpret_cast<const float2*>(
-              ws_o + (my_slot0 + (size_t)min(cb + c, nch - 1) * qmax) * kHD + dp);
-      }
-#pragma unroll
-      for (int c = 0; c < kBatch; ++c) {
-        if (cb + c < nch) {
-          const float wgt = sml[my_g][2 * (cb + c)];
-          o0 = fmaf(wgt, accb[c].x, o0);
-          o1 = fmaf(wgt, accb[c].y, o1);
-        }
-      }
+    for (int dt = 0; dt < 8; ++dt) {
+      const sf_f32x4 o = acc[dt] * inv;
+      *reinterpret_cast<sf_f32x4*>(o32 + off + dt * 16) = o;
+      sf_u32x2 w;
+      w[0] = sf_pack2(o[0], o[1]);
+      w[1] = sf_pack2(o[2], o[3]);
+      *reinterpret_cast<sf_u32x2*>(o_bf + off + dt * 16) = w;
     }
-    const float inv = 1.0f / sZ[my_g];
-    const float r0 = o0 * inv, r1 = o1 * inv;
-    const size_t off = (size_t)row * H * kHD + (h * G + my_g) * kHD + dp;
-    *reinterpret_cast<float2*>(o32 + off) = make_float2(r0, r1);
-    *reinterpret_cast<uint32_t*>(o_bf + off) = sf_pack2(r0, r1);
-    if (dp == 0) {
-      // the natural-base max the block scores and chunk maxima were measured from
-      m_tab[(size_t)row * H + h * G + my_g] = sM[my_g] * 0.69314718055994530942f;
-      z_tab[(size_t)row * H + h * G + my_g] = sZ[my_g];
+    if (grp == 0) {
+      // the natural-base max the scores were measured from
+      m_tab[(size_t)r * H + hq] = m_new * 0.69314718055994530942f;
+      z_tab[(size_t)r * H + hq] = l_new;
     }
   }
 }
 
-__global__ __launch_bounds__(512) void sf_attn_block_merge_kernel(
-    const uint16_t* __restrict__ q_buf, const uint16_t* __restrict__ kv_buf,
-    const int32_t* __restrict__ src, const int32_t* __restrict__ rows,
-    const int32_t* __restrict__ count_p, int bucket, int N, int H, int Hkv, float scale_log2,
-    int causal, const int32_t* __restrict__ p_len, int P_cap, int nchunks_cap, int qmax,
-    const float* __restrict__ ws_o, const float* __restrict__ ws_ml, float* __restrict__ o32,
-    uint16_t* __restrict__ o_bf, float* __restrict__ m_tab, float* __restrict__ z_tab) {
-  __shared__ float sq[kMaxG][kHD];
-  __shared__ __attribute__((aligned(16))) uint16_t sk[kMaxN][kHD];
-  __shared__ __attribute__((aligned(16))) uint16_t sv[kMaxN][kHD];
-  __shared__ float ss[kMaxG][kMaxN];
-  __shared__ float sml[kMaxG][2 * kMaxRanges];   // per q-head: (m, l) of every range
-  __shared__ float sM[kMaxG], sZ[kMaxG];
-  const int count = min(*count_p, bucket);
-  const int G = H / Hkv;
-  const int P = p_len ? min(*p_len, P_cap) : P_cap;
-  // number of prefix partials per query: the prefix kernel's chunk ranges
-  const int nch = merge_ranges(P, count * G, Hkv);
-  for (int it = blockIdx.x; it < count * Hkv; it += gridDim.x) {
-    merge_item(q_buf, kv_buf, src, rows, it / Hkv, it % Hkv, N, H, Hkv, G, scale_log2, causal, nch,
-               nchunks_cap, qmax, ws_o, ws_ml, o32, o_bf, m_tab, z_tab, sq, sk, sv, ss, sml, sM,
-               sZ);
-    __syncthreads();  // LDS is reused by the next item
+}  // namespace
+
+namespace {
+
+size_t partial_bytes(int bucket, int H, int P) {
+  return (size_t)ranges_cap(P) * bucket * H * (kHD + 2) * sizeof(float);
+}
+size_t state_offset(int bucket, int H, int P) { return (partial_bytes(bucket, H, P) + 255) & ~(size_t)255; }
+
+// The prefix pass, its merge and the finalize for the rows of branches
+// [b_first, b_first + b_count) (FOLDED: folded rows too).
+int attention(bool folded, const uint16_t* q_buf, const uint16_t* kv_buf,
+              const uint16_t* prefix_k, const uint16_t* prefix_v, const int32_t* page_table,
+              int P, int page_size, long long page_stride, long long head_stride,
+              const int32_t* src, const int32_t* rows, const int32_t* count, int bucket, int B1,
+              int N, int b_first, int b_count, int H, int Hkv, int hd, float scaling,
+              const int32_t* prefix_len, int block_causal, float* o32, uint16_t* o_bf,
+              float* m_tab, float* z_tab, void* workspace, size_t workspace_bytes,
+              hipStream_t st) {
+  if (!q_buf || !kv_buf || !src || !rows || !count || !o32 || !o_bf || !m_tab || !z_tab)
+    return SF_ERR_ARG;
+  if (hd != kHD || H < 1 || Hkv < 1 || H % Hkv != 0 || H / Hkv > kMaxG) return SF_ERR_SHAPE;
+  if (N < 1 || N > kMaxN || B1 < 1 || bucket < 1 || bucket > B1 * N) return SF_ERR_SHAPE;
+  if (b_first < 0 || b_count < 1 || b_first + b_count > B1) return SF_ERR_SHAPE;
+  if (P < 0 || nchunks_for(P) > kMaxChunks) return SF_ERR_SHAPE;
+  if (P > 0) {
+    if (!prefix_k || !prefix_v || !workspace) return SF_ERR_ARG;
+    // a page holds whole 16-key groups: 16, 32, 64 or 128 keys
+    if (page_table && (page_size < 16 || page_size > 128 || (page_size & (page_size - 1))))
+      return SF_ERR_SHAPE;
+    if (!page_table && head_stride < (long long)P * kHD) return SF_ERR_SHAPE;
+    if (workspace_bytes < sf_attn_workspace_bytes(bucket, H, P)) return SF_ERR_WORKSPACE;
+    if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0) return SF_ERR_ARG;
   }
+  const int G = H / Hkv;
+  const int qmax = bucket * G;
+  const float scale_log2 = scaling * 1.44269504088896340736f;
+  float* state = nullptr;
+  if (P > 0) {
+    const int nch = nchunks_for(P);
+    const int nr_cap = ranges_cap(P);
+    const size_t nslot = (size_t)nr_cap * qmax * Hkv;
+    float* ws_o = reinterpret_cast<float*>(workspace);
+    float* ws_ml = ws_o + nslot * kHD;
+    state = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) +
+                                     state_offset(bucket, H, P));
+    // persistent grid: one 136 KB-LDS workgroup per CU; a multiple of 8
+    const int grid = prefix_launch_grid(qmax, nch, Hkv);
+    hipLaunchKernelGGL(sf_attn_prefix_kernel, dim3(grid), dim3(kPrefixThreads), 0, st, q_buf,
+                       prefix_k, prefix_v, page_table, page_size, page_stride, head_stride,
+                       prefix_len, P, rows, count, bucket, H, Hkv, scale_log2, qmax, nr_cap, ws_o,
+                       ws_ml);
+    hipLaunchKernelGGL(sf_attn_prefix_merge_kernel, dim3((bucket * H + 3) / 4), dim3(256), 0, st,
+                       count, bucket, H, Hkv, prefix_len, P, nr_cap, qmax, ws_o, ws_ml, state);
+  }
+  const dim3 grid3(b_count * Hkv * ((N + kFinRows - 1) / kFinRows));
+  if (folded)
+    hipLaunchKernelGGL(sf_attn_finalize_kernel<true>, grid3, dim3(256), 0, st, q_buf, kv_buf, src,
+                       rows, count, bucket, N, b_first, H, Hkv, scale_log2, block_causal ? 1 : 0,
+                       P > 0 ? 1 : 0, state, o32, o_bf, m_tab, z_tab);
+  else
+    hipLaunchKernelGGL(sf_attn_finalize_kernel<false>, grid3, dim3(256), 0, st, q_buf, kv_buf, src,
+                       rows, count, bucket, N, b_first, H, Hkv, scale_log2, block_causal ? 1 : 0,
+                       P > 0 ? 1 : 0, state, o32, o_bf, m_tab, z_tab);
+  return sf_launch_status();
 }
 
 }  // namespace
@@ -583,9 +734,10 @@ __global__ __launch_bounds__(512) void sf_attn_block_merge_kernel(
 extern "C" size_t sf_attn_workspace_bytes(int bucket, int H, int P) {
   if (bucket < 1 || H < 1 || P < 0) return 0;
   if (P == 0) return 16;
-  // per (kv head, chunk range, query): 128 fp32 acc + (m, l); queries per kv head =
-  // bucket*G, so the total over kv heads is ranges * bucket * H slots.
-  return (size_t)ranges_cap(P) * bucket * H * (kHD + 2) * sizeof(float);
+  // the range partials: per (kv head, chunk range, query) 128 fp32 acc + (m, l), with
+  // bucket*G queries per kv head: ranges * bucket * H slots; then (256-aligned) the
+  // merged prefix state of every (compacted row, q-head): 132 floats
+  return state_offset(bucket, H, P) + (size_t)bucket * H * kStateFloats * sizeof(float);
 }
 
 extern "C" int sf_attn_prefix_block(const uint16_t* q_buf, const uint16_t* kv_buf,
@@ -595,45 +747,24 @@ extern "C" int sf_attn_prefix_block(const uint16_t* q_buf, const uint16_t* kv_bu
                                     const int32_t* src, const int32_t* rows, const int32_t* count,
                                     int bucket, int B1, int N, int H, int Hkv, int hd,
                                     float scaling, const int32_t* prefix_len, int block_causal,
-                                    float* o32,
-                                    uint16_t* o_bf, float* m_tab, float* z_tab, void* workspace,
-                                    size_t workspace_bytes, void* stream) {
-  if (!q_buf || !kv_buf || !src || !rows || !count || !o32 || !o_bf || !m_tab || !z_tab)
-    return SF_ERR_ARG;
-  if (hd != kHD || H < 1 || Hkv < 1 || H % Hkv != 0 || H / Hkv > kMaxG) return SF_ERR_SHAPE;
-  if (N < 1 || N > kMaxN || B1 < 1 || bucket < 1 || bucket > B1 * N) return SF_ERR_SHAPE;
-  if (P < 0 || nchunks_for(P) > kMaxChunks) return SF_ERR_SHAPE;
-  if (P > 0) {
-    if (!prefix_k || !prefix_v || !workspace) return SF_ERR_ARG;
-    // a page holds whole 16-key groups: 16, 32, 64 or 128 keys
-    if (page_table && (page_size < 16 || page_size > 128 || (page_size & (page_size - 1))))
-      return SF_ERR_SHAPE;
-    if (!page_table && head_stride < (long long)P * kHD) return SF_ERR_SHAPE;
-    if (workspace_bytes < sf_attn_workspace_bytes(bucket, H, P)) return SF_ERR_WORKSPACE;
-  }
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const int G = H / Hkv;
-  const int qmax = bucket * G;
-  const int nch = P > 0 ? nchunks_for(P) : 0;
-  const int nr_cap = P > 0 ? ranges_cap(P) : 0;
-  const float scale_log2 = scaling * 1.44269504088896340736f;
-  float* ws_ml = nullptr;
-  float* ws_o = nullptr;
-  if (P > 0) {
-    const size_t nslot = (size_t)nr_cap * qmax * Hkv;
-    ws_o = reinterpret_cast<float*>(workspace);
-    ws_ml = ws_o + nslot * kHD;
-    // persistent grid: one 128 KB-LDS workgroup per CU; a multiple of 8
-    const int grid = prefix_launch_grid(qmax, nch, Hkv);
-    hipLaunchKernelGGL(sf_attn_prefix_kernel, dim3(grid), dim3(kPrefixThreads), 0, st, q_buf,
-                       prefix_k, prefix_v, page_table, page_size, page_stride, head_stride,
-                       prefix_len, P, rows, count, bucket, H, Hkv, scale_log2, qmax, nr_cap, ws_o,
-                       ws_ml);
-  }
-  const int grid2 = min(bucket * Hkv, 2 * kCUs);
-  hipLaunchKernelGGL(sf_attn_block_merge_kernel, dim3(grid2), dim3(512), 0, st, q_buf, kv_buf,
-                     src, rows, count, bucket, N, H, Hkv, scale_log2, block_causal ? 1 : 0,
-                     P > 0 ? prefix_len : nullptr,
-                     P, nr_cap, qmax, ws_o, ws_ml, o32, o_bf, m_tab, z_tab);
-  return sf_launch_status();
+                                    float* o32, uint16_t* o_bf, float* m_tab, float* z_tab,
+                                    void* workspace, size_t workspace_bytes, void* stream) {
+  return attention(false, q_buf, kv_buf, prefix_k, prefix_v, page_table, P, page_size,
+                   page_stride, head_stride, src, rows, count, bucket, B1, N, 0, B1, H, Hkv, hd,
+                   scaling, prefix_len, block_causal, o32, o_bf, m_tab, z_tab, workspace,
+                   workspace_bytes, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int sf_attn_rows(const uint16_t* q_buf, const uint16_t* kv_buf,
+                            const uint16_t* prefix_k, const uint16_t* prefix_v,
+                            const int32_t* page_table, int P, int page_size, long long page_stride,
+                            long long head_stride, const int32_t* src, const int32_t* rows,
+                            const int32_t* count, int bucket, int B1, int N, int b_first,
+                            int b_count, int H, int Hkv, int hd, float scaling,
+                            const int32_t* prefix_len, float* o32, uint16_t* o_bf, float* m_tab,
+                            float* z_tab, void* workspace, size_t workspace_bytes, void* stream) {
+  return attention(true, q_buf, kv_buf, prefix_k, prefix_v, page_table, P, page_size, page_stride,
+                   head_stride, src, rows, count, bucket, B1, N, b_first, b_count, H, Hkv, hd,
+                   scaling, prefix_len, 0, o32, o_bf, m_tab, z_tab, workspace, workspace_bytes,
+                   reinterpret_cast<hipStream_t>(stream));
 }

@@ -5,17 +5,22 @@ branches of one N-token block over a prefix KV cache, all layers, and returns
 the (unshifted) logits.  Per layer (reference: specfold/generate/
 fastdllm_v2_folded.py:296-361 for the launch sequence, :117-220 for the math):
 
-  sf_fold_gate       gate + compaction + src + input RMSNorm   (HIP)
+  sf_fold_gate(_residual)  the previous layer's residual update + gate +
+                     compaction + src + input RMSNorm          (HIP)
   sf_qkv_rope        QKV MFMA GEMM + bias + RoPE + scatter     (HIP)
   sf_kv_append       optional in-place append (block commit)   (HIP)
-  sf_attn_prefix_block  prefix + block attention with (m, Z)   (HIP)
-  sf_chain_correct   folded rows' exact softmax update         (HIP)
-  o_proj + residual for every row (M = B1*N)             (torch mm + add, hipBLASLt)
-  sf_rows_rmsnorm     post-attention RMSNorm of recomputed rows  (HIP)
+  sf_attn_rows       attention of every row with (m, Z): recomputed rows over
+                     [prefix ; own block], folded rows from their source row's
+                     query over their own branch's keys (the chain correction's
+                     result)                                   (HIP)
+  o_proj for every row (M = B1*N)                        (torch mm, hipBLASLt)
+  sf_residual_post_norm  hp = x + attn_out, post-attention RMSNorm of the
+                     recomputed rows                           (HIP)
   sf_ffn_gate_up      gate/up GEMM + SiLU*mul on compacted rows  (HIP)
   sf_ffn_down_scatter down GEMM, scattered to the per-row FFN table (HIP)
-  sf_residual_gather_add  h = hp + ffn[src] (folded rows reuse)  (HIP)
-and after the last layer the final RMSNorm (HIP) and the lm_head (hipBLASLt).
+and after the last layer the residual update + final RMSNorm (HIP) and the
+lm_head (hipBLASLt).  sf_chain_correct (the reference's incremental form of the
+folded rows' attention) stays in the C ABI; the engine forms it with sf_attn_rows.
 
 Nothing here syncs with the host: the branch parent map is computed from the
 tokens on the device (sf_parent_map; the reference copies the tokens to the host
@@ -375,11 +380,11 @@ class FoldedVerifyEngine:
                    on the number of sequences only.  A copy is no branch's parent
                    and leaves every other row's result unchanged; it gates as
                    folded (no GEMM rows, no attention) wherever delta > 0.  At
-                   delta = 0 a copy's chain-corrected attention output, which may
+                   delta = 0 a copy's folded-row attention output, which may
                    round one bf16 step away from its main branch's, can make it
                    recompute at later layers: extra rows, same results.
         The sequences' branches are stacked into one step of sum(B1_s) branches:
-        the gate, compaction, GEMMs and chain correction run once over all of them
+        the gate, compaction and GEMMs run once over all of them
         (the main branch of every sequence is a root: SF_GATE_ROOTS_BY_PARENT), the
         QKV epilogue ropes each branch at its sequence's positions, and attention
         runs per sequence over its own prefix.  Each sequence's result is that of
@@ -532,18 +537,19 @@ class FoldedVerifyEngine:
                                        buf.kv_buf, buf.ws_qkv, batch.pos0_branch)
             if append:
                 cache.append_rows(li, buf.kv_buf, 0, N)
+            # attention of every row (fastdllm_v2_folded.py:164-204): the recomputed
+            # rows over [prefix ; own block], the folded rows from their source row's
+            # query over their own branch's keys (what the chain correction computes)
             if batch is None:
                 self._attention(buf, cache, li, count, bucket, B1, N, causal=causal)
             else:
-                # each sequence's recomputed rows over its own prefix: the compacted
-                # rows are ascending, so sequence s owns a contiguous run of them
+                # each sequence's rows over its own prefix: the compacted rows are
+                # ascending, so sequence s owns a contiguous run of them
                 rows_s, count_s = batch.split_rows(buf.rows, count, bucket, N)
                 for si, c in enumerate(batch.caches):
                     self._attention(buf, c, li, count_s[si:si + 1], bucket, B1, N,
-                                    rows=rows_s[si])
-            _lib.chain_correct(buf.q_buf, buf.kv_buf, buf.src, par, buf.rec, buf.seg, segcnt,
-                               B1, N, H, Hkv, hd, self.scaling, buf.o32, buf.o_bf, buf.m_tab,
-                               buf.z_tab)
+                                    rows=rows_s[si],
+                                    branches=(batch.offsets[si], batch.sizes[si]))
 
             # o_proj for every row (fastdllm_v2_folded.py:207-209): M = BN is a regular
             # GEMM shape, where hipBLASLt beats the skinny-M streaming kernel; then one
@@ -578,7 +584,10 @@ class FoldedVerifyEngine:
         return last
 
     def _attention(self, buf: _Buffers, cache, li: int, count, bucket: int, B1: int, N: int,
-                   causal: bool = False, rows: Optional[torch.Tensor] = None):
+                   causal: bool = False, rows: Optional[torch.Tensor] = None,
+                   branches: Optional[Tuple[int, int]] = None):
+        """Every row of the branches (first, count) (default: all): sf_attn_rows; a
+        causal forward (every row recomputed) takes sf_attn_prefix_block."""
         pv = prefix_view(cache, li)
         if pv is None:
             P_arg, plen = 0, None
@@ -586,13 +595,20 @@ class FoldedVerifyEngine:
             P_arg, plen = pv.capacity, pv.length_dev
         else:
             P_arg, plen = pv.length, None
-        _lib.attn_prefix_block(
-            buf.q_buf, buf.kv_buf, pv.k if pv else None, pv.v if pv else None,
-            pv.page_table if pv else None, P_arg, pv.page_size if pv else 1,
-            pv.page_stride if pv else 0, pv.head_stride if pv else 0,
-            buf.src, buf.rows if rows is None else rows, count, bucket, B1, N, self.H, self.Hkv,
-            self.hd, self.scaling, buf.o32, buf.o_bf, buf.m_tab, buf.z_tab, buf.ws_attn,
-            prefix_len=plen, block_causal=causal)
+        view = (pv.k if pv else None, pv.v if pv else None, pv.page_table if pv else None, P_arg,
+                pv.page_size if pv else 1, pv.page_stride if pv else 0,
+                pv.head_stride if pv else 0)
+        rows = buf.rows if rows is None else rows
+        if causal:
+            _lib.attn_prefix_block(buf.q_buf, buf.kv_buf, *view, buf.src, rows, count, bucket, B1,
+                                   N, self.H, self.Hkv, self.hd, self.scaling, buf.o32, buf.o_bf,
+                                   buf.m_tab, buf.z_tab, buf.ws_attn, prefix_len=plen,
+                                   block_causal=True)
+        else:
+            b0, nb = branches if branches is not None else (0, B1)
+            _lib.attn_rows(buf.q_buf, buf.kv_buf, *view, buf.src, rows, count, bucket, B1, N,
+                           b0, nb, self.H, self.Hkv, self.hd, self.scaling, buf.o32, buf.o_bf,
+                           buf.m_tab, buf.z_tab, buf.ws_attn, prefix_len=plen)
 
     @staticmethod
     def _cache_key(cache):
@@ -692,11 +708,6 @@ class FoldedVerifyEngine:
         def attn():
             self._attention(buf, cache, li, count, bucket, B1, N)
 
-        def chain():
-            _lib.chain_correct(buf.q_buf, buf.kv_buf, buf.src, st["par"], buf.rec, buf.seg, segcnt,
-                               B1, N, H, Hkv, hd, self.scaling, buf.o32, buf.o_bf, buf.m_tab,
-                               buf.z_tab)
-
         def o_proj():
             torch.mm(buf.o_bf, lyr.self_attn.o_proj.weight.t(), out=buf.attn_out)
 
@@ -720,7 +731,7 @@ class FoldedVerifyEngine:
         def lm_head():
             torch.mm(buf.final, self.head.weight.t(), out=logits)
 
-        out = dict(qkv=qkv, attn=attn, chain=chain, o_proj=o_proj, post_norm=post_norm,
+        out = dict(qkv=qkv, attn=attn, o_proj=o_proj, post_norm=post_norm,
                    gate_up=gate_up, down=down, final_norm=final_norm, lm_head=lm_head, gate=gate)
         if isinstance(cache, PagedKVCache) and cache.length + N <= cache.capacity:
             def append():

@@ -259,19 +259,19 @@ def compare_layer(li: int, lt: LayerTrace, ht: dict, parent, B1: int, N: int, H:
     out["O"] = st
     if st["max_abs"] > NS_MAX_ABS * max(st["ref_absmax"], 1.0):
         fails.append("O")
-    for nm, a, b in (("m", m_hip, lt.m.permute(0, 2, 1)), ("Z", z_hip, lt.Z.permute(0, 2, 1))):
-        st = err_stats(a, b)
-        out[nm] = st
-        if st["max_abs"] > NS_MAX_ABS * max(st["ref_absmax"], 1.0):
-            fails.append(nm)
+    # (m, Z) is fixed only up to Z * exp(m): a folded row's m is the reference chain's
+    # running bound max(m0, new scores) (fastdllm_v2_folded.py:183-204), which a
+    # replaced key can leave above the row's own maximum; the kernels report the
+    # row's own maximum.  Their log-sum-exp m + log Z is the same quantity.
+    lse_hip = m_hip.double() + torch.log(z_hip.double())
+    st = err_stats(lse_hip.float(), (lt.m.permute(0, 2, 1).double()
+                                     + torch.log(lt.Z.permute(0, 2, 1).double())).float())
+    out["lse"] = st
+    if st["max_abs"] > NS_MAX_ABS * max(st["ref_absmax"], 1.0):
+        fails.append("lse")
     if eng is not None:
         fo, fm, fz = attention_forced(ht, prefix_kv, B1, N, H, Hkv, hd, eng.scaling,
                                       device=ht["q"].device)
-        # (m, Z) is fixed only up to Z * exp(m): a folded row's m is the chain's
-        # running bound max(m0, new scores) (fastdllm_v2_folded.py:183-204), which
-        # a replaced key can leave above the row's own maximum; compare the
-        # log-sum-exp m + log Z
-        lse_hip = m_hip.double() + torch.log(z_hip.double())
         lse_ref = fm + torch.log(fz)
         for nm, a, b in (("O|qkv", o_hip, fo), ("lse|qkv", lse_hip, lse_ref)):
             st = err_stats(a.float(), b.float())

@@ -65,11 +65,13 @@ int main(int argc, char** argv) {
   std::vector<float> o32((size_t)BN * H * hd, NAN), mt((size_t)BN * H, NAN), zt((size_t)BN * H, NAN);
   std::vector<uint16_t> obf((size_t)BN * H * hd);
   const size_t wsb = sf_attn_workspace_bytes(bucket, H, P);
-  std::vector<float> ws(wsb / 4 + 16);
+  std::vector<float> ws_store(wsb / 4 + 128);  // the entry point wants 256-byte alignment
+  float* ws_al = reinterpret_cast<float*>((reinterpret_cast<uintptr_t>(ws_store.data()) + 255) &
+                                          ~static_cast<uintptr_t>(255));
   const int st = sf_attn_prefix_block(q.data(), kv.data(), pk.data(), pv.data(), table.data(), P, ps,
                                       page_stride, head_stride, src.data(), rows.data(), &count,
                                       bucket, B1, N, H, Hkv, hd, scaling, &plen, causal, o32.data(),
-                                      obf.data(), mt.data(), zt.data(), ws.data(), wsb, nullptr);
+                                      obf.data(), mt.data(), zt.data(), ws_al, wsb, nullptr);
   if (st != 0) {
     fprintf(stderr, "sf_attn_prefix_block returned %d\n", st);
     return 1;

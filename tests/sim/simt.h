@@ -100,6 +100,13 @@ inline int sim_readfirstlane(int v) {
 }
 #define __builtin_amdgcn_readfirstlane(x) sim_readfirstlane(x)
 
+inline float __shfl(float v, int src, int width = 64) {
+  (void)width;
+  float out;
+  sim_wave_exchange(&v, 4, [&](const uint8_t* b) { memcpy(&out, b + (src & 63) * 128, 4); });
+  return out;
+}
+
 inline float __shfl_xor(float v, int mask, int width = 64) {
   (void)width;
   float out;
