@@ -59,6 +59,14 @@ def parse_args(argv=None):
                          "one batched verify step per round (a step = one round)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also time a plain 256 MiB device copy (counter calibration)")
+    ap.add_argument("--pmc-pass", action="store_true",
+                    help="for rocprofv3 --pmc runs: after the decode steps and one verify step, "
+                         "a 0.5 s pause, the copy calibration, then every entry point launched "
+                         "once per layer in PMC_ORDER (no JSON line)")
+    ap.add_argument("--traffic-table", nargs="+", metavar="CSV",
+                    help="on the host: build profiles/traffic_<workload>.json from the "
+                         "counter_collection.csv files of --pmc-pass runs (FETCH_SIZE, "
+                         "WRITE_SIZE, optionally the MFMA counters)")
     return ap.parse_args(argv)
 
 
@@ -153,6 +161,102 @@ def kernel_roofline(name, ms, w, R, B1, N, P):
 
 # kernels launched once per verify step (the others once per layer)
 ONCE_PER_STEP = ("lm_head", "final_norm")
+
+
+# --pmc-pass launch order and the kernels each entry point runs (name prefixes, after
+# stripping "void " and the anonymous namespace), for the verify step's shape
+PMC_ORDER = ("qkv", "attn", "o_proj", "post_norm", "gate_up", "down", "final_norm", "lm_head",
+             "gate")
+PMC_KERNELS = {
+    "qkv": ("sfg::gemm_sk_kernel<1, 0,", "sf_qkv_epilogue_kernel"),
+    "attn": ("sf_attn_prefix_kernel", "sf_attn_prefix_merge_kernel", "sf_attn_finalize_kernel"),
+    "o_proj": ("Cijk_",),
+    "post_norm": ("residual_post_norm_kernel",),
+    "gate_up": ("sfg::gemm_sk_kernel<2, 2,", "silu_fixup_kernel"),
+    "down": ("sfg::gemm_sk_kernel<1, 1,", "down_fixup_kernel"),
+    "final_norm": ("sf_gate_rows_kernel",),
+    "lm_head": ("Cijk_",),
+    "gate": ("sf_gate_rows_kernel", "sf_gate_compact_kernel"),
+}
+
+
+def _kernel_short(name: str) -> str:
+    return name.replace("void ", "").replace("(anonymous namespace)::", "")
+
+
+def traffic_table(csvs, workload: str) -> dict:
+    """Per entry point HBM bytes per launch from --pmc-pass runs: the dispatches after
+    the pass's pause are walked in PMC_ORDER (qkv, attn, ... once per layer, the
+    once-per-step ones once), FETCH_SIZE and WRITE_SIZE (KiB per dispatch) are summed
+    over each launch's kernels and scaled by what the same counters read for the
+    plain copy of known size launched first in the pause (y = 2x, 256 MiB fp32).  MFMA
+    counters, when collected, give each launch's MFMA busy fraction."""
+    import csv as _csv
+    from specfold_amd.configs import workload as get_workload
+
+    w = get_workload(workload)
+    L = w.shape.layers
+    per = {}   # counter -> ordered list of (kernel, value) after the pause
+    for path in csvs:
+        rows = list(_csv.DictReader(open(path)))
+        by_disp = {}
+        for r in rows:
+            d = by_disp.setdefault(int(r["Dispatch_Id"]), {"name": _kernel_short(r["Kernel_Name"]),
+                                                           "t0": int(r["Start_Timestamp"]),
+                                                           "grid": int(r["Grid_Size"])})
+            d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        seq = [by_disp[k] for k in sorted(by_disp)]
+        # the pause: the largest start-time gap in the run's second half
+        half = len(seq) // 2
+        gaps = [(seq[i + 1]["t0"] - seq[i]["t0"], i + 1) for i in range(half, len(seq) - 1)]
+        start = max(gaps)[1]
+        for d in seq[start:]:
+            for c, v in d.items():
+                if c not in ("name", "t0", "grid"):
+                    per.setdefault(c, []).append((d["name"], v, d["grid"]))
+    out = {"workload": workload, "kernels": {}}
+    for counter, seq in per.items():
+        # calibration copy first (the largest elementwise dispatch), then PMC_ORDER
+        cal = seq[0]
+        i = 1
+        table = {}
+        for name in PMC_ORDER:
+            launches = 1 if name in ONCE_PER_STEP else L
+            pats = PMC_KERNELS[name]
+            vals = []
+            for _ in range(launches):
+                tot = 0.0
+                for pat in pats:
+                    while i < len(seq) and not seq[i][0].startswith(pat):
+                        i += 1   # kernels of other libraries between ours (e.g. torch copies)
+                    if i >= len(seq):
+                        raise ValueError(f"{counter}: ran out of dispatches at {name}/{pat}")
+                    tot += seq[i][1]
+                    i += 1
+                vals.append(tot)
+            table[name] = sum(vals) / len(vals)
+        out.setdefault("raw", {})[counter] = {"calibration": cal[1], **table}
+    cal_bytes = 256 << 20
+    f = out["raw"].get("FETCH_SIZE")
+    wr = out["raw"].get("WRITE_SIZE")
+    if f and wr:
+        ff = cal_bytes / (f["calibration"] * 1024)
+        wf = cal_bytes / (wr["calibration"] * 1024)
+        out["calibration"] = {"kernel": "vectorized_elementwise_kernel fp32 y=2x, 256 MiB",
+                              "fetch_factor": round(ff, 4), "write_factor": round(wf, 4)}
+        for name in PMC_ORDER:
+            b = f[name] * 1024 * ff + wr[name] * 1024 * wf
+            out["kernels"][name] = {"fetch_kib_raw": round(f[name], 1),
+                                    "write_kib_raw": round(wr[name], 1),
+                                    "bytes_per_launch": int(b)}
+    mb = out["raw"].get("SQ_VALU_MFMA_BUSY_CYCLES")
+    ga = out["raw"].get("GRBM_GUI_ACTIVE")
+    if mb and ga:
+        simds = 256 * 4
+        for name in PMC_ORDER:
+            k = out["kernels"].setdefault(name, {})
+            k["mfma_busy"] = round(mb[name] / (ga[name] * simds), 4) if ga[name] else None
+    return out
 
 
 def load_traffic(workload: str) -> dict:
@@ -381,6 +485,19 @@ def make_decoders(w):
 @torch.no_grad()
 def main(argv=None) -> int:
     args = parse_args(argv)
+    if args.traffic_table:
+        import subprocess
+        tab = traffic_table(args.traffic_table, args.workload)
+        try:
+            tab["commit"] = subprocess.run(["git", "rev-parse", "--short=12", "HEAD"], cwd=ROOT,
+                                           capture_output=True, text=True).stdout.strip() or None
+        except OSError:
+            tab["commit"] = None
+        tab["sources"] = [str(Path(c)) for c in args.traffic_table]
+        path = ROOT / "profiles" / f"traffic_{args.workload}.json"
+        path.write_text(json.dumps(tab, indent=1) + "\n")
+        print(f"wrote {path.relative_to(ROOT)}")
+        return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the verify step is a single-GPU path in this build "
               "(multi-GPU sharding is design-only); run with --gpus 1", file=sys.stderr)
@@ -507,6 +624,29 @@ def main(argv=None) -> int:
                         "ms_per_sequence": round(ms_b / len(reqs), 4)}
         print(f"[bench] batched verify step ({len(reqs)} sequences) median {ms_b:.3f} ms",
               file=sys.stderr, flush=True)
+
+    if args.pmc_pass:
+        # the counted section: after a pause (the parser finds it by the gap), one
+        # plain copy of known size, then every entry point once per layer on the
+        # buffers of the verify step just run
+        eng = gen._engine
+        n = (256 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        shared = {}
+        per_layer = [eng.profile_launchers(li=li, shared=shared) for li in range(eng.L)]
+        torch.cuda.synchronize()
+        time.sleep(0.5)
+        torch.mul(src, 2.0, out=dst)
+        for name in PMC_ORDER:
+            if name in ONCE_PER_STEP:
+                per_layer[-1][0][name]()
+            else:
+                for pl in per_layer:
+                    pl[0][name]()
+        torch.cuda.synchronize()
+        print(f"[bench] pmc pass done ({w.name}, R {R})", file=sys.stderr, flush=True)
+        return 0
 
     # per-kernel timings on the buffers of the last verify step, cycling through the
     # layers (weights and cache slices) as the step does

@@ -35,9 +35,10 @@ def test_roofline_bytes_follow_the_unit_figures(name):
     assert k["bound"] == "hbm"
     assert k["frac"] == pytest.approx(k["algorithmic_bytes"] / 50e-6 / 8e12, rel=1e-3)
     a = bench.kernel_roofline("attn", 0.05, w, R, B1, N, P)
-    assert a["algorithmic_bytes"] == (2 * Hkv * P * hd * 2 + B1 * N * 2 * Hkv * hd * 2
-                                      + 2 * R * H * hd * 2 + 8 * R * H)
-    assert a["algorithmic_flops"] == 4 * R * H * (P + N) * hd
+    BN = B1 * N
+    assert a["algorithmic_bytes"] == (2 * Hkv * P * hd * 2 + BN * 2 * Hkv * hd * 2
+                                      + R * H * hd * 2 + BN * H * hd * (4 + 2) + 8 * BN * H)
+    assert a["algorithmic_flops"] == 4 * R * H * P * hd + 4 * BN * H * N * hd
     q = bench.kernel_roofline("qkv", 0.02, w, R, B1, N, P)
     nq = (H + 2 * Hkv) * hd
     bias = nq * 2 if sh.qkv_bias else 0
@@ -46,12 +47,60 @@ def test_roofline_bytes_follow_the_unit_figures(name):
         bench.kernel_roofline("nope", 1.0, w, R, B1, N, P)
 
 
-def test_committed_traffic_table_is_per_launch_bytes():
-    t = bench.load_traffic("cfg3_7b")
-    assert t["gate_up"] > 2.7e8                      # the 271 MB weight stream, read once
-    raw = json.loads((bench.ROOT / "profiles" / "traffic_cfg3_7b.json").read_text())
-    for name, v in raw["kernels"].items():
-        assert v["bytes_per_launch"] == t[name]
+def _pmc_csv(path, w, fetch_kib, write_kib, cal_kib):
+    """A counter_collection.csv as rocprofv3 --pmc writes it for one --pmc-pass run:
+    the verify steps before the pause, then the calibration copy and PMC_ORDER's
+    launches (one per layer, the once-per-step ones once), with a torch copy
+    between two of them."""
+    import csv
+    rows, disp, t = [], 0, 0
+
+    def emit(name, kib_f, kib_w, gap=1000):
+        nonlocal disp, t
+        disp += 1
+        t += gap
+        for c, v in (("FETCH_SIZE", kib_f), ("WRITE_SIZE", kib_w)):
+            rows.append({"Dispatch_Id": disp, "Kernel_Name": "void " + name,
+                         "Start_Timestamp": t, "Grid_Size": 256, "Counter_Name": c,
+                         "Counter_Value": v})
+
+    L = w.shape.layers
+    n_after = 1 + sum(len(bench.PMC_KERNELS[n]) * (1 if n in bench.ONCE_PER_STEP else L)
+                      for n in bench.PMC_ORDER) + 1
+    for _ in range(n_after + 5):
+        emit("warmup_kernel", 7.0, 3.0)
+    emit("vectorized_elementwise_kernel", cal_kib, cal_kib, gap=10 ** 9)   # the pause
+    for name in bench.PMC_ORDER:
+        for li in range(1 if name in bench.ONCE_PER_STEP else L):
+            for j, pat in enumerate(bench.PMC_KERNELS[name]):
+                emit(pat + "x>(int)", fetch_kib[name] + li + j, write_kib[name])
+            if name == "attn" and li == 0:
+                emit("elementwise_kernel_copy", 1e6, 1e6)
+    with open(path, "w", newline="") as f:
+        wr = csv.DictWriter(f, fieldnames=list(rows[0]))
+        wr.writeheader()
+        wr.writerows(rows)
+
+
+def test_traffic_table_scales_each_launch_by_the_copy_calibration(tmp_path):
+    """Bytes per launch = mean over layers of the sum over the launch's kernels of
+    FETCH_SIZE and WRITE_SIZE (KiB), times 256 MiB / the calibration copy's reading;
+    kernels of other libraries between ours are skipped."""
+    w = workload("cfg3_7b")
+    L = w.shape.layers
+    fetch = {n: 100.0 * (i + 1) for i, n in enumerate(bench.PMC_ORDER)}
+    write = {n: 10.0 * (i + 1) for i, n in enumerate(bench.PMC_ORDER)}
+    cal = (256 << 20) / 1024 / 2.0          # the counter reads half the copy's bytes
+    p = tmp_path / "counter_collection.csv"
+    _pmc_csv(p, w, fetch, write, cal)
+    out = bench.traffic_table([str(p)], "cfg3_7b")
+    assert out["calibration"]["fetch_factor"] == pytest.approx(2.0)
+    for name in bench.PMC_ORDER:
+        k = len(bench.PMC_KERNELS[name])
+        n = 1 if name in bench.ONCE_PER_STEP else L
+        f_mean = sum(fetch[name] * k + k * li + k * (k - 1) / 2 for li in range(n)) / n
+        want = (f_mean + write[name] * k) * 1024 * 2.0
+        assert out["kernels"][name]["bytes_per_launch"] == int(want), name
     assert bench.load_traffic("no_such_workload") == {}
 
 
