@@ -122,12 +122,10 @@ def kernel_roofline(name, ms, w, R, B1, N, P):
         by = 2 * (2 * N * Hkv * hd * e)
         fl = 0
     elif name == "o_proj":
-        by = D * H * hd * e + BN * H * hd * e + BN * D * e
-        fl = 2 * BN * H * hd * D
-    elif name == "post_norm":
-        # residual add of every row + RMSNorm of the R recomputed rows
-        by = 3 * BN * D * e + R * D * e + D * e
-        fl = BN * D + 4 * R * D
+        # o_proj of every row fused with the residual (x in, hp out) and the
+        # post-attention RMSNorm of the R recomputed rows (zn out, norm weight)
+        by = D * H * hd * e + BN * H * hd * e + 2 * BN * D * e + R * D * e + D * e
+        fl = 2 * BN * H * hd * D + BN * D + 4 * R * D
     elif name == "gate_up":
         I = sh.intermediate
         by = 2 * I * D * e + R * D * e + R * I * e
@@ -165,17 +163,15 @@ ONCE_PER_STEP = ("lm_head", "final_norm")
 
 # --pmc-pass launch order and the kernels each entry point runs (name prefixes, after
 # stripping "void " and the anonymous namespace), for the verify step's shape
-PMC_ORDER = ("qkv", "attn", "o_proj", "post_norm", "gate_up", "down", "final_norm", "lm_head",
-             "gate")
+PMC_ORDER = ("qkv", "attn", "o_proj", "gate_up", "down", "final_norm", "lm_head", "gate")
 PMC_KERNELS = {
     "qkv": ("sfg::gemm_sk_kernel<1, 0,", "sf_qkv_epilogue_kernel"),
     "attn": ("sf_attn_prefix_kernel", "sf_attn_prefix_merge_kernel", "sf_attn_finalize_kernel"),
-    "o_proj": ("Cijk_",),
-    "post_norm": ("residual_post_norm_kernel",),
+    "o_proj": ("sfg::gemm_rows_kernel<", "part_residual_norm_kernel"),
     "gate_up": ("sfg::gemm_sk_kernel<2, 2,", "silu_fixup_kernel"),
     "down": ("sfg::gemm_sk_kernel<1, 1,", "down_fixup_kernel"),
     "final_norm": ("sf_gate_rows_kernel",),
-    "lm_head": ("Cijk_",),
+    "lm_head": ("sfg::gemm_rows_kernel<",),
     "gate": ("sf_gate_rows_kernel", "sf_gate_compact_kernel"),
 }
 
@@ -398,8 +394,8 @@ def kernel_table(w, eng, B1, N, kernel_iters):
     P = info["prefix"]
     R = int(info["count"].item())
     kernels = {}
-    for name in ("qkv", "attn", "o_proj", "post_norm", "gate_up", "down", "final_norm",
-                 "lm_head", "append", "gate"):
+    for name in ("qkv", "attn", "o_proj", "gate_up", "down", "final_norm", "lm_head", "append",
+                 "gate"):
         if name not in per_layer[-1][0]:
             continue
         once = name in ONCE_PER_STEP

@@ -61,7 +61,9 @@ const char* sf_status_string(int status);
  * 4: batched verify steps: SF_GATE_ROOTS_BY_PARENT, sf_qkv_rope_branches.
  * 5: GEMMs on 64-wide K chunks (K % 64, N % 128); sf_ffn_gate_up takes a workspace.
  * 6: sf_logit_stats_noalloc, SF_ERR_SCRATCH.
- * 7: sf_attn_rows; the attention workspace holds the merged prefix states. */
+ * 7: sf_attn_rows; the attention workspace holds the merged prefix states.
+ * 8: all-rows o_proj / lm_head: sf_o_proj_post_norm, sf_o_proj_workspace_bytes (the
+ *    workspace of sf_o_proj_residual). */
 int sf_abi_version(void);
 
 /*
@@ -255,8 +257,18 @@ int sf_kv_append(const uint16_t* kv_buf, int row0, int n_tok, int Hkv, int hd, u
  * sf_qkv_rope), summed in a fixed order by a fix-up kernel (deterministic).
  * Calls sharing a workspace must not overlap.
  *
+ * sf_o_proj_residual, sf_o_proj_post_norm and sf_lm_head apply the weight to every
+ * row instead (M = B1·N): one pass over the weights for up to 256 rows, the
+ * workgroups splitting the columns and, for o_proj, K into up to 16 ranges whose
+ * fp32 sums go to a caller workspace of sf_o_proj_workspace_bytes(M, N, K) bytes
+ * and are added in range order by the residual kernel (deterministic).
+ *
  * sf_pack_weight        out = packed(w), w row-major [N, K]; N % 16 == 0, K % 64 == 0
  * sf_o_proj_residual    hp[r] = bf16(x[r] + bf16(o_bf[r] . Wo^T)), r < M (all rows)
+ * sf_o_proj_post_norm   the same for r < BN, and for recomputed rows (slot[r] >= 0)
+ *                       zn[slot[r]] = bf16(w * bf16(hp[r] * rstd)): o_proj and
+ *                       sf_residual_post_norm in one call, without the bf16 y round
+ *                       trip (fastdllm_v2_folded.py:207-212)
  * sf_residual_post_norm hp[r] = bf16(x[r] + y[r]) for r < BN, and for recomputed rows
  *                       zn[slot[r]] = bf16(w * bf16(hp[r] * rstd)) (y = a bf16 o_proj
  *                       output computed elsewhere, e.g. by a library GEMM)
@@ -272,8 +284,12 @@ int sf_kv_append(const uint16_t* kv_buf, int row0, int n_tok, int Hkv, int hd, u
 size_t sf_gemm_workspace_bytes(int mcap, int N, int K);
 size_t sf_ffn_gate_up_workspace_bytes(int bucket, int D, int I);
 int sf_pack_weight(const uint16_t* w, int N, int K, uint16_t* out, void* stream);
+size_t sf_o_proj_workspace_bytes(int M, int N, int K);
 int sf_o_proj_residual(const uint16_t* o_bf, const uint16_t* x, const uint16_t* wo, int M, int K,
                        int N, uint16_t* hp, void* workspace, size_t workspace_bytes, void* stream);
+int sf_o_proj_post_norm(const uint16_t* o_bf, const uint16_t* x, const uint16_t* wo, int BN, int K,
+                        int D, const int32_t* slot, const uint16_t* ln_w, float eps, uint16_t* hp,
+                        uint16_t* zn, void* workspace, size_t workspace_bytes, void* stream);
 int sf_residual_post_norm(const uint16_t* x, const uint16_t* y, const int32_t* slot, int BN,
                           int D, const uint16_t* w, float eps, uint16_t* hp, uint16_t* zn,
                           void* stream);

@@ -56,7 +56,10 @@ SIGNATURES = {
     "sf_gemm_workspace_bytes": (_sz, [_i, _i, _i]),
     "sf_ffn_gate_up_workspace_bytes": (_sz, [_i, _i, _i]),
     "sf_pack_weight": (_i, [_vp, _i, _i, _vp, _vp]),
+    "sf_o_proj_workspace_bytes": (_sz, [_i, _i, _i]),
     "sf_o_proj_residual": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _vp, _sz, _vp]),
+    "sf_o_proj_post_norm": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _vp, _f, _vp, _vp, _vp, _sz,
+                                 _vp]),
     "sf_residual_post_norm": (_i, [_vp, _vp, _vp, _i, _i, _vp, _f, _vp, _vp, _vp]),
     "sf_rows_rmsnorm": (_i, [_vp, _vp, _vp, _i, _vp, _i, _f, _vp, _vp]),
     "sf_ffn_gate_up": (_i, [_vp, _vp, _i, _vp, _vp, _i, _i, _vp, _vp, _sz, _vp]),
@@ -402,10 +405,34 @@ def o_proj_residual(o_bf, x, wo, M, K, N, hp, workspace, stream=None) -> None:
     _need(x, "x", torch.bfloat16, min_numel=M * N)
     _need(wo, "wo", torch.bfloat16, numel=N * K)
     _need(hp, "hp", torch.bfloat16, min_numel=M * N)
-    _need(workspace, "workspace", torch.uint8, min_numel=gemm_workspace_bytes(M, N, K), align=256)
+    _need(workspace, "workspace", torch.uint8, min_numel=o_proj_workspace_bytes(M, N, K),
+          align=256)
     st = load().sf_o_proj_residual(_ptr(o_bf), _ptr(x), _ptr(wo), M, K, N, _ptr(hp),
                                    _ptr(workspace), workspace.numel(), _stream(stream))
     _check(st, "sf_o_proj_residual")
+
+
+def o_proj_workspace_bytes(M: int, N: int, K: int) -> int:
+    """Bytes of the all-rows o_proj workspace (fp32 sums of its K ranges)."""
+    return int(load().sf_o_proj_workspace_bytes(M, N, K))
+
+
+def o_proj_post_norm(o_bf, x, wo, BN, K, D, slot, w, eps, hp, zn, workspace, stream=None) -> None:
+    """hp = bf16(x + bf16(o_bf . Wo^T)) for every row (Wo packed); zn[slot[r]] =
+    RMSNorm(hp[r]) where slot[r] >= 0."""
+    _need(o_bf, "o_bf", torch.bfloat16, min_numel=BN * K)
+    _need(x, "x", torch.bfloat16, min_numel=BN * D)
+    _need(wo, "wo", torch.bfloat16, numel=D * K)
+    _need(slot, "slot", torch.int32, min_numel=BN, align=4)
+    _need(w, "w", torch.bfloat16, numel=D)
+    _need(hp, "hp", torch.bfloat16, min_numel=BN * D)
+    _need(zn, "zn", torch.bfloat16)
+    _need(workspace, "workspace", torch.uint8, min_numel=o_proj_workspace_bytes(BN, D, K),
+          align=256)
+    st = load().sf_o_proj_post_norm(_ptr(o_bf), _ptr(x), _ptr(wo), BN, K, D, _ptr(slot), _ptr(w),
+                                    float(eps), _ptr(hp), _ptr(zn), _ptr(workspace),
+                                    workspace.numel(), _stream(stream))
+    _check(st, "sf_o_proj_post_norm")
 
 
 def residual_post_norm(x, y, slot, BN, D, w, eps, hp, zn, stream=None) -> None:

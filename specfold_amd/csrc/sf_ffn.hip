@@ -13,6 +13,7 @@
 #include <math.h>
 
 #include "sf_gemm_core.h"
+#include "sf_gemm_rows.h"
 
 namespace {
 
@@ -118,6 +119,102 @@ __global__ __launch_bounds__(256) void residual_post_norm_kernel(
       float f[8], g[8];
       sf_unpack8(xv[i], f);
       sf_unpack8(wv[i], g);
+      sf_u32x4 o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        o[j] = sf_pack2(g[2 * j] * sf_rbf(f[2 * j] * inv), g[2 * j + 1] * sf_rbf(f[2 * j + 1] * inv));
+      orow[idx] = o;
+    }
+  }
+}
+
+// The o_proj residual from the all-rows GEMM's KS fp32 partial slots, one wave
+// (one workgroup) per flat row r: y = bf16(sum_s part[s][r]) in slot order, hp[r]
+// = bf16(x[r] + y) (fastdllm_v2_folded.py:207-209), and with zn given, for a
+// recomputed row (slot[r] >= 0), zn[slot[r]] = bf16(w * bf16(hp[r] * rstd))
+// (:211-212).  The row goes in groups of 4 vectors of 8 per lane, two slots'
+// loads in flight at a time; hp stays in registers for the norm.
+template <int VPL>
+__global__ __launch_bounds__(64) void part_residual_norm_kernel(
+    const float* __restrict__ part, int ks, size_t stride, const uint16_t* __restrict__ x,
+    const int32_t* __restrict__ slot, int D, const uint16_t* __restrict__ w, float eps,
+    uint16_t* __restrict__ hp, uint16_t* __restrict__ zn) {
+  static_assert(VPL % 4 == 0, "groups of 4 vectors");
+  const int r = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int nvec = D >> 3;
+  const sf_u32x4* xr = reinterpret_cast<const sf_u32x4*>(x + (size_t)r * D);
+  const sf_f32x4* pr = reinterpret_cast<const sf_f32x4*>(part + (size_t)r * D);
+  const size_t st4 = stride / 4;  // slot stride in float4
+  sf_u32x4* hrow = reinterpret_cast<sf_u32x4*>(hp + (size_t)r * D);
+  sf_u32x4 hv[VPL];
+  float ss = 0.f;
+#pragma unroll
+  for (int g = 0; g < VPL; g += 4) {
+    int v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = 2 * min(lane + (g + i) * 64, nvec - 1);
+    sf_u32x4 xv[4];
+    sf_f32x4 y[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      xv[i] = xr[v[i] >> 1];
+      y[i][0] = pr[v[i]];
+      y[i][1] = pr[v[i] + 1];
+    }
+    for (int s = 1; s < ks; s += 2) {
+      const size_t oa = (size_t)s * st4, ob = (size_t)min(s + 1, ks - 1) * st4;
+      sf_f32x4 a[4][2], b[4][2];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        a[i][0] = pr[oa + v[i]];
+        a[i][1] = pr[oa + v[i] + 1];
+        b[i][0] = pr[ob + v[i]];
+        b[i][1] = pr[ob + v[i] + 1];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        y[i][0] += a[i][0];
+        y[i][1] += a[i][1];
+        if (s + 1 < ks) {
+          y[i][0] += b[i][0];
+          y[i][1] += b[i][1];
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float a[8];
+      sf_unpack8(xv[i], a);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float y0 = sf_rbf(y[i][j >> 1][(2 * j) & 3]);
+        const float y1 = sf_rbf(y[i][j >> 1][(2 * j + 1) & 3]);
+        hv[g + i][j] = sf_pack2(a[2 * j] + y0, a[2 * j + 1] + y1);
+      }
+      if (lane + (g + i) * 64 < nvec) {
+        hrow[lane + (g + i) * 64] = hv[g + i];
+        float h[8];
+        sf_unpack8(hv[g + i], h);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss = fmaf(h[j], h[j], ss);
+      }
+    }
+  }
+  if (!zn) return;
+  const int sl = slot[r];
+  if (sl < 0) return;  // wave-uniform
+  ss = sf_wave_sum(ss);
+  const float inv = 1.0f / sqrtf(ss / (float)D + eps);
+  const sf_u32x4* wr = reinterpret_cast<const sf_u32x4*>(w);
+  sf_u32x4* orow = reinterpret_cast<sf_u32x4*>(zn + (size_t)sl * D);
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int idx = lane + i * 64;
+    if (idx < nvec) {
+      float f[8], g[8];
+      sf_unpack8(hv[i], f);
+      sf_unpack8(wr[idx], g);
       sf_u32x4 o;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
@@ -254,20 +351,66 @@ extern "C" int sf_pack_weight(const uint16_t* w, int N, int K, uint16_t* out, vo
   return sf_launch_status();
 }
 
+// K ranges of o_proj's all-rows GEMM (the partial slots its consumer adds)
+constexpr int kOprojMaxSplits = 16;
+
+extern "C" size_t sf_o_proj_workspace_bytes(int M, int N, int K) {
+  if (M < 1 || M > 1024 || N < 128 || N % 128 || K < kKC || K % kKC) return 0;
+  const int ks = rows_splits<1>(M, N, K, kOprojMaxSplits);
+  const size_t b = (size_t)ks * M * N * sizeof(float);
+  return b < 256 ? 256 : b;
+}
+
+namespace {
+// o_proj over every row to the workspace's partial slots, then one wave per row
+// adds them to the residual (and normalises the recomputed rows when zn is given)
+int o_proj_launch(const uint16_t* o_bf, const uint16_t* x, const uint16_t* wo, int M, int K, int N,
+                  const int32_t* slot, const uint16_t* ln_w, float eps, uint16_t* hp,
+                  uint16_t* zn, void* workspace, hipStream_t st) {
+  float* part = reinterpret_cast<float*>(workspace);
+  launch_rows<1, kRowsPart>(o_bf, M, wo, K, N, kOprojMaxSplits, part, nullptr, st);
+  const int ks = rows_splits<1>(M, N, K, kOprojMaxSplits);
+  const size_t stride = (size_t)M * N;
+  const int vpl = (N / 8 + 63) / 64;
+  const dim3 grid(M);
+  if (vpl <= 4)
+    hipLaunchKernelGGL(part_residual_norm_kernel<4>, grid, dim3(64), 0, st, part, ks, stride, x,
+                       slot, N, ln_w, eps, hp, zn);
+  else if (vpl <= 8)
+    hipLaunchKernelGGL(part_residual_norm_kernel<8>, grid, dim3(64), 0, st, part, ks, stride, x,
+                       slot, N, ln_w, eps, hp, zn);
+  else
+    hipLaunchKernelGGL(part_residual_norm_kernel<16>, grid, dim3(64), 0, st, part, ks, stride, x,
+                       slot, N, ln_w, eps, hp, zn);
+  return sf_launch_status();
+}
+}  // namespace
+
 extern "C" int sf_o_proj_residual(const uint16_t* o_bf, const uint16_t* x, const uint16_t* wo,
                                   int M, int K, int N, uint16_t* hp, void* workspace,
                                   size_t workspace_bytes, void* stream) {
   if (!o_bf || !x || !wo || !hp || !workspace) return SF_ERR_ARG;
-  if (M < 1 || M > 1024 || K % kKC || N % 128 || !aligned16(o_bf) || !aligned16(wo))
+  if (M < 1 || M > 1024 || K < kKC || K % kKC || N < 128 || N % 128 || N > 8192 ||
+      !aligned16(o_bf) || !aligned16(wo) || !aligned16(x) || !aligned16(hp) ||
+      !aligned16(workspace))
     return SF_ERR_SHAPE;
-  if (workspace_bytes < sf_gemm_workspace_bytes(M, N, K)) return SF_ERR_WORKSPACE;
-  Epi ep{};
-  ep.out = hp;
-  ep.ldo = N;
-  ep.res = x;
-  launch_sk<1, kResid>(make_plan_whole(N / 128, K / kKC), o_bf, nullptr, K, nullptr, M, M, wo,
-                       nullptr, K, N, nullptr, ep, reinterpret_cast<hipStream_t>(stream));
-  return sf_launch_status();
+  if (workspace_bytes < sf_o_proj_workspace_bytes(M, N, K)) return SF_ERR_WORKSPACE;
+  return o_proj_launch(o_bf, x, wo, M, K, N, nullptr, nullptr, 0.f, hp, nullptr, workspace,
+                       reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int sf_o_proj_post_norm(const uint16_t* o_bf, const uint16_t* x, const uint16_t* wo,
+                                   int BN, int K, int D, const int32_t* slot, const uint16_t* ln_w,
+                                   float eps, uint16_t* hp, uint16_t* zn, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  if (!o_bf || !x || !wo || !slot || !ln_w || !hp || !zn || !workspace) return SF_ERR_ARG;
+  if (BN < 1 || BN > 1024 || K < kKC || K % kKC || D < 128 || D % 128 || D > 8192 ||
+      !aligned16(o_bf) || !aligned16(wo) || !aligned16(x) || !aligned16(hp) || !aligned16(zn) ||
+      !aligned16(ln_w) || !aligned16(workspace))
+    return SF_ERR_SHAPE;
+  if (workspace_bytes < sf_o_proj_workspace_bytes(BN, D, K)) return SF_ERR_WORKSPACE;
+  return o_proj_launch(o_bf, x, wo, BN, K, D, slot, ln_w, eps, hp, zn, workspace,
+                       reinterpret_cast<hipStream_t>(stream));
 }
 
 extern "C" int sf_rows_rmsnorm(const uint16_t* x, const int32_t* rows, const int32_t* count,
@@ -364,11 +507,11 @@ extern "C" int sf_residual_gather_add(const uint16_t* hp, const uint16_t* ffn, c
 extern "C" int sf_lm_head(const uint16_t* x, int M, const uint16_t* w, int D, int V,
                           uint16_t* logits, void* stream) {
   if (!x || !w || !logits) return SF_ERR_ARG;
-  if (M < 1 || M > 1024 || D % kKC || V % 128) return SF_ERR_SHAPE;
-  Epi ep{};
-  ep.out = logits;
-  ep.ldo = V;
-  launch_sk<1, kPlain>(make_plan_whole(V / 128, D / kKC), x, nullptr, D, nullptr, M, M, w,
-                       nullptr, D, V, nullptr, ep, reinterpret_cast<hipStream_t>(stream));
+  if (M < 1 || M > 1024 || D < kKC || D % kKC || V < 128 || V % 128 || !aligned16(x) ||
+      !aligned16(w) || !aligned16(logits))
+    return SF_ERR_SHAPE;
+  // 128-column tiles, the whole K per workgroup (no partial buffer)
+  launch_rows<2, kRowsBf16>(x, M, w, D, V, 1, nullptr, logits,
+                            reinterpret_cast<hipStream_t>(stream));
   return sf_launch_status();
 }

@@ -22,12 +22,8 @@
 
 namespace sfg {
 
-constexpr int kKC = 64;       // K per stage: two MFMA K chunks, one per wave of a pair
 constexpr int kThreads = 512; // 8 waves
-constexpr int kLdsBudget = 152 * 1024;
-#ifndef SFG_RING_MAX
-#define SFG_RING_MAX 6
-#endif
+// kKC (K per stage), kLdsBudget and SFG_RING_MAX: sf_index.h
 
 // One ring stage of a workgroup of up to MB rows and WN weight tiles per wave:
 // the two 32-K chunks of the MB/16 A m tiles (1 KB per (chunk, m tile)), then

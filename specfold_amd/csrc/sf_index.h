@@ -32,6 +32,11 @@ namespace sfg {
 // W[16t + l%16][32c + 8(l/16) .. +8]) are one contiguous 1 KB block, and the
 // chunks of a tile follow each other.
 constexpr int kKsStride = 512;     // elements between 32-wide chunks of a tile
+constexpr int kKC = 64;            // K per stage: two 32-wide MFMA chunks
+constexpr int kLdsBudget = 152 * 1024;  // LDS of a stage ring
+#ifndef SFG_RING_MAX
+#define SFG_RING_MAX 6
+#endif
 
 // Lane `lane`'s first fragment of 16-row tile `tile16`, from base W (a pointer to
 // the packed weights in the kernels; an integer 0 gives the element offset).
@@ -118,6 +123,82 @@ SF_IDX Piece plan_piece(int u, int u_end, const Plan& p) {
 // Partial slots of a plan: [plan_slots][mcap][N] fp32.
 inline size_t part_bytes(const Plan& p, int mcap, int N) {
   return (size_t)plan_slots(p) * mcap * N * sizeof(float);
+}
+
+// ---------------------------------------------------------------------------
+// All-rows GEMM (sf_gemm_rows.h): every row of A, up to 128·RG, in one pass over
+// the weights.  The 8 waves are RG row groups (128 rows each) x CG = 8 / RG
+// column groups (WN tiles of 16 columns each), so a workgroup tile is 16·WN·CG
+// columns by all rows.  K (S stages of 64) is cut into KS ranges of whole stages;
+// workgroup g computes range s of tile t, (s, t) = item rows_item(g) in split-major
+// order.  KS > 1 leaves KS fp32 partial sums per output for the consumer to add
+// in range order.
+struct RowsPlan {
+  int T;   // column tiles
+  int KS;  // K ranges
+  int S;   // K stages
+};
+// KS fills SFG_GRID workgroups without exceeding ks_max (1 where the caller has
+// no partial buffer) or an eighth of the stages (a range of at least 8 stages
+// keeps the partial traffic below the weight stream's).
+inline RowsPlan make_rows_plan(int T, int S, int ks_max) {
+  int ks = SFG_GRID / T;
+  ks = sf_imin(ks, (S + 7) / 8);
+  ks = sf_imin(ks, ks_max);
+  return RowsPlan{T, ks < 1 ? 1 : ks, S};
+}
+SF_IDX int rows_grid(const RowsPlan& p) { return p.T * p.KS; }
+// Workgroup g runs on XCD g % 8; the G items are numbered so that one XCD's
+// workgroups take consecutive items (split-major: they share their K range of A,
+// which stays in that XCD's L2).  A bijection of [0, G).
+SF_IDX int rows_item(int g, int G) {
+  const int x = g & 7;
+  return x * (G >> 3) + sf_imin(x, G & 7) + (g >> 3);
+}
+SF_IDX int rows_split_begin(int s, const RowsPlan& p) {
+  return (int)((long long)p.S * s / p.KS);
+}
+// Stage layout of a workgroup of RG row groups and WN 16-column tiles per wave.
+template <int RG, int WN>
+struct RowsStage {
+  static constexpr int kMB = 128 * RG;     // rows per pass
+  static constexpr int kMT = kMB / 16;     // m tiles
+  static constexpr int kCG = 8 / RG;       // column groups
+  static constexpr int kTW = kCG * WN;     // 16-column tiles of a workgroup tile
+  static constexpr int kA = 2 * kMT * 64;  // 16-byte words of A per stage
+  static constexpr int kW = kTW * 2 * 64;  // words of weights per stage
+  static constexpr int kWords = kA + kW;
+  static constexpr int kDA = 2 * kMT / 8;  // A copies per wave per stage
+  static constexpr int kDW = kTW * 2 / 8;  // weight copies per wave per stage
+  static constexpr int kRing =
+      kLdsBudget / (kWords * 16) < SFG_RING_MAX ? kLdsBudget / (kWords * 16) : SFG_RING_MAX;
+  static_assert(kDA * 8 == 2 * kMT && kDW * 8 == kTW * 2, "copies split evenly over 8 waves");
+};
+// A pass of at most 128 rows uses one row group (RG = 1, 8 column groups) with
+// half the tiles per wave (at least one), a pass of up to 256 rows two; WN is
+// the two-group configuration's.
+inline int rows_rg(int mb) { return mb <= 128 ? 1 : 2; }
+template <int WN>
+constexpr int rows_wn(int rg) { return rg == 2 ? WN : (WN > 1 ? WN / 2 : 1); }
+template <int WN>
+inline int rows_tiles(int N, int rg) { return N / (16 * rows_wn<WN>(rg) * (8 / rg)); }
+// K ranges of an all-rows GEMM over M rows: the first pass's plan, used by every
+// pass (the consumer adds the same number of partial slots for every row).
+template <int WN>
+inline int rows_splits(int M, int N, int K, int ks_max) {
+  const int rg = rows_rg(sf_imin(256, M));
+  return make_rows_plan(rows_tiles<WN>(N, rg), K / kKC, ks_max).KS;
+}
+// Direct copies of a stage: copy q = wv + 8j of the 2·MT A tiles (MT m tiles of
+// 16 rows; chunk q / MT, m tile q % MT, in the tile layout of a_copy) and of the
+// 2·TW weight blocks (TW tiles of 16 columns; tile q / 2, chunk q % 2).
+SF_IDX int rows_a_chunk(int q, int MT) { return q / MT; }
+SF_IDX int rows_a_mtile(int q, int MT) { return q % MT; }
+SF_IDX int rows_w_tile(int q) { return q >> 1; }
+SF_IDX int rows_w_chunk(int q) { return q & 1; }
+// fp32 partials of a plan for M rows and N columns: [KS][M][N].
+inline size_t rows_part_bytes(const RowsPlan& p, int M, int N) {
+  return p.KS > 1 ? (size_t)p.KS * M * N * sizeof(float) : 0;
 }
 
 }  // namespace sfg

@@ -13,13 +13,14 @@ fastdllm_v2_folded.py:296-361 for the launch sequence, :117-220 for the math):
                      [prefix ; own block], folded rows from their source row's
                      query over their own branch's keys (the chain correction's
                      result)                                   (HIP)
-  o_proj for every row (M = B1*N)                        (torch mm, hipBLASLt)
-  sf_residual_post_norm  hp = x + attn_out, post-attention RMSNorm of the
+  sf_o_proj_post_norm  o_proj of every row (M = B1*N, all-rows MFMA GEMM), hp =
+                     x + bf16(O Wo^T), post-attention RMSNorm of the
                      recomputed rows                           (HIP)
   sf_ffn_gate_up      gate/up GEMM + SiLU*mul on compacted rows  (HIP)
   sf_ffn_down_scatter down GEMM, scattered to the per-row FFN table (HIP)
 and after the last layer the residual update + final RMSNorm (HIP) and the
-lm_head (hipBLASLt).  sf_chain_correct (the reference's incremental form of the
+lm_head (sf_lm_head, the all-rows GEMM; hipBLASLt for a vocabulary that is not a
+multiple of 128).  sf_chain_correct (the reference's incremental form of the
 folded rows' attention) stays in the C ABI; the engine forms it with sf_attn_rows.
 
 Nothing here syncs with the host: the branch parent map is computed from the
@@ -127,7 +128,6 @@ class _Buffers:
         self.act = torch.zeros(bucket, eng.I, dtype=bf, device=dev)
         self.hid = torch.zeros(2, BN, D, dtype=bf, device=dev)       # layer outputs, ping-pong
         self.final = torch.zeros(BN, D, dtype=bf, device=dev)
-        self.attn_out = torch.zeros(BN, D, dtype=bf, device=dev)
         self.pos0 = torch.zeros(1, **i32)   # first block position (caches without length_dev)
         self.q_scale = torch.ones(N, dtype=torch.float32, device=dev)  # per-position q scale
         self.all_rows = torch.arange(BN, **i32)
@@ -142,6 +142,9 @@ class _Buffers:
                                   dtype=torch.uint8, device=dev)
         self.ws_attn = torch.empty(max(_lib.attn_workspace_bytes(bucket, H, P), 256),
                                    dtype=torch.uint8, device=dev)
+        # o_proj over every row: fp32 sums of its K ranges
+        self.ws_oproj = torch.empty(max(_lib.o_proj_workspace_bytes(BN, D, H * hd), 256),
+                                    dtype=torch.uint8, device=dev)
 
 
 class _Batch:
@@ -231,6 +234,7 @@ class FoldedVerifyEngine:
         # fastdllm_v2_folded.py:77-87).  The module tree keeps its own tensors.
         self._packed: List[Tuple[torch.Tensor, Optional[torch.Tensor]]] = []
         self._packed_mlp: List[Tuple[torch.Tensor, torch.Tensor, torch.Tensor]] = []
+        self._packed_o: List[torch.Tensor] = []
         for lyr in self.layers:
             a = lyr.self_attn
             w = torch.cat([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight], 0).contiguous()
@@ -243,6 +247,11 @@ class FoldedVerifyEngine:
             self._packed_mlp.append((_lib.pack_weight(m.gate_proj.weight.contiguous()),
                                      _lib.pack_weight(m.up_proj.weight.contiguous()),
                                      _lib.pack_weight(m.down_proj.weight.contiguous())))
+            self._packed_o.append(_lib.pack_weight(a.o_proj.weight.contiguous()))
+        # the head through sf_lm_head where its shape allows (V % 128, D % 64)
+        hw = self.head.weight
+        self._packed_head = (_lib.pack_weight(hw.contiguous())
+                             if hw.shape[0] % 128 == 0 and hw.shape[1] % 64 == 0 else None)
         self._bufs: Dict[Tuple[int, int, int], _Buffers] = {}
         # HIP graphs of the layer loop, keyed by shape / prefix / delta / cache
         # (one per branch count the decode loop visits, B1 = 1..8, per sequence's
@@ -251,6 +260,17 @@ class FoldedVerifyEngine:
         self.max_graphs = 48
         self._graphs: Dict[tuple, tuple] = {}
         self._rope: Optional[Tuple[torch.Tensor, torch.Tensor]] = None
+
+    def lm_head(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """logits = x . Wlm^T for every row of x [M, D] (bf16; a fresh tensor unless
+        ``out`` is given): sf_lm_head, one pass over the head weights for every row."""
+        M = x.shape[0]
+        if out is None:
+            out = torch.empty(M, self.V, dtype=torch.bfloat16, device=self.device)
+        if self._packed_head is None:
+            return torch.mm(x, self.head.weight.t(), out=out)
+        _lib.lm_head(x, M, self._packed_head, self.D, self.V, out)
+        return out
 
     @staticmethod
     def _check_device(device: torch.device) -> None:
@@ -359,10 +379,7 @@ class FoldedVerifyEngine:
                           hidden=hidden, delta=delta)
         if not compute_logits:
             return None
-        # lm_head over all BN rows (M = BN) on the final-normed rows: hipBLASLt, a fresh
-        # tensor per call
-        logits = torch.mm(buf.final, self.head.weight.t())
-        return logits.view(B1, N, self.V)
+        return self.lm_head(buf.final).view(B1, N, self.V)
 
     @torch.no_grad()
     def forward_batched(self, blocks: List[torch.Tensor], caches: list, delta: float = 0.1,
@@ -442,7 +459,7 @@ class FoldedVerifyEngine:
         self.last_hidden = hidden
         if not compute_logits:
             return None
-        logits = torch.mm(buf.final, self.head.weight.t()).view(B1, N, self.V)
+        logits = self.lm_head(buf.final).view(B1, N, self.V)
         return [x[:r] for x, r in zip(logits.split(sizes, 0), real)]
 
     def _replay_batched(self, buf: _Buffers, tokens: torch.Tensor, sizes: List[int],
@@ -551,13 +568,12 @@ class FoldedVerifyEngine:
                                     rows=rows_s[si],
                                     branches=(batch.offsets[si], batch.sizes[si]))
 
-            # o_proj for every row (fastdllm_v2_folded.py:207-209): M = BN is a regular
-            # GEMM shape, where hipBLASLt beats the skinny-M streaming kernel; then one
-            # kernel for the residual hp = bf16(x + bf16(O Wo^T)) (two roundings as in
-            # the reference) and the post-attention RMSNorm of the recomputed rows
-            torch.mm(buf.o_bf, lyr.self_attn.o_proj.weight.t(), out=buf.attn_out)
-            _lib.residual_post_norm(hidden, buf.attn_out, buf.slot, BN, D,
-                                    lyr.post_attention_layernorm.weight, self.eps, buf.hp, buf.zn)
+            # o_proj for every row (fastdllm_v2_folded.py:207-209) in one pass over Wo,
+            # the residual hp = bf16(x + bf16(O Wo^T)) (two roundings as in the
+            # reference) and the post-attention RMSNorm of the recomputed rows (:211-212)
+            _lib.o_proj_post_norm(buf.o_bf, hidden, self._packed_o[li], BN, self.H * self.hd, D,
+                                  buf.slot, lyr.post_attention_layernorm.weight, self.eps,
+                                  buf.hp, buf.zn, buf.ws_oproj)
             # FFN on the compacted rows (:211-217)
             wg, wu, wd = self._packed_mlp[li]
             _lib.ffn_gate_up(buf.zn, count, bucket, wg, wu, D, self.I, buf.act, buf.ws_gemm)
@@ -708,12 +724,13 @@ class FoldedVerifyEngine:
         def attn():
             self._attention(buf, cache, li, count, bucket, B1, N)
 
-        def o_proj():
-            torch.mm(buf.o_bf, lyr.self_attn.o_proj.weight.t(), out=buf.attn_out)
+        wo = self._packed_o[li]
 
-        def post_norm():
-            _lib.residual_post_norm(hidden, buf.attn_out, buf.slot, BN, D,
-                                    lyr.post_attention_layernorm.weight, self.eps, buf.hp, buf.zn)
+        def o_proj():
+            # o_proj + residual + post-attention norm (one entry point)
+            _lib.o_proj_post_norm(buf.o_bf, hidden, wo, BN, H * hd, D, buf.slot,
+                                  lyr.post_attention_layernorm.weight, self.eps, buf.hp, buf.zn,
+                                  buf.ws_oproj)
 
         wg, wu, wd = self._packed_mlp[li]
 
@@ -729,10 +746,10 @@ class FoldedVerifyEngine:
                                   self.eps, scratch, normed)
 
         def lm_head():
-            torch.mm(buf.final, self.head.weight.t(), out=logits)
+            self.lm_head(buf.final, out=logits)
 
-        out = dict(qkv=qkv, attn=attn, o_proj=o_proj, post_norm=post_norm,
-                   gate_up=gate_up, down=down, final_norm=final_norm, lm_head=lm_head, gate=gate)
+        out = dict(qkv=qkv, attn=attn, o_proj=o_proj, gate_up=gate_up, down=down,
+                   final_norm=final_norm, lm_head=lm_head, gate=gate)
         if isinstance(cache, PagedKVCache) and cache.length + N <= cache.capacity:
             def append():
                 # writes past the logical end of the cache: never read, length unchanged

@@ -8,7 +8,9 @@
 //   * stream-K GEMM plans: every (tile, stage) unit done exactly once, every
 //     workgroup's range non-empty, the partial slot of each piece inside the
 //     plan's slot count and the library's workspace, whole-tile plans single-
-//     contributor; output columns of each mode inside N and covering each tile
+//     contributor; the all-rows GEMM's (range, tile) items, K ranges, copies,
+//     LDS reads and stores (each output element once per range, inside the
+//     workspace); output columns of each mode inside N and covering each tile
 //     once; every packed-weight load inside the N·K weights, and the fragment it
 //     reads (under the packed layout) belonging to the column the lane writes;
 //   * prefix attention: a staged chunk's LDS layout (the copies fill every cell
@@ -44,7 +46,7 @@ static long long g_checks = 0;
   } while (0)
 
 typedef size_t (*ws3_fn)(int, int, int);
-static ws3_fn f_gemm_ws, f_qkv_ws, f_attn_ws, f_gu_ws;
+static ws3_fn f_gemm_ws, f_qkv_ws, f_attn_ws, f_gu_ws, f_oproj_ws;
 
 // ---------------------------------------------------------------------------
 // GEMM plans
@@ -134,11 +136,148 @@ static void check_plans() {
             "gate/up workspace D=%d I=%d", s.D, s.I);
       plans += 3;
     }
-    walk_plan(sfg::make_plan_whole(s.D / 128, s.D / 64), true);    // o_proj (H·hd = D)
-    walk_plan(sfg::make_plan_whole(s.V / 128, s.D / 64), true);    // lm_head
-    plans += 2;
   }
   printf("gemm plans: %lld plans walked\n", plans);
+}
+
+// All-rows GEMM (o_proj: WN 1, up to 16 K ranges, partials in the library's
+// workspace; lm_head: WN 2, one range, bf16 out), walked as launch_rows and
+// gemm_rows_kernel do for M rows: every workgroup maps to a distinct (range,
+// tile) item and every item is taken; the ranges partition the K stages; every A
+// copy reads a row of its pass inside A, every weight copy lies inside the packed
+// N·K weights and fills the LDS block the readers take; every LDS access lies
+// inside the ring; every store lies inside its output (partial slots: inside the
+// workspace) and each output element is written once per range.
+template <int RG, int WN>
+static void walk_rows_pass(const sfg::RowsPlan& p, int M, int m0, int mb, int N, int K,
+                           int ks, size_t part_elems, std::vector<unsigned char>* hit) {
+  using St = sfg::RowsStage<RG, WN>;
+  CHECK(St::kRing >= 3 && St::kRing * St::kWords * 16 <= 160 * 1024, "ring");
+  CHECK(p.T * St::kTW * 16 == N, "tiles cover N: T=%d N=%d", p.T, N);
+  const int G = sfg::rows_grid(p);
+  std::vector<int> seen(G, 0);
+  for (int g = 0; g < G; ++g) {
+    const int q = sfg::rows_item(g, G);
+    CHECK(q >= 0 && q < G && !seen[q]++, "item %d of %d", q, G);
+  }
+  for (int s = 0; s < p.KS; ++s) {
+    const int s0 = sfg::rows_split_begin(s, p), s1 = sfg::rows_split_begin(s + 1, p);
+    CHECK(s1 > s0 && s0 >= 0 && s1 <= p.S, "range %d [%d, %d)", s, s0, s1);
+    if (s == 0) CHECK(s0 == 0, "first range");
+    if (s == p.KS - 1) CHECK(s1 == p.S, "last range");
+  }
+  // copies of one stage: each A tile (chunk, m tile) and weight block (tile, chunk)
+  // exactly once over the 8 waves
+  std::vector<int> acell(2 * St::kMT, 0), wcell(2 * St::kTW, 0);
+  for (int wv = 0; wv < 8; ++wv) {
+    for (int j = 0; j < St::kDA; ++j) {
+      const int cq = wv + 8 * j;
+      const int ch = sfg::rows_a_chunk(cq, St::kMT), mt = sfg::rows_a_mtile(cq, St::kMT);
+      CHECK(ch < 2 && mt < St::kMT, "a copy");
+      ++acell[ch * St::kMT + mt];
+      for (int L = 0; L < 64; ++L) {
+        const int r = sf_imin(mt * 16 + (L >> 2), mb - 1);
+        CHECK(r >= 0 && r < mb && m0 + r < M, "a row");
+        const size_t last = (size_t)(m0 + r) * K + (size_t)(p.S - 1) * sfg::kKC + ch * 32 +
+                            sfg::a_copy_unit(L) * 8 + 8;
+        CHECK(last <= (size_t)M * K, "a load");
+      }
+    }
+    for (int j = 0; j < St::kDW; ++j) {
+      const int cq = wv + 8 * j;
+      const int tw = sfg::rows_w_tile(cq), c = sfg::rows_w_chunk(cq);
+      CHECK(tw < St::kTW && c < 2, "w copy");
+      ++wcell[tw * 2 + c];
+      for (int t : {0, p.T - 1})
+        for (int L : {0, 63}) {
+          const size_t e = sfg::weight_lane_ptr((size_t)0, t * St::kTW + tw, K, L) +
+                           (size_t)c * sfg::kKsStride +
+                           (size_t)sfg::weight_chunk(p.S - 1, 0) * sfg::kKsStride + 8;
+          CHECK(e <= (size_t)N * K, "w load");
+        }
+    }
+  }
+  for (int v : acell) CHECK(v == 1, "a cell filled %d times", v);
+  for (int v : wcell) CHECK(v == 1, "w cell filled %d times", v);
+  // fragment reads inside the stage's words
+  for (int wv = 0; wv < 8; ++wv) {
+    const int rgrp = wv / St::kCG, cgrp = wv % St::kCG;
+    for (int lane = 0; lane < 64; ++lane)
+      for (int c = 0; c < 2; ++c) {
+        for (int i = 0; i < 8; ++i) {
+          const int w = (c * St::kMT + rgrp * 8 + i) * 64 + sfg::a_read_word(lane);
+          CHECK(w >= 0 && w < St::kA, "a read word %d", w);
+        }
+        for (int tt = 0; tt < WN; ++tt) {
+          const int w = St::kA + (cgrp * WN + tt) * 128 + c * 64 + lane;
+          CHECK(w >= St::kA && w < St::kWords, "w read word %d", w);
+        }
+      }
+  }
+  // stores: lane (row rgrp*128 + 16 i + l%16, columns col0 + 16 tt + 4 (l/16) .. +4)
+  for (int q = 0; q < G; ++q) {
+    const int s = q / p.T, t = q % p.T;
+    for (int wv = 0; wv < 8; ++wv) {
+      const int rgrp = wv / St::kCG, cgrp = wv % St::kCG;
+      for (int lane = 0; lane < 64; ++lane) {
+        const int col0 = (t * St::kTW + cgrp * WN) * 16 + (lane >> 4) * 4;
+        for (int i = 0; i < 8; ++i) {
+          const int row = rgrp * 128 + i * 16 + (lane & 15);
+          if (row >= mb) continue;
+          for (int tt = 0; tt < WN; ++tt) {
+            const size_t o = (size_t)(m0 + row) * N + col0 + tt * 16;
+            CHECK(col0 + tt * 16 + 4 <= N && o + 4 <= (size_t)M * N, "store");
+            const size_t e = (size_t)s * M * N + o;
+            CHECK(e + 4 <= part_elems, "partial store %zu of %zu", e, part_elems);
+            for (int k = 0; k < 4; ++k) CHECK(!(*hit)[e + k]++, "element written twice");
+          }
+        }
+      }
+    }
+  }
+  (void)ks;
+}
+
+template <int WN>
+static void walk_rows(int M, int N, int K, int ks_max, size_t ws_bytes) {
+  const int ks = sfg::rows_splits<WN>(M, N, K, ks_max);
+  CHECK(ks >= 1 && ks <= ks_max, "ks %d", ks);
+  const size_t part_elems = (size_t)ks * M * N;
+  if (ks_max > 1) CHECK(ws_bytes >= part_elems * 4, "o_proj workspace %zu < %zu", ws_bytes, part_elems * 4);
+  std::vector<unsigned char> hit(part_elems, 0);
+  for (int m0 = 0; m0 < M; m0 += 256) {
+    const int mb = sf_imin(256, M - m0);
+    const int rg = sfg::rows_rg(mb);
+    const sfg::RowsPlan p{sfg::rows_tiles<WN>(N, rg), ks, K / sfg::kKC};
+    if (rg == 1)
+      walk_rows_pass<1, sfg::rows_wn<WN>(1)>(p, M, m0, mb, N, K, ks, part_elems, &hit);
+    else
+      walk_rows_pass<2, WN>(p, M, m0, mb, N, K, ks, part_elems, &hit);
+  }
+  for (unsigned char h : hit) CHECK(h == 1, "element not written");
+}
+
+static void check_rows_plans() {
+  long long n = 0;
+  const int dims[] = {1536, 3584, 4096, 5120, 896};
+  for (int D : dims)
+    for (int M : {1, 39, 128, 129, 256, 300}) {
+      walk_rows<1>(M, D, D, 16, f_oproj_ws(M, D, D));
+      ++n;
+    }
+  // lm_head at a reduced vocabulary of the same tile structure (the walk marks
+  // every element); the full vocabularies' tile counts
+  for (int D : {1536, 3584})
+    for (int M : {1, 129, 256}) {
+      walk_rows<2>(M, 2048, D, 1, 0);
+      ++n;
+    }
+  for (int V : {151936, 152064, 131072})
+    for (int rg : {1, 2}) {
+      const int T = sfg::rows_tiles<2>(V, rg);
+      CHECK(T * 16 * sfg::rows_wn<2>(rg) * (8 / rg) == V, "lm_head tiles V=%d", V);
+    }
+  printf("all-rows GEMM: %lld launches walked\n", n);
 }
 
 // Output columns and packed-weight addressing of one GEMM mode: N output
@@ -462,11 +601,13 @@ int main(int argc, char** argv) {
   f_qkv_ws = (ws3_fn)dlsym(lib, "sf_qkv_workspace_bytes");
   f_attn_ws = (ws3_fn)dlsym(lib, "sf_attn_workspace_bytes");
   f_gu_ws = (ws3_fn)dlsym(lib, "sf_ffn_gate_up_workspace_bytes");
-  if (!f_gemm_ws || !f_qkv_ws || !f_attn_ws || !f_gu_ws) {
+  f_oproj_ws = (ws3_fn)dlsym(lib, "sf_o_proj_workspace_bytes");
+  if (!f_gemm_ws || !f_qkv_ws || !f_attn_ws || !f_gu_ws || !f_oproj_ws) {
     fprintf(stderr, "missing workspace queries\n");
     return 2;
   }
   check_plans();
+  check_rows_plans();
   check_gemm_columns();
   check_lds_paths();
   check_page_addressing();

@@ -5,7 +5,10 @@
 //   sf_ffn_gate_up      act[m] = bf16(bf16(silu(bf16 g)) * bf16 u), m < count (stream-K, fix-up)
 //   sf_ffn_down_scatter ffn[rows[m]] = bf16(act[m] . Wd^T), m < count (stream-K, fix-up);
 //                       rows not in `rows` stay untouched
-//   sf_o_proj_residual  hp[r] = bf16(x[r] + bf16(o[r] . Wo^T)), r < M (static M)
+//   sf_o_proj_residual  hp[r] = bf16(x[r] + bf16(o[r] . Wo^T)), r < M (static M; all-rows
+//                       GEMM, K ranges through fp32 partial slots)
+//   sf_o_proj_post_norm the same hp, and zn[slot[r]] = bf16(w * bf16(hp[r] * rstd)) for
+//                       the rows with slot[r] >= 0
 //   sf_lm_head          logits[m] = bf16(x[m] . W^T), m < M
 //   sf_qkv_rope         q / k / v of the recomputed rows: bias, RoPE from absolute
 //                       position tables, the optional q scale, scatter by flat row
@@ -172,13 +175,13 @@ int main(int argc, char** argv) {
     auto wo = rnd((size_t)D * D, 0.05f);
     const auto po = pack(wo, D, D);
     std::vector<uint16_t> hp((size_t)M * D);
-    std::vector<float> ws(sf_gemm_workspace_bytes(M, D, D) / 4 + 16);
+    std::vector<float> ws(sf_o_proj_workspace_bytes(M, D, D) / 4 + 16);
     if (sf_o_proj_residual(o.data(), x.data(), po.data(), M, D, D, hp.data(), ws.data(),
                            ws.size() * 4, nullptr)) {
       fprintf(stderr, "sf_o_proj_residual failed\n");
       return 1;
     }
-    Checker co{"o_proj + residual"};
+    std::vector<double> yref((size_t)M * D), ymag((size_t)M * D);
     for (int r = 0; r < M; ++r)
       for (int c = 0; c < D; ++c) {
         double y = 0, mag = 0;
@@ -186,13 +189,58 @@ int main(int argc, char** argv) {
           y += fb(o[(size_t)r * D + k]) * fb(wo[(size_t)c * D + k]);
           mag += std::fabs(fb(o[(size_t)r * D + k]) * fb(wo[(size_t)c * D + k]));
         }
-        // a one-step flip of bf16(y) carries through the residual sum
-        const double uy = std::ldexp(1.0, std::ilogb(std::fabs(y) + 1e-30) - 7);
-        co.add(hp[(size_t)r * D + c], (double)(float)(fb(x[(size_t)r * D + c]) + fb(bf(y))), mag, uy);
+        yref[(size_t)r * D + c] = y;
+        ymag[(size_t)r * D + c] = mag;
       }
-    ok &= co.report();
+    auto check_hp = [&](const char* name, const std::vector<uint16_t>& h) {
+      Checker co{name};
+      for (int r = 0; r < M; ++r)
+        for (int c = 0; c < D; ++c) {
+          const double y = yref[(size_t)r * D + c];
+          // a one-step flip of bf16(y) carries through the residual sum
+          const double uy = std::ldexp(1.0, std::ilogb(std::fabs(y) + 1e-30) - 7);
+          co.add(h[(size_t)r * D + c], (double)(float)(fb(x[(size_t)r * D + c]) + fb(bf(y))),
+                 ymag[(size_t)r * D + c], uy);
+        }
+      return co.report();
+    };
+    ok &= check_hp("o_proj + residual", hp);
+    printf("  o_proj K ranges: %zu\n", sf_o_proj_workspace_bytes(M, D, D) / (4 * (size_t)M * D));
 
-    const int V = 256;
+    // o_proj + residual + post-attention RMSNorm of the recomputed rows (slot >= 0);
+    // the norm is checked on the kernel's own hp
+    {
+      std::vector<int32_t> slot(M);
+      int ns = 0;
+      for (int r = 0; r < M; ++r) slot[r] = (rng() % 3 == 0) ? -1 : ns++;
+      auto lw = rnd(D, 1.f);
+      const float eps = 1e-6f;
+      std::vector<uint16_t> hp2((size_t)M * D), zn((size_t)std::max(ns, 1) * D, 0x1234);
+      if (sf_o_proj_post_norm(o.data(), x.data(), po.data(), M, D, D, slot.data(), lw.data(), eps,
+                              hp2.data(), zn.data(), ws.data(), ws.size() * 4, nullptr)) {
+        fprintf(stderr, "sf_o_proj_post_norm failed\n");
+        return 1;
+      }
+      ok &= check_hp("o_proj + post norm: hp", hp2);
+      const bool same = hp2 == hp;
+      printf("  %-22s %s\n", "hp of both entries", same ? "identical" : "DIFFER");
+      ok &= same;
+      Checker cz{"o_proj + post norm: zn"};
+      for (int r = 0; r < M; ++r) {
+        if (slot[r] < 0) continue;
+        float ss = 0.f;
+        for (int c = 0; c < D; ++c) ss += fb(hp2[(size_t)r * D + c]) * fb(hp2[(size_t)r * D + c]);
+        const float inv = 1.0f / std::sqrt(ss / (float)D + eps);
+        for (int c = 0; c < D; ++c) {
+          const double t = fb(bf((double)((float)fb(hp2[(size_t)r * D + c]) * inv)));
+          const double ut = std::ldexp(1.0, std::ilogb(std::fabs(t) + 1e-30) - 7);
+          cz.add(zn[(size_t)slot[r] * D + c], fb(lw[c]) * t, 0, std::fabs(fb(lw[c])) * ut);
+        }
+      }
+      ok &= cz.report();
+    }
+
+    const int V = 384;
     auto wl = rnd((size_t)V * D, 0.05f);
     const auto pl = pack(wl, V, D);
     std::vector<uint16_t> logits((size_t)M * V);

@@ -74,18 +74,67 @@ def test_pack_weight_layout(N, K):
     assert torch.equal(out.view(-1), ref.reshape(-1))
 
 
-@pytest.mark.parametrize("M", [1, 37, 128, 200, 256])
-def test_o_proj_residual(M):
-    g = torch.Generator().manual_seed(M)
-    K, N = 3584, 3584
+O_PROJ_CASES = [(1, 3584), (37, 3584), (128, 3584), (200, 3584), (256, 3584), (300, 3584),
+                (256, 1536), (256, 4096), (256, 5120), (129, 5120)]
+
+
+@pytest.mark.parametrize("M,D", O_PROJ_CASES)
+def test_o_proj_residual(M, D):
+    """The all-rows GEMM over one or two passes (<= 128 rows: one row group, <= 256:
+    two, 300: 256 + 44) and the workloads' hidden sizes (1 to 4 K ranges)."""
+    g = torch.Generator().manual_seed(M + D)
+    K, N = D, D
     o, x, w = rnd(M, K, gen=g), rnd(M, N, gen=g), rnd(N, K, std=0.02, gen=g)
     hp = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
-    ws = zeros_ws(_lib.gemm_workspace_bytes(M, N, K))
+    ws = zeros_ws(_lib.o_proj_workspace_bytes(M, N, K))
     wp = packed(w)
     _lib.o_proj_residual(o, x, wp, M, K, N, hp, ws)
     mm = mm64(o, w)
     ref = (x.float().cpu() + mm.float()).to(torch.bfloat16)
     close_bf16(hp, ref, scale=ref.float().abs() + mm.float().abs(), atol=acc_bound(o, w))
+
+
+@pytest.mark.parametrize("M,D", [(256, 3584), (37, 3584), (300, 4096), (256, 5120)])
+def test_o_proj_post_norm(M, D):
+    """hp as sf_o_proj_residual's (bit for bit), and zn[slot[r]] = bf16(w * bf16(hp[r]
+    * rstd)) for the recomputed rows on the kernel's own hp; rows without a slot
+    leave zn untouched."""
+    g = torch.Generator().manual_seed(7 * M + D)
+    o, x, w = rnd(M, D, gen=g), rnd(M, D, gen=g), rnd(D, D, std=0.02, gen=g)
+    lnw = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).cuda()
+    keep = torch.rand(M, generator=g) < 0.6
+    slot = torch.full((M,), -1, dtype=torch.int32)
+    slot[keep] = torch.arange(int(keep.sum()), dtype=torch.int32)
+    slot = slot.cuda()
+    R = int(keep.sum())
+    ws = zeros_ws(_lib.o_proj_workspace_bytes(M, D, D))
+    wp = packed(w)
+    hp = torch.empty(M, D, dtype=torch.bfloat16, device="cuda")
+    zn = torch.full((R + 1, D), 7.0, dtype=torch.bfloat16, device="cuda")
+    for _ in range(2):  # twice through one workspace
+        _lib.o_proj_post_norm(o, x, wp, M, D, D, slot, lnw, 1e-6, hp, zn, ws)
+    hp1 = torch.empty_like(hp)
+    _lib.o_proj_residual(o, x, wp, M, D, D, hp1, ws)
+    torch.cuda.synchronize()
+    assert torch.equal(hp, hp1)
+    mm = mm64(o, w)
+    ref = (x.float().cpu() + mm.float()).to(torch.bfloat16)
+    close_bf16(hp, ref, scale=ref.float().abs() + mm.float().abs(), atol=acc_bound(o, w))
+    h = hp[keep.cuda()].float()
+    z_ref = lnw * (h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + 1e-6)).to(torch.bfloat16)
+    close_bf16(zn[:R], z_ref, scale=2 * z_ref.float().abs())
+    assert torch.all(zn[R] == 7.0)
+
+
+@pytest.mark.parametrize("M", [1, 100, 300])
+def test_lm_head_rows(M):
+    """One row group (<= 128 rows) and two passes (300 rows) of the head GEMM."""
+    g = torch.Generator().manual_seed(M)
+    D, V = 3584, 16384
+    x, w = rnd(M, D, gen=g), rnd(V, D, std=0.02, gen=g)
+    logits = torch.empty(M, V, dtype=torch.bfloat16, device="cuda")
+    _lib.lm_head(x, M, packed(w), D, V, logits)
+    close_bf16(logits, mm64(x, w), atol=acc_bound(x, w))
 
 
 @pytest.mark.parametrize("count,D,I,bucket", [(1, 1536, 8960, 256), (39, 1536, 8960, 256),

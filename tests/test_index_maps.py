@@ -38,7 +38,8 @@ def test_index_maps(checker):
     r = subprocess.run([str(checker), str(lib)], capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stdout + r.stderr
     out = r.stdout
-    for family in ("gemm plans", "gemm columns", "operand reads", "page-group", "attention grids"):
+    for family in ("gemm plans", "all-rows GEMM", "gemm columns", "operand reads", "page-group",
+                   "attention grids"):
         assert family in out, out
     assert out.strip().splitlines()[-1].startswith("OK"), out
 

@@ -2,8 +2,9 @@
 sf_qkv.hip, sf_gemm_core.h) run on the CPU through the SIMT simulator of
 tests/sim, called through the library's entry points: weight packing, FFN
 gate/up (stream-K, SiLU epilogue from registers or in the fix-up), FFN down
-(stream-K with partial slots, fix-up, row scatter), o_proj + residual and
-lm_head (static row counts), and the QKV projection with bias, RoPE from
+(stream-K with partial slots, fix-up, row scatter), o_proj + residual (+ the
+post-attention norm) and lm_head (all-rows GEMM, static row counts, one or two
+passes, one to three K ranges), and the QKV projection with bias, RoPE from
 absolute-position tables, the optional q scale and the scatter by flat row, for
 row counts of one row up to two passes of 128 rows, against float64 dot products
 rounded as each epilogue specifies (tests/sim/gemm_sim.cpp states the
@@ -29,7 +30,7 @@ def gemm_sim(tmp_path_factory):
     d = tmp_path_factory.mktemp("gemm_sim")
     # copies, so the sources' quoted includes of sf_common.h resolve to the
     # simulator's host header instead of the HIP one next to the originals
-    for f in ("sf_ffn.hip", "sf_qkv.hip", "sf_gemm_core.h"):
+    for f in ("sf_ffn.hip", "sf_qkv.hip", "sf_gemm_core.h", "sf_gemm_rows.h"):
         (d / f).write_text((CSRC / f).read_text())
     flags = ["-std=c++20", "-O2", "-Wno-unknown-attributes", "-Wno-psabi", f"-I{SIM}",
              f"-I{ROOT / 'include'}", f"-I{CSRC}"]
@@ -54,6 +55,8 @@ def gemm_sim(tmp_path_factory):
     (512, 640, 130, 256, 130, 3),   # three of four row blocks in use
     (256, 384, 1, 256, 1, 4),       # a single row
     (640, 768, 200, 256, 256, 5),   # four full row blocks for the static-M GEMMs
+    (256, 384, 50, 64, 300, 8),     # all-rows GEMMs in two passes (256 + 44 rows)
+    (1152, 384, 40, 64, 40, 9),     # o_proj over three K ranges
 ], ids=lambda c: "D%d_I%d_count%d_bucket%d_M%d" % c[:5])
 def test_gemm_kernels_in_simulator(gemm_sim, case):
     r = subprocess.run([str(gemm_sim), *map(str, case)], capture_output=True, text=True,
