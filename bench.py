@@ -171,7 +171,7 @@ PMC_KERNELS = {
     "gate_up": ("sfg::gemm_sk_kernel<2, 2,", "silu_fixup_kernel"),
     "down": ("sfg::gemm_sk_kernel<1, 1,", "down_fixup_kernel"),
     "final_norm": ("sf_gate_rows_kernel",),
-    "lm_head": ("sfg::gemm_rows_kernel<",),
+    "lm_head": ("Cijk_",),
     "gate": ("sf_gate_rows_kernel", "sf_gate_compact_kernel"),
 }
 

@@ -19,8 +19,7 @@ fastdllm_v2_folded.py:296-361 for the launch sequence, :117-220 for the math):
   sf_ffn_gate_up      gate/up GEMM + SiLU*mul on compacted rows  (HIP)
   sf_ffn_down_scatter down GEMM, scattered to the per-row FFN table (HIP)
 and after the last layer the residual update + final RMSNorm (HIP) and the
-lm_head (sf_lm_head, the all-rows GEMM; hipBLASLt for a vocabulary that is not a
-multiple of 128).  sf_chain_correct (the reference's incremental form of the
+lm_head (hipBLASLt; sf_lm_head stays in the C ABI).  sf_chain_correct (the reference's incremental form of the
 folded rows' attention) stays in the C ABI; the engine forms it with sf_attn_rows.
 
 Nothing here syncs with the host: the branch parent map is computed from the
@@ -248,10 +247,6 @@ class FoldedVerifyEngine:
                                      _lib.pack_weight(m.up_proj.weight.contiguous()),
                                      _lib.pack_weight(m.down_proj.weight.contiguous())))
             self._packed_o.append(_lib.pack_weight(a.o_proj.weight.contiguous()))
-        # the head through sf_lm_head where its shape allows (V % 128, D % 64)
-        hw = self.head.weight
-        self._packed_head = (_lib.pack_weight(hw.contiguous())
-                             if hw.shape[0] % 128 == 0 and hw.shape[1] % 64 == 0 else None)
         self._bufs: Dict[Tuple[int, int, int], _Buffers] = {}
         # HIP graphs of the layer loop, keyed by shape / prefix / delta / cache
         # (one per branch count the decode loop visits, B1 = 1..8, per sequence's
@@ -263,14 +258,13 @@ class FoldedVerifyEngine:
 
     def lm_head(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
         """logits = x . Wlm^T for every row of x [M, D] (bf16; a fresh tensor unless
-        ``out`` is given): sf_lm_head, one pass over the head weights for every row."""
+        ``out`` is given), on hipBLASLt: at M = 256 rows the head does 256 flop per
+        weight byte, near the MFMA/HBM ridge, where the library's tiles run 302 us at
+        the 7B shape against 368 us for sf_lm_head's all-rows kernel."""
         M = x.shape[0]
         if out is None:
             out = torch.empty(M, self.V, dtype=torch.bfloat16, device=self.device)
-        if self._packed_head is None:
-            return torch.mm(x, self.head.weight.t(), out=out)
-        _lib.lm_head(x, M, self._packed_head, self.D, self.V, out)
-        return out
+        return torch.mm(x, self.head.weight.t(), out=out)
 
     @staticmethod
     def _check_device(device: torch.device) -> None:
