@@ -38,9 +38,14 @@ from typing import Dict, List, Optional, Tuple
 import torch
 
 from specfold_amd import _lib
-from specfold_amd.kv_cache import PagedKVCache, cache_length, prefix_view
+from specfold_amd.kv_cache import ContiguousMirror, PagedKVCache, cache_length, prefix_view
 
 logger = logging.getLogger(__name__)
+
+
+def _device_cache(cache) -> bool:
+    """A cache whose buffers stay put and whose length lives in device memory."""
+    return isinstance(cache, (PagedKVCache, ContiguousMirror))
 
 
 def build_parent_map(batched_input: torch.Tensor) -> Tuple[List[Optional[int]], List[int]]:
@@ -255,6 +260,7 @@ class FoldedVerifyEngine:
         self.max_graphs = 48
         self._graphs: Dict[tuple, tuple] = {}
         self._rope: Optional[Tuple[torch.Tensor, torch.Tensor]] = None
+        self._mirror: Optional[ContiguousMirror] = None   # reference-style caches
 
     def lm_head(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
         """logits = x . Wlm^T for every row of x [M, D] (bf16; a fresh tensor unless
@@ -331,12 +337,16 @@ class FoldedVerifyEngine:
             raise ValueError("append needs B1 == 1 and a PagedKVCache")
         batched_input = batched_input.to(self.device).contiguous()
         P = cache_length(cache)
-        P_alloc = cache.capacity if isinstance(cache, PagedKVCache) else P
+        if cache is not None and not _device_cache(cache):
+            # a reference-style cache is read through the engine's mirror: fixed
+            # buffers and a device length, so the captured step outlives its commits
+            cache = self._mirror_of(cache, P) if P > 0 else None
+        P_alloc = cache.capacity if _device_cache(cache) else P
         buf = self.buffers(B1, N, bucket, P_alloc)
         if causal and self.gate_mode != _lib.SF_GATE_ALL:
             raise ValueError("a causal forward recomputes every row (gate mode SF_GATE_ALL)")
         self.rope_tables(P + N)
-        if not isinstance(cache, PagedKVCache):
+        if not _device_cache(cache):
             buf.pos0.fill_(P)
         qs = None
         if q_scale is not None:
@@ -517,7 +527,7 @@ class FoldedVerifyEngine:
             batch.refresh_positions()
         hidden = base.embed_tokens(tokens).reshape(BN, D)
         cos, sin = self._rope
-        pos0 = cache.length_dev if isinstance(cache, PagedKVCache) else buf.pos0
+        pos0 = cache.length_dev if _device_cache(cache) else buf.pos0
         for li, lyr in enumerate(self.layers):
             count = buf.count_slab[li:li + 1]
             segcnt = buf.segcnt_slab[li * B1:(li + 1) * B1]
@@ -622,15 +632,32 @@ class FoldedVerifyEngine:
 
     @staticmethod
     def _cache_key(cache):
-        """A paged cache's identity for a captured graph (its buffers' addresses)."""
+        """A paged cache's or the mirror's identity for a captured graph (its
+        buffers' addresses)."""
         if cache is None:
             return None
+        if isinstance(cache, ContiguousMirror):
+            return (id(cache), cache.k.data_ptr(), cache.v.data_ptr(),
+                    cache.length_dev.data_ptr(), cache.capacity)
         return (id(cache), cache.k_pages.data_ptr(), cache.v_pages.data_ptr(),
                 cache.page_table.data_ptr(), cache.length_dev.data_ptr(), cache.capacity)
 
+    def _mirror_of(self, cache, P: int) -> ContiguousMirror:
+        """The engine's mirror of a reference-style cache, synced to it.  Capacity:
+        the next power of two above the prefix (at least 1024 keys); outgrowing it
+        allocates a larger mirror and drops the graphs captured against the old."""
+        m = self._mirror
+        if m is None or m.capacity < P:
+            cap = max(1024, 1 << max(0, int(P) - 1).bit_length())
+            self._graphs.clear()
+            self._mirror = m = ContiguousMirror(self.L, self.Hkv, self.hd, cap,
+                                                device=self.device)
+        m.sync(cache)
+        return m
+
     def _graph_key(self, buf: _Buffers, cache, P: int, delta: float, bucket: int,
                    q_scaled: bool = False, causal: bool = False):
-        if isinstance(cache, PagedKVCache):
+        if _device_cache(cache):
             # the prefix length is read on the device: one graph for every length
             P = -1
             ck = self._cache_key(cache)
@@ -708,7 +735,7 @@ class FoldedVerifyEngine:
                                     segcnt, buf.slot, buf.rstd, buf.xn)
 
         cos, sin = self._rope
-        pos0 = cache.length_dev if isinstance(cache, PagedKVCache) else buf.pos0
+        pos0 = cache.length_dev if _device_cache(cache) else buf.pos0
 
         def qkv():
             _lib.qkv_rope(buf.xn, buf.rows, count, bucket, BN, w_qkv, b_qkv, cos, sin,

@@ -127,6 +127,75 @@ class PagedKVCache:
         self.length_dev.fill_(P)
 
 
+class ContiguousMirror:
+    """Engine-owned contiguous copy of a reference-style cache (the reference's
+    ``DynamicCache``, which grows by ``torch.cat`` and so moves every layer's
+    tensors at each commit: fastdllm_v2_folded.py:122 reads it per layer).
+
+    K and V of every layer live in fixed buffers ``[L, Hkv, capacity, hd]`` with the
+    length in device memory, so a verify step captured against the mirror stays
+    valid while the reference cache grows: one capture per step shape instead of
+    one per commit.  ``sync`` copies the whole prefix again whenever the cache's
+    length or any layer's storage changed since the last sync (a commit, a crop, or
+    another sequence's cache); a cache rewritten in place at the same length and
+    the same storage is not detected (call ``invalidate`` after such an update)."""
+
+    def __init__(self, num_layers: int, num_kv_heads: int, head_dim: int, capacity: int,
+                 device="cuda", dtype=torch.bfloat16):
+        self.num_layers = num_layers
+        self.Hkv = num_kv_heads
+        self.hd = head_dim
+        self.capacity = int(capacity)
+        self.device = torch.device(device)
+        shape = (num_layers, num_kv_heads, self.capacity, head_dim)
+        self.k = torch.zeros(shape, dtype=dtype, device=self.device)
+        self.v = torch.zeros(shape, dtype=dtype, device=self.device)
+        self.length = 0
+        self.length_dev = torch.zeros(1, dtype=torch.int32, device=self.device)
+        self._sig = None
+
+    def get_seq_length(self, layer_idx: int = 0) -> int:
+        return self.length
+
+    def __len__(self) -> int:
+        return self.num_layers
+
+    def invalidate(self) -> None:
+        self._sig = None
+
+    @staticmethod
+    def signature(cache, num_layers: int) -> tuple:
+        views = [prefix_view(cache, li) for li in range(num_layers)]
+        return (id(cache), cache_length(cache),
+                tuple((0, 0) if pv is None else (pv.k.data_ptr(), pv.v.data_ptr())
+                      for pv in views))
+
+    def sync(self, cache) -> bool:
+        """Make the mirror hold ``cache``'s prefix; returns True if it copied."""
+        sig = self.signature(cache, self.num_layers)
+        if sig == self._sig:
+            return False
+        P = sig[1]
+        if P > self.capacity:
+            raise ValueError(f"prefix of {P} keys exceeds the mirror's capacity {self.capacity}")
+        for li in range(self.num_layers):
+            pv = prefix_view(cache, li)
+            if pv is None:
+                continue
+            self.k[li, :, :P].copy_(pv.k)
+            self.v[li, :, :P].copy_(pv.v)
+        self.length = P
+        self.length_dev.fill_(P)
+        self._sig = sig
+        return True
+
+    def view(self, li: int) -> PrefixView:
+        return PrefixView(k=self.k[li], v=self.v[li], page_table=None, length=self.length,
+                          page_size=max(self.capacity, 1), page_stride=0,
+                          head_stride=self.capacity * self.hd, capacity=self.capacity,
+                          length_dev=self.length_dev)
+
+
 def contiguous_view(k: torch.Tensor, v: torch.Tensor) -> PrefixView:
     """Kernel view of a reference-style contiguous [1, Hkv, P, hd] layer cache."""
     if k.dim() != 4 or k.shape[0] != 1:
@@ -154,7 +223,7 @@ def prefix_view(cache, li: int) -> Optional[PrefixView]:
     """Kernel view of layer li of either a PagedKVCache or a reference-style cache."""
     if cache is None:
         return None
-    if isinstance(cache, PagedKVCache):
+    if isinstance(cache, (PagedKVCache, ContiguousMirror)):
         return cache.view(li)
     if len(cache) <= li:
         return None

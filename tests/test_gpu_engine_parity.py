@@ -186,3 +186,37 @@ def test_graph_replays_match_eager():
     eng.use_graphs = True
     for _ in range(2):
         assert torch.equal(eng.forward(t, cache, case.delta), ref2)
+
+
+def test_reference_cache_graph_survives_commits():
+    """A transformers DynamicCache (the reference's cache, fastdllm_v2_folded.py:122)
+    grown by torch.cat over three block commits: the engine reads it through its
+    mirror, so the verify step is captured once for the branch count and every
+    replay equals the eager step bit for bit, before and after each commit."""
+    from transformers.cache_utils import DynamicCache
+    case = make_case(SHAPE_G7, 13, P=130, delta=0.05)
+    model = to_gpu_model(case.model_cpu)
+    eng = FoldedVerifyEngine(model)
+    cache = DynamicCache()
+    for li, (k, v) in enumerate(case.kv):
+        cache.update(k.cuda(), v.cuda(), li)
+    Hkv, hd = case.kv[0][0].shape[1], case.kv[0][0].shape[3]
+    t = case.tokens.cuda()
+    gen = torch.Generator().manual_seed(4)
+    captures = 0
+    for commit in range(4):
+        eng.use_graphs = False
+        ref = eng.forward(t, cache, case.delta)
+        eng.use_graphs = True
+        n0 = len(eng._graphs)
+        for _ in range(2):
+            out = eng.forward(t, cache, case.delta)
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref), f"commit {commit}: replay differs from eager"
+        captures += len(eng._graphs) - n0
+        for li in range(len(case.kv)):   # commit 32 tokens: every layer grows by torch.cat
+            kn = torch.randn(1, Hkv, 32, hd, generator=gen).to(torch.bfloat16).cuda()
+            vn = torch.randn(1, Hkv, 32, hd, generator=gen).to(torch.bfloat16).cuda()
+            cache.update(kn, vn, li)
+    assert cache.get_seq_length() == 130 + 4 * 32
+    assert captures == 1, f"{captures} captures over four prefix lengths"
