@@ -53,17 +53,17 @@ struct Ring {
 // Rows handled by one workgroup of a launch whose row count is at most mcap.
 inline int row_block(int mcap) { return mcap <= 64 ? 64 : 128; }
 
-// The A fragments (NMT m tiles, 1 KB apart) and weight fragments (WN tiles, 2 KB
-// apart) of K chunk C of a stage, read from LDS without waiting (sf_lds_read16
-// with compile-time offsets).
-template <int NMT, int WN, int I = 0>
+// The A fragments (NMT m tiles, 1 KB apart) and weight fragments (WN tiles, CPS KB
+// apart: a tile's CPS chunk blocks follow each other) of K chunk C of a stage, read
+// from LDS without waiting (sf_lds_read16 with compile-time offsets).
+template <int NMT, int WN, int CPS = 2, int I = 0>
 SF_DEV void lds_fragments(sf_u32x4 (&f)[NMT + WN], sf_lds_off a_addr, sf_lds_off w_addr) {
   if constexpr (I < NMT) {
     f[I] = sf_lds_read16<I * 1024>(a_addr);
-    lds_fragments<NMT, WN, I + 1>(f, a_addr, w_addr);
+    lds_fragments<NMT, WN, CPS, I + 1>(f, a_addr, w_addr);
   } else if constexpr (I < NMT + WN) {
-    f[I] = sf_lds_read16<(I - NMT) * 2048>(w_addr);
-    lds_fragments<NMT, WN, I + 1>(f, a_addr, w_addr);
+    f[I] = sf_lds_read16<(I - NMT) * CPS * 1024>(w_addr);
+    lds_fragments<NMT, WN, CPS, I + 1>(f, a_addr, w_addr);
   }
 }
 

@@ -56,11 +56,12 @@ void gemm_rows_kernel(const uint16_t* __restrict__ A, int M, const uint16_t* __r
   // this wave's copies: lane L of an A copy brings row L/4 of its m tile (rows
   // past M re-read row M - 1), A unit a_copy_unit(L) of the chunk; lane L of a
   // weight copy brings lane L's fragment of its (tile, chunk) block
+  constexpr int CPS = St::kCPS;
   const uint16_t* asrc[St::kDA];
   int adst[St::kDA];
 #pragma unroll
   for (int j = 0; j < St::kDA; ++j) {
-    const int cq = wv + 8 * j;
+    const int cq = rows_a_copy(wv + 8 * j, St::kNA);
     const int ch = rows_a_chunk(cq, kMT), mt = rows_a_mtile(cq, kMT);
     const int r = sf_imin(mt * 16 + (lane >> 2), M - 1);
     asrc[j] = A + (size_t)r * K + ch * 32 + a_copy_unit(lane) * 8;
@@ -70,19 +71,19 @@ void gemm_rows_kernel(const uint16_t* __restrict__ A, int M, const uint16_t* __r
   int wdst[St::kDW];
 #pragma unroll
   for (int j = 0; j < St::kDW; ++j) {
-    const int cq = wv + 8 * j;
-    const int tw = rows_w_tile(cq), c = rows_w_chunk(cq);
+    const int cq = rows_w_copy(wv + 8 * j, St::kNW);
+    const int tw = rows_w_tile(cq, CPS), c = rows_w_chunk(cq, CPS);
     wsrc[j] = weight_lane_ptr(W, t * St::kTW + tw, K, lane) + (size_t)c * kKsStride;
-    wdst[j] = St::kA + (tw * 2 + c) * 64;
+    wdst[j] = St::kA + (tw * CPS + c) * 64;
   }
   auto slot = [&](int j) { return ring + j * St::kWords; };
   auto issue = [&](int sg, sf_u32x4* sl) {
     const int sc = sf_imin(sg, slast);
 #pragma unroll
-    for (int j = 0; j < St::kDA; ++j) sf_lds_dma16(asrc[j] + sc * kKC, sl + adst[j]);
+    for (int j = 0; j < St::kDA; ++j) sf_lds_dma16(asrc[j] + sc * St::kKS, sl + adst[j]);
 #pragma unroll
     for (int j = 0; j < St::kDW; ++j)
-      sf_lds_dma16(wsrc[j] + (size_t)weight_chunk(sc, 0) * kKsStride, sl + wdst[j]);
+      sf_lds_dma16(wsrc[j] + (size_t)sc * CPS * kKsStride, sl + wdst[j]);
   };
 #pragma unroll
   for (int j = 0; j < R - 1; ++j) issue(s0 + j, slot(j));
@@ -97,7 +98,7 @@ void gemm_rows_kernel(const uint16_t* __restrict__ A, int M, const uint16_t* __r
   // of A tile (c, mt); its weight fragment of tile cgrp*WN + tt: word `lane` of
   // block (tile, c)
   const sf_lds_off a_byte = (sf_lds_off)(rgrp * 8 * 64 + a_read_word(lane)) * 16;
-  const sf_lds_off w_byte = (sf_lds_off)(St::kA + cgrp * WN * 2 * 64 + lane) * 16;
+  const sf_lds_off w_byte = (sf_lds_off)(St::kA + cgrp * WN * CPS * 64 + lane) * 16;
 #pragma unroll 1
   for (int sb = s0; sb < s1; sb += R) {
 #pragma unroll
@@ -107,9 +108,9 @@ void gemm_rows_kernel(const uint16_t* __restrict__ A, int M, const uint16_t* __r
         issue(sb + j + R - 1, slot((j + R - 1) % R));
         const sf_lds_off base = sf_lds_addr(slot(j));
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
+        for (int c = 0; c < CPS; ++c) {
           sf_u32x4 f[8 + WN];
-          lds_fragments<8, WN>(f, base + a_byte + c * kMT * 1024, base + w_byte + c * 1024);
+          lds_fragments<8, WN, CPS>(f, base + a_byte + c * kMT * 1024, base + w_byte + c * 1024);
           sf_lds_reads_done(f);
 #pragma unroll
           for (int i = 0; i < 8; ++i)
@@ -154,7 +155,7 @@ inline void launch_rows(const uint16_t* A, int M, const uint16_t* W, int K, int 
   for (int m0 = 0; m0 < M; m0 += 256) {
     const int mb = sf_imin(256, M - m0);
     const int rg = rows_rg(mb);
-    const RowsPlan p{rows_tiles<WN>(N, rg), ks, K / kKC};
+    const RowsPlan p{rows_tiles<WN>(N, rg), ks, rows_stages(K)};
     const dim3 grid(rows_grid(p));
     const uint16_t* a = A + (size_t)m0 * K;
     float* pp = part ? part + (size_t)m0 * N : nullptr;

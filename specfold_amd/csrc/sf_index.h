@@ -158,21 +158,30 @@ SF_IDX int rows_item(int g, int G) {
 SF_IDX int rows_split_begin(int s, const RowsPlan& p) {
   return (int)((long long)p.S * s / p.KS);
 }
-// Stage layout of a workgroup of RG row groups and WN 16-column tiles per wave.
-template <int RG, int WN>
+// Stage layout of a workgroup of RG row groups and WN 16-column tiles per wave,
+// CPS 32-wide K chunks per stage.  The copies of a stage are dealt over the 8 waves
+// (copy q = wv + 8j); a wave with fewer real copies repeats the last one (the same
+// bytes to the same place), so every wave issues the same number per stage.
+#ifndef SFG_ROWS_CPS
+#define SFG_ROWS_CPS 2
+#endif
+template <int RG, int WN, int CPS = SFG_ROWS_CPS>
 struct RowsStage {
-  static constexpr int kMB = 128 * RG;     // rows per pass
-  static constexpr int kMT = kMB / 16;     // m tiles
-  static constexpr int kCG = 8 / RG;       // column groups
-  static constexpr int kTW = kCG * WN;     // 16-column tiles of a workgroup tile
-  static constexpr int kA = 2 * kMT * 64;  // 16-byte words of A per stage
-  static constexpr int kW = kTW * 2 * 64;  // words of weights per stage
+  static constexpr int kMB = 128 * RG;       // rows per pass
+  static constexpr int kMT = kMB / 16;       // m tiles
+  static constexpr int kCG = 8 / RG;         // column groups
+  static constexpr int kTW = kCG * WN;       // 16-column tiles of a workgroup tile
+  static constexpr int kCPS = CPS;           // K chunks per stage
+  static constexpr int kKS = 32 * CPS;       // K per stage
+  static constexpr int kNA = CPS * kMT;      // A tile copies per stage
+  static constexpr int kNW = CPS * kTW;      // weight block copies per stage
+  static constexpr int kA = kNA * 64;        // 16-byte words of A per stage
+  static constexpr int kW = kNW * 64;        // words of weights per stage
   static constexpr int kWords = kA + kW;
-  static constexpr int kDA = 2 * kMT / 8;  // A copies per wave per stage
-  static constexpr int kDW = kTW * 2 / 8;  // weight copies per wave per stage
+  static constexpr int kDA = (kNA + 7) / 8;  // A copies per wave per stage
+  static constexpr int kDW = (kNW + 7) / 8;  // weight copies per wave per stage
   static constexpr int kRing =
       kLdsBudget / (kWords * 16) < SFG_RING_MAX ? kLdsBudget / (kWords * 16) : SFG_RING_MAX;
-  static_assert(kDA * 8 == 2 * kMT && kDW * 8 == kTW * 2, "copies split evenly over 8 waves");
 };
 // A pass of at most 128 rows uses one row group (RG = 1, 8 column groups) with
 // half the tiles per wave (at least one), a pass of up to 256 rows two; WN is
@@ -182,20 +191,23 @@ template <int WN>
 constexpr int rows_wn(int rg) { return rg == 2 ? WN : (WN > 1 ? WN / 2 : 1); }
 template <int WN>
 inline int rows_tiles(int N, int rg) { return N / (16 * rows_wn<WN>(rg) * (8 / rg)); }
+// K stages of an all-rows GEMM (32·CPS each).
+inline int rows_stages(int K) { return K / (32 * SFG_ROWS_CPS); }
 // K ranges of an all-rows GEMM over M rows: the first pass's plan, used by every
 // pass (the consumer adds the same number of partial slots for every row).
 template <int WN>
 inline int rows_splits(int M, int N, int K, int ks_max) {
   const int rg = rows_rg(sf_imin(256, M));
-  return make_rows_plan(rows_tiles<WN>(N, rg), K / kKC, ks_max).KS;
+  return make_rows_plan(rows_tiles<WN>(N, rg), rows_stages(K), ks_max).KS;
 }
-// Direct copies of a stage: copy q = wv + 8j of the 2·MT A tiles (MT m tiles of
-// 16 rows; chunk q / MT, m tile q % MT, in the tile layout of a_copy) and of the
-// 2·TW weight blocks (TW tiles of 16 columns; tile q / 2, chunk q % 2).
+// Copy q of a stage (clamped to the last real copy): A tile (chunk q / MT, m tile
+// q % MT, in the tile layout of a_copy); weight block (tile q / CPS, chunk q % CPS).
+SF_IDX int rows_a_copy(int q, int NA) { return sf_imin(q, NA - 1); }
 SF_IDX int rows_a_chunk(int q, int MT) { return q / MT; }
 SF_IDX int rows_a_mtile(int q, int MT) { return q % MT; }
-SF_IDX int rows_w_tile(int q) { return q >> 1; }
-SF_IDX int rows_w_chunk(int q) { return q & 1; }
+SF_IDX int rows_w_copy(int q, int NW) { return sf_imin(q, NW - 1); }
+SF_IDX int rows_w_tile(int q, int CPS) { return q / CPS; }
+SF_IDX int rows_w_chunk(int q, int CPS) { return q % CPS; }
 // fp32 partials of a plan for M rows and N columns: [KS][M][N].
 inline size_t rows_part_bytes(const RowsPlan& p, int M, int N) {
   return p.KS > 1 ? (size_t)p.KS * M * N * sizeof(float) : 0;

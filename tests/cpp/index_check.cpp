@@ -167,49 +167,51 @@ static void walk_rows_pass(const sfg::RowsPlan& p, int M, int m0, int mb, int N,
     if (s == p.KS - 1) CHECK(s1 == p.S, "last range");
   }
   // copies of one stage: each A tile (chunk, m tile) and weight block (tile, chunk)
-  // exactly once over the 8 waves
-  std::vector<int> acell(2 * St::kMT, 0), wcell(2 * St::kTW, 0);
+  // at least once over the 8 waves (waves past the last copy repeat it)
+  constexpr int CPS = St::kCPS;
+  std::vector<int> acell(St::kNA, 0), wcell(St::kNW, 0);
   for (int wv = 0; wv < 8; ++wv) {
     for (int j = 0; j < St::kDA; ++j) {
-      const int cq = wv + 8 * j;
+      const int cq = sfg::rows_a_copy(wv + 8 * j, St::kNA);
       const int ch = sfg::rows_a_chunk(cq, St::kMT), mt = sfg::rows_a_mtile(cq, St::kMT);
-      CHECK(ch < 2 && mt < St::kMT, "a copy");
+      CHECK(ch < CPS && mt < St::kMT, "a copy");
       ++acell[ch * St::kMT + mt];
       for (int L = 0; L < 64; ++L) {
         const int r = sf_imin(mt * 16 + (L >> 2), mb - 1);
         CHECK(r >= 0 && r < mb && m0 + r < M, "a row");
-        const size_t last = (size_t)(m0 + r) * K + (size_t)(p.S - 1) * sfg::kKC + ch * 32 +
+        const size_t last = (size_t)(m0 + r) * K + (size_t)(p.S - 1) * St::kKS + ch * 32 +
                             sfg::a_copy_unit(L) * 8 + 8;
         CHECK(last <= (size_t)M * K, "a load");
       }
     }
     for (int j = 0; j < St::kDW; ++j) {
-      const int cq = wv + 8 * j;
-      const int tw = sfg::rows_w_tile(cq), c = sfg::rows_w_chunk(cq);
-      CHECK(tw < St::kTW && c < 2, "w copy");
-      ++wcell[tw * 2 + c];
+      const int cq = sfg::rows_w_copy(wv + 8 * j, St::kNW);
+      const int tw = sfg::rows_w_tile(cq, CPS), c = sfg::rows_w_chunk(cq, CPS);
+      CHECK(tw < St::kTW && c < CPS, "w copy");
+      ++wcell[tw * CPS + c];
       for (int t : {0, p.T - 1})
         for (int L : {0, 63}) {
           const size_t e = sfg::weight_lane_ptr((size_t)0, t * St::kTW + tw, K, L) +
                            (size_t)c * sfg::kKsStride +
-                           (size_t)sfg::weight_chunk(p.S - 1, 0) * sfg::kKsStride + 8;
+                           (size_t)(p.S - 1) * CPS * sfg::kKsStride + 8;
           CHECK(e <= (size_t)N * K, "w load");
         }
     }
   }
-  for (int v : acell) CHECK(v == 1, "a cell filled %d times", v);
-  for (int v : wcell) CHECK(v == 1, "w cell filled %d times", v);
+  for (int v : acell) CHECK(v >= 1, "a cell filled %d times", v);
+  for (int v : wcell) CHECK(v >= 1, "w cell filled %d times", v);
+  CHECK(p.S * St::kKS == K, "stages cover K");
   // fragment reads inside the stage's words
   for (int wv = 0; wv < 8; ++wv) {
     const int rgrp = wv / St::kCG, cgrp = wv % St::kCG;
     for (int lane = 0; lane < 64; ++lane)
-      for (int c = 0; c < 2; ++c) {
+      for (int c = 0; c < CPS; ++c) {
         for (int i = 0; i < 8; ++i) {
           const int w = (c * St::kMT + rgrp * 8 + i) * 64 + sfg::a_read_word(lane);
           CHECK(w >= 0 && w < St::kA, "a read word %d", w);
         }
         for (int tt = 0; tt < WN; ++tt) {
-          const int w = St::kA + (cgrp * WN + tt) * 128 + c * 64 + lane;
+          const int w = St::kA + ((cgrp * WN + tt) * CPS + c) * 64 + lane;
           CHECK(w >= St::kA && w < St::kWords, "w read word %d", w);
         }
       }
@@ -248,7 +250,7 @@ static void walk_rows(int M, int N, int K, int ks_max, size_t ws_bytes) {
   for (int m0 = 0; m0 < M; m0 += 256) {
     const int mb = sf_imin(256, M - m0);
     const int rg = sfg::rows_rg(mb);
-    const sfg::RowsPlan p{sfg::rows_tiles<WN>(N, rg), ks, K / sfg::kKC};
+    const sfg::RowsPlan p{sfg::rows_tiles<WN>(N, rg), ks, sfg::rows_stages(K)};
     if (rg == 1)
       walk_rows_pass<1, sfg::rows_wn<WN>(1)>(p, M, m0, mb, N, K, ks, part_elems, &hit);
     else
