@@ -547,6 +547,15 @@ def main(argv=None) -> int:
     prefill_s = time.time() - t0
     print(f"[bench] prefill {len(gens)} x {w.prefix} tokens in {prefill_s:.2f}s", file=sys.stderr,
           flush=True)
+    # start-up work of a serving engine: the verify step's graph for every branch
+    # count the draft graph can produce, captured against each sequence's cache
+    t0 = time.time()
+    warmed = sum(g.warm_graphs() for g in gens if hasattr(g, "warm_graphs")) if not lockstep else 0
+    torch.cuda.synchronize()
+    warm_s = time.time() - t0
+    if warmed:
+        print(f"[bench] {warmed} verify-step graphs captured in {warm_s:.2f}s", file=sys.stderr,
+              flush=True)
     for i in range(args.warmup):
         advance(i)
     kinds = {}
@@ -705,6 +714,7 @@ def main(argv=None) -> int:
         "decode_step_kinds": kinds,
         "tokens_per_step": round(tokens_per_step, 4),
         "prefill_s": round(prefill_s, 3),
+        "graph_warmup": {"graphs": warmed, "s": round(warm_s, 3)},
         "roofline": dict(kernels[dominant], kernel=dominant),
         "kernels": kernels,
         "copy_calibration": copy,

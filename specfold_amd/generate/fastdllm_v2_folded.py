@@ -60,6 +60,40 @@ class SpecFoldHIPFastDLLMV2Generation(FastDLLMV2SpeculativeGeneration):
             eng = FoldedVerifyEngine(ex.model, gate_mode=self.gate_mode)
         self._engine = eng
 
+    def draft_limit(self) -> int:
+        """The most draft blocks a verify step can carry: the draft graph's nodes."""
+        g = self.calibration_graph or {}
+        return sum(1 for n in g.get("selected_nodes", []) if n.get("ij_set"))
+
+    @torch.no_grad()
+    def warm_graphs(self, past_key_values=None) -> int:
+        """Capture the verify step's HIP graph (and select the head GEMM's kernel)
+        for every branch count the draft graph can produce — B1 = 1 (the main block
+        alone, the dense path) and 2 .. drafts + 1 (the folded step) — at the current
+        prefix cache, so the decode loop replays from its first step: the start-up
+        work of a serving engine.  Runs the steps on placeholder tokens (a verify
+        step reads the cache and writes nothing back); the fold counters are
+        untouched.  Returns the number of branch counts prepared."""
+        cache = self._state["cache"] if past_key_values is None else past_key_values
+        if self._engine is None:
+            self._pack_layer_weights()
+        eng = self._engine
+        N = self.block_length
+        main = torch.full((1, N), self.mask_id, dtype=torch.long, device=eng.device)
+        FastDLLMV2SpeculativeGeneration._batched_block_forward(self, main, cache)
+        n = 1
+        prev_mode, eng.gate_mode = eng.gate_mode, self.gate_mode
+        try:
+            for B1 in range(2, self.draft_limit() + 2):
+                tokens = torch.full((B1, N), self.mask_id, dtype=torch.long, device=eng.device)
+                tokens[1:, 0] = torch.arange(1, B1, device=eng.device)
+                bucket = B1 * N if self.fold_bucket is None else min(self.fold_bucket, B1 * N)
+                eng.forward(tokens, cache, delta=self.delta, bucket=bucket)
+                n += 1
+        finally:
+            eng.gate_mode = prev_mode
+        return n
+
     @torch.no_grad()
     def _batched_block_forward(self, batched_input: torch.Tensor, past_key_values) -> torch.Tensor:
         B1, N = batched_input.shape

@@ -111,7 +111,7 @@ class FastDLLMV2SpeculativeGeneration:
                          mask_index: Optional[torch.Tensor] = None, start_pos=None, end_pos=None,
                          small_block_start: Optional[int] = None,
                          small_block_end: Optional[int] = None, stats=None,
-                         **kwargs) -> List[Dict]:
+                         n_masked: Optional[int] = None, **kwargs) -> List[Dict]:
         """One draft block per calibration-graph node (:387-474).
 
         Node ij_set = [(position rank, vocab rank), ...]: take the masked
@@ -119,7 +119,8 @@ class FastDLLMV2SpeculativeGeneration:
         the vocab_rank-th most likely token at the pos_rank-th position.
         ``stats``: sf_logit_stats of the small block's rows, when the caller has
         them (their maximum probabilities and top tokens replace the softmax and
-        the vocabulary topk).
+        the vocabulary topk).  ``n_masked``: the small block's masked-position count
+        when the caller already holds it on the host (no device read).
         """
         if self.calibration_graph is None:
             return []
@@ -131,7 +132,8 @@ class FastDLLMV2SpeculativeGeneration:
             small_mask, small_logits, offset = mask_index, p, 0
         if small_mask is None:
             return []
-        n_masked = int(small_mask.sum().item())
+        if n_masked is None:
+            n_masked = int(small_mask.sum().item())
         if n_masked == 0:
             return []
         active = []
@@ -188,12 +190,51 @@ class FastDLLMV2SpeculativeGeneration:
         first = int(hits[0][1])
         return int((tail[:, :first] == self.mask_id).sum()) == 0
 
+    def _loop_facts(self, x_t: torch.Tensor, plen: int, called, unmask=None) -> Dict:
+        """Everything the loop's control flow reads from the token state, in one
+        device-to-host copy: whether the stop token ends the text (_stop_reached),
+        the block's and each small block's masked positions, the first cached draft
+        state equal to the current block (the draft-logit cache hit, :599-617) and
+        the committed-position count of ``unmask``.  The reference reads each of
+        these with its own host sync; here the decisions of a step, its draft
+        construction and the next step's facts are enqueued behind the forward
+        and read once."""
+        bl, sbs = self.block_length, self.small_block_size
+        blk = x_t[:, -bl:]
+        masked = blk == self.mask_id
+        tail = x_t[:, plen:]
+        is_stop = tail == self.stop_token
+        first = is_stop.int().argmax(dim=1, keepdim=True)      # 0 when there is none
+        ahead = torch.arange(tail.shape[1], device=x_t.device).unsqueeze(0) < first
+        before = ((tail == self.mask_id) & ahead).sum()
+        parts = [(is_stop.any() & (before == 0)).reshape(1), masked.sum().reshape(1),
+                 masked[0].view(-1, sbs).sum(dim=1)]
+        if called:
+            eq = torch.stack([st for st, _ in called]).eq(blk[0]).all(dim=1)
+            parts.append(torch.where(eq.any(), eq.int().argmax(), -1).reshape(1))
+        if unmask is not None:
+            parts.append(unmask.sum().reshape(1))
+        v = torch.cat([t.to(torch.long) for t in parts]).tolist()
+        n_small = bl // sbs
+        out = {"stop": bool(v[0]), "block_masks": v[1], "small": v[2:2 + n_small]}
+        k = 2 + n_small
+        out["hit"] = v[k] if called else -1
+        k += 1 if called else 0
+        out["n"] = v[k] if unmask is not None else None
+        return out
+
     @torch.no_grad()
     def decode_steps(self, prompt_ids: torch.Tensor, defer_forward: bool = False):
         """The decode loop of generate_with_draft_speculation (:483-700) as a
         generator: yields one event per loop iteration —
         {"kind": "prefill" | "commit" | "verify" | "hit", "committed": tokens
         unmasked by the iteration}.  Loop state is on ``self._state``.
+
+        The control flow is the reference's; the host reads it needs (stop token,
+        masked counts, cache hit, committed count) come from one ``_loop_facts``
+        copy per iteration, taken after the iteration's decisions, so the host
+        enqueues the sampling, the draft construction and the decisions while the
+        forward runs.
 
         defer_forward: instead of calling ``_batched_block_forward`` the loop yields
         {"kind": "forward", "batched": [B1, N] tokens, "cache": prefix cache,
@@ -229,11 +270,11 @@ class FastDLLMV2SpeculativeGeneration:
             x_t = torch.cat([x_t, torch.full((x_t.shape[0], fill), self.mask_id,
                                              device=self.device, dtype=torch.long)], dim=1)
             st["x_t"] = x_t
+            facts = self._loop_facts(x_t, plen, called)
             while True:
-                if self._stop_reached(x_t, plen):
+                if facts["stop"]:
                     break
-                mask_idx = x_t[:, -bl:] == self.mask_id
-                if int(mask_idx.sum()) == 0:
+                if facts["block_masks"] == 0:
                     out = self.model_executor.forward(x_t[:, -bl:], past_key_values=st["cache"],
                                                       use_cache=True, update_past_key_values=True)
                     st["cache"] = out.past_key_values
@@ -246,17 +287,11 @@ class FastDLLMV2SpeculativeGeneration:
                 for sb in range(n_small):
                     s0, s1 = sb * sbs, sb * sbs + sbs
                     while True:
+                        if facts["small"][sb] == 0 or facts["stop"]:
+                            break
                         mask_idx = x_t[:, -bl:] == self.mask_id
                         small_mask = mask_idx[:, s0:s1]
-                        if int(small_mask.sum()) == 0:
-                            break
-                        if self._stop_reached(x_t, plen):
-                            break
-                        hit = -1
-                        if called:
-                            cur = x_t[0, -bl:]
-                            eq = torch.stack([s for s, _ in called]).eq(cur).all(dim=1).tolist()
-                            hit = eq.index(True) if True in eq else -1
+                        hit = facts["hit"] if called else -1
                         if hit >= 0:
                             _, hit_logits = called.pop(hit)
                             x_1, conf, _ = self._sample_rows(hit_logits[:, s0:s1, :])
@@ -285,7 +320,8 @@ class FastDLLMV2SpeculativeGeneration:
                                 draft_blocks = self.get_draft_blocks(
                                     x_t[0, -bl:], main_logits[0], mask_idx[0],
                                     start_pos=x_t.shape[1] - bl, end_pos=x_t.shape[1],
-                                    small_block_start=s0, small_block_end=s1, stats=stats)
+                                    small_block_start=s0, small_block_end=s1, stats=stats,
+                                    n_masked=facts["small"][sb])
                                 st["drafts_computed"] += len(draft_blocks)
                             kind = "verify"
                         conf = torch.where(small_mask, conf, -torch.inf)
@@ -295,7 +331,8 @@ class FastDLLMV2SpeculativeGeneration:
                         unmask = unmask & small_mask
                         region = x_t[:, x_t.shape[1] - bl + s0: x_t.shape[1] - bl + s1]
                         region.copy_(torch.where(unmask, x_1, region))
-                        n = int(unmask.sum())
+                        facts = self._loop_facts(x_t, plen, called, unmask)
+                        n = facts["n"]
                         self.last_commits.append(n)
                         # the decision itself rides along (device tensors, no sync):
                         # sampled tokens, maskable positions and the committed ones

@@ -63,23 +63,26 @@ def get_transfer_index(logits: torch.Tensor, temperature: float, mask_index: tor
 
 
 def greedy_transfer_index(stats, mask_index: torch.Tensor, x: torch.Tensor,
-                          num_transfer_tokens: torch.Tensor, threshold: Optional[float] = None):
+                          num_transfer_tokens: torch.Tensor, threshold: Optional[float] = None,
+                          ks=None):
     """get_transfer_index at temperature 0 from sf_logit_stats of the block's rows:
     x0 = the argmax token, its probability = the bf16 softmax maximum."""
     x0 = stats.top_idx[:, 0].long().unsqueeze(0)
     x0_p = greedy.max_prob_bf16(stats).unsqueeze(0)
-    return transfer_from(x0, x0_p, mask_index, x, num_transfer_tokens, threshold)
+    return transfer_from(x0, x0_p, mask_index, x, num_transfer_tokens, threshold, ks)
 
 
-def transfer_from(x0, x0_p, mask_index, x, num_transfer_tokens, threshold=None):
+def transfer_from(x0, x0_p, mask_index, x, num_transfer_tokens, threshold=None, ks=None):
     """The selection part of get_transfer_index, given the argmax tokens x0 and
-    their probabilities x0_p."""
+    their probabilities x0_p.  ``ks``: the per-row counts (masked positions with a
+    threshold, else ``num_transfer_tokens``) when the caller holds them on the host."""
     x0 = torch.where(mask_index, x0, x)
     confidence = torch.where(mask_index, x0_p, float("-inf"))
     transfer_index = torch.zeros_like(x0, dtype=torch.bool)
-    if threshold is not None:
-        num_transfer_tokens = mask_index.sum(dim=1, keepdim=True)
-    ks = num_transfer_tokens.reshape(-1).tolist()
+    if ks is None:
+        if threshold is not None:
+            num_transfer_tokens = mask_index.sum(dim=1, keepdim=True)
+        ks = num_transfer_tokens.reshape(-1).tolist()
     for j in range(confidence.shape[0]):
         k = int(ks[j])
         _, select_index = torch.topk(confidence[j], k=k)
@@ -127,16 +130,19 @@ class NLDDiffusionGeneration:
     # -- drafts -----------------------------------------------------------------------
     @torch.no_grad()
     def get_draft_blocks(self, x_block: torch.Tensor, logits_block: torch.Tensor,
-                         mask_index: torch.Tensor, stats=None) -> List[Dict]:
+                         mask_index: torch.Tensor, stats=None,
+                         num_mask_positions: Optional[int] = None) -> List[Dict]:
         """One draft block per graph node over the whole block (:105-151): the
         pos_rank-th most confident masked position gets its vocab_rank-th most
         likely token.  Indices stay on the device (no host sync per node).
         ``stats``: sf_logit_stats of the block's rows (their 1/Z and top tokens
-        replace the fp32 softmax and the vocabulary topk)."""
+        replace the fp32 softmax and the vocabulary topk).  ``num_mask_positions``:
+        the masked count when the caller holds it on the host (no device read)."""
         nodes = self._graph_nodes()
         if not nodes:
             return []
-        num_mask_positions = int(mask_index.sum().item())
+        if num_mask_positions is None:
+            num_mask_positions = int(mask_index.sum().item())
         if num_mask_positions == 0:
             return []
         if stats is not None:
@@ -178,12 +184,46 @@ class NLDDiffusionGeneration:
         return torch.multinomial(torch.softmax(last_logit / self.temperature, dim=-1), 1)
 
     # -- the decode loop ----------------------------------------------------------------
+    def _loop_facts(self, x_accum: torch.Tensor, block_slice: slice, called,
+                    transfer=None) -> Dict:
+        """What the loop's control flow reads from the token state, in one
+        device-to-host copy: the block's masked count (per row and in total), the
+        first cached draft state equal to the block (the draft-logit cache hit), and
+        after a step its committed count and whether an EOS with no mask before it
+        ends the block (:226-296).  The reference reads each with its own sync."""
+        blk = x_accum[:, block_slice]
+        masked = blk == self.mask_id
+        parts = [masked.sum(dim=1)]
+        if called:
+            eq = torch.stack([st for st, _ in called]).eq(blk[0]).all(dim=1)
+            parts.append(torch.where(eq.any(), eq.int().argmax(), -1).reshape(1))
+        if transfer is not None:
+            parts.append(transfer.sum().reshape(1))
+            if self.stop_token is not None:
+                eos = blk == self.stop_token
+                before = masked & ~eos.cumsum(dim=1).bool()
+                parts.append((eos.any() & (eos.any(dim=1) & ~before.any(dim=1)).any()).reshape(1))
+        v = torch.cat([t.to(torch.long) for t in parts]).tolist()
+        B = blk.shape[0]
+        out = {"masked_rows": v[:B], "block_masks": sum(v[:B])}
+        k = B
+        out["hit"] = v[k] if called else -1
+        k += 1 if called else 0
+        out["n"] = v[k] if transfer is not None else None
+        out["eos_break"] = bool(v[k + 1]) if (transfer is not None and
+                                              self.stop_token is not None) else False
+        return out
+
     @torch.no_grad()
     def decode_steps(self, prompt_ids: torch.Tensor, defer_forward: bool = False):
         """The decode loop of generate_with_draft_speculation (:153-316) as a
         generator: one event per iteration — {"kind": "prefill" | "verify" |
         "hit" | "commit", "committed": tokens unmasked by it}.  State on
         ``self._state``.
+
+        The control flow is the reference's; its host reads (masked counts, cache
+        hit, committed count, the EOS stop) come from one ``_loop_facts`` copy per
+        iteration, taken after the iteration's decisions.
 
         defer_forward: instead of calling ``_batched_block_forward`` the loop yields
         {"kind": "forward", "batched": [B1, N] tokens, "cache": prefix cache,
@@ -232,16 +272,13 @@ class NLDDiffusionGeneration:
             num_transfer_tokens = get_num_transfer_tokens(mask_block_idx0, steps_per_block)
             draft_blocks: List[Dict] = []
             called: List[Tuple[torch.Tensor, torch.Tensor]] = []
+            facts = self._loop_facts(x_accum, block_slice, called)
 
             for i in range(steps_per_block):
-                mask_block_idx = x_accum[:, block_slice] == mask_id
-                if int(mask_block_idx.sum()) == 0:
+                if facts["block_masks"] == 0:
                     break
-                hit = -1
-                if called:
-                    cur = x_accum[0, block_slice]
-                    eq = torch.stack([s for s, _ in called]).eq(cur).all(dim=1).tolist()
-                    hit = eq.index(True) if True in eq else -1
+                mask_block_idx = x_accum[:, block_slice] == mask_id
+                hit = facts["hit"] if called else -1
                 stats = None
                 if hit >= 0:
                     _, logits_block = called.pop(hit)
@@ -269,15 +306,19 @@ class NLDDiffusionGeneration:
                     if self._graph_nodes():
                         draft_blocks = self.get_draft_blocks(x_accum[0, block_slice],
                                                              logits_block[0], mask_block_idx[0],
-                                                             stats=stats)
+                                                             stats=stats,
+                                                             num_mask_positions=facts["masked_rows"][0])
                         st["drafts_computed"] += len(draft_blocks)
                     kind = "verify"
                 if stats is None and B == 1 and greedy.usable(logits_block, self.temperature):
                     stats = greedy.stats(logits_block[0])
+                # with a threshold every masked position is a candidate: the counts
+                # are the rows' masked counts, already on the host
+                ks = facts["masked_rows"] if self.threshold is not None else None
                 if stats is not None:
                     x0, transfer = greedy_transfer_index(
                         stats, mask_block_idx, x_accum[:, block_slice],
-                        num_transfer_tokens[:, i], threshold=self.threshold)
+                        num_transfer_tokens[:, i], threshold=self.threshold, ks=ks)
                 else:
                     x0, transfer = get_transfer_index(
                         logits_block, self.temperature, mask_block_idx, x_accum[:, block_slice],
@@ -285,17 +326,12 @@ class NLDDiffusionGeneration:
                 cur = x_accum[:, block_slice].clone()
                 cur = torch.where(transfer, x0, cur)
                 x_accum[:, block_slice] = cur
-                n = int(transfer.sum())
+                facts = self._loop_facts(x_accum, block_slice, called, transfer)
+                n = facts["n"]
                 self.last_commits.append(n)
                 yield {"kind": kind, "committed": n}
-                if eos_id is not None:
-                    block_tokens = x_accum[:, block_slice]
-                    eos_mask = block_tokens == eos_id
-                    if bool(eos_mask.any()):
-                        after_eos = eos_mask.cumsum(dim=1).bool()
-                        mask_before = (block_tokens == mask_id) & ~after_eos
-                        if bool((eos_mask.any(dim=1) & ~mask_before.any(dim=1)).any()):
-                            break
+                if facts["eos_break"]:
+                    break
 
             if self.causal_context:
                 executor.set_diffusion_lm(False)

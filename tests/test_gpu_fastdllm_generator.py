@@ -143,3 +143,25 @@ def test_decode_decisions_match_reference_sampler(scale):
           f"{mism} mismatches", flush=True)
     assert steps >= 10
     assert mism == 0
+
+
+def test_warm_graphs_then_decode_replays_only():
+    """warm_graphs captures the verify step for every branch count the draft graph
+    can produce (the main block alone included); the decode loop afterwards captures
+    nothing new and commits the same tokens as a loop that captured on the way."""
+    prompt = torch.randint(0, SHAPE.vocab - 2, (1, 40), generator=torch.Generator().manual_seed(8))
+    outs = []
+    for warm in (False, True):
+        gen = _generator(_scaled_model(22, 12.0))
+        loop = gen.decode_steps(prompt.cuda())
+        assert next(loop)["kind"] == "prefill"
+        n0 = 0
+        if warm:
+            assert gen.warm_graphs() == gen.draft_limit() + 1 >= 2
+            n0 = len(gen._engine._graphs)
+        for _ in loop:
+            pass
+        if warm:
+            assert len(gen._engine._graphs) == n0, "the decode loop captured a new graph"
+        outs.append(gen._state["x_t"].clone())
+    assert torch.equal(outs[0], outs[1])
