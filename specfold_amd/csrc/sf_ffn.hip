@@ -128,93 +128,99 @@ __global__ __launch_bounds__(256) void residual_post_norm_kernel(
   }
 }
 
-// The o_proj residual from the all-rows GEMM's KS fp32 partial slots, one wave
-// (one workgroup) per flat row r: y = bf16(sum_s part[s][r]) in slot order, hp[r]
-// = bf16(x[r] + y) (fastdllm_v2_folded.py:207-209), and with zn given, for a
+// The o_proj residual from the all-rows GEMM's KS fp32 partial slots, one
+// 256-thread workgroup per flat row r: y = bf16(sum_s part[s][r]) in slot order,
+// hp[r] = bf16(x[r] + y) (fastdllm_v2_folded.py:207-209), and with zn given, for a
 // recomputed row (slot[r] >= 0), zn[slot[r]] = bf16(w * bf16(hp[r] * rstd))
-// (:211-212).  The row goes in groups of 4 vectors of 8 per lane, two slots'
-// loads in flight at a time; hp stays in registers for the norm.
-template <int VPL>
-__global__ __launch_bounds__(64) void part_residual_norm_kernel(
+// (:211-212).  Thread t takes vectors of 8 t, t + 256, ... (VPT of them); every
+// load of the row (x, the norm weights, up to 4 slots of partials) is in flight
+// at once, so a row costs one memory round trip per 4 slots.  hp stays in
+// registers for the norm; the sum of squares is reduced per wave, then over the
+// 4 waves in wave order.
+constexpr int kPrnThreads = 256;
+template <int VPT>
+__global__ __launch_bounds__(kPrnThreads) void part_residual_norm_kernel(
     const float* __restrict__ part, int ks, size_t stride, const uint16_t* __restrict__ x,
     const int32_t* __restrict__ slot, int D, const uint16_t* __restrict__ w, float eps,
     uint16_t* __restrict__ hp, uint16_t* __restrict__ zn) {
-  static_assert(VPL % 4 == 0, "groups of 4 vectors");
+  __shared__ float s_ss[kPrnThreads / 64];
   const int r = blockIdx.x;
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x;
   const int nvec = D >> 3;
+  const int sl = zn ? slot[r] : -1;  // workgroup-uniform
   const sf_u32x4* xr = reinterpret_cast<const sf_u32x4*>(x + (size_t)r * D);
   const sf_f32x4* pr = reinterpret_cast<const sf_f32x4*>(part + (size_t)r * D);
   const size_t st4 = stride / 4;  // slot stride in float4
-  sf_u32x4* hrow = reinterpret_cast<sf_u32x4*>(hp + (size_t)r * D);
-  sf_u32x4 hv[VPL];
-  float ss = 0.f;
+  int v[VPT];
 #pragma unroll
-  for (int g = 0; g < VPL; g += 4) {
-    int v[4];
+  for (int i = 0; i < VPT; ++i) v[i] = min(tid + i * kPrnThreads, nvec - 1);
+  sf_u32x4 xv[VPT], wv[VPT];
+  sf_f32x4 y[VPT][2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = 2 * min(lane + (g + i) * 64, nvec - 1);
-    sf_u32x4 xv[4];
-    sf_f32x4 y[4][2];
+  for (int i = 0; i < VPT; ++i) {
+    xv[i] = xr[v[i]];
+    wv[i] = zn ? reinterpret_cast<const sf_u32x4*>(w)[v[i]] : sf_u32x4{0u, 0u, 0u, 0u};
+    y[i][0] = pr[2 * v[i]];
+    y[i][1] = pr[2 * v[i] + 1];
+  }
+  for (int s0 = 1; s0 < ks; s0 += 4) {
+    sf_f32x4 a[4][VPT][2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      xv[i] = xr[v[i] >> 1];
-      y[i][0] = pr[v[i]];
-      y[i][1] = pr[v[i] + 1];
-    }
-    for (int s = 1; s < ks; s += 2) {
-      const size_t oa = (size_t)s * st4, ob = (size_t)min(s + 1, ks - 1) * st4;
-      sf_f32x4 a[4][2], b[4][2];
+    for (int j = 0; j < 4; ++j) {
+      const size_t o = (size_t)min(s0 + j, ks - 1) * st4;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        a[i][0] = pr[oa + v[i]];
-        a[i][1] = pr[oa + v[i] + 1];
-        b[i][0] = pr[ob + v[i]];
-        b[i][1] = pr[ob + v[i] + 1];
+      for (int i = 0; i < VPT; ++i) {
+        a[j][i][0] = pr[o + 2 * v[i]];
+        a[j][i][1] = pr[o + 2 * v[i] + 1];
       }
+    }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        y[i][0] += a[i][0];
-        y[i][1] += a[i][1];
-        if (s + 1 < ks) {
-          y[i][0] += b[i][0];
-          y[i][1] += b[i][1];
+    for (int j = 0; j < 4; ++j)
+      if (s0 + j < ks) {
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+          y[i][0] += a[j][i][0];
+          y[i][1] += a[j][i][1];
         }
       }
+  }
+  sf_u32x4* hrow = reinterpret_cast<sf_u32x4*>(hp + (size_t)r * D);
+  sf_u32x4 hv[VPT];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    float a[8];
+    sf_unpack8(xv[i], a);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float y0 = sf_rbf(y[i][j >> 1][(2 * j) & 3]);
+      const float y1 = sf_rbf(y[i][j >> 1][(2 * j + 1) & 3]);
+      hv[i][j] = sf_pack2(a[2 * j] + y0, a[2 * j + 1] + y1);
     }
+    if (tid + i * kPrnThreads < nvec) {
+      hrow[tid + i * kPrnThreads] = hv[i];
+      float h[8];
+      sf_unpack8(hv[i], h);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float a[8];
-      sf_unpack8(xv[i], a);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float y0 = sf_rbf(y[i][j >> 1][(2 * j) & 3]);
-        const float y1 = sf_rbf(y[i][j >> 1][(2 * j + 1) & 3]);
-        hv[g + i][j] = sf_pack2(a[2 * j] + y0, a[2 * j + 1] + y1);
-      }
-      if (lane + (g + i) * 64 < nvec) {
-        hrow[lane + (g + i) * 64] = hv[g + i];
-        float h[8];
-        sf_unpack8(hv[g + i], h);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) ss = fmaf(h[j], h[j], ss);
-      }
+      for (int j = 0; j < 8; ++j) ss = fmaf(h[j], h[j], ss);
     }
   }
-  if (!zn) return;
-  const int sl = slot[r];
-  if (sl < 0) return;  // wave-uniform
+  if (sl < 0) return;  // workgroup-uniform: no barrier is skipped by part of it
   ss = sf_wave_sum(ss);
-  const float inv = 1.0f / sqrtf(ss / (float)D + eps);
-  const sf_u32x4* wr = reinterpret_cast<const sf_u32x4*>(w);
+  if ((tid & 63) == 0) s_ss[tid >> 6] = ss;
+  __syncthreads();
+  float tot = s_ss[0];
+#pragma unroll
+  for (int k = 1; k < kPrnThreads / 64; ++k) tot += s_ss[k];
+  const float inv = 1.0f / sqrtf(tot / (float)D + eps);
   sf_u32x4* orow = reinterpret_cast<sf_u32x4*>(zn + (size_t)sl * D);
 #pragma unroll
-  for (int i = 0; i < VPL; ++i) {
-    const int idx = lane + i * 64;
+  for (int i = 0; i < VPT; ++i) {
+    const int idx = tid + i * kPrnThreads;
     if (idx < nvec) {
       float f[8], g[8];
       sf_unpack8(hv[i], f);
-      sf_unpack8(wr[idx], g);
+      sf_unpack8(wv[i], g);
       sf_u32x4 o;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
@@ -371,17 +377,17 @@ int o_proj_launch(const uint16_t* o_bf, const uint16_t* x, const uint16_t* wo, i
   launch_rows<1, kRowsPart>(o_bf, M, wo, K, N, kOprojMaxSplits, part, nullptr, st);
   const int ks = rows_splits<1>(M, N, K, kOprojMaxSplits);
   const size_t stride = (size_t)M * N;
-  const int vpl = (N / 8 + 63) / 64;
+  const int vpt = (N / 8 + kPrnThreads - 1) / kPrnThreads;
   const dim3 grid(M);
-  if (vpl <= 4)
-    hipLaunchKernelGGL(part_residual_norm_kernel<4>, grid, dim3(64), 0, st, part, ks, stride, x,
-                       slot, N, ln_w, eps, hp, zn);
-  else if (vpl <= 8)
-    hipLaunchKernelGGL(part_residual_norm_kernel<8>, grid, dim3(64), 0, st, part, ks, stride, x,
-                       slot, N, ln_w, eps, hp, zn);
+  if (vpt <= 1)
+    hipLaunchKernelGGL(part_residual_norm_kernel<1>, grid, dim3(kPrnThreads), 0, st, part, ks,
+                       stride, x, slot, N, ln_w, eps, hp, zn);
+  else if (vpt <= 2)
+    hipLaunchKernelGGL(part_residual_norm_kernel<2>, grid, dim3(kPrnThreads), 0, st, part, ks,
+                       stride, x, slot, N, ln_w, eps, hp, zn);
   else
-    hipLaunchKernelGGL(part_residual_norm_kernel<16>, grid, dim3(64), 0, st, part, ks, stride, x,
-                       slot, N, ln_w, eps, hp, zn);
+    hipLaunchKernelGGL(part_residual_norm_kernel<4>, grid, dim3(kPrnThreads), 0, st, part, ks,
+                       stride, x, slot, N, ln_w, eps, hp, zn);
   return sf_launch_status();
 }
 }  // namespace
