@@ -325,10 +325,11 @@ class FastDLLMV2SpeculativeGeneration:
                                 st["drafts_computed"] += len(draft_blocks)
                             kind = "verify"
                         conf = torch.where(small_mask, conf, -torch.inf)
-                        unmask = conf > self.threshold
-                        best = conf.argmax(dim=-1)
-                        unmask[torch.arange(x_1.shape[0], device=self.device), best] = True
-                        unmask = unmask & small_mask
+                        # the reference's unmask[arange, argmax] = True, as a compare with
+                        # the argmax column (an index_put_ of a host scalar syncs)
+                        best = conf.argmax(dim=-1, keepdim=True)
+                        cols = torch.arange(conf.shape[-1], device=self.device)
+                        unmask = ((conf > self.threshold) | (cols == best)) & small_mask
                         region = x_t[:, x_t.shape[1] - bl + s0: x_t.shape[1] - bl + s1]
                         region.copy_(torch.where(unmask, x_1, region))
                         facts = self._loop_facts(x_t, plen, called, unmask)

@@ -90,7 +90,9 @@ def transfer_from(x0, x0_p, mask_index, x, num_transfer_tokens, threshold=None, 
         if threshold is not None and k > 1:
             # the reference's per-position loop: drop select_index[i >= 1] if conf < thr
             keep[1:] = ~(confidence[j, select_index[1:]] < threshold)
-        transfer_index[j, select_index[keep]] = True
+        # transfer_index[j, select_index[keep]] = True without a host sync (the
+        # topk indices are distinct and the row starts False)
+        transfer_index[j].scatter_(0, select_index, keep)
     return x0, transfer_index
 
 

@@ -41,11 +41,28 @@ def llama4_q_scale(config, P: int, N: int, device=None) -> Optional[torch.Tensor
     omax = rp.get("original_max_position_embeddings")
     if beta is None or omax is None:
         return None
+    if device is None:
+        return _q_scale_host(float(beta), omax, P, N)
+    # a device copy per (prefix length, block): the verify steps of one block reuse
+    # it instead of copying from pageable host memory (a synchronizing copy) each time
+    key = (float(beta), omax, P, N, str(torch.device(device)))
+    if key not in _Q_SCALE_DEV:
+        scale = _q_scale_host(float(beta), omax, P, N)
+        if len(_Q_SCALE_DEV) >= 64:
+            _Q_SCALE_DEV.pop(next(iter(_Q_SCALE_DEV)))
+        _Q_SCALE_DEV[key] = None if scale is None else scale.to(device)
+    return _Q_SCALE_DEV[key]
+
+
+_Q_SCALE_DEV: dict = {}
+
+
+def _q_scale_host(beta: float, omax, P: int, N: int) -> Optional[torch.Tensor]:
     pos = torch.arange(P, P + N, dtype=torch.float32)
     scale = 1.0 + beta * torch.log(1.0 + torch.floor(pos / omax))
     if bool((scale == 1.0).all()):
         return None
-    return scale.to(device) if device is not None else scale
+    return scale
 
 
 class NLDModelExecutor:
