@@ -60,9 +60,10 @@ def parse_args(argv=None):
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also time a plain 256 MiB device copy (counter calibration)")
     ap.add_argument("--pmc-pass", action="store_true",
-                    help="for rocprofv3 --pmc runs: after the decode steps and one verify step, "
-                         "a 0.5 s pause, the copy calibration, then every entry point launched "
-                         "once per layer in PMC_ORDER (no JSON line)")
+                    help="for rocprofv3 --pmc runs: the model, a prefix cache of random K/V "
+                         "(no prefill, no decode loop, no graphs), one eager verify step, a 2 s "
+                         "pause, the copy calibration, then every entry point launched once per "
+                         "layer in PMC_ORDER (no JSON line)")
     ap.add_argument("--traffic-table", nargs="+", metavar="CSV",
                     help="on the host: build profiles/traffic_<workload>.json from the "
                          "counter_collection.csv files of --pmc-pass runs (FETCH_SIZE, "
@@ -171,7 +172,7 @@ PMC_KERNELS = {
     "gate_up": ("sfg::gemm_sk_kernel<2, 2,", "silu_fixup_kernel"),
     "down": ("sfg::gemm_sk_kernel<1, 1,", "down_fixup_kernel"),
     "final_norm": ("sf_gate_rows_kernel",),
-    "lm_head": ("Cijk_",),
+    "lm_head": (("Cijk_", "Custom_Cijk_"),),   # hipBLASLt's kernel names
     "gate": ("sf_gate_rows_kernel", "sf_gate_compact_kernel"),
 }
 
@@ -200,15 +201,19 @@ def traffic_table(csvs, workload: str) -> dict:
             d = by_disp.setdefault(int(r["Dispatch_Id"]), {"name": _kernel_short(r["Kernel_Name"]),
                                                            "t0": int(r["Start_Timestamp"]),
                                                            "grid": int(r["Grid_Size"])})
+            if r.get("End_Timestamp"):
+                d["DURATION_NS"] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
             d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
         seq = [by_disp[k] for k in sorted(by_disp)]
-        # the pause: the largest start-time gap in the run's second half
-        half = len(seq) // 2
-        gaps = [(seq[i + 1]["t0"] - seq[i]["t0"], i + 1) for i in range(half, len(seq) - 1)]
+        # the pause: the largest start-time gap before a torch elementwise dispatch
+        # (the calibration copy that opens the counted section)
+        gaps = [(seq[i + 1]["t0"] - seq[i]["t0"], i + 1) for i in range(len(seq) - 1)
+                if "elementwise_kernel" in seq[i + 1]["name"]]
         start = max(gaps)[1]
         for d in seq[start:]:
             for c, v in d.items():
-                if c not in ("name", "t0", "grid"):
+                if c not in ("name", "t0", "grid") and (c != "DURATION_NS" or c not in per
+                                                         or path == csvs[0]):
                     per.setdefault(c, []).append((d["name"], v, d["grid"]))
     out = {"workload": workload, "kernels": {}}
     for counter, seq in per.items():
@@ -223,7 +228,7 @@ def traffic_table(csvs, workload: str) -> dict:
             for _ in range(launches):
                 tot = 0.0
                 for pat in pats:
-                    while i < len(seq) and not seq[i][0].startswith(pat):
+                    while i < len(seq) and not seq[i][0].startswith(pat):   # str or tuple
                         i += 1   # kernels of other libraries between ours (e.g. torch copies)
                     if i >= len(seq):
                         raise ValueError(f"{counter}: ran out of dispatches at {name}/{pat}")
@@ -245,13 +250,33 @@ def traffic_table(csvs, workload: str) -> dict:
             out["kernels"][name] = {"fetch_kib_raw": round(f[name], 1),
                                     "write_kib_raw": round(wr[name], 1),
                                     "bytes_per_launch": int(b)}
+    dur = out["raw"].get("DURATION_NS")
+    if dur:
+        for name in PMC_ORDER:
+            out["kernels"].setdefault(name, {})["pmc_run_us"] = round(dur[name] / 1e3, 3)
     mb = out["raw"].get("SQ_VALU_MFMA_BUSY_CYCLES")
     ga = out["raw"].get("GRBM_GUI_ACTIVE")
-    if mb and ga:
+    if mb:
+        # MFMA busy fraction of all 256 CUs x 4 SIMDs over the launch's own duration
+        # at the 2.4 GHz peak engine clock.  GRBM_GUI_ACTIVE is not the denominator:
+        # on this part it reads the sum over the 8 XCDs plus the profiler's time around
+        # each dispatch (gui_active_per_us, 17k-42k per us against 2.4k per clock)
         simds = 256 * 4
         for name in PMC_ORDER:
             k = out["kernels"].setdefault(name, {})
-            k["mfma_busy"] = round(mb[name] / (ga[name] * simds), 4) if ga[name] else None
+            if dur and dur[name]:
+                k["mfma_busy"] = round(mb[name] / (simds * dur[name] * 2.4), 4)
+                if ga:
+                    k["gui_active_per_us"] = round(ga[name] / (dur[name] / 1e3), 1)
+    mo = out["raw"].get("SQ_INSTS_VALU_MFMA_MOPS_BF16")
+    if mo:
+        # MOPS counts 512 flops per unit: the MFMA work issued (row tiles padded to 16
+        # or to the GEMM's row block), and its rate over the launch's duration
+        for name in PMC_ORDER:
+            k = out["kernels"].setdefault(name, {})
+            k["mfma_bf16_flops"] = int(mo[name] * 512)
+            if dur and dur[name]:
+                k["mfma_tflops_issued"] = round(mo[name] * 512 / dur[name] / 1e3, 2)
     return out
 
 
@@ -445,6 +470,56 @@ def mode_b(w, gen, batched, iters, kernel_iters):
             "data": "synthetic layer inputs (branch = parent + sigma N(0,1)), every layer"}
 
 
+@torch.no_grad()
+def pmc_pass(w) -> int:
+    """The program counted by rocprofv3 --pmc runs.  Few dispatches and no graph
+    replays: the workload's model and engine, the sequence's paged cache filled
+    with N(0, 1) K/V at the workload's prefix (no prefill), one eager verify step
+    of the draft tree (so the engine's buffers hold a real step: rows, counts,
+    src), then, after a 2 s pause (the parser finds it by the gap), one plain copy
+    of known size and every entry point once per layer in PMC_ORDER on the buffers
+    of that step."""
+    from specfold_amd.synthetic import draft_tree_block, TREE_DIFFS
+    gens, _ = make_decoders(w)
+    gen = gens[0]
+    ex = gen.model_executor
+    cache = ex.new_cache()
+    g = torch.Generator(device="cuda").manual_seed(w.seed)
+    shp = (1, cache.Hkv, w.prefix, cache.hd)
+    kv = [(torch.randn(shp, generator=g, device="cuda").to(torch.bfloat16),
+           torch.randn(shp, generator=g, device="cuda").to(torch.bfloat16))
+          for _ in range(cache.num_layers)]
+    cache.load_dense(kv)
+    del kv
+    gen._pack_layer_weights()
+    eng = gen._engine
+    eng.use_graphs = False
+    tokens = draft_tree_block(w.block, w.shape.vocab, torch.Generator().manual_seed(w.seed),
+                              diffs=TREE_DIFFS[:w.branches]).to("cuda")
+    gen._batched_block_forward(tokens, cache)
+    counts = gen.last_stats.counts
+    R = round(sum(counts) / len(counts))
+    n = (256 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    shared = {}
+    per_layer = [eng.profile_launchers(li=li, shared=shared) for li in range(eng.L)]
+    torch.cuda.synchronize()
+    time.sleep(2.0)
+    torch.mul(src, 2.0, out=dst)
+    for name in PMC_ORDER:
+        if name in ONCE_PER_STEP:
+            per_layer[-1][0][name]()
+        else:
+            for pl in per_layer:
+                pl[0][name]()
+    torch.cuda.synchronize()
+    print(f"[bench] pmc pass done ({w.name}, P {cache.length}, R {R})", file=sys.stderr,
+          flush=True)
+    return 0
+
+
+
 def make_decoders(w):
     """One generator per sequence of the workload (sharing one executor, so the
     weights and packed weights exist once) and each sequence's random prompt."""
@@ -505,6 +580,8 @@ def main(argv=None) -> int:
 
     torch.cuda.set_device(0)
     w = workload(args.workload)
+    if args.pmc_pass:
+        return pmc_pass(w)
     t_build = time.time()
     gens, prompts = make_decoders(w)
     torch.cuda.synchronize()
@@ -629,29 +706,6 @@ def main(argv=None) -> int:
                         "ms_per_sequence": round(ms_b / len(reqs), 4)}
         print(f"[bench] batched verify step ({len(reqs)} sequences) median {ms_b:.3f} ms",
               file=sys.stderr, flush=True)
-
-    if args.pmc_pass:
-        # the counted section: after a pause (the parser finds it by the gap), one
-        # plain copy of known size, then every entry point once per layer on the
-        # buffers of the verify step just run
-        eng = gen._engine
-        n = (256 << 20) // 4
-        src = torch.ones(n, dtype=torch.float32, device="cuda")
-        dst = torch.empty_like(src)
-        shared = {}
-        per_layer = [eng.profile_launchers(li=li, shared=shared) for li in range(eng.L)]
-        torch.cuda.synchronize()
-        time.sleep(0.5)
-        torch.mul(src, 2.0, out=dst)
-        for name in PMC_ORDER:
-            if name in ONCE_PER_STEP:
-                per_layer[-1][0][name]()
-            else:
-                for pl in per_layer:
-                    pl[0][name]()
-        torch.cuda.synchronize()
-        print(f"[bench] pmc pass done ({w.name}, R {R})", file=sys.stderr, flush=True)
-        return 0
 
     # per-kernel timings on the buffers of the last verify step, cycling through the
     # layers (weights and cache slices) as the step does

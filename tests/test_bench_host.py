@@ -73,6 +73,7 @@ def _pmc_csv(path, w, fetch_kib, write_kib, cal_kib):
     for name in bench.PMC_ORDER:
         for li in range(1 if name in bench.ONCE_PER_STEP else L):
             for j, pat in enumerate(bench.PMC_KERNELS[name]):
+                pat = pat if isinstance(pat, str) else pat[-1]   # the last alternative
                 emit(pat + "x>(int)", fetch_kib[name] + li + j, write_kib[name])
             if name == "attn" and li == 0:
                 emit("elementwise_kernel_copy", 1e6, 1e6)
