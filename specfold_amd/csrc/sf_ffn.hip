@@ -332,6 +332,18 @@ __global__ __launch_bounds__(256) void pack_weight_kernel(const uint16_t* __rest
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// The gate/up split.  With at least kWholeMinTiles 128-column tiles (and no more
+// than one per CU) every workgroup streams one whole tile over all of K: no tile
+// is shared, so there are no partial slots and no fix-up launch, at the price of
+// the CUs beyond T idling; fewer tiles are dealt out stream-K over 256 workgroups.
+#ifndef SF_WHOLE_MIN_TILES
+#define SF_WHOLE_MIN_TILES 128
+#endif
+constexpr int kWholeMinTiles = SF_WHOLE_MIN_TILES;
+Plan gate_up_plan(int T, int S) {
+  return T >= kWholeMinTiles && T <= 256 ? make_plan_whole(T, S) : make_plan(T, S);
+}
+
 }  // namespace
 
 extern "C" size_t sf_gemm_workspace_bytes(int mcap, int N, int K) {
@@ -467,15 +479,16 @@ extern "C" int sf_ffn_gate_up(const uint16_t* zn, const int32_t* count, int buck
   if (bucket < 1 || bucket > 1024 || D % kKC || I % 128) return SF_ERR_SHAPE;
   if (workspace_bytes < sf_ffn_gate_up_workspace_bytes(bucket, D, I)) return SF_ERR_WORKSPACE;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const Plan p = make_plan(I / 128, D / kKC);
+  const Plan p = gate_up_plan(I / 128, D / kKC);
   float* part = reinterpret_cast<float*>(workspace);
   Epi ep{};
   ep.out = act;
   ep.ldo = I;
   // whole tiles get SiLU*mul straight from registers, shared tiles in the fix-up
   launch_sk<2, kSilu>(p, zn, nullptr, D, count, 0, bucket, wg, wu, D, I, part, ep, st);
-  hipLaunchKernelGGL(silu_fixup_kernel, dim3(p.T, (bucket + kFixRows - 1) / kFixRows), dim3(256), 0,
-                     st, part, p, bucket, count, I, act);
+  if (p.U < p.S)
+    hipLaunchKernelGGL(silu_fixup_kernel, dim3(p.T, (bucket + kFixRows - 1) / kFixRows), dim3(256),
+                       0, st, part, p, bucket, count, I, act);
   return sf_launch_status();
 }
 
