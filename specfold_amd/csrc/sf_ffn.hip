@@ -332,16 +332,15 @@ __global__ __launch_bounds__(256) void pack_weight_kernel(const uint16_t* __rest
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// The gate/up split.  With at least kWholeMinTiles 128-column tiles (and no more
-// than one per CU) every workgroup streams one whole tile over all of K: no tile
-// is shared, so there are no partial slots and no fix-up launch, at the price of
-// the CUs beyond T idling; fewer tiles are dealt out stream-K over 256 workgroups.
-#ifndef SF_WHOLE_MIN_TILES
-#define SF_WHOLE_MIN_TILES 128
-#endif
-constexpr int kWholeMinTiles = SF_WHOLE_MIN_TILES;
-Plan gate_up_plan(int T, int S) {
-  return T >= kWholeMinTiles && T <= 256 ? make_plan_whole(T, S) : make_plan(T, S);
+// The gate/up split.  With at least two 16-column units per workgroup of the
+// grid (and at most eight), the column-spread plan: every workgroup streams its
+// 4-5 units (cfg3: 1184 units over 256 workgroups) over all of K, so no tile is
+// shared -- no partial slots, no fix-up launch -- and every CU streams a similar
+// share of the weights.  Narrower outputs are dealt out stream-K.
+Plan gate_up_plan(int I, int S) {
+  const int nu = I / 16;
+  if (nu >= 2 * SFG_GRID && nu <= 8 * SFG_GRID) return make_plan_spread(nu, S, SFG_GRID);
+  return make_plan(I / 128, S);
 }
 
 }  // namespace
@@ -479,7 +478,7 @@ extern "C" int sf_ffn_gate_up(const uint16_t* zn, const int32_t* count, int buck
   if (bucket < 1 || bucket > 1024 || D % kKC || I % 128) return SF_ERR_SHAPE;
   if (workspace_bytes < sf_ffn_gate_up_workspace_bytes(bucket, D, I)) return SF_ERR_WORKSPACE;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const Plan p = gate_up_plan(I / 128, D / kKC);
+  const Plan p = gate_up_plan(I, D / kKC);
   float* part = reinterpret_cast<float*>(workspace);
   Epi ep{};
   ep.out = act;

@@ -84,10 +84,14 @@ SF_DEV void lds_fragments(sf_u32x4 (&f)[NMT + WN], sf_lds_off a_addr, sf_lds_off
 // more.  Copies past the last stage re-read it (clamped) and rows past mrows
 // re-read the last row, which keeps every count exact; the loop drains them at
 // its end.
+// A wave with no columns of its own (wact false: a column-spread workgroup with
+// fewer units than waves) issues the same number of copies, but re-reads its first
+// A copy (L2-resident) into its own weight slots instead of weight bytes, and its
+// results are dropped.
 template <int WN, int NMT, int MB>
 SF_DEV void mainloop(const uint16_t* __restrict__ A, int lda, int mrows, const int* rows,
                      const uint16_t* const (&wsrc)[WN], int s0, int s1, const Ring<MB, WN>& rg,
-                     sf_f32x4 (&acc)[MB / 16][WN]) {
+                     sf_f32x4 (&acc)[MB / 16][WN], bool wact = true) {
   using St = Stage<MB, WN>;
   constexpr int R = St::kRing;
   static_assert(R >= 3, "the ring needs three stages");
@@ -118,7 +122,8 @@ SF_DEV void mainloop(const uint16_t* __restrict__ A, int lda, int mrows, const i
     for (int t = 0; t < WN; ++t)
 #pragma unroll
       for (int c = 0; c < 2; ++c)
-        sf_lds_dma16(wsrc[t] + (size_t)weight_chunk(sc, c) * kKsStride,
+        sf_lds_dma16(wact ? wsrc[t] + (size_t)weight_chunk(sc, c) * kKsStride
+                          : asrc[0] + sc * kKC,
                      slot + wdst + (t * 2 + c) * 64);
   };
 #pragma unroll
@@ -276,8 +281,14 @@ void gemm_sk_kernel(const uint16_t* __restrict__ A, const int32_t* __restrict__ 
     const int cg = wv;  // column group
     int col[WN];
     const uint16_t* wrow[WN];  // this lane's weight stream of each column tile
+    // column-spread plan: this workgroup's units [ub, ue); a wave past them keeps the
+    // last one's column (in range) but streams no weights (mainloop's wact) and its
+    // results are not written: only ue - ub column groups are
+    const int ub = plan.NU ? spread_begin(t, plan) : 0;
+    const int ue = plan.NU ? spread_begin(t + 1, plan) : 0;
     if (MODE == kSilu) {
-      const int c = gemm_col<WN, true>(t, cg, 0, lane);
+      const int c = plan.NU ? 16 * sf_imin(ub + cg, ue - 1) + (lane & 15)
+                            : gemm_col<WN, true>(t, cg, 0, lane);
 #pragma unroll
       for (int tt = 0; tt < WN; ++tt) col[tt] = c;
       wrow[0] = weight_lane_ptr(W0, c >> 4, K, lane);
@@ -296,12 +307,13 @@ void gemm_sk_kernel(const uint16_t* __restrict__ A, const int32_t* __restrict__ 
       for (int tt = 0; tt < WN; ++tt) acc[mt][tt] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
     // m tiles rounded up to 2, 4 or 8 (fewer instantiations; the extra tiles
     // re-read the last row and their results are dropped)
+    const bool wact = !plan.NU || cg < ue - ub;
     if (nmt <= 2)
-      mainloop<WN, 2, MB>(A, lda, mrows, rows_s, wrow, sa, sb, rg, acc);
+      mainloop<WN, 2, MB>(A, lda, mrows, rows_s, wrow, sa, sb, rg, acc, wact);
     else if (nmt <= 4 || kMT < 8)
-      mainloop<WN, (kMT < 4 ? kMT : 4), MB>(A, lda, mrows, rows_s, wrow, sa, sb, rg, acc);
+      mainloop<WN, (kMT < 4 ? kMT : 4), MB>(A, lda, mrows, rows_s, wrow, sa, sb, rg, acc, wact);
     else
-      mainloop<WN, (kMT < 8 ? kMT : 8), MB>(A, lda, mrows, rows_s, wrow, sa, sb, rg, acc);
+      mainloop<WN, (kMT < 8 ? kMT : 8), MB>(A, lda, mrows, rows_s, wrow, sa, sb, rg, acc, wact);
     // the tile to LDS (the ring's memory), then every thread takes 4 consecutive
     // columns of a row: epilogue, vector stores
     constexpr bool kS = MODE == kSilu;
@@ -316,7 +328,8 @@ void gemm_sk_kernel(const uint16_t* __restrict__ A, const int32_t* __restrict__ 
     // partial slot rows: N columns (kSilu: 2N, the gate sums then the up sums)
     constexpr int kPW = kS ? 2 : 1;
     float* pw = part + ((size_t)(g - first) * stride + (size_t)m0 * N) * kPW;
-    const int c0 = kS ? t * 128 : t * kTW;   // first output column of the tile
+    const int c0 = kS ? (plan.NU ? 16 * ub : t * 128) : t * kTW;   // first output column
+    const int cw = kS && plan.NU ? 16 * (ue - ub) : 128;   // kSilu: columns of the tile
     for (int e = tid; e < mrows * (kTW / 4); e += kThreads) {
       const int m = e / (kTW / 4);
       const int c = (e - m * (kTW / 4)) * 4;          // column in the LDS tile
@@ -328,7 +341,7 @@ void gemm_sk_kernel(const uint16_t* __restrict__ A, const int32_t* __restrict__ 
                              : (size_t)c0 + c;
         *reinterpret_cast<sf_f32x4*>(pw + (size_t)m * N * kPW + pc) = y;
       } else if (kS) {
-        if (c < 128) {
+        if (c < cw) {
           const sf_f32x4 up = *reinterpret_cast<const sf_f32x4*>(tl + m * kTW + 128 + c);
           float r[4];
 #pragma unroll

@@ -76,9 +76,10 @@ SF_IDX int gemm_col(int t, int wv, int tt, int lane) {
 #endif
 
 struct Plan {
-  int T;  // column tiles
-  int S;  // K stages
-  int U;  // units per workgroup
+  int T;       // column tiles
+  int S;       // K stages
+  int U;       // units per workgroup
+  int NU = 0;  // > 0: column-spread plan (below) over NU column units of 16
 };
 
 // Balanced plan over SFG_GRID workgroups.
@@ -89,6 +90,13 @@ inline Plan make_plan(int T, int S) {
 }
 // One workgroup per whole tile: every tile has a single contributor.
 inline Plan make_plan_whole(int T, int S) { return Plan{T, S, S}; }
+// Column-spread plan (gate/up: kSilu only): the NU 16-column units of the output
+// are dealt out over T workgroups, workgroup t taking units [spread_begin(t),
+// spread_begin(t + 1)) -- between 1 and 8, one per wave -- over all S stages of K.
+// Every tile (a workgroup's columns) is whole, so there are no partial slots, and
+// every CU streams NU/T units instead of the 8 of a 128-column tile.
+inline Plan make_plan_spread(int NU, int S, int T) { return Plan{T, S, S, NU}; }
+SF_IDX int spread_begin(int t, const Plan& p) { return (int)((long long)t * p.NU / p.T); }
 inline int plan_grid(const Plan& p) {
   return (int)(((long long)p.T * p.S + p.U - 1) / p.U);
 }

@@ -112,6 +112,31 @@ static void check_plans() {
       walk_plan(w, true);
       plans += 2;
     }
+  // column-spread plans (gate/up): over T workgroups, workgroup t's units
+  // [spread_begin(t), spread_begin(t + 1)) -- 1..8 of them, one per wave, waves past
+  // them repeating the last -- cover every 16-column unit exactly once, with whole
+  // tiles (no partial slots) and T workgroups
+  for (int T : {1, 3, 8, 64, 255, 256})
+    for (int NU = T; NU <= 8 * T; NU += (NU < 3 * T ? 1 : 7)) {
+      const sfg::Plan sp = sfg::make_plan_spread(NU, 56, T);
+      CHECK(sfg::plan_grid(sp) == T, "spread grid");
+      std::vector<int> hit(NU, 0);
+      for (int t = 0; t < T; ++t) {
+        CHECK(sfg::tile_first(t, sp) == t && sfg::tile_last(t, sp) == t, "spread tile shared");
+        const int ub = sfg::spread_begin(t, sp), ue = sfg::spread_begin(t + 1, sp);
+        CHECK(ue - ub >= 1 && ue - ub <= 8, "spread units %d", ue - ub);
+        for (int wv = 0; wv < 8; ++wv) {
+          const int unit = std::min(ub + wv, ue - 1);   // the kernel's column unit
+          CHECK(unit >= 0 && unit < NU, "spread unit %d", unit);
+          if (wv < ue - ub) {
+            CHECK(unit == ub + wv, "spread written unit");
+            ++hit[unit];
+          }
+        }
+      }
+      for (int u = 0; u < NU; ++u) CHECK(hit[u] == 1, "spread unit %d written %d times", u, hit[u]);
+      ++plans;
+    }
   // the shapes of the workloads (hidden D, q/k/v width, intermediate I, vocab V)
   struct Shape { int D, nqkv, I, V; };
   const Shape shapes[] = {{1536, 2048, 8960, 151936},  {3584, 4608, 18944, 152064},

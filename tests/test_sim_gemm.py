@@ -22,8 +22,7 @@ CSRC = ROOT / "specfold_amd" / "csrc"
 CLANG = Path("/opt/rocm/llvm/bin/clang++")
 
 
-@pytest.fixture(scope="module")
-def gemm_sim(tmp_path_factory):
+def _build(tmp_path_factory, extra=()):
     cxx = str(CLANG) if CLANG.exists() else shutil.which("clang++")
     if cxx is None:
         pytest.skip("no clang++ (the simulator needs clang's vector extensions)")
@@ -33,7 +32,7 @@ def gemm_sim(tmp_path_factory):
     for f in ("sf_ffn.hip", "sf_qkv.hip", "sf_gemm_core.h", "sf_gemm_rows.h"):
         (d / f).write_text((CSRC / f).read_text())
     flags = ["-std=c++20", "-O2", "-Wno-unknown-attributes", "-Wno-psabi", f"-I{SIM}",
-             f"-I{ROOT / 'include'}", f"-I{CSRC}"]
+             f"-I{ROOT / 'include'}", f"-I{CSRC}", *extra]
     objs = []
     for src, obj in ((d / "sf_ffn.hip", d / "ffn.o"), (d / "sf_qkv.hip", d / "qkv.o"),
                      (SIM / "gemm_sim.cpp", d / "drv.o")):
@@ -48,6 +47,20 @@ def gemm_sim(tmp_path_factory):
     return exe
 
 
+@pytest.fixture(scope="module")
+def gemm_sim(tmp_path_factory):
+    return _build(tmp_path_factory)
+
+
+@pytest.fixture(scope="module")
+def gemm_sim_grid3(tmp_path_factory):
+    """The library with a 3-workgroup grid: small outputs then take the gate/up's
+    column-spread plan (I/16 units over 3 workgroups, 2 to 8 each, uneven where
+    3 does not divide them) that the 7B-14B intermediate widths take on the
+    256-workgroup grid."""
+    return _build(tmp_path_factory, ("-DSFG_GRID=3",))
+
+
 @pytest.mark.parametrize("case", [
     (256, 384, 39, 64, 40, 1),      # D, I, count, bucket, M, seed: one row block
     (384, 512, 100, 128, 70, 2),    # two row blocks
@@ -60,6 +73,18 @@ def gemm_sim(tmp_path_factory):
 ], ids=lambda c: "D%d_I%d_count%d_bucket%d_M%d" % c[:5])
 def test_gemm_kernels_in_simulator(gemm_sim, case):
     r = subprocess.run([str(gemm_sim), *map(str, case)], capture_output=True, text=True,
+                       timeout=600)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
+
+
+@pytest.mark.parametrize("case", [
+    (256, 384, 39, 64, 40, 11),     # 24 units: 8 per workgroup
+    (128, 256, 70, 128, 70, 12),    # 16 units: 5, 5, 6; two row blocks
+    (256, 128, 5, 64, 5, 13),       # 8 units: 2, 3, 3
+], ids=lambda c: "D%d_I%d_count%d_bucket%d_M%d" % c[:5])
+def test_gemm_kernels_column_spread_plan(gemm_sim_grid3, case):
+    r = subprocess.run([str(gemm_sim_grid3), *map(str, case)], capture_output=True, text=True,
                        timeout=600)
     print(r.stdout)
     assert r.returncode == 0, r.stdout + r.stderr
