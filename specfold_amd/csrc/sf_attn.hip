@@ -5,30 +5,26 @@
 // scores = (q . k) * scaling, m = max, Z = sum exp(s - m), O = sum exp(s - m) v / Z,
 // no mask) and the Triton kernel specfold/generate/triton_kernels.py:301-361.
 //
-// Two kernels (flash-decoding split over the prefix):
-//  * prefix: a persistent grid walks the active (query tile, range of 128-key
-//    prefix chunks, kv head) items; the item count follows the device-side row
-//    count and prefix length, so no workgroup is dispatched for an empty tile.
-//    All recomputed rows x the G q-heads of one kv head are flattened to queries
-//    qi = m*G + g and tiled 64 per item (16 per wave), so each prefix K/V
-//    element is read by the few query tiles of its chunk instead of once per
-//    row.  Items of one chunk range are consecutive and go to one XCD
-//    (workgroup b runs on XCD b % 8), so the range's later reads hit that XCD's
-//    L2.  A range is one chunk while one-chunk items fill about two rounds of
-//    the grid and grows with the prefix beyond that (long contexts: fewer
-//    partials, and chunk c+1's K/V loads are in flight while chunk c is
-//    computed).  Per chunk, K is staged in LDS and V written transposed; scores
-//    are formed transposed, S^T = K Q^T, so every lane holds keys of ONE query:
-//    the softmax is per lane, rescaled across the range's chunks as in flash
-//    attention, and P^T feeds the P.V MFMA straight from registers (the 8
-//    k-slots of a lane are keys {4g..4g+3} of two 16-key tiles, and V^T is read
-//    in that same order).  P is split into bf16 hi + lo halves (two MFMAs) so
-//    P.V keeps ~16 mantissa bits, close to the reference's fp32 einsum.  Each
-//    item writes its (m, l, acc) partial.
-//  * block + merge: one 512-thread workgroup per active (recomputed row, kv
-//    head): every load (q, the branch's N block keys/values gathered through src,
-//    all range partials) is issued up front; block scores, the merged max, Z and
-//    O follow from LDS.
+// Three kernels (flash-decoding split over the prefix, then the branch blocks):
+//  * prefix (sf_attn_prefix_kernel): a persistent grid walks the active (query
+//    tile, range of 64-key prefix chunks, kv head) items; the item count follows
+//    the device-side row count and prefix length.  All recomputed rows x the G
+//    q-heads of one kv head are flattened to queries qi = m*G + g and tiled 128
+//    per item (32 per wave, against one key half of every chunk), so each prefix
+//    K/V element is read by the few query tiles of its range instead of once per
+//    row.  Items of one chunk range are consecutive and go to one XCD, so the
+//    range's later reads hit that XCD's L2.  K/V chunks go straight to an LDS ring
+//    by direct copies; scores are formed transposed, S^T = K Q^T, so every lane
+//    holds keys of ONE query and the softmax is per lane; P^T feeds the P.V MFMA
+//    from registers, V^T comes from transposing LDS reads.  P is split into bf16
+//    hi + lo parts (two MFMAs), so P.V keeps ~16 mantissa bits, close to the
+//    reference's fp32 einsum.  Each item writes its (m, l, acc) partial.
+//  * merge (sf_attn_prefix_merge_kernel): one wave per (recomputed row, q-head)
+//    combines its range partials into one prefix state {acc, m, l}.
+//  * finalize (sf_attn_finalize_kernel): one workgroup per (branch, kv head, 8
+//    positions) attends every row of the branch - its own prefix state if it was
+//    recomputed, its source row's otherwise - over the branch's N block keys
+//    (gathered through src), on MFMA, and writes O, m and Z.
 // Softmax exponentials are exp2 of scores pre-scaled by log2(e) (one v_exp_f32
 // each); partial maxima stay in that base-2 domain and the emitted m is converted
 // back, so (m, Z) describe the natural-base softmax the reference computes.
@@ -73,6 +69,7 @@ constexpr int kCUs = 256;  // MI355X compute units
 #define SFA_P_PARTS 2
 #endif
 constexpr int kPParts = SFA_P_PARTS;
+constexpr float kLazy = 8.f;   // base-2 headroom of the softmax reference (exponentials <= 256)
 constexpr int kRing = 4;                          // chunks in the LDS ring
 constexpr int kSlotBytes = 2 * kHalfBytes;        // K then V rows: 32 KB
 constexpr int kPrefixThreads = 512;
@@ -154,6 +151,10 @@ SF_DEV void prefix_item(const uint16_t* __restrict__ q_buf, const uint16_t* __re
     const int p = lane & 15;
     unit_off[i] = (is_v ? v_unit(row, p) : k_unit(row, p)) * 8;
   }
+  // the same offsets with the key row folded in, for a group of 16 keys in the prefix
+  int lane_off[kCopiesPerChunk];
+#pragma unroll
+  for (int i = 0; i < kCopiesPerChunk; ++i) lane_off[i] = (4 * i + (lane >> 4)) * kHD + unit_off[i];
   const int dst0 = (is_v ? kHalfBytes : 0) + 16 * jg * kRowBytes;
   const sf_lds_off pg_addr = sf_lds_addr(s_pg) + 4 * jg;
   auto issue = [&](int ci, uint8_t* slot) {
@@ -166,10 +167,16 @@ SF_DEV void prefix_item(const uint16_t* __restrict__ q_buf, const uint16_t* __re
       grow = (long long)pg * page_stride + (long long)(g0 & (page_size - 1)) * kHD;
     }
     const uint16_t* gsrc = src_base + grow;
+    if (g0 + 16 <= P) {  // wave-uniform: all 16 keys of the group exist
 #pragma unroll
-    for (int i = 0; i < kCopiesPerChunk; ++i) {
-      const int kr = group_key(4 * i + (lane >> 4), g0, P);
-      sf_lds_dma16(gsrc + (size_t)kr * kHD + unit_off[i], slot + dst0 + 4 * i * kRowBytes);
+      for (int i = 0; i < kCopiesPerChunk; ++i)
+        sf_lds_dma16(gsrc + lane_off[i], slot + dst0 + 4 * i * kRowBytes);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kCopiesPerChunk; ++i) {
+        const int kr = group_key(4 * i + (lane >> 4), g0, P);
+        sf_lds_dma16(gsrc + (size_t)kr * kHD + unit_off[i], slot + dst0 + 4 * i * kRowBytes);
+      }
     }
   };
 #pragma unroll
@@ -202,7 +209,13 @@ SF_DEV void prefix_item(const uint16_t* __restrict__ q_buf, const uint16_t* __re
   const int vsw = vrow & 7;
   const uint32_t vlane = (uint32_t)(v_tr_off(lane, 0) - 32 * vsw + 32 * kh * kRowBytes);
 
-  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+  // online softmax state per query: m_ref is the reference acc and l are kept
+  // against (-inf: nothing accumulated yet), m_hi the running maximum.  The
+  // reference is moved up to the maximum only when the maximum passes it by more
+  // than kLazy (base 2), so most chunks skip the rescale of acc; every exponential
+  // is then at most 2^kLazy.
+  float m_ref[2] = {-INFINITY, -INFINITY}, m_hi[2] = {-INFINITY, -INFINITY};
+  float l_run[2] = {0.f, 0.f};
   sf_f32x4 acc[2][8];
 #pragma unroll
   for (int qs = 0; qs < 2; ++qs)
@@ -243,10 +256,13 @@ SF_DEV void prefix_item(const uint16_t* __restrict__ q_buf, const uint16_t* __re
             if (kbase + 16 * t + i >= P) s[t][qs][i] = -INFINITY;
     }
 
-    // online softmax per query (base 2, scores pre-scaled by log2(e) * scaling):
-    // the max over the 4 lane groups first (lane shuffles go through the LDS
-    // pipe), then the V^T operand reads, whose latency the exponentials cover
-    float m_use[2], alpha[2];
+    // online softmax per query (base 2, scores pre-scaled by log2(e) * scaling),
+    // then the V^T operand reads, whose latency the exponentials cover.  m_hi is
+    // kept per lane (the maximum of the lane's own keys) and checked against the
+    // reference per lane; only a rescale takes the maximum over the query's four
+    // lane groups (shuffles), so most chunks need no cross-lane step
+    float m_use[2];
+    bool need = false;
 #pragma unroll
     for (int qs = 0; qs < 2; ++qs) {
       float mx = -INFINITY;
@@ -254,14 +270,28 @@ SF_DEV void prefix_item(const uint16_t* __restrict__ q_buf, const uint16_t* __re
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[t][qs][i]);
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      const float m_new = fmaxf(m_run[qs], mx * scale_log2);
-      // a key half with no key yet (only past a short prefix's end) stays empty
-      m_use[qs] = m_new == -INFINITY ? 0.f : m_new;
-      alpha[qs] = __builtin_amdgcn_exp2f(m_run[qs] - m_use[qs]);
-      m_run[qs] = m_new;
+      mx *= scale_log2;
+      m_hi[qs] = fmaxf(m_hi[qs], mx);
+      need = need || mx > m_ref[qs] + kLazy;   // m_ref -inf: any finite key
     }
+    // wave-uniform: rescale every query of the wave to its running maximum
+    const bool resc = __ballot(need) != 0;
+    float alpha[2] = {1.f, 1.f};
+    if (resc) {
+#pragma unroll
+      for (int qs = 0; qs < 2; ++qs) {
+        float mx = m_hi[qs];
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        m_hi[qs] = mx;
+        // a key half with no key yet (only past a short prefix's end) stays empty
+        const float nr = mx == -INFINITY ? 0.f : mx;
+        alpha[qs] = __builtin_amdgcn_exp2f(m_ref[qs] - nr);
+        m_ref[qs] = mx;
+      }
+    }
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) m_use[qs] = m_ref[qs] == -INFINITY ? 0.f : m_ref[qs];
     sf_u32x2 vf[16];  // [dt * 2 + t]
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
@@ -279,8 +309,10 @@ SF_DEV void prefix_item(const uint16_t* __restrict__ q_buf, const uint16_t* __re
           s[t][qs][i] = __builtin_amdgcn_exp2f(fmaf(s[t][qs][i], scale_log2, -m_use[qs]));
           lsum[qs] += s[t][qs][i];
         }
+      if (resc) {
 #pragma unroll
-      for (int dt = 0; dt < 8; ++dt) acc[qs][dt] = acc[qs][dt] * alpha[qs];
+        for (int dt = 0; dt < 8; ++dt) acc[qs][dt] = acc[qs][dt] * alpha[qs];
+      }
     }
     // the exponentials and rescales are done before the wait for the V^T reads
     // (an empty asm that takes them in keeps the compiler from sinking them past it)
@@ -294,12 +326,10 @@ SF_DEV void prefix_item(const uint16_t* __restrict__ q_buf, const uint16_t* __re
       for (int dt = 0; dt < 8; ++dt) sf_pin(acc[qs][dt]);
     }
     sf_lds_reads_done(vf);
+    // l is kept per lane (its own keys' terms; alpha is the same for the query's
+    // four lane groups) and summed over them when the range is done
 #pragma unroll
-    for (int qs = 0; qs < 2; ++qs) {
-      lsum[qs] += __shfl_xor(lsum[qs], 16, 64);
-      lsum[qs] += __shfl_xor(lsum[qs], 32, 64);
-      l_run[qs] = l_run[qs] * alpha[qs] + lsum[qs];
-    }
+    for (int qs = 0; qs < 2; ++qs) l_run[qs] = l_run[qs] * alpha[qs] + lsum[qs];
 
     // O^T += V^T P^T over the wave's 32 keys (smallest P part first)
     sf_bf16x8 pb[2][kPParts];
@@ -338,8 +368,16 @@ SF_DEV void prefix_item(const uint16_t* __restrict__ q_buf, const uint16_t* __re
   sf_wait_vm_barrier<0>();
 
   // ---- combine the two key halves of each query, write the partial -----------------
+  // the query's maximum and l over its four lane groups
+#pragma unroll
+  for (int qs = 0; qs < 2; ++qs) {
+    m_hi[qs] = fmaxf(m_hi[qs], __shfl_xor(m_hi[qs], 16, 64));
+    m_hi[qs] = fmaxf(m_hi[qs], __shfl_xor(m_hi[qs], 32, 64));
+    l_run[qs] += __shfl_xor(l_run[qs], 16, 64);
+    l_run[qs] += __shfl_xor(l_run[qs], 32, 64);
+  }
   float* xo = reinterpret_cast<float*>(ring);            // [qg][qs][dt][lane] x 4
-  float* xml = xo + 4 * 2 * 8 * 64 * 4;                   // [qg][qs][ql] x (m, l)
+  float* xml = xo + 4 * 2 * 8 * 64 * 4;   // [qg][qs][ql] x (m_ref, l, m_hi, -)
   if (kh == 1) {
 #pragma unroll
     for (int qs = 0; qs < 2; ++qs) {
@@ -347,8 +385,9 @@ SF_DEV void prefix_item(const uint16_t* __restrict__ q_buf, const uint16_t* __re
       for (int dt = 0; dt < 8; ++dt)
         *reinterpret_cast<sf_f32x4*>(xo + (((qg * 2 + qs) * 8 + dt) * 64 + lane) * 4) = acc[qs][dt];
       if (grp == 0) {
-        xml[((qg * 2 + qs) * 16 + ql) * 2] = m_run[qs];
-        xml[((qg * 2 + qs) * 16 + ql) * 2 + 1] = l_run[qs];
+        xml[((qg * 2 + qs) * 16 + ql) * 4] = m_ref[qs];
+        xml[((qg * 2 + qs) * 16 + ql) * 4 + 1] = l_run[qs];
+        xml[((qg * 2 + qs) * 16 + ql) * 4 + 2] = m_hi[qs];
       }
     }
   }
@@ -357,10 +396,13 @@ SF_DEV void prefix_item(const uint16_t* __restrict__ q_buf, const uint16_t* __re
 #pragma unroll
     for (int qs = 0; qs < 2; ++qs) {
       const int qi = qt * kQT + qg * 32 + qs * 16 + ql;
-      const float m1 = xml[((qg * 2 + qs) * 16 + ql) * 2];
-      const float l1 = xml[((qg * 2 + qs) * 16 + ql) * 2 + 1];
-      const float mm = fmaxf(m_run[qs], m1);  // finite: half 0 holds the range's first key
-      const float w0 = __builtin_amdgcn_exp2f(m_run[qs] - mm);
+      // the partial is kept against the range's maximum mm: each half's (acc, l)
+      // moves from its reference to mm (an empty half 1 has m_ref -inf: weight 0)
+      const float m1 = xml[((qg * 2 + qs) * 16 + ql) * 4];
+      const float l1 = xml[((qg * 2 + qs) * 16 + ql) * 4 + 1];
+      const float h1 = xml[((qg * 2 + qs) * 16 + ql) * 4 + 2];
+      const float mm = fmaxf(m_hi[qs], h1);  // finite: half 0 holds the range's first key
+      const float w0 = __builtin_amdgcn_exp2f(m_ref[qs] - mm);
       const float w1 = __builtin_amdgcn_exp2f(m1 - mm);
       if (qi < nq) {
         const size_t slot = attn_slot(h, r, qi, nr_cap, qmax);

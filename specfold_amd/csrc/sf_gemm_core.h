@@ -305,11 +305,13 @@ void gemm_sk_kernel(const uint16_t* __restrict__ A, const int32_t* __restrict__ 
     for (int mt = 0; mt < kMT; ++mt)
 #pragma unroll
       for (int tt = 0; tt < WN; ++tt) acc[mt][tt] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
-    // m tiles rounded up to 2, 4 or 8 (fewer instantiations; the extra tiles
+    // m tiles rounded up to 2, 3, 4 or 8 (fewer instantiations; the extra tiles
     // re-read the last row and their results are dropped)
     const bool wact = !plan.NU || cg < ue - ub;
     if (nmt <= 2)
       mainloop<WN, 2, MB>(A, lda, mrows, rows_s, wrow, sa, sb, rg, acc, wact);
+    else if (nmt == 3)
+      mainloop<WN, 3, MB>(A, lda, mrows, rows_s, wrow, sa, sb, rg, acc, wact);
     else if (nmt <= 4 || kMT < 8)
       mainloop<WN, (kMT < 4 ? kMT : 4), MB>(A, lda, mrows, rows_s, wrow, sa, sb, rg, acc, wact);
     else
