@@ -334,12 +334,13 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 // The gate/up split.  With at least two 16-column units per workgroup of the
 // grid (and at most eight), the column-spread plan: every workgroup streams its
-// 4-5 units (cfg3: 1184 units over 256 workgroups) over all of K, so no tile is
-// shared -- no partial slots, no fix-up launch -- and every CU streams a similar
+// units over all of K (cfg3: 1184 units, 5 each over 237 workgroups), so no tile
+// is shared -- no partial slots, no fix-up launch -- and every CU streams the same
 // share of the weights.  Narrower outputs are dealt out stream-K.
 Plan gate_up_plan(int I, int S) {
   const int nu = I / 16;
-  if (nu >= 2 * SFG_GRID && nu <= 8 * SFG_GRID) return make_plan_spread(nu, S, SFG_GRID);
+  if (nu >= 2 * SFG_GRID && nu <= 8 * SFG_GRID)
+    return make_plan_spread(nu, S, spread_workgroups(nu, SFG_GRID));
   return make_plan(I / 128, S);
 }
 

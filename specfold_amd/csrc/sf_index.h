@@ -97,6 +97,14 @@ inline Plan make_plan_whole(int T, int S) { return Plan{T, S, S}; }
 // every CU streams NU/T units instead of the 8 of a 128-column tile.
 inline Plan make_plan_spread(int NU, int S, int T) { return Plan{T, S, S, NU}; }
 SF_IDX int spread_begin(int t, const Plan& p) { return (int)((long long)t * p.NU / p.T); }
+// Workgroups of a column-spread plan over nu units: the fewest that give none more
+// than ceil(nu / grid) units, so all but a few carry the same count (a full grid
+// of 4 and 5 units leaves the CUs with 4 idle through the last fifth of the
+// stream, when the others no longer fill HBM).
+SF_IDX int spread_workgroups(int nu, int grid) {
+  const int k = (nu + grid - 1) / grid;
+  return (nu + k - 1) / k;
+}
 inline int plan_grid(const Plan& p) {
   return (int)(((long long)p.T * p.S + p.U - 1) / p.U);
 }

@@ -116,8 +116,29 @@ static void check_plans() {
   // [spread_begin(t), spread_begin(t + 1)) -- 1..8 of them, one per wave, waves past
   // them repeating the last -- cover every 16-column unit exactly once, with whole
   // tiles (no partial slots) and T workgroups
+  // (T, NU): a sweep of grids, then the grids gate/up picks (spread_workgroups) for
+  // every unit count it takes the plan at on 256 CUs, with the unit counts per
+  // workgroup all equal to ceil(NU / 256) but a few one lower
+  std::vector<std::pair<int, int>> spread_cases;
   for (int T : {1, 3, 8, 64, 255, 256})
-    for (int NU = T; NU <= 8 * T; NU += (NU < 3 * T ? 1 : 7)) {
+    for (int NU = T; NU <= 8 * T; NU += (NU < 3 * T ? 1 : 7)) spread_cases.push_back({T, NU});
+  for (int NU = 2 * 256; NU <= 8 * 256; ++NU) {
+    const int T = sfg::spread_workgroups(NU, 256);
+    const int k = (NU + 255) / 256;
+    CHECK(T <= 256 && T * k >= NU && (T - 1) * k < NU, "spread grid %d for %d units", T, NU);
+    int fewer = 0;
+    const sfg::Plan sp = sfg::make_plan_spread(NU, 56, T);
+    for (int t = 0; t < T; ++t) {
+      const int n = sfg::spread_begin(t + 1, sp) - sfg::spread_begin(t, sp);
+      CHECK(n == k || n == k - 1, "spread units %d of %d", n, k);
+      fewer += n < k;
+    }
+    CHECK(fewer < T, "spread: every workgroup short");
+    spread_cases.push_back({T, NU});
+  }
+  for (const auto& tc : spread_cases) {
+    const int T = tc.first, NU = tc.second;
+    {
       const sfg::Plan sp = sfg::make_plan_spread(NU, 56, T);
       CHECK(sfg::plan_grid(sp) == T, "spread grid");
       std::vector<int> hit(NU, 0);
@@ -137,6 +158,7 @@ static void check_plans() {
       for (int u = 0; u < NU; ++u) CHECK(hit[u] == 1, "spread unit %d written %d times", u, hit[u]);
       ++plans;
     }
+  }
   // the shapes of the workloads (hidden D, q/k/v width, intermediate I, vocab V)
   struct Shape { int D, nqkv, I, V; };
   const Shape shapes[] = {{1536, 2048, 8960, 151936},  {3584, 4608, 18944, 152064},

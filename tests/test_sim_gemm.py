@@ -61,6 +61,14 @@ def gemm_sim_grid3(tmp_path_factory):
     return _build(tmp_path_factory, ("-DSFG_GRID=3",))
 
 
+@pytest.fixture(scope="module")
+def gemm_sim_grid7(tmp_path_factory):
+    """A 7-workgroup grid: 24 gate/up units take the spread plan over
+    spread_workgroups(24, 7) = 6 workgroups (4 units each), fewer than the grid, as
+    1184 units take 237 of 256 at the 7B shape."""
+    return _build(tmp_path_factory, ("-DSFG_GRID=7",))
+
+
 @pytest.mark.parametrize("case", [
     (256, 384, 39, 64, 40, 1),      # D, I, count, bucket, M, seed: one row block
     (384, 512, 100, 128, 70, 2),    # two row blocks
@@ -86,5 +94,12 @@ def test_gemm_kernels_in_simulator(gemm_sim, case):
 def test_gemm_kernels_column_spread_plan(gemm_sim_grid3, case):
     r = subprocess.run([str(gemm_sim_grid3), *map(str, case)], capture_output=True, text=True,
                        timeout=600)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
+
+
+def test_gemm_kernels_spread_plan_on_part_of_the_grid(gemm_sim_grid7):
+    r = subprocess.run([str(gemm_sim_grid7), "256", "384", "39", "64", "40", "14"],
+                       capture_output=True, text=True, timeout=600)
     print(r.stdout)
     assert r.returncode == 0, r.stdout + r.stderr
