@@ -47,7 +47,21 @@ def test_roofline_bytes_follow_the_unit_figures(name):
         bench.kernel_roofline("nope", 1.0, w, R, B1, N, P)
 
 
-def _pmc_csv(path, w, fetch_kib, write_kib, cal_kib):
+def _launched(name, optional):
+    """The kernel names one launch of entry point `name` dispatches: each pattern's
+    last alternative; optional ("?") kernels only when `optional`."""
+    out = []
+    for pat in bench.PMC_KERNELS[name]:
+        pat = pat if isinstance(pat, str) else pat[-1]
+        if pat.startswith("?"):
+            if optional:
+                out.append(pat[1:])
+        else:
+            out.append(pat)
+    return out
+
+
+def _pmc_csv(path, w, fetch_kib, write_kib, cal_kib, optional=True):
     """A counter_collection.csv as rocprofv3 --pmc writes it for one --pmc-pass run:
     the verify steps before the pause, then the calibration copy and PMC_ORDER's
     launches (one per layer, the once-per-step ones once), with a torch copy
@@ -72,8 +86,7 @@ def _pmc_csv(path, w, fetch_kib, write_kib, cal_kib):
     emit("vectorized_elementwise_kernel", cal_kib, cal_kib, gap=10 ** 9)   # the pause
     for name in bench.PMC_ORDER:
         for li in range(1 if name in bench.ONCE_PER_STEP else L):
-            for j, pat in enumerate(bench.PMC_KERNELS[name]):
-                pat = pat if isinstance(pat, str) else pat[-1]   # the last alternative
+            for j, pat in enumerate(_launched(name, optional)):
                 emit(pat + "x>(int)", fetch_kib[name] + li + j, write_kib[name])
             if name == "attn" and li == 0:
                 emit("elementwise_kernel_copy", 1e6, 1e6)
@@ -83,21 +96,24 @@ def _pmc_csv(path, w, fetch_kib, write_kib, cal_kib):
         wr.writerows(rows)
 
 
-def test_traffic_table_scales_each_launch_by_the_copy_calibration(tmp_path):
+@pytest.mark.parametrize("optional", [True, False])
+def test_traffic_table_scales_each_launch_by_the_copy_calibration(tmp_path, optional):
     """Bytes per launch = mean over layers of the sum over the launch's kernels of
     FETCH_SIZE and WRITE_SIZE (KiB), times 256 MiB / the calibration copy's reading;
-    kernels of other libraries between ours are skipped."""
+    kernels of other libraries between ours are skipped; an optional kernel ("?":
+    gate/up's SiLU fix-up) counts where it was launched and is not looked for
+    further on where it was not."""
     w = workload("cfg3_7b")
     L = w.shape.layers
     fetch = {n: 100.0 * (i + 1) for i, n in enumerate(bench.PMC_ORDER)}
     write = {n: 10.0 * (i + 1) for i, n in enumerate(bench.PMC_ORDER)}
     cal = (256 << 20) / 1024 / 2.0          # the counter reads half the copy's bytes
     p = tmp_path / "counter_collection.csv"
-    _pmc_csv(p, w, fetch, write, cal)
+    _pmc_csv(p, w, fetch, write, cal, optional)
     out = bench.traffic_table([str(p)], "cfg3_7b")
     assert out["calibration"]["fetch_factor"] == pytest.approx(2.0)
     for name in bench.PMC_ORDER:
-        k = len(bench.PMC_KERNELS[name])
+        k = len(_launched(name, optional))
         n = 1 if name in bench.ONCE_PER_STEP else L
         f_mean = sum(fetch[name] * k + k * li + k * (k - 1) / 2 for li in range(n)) / n
         want = (f_mean + write[name] * k) * 1024 * 2.0
