@@ -48,7 +48,8 @@ def reference(q_buf, kv_buf, pk, pv, src, rows, B1, N, H, Hkv, scaling, causal):
     return torch.stack(out_o), torch.stack(out_m), torch.stack(out_z)
 
 
-def run_case(P, B1, N, H, Hkv, count, seed, causal=False, P_cap=None, page_size=16):
+def run_case(P, B1, N, H, Hkv, count, seed, causal=False, P_cap=None, page_size=16,
+             key_ramp=None):
     torch.manual_seed(seed)
     dev = "cuda"
     BN = B1 * N
@@ -69,7 +70,11 @@ def run_case(P, B1, N, H, Hkv, count, seed, causal=False, P_cap=None, page_size=
         cap = P_cap or P
         cache = PagedKVCache(1, Hkv, HD, cap, page_size=page_size, device=dev,
                              page_order="shuffled", seed=seed)
-        pk = torch.randn(1, Hkv, P, HD, device=dev).to(torch.bfloat16)
+        pk = torch.randn(1, Hkv, P, HD, device=dev)
+        if key_ramp is not None:
+            # key magnitudes growing along the prefix: the scores' maximum keeps rising
+            pk = pk * torch.linspace(key_ramp[0], key_ramp[1], P, device=dev)[None, None, :, None]
+        pk = pk.to(torch.bfloat16)
         pv = torch.randn(1, Hkv, P, HD, device=dev).to(torch.bfloat16)
         cache.load_dense([(pk, pv)])
     o32 = torch.zeros(BN, H * HD, device=dev)
@@ -134,3 +139,16 @@ def test_attention_causal_block_long_prefix():
 
 def test_attention_no_prefix():
     run_case(0, 4, 32, 28, 4, 50, seed=6)
+
+
+@pytest.mark.parametrize("P,B1,N,H,Hkv,count,ramp", [
+    (16384, 8, 32, 40, 8, 39, (0.1, 8.0)),   # rising: the maximum passes the softmax
+    (3000, 8, 32, 28, 4, 100, (0.1, 8.0)),   # reference many times inside a range
+    (16384, 8, 32, 40, 8, 39, (8.0, 0.1)),   # falling: set by the first chunks
+])
+def test_attention_rising_and_falling_scores(P, B1, N, H, Hkv, count, ramp):
+    """Scores whose maximum grows by several powers of two from chunk to chunk (the
+    prefix pass moves its softmax reference up each time the maximum passes it by
+    2^8, rescaling the accumulated terms) or shrinks along the prefix (one
+    reference for the whole range)."""
+    run_case(P, B1, N, H, Hkv, count, seed=11, key_ramp=ramp)
