@@ -85,9 +85,10 @@ SF_DEV void lds_fragments(sf_u32x4 (&f)[NMT + WN], sf_lds_off a_addr, sf_lds_off
 // re-read the last row, which keeps every count exact; the loop drains them at
 // its end.
 // A wave with no columns of its own (wact false: a column-spread workgroup with
-// fewer units than waves) issues the same number of copies, but re-reads its first
-// A copy (L2-resident) into its own weight slots instead of weight bytes, and its
-// results are dropped.
+// fewer units than waves) issues the same number of copies (the waits count them),
+// but re-reads its first A copy (L2-resident) into its own weight slots instead of
+// weight bytes, and reads no fragments and issues no MFMAs (its results are
+// dropped), which leaves the LDS and the matrix cores of its SIMD to the others.
 template <int WN, int NMT, int MB>
 SF_DEV void mainloop(const uint16_t* __restrict__ A, int lda, int mrows, const int* rows,
                      const uint16_t* const (&wsrc)[WN], int s0, int s1, const Ring<MB, WN>& rg,
@@ -141,6 +142,7 @@ SF_DEV void mainloop(const uint16_t* __restrict__ A, int lda, int mrows, const i
         sf_wait_vm_barrier<(R - 2) * (DPW + 2 * WN)>();
         issue(sb + j + R - 1, rg.slot[(j + R - 1) % R]);
         const sf_lds_off base = sf_lds_addr(rg.slot[j]);
+        if (!wact) continue;   // wave-uniform: no operand reads or MFMAs for dropped results
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
           sf_u32x4 f[NMT + WN];
