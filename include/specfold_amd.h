@@ -40,6 +40,8 @@ extern "C" {
 #define SF_ERR_WORKSPACE 3 /* workspace smaller than *_workspace_bytes() */
 #define SF_ERR_HIP 4       /* a HIP launch failed */
 #define SF_ERR_SCRATCH 5   /* larger than the fixed scratch of an allocation-free entry point */
+#define SF_ERR_CAPTURE 6   /* an allocation-free entry point's first call on a device made
+                              under stream capture (its set-up must run eagerly) */
 
 /* Gate precision modes for sf_fold_gate. */
 #define SF_GATE_MODEL_DTYPE 0 /* norms rounded to bf16 as the PyTorch reference
@@ -63,7 +65,8 @@ const char* sf_status_string(int status);
  * 6: sf_logit_stats_noalloc, SF_ERR_SCRATCH.
  * 7: sf_attn_rows; the attention workspace holds the merged prefix states.
  * 8: all-rows o_proj / lm_head: sf_o_proj_post_norm, sf_o_proj_workspace_bytes (the
- *    workspace of sf_o_proj_residual). */
+ *    workspace of sf_o_proj_residual).
+ * 9: SF_ERR_CAPTURE; attention entry points refuse bucket or B1*N above 1024. */
 int sf_abi_version(void);
 
 /*
@@ -174,8 +177,9 @@ int sf_qkv_rope_branches(const uint16_t* xn, const int32_t* rows, const int32_t*
  * P is then the capacity the grid and workspace are sized for (so one captured
  * graph serves a growing cache).  With prefix_len NULL, P is the length.
  * workspace: sf_attn_workspace_bytes(bucket, H, P) bytes, 16-byte aligned (scratch).
- * Limits: hd == 128, H % Hkv == 0, N <= 64, H/Hkv <= 8, P <= 32768, a page size
- * of 16, 32, 64 or 128 tokens (a page holds whole 16-key groups).
+ * Limits: hd == 128, H % Hkv == 0, N <= 64, H/Hkv <= 8, B1*N <= 1024 and
+ * bucket <= 1024 (else SF_ERR_SHAPE), P <= 32768, a page size of 16, 32, 64 or
+ * 128 tokens (a page holds whole 16-key groups).
  */
 size_t sf_attn_workspace_bytes(int bucket, int H, int P);
 int sf_attn_prefix_block(const uint16_t* q_buf, const uint16_t* kv_buf, const uint16_t* prefix_k,
@@ -198,7 +202,8 @@ int sf_attn_prefix_block(const uint16_t* q_buf, const uint16_t* kv_buf, const ui
  * sf_attn_prefix_block + sf_chain_correct.  rows / count: the recomputed rows of
  * those branches (ascending; every folded row's source row among them).  A batched
  * step calls it once per sequence with that sequence's branch range and rows.
- * Same workspace and limits as sf_attn_prefix_block; no causal mode.
+ * Same workspace and limits as sf_attn_prefix_block (B1*N <= 1024, bucket <=
+ * 1024); no causal mode.
  */
 int sf_attn_rows(const uint16_t* q_buf, const uint16_t* kv_buf, const uint16_t* prefix_k,
                  const uint16_t* prefix_v, const int32_t* page_table, int P, int page_size,
@@ -340,8 +345,11 @@ int sf_logit_stats(const uint16_t* logits, int M, int V, long long ld, float top
  * (16 MiB + 32 KiB per GPU).  No counterpart in the reference: it is for callers
  * that cannot allocate device memory (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc).  It calls no allocating
- * routine; the first call on a device looks the array up and clears it on
- * `stream` (the current device must be the stream's).
+ * routine; the first call on a device looks the array up, clears it on
+ * `stream` and waits for the clear (the current device must be the stream's),
+ * so that first call must not be made under stream capture: it returns
+ * SF_ERR_CAPTURE there without launching anything.  Make one eager call per
+ * device before capturing; later calls may be captured.
  * Limit: M <= sf_logit_stats_noalloc_max_rows() (64), else SF_ERR_SCRATCH.
  * Every call on one GPU shares that GPU's array: calls that overlap on one GPU
  * (other streams, other host threads) race and must be ordered by the caller.

@@ -170,12 +170,18 @@ def folded_layer(
     counters: Optional[FoldCounters] = None,
     trace: Optional[LayerTrace] = None,
     q_scale: Optional[torch.Tensor] = None,
+    qkv_rows=None,
 ) -> List[torch.Tensor]:
     """One decoder layer of the folded verify step for all B1 branches.
 
     Follows fastdllm_v2_folded.py:117-220 (and nld_folded.py:132-232, which adds
     ``q_scale``).  ``h`` is a list of B1 tensors [1, N, D]; returns the list of
     next-layer hidden states.
+
+    ``qkv_rows`` (stage forcing, for tests): a callable (branch i, recomputed
+    positions rsel) -> (q [H, n, hd], k [Hkv, n, hd], v [Hkv, n, hd]) that
+    replaces the roped (and scaled) projections of those rows, so that the
+    attention and the chain correction below run on given q/k/v.
     """
     attn = lyr.self_attn
     hd = attn.head_dim
@@ -245,6 +251,8 @@ def folded_layer(
             kn = kn * c + rotate_half(kn) * s
             if q_scale is not None:                               # nld_folded.py:173-174
                 qn = qn * q_scale.to(qn.device)[rsel].view(1, n_rec, 1).to(qn.dtype)
+            if qkv_rows is not None:
+                qn, kn, vn = (t.to(device=dev, dtype=x_dtype) for t in qkv_rows(i, rsel))
             if p is not None:
                 k_prev = kt[:, rsel].clone()
                 v_prev = vt[:, rsel].clone()

@@ -14,10 +14,12 @@ from __future__ import annotations
 import argparse
 import concurrent.futures as cf
 import os
+import re
 import shutil
 import subprocess
 import sys
 from pathlib import Path
+from typing import Dict, List
 
 PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
@@ -44,12 +46,54 @@ def sources():
     return sorted(CSRC.glob("*.hip"))
 
 
+_REMARK = re.compile(r"remark:\s+(Function Name|ScratchSize \[bytes/lane\]|VGPRs Spill|SGPRs Spill"
+                     r"|VGPRs|AGPRs):\s*(\S+)")
+
+
+def kernel_resources(remarks: str) -> Dict[str, Dict[str, str]]:
+    """Per kernel (mangled name) its VGPRs, AGPRs, ScratchSize and spill counts,
+    from hipcc's -Rpass-analysis=kernel-resource-usage remarks."""
+    out: Dict[str, Dict[str, str]] = {}
+    cur = None
+    for m in _REMARK.finditer(remarks):
+        key, val = m.group(1), m.group(2)
+        if key == "Function Name":
+            cur = out.setdefault(val, {})
+        elif cur is not None:
+            cur[key] = val
+    return out
+
+
+def spilling_kernels(res: Dict[str, Dict[str, str]]) -> List[str]:
+    """Kernels with private scratch or spilled registers.  The kernels read LDS
+    with untracked inline-asm loads (sf_lds_read16 and kin) that are waited for
+    by an explicit lgkmcnt wait: a spill or register copy of a destination
+    placed between the read and its wait would store stale data silently, so
+    the build refuses any kernel that spills or uses scratch at all."""
+    bad = []
+    for name, r in res.items():
+        if int(r.get("ScratchSize [bytes/lane]", "0")) or int(r.get("VGPRs Spill", "0")) or \
+                int(r.get("SGPRs Spill", "0")):
+            bad.append(f"{name}: {r}")
+    return bad
+
+
 def _compile(src: Path, asm: bool) -> Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [HIPCC, *DEVICE_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *DEVICE_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj),
+           "-Rpass-analysis=kernel-resource-usage"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{r.stderr}")
+    res = kernel_resources(r.stderr)
+    if not res:
+        raise RuntimeError(f"hipcc reported no kernel resource usage for {src.name}")
+    bad = spilling_kernels(res)
+    if bad:
+        raise RuntimeError(f"{src.name}: kernels with scratch or register spills:\n" +
+                           "\n".join(bad))
+    (BUILD / (src.stem + ".resources.txt")).write_text(
+        "".join(f"{k} {v}\n" for k, v in sorted(res.items())))
     if asm:
         s = BUILD / (src.stem + f"-{ARCH}.s")
         cmd = [HIPCC, *DEVICE_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "--cuda-device-only", "-S",

@@ -727,6 +727,8 @@ int attention(bool folded, const uint16_t* q_buf, const uint16_t* kv_buf,
     return SF_ERR_ARG;
   if (hd != kHD || H < 1 || Hkv < 1 || H % Hkv != 0 || H / Hkv > kMaxG) return SF_ERR_SHAPE;
   if (N < 1 || N > kMaxN || B1 < 1 || bucket < 1 || bucket > B1 * N) return SF_ERR_SHAPE;
+  // the finalize stages the compacted rows in a kMaxBucket-entry LDS table
+  if (bucket > kMaxBucket || B1 * N > kMaxBucket) return SF_ERR_SHAPE;
   if (b_first < 0 || b_count < 1 || b_first + b_count > B1) return SF_ERR_SHAPE;
   if (P < 0 || nchunks_for(P) > kMaxChunks) return SF_ERR_SHAPE;
   if (P > 0) {

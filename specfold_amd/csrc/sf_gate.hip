@@ -266,6 +266,9 @@ extern "C" const char* sf_status_string(int status) {
     case SF_ERR_WORKSPACE: return "workspace too small";
     case SF_ERR_HIP: return "HIP launch failed";
     case SF_ERR_SCRATCH: return "size beyond the fixed scratch of an allocation-free entry point";
+    case SF_ERR_CAPTURE:
+      return "first call of an allocation-free entry point on this device made under stream "
+             "capture (make one eager call first)";
     default: return "unknown status";
   }
 }
@@ -305,7 +308,7 @@ __global__ __launch_bounds__(64) void sf_parent_map_kernel(const int64_t* __rest
 
 }  // namespace
 
-extern "C" int sf_abi_version(void) { return 8; }
+extern "C" int sf_abi_version(void) { return 9; }
 
 extern "C" int sf_parent_map(const int64_t* tokens, int B1, int N, int32_t* par, int32_t* counts,
                              void* stream) {

@@ -384,18 +384,24 @@ std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices];  // scratch's device address per device; null until set up
 
 // The current device's copy of scratch.  The first call on a device looks its
-// address up and clears the histograms (a fill kernel on `st`, so that it also
-// works under stream capture); every call leaves them zero again after that.
+// address up and clears the histograms with a fill kernel on `st`, then waits for
+// it, so the address is published only once the array is zero for every stream;
+// that first call is refused under stream capture (the clear would become a node
+// of the caller's graph, run again on every replay, and would not have run when
+// the address is published).  Every call leaves the histograms zero again.
 int scratch_for_current_device(hipStream_t st, void** out) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return SF_ERR_HIP;
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess) return SF_ERR_HIP;
+    if (cs != hipStreamCaptureStatusNone) return SF_ERR_CAPTURE;
     void* p = nullptr;
     if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return SF_ERR_HIP;
     hipLaunchKernelGGL(sf_zero_kernel, dim3(1024), dim3(256), 0, st,
                        reinterpret_cast<sf_u32x4*>(p), kNoAllocHistBytes / 16);
-    if (sf_launch_status() != SF_OK) return SF_ERR_HIP;
+    if (sf_launch_status() != SF_OK || hipStreamSynchronize(st) != hipSuccess) return SF_ERR_HIP;
     g_scratch_ptr[dev] = p;
   }
   *out = g_scratch_ptr[dev];

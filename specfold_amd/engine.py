@@ -390,7 +390,8 @@ class FoldedVerifyEngine:
                         bucket: Optional[int] = None,
                         q_scales: Optional[List[Optional[torch.Tensor]]] = None,
                         stats: Optional[StepStats] = None, compute_logits: bool = True,
-                        pad_to: Optional[int] = None) -> Optional[List[torch.Tensor]]:
+                        pad_to: Optional[int] = None,
+                        trace: Optional[list] = None) -> Optional[List[torch.Tensor]]:
         """One verify step over several independent sequences -> per-sequence logits
         [B1_s, N, V] (unshifted).
 
@@ -411,7 +412,8 @@ class FoldedVerifyEngine:
         runs per sequence over its own prefix.  Each sequence's result is that of
         ``forward`` on it alone.  No counterpart in the reference, whose verify step
         takes one sequence.  ``stats`` counts every recomputed row, padded ones
-        included."""
+        included.  ``trace``: as in ``forward``, one dict per layer of the stacked
+        step's buffers (runs eagerly)."""
         if not blocks or len(blocks) != len(caches):
             raise ValueError("forward_batched needs one cache (or None) per token block")
         if q_scales is not None and len(q_scales) != len(blocks):
@@ -443,13 +445,14 @@ class FoldedVerifyEngine:
         buf = self.buffers(B1, N, bucket, P_alloc)
         self.rope_tables(max(cache_length(c) for c in caches) + N)
         q_scaled = q_scales is not None and any(q is not None for q in q_scales)
-        if self.use_graphs:
+        if self.use_graphs and trace is None:
             hidden = self._replay_batched(buf, tokens, sizes, caches, N, delta, bucket,
                                           q_scales if q_scaled else None)
         else:
             batch = _Batch(self, sizes, caches, N, q_scaled)
             batch.set_q_scales(q_scales, N)
-            hidden = self._run_layers(buf, tokens, None, delta, bucket, batch=batch)
+            hidden = self._run_layers(buf, tokens, None, delta, bucket, batch=batch,
+                                      trace=trace)
         overflow = bucket < BN and int(buf.count_slab.max()) > bucket
         if stats is not None:
             stats.count_dev, stats.bucket, stats.overflow = buf.count_slab.clone(), bucket, overflow
@@ -457,9 +460,11 @@ class FoldedVerifyEngine:
         if overflow:
             logger.warning("SpecFold bucket overflow (> %d); recomputing with bucket=%d",
                            bucket, BN)
+            if trace is not None:
+                trace.clear()
             return self.forward_batched(orig_blocks, caches, delta, bucket=BN, q_scales=q_scales,
                                         stats=stats, compute_logits=compute_logits,
-                                        pad_to=pad_to)
+                                        pad_to=pad_to, trace=trace)
         self.last_hidden = hidden
         if not compute_logits:
             return None
@@ -641,6 +646,13 @@ class FoldedVerifyEngine:
                     cache.length_dev.data_ptr(), cache.capacity)
         return (id(cache), cache.k_pages.data_ptr(), cache.v_pages.data_ptr(),
                 cache.page_table.data_ptr(), cache.length_dev.data_ptr(), cache.capacity)
+
+    def invalidate_prefix(self) -> None:
+        """Make the next step re-read a reference-style cache in full (after the
+        caller rewrote it in place at the same length and tensors, which the
+        engine's mirror cannot see)."""
+        if self._mirror is not None:
+            self._mirror.invalidate()
 
     def _mirror_of(self, cache, P: int) -> ContiguousMirror:
         """The engine's mirror of a reference-style cache, synced to it.  Capacity:

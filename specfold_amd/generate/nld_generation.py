@@ -27,13 +27,16 @@ logger = logging.getLogger(__name__)
 
 
 def add_gumbel_noise(logits: torch.Tensor, temperature: float) -> torch.Tensor:
-    """Scores whose argmax is a Gumbel-max sample at ``temperature``: exp(l) * E^-T
+    """Scores whose argmax is a Gumbel-max sample at ``temperature``: exp(l) / E^T
     with E = -ln U, U ~ U(0, 1), all in float64; the logits themselves at
-    temperature 0 (the rule of modeling_nemotron_labs_diffusion.py:814-821)."""
+    temperature 0.  The expression and its float64 roundings are the reference's
+    (modeling_nemotron_labs_diffusion.py:814-821), so that a seeded draw picks the
+    same token even at a near tie."""
     if temperature == 0:
         return logits
-    u = torch.rand(logits.shape, dtype=torch.float64, device=logits.device)
-    return torch.exp(logits.double()) * torch.pow(-torch.log(u), -float(temperature))
+    scores = logits.to(torch.float64)
+    u = torch.rand_like(scores)
+    return scores.exp() / (-torch.log(u)) ** temperature
 
 
 def get_num_transfer_tokens(mask_index: torch.Tensor, steps: int) -> torch.Tensor:

@@ -15,6 +15,7 @@ page, which must not change any result.
 
 from __future__ import annotations
 
+import weakref
 from dataclasses import dataclass
 from typing import List, Optional, Sequence, Tuple
 
@@ -135,10 +136,14 @@ class ContiguousMirror:
     K and V of every layer live in fixed buffers ``[L, Hkv, capacity, hd]`` with the
     length in device memory, so a verify step captured against the mirror stays
     valid while the reference cache grows: one capture per step shape instead of
-    one per commit.  ``sync`` copies the whole prefix again whenever the cache's
-    length or any layer's storage changed since the last sync (a commit, a crop, or
-    another sequence's cache); a cache rewritten in place at the same length and
-    the same storage is not detected (call ``invalidate`` after such an update)."""
+    one per commit.  ``sync`` copies the whole prefix again unless the cache is the
+    very object last synced, holding the very same per-layer tensor objects at the
+    same length and storage: identity is kept by weak references (to the cache
+    where it allows one, and to every layer's K and V tensor), never by ``id()``,
+    which CPython hands to a new object once the old one is freed, just as the
+    caching allocator hands its blocks to new tensors.  A cache rewritten in place
+    at the same length and the same tensors is not detected (call ``invalidate``
+    after such an update)."""
 
     def __init__(self, num_layers: int, num_kv_heads: int, head_dim: int, capacity: int,
                  device="cuda", dtype=torch.bfloat16):
@@ -153,6 +158,7 @@ class ContiguousMirror:
         self.length = 0
         self.length_dev = torch.zeros(1, dtype=torch.int32, device=self.device)
         self._sig = None
+        self._refs: tuple = ()
 
     def get_seq_length(self, layer_idx: int = 0) -> int:
         return self.length
@@ -162,20 +168,40 @@ class ContiguousMirror:
 
     def invalidate(self) -> None:
         self._sig = None
+        self._refs = ()
 
     @staticmethod
     def signature(cache, num_layers: int) -> tuple:
         views = [prefix_view(cache, li) for li in range(num_layers)]
-        return (id(cache), cache_length(cache),
+        return (cache_length(cache),
                 tuple((0, 0) if pv is None else (pv.k.data_ptr(), pv.v.data_ptr())
                       for pv in views))
+
+    @staticmethod
+    def _identity(cache, num_layers: int) -> tuple:
+        """The objects whose identity the mirror's contents stand for: the cache
+        (when it can be weakly referenced; a list cannot) and each layer's K and V
+        tensor objects as the cache holds them."""
+        objs = [cache] if _weakrefable(cache) else [None]
+        for li in range(num_layers):
+            objs.extend(layer_kv(cache, li))
+        return tuple(objs)
+
+    def _same_objects(self, objs: tuple) -> bool:
+        if len(objs) != len(self._refs):
+            return False
+        for o, r in zip(objs, self._refs):
+            if (o is None) != (r is None) or (r is not None and r() is not o):
+                return False
+        return True
 
     def sync(self, cache) -> bool:
         """Make the mirror hold ``cache``'s prefix; returns True if it copied."""
         sig = self.signature(cache, self.num_layers)
-        if sig == self._sig:
+        objs = self._identity(cache, self.num_layers)
+        if sig == self._sig and self._same_objects(objs):
             return False
-        P = sig[1]
+        P = sig[0]
         if P > self.capacity:
             raise ValueError(f"prefix of {P} keys exceeds the mirror's capacity {self.capacity}")
         for li in range(self.num_layers):
@@ -187,6 +213,7 @@ class ContiguousMirror:
         self.length = P
         self.length_dev.fill_(P)
         self._sig = sig
+        self._refs = tuple(None if o is None else weakref.ref(o) for o in objs)
         return True
 
     def view(self, li: int) -> PrefixView:
@@ -219,18 +246,32 @@ def cache_length(cache) -> int:
     return int(cache[0][0].shape[-2])
 
 
+def _weakrefable(obj) -> bool:
+    try:
+        weakref.ref(obj)
+    except TypeError:
+        return False
+    return True
+
+
+def layer_kv(cache, li: int) -> Tuple[Optional[torch.Tensor], Optional[torch.Tensor]]:
+    """Layer li's (k, v) tensor objects as a reference-style cache holds them
+    (a transformers DynamicCache, old or new API, or a list of per-layer pairs);
+    (None, None) past its layers."""
+    if len(cache) <= li:
+        return None, None
+    if hasattr(cache, "layers") and not hasattr(cache, "__getitem__"):
+        return cache.layers[li].keys, cache.layers[li].values   # transformers>=5 DynamicCache
+    return cache[li][0], cache[li][1]
+
+
 def prefix_view(cache, li: int) -> Optional[PrefixView]:
     """Kernel view of layer li of either a PagedKVCache or a reference-style cache."""
     if cache is None:
         return None
     if isinstance(cache, (PagedKVCache, ContiguousMirror)):
         return cache.view(li)
-    if len(cache) <= li:
-        return None
-    if hasattr(cache, "layers") and not hasattr(cache, "__getitem__"):
-        k, v = cache.layers[li].keys, cache.layers[li].values   # transformers>=5 DynamicCache
-    else:
-        k, v = cache[li][0], cache[li][1]
+    k, v = layer_kv(cache, li)
     if k is None or k.shape[-2] == 0:
         return None
     return contiguous_view(k, v)

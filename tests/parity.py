@@ -25,8 +25,9 @@ Tolerances (per quantity; the same everywhere they are used):
                                             max|ref|), mean rel <= 1e-3
   O (fp32), m, Z                            max |hip - ref| <= 2e-3 * max|ref|
   h_out (layer-input forced)                max abs <= 2e-2 * max(1, max|ref|) and mean rel
-                                            <= H_OUT_MEAN_REL_MAX against the CPU oracle;
-                                            the oracle's own GPU-vs-CPU spread and HIP vs
+                                            <= H_OUT_MEAN_REL_MAX (3.5e-3; measured <= 2.7e-3)
+                                            against the CPU oracle; the oracle's own
+                                            GPU-vs-CPU spread (measured <= 2.4e-3) and HIP vs
                                             the oracle on the GPU are reported beside it.
 
 Why the layer-input-forced h_out is further than 1e-3: the QKV GEMM's fp32
@@ -51,7 +52,14 @@ from tests.helpers import err_stats, src_from_mask
 
 NS_MAX_ABS = 2e-2       # north star: hidden states and logits, max abs (x max(1, |ref|))
 NS_MEAN_REL = 1e-3      # north star: hidden states and logits, mean relative
-H_OUT_MEAN_REL_MAX = 4e-3   # layer-input-forced h_out, whatever the oracle's own spread
+# Layer-input-forced h_out against the CPU oracle: measured at most 2.70e-3 mean rel
+# over every parity layer (cfg4 layer 0, where the oracle's own GPU-vs-CPU spread
+# is 1.88e-3; 2.38e-3 is the largest such spread measured), bound with a 30% margin.
+H_OUT_MEAN_REL_MAX = 3.5e-3
+# End to end (no forcing), the HIP step may be no further from the oracle run on
+# the same GPU than this many times the oracle's own GPU-vs-CPU spread (or the
+# north star's mean rel, whichever is larger).
+LOGITS_SPREAD_FACTOR = 1.5
 
 
 def bf16_close(a, b, rel=2 ** -7, abs_=2 ** -7):
@@ -105,11 +113,12 @@ def ns_ok(st: dict) -> bool:
 
 def oracle_layer(lyr, h_in: torch.Tensor, parent, counts, kv, cos_n, sin_n, delta: float,
                  H: int, Hkv: int, q_scale: Optional[torch.Tensor] = None,
-                 device: str = "cpu") -> LayerTrace:
+                 device: str = "cpu", qkv_rows=None) -> LayerTrace:
     """The oracle's folded layer on ``device`` for layer inputs ``h_in``
     [B1, N, D] (any device); the layer module ``lyr`` is copied there when it
     lives elsewhere.  kv = (k, v) [1, Hkv, P, hd] or None; cos_n/sin_n [N, hd]
-    of the block positions.  The trace comes back on the CPU."""
+    of the block positions; ``qkv_rows`` forces the recomputed rows' q/k/v
+    (folded_layer's stage forcing).  The trace comes back on the CPU."""
     dev = torch.device(device)
     on_dev = next(lyr.parameters()).device == dev
     lyr_d = lyr if on_dev else copy.deepcopy(lyr).to(dev)
@@ -120,7 +129,7 @@ def oracle_layer(lyr, h_in: torch.Tensor, parent, counts, kv, cos_n, sin_n, delt
     with torch.no_grad():
         folded_layer(lyr_d, hs, parent, topo_order(counts), kv_d, cos_n.to(dev), sin_n.to(dev),
                      float(delta), H, Hkv, trace=lt,
-                     q_scale=None if q_scale is None else q_scale.to(dev))
+                     q_scale=None if q_scale is None else q_scale.to(dev), qkv_rows=qkv_rows)
     if not on_dev:
         del lyr_d
     return lt
@@ -326,4 +335,23 @@ def compare_layer(li: int, lt: LayerTrace, ht: dict, parent, B1: int, N: int, H:
             print(f"    {k:32s} max {v['max_abs']:.3g} mean_rel {v['mean_rel']:.2e} "
                   f"diff {v['frac_diff']:.4f} |ref| {v['ref_absmax']:.3g}{extra}", flush=True)
     assert not fails, f"layer {li}: {fails}"
+    return out
+
+
+def slice_trace(ht: dict, o: int, b: int, N: int) -> dict:
+    """Sequence s's part of one layer of a batched step's trace
+    (FoldedVerifyEngine.forward_batched(trace=...)): branches o .. o+b-1 of the
+    stacked step, re-indexed as that sequence's own step (flat rows from 0,
+    src branch ids from 0, its compacted rows in ascending order with the tail
+    at b*N), in the form ``compare_layer`` reads."""
+    lo, hi = o * N, (o + b) * N
+    cnt = int(ht["count"].item())
+    rows = ht["rows"][:cnt].long()
+    mine = rows[(rows >= lo) & (rows < hi)] - lo
+    rows_s = torch.full((b * N,), b * N, dtype=torch.int32, device=rows.device)
+    rows_s[:mine.numel()] = mine.to(torch.int32)
+    out = dict(rows=rows_s, count=torch.tensor([int(mine.numel())], dtype=torch.int32),
+               src=ht["src"][lo:hi] - o)
+    for k in ("h_in", "rec", "q", "kv", "o32", "o_bf", "m", "z", "hp", "h_out", "xn"):
+        out[k] = ht[k][lo:hi]
     return out

@@ -271,6 +271,13 @@ inline hipError_t hipGetSymbolAddress(void** p, const void* sym) {
   *p = const_cast<void*>(sym);
   return hipSuccess;
 }
+// Launches run to completion when they are made and nothing is ever captured.
+enum hipStreamCaptureStatus { hipStreamCaptureStatusNone = 0, hipStreamCaptureStatusActive = 1 };
+inline hipError_t hipStreamIsCapturing(hipStream_t, hipStreamCaptureStatus* s) {
+  *s = hipStreamCaptureStatusNone;
+  return hipSuccess;
+}
+inline hipError_t hipStreamSynchronize(hipStream_t) { return hipSuccess; }
 
 // Runs grid x block work-items: the workgroups are shared out over a pool of OS
 // threads; a workgroup runs as blockDim fibers on one of them (its __shared__

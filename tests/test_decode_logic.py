@@ -55,3 +55,22 @@ def test_draft_blocks_match_literal_loop():
         assert len(got) == len(ref)
         for d, r in zip(got, ref):
             assert torch.equal(d["state"], r)
+
+
+def test_gumbel_noise_is_the_reference_expression():
+    """Seeded Gumbel-max scores equal the reference's float64 expression
+    exp(l) / (-log u)^T (modeling_nemotron_labs_diffusion.py:814-821) bit for
+    bit, so a seeded draw transfers the same tokens, near ties included."""
+    from specfold_amd.generate.nld_generation import add_gumbel_noise
+    gen = torch.Generator().manual_seed(0)
+    for seed, T in ((1, 1.0), (2, 0.7), (3, 0.3)):
+        logits = torch.randn(4, 64, 257, generator=gen).to(torch.bfloat16)
+        logits[0, 0, 3] = logits[0, 0, 5]                       # a tie
+        torch.manual_seed(seed)
+        got = add_gumbel_noise(logits, T)
+        torch.manual_seed(seed)
+        lg = logits.to(torch.float64)
+        ref = lg.exp() / (-torch.log(torch.rand_like(lg, dtype=torch.float64))) ** T
+        assert torch.equal(got, ref)
+        assert torch.equal(got.argmax(-1), ref.argmax(-1))
+    assert add_gumbel_noise(logits, 0) is logits

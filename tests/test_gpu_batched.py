@@ -1,8 +1,10 @@
 """GPU check of FoldedVerifyEngine.forward_batched (sf_qkv_rope_branches and the
 SF_GATE_ROOTS_BY_PARENT gate): several sequences in one verify step against each
 sequence's own forward.  Integer outputs (per-layer recomputed-row counts) must
-be identical; logits within the parity tolerance (o_proj and lm_head run on
-hipBLASLt, whose kernel choice may change with M = total rows)."""
+be identical, and so must the final hidden state, bit for bit (every kernel's
+per-row summation order is independent of the other sequences' rows); the
+logits too when the head runs on the library's own kernel, else within the
+north star's bound (hipBLASLt's tile choice follows M = total rows)."""
 
 import pytest
 import torch
@@ -46,18 +48,26 @@ def test_batched_step_gpu(family):
         qss.append(qs.cuda() if qs is not None else None)
     print(f"[batched_gpu] {family} specs={specs}", flush=True)
     eng = FoldedVerifyEngine(model)
-    single, counts = [], []
+    single, counts, hidden = [], [], []
     for (tok, kv), qs in zip(seqs, qss):
         st = StepStats()
         single.append(eng.forward(tok, _paged(kv), 0.1, q_scale=qs, stats=st))
+        hidden.append(eng.last_hidden.clone())
         counts.append(st.counts)
     stb = StepStats()
     batched = eng.forward_batched([t for t, _ in seqs], [_paged(kv) for _, kv in seqs], 0.1,
                                   q_scales=qss, stats=stb)
     torch.cuda.synchronize()
     assert stb.counts == [sum(c) for c in zip(*counts)]
-    for a, b in zip(batched, single):
+    o = 0
+    for a, b, h, (tok, _) in zip(batched, single, hidden, seqs):
+        n = tok.shape[0] * 32
+        assert torch.equal(eng.last_hidden[o:o + n], h), "final hidden differs from alone"
+        o += n
         st = err_stats(a.float(), b.float())
+        print(f"[batched_gpu] logits vs alone {st}", flush=True)
+        if getattr(eng, "head_kernel", "hipblaslt") == "hip":
+            assert torch.equal(a, b), st
         assert st["max_abs"] <= 2e-2 * max(1.0, st["ref_absmax"]), st
 
 

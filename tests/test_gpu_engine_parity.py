@@ -15,7 +15,8 @@ from oracle.folded_reference import StepTrace, folded_verify_step
 from specfold_amd.engine import FoldedVerifyEngine, build_parent_map
 from specfold_amd.kv_cache import PagedKVCache
 from tests.helpers import SHAPE_G2, SHAPE_G6, SHAPE_G7, err_stats, make_case, to_gpu_model
-from tests.parity import NS_MAX_ABS, NS_MEAN_REL, bf16_close, compare_layer, oracle_layer
+from tests.parity import (LOGITS_SPREAD_FACTOR, NS_MAX_ABS, NS_MEAN_REL, compare_layer,
+                          oracle_layer)
 
 pytestmark = pytest.mark.gpu
 
@@ -81,7 +82,9 @@ def test_end_to_end_logits(name, shape, seed, P, delta):
     check_end_to_end(name, make_case(shape, seed, P=P, delta=delta))
 
 
-LOGITS_MEAN_REL_MAX = 8e-3   # end to end, whatever the oracle's own cross-device spread
+# End to end against the CPU oracle (2-layer cases): measured at most 5.55e-3 mean rel
+# (g7_p300; the oracle's own GPU-vs-CPU spread there is 3.99e-3), bound with a 25% margin.
+LOGITS_MEAN_REL_MAX = 7e-3
 
 
 def check_end_to_end(name, case, q_scale=None):
@@ -92,9 +95,9 @@ def check_end_to_end(name, case, q_scale=None):
       * zero mask flips against the CPU oracle at every layer;
       * max |d| <= 2e-2 * max(1, |ref|) against the CPU oracle and against the
         oracle on the same GPU;
-      * mean rel <= 1e-3 against the oracle on the same GPU unless the oracle
-        itself on the GPU is further than 1e-3 from its CPU result, and in every
-        case <= LOGITS_MEAN_REL_MAX;
+      * mean rel against the oracle on the same GPU <= max(1e-3,
+        LOGITS_SPREAD_FACTOR x the oracle's own GPU-vs-CPU spread), and against
+        the CPU oracle <= LOGITS_MEAN_REL_MAX;
       * the head alone (HIP final hidden state -> the oracle's norm + head on the
         same GPU) within max abs 2e-2 and mean rel 1e-3."""
     tr, ref_logits, trace, logits, eng = run_pair(case, teacher=False, q_scale=q_scale)
@@ -116,8 +119,9 @@ def check_end_to_end(name, case, q_scale=None):
     assert flips == 0
     for st in (st_cpu, st_gpu):
         assert st["max_abs"] <= NS_MAX_ABS * max(1.0, st["ref_absmax"]), st
-    assert st_gpu["mean_rel"] <= NS_MEAN_REL or spread["mean_rel"] > NS_MEAN_REL, (st_gpu, spread)
-    assert st_gpu["mean_rel"] <= LOGITS_MEAN_REL_MAX and st_cpu["mean_rel"] <= LOGITS_MEAN_REL_MAX
+    assert st_gpu["mean_rel"] <= max(NS_MEAN_REL, LOGITS_SPREAD_FACTOR * spread["mean_rel"]), \
+        (st_gpu, spread)
+    assert st_cpu["mean_rel"] <= LOGITS_MEAN_REL_MAX, st_cpu
     assert st_head["max_abs"] <= NS_MAX_ABS * max(1.0, st_head["ref_absmax"]) and \
         st_head["mean_rel"] <= NS_MEAN_REL, st_head
 

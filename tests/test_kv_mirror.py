@@ -70,3 +70,43 @@ def test_mirror_rejects_a_longer_prefix():
         assert "capacity" in str(e)
     else:
         raise AssertionError("a prefix longer than the capacity must be refused")
+
+
+def test_mirror_resyncs_new_objects_on_reused_storage():
+    """The drop-in path: the reference loop builds a fresh cache per generate
+    call.  A new cache object (or new per-layer tensors in the same container)
+    on the storage the old one used, at the same length, holds other contents:
+    the mirror must copy again, though the length and every data pointer are
+    unchanged (an id()-based key could also match, once CPython reuses the id)."""
+    L, Hkv, hd, P = 2, 2, 8, 12
+    g = torch.Generator().manual_seed(5)
+    store = [(torch.randn(1, Hkv, P, hd, generator=g).to(torch.bfloat16),
+              torch.randn(1, Hkv, P, hd, generator=g).to(torch.bfloat16)) for _ in range(L)]
+    cache = [(k, v) for k, v in store]
+    m = ContiguousMirror(L, Hkv, hd, 32, device="cpu")
+    assert m.sync(cache) is True
+    assert m.sync(cache) is False
+    # the same list object (same id), new tensor objects over the same storage,
+    # rewritten with other values
+    for li in range(L):
+        k, v = store[li]
+        k2, v2 = k.view_as(k), v.view_as(v)
+        k2.copy_(torch.randn(k.shape, generator=g))
+        v2.copy_(torch.randn(v.shape, generator=g))
+        cache[li] = (k2, v2)
+    assert ContiguousMirror.signature(cache, L) == m._sig    # length and pointers unchanged
+    assert m.sync(cache) is True
+    _check_same(m, cache, L)
+    # a DynamicCache dropped and a new one built on the same storage
+    dyn, _ = _dyn(L, Hkv, P, hd, 6)
+    assert m.sync(dyn) is True
+    from transformers.cache_utils import DynamicCache
+    layers = [(dyn.layers[li].keys, dyn.layers[li].values) for li in range(L)]
+    del dyn
+    dyn2 = DynamicCache()
+    for li, (k, v) in enumerate(layers):
+        k.mul_(-1)
+        dyn2.update(k.view_as(k), v.view_as(v), li)
+    assert m.sync(dyn2) is True
+    _check_same(m, dyn2, L)
+    assert m.sync(dyn2) is False

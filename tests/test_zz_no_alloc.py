@@ -60,3 +60,56 @@ def test_noalloc_rejects_rows_beyond_scratch():
     assert "allocation-free" in lib.sf_status_string(st).decode()
     with pytest.raises(_lib.SpecFoldKernelError):
         _lib.logit_stats_noalloc(x, out)
+
+
+_FIRST_CALL_UNDER_CAPTURE = r"""
+import sys, torch
+sys.path.insert(0, sys.argv[1])
+from specfold_amd import _lib
+V = 152064
+x = (torch.randn(8, V, device="cuda") * 3).to(torch.bfloat16)
+out = _lib.LogitStats(8, "cuda")
+g = torch.cuda.CUDAGraph()
+print("[child] first call under capture", flush=True)
+try:
+    with torch.cuda.graph(g):
+        _lib.logit_stats_noalloc(x, out, top_p=0.9)
+except _lib.SpecFoldKernelError as e:
+    print("[child] refused:", e, flush=True)
+    assert "capture" in str(e)
+else:
+    raise AssertionError("a first call under capture must be refused")
+torch.cuda.synchronize()
+print("[child] eager call, then a captured one", flush=True)
+ref = _lib.logit_stats(x, top_p=0.9)
+_lib.logit_stats_noalloc(x, out, top_p=0.9)
+g2 = torch.cuda.CUDAGraph()
+out2 = _lib.LogitStats(8, "cuda")
+with torch.cuda.graph(g2):
+    _lib.logit_stats_noalloc(x, out2, top_p=0.9)
+for rep in range(3):
+    for n in _lib.LogitStats.__slots__:
+        getattr(out2, n).zero_()
+    g2.replay()
+    torch.cuda.synchronize()
+    for n in _lib.LogitStats.__slots__:
+        assert torch.equal(getattr(out2, n).view(torch.int32), getattr(ref, n).view(torch.int32)), n
+    _ = (x.float().sum()).item()          # eager work between replays
+print("[child] ok", flush=True)
+"""
+
+
+def test_noalloc_first_call_under_capture_is_refused():
+    """A process's first call on a device sets the scratch array up (symbol
+    lookup, a clear it waits for): under stream capture it is refused with
+    SF_ERR_CAPTURE and nothing is launched; after one eager call, captured calls
+    replay with the workspace entry point's results.  Runs in a fresh child
+    process, since this process has set its array up already."""
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = str(Path(__file__).resolve().parents[1])
+    r = subprocess.run([sys.executable, "-c", _FIRST_CALL_UNDER_CAPTURE, root],
+                       capture_output=True, text=True, timeout=300)
+    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0 and "[child] ok" in r.stdout
