@@ -66,7 +66,8 @@ const char* sf_status_string(int status);
  * 7: sf_attn_rows; the attention workspace holds the merged prefix states.
  * 8: all-rows o_proj / lm_head: sf_o_proj_post_norm, sf_o_proj_workspace_bytes (the
  *    workspace of sf_o_proj_residual).
- * 9: SF_ERR_CAPTURE; attention entry points refuse bucket or B1*N above 1024. */
+ * 9: SF_ERR_CAPTURE; attention entry points refuse bucket or B1*N above 1024.
+ * 10: sf_head_logits (the head with the Fast-dLLM shift); sf_lm_head runs on it. */
 int sf_abi_version(void);
 
 /*
@@ -262,11 +263,12 @@ int sf_kv_append(const uint16_t* kv_buf, int row0, int n_tok, int Hkv, int hd, u
  * sf_qkv_rope), summed in a fixed order by a fix-up kernel (deterministic).
  * Calls sharing a workspace must not overlap.
  *
- * sf_o_proj_residual, sf_o_proj_post_norm and sf_lm_head apply the weight to every
- * row instead (M = B1·N): one pass over the weights for up to 256 rows, the
- * workgroups splitting the columns and, for o_proj, K into up to 16 ranges whose
- * fp32 sums go to a caller workspace of sf_o_proj_workspace_bytes(M, N, K) bytes
- * and are added in range order by the residual kernel (deterministic).
+ * sf_o_proj_residual and sf_o_proj_post_norm apply the weight to every row
+ * instead (M = B1·N): one pass over the weights for up to 256 rows, the
+ * workgroups splitting the columns and K into up to 16 ranges whose fp32 sums go
+ * to a caller workspace of sf_o_proj_workspace_bytes(M, N, K) bytes and are added
+ * in range order by the residual kernel (deterministic).  sf_head_logits (and
+ * sf_lm_head) too, each workgroup over the whole of K (no workspace).
  *
  * sf_pack_weight        out = packed(w), w row-major [N, K]; N % 16 == 0, K % 64 == 0
  * sf_o_proj_residual    hp[r] = bf16(x[r] + bf16(o_bf[r] . Wo^T)), r < M (all rows)
@@ -310,6 +312,26 @@ int sf_residual_gather_add(const uint16_t* hp, const uint16_t* ffn, const int32_
                            int N, int D, uint16_t* out, void* stream);
 int sf_lm_head(const uint16_t* x, int M, const uint16_t* w, int D, int V, uint16_t* logits,
                void* stream);
+
+/*
+ * (8) Output head of the verify step, with Fast-dLLM's logit shift in its stores.
+ * logits = x . Wlm^T for the M rows of x (the final-norm hidden states of the
+ * B1·N block rows), Wlm [V, D] packed by sf_pack_weight, bf16 out, fp32
+ * accumulation over D in one fixed order (a row's logits do not depend on M or on
+ * the other rows).  shift_n = 0: row m goes to logits row m (NLD,
+ * specfold/generate/nld_folded.py:237; sf_lm_head is this with ld_out = V).
+ * shift_n = N: x holds blocks of N rows and the output is the reference's
+ * _shift_logits(lm_head(norm(h))) (specfold/generate/fastdllm_v2_generation.py:
+ * 121-126 applied to specfold/generate/fastdllm_v2_folded.py:222-223): row (b, n)
+ * is stored at (b, n + 1), row (b, 0) at (b, 0) and (b, 1), row (b, N - 1) not at
+ * all.  Replaces lm_head + _shift_logits, a library GEMM and a copy of the logits.
+ * ld_out: the logits row stride in elements (>= V, a multiple of 4).  No workspace.
+ * Limits: 1 <= M <= 1024 (one pass over the weights per 256 rows), D % 64 == 0,
+ * V % 128 == 0, shift_n == 0 or (shift_n >= 2 and M % shift_n == 0); x and w
+ * 16-byte aligned, logits 8-byte aligned.
+ */
+int sf_head_logits(const uint16_t* x, int M, const uint16_t* w, int D, int V, int shift_n,
+                   uint16_t* logits, long long ld_out, void* stream);
 
 /* ---- greedy decoding statistics of logits rows ----------------------------------
  * Replaces, at temperature 0, the top-p sampler of the reference decode loop

@@ -66,6 +66,7 @@ SIGNATURES = {
     "sf_ffn_down_scatter": (_i, [_vp, _vp, _i, _vp, _vp, _i, _i, _vp, _vp, _sz, _vp]),
     "sf_residual_gather_add": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _vp]),
     "sf_lm_head": (_i, [_vp, _i, _vp, _i, _i, _vp, _vp]),
+    "sf_head_logits": (_i, [_vp, _i, _vp, _i, _i, _i, _vp, _ll, _vp]),
     "sf_logit_stats_workspace_bytes": (ctypes.c_size_t, [_i]),
     "sf_parent_map": (_i, [_vp, _i, _i, _vp, _vp, _vp]),
     "sf_logit_stats": (_i, [_vp, _i, _i, _ll, _f] + [_vp] * 7 + [_vp, ctypes.c_size_t, _vp]),
@@ -506,6 +507,21 @@ def lm_head(x, M, w, D, V, logits, stream=None) -> None:
     _need(logits, "logits", torch.bfloat16, min_numel=M * V)
     st = load().sf_lm_head(_ptr(x), M, _ptr(w), D, V, _ptr(logits), _stream(stream))
     _check(st, "sf_lm_head")
+
+
+def head_logits(x, M, w, D, V, logits, shift_n: int = 0, stream=None) -> None:
+    """logits [M, V] (row stride logits.stride(0)) = x [M, D] . W^T with W packed
+    [V, D]; shift_n = N: Fast-dLLM's shift of N-row blocks in the stores
+    (sf_head_logits)."""
+    _need(x, "x", torch.bfloat16, min_numel=M * D)
+    _need(w, "w", torch.bfloat16, numel=V * D)
+    ld = logits.stride(0) if logits.dim() == 2 else V
+    if logits.dtype != torch.bfloat16 or logits.stride(-1) != 1 or \
+            logits.storage_offset() + (M - 1) * ld + V > logits.untyped_storage().nbytes() // 2:
+        raise ValueError(f"logits must be bf16 rows of stride {ld} holding {M} x {V}")
+    st = load().sf_head_logits(_ptr(x), M, _ptr(w), D, V, int(shift_n), _ptr(logits), ld,
+                               _stream(stream))
+    _check(st, "sf_head_logits")
 
 
 class LogitStats:

@@ -523,14 +523,3 @@ extern "C" int sf_residual_gather_add(const uint16_t* hp, const uint16_t* ffn, c
   return sf_launch_status();
 }
 
-extern "C" int sf_lm_head(const uint16_t* x, int M, const uint16_t* w, int D, int V,
-                          uint16_t* logits, void* stream) {
-  if (!x || !w || !logits) return SF_ERR_ARG;
-  if (M < 1 || M > 1024 || D < kKC || D % kKC || V < 128 || V % 128 || !aligned16(x) ||
-      !aligned16(w) || !aligned16(logits))
-    return SF_ERR_SHAPE;
-  // 128-column tiles, the whole K per workgroup (no partial buffer)
-  launch_rows<2, kRowsBf16>(x, M, w, D, V, 1, nullptr, logits,
-                            reinterpret_cast<hipStream_t>(stream));
-  return sf_launch_status();
-}

@@ -1,0 +1,281 @@
+// The verify step's output head: logits of every row of the block in one pass
+// over the head weights, with Fast-dLLM's shift done by the stores.
+//
+// Reference semantics:
+//   specfold/generate/fastdllm_v2_folded.py:222-223   logits = lm_head(norm(h))
+//   specfold/generate/fastdllm_v2_generation.py:121-126  _shift_logits: position n
+//       of a block takes position n-1's logits, position 0 keeps its own
+//   specfold/generate/nld_folded.py:237                 NLD: unshifted
+// (the Triton path, fastdllm_v2_folded.py:365-366, runs the same torch ops).
+//
+// logits[m, v] = sum_k X[m, k] W[v, k] for M <= 256 rows per pass (B1·N = 256 at
+// B1 = 8) and V = 131k-152k columns: 256 flop per weight byte, so the head is
+// bound by streaming W (1.09 GB at 7B) unless the MFMAs fall below ~60% of their
+// peak.  Design (one 8-wave workgroup per CU, one 128-column tile per workgroup,
+// the whole of K):
+//   * the weights go from HBM straight into VGPRs: wave w = (row group rg, column
+//     group cg) owns WN = 2 tiles of 16 columns; in the packed layout
+//     (sf_pack_weight) a tile's 32-K chunk is one contiguous 1 KB block, so each
+//     weight load is a fully used 1 KB read, and a wave's stream is sequential.
+//     The two row groups load the same blocks (the second read hits L2).  Three
+//     64-K stages of weights are in flight per wave (48 VGPRs);
+//   * the rows X are shared by the 8 waves: each 64-K stage (256 rows x 64 K,
+//     32 KB) goes to an LDS ring of 4 stages by direct global -> LDS copies (X is
+//     1.8 MB and stays in L2), XOR-swizzled so the fragment reads are
+//     conflict-free (the A-tile layout of the other GEMMs: sf_index.h);
+//   * v_mfma_f32_16x16x32_bf16 with the weight fragment as the first operand, so
+//     each lane ends with 4 consecutive columns of one row (8-byte stores);
+//   * the store's row map does the shift: row (b, n) goes to output row
+//     (b, n + 1), row (b, 0) also to (b, 0), row (b, N - 1) nowhere.
+// Each 64-K stage per wave: 4 A copies + 4 weight loads issued, 16 A fragment
+// reads, 32 MFMAs.  fp32 accumulation over the whole of K in one order (K
+// ascending), so a row's logits do not depend on the other rows or on M.
+#include <type_traits>
+
+#include "sf_common.h"
+#include "sf_index.h"
+
+namespace {
+
+using namespace sfg;
+
+constexpr int kHRows = 256;                  // rows per pass: 16 m tiles of 16
+constexpr int kHMT = kHRows / 16;
+constexpr int kHStageWords = 2 * kHMT * 64;  // 16-byte words of X per stage (32 KB)
+
+// A workgroup of NW waves = RG row groups x NW / RG column groups of WN 16-column
+// tiles; TN columns per workgroup tile; a ring of R 64-K stages (X in LDS, each
+// wave's weight fragments in VGPRs), R - 1 of them in flight.
+template <int NW, int RG, int WN, int R>
+struct HeadShape {
+  static constexpr int kRing = R;
+  static constexpr int kCG = NW / RG;              // column groups
+  static constexpr int kNMT = kHMT / RG;           // m tiles per wave
+  static constexpr int kTN = kCG * WN * 16;        // columns of a tile
+  static constexpr int kDA = 2 * kHMT / NW;        // X copies per wave per stage
+  static constexpr int kDB = 2 * WN;               // weight loads per wave per stage
+  static_assert(kDA * NW == 2 * kHMT, "the X copies of a stage divide over the waves");
+  // X fragments read (and waited for) FG m tiles at a time: 4 where the
+  // accumulators leave no room for 8
+  static constexpr int kFG = kNMT * WN >= 32 ? 4 : 8;
+  static_assert(kNMT % kFG == 0, "whole fragment groups");
+};
+// The whole rounds: 4 waves (one per SIMD, 512 registers each: 256 accumulators,
+// three 64-K stages of weight fragments) x 64 columns over all 256 rows -- each
+// weight byte loaded by one wave, 64 KB of weights in flight per CU.
+using HeadMain = HeadShape<8, 1, 2, 3>;
+// The partial last round: 8 waves = 2 row groups x 4 column groups of 32 columns
+// (each weight block loaded by both row groups), 128-column tiles spread over
+// twice as many CUs.
+using HeadTail = HeadShape<8, 2, 2, 4>;
+
+// The X fragments of FG consecutive m tiles (1 KB apart) from LDS byte address a,
+// without waiting (sf_lds_read16 with compile-time offsets).
+template <int FG, int I = 0>
+SF_DEV void head_fragments(sf_u32x4 (&f)[FG], sf_lds_off a) {
+  if constexpr (I < FG) {
+    f[I] = sf_lds_read16<I * 1024>(a);
+    head_fragments<FG, I + 1>(f, a);
+  }
+}
+
+// Calls f(sb + J, J) for J = J0 .. R-1 (with J a compile-time constant, so every
+// ring index below stays static), or only for sb + J < S when TAIL.
+template <int J, int R, bool TAIL, class F>
+SF_DEV void head_stages(int sb, int S, F& f) {
+  if constexpr (J < R) {
+    if (!TAIL || sb + J < S) f(sb + J, std::integral_constant<int, J>{});
+    head_stages<J + 1, R, TAIL>(sb, S, f);
+  }
+}
+
+// Output row of block row m_glob, or -1: shift_n = 0 stores every row in place;
+// shift_n = N > 0 (Fast-dLLM) moves row (b, n) of each N-row block to (b, n + 1)
+// and drops (b, N - 1); (b, 0) is also stored in place (`second`).
+SF_DEV int head_row(int m_glob, int shift_n, bool second) {
+  if (shift_n == 0) return second ? -1 : m_glob;
+  const int n = m_glob % shift_n;
+  if (second) return n == 0 ? m_glob : -1;
+  return n == shift_n - 1 ? -1 : m_glob + 1;
+}
+
+// One pass of at most 256 rows over the column tiles t0 + blockIdx.x of TN
+// columns.  X: this pass's rows (row stride K); m0: the pass's first row in the
+// block (for the shift); W: packed [V, K]; out: row stride ldo, indexed by block
+// row.
+template <int NW, int RG, int WN, int R>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(8 / NW, 8 / NW)))
+void head_kernel(const uint16_t* __restrict__ X, int M, int m0, const uint16_t* __restrict__ W,
+                 int K, int t0, int shift_n, uint16_t* __restrict__ out, long long ldo) {
+  using Sh = HeadShape<NW, RG, WN, R>;
+  constexpr int kHDA = Sh::kDA;
+  constexpr int kHDB = Sh::kDB;
+  constexpr int kHWN = WN;
+  __shared__ sf_u32x4 ring[R * kHStageWords];
+  constexpr int CG = Sh::kCG;
+  constexpr int NMT = Sh::kNMT;
+  constexpr int TN = Sh::kTN;
+  constexpr int FG = Sh::kFG;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  // the wave index in a scalar register: the copies' LDS bases (M0) are then
+  // wave-uniform for the compiler too
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rg = wv / CG;
+  const int cg = wv - rg * CG;
+  const int t = t0 + blockIdx.x;
+  const int S = K / kKC;
+  const int slast = S - 1;
+
+  // X copies: copy q = wv + NW*j is (chunk q / 16, m tile q % 16); lane L brings
+  // row L/4 of the tile (rows past M re-read row M - 1), unit a_copy_unit(L)
+  const uint16_t* asrc[kHDA];
+  int adst[kHDA];
+#pragma unroll
+  for (int j = 0; j < kHDA; ++j) {
+    const int q = wv + NW * j;
+    const int ch = q / kHMT, mt = q - ch * kHMT;
+    const int r = sf_imin(mt * 16 + (lane >> 2), M - 1);
+    asrc[j] = X + (size_t)r * K + ch * 32 + a_copy_unit(lane) * 8;
+    adst[j] = (ch * kHMT + mt) * 64;
+  }
+  // this lane's weight streams: 16-column tiles t*TN/16 + cg*WN + tt
+  const uint16_t* wsrc[kHWN];
+#pragma unroll
+  for (int tt = 0; tt < kHWN; ++tt)
+    wsrc[tt] = weight_lane_ptr(W, t * (TN / 16) + cg * kHWN + tt, K, lane);
+
+  // Issues are made for consecutive stages s = 0, 1, ...; the stream pointers
+  // advance one stage after each issue until they reach the last stage, so an
+  // issue past it re-reads the last stage (clamped) and one pointer per stream
+  // stays live (no per-issue address arithmetic).
+  sf_u32x4 wreg[R][2][kHWN];   // the weight fragments of the R - 1 stages in flight
+  auto issue = [&](int s, int j) {
+    sf_u32x4* sl = ring + j * kHStageWords;
+#pragma unroll
+    for (int q = 0; q < kHDA; ++q) sf_lds_dma16(asrc[q], sl + adst[q]);
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int tt = 0; tt < kHWN; ++tt)
+        wreg[j][c][tt] = *reinterpret_cast<const sf_u32x4*>(wsrc[tt] + c * kKsStride);
+    // advance unless this was the last stage (a select, not a branch)
+    const int live = s < slast ? 1 : 0;
+#pragma unroll
+    for (int q = 0; q < kHDA; ++q) asrc[q] += live * kKC;
+#pragma unroll
+    for (int tt = 0; tt < kHWN; ++tt) wsrc[tt] += live * (2 * kKsStride);
+  };
+#pragma unroll
+  for (int j = 0; j < R - 1; ++j) issue(j, j);
+
+  sf_f32x4 acc[NMT][kHWN];
+#pragma unroll
+  for (int i = 0; i < NMT; ++i)
+#pragma unroll
+    for (int tt = 0; tt < kHWN; ++tt) acc[i][tt] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // this lane's X fragment of m tile rg*NMT + i in chunk c: word a_read_word(lane)
+  // of tile (c, rg*NMT + i)
+  const sf_lds_off a_byte = (sf_lds_off)((rg * NMT) * 64 + a_read_word(lane)) * 16;
+  // stage s in ring slot j: wait for it (issued R - 1 stages ago: its X copies of
+  // every wave -- the barrier -- and this wave's weights; no wave still reads slot
+  // j - 1), issue stage s + R - 1 into slot j - 1, then its MFMAs, FG m tiles at
+  // a time.  Every m tile is computed (rows past M are copies of row M - 1, never
+  // stored): no branch in the loop, so the compiler's waits stay exact.
+  auto stage = [&](int s, auto jc) {
+    constexpr int j = decltype(jc)::value;
+    sf_wait_vm_barrier<(R - 2) * (kHDA + kHDB)>();
+    issue(s + R - 1, (j + R - 1) % R);
+    const sf_lds_off base = sf_lds_addr(ring + j * kHStageWords);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+#pragma unroll
+      for (int h = 0; h < NMT / FG; ++h) {
+        sf_u32x4 f[FG];
+        const sf_lds_off a = base + a_byte + (c * kHMT + h * FG) * 1024;
+        head_fragments<FG>(f, a);
+        sf_lds_reads_done(f);
+#pragma unroll
+        for (int i = 0; i < FG; ++i)
+#pragma unroll
+          for (int tt = 0; tt < kHWN; ++tt)
+            acc[h * FG + i][tt] = sf_mfma16x16x32(sf_as_bf16x8(wreg[j][c][tt]),
+                                                  sf_as_bf16x8(f[i]), acc[h * FG + i][tt]);
+      }
+    }
+  };
+  int sb = 0;
+#pragma unroll 1
+  for (; sb + R <= S; sb += R)   // whole groups of R stages: no branch inside
+    head_stages<0, R, false>(sb, S, stage);
+  head_stages<0, R, true>(sb, S, stage);   // the last S % R (wave-uniform branches, once)
+  // drain the clamped re-issues past the last stage before the workgroup exits
+  sf_wait_vm_barrier<0>();
+
+  // lane: row rg*128*(RG-1) + 16 i + lane%16 of the pass, columns col0 + 16 tt .. +4
+  const int col0 = t * TN + cg * kHWN * 16 + (lane >> 4) * 4;
+#pragma unroll
+  for (int i = 0; i < NMT; ++i) {
+    const int row = (rg * NMT + i) * 16 + (lane & 15);
+    if (row < M) {
+      sf_u32x2 v[kHWN];
+#pragma unroll
+      for (int tt = 0; tt < kHWN; ++tt) {
+        v[tt][0] = sf_pack2(acc[i][tt][0], acc[i][tt][1]);
+        v[tt][1] = sf_pack2(acc[i][tt][2], acc[i][tt][3]);
+      }
+#pragma unroll
+      for (int second = 0; second < 2; ++second) {
+        const int orow = head_row(m0 + row, shift_n, second != 0);
+        if (orow >= 0) {
+#pragma unroll
+          for (int tt = 0; tt < kHWN; ++tt)
+            *reinterpret_cast<sf_u32x2*>(out + (size_t)orow * ldo + col0 + tt * 16) = v[tt];
+        }
+      }
+    }
+  }
+}
+
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+}  // namespace
+
+extern "C" int sf_head_logits(const uint16_t* x, int M, const uint16_t* w, int D, int V,
+                              int shift_n, uint16_t* logits, long long ld_out, void* stream);
+
+extern "C" int sf_lm_head(const uint16_t* x, int M, const uint16_t* w, int D, int V,
+                          uint16_t* logits, void* stream) {
+  return sf_head_logits(x, M, w, D, V, 0, logits, V, stream);
+}
+
+extern "C" int sf_head_logits(const uint16_t* x, int M, const uint16_t* w, int D, int V,
+                              int shift_n, uint16_t* logits, long long ld_out, void* stream) {
+  if (!x || !w || !logits) return SF_ERR_ARG;
+  if (M < 1 || M > 1024 || D < kKC || D % kKC || V < HeadTail::kTN || V % HeadTail::kTN ||
+      ld_out < V ||
+      ld_out % 4 || !aligned16(x) || !aligned16(w) || reinterpret_cast<uintptr_t>(logits) % 8)
+    return SF_ERR_SHAPE;
+  if (shift_n < 0 || shift_n == 1 || (shift_n > 0 && M % shift_n)) return SF_ERR_SHAPE;
+
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  // whole rounds of 256-column tiles (one per CU), the rest in 128-column tiles
+  // (the partial last round spread over up to twice the CUs)
+  constexpr int kCUs = 256;
+  const int t_main = V / HeadMain::kTN;
+  const int n_main = (t_main / kCUs) * kCUs;
+  const int n_rest = (V - n_main * HeadMain::kTN) / HeadTail::kTN;
+  for (int m0 = 0; m0 < M; m0 += kHRows) {
+    const int mb = sf_imin(kHRows, M - m0);
+    const uint16_t* xp = x + (size_t)m0 * D;
+    if (n_main)
+      hipLaunchKernelGGL((head_kernel<8, 1, 2, 3>), dim3(n_main), dim3(8 * 64), 0, st, xp, mb,
+                         m0, w, D, 0, shift_n, logits, ld_out);
+    if (n_rest)
+      hipLaunchKernelGGL((head_kernel<8, 2, 2, 4>), dim3(n_rest), dim3(8 * 64), 0, st, xp, mb,
+                         m0, w, D, n_main * (HeadMain::kTN / HeadTail::kTN), shift_n, logits,
+                         ld_out);
+  }
+  return sf_launch_status();
+}

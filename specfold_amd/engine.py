@@ -19,8 +19,10 @@ fastdllm_v2_folded.py:296-361 for the launch sequence, :117-220 for the math):
   sf_ffn_gate_up      gate/up GEMM + SiLU*mul on compacted rows  (HIP)
   sf_ffn_down_scatter down GEMM, scattered to the per-row FFN table (HIP)
 and after the last layer the residual update + final RMSNorm (HIP) and the
-lm_head (hipBLASLt; sf_lm_head stays in the C ABI).  sf_chain_correct (the reference's incremental form of the
-folded rows' attention) stays in the C ABI; the engine forms it with sf_attn_rows.
+head (HIP, sf_head_logits: one pass over the packed head weights for every row,
+with Fast-dLLM's logit shift done by its stores when asked for).  sf_chain_correct
+(the reference's incremental form of the folded rows' attention) stays in the C
+ABI; the engine forms it with sf_attn_rows.
 
 Nothing here syncs with the host: the branch parent map is computed from the
 tokens on the device (sf_parent_map; the reference copies the tokens to the host
@@ -252,6 +254,15 @@ class FoldedVerifyEngine:
                                      _lib.pack_weight(m.up_proj.weight.contiguous()),
                                      _lib.pack_weight(m.down_proj.weight.contiguous())))
             self._packed_o.append(_lib.pack_weight(a.o_proj.weight.contiguous()))
+        # the head, packed once; zero rows pad it to whole 128-column tiles of the
+        # head kernel (their logit columns are never returned)
+        self.V_pad = -(-self.V // 128) * 128
+        w = head.weight.contiguous()
+        if self.V_pad != self.V:
+            w = torch.cat([w, w.new_zeros(self.V_pad - self.V, self.D)])
+        self._packed_head = _lib.pack_weight(w)
+        del w
+        self.head_kernel = "hip"
         self._bufs: Dict[Tuple[int, int, int], _Buffers] = {}
         # HIP graphs of the layer loop, keyed by shape / prefix / delta / cache
         # (one per branch count the decode loop visits, B1 = 1..8, per sequence's
@@ -262,15 +273,19 @@ class FoldedVerifyEngine:
         self._rope: Optional[Tuple[torch.Tensor, torch.Tensor]] = None
         self._mirror: Optional[ContiguousMirror] = None   # reference-style caches
 
-    def lm_head(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """logits = x . Wlm^T for every row of x [M, D] (bf16; a fresh tensor unless
-        ``out`` is given), on hipBLASLt: at M = 256 rows the head does 256 flop per
-        weight byte, near the MFMA/HBM ridge, where the library's tiles run 302 us at
-        the 7B shape against 368 us for sf_lm_head's all-rows kernel."""
+    def lm_head(self, x: torch.Tensor, out: Optional[torch.Tensor] = None,
+                shift_n: int = 0) -> torch.Tensor:
+        """logits [M, V] = x . Wlm^T for every row of x [M, D] (sf_head_logits on the
+        packed head weights; ``out``: an [M, V_pad] bf16 buffer, else a fresh one).
+        shift_n = N: x holds blocks of N rows and the result is Fast-dLLM's shifted
+        logits (row (b, n) takes row (b, n - 1)'s logits, row (b, 0) its own;
+        fastdllm_v2_generation.py:121-126), written so by the head's stores.  A view of
+        V columns (rows of V_pad elements, contiguous when V % 128 == 0)."""
         M = x.shape[0]
         if out is None:
-            out = torch.empty(M, self.V, dtype=torch.bfloat16, device=self.device)
-        return torch.mm(x, self.head.weight.t(), out=out)
+            out = torch.empty(M, self.V_pad, dtype=torch.bfloat16, device=self.device)
+        _lib.head_logits(x, M, self._packed_head, self.D, self.V_pad, out, shift_n=shift_n)
+        return out[:, :self.V]
 
     @staticmethod
     def _check_device(device: torch.device) -> None:
@@ -314,8 +329,10 @@ class FoldedVerifyEngine:
                 trace: Optional[list] = None,
                 teacher: Optional[Dict[int, torch.Tensor]] = None,
                 stats: Optional[StepStats] = None,
-                causal: bool = False) -> Optional[torch.Tensor]:
-        """Verify step -> logits [B1, N, V] (unshifted), or None if not compute_logits.
+                causal: bool = False, shift: bool = False) -> Optional[torch.Tensor]:
+        """Verify step -> logits [B1, N, V] (unshifted, or with ``shift`` Fast-dLLM's
+        shifted logits, fastdllm_v2_generation.py:121-126, from the head's stores), or
+        None if not compute_logits.
 
         batched_input  [B1, N] int64 on the model's device; row 0 = main branch.
         cache          PagedKVCache, a reference-style per-layer (k, v) cache, or None.
@@ -377,13 +394,13 @@ class FoldedVerifyEngine:
                            bucket, BN)
             return self.forward(batched_input, cache, delta, bucket=BN,
                                 compute_logits=compute_logits, q_scale=q_scale, trace=trace,
-                                teacher=teacher, stats=stats, causal=causal)
+                                teacher=teacher, stats=stats, causal=causal, shift=shift)
         self.last_hidden = hidden
         self._last = dict(B1=B1, N=N, bucket=bucket, cache=cache, par=buf.par, q_scale=qs,
-                          hidden=hidden, delta=delta)
+                          hidden=hidden, delta=delta, shift=shift)
         if not compute_logits:
             return None
-        return self.lm_head(buf.final).view(B1, N, self.V)
+        return self.lm_head(buf.final, shift_n=N if shift else 0).view(B1, N, self.V)
 
     @torch.no_grad()
     def forward_batched(self, blocks: List[torch.Tensor], caches: list, delta: float = 0.1,
@@ -391,7 +408,8 @@ class FoldedVerifyEngine:
                         q_scales: Optional[List[Optional[torch.Tensor]]] = None,
                         stats: Optional[StepStats] = None, compute_logits: bool = True,
                         pad_to: Optional[int] = None,
-                        trace: Optional[list] = None) -> Optional[List[torch.Tensor]]:
+                        trace: Optional[list] = None,
+                        shift: bool = False) -> Optional[List[torch.Tensor]]:
         """One verify step over several independent sequences -> per-sequence logits
         [B1_s, N, V] (unshifted).
 
@@ -413,7 +431,8 @@ class FoldedVerifyEngine:
         ``forward`` on it alone.  No counterpart in the reference, whose verify step
         takes one sequence.  ``stats`` counts every recomputed row, padded ones
         included.  ``trace``: as in ``forward``, one dict per layer of the stacked
-        step's buffers (runs eagerly)."""
+        step's buffers (runs eagerly).  ``shift``: Fast-dLLM's shifted logits, as in
+        ``forward``."""
         if not blocks or len(blocks) != len(caches):
             raise ValueError("forward_batched needs one cache (or None) per token block")
         if q_scales is not None and len(q_scales) != len(blocks):
@@ -464,11 +483,11 @@ class FoldedVerifyEngine:
                 trace.clear()
             return self.forward_batched(orig_blocks, caches, delta, bucket=BN, q_scales=q_scales,
                                         stats=stats, compute_logits=compute_logits,
-                                        pad_to=pad_to, trace=trace)
+                                        pad_to=pad_to, trace=trace, shift=shift)
         self.last_hidden = hidden
         if not compute_logits:
             return None
-        logits = self.lm_head(buf.final).view(B1, N, self.V)
+        logits = self.lm_head(buf.final, shift_n=N if shift else 0).view(B1, N, self.V)
         return [x[:r] for x, r in zip(logits.split(sizes, 0), real)]
 
     def _replay_batched(self, buf: _Buffers, tokens: torch.Tensor, sizes: List[int],
@@ -736,7 +755,8 @@ class FoldedVerifyEngine:
         if "scratch" not in shared:
             shared["scratch"] = torch.empty_like(buf.hid[0])
             shared["normed"] = torch.empty_like(buf.hid[0])
-            shared["logits"] = torch.empty(BN, self.V, dtype=torch.bfloat16, device=self.device)
+            shared["logits"] = torch.empty(BN, self.V_pad, dtype=torch.bfloat16,
+                                           device=self.device)
         scratch, normed, logits = shared["scratch"], shared["normed"], shared["logits"]
 
         def gate():
@@ -779,7 +799,7 @@ class FoldedVerifyEngine:
                                   self.eps, scratch, normed)
 
         def lm_head():
-            self.lm_head(buf.final, out=logits)
+            self.lm_head(buf.final, out=logits, shift_n=N if st.get("shift") else 0)
 
         out = dict(qkv=qkv, attn=attn, o_proj=o_proj, gate_up=gate_up, down=down,
                    final_norm=final_norm, lm_head=lm_head, gate=gate)

@@ -108,7 +108,7 @@ class SpecFoldHIPFastDLLMV2Generation(FastDLLMV2SpeculativeGeneration):
         prev_mode, eng.gate_mode = eng.gate_mode, self.gate_mode
         try:
             logits = eng.forward(batched_input, past_key_values, delta=self.delta, bucket=bucket,
-                                 stats=stats)
+                                 stats=stats, shift=True)
         finally:
             eng.gate_mode = prev_mode
         # fold counters stay on the device (no host sync per step)
@@ -118,7 +118,7 @@ class SpecFoldHIPFastDLLMV2Generation(FastDLLMV2SpeculativeGeneration):
         self._fold_draft_recomputed = rec if self._fold_draft_recomputed is None else \
             self._fold_draft_recomputed + rec
         self.last_stats = stats
-        return self._shift_logits(logits)
+        return logits      # shifted by the head's stores (_shift_logits, :121-126)
 
 
 # The reference's fused-path class name, so callers switch without code changes.

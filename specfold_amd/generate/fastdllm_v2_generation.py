@@ -100,9 +100,13 @@ class FastDLLMV2SpeculativeGeneration:
 
     # -- the seam ---------------------------------------------------------------------
     def _batched_block_forward(self, batched_input: torch.Tensor, past_key_values) -> torch.Tensor:
-        """Dense B+1-row block forward -> shifted logits [B+1, N, V] (:151-186)."""
-        out = self.model_executor.forward(batched_input, past_key_values=past_key_values,
-                                          use_cache=True, update_past_key_values=False)
+        """Dense B+1-row block forward -> shifted logits [B+1, N, V] (:151-186); an
+        executor with ``forward_shifted`` returns them shifted by its head's stores."""
+        ex = self.model_executor
+        if hasattr(ex, "forward_shifted"):
+            return ex.forward_shifted(batched_input, past_key_values)
+        out = ex.forward(batched_input, past_key_values=past_key_values,
+                         use_cache=True, update_past_key_values=False)
         return self._shift_logits(out.logits)
 
     # -- drafts -----------------------------------------------------------------------

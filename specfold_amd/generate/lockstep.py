@@ -87,6 +87,8 @@ class LockstepDecoder:
         chunks.append(cur)
         logits = [None] * len(requests)
         rec = None
+        # Fast-dLLM generators take shifted logits: the head's stores shift them
+        shifted = hasattr(g0, "_shift_logits")
         prev_mode, eng.gate_mode = eng.gate_mode, g0.gate_mode
         try:
             for idx in chunks:
@@ -98,6 +100,7 @@ class LockstepDecoder:
                     for i in idx)
                 out = eng.forward_batched([requests[i][0] for i in idx],
                                           [requests[i][1] for i in idx], delta=g0.delta,
+                                          shift=shifted,
                                           bucket=bucket, q_scales=[q_scales[i] for i in idx],
                                           stats=stats, pad_to=self.pad_to)
                 for i, x in zip(idx, out):
@@ -111,8 +114,7 @@ class LockstepDecoder:
         self.batched_steps += len(chunks) - 1      # rounds() counts one step per round
         self.draft_positions += (total - len(requests) * N) * eng.L
         self._recomputed = rec if self._recomputed is None else self._recomputed + rec
-        shift = getattr(g0, "_shift_logits", None)
-        return [shift(x) for x in logits] if shift is not None else logits
+        return logits
 
     def rounds(self, prompts: Sequence[torch.Tensor]):
         """Generator: one event per round, {"kind": "round", "committed": tokens

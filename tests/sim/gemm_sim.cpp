@@ -10,6 +10,8 @@
 //   sf_o_proj_post_norm the same hp, and zn[slot[r]] = bf16(w * bf16(hp[r] * rstd)) for
 //                       the rows with slot[r] >= 0
 //   sf_lm_head          logits[m] = bf16(x[m] . W^T), m < M
+//   sf_head_logits      the same, shifted: row (b, n) of each block to (b, n + 1),
+//                       (b, 0) kept, bit for bit the unshifted rows
 //   sf_qkv_rope         q / k / v of the recomputed rows: bias, RoPE from absolute
 //                       position tables, the optional q scale, scatter by flat row
 // A result may differ from the rounded float64 value where the fp32 sum (another
@@ -259,6 +261,36 @@ int main(int argc, char** argv) {
         cl.add(logits[(size_t)m * V + v], y, mag);
       }
     ok &= cl.report();
+
+    // the same head with Fast-dLLM's shift in the stores (sf_head_logits): blocks of
+    // sn rows, output row (b, n + 1) = row (b, n) of the unshifted logits bit for
+    // bit, row (b, 0) kept; into rows of stride V + 8 whose padding stays untouched
+    int sn = 0;
+    for (int c : {32, 16, 10, 8, 5, 4, 2})
+      if (M % c == 0) {
+        sn = c;
+        break;
+      }
+    if (sn) {
+      const int ld = V + 8;
+      std::vector<uint16_t> sh((size_t)M * ld, 0xBEEF);
+      if (sf_head_logits(x.data(), M, pl.data(), D, V, sn, sh.data(), ld, nullptr)) {
+        fprintf(stderr, "sf_head_logits failed\n");
+        return 1;
+      }
+      long bad = 0;
+      for (int m = 0; m < M; ++m) {
+        const int n = m % sn;
+        const int srow = n == 0 ? m : m - 1;
+        for (int v = 0; v < ld; ++v) {
+          const uint16_t want = v < V ? logits[(size_t)srow * V + v] : 0xBEEF;
+          bad += sh[(size_t)m * ld + v] != want;
+        }
+      }
+      printf("  %-22s %7ld outputs: %ld wrong (blocks of %d rows)\n", "head_logits shifted",
+             (long)M * ld, bad, sn);
+      ok &= bad == 0;
+    }
   }
   // ---- QKV projection + bias + RoPE (+ q scale) + scatter ----------------------------------
   // the reference's op sequence (fastdllm_v2_folded.py:151-161, nld_folded.py:173-174):

@@ -326,8 +326,9 @@ def test_fastdllm_lockstep_same_results():
 def test_lockstep_engine_glue():
     """The default batched forward of LockstepDecoder: one forward_batched call
     with every request, the executor's q scale per sequence where it has one,
-    padding to the draft graph's width, the generator's logit shift applied per
-    sequence, and the fold counters over real draft rows only."""
+    padding to the draft graph's width, the logit shift asked of the engine's head
+    exactly for generators that shift (Fast-dLLM), and the fold counters over real
+    draft rows only."""
     from specfold_amd.generate.lockstep import LockstepDecoder
 
     class Cache:
@@ -342,12 +343,15 @@ def test_lockstep_engine_glue():
     class Eng:
         L, gate_mode, device = 2, 0, torch.device("cpu")
 
-        def forward_batched(self, blocks, caches, delta, bucket, q_scales, stats, pad_to):
+        def forward_batched(self, blocks, caches, delta, bucket, q_scales, stats, pad_to,
+                            shift=False):
             calls.append(dict(blocks=blocks, caches=caches, delta=delta, bucket=bucket,
-                              q_scales=q_scales, pad_to=pad_to))
+                              q_scales=q_scales, pad_to=pad_to, shift=shift))
             stats.count_dev = torch.tensor([40, 36], dtype=torch.int32)
-            return [torch.arange(b.shape[0] * b.shape[1] * 3, dtype=torch.float32)
-                    .view(b.shape[0], b.shape[1], 3) for b in blocks]
+            out = [torch.arange(b.shape[0] * b.shape[1] * 3, dtype=torch.float32)
+                   .view(b.shape[0], b.shape[1], 3) for b in blocks]
+            # the engine's head shifts in its stores: the same values as the torch shift
+            return [torch.cat([x[:, :1], x[:, :-1]], 1) for x in out] if shift else out
 
     def gen(executor, shift):
         g = types.SimpleNamespace(_engine=Eng(), gate_mode=0, delta=0.2, fold_bucket=None,
@@ -367,6 +371,7 @@ def test_lockstep_engine_glue():
     out = dec.forward_many(list(zip(blocks, caches)))
     c = calls[-1]
     assert c["pad_to"] == 1 + n_drafts and c["delta"] == 0.2 and c["bucket"] is None
+    assert c["shift"] is False
     assert [float(q[0]) for q in c["q_scales"]] == [5.0, 70.0]
     assert torch.equal(out[0], torch.arange(72, dtype=torch.float32).view(3, 8, 3))
     assert dec.draft_positions == (4 - 2) * 8 * 2
@@ -376,7 +381,7 @@ def test_lockstep_engine_glue():
     ex2 = types.SimpleNamespace()
     dec2 = LockstepDecoder([gen(ex2, True), gen(ex2, True)])
     out2 = dec2.forward_many(list(zip(blocks, caches)))
-    assert calls[-1]["q_scales"] == [None, None]
+    assert calls[-1]["q_scales"] == [None, None] and calls[-1]["shift"] is True
     raw = torch.arange(72, dtype=torch.float32).view(3, 8, 3)
     assert torch.equal(out2[0], torch.cat([raw[:, :1], raw[:, :-1]], dim=1))
 

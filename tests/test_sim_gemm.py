@@ -3,8 +3,9 @@ sf_qkv.hip, sf_gemm_core.h) run on the CPU through the SIMT simulator of
 tests/sim, called through the library's entry points: weight packing, FFN
 gate/up (stream-K, SiLU epilogue from registers or in the fix-up), FFN down
 (stream-K with partial slots, fix-up, row scatter), o_proj + residual (+ the
-post-attention norm) and lm_head (all-rows GEMM, static row counts, one or two
-passes, one to three K ranges), and the QKV projection with bias, RoPE from
+post-attention norm), the head (sf_head.hip: weights straight into registers,
+rows through an LDS ring; one or two passes; unshifted, and with Fast-dLLM's
+shift in the stores, across a pass boundary inside a block), and the QKV projection with bias, RoPE from
 absolute-position tables, the optional q scale and the scatter by flat row, for
 row counts of one row up to two passes of 128 rows, against float64 dot products
 rounded as each epilogue specifies (tests/sim/gemm_sim.cpp states the
@@ -29,13 +30,13 @@ def _build(tmp_path_factory, extra=()):
     d = tmp_path_factory.mktemp("gemm_sim")
     # copies, so the sources' quoted includes of sf_common.h resolve to the
     # simulator's host header instead of the HIP one next to the originals
-    for f in ("sf_ffn.hip", "sf_qkv.hip", "sf_gemm_core.h", "sf_gemm_rows.h"):
+    for f in ("sf_ffn.hip", "sf_qkv.hip", "sf_head.hip", "sf_gemm_core.h", "sf_gemm_rows.h"):
         (d / f).write_text((CSRC / f).read_text())
     flags = ["-std=c++20", "-O2", "-Wno-unknown-attributes", "-Wno-psabi", f"-I{SIM}",
              f"-I{ROOT / 'include'}", f"-I{CSRC}", *extra]
     objs = []
     for src, obj in ((d / "sf_ffn.hip", d / "ffn.o"), (d / "sf_qkv.hip", d / "qkv.o"),
-                     (SIM / "gemm_sim.cpp", d / "drv.o")):
+                     (d / "sf_head.hip", d / "head.o"), (SIM / "gemm_sim.cpp", d / "drv.o")):
         lang = ["-x", "c++"] if src.suffix == ".hip" else []
         r = subprocess.run([cxx, *flags, *lang, "-c", str(src), "-o", str(obj)],
                            capture_output=True, text=True)
