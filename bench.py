@@ -51,9 +51,9 @@ def parse_args(argv=None):
     ap.add_argument("--kernel-iters", type=int, default=200)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--mode-b", action="store_true",
-                    help="also measure the verify step at a fold ratio near 0.62 (synthetic "
-                         "layer inputs; reported under 'mode_b')")
+    ap.add_argument("--no-mode-b", dest="mode_b", action="store_false",
+                    help="skip the verify step at a fold ratio near 0.62 (synthetic layer "
+                         "inputs; reported under 'mode_b', measured by default)")
     ap.add_argument("--lockstep", action="store_true",
                     help="a multi-sequence workload (cfg4) decodes its sequences in lockstep, "
                          "one batched verify step per round (a step = one round)")
@@ -158,6 +158,19 @@ def kernel_roofline(name, ms, w, R, B1, N, P):
             "hbm_gbps": round(by / s / 1e9, 2), "mfma_tflops": round(fl / s / 1e12, 3)}
 
 
+def roofline_entry(k: dict, name: str) -> dict:
+    """The bench line's roofline object for the dominant kernel: achieved and frac
+    from its average duration inside the verify step, the isolated
+    (back-to-back launches) figures kept beside."""
+    r = dict(k, kernel=name)
+    if "in_step_us" in k:
+        r.update(achieved=k["in_step_achieved"], frac=k["in_step_frac"],
+                 isolated_achieved=k["achieved"], isolated_frac=k["frac"],
+                 isolated_us=k["avg_us"], avg_us=k["in_step_us"],
+                 timing="HIP events around the kernel's launches inside an eager verify step")
+    return r
+
+
 # kernels launched once per verify step (the others once per layer)
 ONCE_PER_STEP = ("lm_head", "final_norm")
 
@@ -174,7 +187,9 @@ PMC_KERNELS = {
     "gate_up": ("sfg::gemm_sk_kernel<2, 2,", "?silu_fixup_kernel"),
     "down": ("sfg::gemm_sk_kernel<1, 1,", "down_fixup_kernel"),
     "final_norm": ("sf_gate_rows_kernel",),
-    "lm_head": (("Cijk_", "Custom_Cijk_"),),   # hipBLASLt's kernel names
+    # the head: the whole rounds' 256-column kernel, then (where V leaves a partial
+    # round) the 128-column one
+    "lm_head": ("head_kernel<8, 1,", "?head_kernel<8, 2,"),
     "gate": ("sf_gate_rows_kernel", "sf_gate_compact_kernel"),
 }
 
@@ -438,6 +453,78 @@ def kernel_table(w, eng, B1, N, kernel_iters):
     return kernels, P, R
 
 
+# The engine's calls into the library per entry point of the kernel table (the
+# entry points launched by FoldedVerifyEngine._run_layers and its head).
+IN_STEP_CALLS = {"gate": "fold_gate_residual", "qkv": "qkv_rope", "attn": "attn_rows",
+                 "o_proj": "o_proj_post_norm", "gate_up": "ffn_gate_up",
+                 "down": "ffn_down_scatter", "final_norm": "residual_rmsnorm",
+                 "lm_head": "head_logits"}
+
+
+def in_step_times(run_step, reps: int = 3) -> dict:
+    """Each entry point's average GPU time inside the verify step itself, next to
+    the kernels it runs between in the step: the step runs eagerly with HIP events
+    recorded on the launch stream right before and after every library call the
+    engine makes (its _lib functions wrapped for the duration), behind a GPU sleep
+    long enough that the host has queued the whole step before the GPU reaches it
+    (so the events bracket the kernels, not host launch gaps); the median time of
+    an empty event pair queued the same way is subtracted.  Returns {name:
+    {"in_step_us": mean - pair, "in_step_us_raw": mean, "launches": n}}."""
+    from specfold_amd import _lib
+    spans = {k: [] for k in IN_STEP_CALLS}
+    saved = {}
+    for name, fn in IN_STEP_CALLS.items():
+        orig = getattr(_lib, fn)
+        saved[fn] = orig
+
+        def wrapped(*a, _orig=orig, _name=name, **k):
+            s = torch.cuda.Event(enable_timing=True)
+            e = torch.cuda.Event(enable_timing=True)
+            s.record()
+            _orig(*a, **k)
+            e.record()
+            spans[_name].append((s, e))
+        setattr(_lib, fn, wrapped)
+    empty = []
+    try:
+        for _ in range(reps):
+            torch.cuda._sleep(200_000_000)      # ~0.1 s of GPU spin: the host runs ahead
+            run_step()
+            # the cost of an event pair itself, queued the same way: subtracted below
+            for _ in range(32):
+                s = torch.cuda.Event(enable_timing=True)
+                e = torch.cuda.Event(enable_timing=True)
+                s.record()
+                e.record()
+                empty.append((s, e))
+        torch.cuda.synchronize()
+    finally:
+        for fn, orig in saved.items():
+            setattr(_lib, fn, orig)
+    pair_us = statistics.median(s.elapsed_time(e) * 1e3 for s, e in empty)
+    out = {"_event_pair_us": round(pair_us, 3)}
+    for name, ev in spans.items():
+        if ev:
+            us = [s.elapsed_time(e) * 1e3 for s, e in ev]
+            out[name] = {"in_step_us": round(statistics.mean(us) - pair_us, 3),
+                         "in_step_us_raw": round(statistics.mean(us), 3), "launches": len(us)}
+    return out
+
+
+def with_in_step(kernels: dict, steps: dict, w, R, B1, N, P) -> None:
+    """Adds each kernel's in-step time and the roofline it gives beside the
+    isolated (back-to-back launch) figures of the table."""
+    for name, k in kernels.items():
+        st = steps.get(name)
+        if not st:
+            continue
+        rl = kernel_roofline(name, st["in_step_us"] / 1e3, w, R, B1, N, P)
+        k["in_step_us"] = st["in_step_us"]
+        k["in_step_us_raw"] = st["in_step_us_raw"]
+        k["in_step_frac"] = rl["frac"]
+        k["in_step_achieved"] = rl["achieved"]
+
+
 def mode_b(w, gen, batched, iters, kernel_iters):
     """The verify step at the reference's fold regime: every layer's input is
     replaced by synthetic hidden states in which branch i = its parent's +
@@ -470,10 +557,17 @@ def mode_b(w, gen, batched, iters, kernel_iters):
     counts = st.counts
     R = sum(counts) / len(counts)
     kernels, P, R_last = kernel_table(w, eng, B1, N, kernel_iters)
+    steps = in_step_times(lambda: eng.forward(batched, cache, w.delta, teacher=teacher,
+                                              q_scale=qs))
+    with_in_step(kernels, steps, w, R_last, B1, N, P)
     fold = 1 - (sum(counts) - len(counts) * N) / ((B1 - 1) * N * len(counts))
+    dominant = max((n for n in kernels if n != "append"),
+                   key=lambda n: kernels[n].get("in_step_us", kernels[n]["avg_us"])
+                   * kernels[n]["launches_per_step"])
     return {"verify_step_ms_eager": round(statistics.median(lat), 4),
             "recomputed_rows_mean": round(R, 2), "recomputed_rows_last_layer": R_last,
-            "fold_ratio": round(fold, 4), "prefix": P, "kernels": kernels,
+            "fold_ratio": round(fold, 4), "prefix": P,
+            "roofline": roofline_entry(kernels[dominant], dominant), "kernels": kernels,
             "data": "synthetic layer inputs (branch = parent + sigma N(0,1)), every layer"}
 
 
@@ -721,11 +815,21 @@ def main(argv=None) -> int:
     traffic = load_traffic(w.name)
     for name, k in kernels.items():
         k["traffic"] = traffic.get(name)
-    print(f"[bench] kernels {json.dumps({k: v['avg_us'] for k, v in kernels.items()})}",
+    # the same entry points inside the verify step (eager, events around each call)
+    eng.use_graphs = False
+    try:
+        steps = in_step_times(lambda: gen._batched_block_forward(batched, cache))
+    finally:
+        eng.use_graphs = True
+    with_in_step(kernels, steps, w, R_last, B1, N, P)
+    print(f"[bench] kernels isolated {json.dumps({k: v['avg_us'] for k, v in kernels.items()})}"
+          f"\n[bench] kernels in step "
+          f"{json.dumps({k: v.get('in_step_us') for k, v in kernels.items()})}",
           file=sys.stderr, flush=True)
-    # the dominant kernel: largest GPU time per verify step
+    # the dominant kernel: largest GPU time per verify step (in the step)
     dominant = max((n for n in kernels if n != "append"),
-                   key=lambda n: kernels[n]["avg_us"] * kernels[n]["launches_per_step"])
+                   key=lambda n: kernels[n].get("in_step_us", kernels[n]["avg_us"])
+                   * kernels[n]["launches_per_step"])
     copy = copy_calibration() if args.copy_calibration else None
 
     # tokens per sequence's decode step (a lockstep round steps every sequence)
@@ -776,8 +880,9 @@ def main(argv=None) -> int:
         "tokens_per_step": round(tokens_per_step, 4),
         "prefill_s": round(prefill_s, 3),
         "graph_warmup": {"graphs": warmed, "s": round(warm_s, 3)},
-        "roofline": dict(kernels[dominant], kernel=dominant),
+        "roofline": roofline_entry(kernels[dominant], dominant),
         "kernels": kernels,
+        "in_step_event_pair_us": steps.get("_event_pair_us"),
         "copy_calibration": copy,
         "cpu_baseline": cpu,
         "mode_b": mb,
