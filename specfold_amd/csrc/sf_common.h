@@ -115,6 +115,17 @@ SF_DEV void sf_lds_reads_done(sf_u32x4 (&v)[N]) {
 #pragma unroll
   for (int i = 0; i < N; ++i) asm volatile("" : "+v"(v[i]));
 }
+// The same, leaving the LATER youngest LDS reads in flight (s_waitcnt
+// lgkmcnt(LATER)): the reads of v were issued before those LATER.  Valid only where
+// LDS operations are the wave's only lgkmcnt traffic (LDS operations complete in
+// order; scalar memory loads would not).
+template <int LATER, int N>
+SF_DEV void sf_lds_reads_done_but(sf_u32x4 (&v)[N]) {
+  static_assert(LATER >= 0 && LATER < 16, "lgkmcnt is 4 bits");
+  asm volatile("s_waitcnt lgkmcnt(%0)" ::"i"(LATER) : "memory");
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+v"(v[i]));
+}
 // Transposing LDS read (ds_read_b64_tr_b16), untracked like sf_lds_read16: within
 // each group of 16 lanes, lane i receives the 4 16-bit elements
 //   out[i][k] = (8 bytes at the address of lane 4k + i/4)[i % 4],   k = 0..3,

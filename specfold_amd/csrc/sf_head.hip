@@ -188,21 +188,31 @@ void head_kernel(const uint16_t* __restrict__ X, int M, int m0, const uint16_t* 
     sf_wait_vm_barrier<(R - 2) * (kHDA + kHDB)>();
     issue(s + R - 1, (j + R - 1) % R);
     const sf_lds_off base = sf_lds_addr(ring + j * kHStageWords);
+    // the stage's NG = 2 chunks x NMT / FG fragment groups, software-pipelined:
+    // group g + 1's reads are issued before group g's wait, so the LDS latency of
+    // one group hides behind the MFMAs of the other
+    constexpr int NH = NMT / FG;
+    constexpr int NG = 2 * NH;
+    sf_u32x4 fb[2][FG];
+    auto group_addr = [&](int gi) {
+      return base + a_byte + ((gi / NH) * kHMT + (gi % NH) * FG) * 1024;
+    };
+    head_fragments<FG>(fb[0], group_addr(0));
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-#pragma unroll
-      for (int h = 0; h < NMT / FG; ++h) {
-        sf_u32x4 f[FG];
-        const sf_lds_off a = base + a_byte + (c * kHMT + h * FG) * 1024;
-        head_fragments<FG>(f, a);
-        sf_lds_reads_done(f);
-#pragma unroll
-        for (int i = 0; i < FG; ++i)
-#pragma unroll
-          for (int tt = 0; tt < kHWN; ++tt)
-            acc[h * FG + i][tt] = sf_mfma16x16x32(sf_as_bf16x8(wreg[j][c][tt]),
-                                                  sf_as_bf16x8(f[i]), acc[h * FG + i][tt]);
+    for (int gi = 0; gi < NG; ++gi) {
+      if (gi + 1 < NG) {
+        head_fragments<FG>(fb[(gi + 1) & 1], group_addr(gi + 1));
+        sf_lds_reads_done_but<FG>(fb[gi & 1]);
+      } else {
+        sf_lds_reads_done(fb[gi & 1]);
       }
+      const int c = gi / NH, h = gi % NH;
+#pragma unroll
+      for (int i = 0; i < FG; ++i)
+#pragma unroll
+        for (int tt = 0; tt < kHWN; ++tt)
+          acc[h * FG + i][tt] = sf_mfma16x16x32(sf_as_bf16x8(wreg[j][c][tt]),
+                                                sf_as_bf16x8(fb[gi & 1][i]), acc[h * FG + i][tt]);
     }
   };
   int sb = 0;

@@ -71,6 +71,8 @@ SF_DEV sf_u32x4 sf_lds_read16(sf_lds_off addr) {
 }
 template <int N>
 SF_DEV void sf_lds_reads_done(sf_u32x4 (&)[N]) {}
+template <int LATER, int N>
+SF_DEV void sf_lds_reads_done_but(sf_u32x4 (&)[N]) {}
 SF_DEV sf_lds_off sf_lds_addr(const void* p) { return reinterpret_cast<uintptr_t>(p); }
 SF_DEV uint32_t sf_lds_read4_now(sf_lds_off addr) {
   uint32_t v;
