@@ -180,7 +180,7 @@ ONCE_PER_STEP = ("lm_head", "final_norm")
 PMC_ORDER = ("qkv", "attn", "o_proj", "gate_up", "down", "final_norm", "lm_head", "gate")
 PMC_KERNELS = {
     "qkv": ("sfg::gemm_sk_kernel<1, 0,", "sf_qkv_epilogue_kernel"),
-    "attn": ("sf_attn_prefix_kernel", "sf_attn_prefix_merge_kernel", "sf_attn_finalize_kernel"),
+    "attn": ("sf_attn_prefix_kernel", "sf_attn_rows_kernel"),
     "o_proj": ("sfg::gemm_rows_kernel<", "part_residual_norm_kernel"),
     # the SiLU fix-up only follows a stream-K gate/up (narrow intermediates); "?" marks
     # a kernel taken when it is the next dispatch

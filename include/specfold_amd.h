@@ -67,7 +67,9 @@ const char* sf_status_string(int status);
  * 8: all-rows o_proj / lm_head: sf_o_proj_post_norm, sf_o_proj_workspace_bytes (the
  *    workspace of sf_o_proj_residual).
  * 9: SF_ERR_CAPTURE; attention entry points refuse bucket or B1*N above 1024.
- * 10: sf_head_logits (the head with the Fast-dLLM shift); sf_lm_head runs on it. */
+ * 10: sf_head_logits (the head with the Fast-dLLM shift); sf_lm_head runs on it.
+ * 11: attention merges each recomputed row's prefix partials in the kernel that
+ *     attends its rows: the workspace holds the range partials only; B1 <= 64. */
 int sf_abi_version(void);
 
 /*
@@ -178,9 +180,9 @@ int sf_qkv_rope_branches(const uint16_t* xn, const int32_t* rows, const int32_t*
  * P is then the capacity the grid and workspace are sized for (so one captured
  * graph serves a growing cache).  With prefix_len NULL, P is the length.
  * workspace: sf_attn_workspace_bytes(bucket, H, P) bytes, 16-byte aligned (scratch).
- * Limits: hd == 128, H % Hkv == 0, N <= 64, H/Hkv <= 8, B1*N <= 1024 and
- * bucket <= 1024 (else SF_ERR_SHAPE), P <= 32768, a page size of 16, 32, 64 or
- * 128 tokens (a page holds whole 16-key groups).
+ * Limits: hd == 128, H % Hkv == 0, N <= 64, H/Hkv <= 8, B1 <= 64, B1*N <= 1024
+ * and bucket <= 1024 (else SF_ERR_SHAPE), P <= 32768, a page size of 16, 32, 64
+ * or 128 tokens (a page holds whole 16-key groups).
  */
 size_t sf_attn_workspace_bytes(int bucket, int H, int P);
 int sf_attn_prefix_block(const uint16_t* q_buf, const uint16_t* kv_buf, const uint16_t* prefix_k,
@@ -195,7 +197,8 @@ int sf_attn_prefix_block(const uint16_t* q_buf, const uint16_t* kv_buf, const ui
  * (3)+(4) Attention of every row of branches [b_first, b_first + b_count): the
  * recomputed rows as sf_attn_prefix_block computes them, and each folded row
  * (b, n) from the query of its source row s = src[b*N+n]*N + n over the prefix
- * (s's merged prefix state) and branch b's own block keys -- the exact softmax
+ * (s's merged prefix state, merged once for s and every row it serves) and
+ * branch b's own block keys -- the exact softmax
  * over the branch's keys that the reference's chain correction reaches
  * incrementally (specfold/generate/fastdllm_v2_folded.py:164-204; Triton
  * specfold_flash_attn_gqa_kernel + specfold_chain_correction_gqa_kernel,
@@ -203,8 +206,8 @@ int sf_attn_prefix_block(const uint16_t* q_buf, const uint16_t* kv_buf, const ui
  * sf_attn_prefix_block + sf_chain_correct.  rows / count: the recomputed rows of
  * those branches (ascending; every folded row's source row among them).  A batched
  * step calls it once per sequence with that sequence's branch range and rows.
- * Same workspace and limits as sf_attn_prefix_block (B1*N <= 1024, bucket <=
- * 1024); no causal mode.
+ * Same workspace and limits as sf_attn_prefix_block (B1 <= 64, B1*N <= 1024,
+ * bucket <= 1024); no causal mode.
  */
 int sf_attn_rows(const uint16_t* q_buf, const uint16_t* kv_buf, const uint16_t* prefix_k,
                  const uint16_t* prefix_v, const int32_t* page_table, int P, int page_size,

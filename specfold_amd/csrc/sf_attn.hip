@@ -5,7 +5,7 @@
 // scores = (q . k) * scaling, m = max, Z = sum exp(s - m), O = sum exp(s - m) v / Z,
 // no mask) and the Triton kernel specfold/generate/triton_kernels.py:301-361.
 //
-// Three kernels (flash-decoding split over the prefix, then the branch blocks):
+// Two kernels (flash-decoding split over the prefix, then the branch blocks):
 //  * prefix (sf_attn_prefix_kernel): a persistent grid walks the active (query
 //    tile, range of 64-key prefix chunks, kv head) items; the item count follows
 //    the device-side row count and prefix length.  All recomputed rows x the G
@@ -19,12 +19,11 @@
 //    from registers, V^T comes from transposing LDS reads.  P is split into bf16
 //    hi + lo parts (two MFMAs), so P.V keeps ~16 mantissa bits, close to the
 //    reference's fp32 einsum.  Each item writes its (m, l, acc) partial.
-//  * merge (sf_attn_prefix_merge_kernel): one wave per (recomputed row, q-head)
-//    combines its range partials into one prefix state {acc, m, l}.
-//  * finalize (sf_attn_finalize_kernel): one workgroup per (branch, kv head, 8
-//    positions) attends every row of the branch - its own prefix state if it was
-//    recomputed, its source row's otherwise - over the branch's N block keys
-//    (gathered through src), on MFMA, and writes O, m and Z.
+//  * rows (sf_attn_rows_kernel): one workgroup per (recomputed row, kv head)
+//    merges the row's range partials into one prefix state per q-head and then
+//    attends every row that takes this row's query -- itself and the folded rows
+//    whose source it is -- over the prefix state and that row's own branch's N
+//    block keys (gathered through src), on MFMA, writing O, m and Z.
 // Softmax exponentials are exp2 of scores pre-scaled by log2(e) (one v_exp_f32
 // each); partial maxima stay in that base-2 domain and the emitted m is converted
 // back, so (m, Z) describe the natural-base softmax the reference computes.
@@ -454,253 +453,297 @@ sf_attn_prefix_kernel(
   }
 }
 
-// ---- prefix merge ----------------------------------------------------------------------
-// One wave per (recomputed row m, q-head): the nr range partials of its query are
-// combined into one prefix state {acc[128], m, l} (m in the scaled base-2 domain of
-// the partials) at state[m][q-head] (132 floats).  Lane l takes dims 2l, 2l+1 and
-// the (m, l) of range l (nr <= 64).
-constexpr int kStateFloats = kHD + 4;
+// ---- rows: the prefix merge and the block attention, per source row ---------------------
+// One 8-wave workgroup per (compacted row m, kv head h).  Its row r = rows[m] = (b, n)
+// was recomputed.  The nr range partials of its G q-heads are merged into one
+// prefix state {acc[128], m, l} per q-head (m in the scaled base-2 domain of the
+// partials), held in LDS: wave g merges q-head g, lane l dims 2l, 2l+1 and the
+// (m, l) of range l (nr <= 64).  Every row of position n that takes r's query --
+// r itself, and (FOLDED) each folded row (b', n) whose source is r, i.e.
+// src[b'*N + n] == b -- then attends with that query over the merged prefix and
+// over its own branch b''s N block keys (kv rows src[b'*N + j]*N + j).  For a
+// folded row this is the softmax over its own keys that the reference reaches by
+// chain correction (fastdllm_v2_folded.py:183-204: the old keys' terms swapped for
+// the new ones); the prefix part is the same for all of them, so it is merged once.
+// The waves deal those rows out (one each up to 8 branches): the G q-heads are the
+// columns of one 16-query MFMA tile (columns past G repeat q-head G - 1; their
+// results are dropped); block scores S^T = K Q^T with the K fragments read straight
+// from the kv rows, O^T += V^T P^T with the branch's V rows copied to the wave's own
+// LDS region for the transposing reads.
+// Latency: the row, the src table and the count are one round of loads; the
+// partials and the query go out as soon as the count is known; the first row's K
+// and V once the src table is in LDS, before the merge arithmetic.
+// FOLDED = false computes the listed rows only (each is its own and only row).
+constexpr int kRowsWaves = 8;
+constexpr int kRowsThreads = kRowsWaves * 64;
+constexpr int kMaxBucket = 1024;  // compacted rows, B1 * N <= 1024
+constexpr int kMaxB1 = 64;        // branches: one ballot covers them
 
-__global__ __launch_bounds__(256) void sf_attn_prefix_merge_kernel(
-    const int32_t* __restrict__ count_p, int bucket, int H, int Hkv,
-    const int32_t* __restrict__ p_len, int P_cap, int nr_cap, int qmax,
-    const float* __restrict__ ws_o, const float* __restrict__ ws_ml, float* __restrict__ state) {
+// The block K fragments (S^T tiles t of 16 keys, MFMA A operand: lane l holds key
+// 16t + l%16, dims 32 ds + 8 (l/16) .. +8) of kv head h for branch bd, straight from
+// the kv rows (keys past N repeat key N - 1, finite under their zero weights), and
+// the V rows of the branch by direct copies to the wave's LDS region sv (row r at
+// r * kRowBytes, 16-byte unit p holding logical unit v_unit(r, p); rows padded to
+// 64 rows the same way).  Lane L looks up the kv row of key L once;
+// the other lanes' rows come by shuffles, so the loads are not held up by a chain
+// of LDS reads.
+template <int NB>
+SF_DEV void row_kv_issue(const uint16_t* __restrict__ kv_buf, const int* s_src, int bd, int N,
+                         int Hkv, int h, sf_u32x4 (&kf)[NB / 16][4], uint8_t* sv) {
+  // every tile and copy of the NB-key block is issued whatever N is (keys past N
+  // repeat key N - 1), so the loads carry no branches and the compiler's wait
+  // counts after them stay exact
+  constexpr int NT = NB / 16, NC = NB / 4;
   const int lane = threadIdx.x & 63;
-  const int it = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int count = min(*count_p, bucket);
-  if (it >= count * H) return;
-  const int G = H / Hkv;
-  const int m = it / H, hq = it - m * H;
-  const int h = hq / G, g = hq - h * G;
-  const int P = p_len ? min(*p_len, P_cap) : P_cap;
-  const int nr = merge_ranges(P, count * G, Hkv);
-  const int qi = m * G + g;
-  constexpr int kB = 16;  // range partials loaded per round (clamped addresses)
-  float2 a[kB];
-  const float2 ml = lane < nr ? *reinterpret_cast<const float2*>(ws_ml + attn_slot(h, lane, qi, nr_cap, qmax) * 2)
-                              : make_float2(-INFINITY, 0.f);
+  const int grp = lane >> 4;
+  const size_t kvs = (size_t)2 * Hkv * kHD;
+  const int jl = sf_imin(lane, N - 1);
+  const int row_l = s_src[bd * N + jl] * N + jl;   // kv row of key lane (N <= 64)
+  int krow[NT], vrow[NC];
 #pragma unroll
-  for (int u = 0; u < kB; ++u)
-    a[u] = *reinterpret_cast<const float2*>(
-        ws_o + attn_slot(h, min(u, max(nr - 1, 0)), qi, nr_cap, qmax) * kHD + 2 * lane);
-  const float mm = sf_wave_max(ml.x);  // -inf only with no prefix key at all
-  const float w = (lane < nr && mm > -INFINITY) ? __builtin_amdgcn_exp2f(ml.x - mm) : 0.f;
-  const float l = sf_wave_sum(ml.y * w);
-  float2 acc = make_float2(0.f, 0.f);
-  for (int r0 = 0; r0 < nr; r0 += kB) {
-    if (r0 > 0) {
+  for (int t = 0; t < NT; ++t) krow[t] = __shfl(row_l, 16 * t + (lane & 15), 64);
 #pragma unroll
-      for (int u = 0; u < kB; ++u)
-        a[u] = *reinterpret_cast<const float2*>(
-            ws_o + attn_slot(h, min(r0 + u, nr - 1), qi, nr_cap, qmax) * kHD + 2 * lane);
-    }
+  for (int i = 0; i < NC; ++i) vrow[i] = __shfl(row_l, 4 * i + (lane >> 4), 64);
 #pragma unroll
-    for (int u = 0; u < kB; ++u) {
-      const float wr = __shfl(w, min(r0 + u, 63), 64);   // 0 past nr
-      acc.x = fmaf(wr, a[u].x, acc.x);
-      acc.y = fmaf(wr, a[u].y, acc.y);
-    }
+  for (int t = 0; t < NT; ++t) {
+    const uint16_t* kp = kv_buf + (size_t)krow[t] * kvs + h * kHD + grp * 8;
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds) kf[t][ds] = *reinterpret_cast<const sf_u32x4*>(kp + ds * 32);
   }
-  float* st = state + ((size_t)m * H + hq) * kStateFloats;
-  *reinterpret_cast<float2*>(st + 2 * lane) = acc;
-  if (lane == 0) *reinterpret_cast<float2*>(st + kHD) = make_float2(mm, l);
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int row = 4 * i + (lane >> 4);
+    const uint16_t* vp = kv_buf + (size_t)vrow[i] * kvs + (Hkv + h) * kHD;
+    sf_lds_dma16(vp + v_unit(row, lane & 15) * 8, sv + i * 1024);
+  }
 }
 
-// ---- finalize --------------------------------------------------------------------------
-// One 256-thread workgroup per (branch b, kv head h, 8 block positions): a row (b, n)
-// listed among the compacted rows takes its own query; any other (folded) row the
-// query of its source row s = src[b*N + n]*N + n (its nearest recomputing
-// ancestor's, which is listed).  Either attends over the prefix -- that query's
-// merged prefix state -- and branch b's own N block keys (kv rows
-// src[b*N + j]*N + j).  For a folded row this is the
-// softmax over its own keys that the reference reaches by chain correction
-// (fastdllm_v2_folded.py:183-204: the old keys' terms swapped for the new ones);
-// here it is formed directly, with the branch's block K/V staged once in LDS for all
-// its rows.  The 8 positions x G q-heads (<= 64 queries) are 4 tiles of 16, one per
-// wave; block scores S^T = K Q^T and O^T += V^T P^T on MFMA as in the prefix pass.
-// FOLDED = false computes the listed rows only.
-constexpr int kFinRows = 8;
-constexpr int kMaxBucket = 1024;  // compacted rows (B1 * N <= 1024)
-
-template <bool FOLDED>
-__global__ __launch_bounds__(256) void sf_attn_finalize_kernel(
+template <bool FOLDED, int NB>
+__global__ __launch_bounds__(kRowsThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+sf_attn_rows_kernel(
     const uint16_t* __restrict__ q_buf, const uint16_t* __restrict__ kv_buf,
     const int32_t* __restrict__ src, const int32_t* __restrict__ rows,
-    const int32_t* __restrict__ count_p, int bucket, int N, int b_first, int H, int Hkv,
-    float scale_log2, int causal, int has_prefix, const float* __restrict__ state,
+    const int32_t* __restrict__ count_p, int bucket, int B1, int N, int b_first, int b_count,
+    int H, int Hkv, float scale_log2, int causal, const int32_t* __restrict__ p_len, int P_cap,
+    int nr_cap, int qmax, const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
     float* __restrict__ o32, uint16_t* __restrict__ o_bf, float* __restrict__ m_tab,
     float* __restrict__ z_tab) {
-  __shared__ __attribute__((aligned(16))) uint8_t sKV[2 * kMaxN * kRowBytes];  // K rows, V rows
-  __shared__ int sRows[kMaxBucket];
+  constexpr int NT = NB / 16;   // 16-key tiles of the block
+  __shared__ __attribute__((aligned(16))) uint8_t sV[kRowsWaves][NB * kRowBytes];
+  __shared__ __attribute__((aligned(16))) float sAcc[kMaxG][kHD];
+  __shared__ float sM[kMaxG], sL[kMaxG];
+  __shared__ int sSrc[kMaxBucket];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = tid >> 6;
   const int grp = lane >> 4;
   const int ql = lane & 15;
   const int G = H / Hkv;
-  const int ngr = (N + kFinRows - 1) / kFinRows;
-  const int item = blockIdx.x;
-  const int h = item % Hkv;
-  const int b = b_first + (item / Hkv) / ngr;
-  const int n0 = ((item / Hkv) % ngr) * kFinRows;
-  const int count = min(*count_p, bucket);
-  const int kvs = 2 * Hkv * kHD;
-  const int nkt = (N + 15) >> 4;  // 16-key tiles of the block
+  const int m = blockIdx.x / Hkv;   // < bucket: the grid is bucket * Hkv
+  const int h = blockIdx.x - m * Hkv;
+  const int BN = B1 * N;
 
-  // ---- branch b's block K/V of head h to LDS, whole 32-key blocks (rows past N repeat
-  // row N-1: finite values under the zero weights of masked keys) -------------------------
-  {
-    const int nunits = ((nkt + 1) / 2) * 32 * 16;  // (row, 16-byte unit) pairs per K or V
-    for (int i = tid; i < 2 * nunits; i += 256) {
-      const int v = i >= nunits;
-      const int ii = i - v * nunits;
-      const int row = ii >> 4, p = ii & 15;
-      const int j = min(row, N - 1);
-      const size_t kvrow = (size_t)(src[b * N + j] * N + j) * kvs;
-      const int u = v ? v_unit(row, p) : k_unit(row, p);
-      *reinterpret_cast<sf_u32x4*>(sKV + v * kMaxN * kRowBytes + row * kRowBytes + p * 16) =
-          *reinterpret_cast<const sf_u32x4*>(kv_buf + kvrow + (v ? Hkv + h : h) * kHD + u * 8);
-    }
-  }
+  // ---- round 1: the row, the src table, the count and the prefix length, as one
+  // round of loads: the exit test reads all of them (r < BN and P >= 0 always hold),
+  // so the compiler cannot sink any load past it, and the whole table is written
+  // (entries past BN repeat the last) with no branch -------------------------------------
+  const int r = rows[m];
+  const int cnt_raw = *count_p;
+  const int plen_raw = *(p_len ? p_len : count_p);   // a select, not a branch
+  const int count = min(cnt_raw, bucket);
+  const int P = P_cap > 0 ? (p_len ? min(plen_raw, P_cap) : P_cap) : 0;
+  constexpr int kSrcPerThread = kMaxBucket / kRowsThreads;
+  int srcv[kSrcPerThread];
+#pragma unroll
+  for (int k = 0; k < kSrcPerThread; ++k) srcv[k] = src[min(tid + k * kRowsThreads, BN - 1)];
+#pragma unroll
+  for (int k = 0; k < kSrcPerThread; ++k) sSrc[tid + k * kRowsThreads] = srcv[k];
+  if ((m >= count) | (r >= BN) | (P < 0)) return;   // workgroup-uniform; no short circuit
+  const int b = r / N;
+  const int n = r - b * N;
+  const int nr = P > 0 ? merge_ranges(P, count * G, Hkv) : 0;
 
-  // the compacted rows, for lookups
-  for (int i = tid; i < count; i += 256) sRows[i] = rows[i];
-  __syncthreads();
-  auto find = [&](int row) {  // first index with sRows[i] >= row (ascending rows)
-    int lo = 0, hi = count;
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      if (sRows[mid] < row) lo = mid + 1; else hi = mid;
-    }
-    return min(lo, max(count - 1, 0));
-  };
-
-  // ---- this lane's query (tile wv, column ql) ------------------------------------------
-  const int qloc = wv * 16 + ql;         // query = position n0 + qloc / G, q-head qloc % G
-  const int nl = qloc / G;
-  const int g = qloc - nl * G;
-  const int n = n0 + nl;
-  const bool qvalid = nl < kFinRows && n < N;
-  const int r = b * N + min(n, N - 1);
-  // a listed (recomputed) row takes its own query and prefix state; an unlisted one
-  // (folded) those of its source row, which is listed
-  int sidx = find(r);
-  const bool listed = count > 0 && sRows[sidx] == r;
-  const int srow = listed ? r : src[r] * N + min(n, N - 1);
-  if (!listed) sidx = find(srow);
-  const bool compute = qvalid && (FOLDED || listed);
-  const int hq = h * G + min(g, G - 1);
+  // ---- round 2: this wave's q-head's range partials and the query -------------------------
+  // Branch-free: without a prefix (nr = 0) the loads re-read q (any valid address)
+  // and are dropped; waves past G load q-head G - 1's and drop them.
+  constexpr int kB = 16;  // range partials loaded per round (clamped addresses)
+  const int gm = min(wv, G - 1);
+  const int qi = m * G + gm;
+  // range u of query qi sits at attn_slot(h, u, qi) = attn_slot(h, 0, qi) + u * qmax
+  const bool pre = nr > 0;
+  const size_t slot0 = pre ? attn_slot(h, 0, qi, nr_cap, qmax) : 0;
+  const size_t rstride = pre ? (size_t)qmax : 0;
+  const float* pw_o = pre ? ws_o + slot0 * kHD + 2 * lane : reinterpret_cast<const float*>(q_buf);
+  const float* pw_ml = pre ? ws_ml + slot0 * 2 : reinterpret_cast<const float*>(q_buf);
+  const int nr1 = max(nr, 1);
+  float2 ml = *reinterpret_cast<const float2*>(pw_ml + (size_t)min(lane, nr1 - 1) * rstride * 2);
+  float2 a[kB];
+#pragma unroll
+  for (int u = 0; u < kB; ++u)
+    a[u] = *reinterpret_cast<const float2*>(pw_o + (size_t)min(u, nr1 - 1) * rstride * kHD);
+  // Q^T operand: lane holds q[q-head ql][ds*32 + grp*8 .. +8] of row r
   sf_u32x4 qf[4];
   {
-    const uint16_t* qp = q_buf + (size_t)srow * H * kHD + hq * kHD + grp * 8;
+    const int hq = h * G + min(ql, G - 1);
+    const uint16_t* qp = q_buf + (size_t)r * H * kHD + hq * kHD + grp * 8;
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds) qf[ds] = *reinterpret_cast<const sf_u32x4*>(qp + ds * 32);
   }
-  // the source row's merged prefix state: its index among the ascending compacted rows
-  float m_run = -INFINITY, l_run = 0.f;
-  sf_f32x4 acc[8];
-#pragma unroll
-  for (int dt = 0; dt < 8; ++dt) acc[dt] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
-  if (has_prefix) {
-    const float* st = state + ((size_t)sidx * H + hq) * kStateFloats;
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) acc[dt] = *reinterpret_cast<const sf_f32x4*>(st + dt * 16 + grp * 4);
-    const float2 ml = *reinterpret_cast<const float2*>(st + kHD);
-    m_run = ml.x;
-    l_run = ml.y;
-  }
-  __syncthreads();  // sKV
+  sf_lds_barrier();  // sSrc (the partials and the query stay in flight)
 
-  // ---- block scores S^T = K Q^T ----------------------------------------------------------
-  float s_t[4][4];  // [key tile][i]: key 16t + 4*grp + i of this lane's query
+  // ---- this wave's rows: every kRowsWaves-th of the rows that take r's query, in
+  // branch order (one ballot: B1 <= 64); the first one's K and V go out now ----------------
+  unsigned long long mine = 0;
+  {
+    const int bb = b_first + lane;
+    const bool dep = lane < b_count && (FOLDED ? sSrc[bb * N + n] == b : bb == b);
+    unsigned long long mask = __ballot(dep);
+    for (int k = 0; mask; ++k) {
+      const unsigned long long bit = mask & (0ull - mask);
+      if ((k & (kRowsWaves - 1)) == wv) mine |= bit;
+      mask ^= bit;
+    }
+  }
+  uint8_t* sv = sV[wv];
+  sf_u32x4 kf[NT][4];
+  int bd = mine ? b_first + __builtin_ctzll(mine) : -1;   // wave-uniform
+  // a wave without a row issues its own branch's copies too (dropped): no branch
+  row_kv_issue<NB>(kv_buf, sSrc, bd >= 0 ? bd : b, N, Hkv, h, kf, sv);
+
+  // ---- the merged prefix state of q-head wv ------------------------------------------------
+  if (wv < G) {  // wave-uniform
+    float2 acc = make_float2(0.f, 0.f);
+    float mm = -INFINITY, l = 0.f;
+    if (nr > 0) {
+      ml = lane < nr ? ml : make_float2(-INFINITY, 0.f);
+      mm = sf_wave_max(ml.x);  // -inf only with no prefix key at all
+      const float w = (lane < nr && mm > -INFINITY) ? __builtin_amdgcn_exp2f(ml.x - mm) : 0.f;
+      l = sf_wave_sum(ml.y * w);
+      for (int r0 = 0; r0 < nr; r0 += kB) {
+        if (r0 > 0) {
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    sf_f32x4 a = {0.f, 0.f, 0.f, 0.f};
-    if (t < nkt) {  // uniform
-      sf_u32x4 kf[4];
+          for (int u = 0; u < kB; ++u)
+            a[u] = *reinterpret_cast<const float2*>(pw_o + (size_t)min(r0 + u, nr - 1) * rstride * kHD);
+        }
+#pragma unroll
+        for (int u = 0; u < kB; ++u) {
+          const float wr = __shfl(w, min(r0 + u, 63), 64);   // 0 past nr
+          acc.x = fmaf(wr, a[u].x, acc.x);
+          acc.y = fmaf(wr, a[u].y, acc.y);
+        }
+      }
+    }
+    *reinterpret_cast<float2*>(&sAcc[wv][2 * lane]) = acc;
+    if (lane == 0) {
+      sM[wv] = mm;
+      sL[wv] = l;
+    }
+  }
+  // the states are in LDS for every wave (the block copies stay in flight)
+  sf_lds_barrier();
+
+  const int gq = min(ql, G - 1);
+  const float m_run = sM[gq], l_run = sL[gq];
+  while (bd >= 0) {  // wave-uniform
+    // ---- block scores S^T = K Q^T ----------------------------------------------------------
+    float s_t[NT][4];  // [key tile][i]: key 16t + 4*grp + i of this lane's query
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      sf_f32x4 acc_s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ds = 0; ds < 4; ++ds)
-        kf[ds] = *reinterpret_cast<const sf_u32x4*>(sKV + t * 16 * kRowBytes + k_frag_off(lane, ds));
+        acc_s = sf_mfma16x16x32(sf_as_bf16x8(kf[t][ds]), sf_as_bf16x8(qf[ds]), acc_s);
 #pragma unroll
-      for (int ds = 0; ds < 4; ++ds) a = sf_mfma16x16x32(sf_as_bf16x8(kf[ds]), sf_as_bf16x8(qf[ds]), a);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int j = 16 * t + 4 * grp + i;
-      const bool keep = t < nkt && j < N && !(causal && j > n);
-      s_t[t][i] = keep ? a[i] : -INFINITY;   // exp2 gives 0
-    }
-  }
-  float mx = -INFINITY;
-#pragma unroll
-  for (int t = 0; t < 4; ++t)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s_t[t][i]);
-  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-  const float m_new = fmaxf(m_run, mx * scale_log2);   // finite: key 0 is never masked
-  const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-  float lsum = 0.f;
-#pragma unroll
-  for (int t = 0; t < 4; ++t)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      s_t[t][i] = __builtin_amdgcn_exp2f(fmaf(s_t[t][i], scale_log2, -m_new));
-      lsum += s_t[t][i];
-    }
-  lsum += __shfl_xor(lsum, 16, 64);
-  lsum += __shfl_xor(lsum, 32, 64);
-  const float l_new = l_run * alpha + lsum;
-#pragma unroll
-  for (int dt = 0; dt < 8; ++dt) acc[dt] = acc[dt] * alpha;
-
-  // ---- O^T += V^T P^T over 32-key blocks ---------------------------------------------------
-#pragma unroll
-  for (int kb = 0; kb < 2; ++kb) {
-    if (2 * kb < nkt) {  // uniform
-      float p2[2][4];
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) p2[t][i] = s_t[2 * kb + t][i];   // 0 past the last tile
-      sf_bf16x8 pb[kPParts];
-      pv_parts<kPParts>(p2, pb);
-      sf_u32x2 vf[16];
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const sf_lds_off va = sf_lds_addr(sKV) + (uint32_t)(v_tr_off(lane, dt) + 32 * kb * kRowBytes);
-        vf[2 * dt] = sf_lds_read8_tr<0>(va);
-        vf[2 * dt + 1] = sf_lds_read8_tr<16 * kRowBytes>(va);
-      }
-      sf_lds_reads_done(vf);
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const sf_u32x4 vw = {vf[2 * dt][0], vf[2 * dt][1], vf[2 * dt + 1][0], vf[2 * dt + 1][1]};
-        const sf_bf16x8 va = sf_as_bf16x8(vw);
-#pragma unroll
-        for (int pp = kPParts - 1; pp >= 0; --pp) acc[dt] = sf_mfma16x16x32(va, pb[pp], acc[dt]);
+      for (int i = 0; i < 4; ++i) {
+        const int j = 16 * t + 4 * grp + i;
+        const bool keep = j < N && !(causal && j > n);
+        s_t[t][i] = keep ? acc_s[i] : -INFINITY;   // exp2 gives 0
       }
     }
-  }
-
-  // ---- outputs ------------------------------------------------------------------------------
-  if (compute) {
-    const float inv = 1.0f / l_new;
-    const size_t off = (size_t)r * H * kHD + hq * kHD + grp * 4;
+    float mx = -INFINITY;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const sf_f32x4 o = acc[dt] * inv;
-      *reinterpret_cast<sf_f32x4*>(o32 + off + dt * 16) = o;
-      sf_u32x2 w;
-      w[0] = sf_pack2(o[0], o[1]);
-      w[1] = sf_pack2(o[2], o[3]);
-      *reinterpret_cast<sf_u32x2*>(o_bf + off + dt * 16) = w;
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s_t[t][i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx * scale_log2);   // finite: key 0 is never masked
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+    float lsum = 0.f;
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        s_t[t][i] = __builtin_amdgcn_exp2f(fmaf(s_t[t][i], scale_log2, -m_new));
+        lsum += s_t[t][i];
+      }
+    lsum += __shfl_xor(lsum, 16, 64);
+    lsum += __shfl_xor(lsum, 32, 64);
+    const float l_new = l_run * alpha + lsum;
+    // the prefix state's acc (O^T layout: dims 16 dt + 4 grp + i of q-head gq), rescaled
+    sf_f32x4 acc[8];
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+      acc[dt] = *reinterpret_cast<const sf_f32x4*>(&sAcc[gq][dt * 16 + grp * 4]) * alpha;
+
+    // ---- O^T += V^T P^T over 32-key blocks (the V copies landed) -------------------------------
+    sf_wait_vm_loads();
+#pragma unroll
+    for (int kb = 0; kb < NB / 32; ++kb) {
+      {
+        float p2[2][4];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) p2[t][i] = s_t[2 * kb + t][i];   // 0 past key N - 1
+        sf_bf16x8 pb[kPParts];
+        pv_parts<kPParts>(p2, pb);
+        sf_u32x2 vf[16];
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+          // v_tr_off counts from a staged chunk's K rows; the region holds V rows only
+          const sf_lds_off va = sf_lds_addr(sv) - (uint32_t)kHalfBytes +
+                                (uint32_t)(v_tr_off(lane, dt) + 32 * kb * kRowBytes);
+          vf[2 * dt] = sf_lds_read8_tr<0>(va);
+          vf[2 * dt + 1] = sf_lds_read8_tr<16 * kRowBytes>(va);
+        }
+        sf_lds_reads_done(vf);
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+          const sf_u32x4 vw = {vf[2 * dt][0], vf[2 * dt][1], vf[2 * dt + 1][0], vf[2 * dt + 1][1]};
+          const sf_bf16x8 va = sf_as_bf16x8(vw);
+#pragma unroll
+          for (int pp = kPParts - 1; pp >= 0; --pp) acc[dt] = sf_mfma16x16x32(va, pb[pp], acc[dt]);
+        }
+      }
     }
-    if (grp == 0) {
-      // the natural-base max the scores were measured from
-      m_tab[(size_t)r * H + hq] = m_new * 0.69314718055994530942f;
-      z_tab[(size_t)r * H + hq] = l_new;
+
+    // ---- outputs of row (bd, n) ---------------------------------------------------------------
+    if (ql < G) {
+      const int ro = bd * N + n;
+      const int hq = h * G + ql;
+      const float inv = 1.0f / l_new;
+      const size_t off = (size_t)ro * H * kHD + hq * kHD + grp * 4;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const sf_f32x4 o = acc[dt] * inv;
+        *reinterpret_cast<sf_f32x4*>(o32 + off + dt * 16) = o;
+        sf_u32x2 w;
+        w[0] = sf_pack2(o[0], o[1]);
+        w[1] = sf_pack2(o[2], o[3]);
+        *reinterpret_cast<sf_u32x2*>(o_bf + off + dt * 16) = w;
+      }
+      if (grp == 0) {
+        // the natural-base max the scores were measured from
+        m_tab[(size_t)ro * H + hq] = m_new * 0.69314718055994530942f;
+        z_tab[(size_t)ro * H + hq] = l_new;
+      }
     }
+    // the next row of this wave (its V copies overwrite the region: the reads of
+    // this one are done)
+    mine &= mine - 1;
+    bd = mine ? b_first + __builtin_ctzll(mine) : -1;
+    if (bd >= 0) row_kv_issue<NB>(kv_buf, sSrc, bd, N, Hkv, h, kf, sv);
   }
 }
 
@@ -711,9 +754,8 @@ namespace {
 size_t partial_bytes(int bucket, int H, int P) {
   return (size_t)ranges_cap(P) * bucket * H * (kHD + 2) * sizeof(float);
 }
-size_t state_offset(int bucket, int H, int P) { return (partial_bytes(bucket, H, P) + 255) & ~(size_t)255; }
 
-// The prefix pass, its merge and the finalize for the rows of branches
+// The prefix pass, then the merge + block attention for the rows of branches
 // [b_first, b_first + b_count) (FOLDED: folded rows too).
 int attention(bool folded, const uint16_t* q_buf, const uint16_t* kv_buf,
               const uint16_t* prefix_k, const uint16_t* prefix_v, const int32_t* page_table,
@@ -727,8 +769,9 @@ int attention(bool folded, const uint16_t* q_buf, const uint16_t* kv_buf,
     return SF_ERR_ARG;
   if (hd != kHD || H < 1 || Hkv < 1 || H % Hkv != 0 || H / Hkv > kMaxG) return SF_ERR_SHAPE;
   if (N < 1 || N > kMaxN || B1 < 1 || bucket < 1 || bucket > B1 * N) return SF_ERR_SHAPE;
-  // the finalize stages the compacted rows in a kMaxBucket-entry LDS table
-  if (bucket > kMaxBucket || B1 * N > kMaxBucket) return SF_ERR_SHAPE;
+  // the rows kernel stages src in a kMaxBucket-entry LDS table and finds a row's
+  // branches with one 64-lane ballot
+  if (bucket > kMaxBucket || B1 * N > kMaxBucket || B1 > kMaxB1) return SF_ERR_SHAPE;
   if (b_first < 0 || b_count < 1 || b_first + b_count > B1) return SF_ERR_SHAPE;
   if (P < 0 || nchunks_for(P) > kMaxChunks) return SF_ERR_SHAPE;
   if (P > 0) {
@@ -743,33 +786,35 @@ int attention(bool folded, const uint16_t* q_buf, const uint16_t* kv_buf,
   const int G = H / Hkv;
   const int qmax = bucket * G;
   const float scale_log2 = scaling * 1.44269504088896340736f;
-  float* state = nullptr;
+  float* ws_o = nullptr;
+  float* ws_ml = nullptr;
+  int nr_cap = 0;
   if (P > 0) {
     const int nch = nchunks_for(P);
-    const int nr_cap = ranges_cap(P);
+    nr_cap = ranges_cap(P);
     const size_t nslot = (size_t)nr_cap * qmax * Hkv;
-    float* ws_o = reinterpret_cast<float*>(workspace);
-    float* ws_ml = ws_o + nslot * kHD;
-    state = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) +
-                                     state_offset(bucket, H, P));
+    ws_o = reinterpret_cast<float*>(workspace);
+    ws_ml = ws_o + nslot * kHD;
     // persistent grid: one 136 KB-LDS workgroup per CU; a multiple of 8
     const int grid = prefix_launch_grid(qmax, nch, Hkv);
     hipLaunchKernelGGL(sf_attn_prefix_kernel, dim3(grid), dim3(kPrefixThreads), 0, st, q_buf,
                        prefix_k, prefix_v, page_table, page_size, page_stride, head_stride,
                        prefix_len, P, rows, count, bucket, H, Hkv, scale_log2, qmax, nr_cap, ws_o,
                        ws_ml);
-    hipLaunchKernelGGL(sf_attn_prefix_merge_kernel, dim3((bucket * H + 3) / 4), dim3(256), 0, st,
-                       count, bucket, H, Hkv, prefix_len, P, nr_cap, qmax, ws_o, ws_ml, state);
   }
-  const dim3 grid3(b_count * Hkv * ((N + kFinRows - 1) / kFinRows));
-  if (folded)
-    hipLaunchKernelGGL(sf_attn_finalize_kernel<true>, grid3, dim3(256), 0, st, q_buf, kv_buf, src,
-                       rows, count, bucket, N, b_first, H, Hkv, scale_log2, block_causal ? 1 : 0,
-                       P > 0 ? 1 : 0, state, o32, o_bf, m_tab, z_tab);
-  else
-    hipLaunchKernelGGL(sf_attn_finalize_kernel<false>, grid3, dim3(256), 0, st, q_buf, kv_buf, src,
-                       rows, count, bucket, N, b_first, H, Hkv, scale_log2, block_causal ? 1 : 0,
-                       P > 0 ? 1 : 0, state, o32, o_bf, m_tab, z_tab);
+  const dim3 grid2(bucket * Hkv);
+  const int causal = block_causal ? 1 : 0;
+#define SF_ATTN_ROWS(F, NB)                                                                      \
+  hipLaunchKernelGGL((sf_attn_rows_kernel<F, NB>), grid2, dim3(kRowsThreads), 0, st, q_buf,     \
+                     kv_buf, src, rows, count, bucket, B1, N, b_first, b_count, H, Hkv,          \
+                     scale_log2, causal, prefix_len, P, nr_cap, qmax, ws_o, ws_ml, o32, o_bf,    \
+                     m_tab, z_tab)
+  if (folded) {
+    if (N <= 32) SF_ATTN_ROWS(true, 32); else SF_ATTN_ROWS(true, 64);
+  } else {
+    if (N <= 32) SF_ATTN_ROWS(false, 32); else SF_ATTN_ROWS(false, 64);
+  }
+#undef SF_ATTN_ROWS
   return sf_launch_status();
 }
 
@@ -779,9 +824,8 @@ extern "C" size_t sf_attn_workspace_bytes(int bucket, int H, int P) {
   if (bucket < 1 || H < 1 || P < 0) return 0;
   if (P == 0) return 16;
   // the range partials: per (kv head, chunk range, query) 128 fp32 acc + (m, l), with
-  // bucket*G queries per kv head: ranges * bucket * H slots; then (256-aligned) the
-  // merged prefix state of every (compacted row, q-head): 132 floats
-  return state_offset(bucket, H, P) + (size_t)bucket * H * kStateFloats * sizeof(float);
+  // bucket*G queries per kv head: ranges * bucket * H slots
+  return partial_bytes(bucket, H, P);
 }
 
 extern "C" int sf_attn_prefix_block(const uint16_t* q_buf, const uint16_t* kv_buf,

@@ -97,6 +97,10 @@ SF_DEV void sf_wait_vm_barrier() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+// A workgroup barrier once this wave's LDS accesses have completed; its vector
+// memory loads (direct copies included) stay in flight.
+SF_DEV void sf_lds_barrier() { sf_wait_vm_barrier<63>(); }
+
 // LDS fragment reads the compiler does not track: 16 bytes at byte address
 // `addr` + OFF of LDS into a register, no wait; sf_lds_reads_done makes the values
 // usable (s_waitcnt lgkmcnt(0), with every value passed through it so that no use

@@ -61,6 +61,8 @@ SF_DEV void sf_wait_vm_barrier() {
   __syncthreads();
 }
 
+SF_DEV void sf_lds_barrier() { __syncthreads(); }
+
 // LDS fragment reads (the GPU issues them untracked and waits once): plain reads.
 typedef uintptr_t sf_lds_off;
 template <int OFF>

@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_host_side_validation_without_gpu():
     lib = _lib.load()
-    assert lib.sf_abi_version() == 10
+    assert lib.sf_abi_version() == 11
     assert lib.sf_status_string(1).decode() == "shape outside kernel limits"
     # NULL pointers and bad shapes are rejected before any launch
     assert lib.sf_fold_gate(*([None] * 3), 8, 32, 64, 256, 0.1, 1e-6, 0, *([None] * 11)) == 2
@@ -59,24 +59,26 @@ def test_host_side_validation_without_gpu():
     assert lib.sf_logit_stats_workspace_bytes(8) >= 8 * 65536 * 4
     assert lib.sf_parent_map(None, 8, 32, fake, None, None) == 2
     assert lib.sf_parent_map(fake, 65, 32, fake, None, None) == 1
-    # attention: the finalize's LDS row table holds 1024 compacted rows, so a
-    # bucket (or a step) beyond that is a shape error, not an overrun
+    # attention: the rows kernel stages src in a 1024-entry LDS table and finds a
+    # row's branches with one 64-lane ballot, so a bucket or a step beyond 1024 rows,
+    # or more than 64 branches, is a shape error, not an overrun
     p = [ctypes.c_void_p(4096 * (i + 1)) for i in range(9)]
     q, kv, src, rows, cnt, o32, obf, mt, zt = p
 
-    def attn_rows(bucket, B1):
+    def attn_rows(bucket, B1, N=32):
         return lib.sf_attn_rows(q, kv, None, None, None, 0, 16, 0, 0, src, rows, cnt, bucket, B1,
-                                32, 0, B1, 28, 4, 128, 0.088, None, o32, obf, mt, zt, None, 0,
+                                N, 0, B1, 28, 4, 128, 0.088, None, o32, obf, mt, zt, None, 0,
                                 None)
 
-    def attn_block(bucket, B1):
+    def attn_block(bucket, B1, N=32):
         return lib.sf_attn_prefix_block(q, kv, None, None, None, 0, 16, 0, 0, src, rows, cnt,
-                                        bucket, B1, 32, 28, 4, 128, 0.088, None, 0, o32, obf, mt,
+                                        bucket, B1, N, 28, 4, 128, 0.088, None, 0, o32, obf, mt,
                                         zt, None, 0, None)
     for fn in (attn_rows, attn_block):
         assert fn(1025, 33) == 1
         assert fn(1024, 33) == 1      # 33 * 32 rows > 1024
         assert fn(1025, 32) == 1      # bucket above B1 * N
+        assert fn(100, 65, 8) == 1    # 65 branches
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

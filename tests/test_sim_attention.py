@@ -9,7 +9,8 @@ launch arithmetic, and checked against a float64 restatement of the attention.
 
 This pins the kernels' data movement and indexing (paged and shuffled prefix
 pages, permuted key slots, swizzled V^T, chunk ranges with the flash rescale,
-persistent-grid walk, partial slots, merge, causal block) on machines without a
+persistent-grid walk, partial slots, the per-row merge, folded rows, causal block)
+on machines without a
 GPU; the GPU tests pin the same kernels on the hardware."""
 
 import shutil
@@ -44,7 +45,7 @@ def attn_sim(tmp_path_factory):
 
 
 CASES = [
-    # P, page size, B1, N, H, Hkv, R, causal, seed
+    # P, page size, B1, N, H, Hkv, R, causal, seed[, folded]
     (1, 16, 2, 8, 4, 2, 5, 0, 1),        # one prefix key
     (17, 16, 3, 8, 4, 2, 9, 0, 2),       # two pages, partial last
     (130, 32, 2, 16, 6, 2, 11, 1, 3),    # partial second chunk, causal block
@@ -53,11 +54,17 @@ CASES = [
     (0, 16, 2, 8, 4, 2, 6, 1, 6),        # no prefix: block keys only
     (2112, 16, 8, 32, 28, 4, 39, 0, 11),  # the 7B verify shape
     (4096, 16, 8, 32, 16, 8, 256, 0, 12),  # two chunks per work item (flash rescale)
+    # sf_attn_rows over a gate structure: every row, folded ones from their source's query
+    (0, 16, 4, 8, 4, 2, 0, 0, 21, 1),    # no prefix
+    (130, 32, 5, 16, 6, 2, 0, 0, 22, 1),  # partial chunk, G = 3
+    (300, 16, 9, 8, 8, 1, 0, 0, 23, 1),  # G = 8, 9 branches (a wave takes 3 rows)
+    (17, 16, 3, 64, 4, 2, 0, 0, 25, 1),  # N = 64: two 32-key blocks
+    (520, 16, 8, 32, 28, 4, 0, 0, 24, 1),  # the 7B verify shape, shorter prefix
 ]
 
 
-@pytest.mark.parametrize("case", CASES, ids=lambda c: "P%d_ps%d_H%d-%d_R%d_c%d" % (
-    c[0], c[1], c[4], c[5], c[6], c[7]))
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "P%d_ps%d_B%d_N%d_H%d-%d_R%d_c%d%s" % (
+    c[0], c[1], c[2], c[3], c[4], c[5], c[6], c[7], "_folded" if len(c) > 9 and c[9] else ""))
 def test_attention_kernels_in_simulator(attn_sim, case):
     r = subprocess.run([str(attn_sim), *map(str, case)], capture_output=True, text=True,
                        timeout=600)
