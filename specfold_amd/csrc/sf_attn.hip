@@ -406,15 +406,15 @@ SF_DEV void prefix_item(const uint16_t* __restrict__ q_buf, const uint16_t* __re
       if (qi < nq) {
         const size_t slot = attn_slot(h, r, qi, nr_cap, qmax);
         if (grp == 0) {
-          ws_ml[slot * 2] = mm;
-          ws_ml[slot * 2 + 1] = l_run[qs] * w0 + l1 * w1;
+          sf_handoff_store(reinterpret_cast<sf_f32x2*>(ws_ml + slot * 2),
+                           sf_f32x2{mm, l_run[qs] * w0 + l1 * w1});
         }
         float* op = ws_o + slot * kHD + grp * 4;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) {
           const sf_f32x4 a1 =
               *reinterpret_cast<const sf_f32x4*>(xo + (((qg * 2 + qs) * 8 + dt) * 64 + lane) * 4);
-          *reinterpret_cast<sf_f32x4*>(op + dt * 16) = acc[qs][dt] * w0 + a1 * w1;
+          sf_handoff_store(reinterpret_cast<sf_f32x4*>(op + dt * 16), acc[qs][dt] * w0 + a1 * w1);
         }
       }
     }
@@ -576,11 +576,13 @@ sf_attn_rows_kernel(
   const float* pw_o = pre ? ws_o + slot0 * kHD + 2 * lane : reinterpret_cast<const float*>(q_buf);
   const float* pw_ml = pre ? ws_ml + slot0 * 2 : reinterpret_cast<const float*>(q_buf);
   const int nr1 = max(nr, 1);
-  float2 ml = *reinterpret_cast<const float2*>(pw_ml + (size_t)min(lane, nr1 - 1) * rstride * 2);
-  float2 a[kB];
+  sf_f32x2 ml = sf_handoff_load(
+      reinterpret_cast<const sf_f32x2*>(pw_ml + (size_t)min(lane, nr1 - 1) * rstride * 2));
+  sf_f32x2 a[kB];
 #pragma unroll
   for (int u = 0; u < kB; ++u)
-    a[u] = *reinterpret_cast<const float2*>(pw_o + (size_t)min(u, nr1 - 1) * rstride * kHD);
+    a[u] = sf_handoff_load(
+        reinterpret_cast<const sf_f32x2*>(pw_o + (size_t)min(u, nr1 - 1) * rstride * kHD));
   // Q^T operand: lane holds q[q-head ql][ds*32 + grp*8 .. +8] of row r
   sf_u32x4 qf[4];
   {
@@ -615,7 +617,7 @@ sf_attn_rows_kernel(
     float2 acc = make_float2(0.f, 0.f);
     float mm = -INFINITY, l = 0.f;
     if (nr > 0) {
-      ml = lane < nr ? ml : make_float2(-INFINITY, 0.f);
+      ml = lane < nr ? ml : sf_f32x2{-INFINITY, 0.f};
       mm = sf_wave_max(ml.x);  // -inf only with no prefix key at all
       const float w = (lane < nr && mm > -INFINITY) ? __builtin_amdgcn_exp2f(ml.x - mm) : 0.f;
       l = sf_wave_sum(ml.y * w);
@@ -623,7 +625,8 @@ sf_attn_rows_kernel(
         if (r0 > 0) {
 #pragma unroll
           for (int u = 0; u < kB; ++u)
-            a[u] = *reinterpret_cast<const float2*>(pw_o + (size_t)min(r0 + u, nr - 1) * rstride * kHD);
+            a[u] = sf_handoff_load(reinterpret_cast<const sf_f32x2*>(
+                pw_o + (size_t)min(r0 + u, nr - 1) * rstride * kHD));
         }
 #pragma unroll
         for (int u = 0; u < kB; ++u) {

@@ -160,8 +160,8 @@ __global__ __launch_bounds__(kPrnThreads) void part_residual_norm_kernel(
   for (int i = 0; i < VPT; ++i) {
     xv[i] = xr[v[i]];
     wv[i] = zn ? reinterpret_cast<const sf_u32x4*>(w)[v[i]] : sf_u32x4{0u, 0u, 0u, 0u};
-    y[i][0] = pr[2 * v[i]];
-    y[i][1] = pr[2 * v[i] + 1];
+    y[i][0] = sf_handoff_load(pr + 2 * v[i]);
+    y[i][1] = sf_handoff_load(pr + 2 * v[i] + 1);
   }
   for (int s0 = 1; s0 < ks; s0 += 4) {
     sf_f32x4 a[4][VPT][2];
@@ -170,8 +170,8 @@ __global__ __launch_bounds__(kPrnThreads) void part_residual_norm_kernel(
       const size_t o = (size_t)min(s0 + j, ks - 1) * st4;
 #pragma unroll
       for (int i = 0; i < VPT; ++i) {
-        a[j][i][0] = pr[o + 2 * v[i]];
-        a[j][i][1] = pr[o + 2 * v[i] + 1];
+        a[j][i][0] = sf_handoff_load(pr + o + 2 * v[i]);
+        a[j][i][1] = sf_handoff_load(pr + o + 2 * v[i] + 1);
       }
     }
 #pragma unroll

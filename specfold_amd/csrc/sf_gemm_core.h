@@ -209,12 +209,12 @@ SF_DEV void tile_to_lds(float* x, const sf_f32x4 (&acc)[MB / 16][WN], int nmt) {
 // at a time from clamped addresses with no branch in between.
 template <typename T>
 SF_DEV T sum_slots(const float* p, size_t stride, int n) {
-  T acc = *reinterpret_cast<const T*>(p);
+  T acc = sf_handoff_load(reinterpret_cast<const T*>(p));
   for (int s0 = 1; s0 < n; s0 += 4) {
     T v[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      v[j] = *reinterpret_cast<const T*>(p + (size_t)min(s0 + j, n - 1) * stride);
+      v[j] = sf_handoff_load(reinterpret_cast<const T*>(p + (size_t)min(s0 + j, n - 1) * stride));
 #pragma unroll
     for (int j = 0; j < 4; ++j)
       if (s0 + j < n) acc += v[j];
@@ -343,7 +343,7 @@ void gemm_sk_kernel(const uint16_t* __restrict__ A, const int32_t* __restrict__ 
         // up sums -> pw[.. + N + c0 + c - 128]
         const size_t pc = kS ? (c < 128 ? (size_t)c0 + c : (size_t)N + c0 + c - 128)
                              : (size_t)c0 + c;
-        *reinterpret_cast<sf_f32x4*>(pw + (size_t)m * N * kPW + pc) = y;
+        sf_handoff_store(reinterpret_cast<sf_f32x4*>(pw + (size_t)m * N * kPW + pc), y);
       } else if (kS) {
         if (c < cw) {
           const sf_f32x4 up = *reinterpret_cast<const sf_f32x4*>(tl + m * kTW + 128 + c);

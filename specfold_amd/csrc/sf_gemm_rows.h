@@ -134,7 +134,8 @@ void gemm_rows_kernel(const uint16_t* __restrict__ A, int M, const uint16_t* __r
       for (int tt = 0; tt < WN; ++tt) {
         const size_t o = (size_t)row * N + col0 + tt * 16;
         if (MODE == kRowsPart) {
-          *reinterpret_cast<sf_f32x4*>(part + (size_t)s * part_stride + o) = acc[i][tt];
+          sf_handoff_store(reinterpret_cast<sf_f32x4*>(part + (size_t)s * part_stride + o),
+                           acc[i][tt]);
         } else {
           sf_u32x2 v;
           v[0] = sf_pack2(acc[i][tt][0], acc[i][tt][1]);

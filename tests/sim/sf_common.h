@@ -16,6 +16,7 @@ typedef uint16_t sf_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float sf_f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t sf_u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t sf_u32x2 __attribute__((ext_vector_type(2)));
+typedef float sf_f32x2 __attribute__((ext_vector_type(2)));
 
 SF_DEV float sf_bf2f(uint16_t b) { return sim_bf16_to_f(b); }
 SF_DEV uint16_t sf_f2bf(float f) { return sim_f_to_bf16(f); }
@@ -62,6 +63,10 @@ SF_DEV void sf_wait_vm_barrier() {
 }
 
 SF_DEV void sf_lds_barrier() { __syncthreads(); }
+template <typename T>
+SF_DEV void sf_handoff_store(T* p, T v) { *p = v; }
+template <typename T>
+SF_DEV T sf_handoff_load(const T* p) { return *p; }
 
 // LDS fragment reads (the GPU issues them untracked and waits once): plain reads.
 typedef uintptr_t sf_lds_off;
