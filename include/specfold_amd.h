@@ -56,6 +56,11 @@ extern "C" {
    step; each sequence's main branch has par[b] == b).  No counterpart in the
    reference, whose verify step takes one sequence. */
 #define SF_GATE_ROOTS_BY_PARENT 16
+/* gate_mode flag: the gate entry points launch the row kernel only (rec, rstd, xn,
+ * hidden_out); the compaction (f, src, rows, count, seg, segcnt, slot, which may
+ * then be NULL here) is left to sf_qkv_rope_gated, which runs it in its GEMM's
+ * prologue. */
+#define SF_GATE_DEFER_COMPACT 32
 
 const char* sf_status_string(int status);
 /* 2: GEMM weights in the packed layout of sf_pack_weight; fused residual entries.
@@ -69,7 +74,8 @@ const char* sf_status_string(int status);
  * 9: SF_ERR_CAPTURE; attention entry points refuse bucket or B1*N above 1024.
  * 10: sf_head_logits (the head with the Fast-dLLM shift); sf_lm_head runs on it.
  * 11: attention merges each recomputed row's prefix partials in the kernel that
- *     attends its rows: the workspace holds the range partials only; B1 <= 64. */
+ *     attends its rows: the workspace holds the range partials only; B1 <= 64.
+ * 12: SF_GATE_DEFER_COMPACT and sf_qkv_rope_gated (the compaction in the QKV GEMM). */
 int sf_abi_version(void);
 
 /*
@@ -164,6 +170,26 @@ int sf_qkv_rope_branches(const uint16_t* xn, const int32_t* rows, const int32_t*
                          const int32_t* pos0_branch, int table_rows, const float* q_scale_rows,
                          int N, int D, int H, int Hkv, int hd, uint16_t* q_buf, uint16_t* kv_buf,
                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* (1)+(2) for a gate launched with SF_GATE_DEFER_COMPACT: the compaction of rec
+ * runs in the prologue of every workgroup of the QKV GEMM (each needs the
+ * compacted rows as its A rows), and workgroup 0 writes f, src, rows, count, seg,
+ * segcnt and slot (may be NULL) exactly as sf_fold_gate documents them, so the
+ * gate's separate compaction launch goes (fastdllm_v2_folded.py:141-152 and
+ * :151-161; Triton src_resolve_kernel + fused_ln_qkv_rope_scatter_kernel,
+ * specfold/generate/triton_kernels.py:18-87).  pos0_per_branch = 0: the rope and
+ * q scale of sf_qkv_rope (pos0 [1] or NULL, q_scale [N] or NULL); 1: those of
+ * sf_qkv_rope_branches (pos0 [B1], q_scale [B1*N] or NULL).  The q/kv outputs
+ * equal those of sf_fold_gate + sf_qkv_rope bit for bit.  Same workspace as
+ * sf_qkv_rope.  Limits: B1 <= 64, B1*N <= 1024, 1 <= bucket <= B1*N, and those of
+ * sf_qkv_rope.  No counterpart in the reference. */
+int sf_qkv_rope_gated(const uint16_t* xn, const int8_t* rec, const int32_t* par, int B1, int N,
+                      int bucket, int32_t* f, int32_t* src, int32_t* rows, int32_t* count,
+                      int32_t* seg, int32_t* segcnt, int32_t* slot, const uint16_t* w_qkv,
+                      const uint16_t* b_qkv, const uint16_t* cos_tab, const uint16_t* sin_tab,
+                      const int32_t* pos0, int pos0_per_branch, int table_rows,
+                      const float* q_scale, int D, int H, int Hkv, int hd, uint16_t* q_buf,
+                      uint16_t* kv_buf, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * (3) Attention of the recomputed rows over [shared prefix ; own branch block],

@@ -22,6 +22,7 @@ SF_GATE_MODEL_DTYPE = 0
 SF_GATE_FP32_SQUARED = 1
 SF_GATE_ALL = 2
 SF_GATE_ROOTS_BY_PARENT = 16  # flag: roots are the branches with par[b] == b
+SF_GATE_DEFER_COMPACT = 32  # flag: the compaction runs in sf_qkv_rope_gated
 
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
@@ -43,6 +44,9 @@ SIGNATURES = {
                          _i, _i, _i, _i, _i, _vp, _vp, _vp, _sz, _vp]),
     "sf_qkv_rope_branches": (_i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _vp, _i, _vp,
                                   _i, _i, _i, _i, _i, _vp, _vp, _vp, _sz, _vp]),
+    "sf_qkv_rope_gated": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                               _vp, _vp, _vp, _vp, _vp, _i, _i, _vp, _i, _i, _i, _i, _vp, _vp,
+                               _vp, _sz, _vp]),
     "sf_attn_workspace_bytes": (_sz, [_i, _i, _i]),
     "sf_attn_prefix_block": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _ll, _ll, _vp, _vp, _vp,
                                   _i, _i, _i, _i, _i, _i, _f, _vp, _i, _vp, _vp, _vp, _vp, _vp,
@@ -270,6 +274,51 @@ def qkv_rope_branches(xn, rows, count, bucket, BN, w_qkv, b_qkv, cos, sin, q_sca
                                      _ptr(q_buf), _ptr(kv_buf), _ptr(workspace),
                                      workspace.numel(), _stream(stream))
     _check(st, "sf_qkv_rope_branches")
+
+
+def qkv_rope_gated(xn, rec, par, B1, N, bucket, f, src, rows, count, seg, segcnt, slot, w_qkv,
+                   b_qkv, cos, sin, q_scale, D, H, Hkv, hd, q_buf, kv_buf, workspace,
+                   pos0=None, pos0_branch=None, stream=None) -> None:
+    """The QKV projection with the fold gate's compaction in its GEMM's prologue,
+    after a gate launched with SF_GATE_DEFER_COMPACT: writes f, src, rows, count,
+    seg, segcnt and slot as fold_gate does, then q/kv as qkv_rope (``pos0``: an
+    int32 device scalar, ``q_scale`` [N]) or qkv_rope_branches (``pos0_branch``
+    int32 [B1], ``q_scale`` [B1*N])."""
+    BN = B1 * N
+    nq = (H + 2 * Hkv) * hd
+    _need(xn, "xn", torch.bfloat16, min_numel=BN * D)
+    _need(rec, "rec", torch.int8, min_numel=BN, align=4)
+    _need(par, "par", torch.int32, numel=B1, align=4)
+    for nm, t, n in (("f", f, BN), ("src", src, BN), ("rows", rows, bucket), ("count", count, 1),
+                     ("seg", seg, BN), ("segcnt", segcnt, B1)):
+        _need(t, nm, torch.int32, min_numel=n, align=4)
+    if slot is not None:
+        _need(slot, "slot", torch.int32, min_numel=BN, align=4)
+    _need(w_qkv, "w_qkv", torch.bfloat16, numel=nq * D)
+    if b_qkv is not None:
+        _need(b_qkv, "b_qkv", torch.bfloat16, numel=nq, align=4)
+    if pos0_branch is not None:
+        _need(pos0_branch, "pos0_branch", torch.int32, numel=B1, align=4)
+        pos, per_branch, nscale = pos0_branch, 1, BN
+    else:
+        if pos0 is not None:
+            _need(pos0, "pos0", torch.int32, min_numel=1, align=4)
+        pos, per_branch, nscale = pos0, 0, N
+    table_rows = cos.numel() // hd if pos is not None else N
+    _need(cos, "cos", torch.bfloat16, numel=table_rows * hd, align=4)
+    _need(sin, "sin", torch.bfloat16, numel=cos.numel(), align=4)
+    if q_scale is not None:
+        _need(q_scale, "q_scale", torch.float32, numel=nscale, align=4)
+    _need(q_buf, "q_buf", torch.bfloat16, min_numel=(BN + 1) * H * hd)
+    _need(kv_buf, "kv_buf", torch.bfloat16, min_numel=(BN + 1) * 2 * Hkv * hd)
+    _need(workspace, "workspace", torch.uint8, min_numel=qkv_workspace_bytes(bucket, D, nq),
+          align=256)
+    st = load().sf_qkv_rope_gated(
+        _ptr(xn), _ptr(rec), _ptr(par), B1, N, bucket, _ptr(f), _ptr(src), _ptr(rows),
+        _ptr(count), _ptr(seg), _ptr(segcnt), _ptr(slot), _ptr(w_qkv), _ptr(b_qkv), _ptr(cos),
+        _ptr(sin), _ptr(pos), per_branch, table_rows, _ptr(q_scale), D, H, Hkv, hd, _ptr(q_buf),
+        _ptr(kv_buf), _ptr(workspace), workspace.numel(), _stream(stream))
+    _check(st, "sf_qkv_rope_gated")
 
 
 def attn_workspace_bytes(bucket: int, H: int, P: int) -> int:

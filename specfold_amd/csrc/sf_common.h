@@ -185,7 +185,7 @@ SF_DEV void sf_handoff_store(T* p, T v) {
 }
 template <typename T>
 SF_DEV T sf_handoff_load(const T* p) {
-#ifdef SF_PLAIN_HANDOFF
+#if defined(SF_PLAIN_HANDOFF) || defined(SF_PLAIN_HANDOFF_LOADS)
   return *p;
 #else
   return __builtin_nontemporal_load(p);

@@ -8,6 +8,7 @@
 // order, which equals the concatenation of the reference's per-branch
 // nonzero() lists.
 #include "sf_common.h"
+#include "sf_compact.h"
 
 namespace {
 
@@ -147,8 +148,7 @@ __global__ __launch_bounds__(256) void sf_gate_rows_kernel(
   }
 }
 
-// One workgroup of 1024 threads, thread t = flat row t: ballot/popcount scan of
-// the rec flags, ascending compaction, per-branch segments and the src chase.
+// One workgroup of 1024 threads, thread t = flat row t (gate_compact, sf_compact.h).
 __global__ __launch_bounds__(1024) void sf_gate_compact_kernel(
     const int8_t* __restrict__ rec, const int32_t* __restrict__ par, int B1, int N, int bucket,
     int32_t* __restrict__ f, int32_t* __restrict__ src, int32_t* __restrict__ rows,
@@ -156,49 +156,9 @@ __global__ __launch_bounds__(1024) void sf_gate_compact_kernel(
     int32_t* __restrict__ slot_out) {
   __shared__ int s_f[1024];
   __shared__ int s_slot[1024];
-  __shared__ int s_wave_tot[16];
-  const int BN = B1 * N;
-  const int t = threadIdx.x;
-  const int lane = t & 63;
-  const int w = t >> 6;
-  const int flag = (t < BN) ? (rec[t] != 0) : 0;
-  const unsigned long long bal = __ballot(flag);
-  const unsigned long long below = (lane == 0) ? 0ull : (bal & ((~0ull) >> (64 - lane)));
-  const int pre = __popcll(below);
-  if (lane == 0) s_wave_tot[w] = __popcll(bal);
-  __syncthreads();
-  int base = 0, total = 0;
-  for (int i = 0; i < 16; ++i) {
-    const int v = s_wave_tot[i];
-    base += (i < w) ? v : 0;
-    total += v;
-  }
-  const int slot = base + pre;  // exclusive prefix count of recomputed rows before t
-  const int b = (t < BN) ? t / N : 0;
-  const int n = (t < BN) ? t - b * N : 0;
-  if (t < BN) {
-    int p = par[b];
-    p = p < 0 ? 0 : (p >= B1 ? B1 - 1 : p);
-    const int fv = flag ? b : p;
-    s_f[t] = fv;
-    s_slot[t] = slot;
-    f[t] = fv;
-    if (flag && slot < bucket) rows[slot] = t;
-    if (slot_out) slot_out[t] = (flag && slot < bucket) ? slot : -1;
-  }
-  for (int s = t; s < bucket; s += blockDim.x)
-    if (s >= total) rows[s] = BN;
-  __syncthreads();
-  if (t < BN) {
-    const int first = s_slot[b * N];
-    if (flag) seg[b * N + (slot - first)] = t;
-    if (n == 0) segcnt[b] = ((b + 1 < B1) ? s_slot[(b + 1) * N] : total) - first;
-    // Chains strictly shorten towards branch 0, so B1 hops reach the fixed point.
-    int s = s_f[t];
-    for (int hop = 0; hop < B1; ++hop) s = s_f[s * N + n];
-    src[t] = s;
-  }
-  if (t == 0) *count = total;
+  __shared__ int s_tot[16];
+  const GateOut out{f, src, rows, count, seg, segcnt, slot_out};
+  gate_compact<1024, 1>(rec, par, B1, N, bucket, s_f, s_slot, s_tot, nullptr, true, out);
 }
 
 template <int VPL, bool RESID, bool ROOTS>
@@ -237,7 +197,7 @@ void launch_rows_mode(int D, const uint16_t* hidden, const uint16_t* ffn, const 
                       const int32_t* par, const uint16_t* ln_w, int B1, int N, float delta,
                       float eps, int gate_mode, uint16_t* hidden_out, int8_t* rec, float* rstd,
                       uint16_t* xn, hipStream_t st) {
-  const int mode = gate_mode & ~SF_GATE_ROOTS_BY_PARENT;
+  const int mode = gate_mode & ~(SF_GATE_ROOTS_BY_PARENT | SF_GATE_DEFER_COMPACT);
   if (gate_mode & SF_GATE_ROOTS_BY_PARENT)
     launch_rows_any<RESID, true>(D, hidden, ffn, src_prev, par, ln_w, B1, N, delta, eps, mode,
                                  hidden_out, rec, rstd, xn, st);
@@ -247,7 +207,7 @@ void launch_rows_mode(int D, const uint16_t* hidden, const uint16_t* ffn, const 
 }
 
 int check_gate_args(int B1, int N, int D, int bucket, int gate_mode) {
-  const int mode = gate_mode & ~SF_GATE_ROOTS_BY_PARENT;
+  const int mode = gate_mode & ~(SF_GATE_ROOTS_BY_PARENT | SF_GATE_DEFER_COMPACT);
   if (mode != SF_GATE_MODEL_DTYPE && mode != SF_GATE_FP32_SQUARED && mode != SF_GATE_ALL)
     return SF_ERR_ARG;
   if (B1 < 1 || B1 > 64 || N < 1 || B1 * N > 1024) return SF_ERR_SHAPE;
@@ -308,7 +268,7 @@ __global__ __launch_bounds__(64) void sf_parent_map_kernel(const int64_t* __rest
 
 }  // namespace
 
-extern "C" int sf_abi_version(void) { return 11; }
+extern "C" int sf_abi_version(void) { return 12; }
 
 extern "C" int sf_parent_map(const int64_t* tokens, int B1, int N, int32_t* par, int32_t* counts,
                              void* stream) {
@@ -324,16 +284,17 @@ extern "C" int sf_fold_gate(const uint16_t* hidden, const int32_t* par, const ui
                             int8_t* rec, int32_t* f, int32_t* src, int32_t* rows, int32_t* count,
                             int32_t* seg, int32_t* segcnt, int32_t* slot, float* rstd, uint16_t* xn,
                             void* stream) {
-  if (!hidden || !par || !ln_w || !rec || !f || !src || !rows || !count || !seg || !segcnt ||
-      !rstd || !xn)
-    return SF_ERR_ARG;
+  const bool defer = (gate_mode & SF_GATE_DEFER_COMPACT) != 0;
+  if (!hidden || !par || !ln_w || !rec || !rstd || !xn) return SF_ERR_ARG;
+  if (!defer && (!f || !src || !rows || !count || !seg || !segcnt)) return SF_ERR_ARG;
   const int chk = check_gate_args(B1, N, D, bucket, gate_mode);
   if (chk != SF_OK) return chk;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   launch_rows_mode<false>(D, hidden, nullptr, nullptr, par, ln_w, B1, N, delta, eps, gate_mode,
                          nullptr, rec, rstd, xn, st);
-  hipLaunchKernelGGL(sf_gate_compact_kernel, dim3(1), dim3(1024), 0, st, rec, par, B1, N, bucket,
-                     f, src, rows, count, seg, segcnt, slot);
+  if (!defer)
+    hipLaunchKernelGGL(sf_gate_compact_kernel, dim3(1), dim3(1024), 0, st, rec, par, B1, N,
+                       bucket, f, src, rows, count, seg, segcnt, slot);
   return sf_launch_status();
 }
 
@@ -344,9 +305,10 @@ extern "C" int sf_fold_gate_residual(const uint16_t* hp, const uint16_t* ffn,
                                      int8_t* rec, int32_t* f, int32_t* src, int32_t* rows,
                                      int32_t* count, int32_t* seg, int32_t* segcnt, int32_t* slot,
                                      float* rstd, uint16_t* xn, void* stream) {
-  if (!hp || !ffn || !src_prev || !par || !ln_w || !hidden_out || !rec || !f || !src || !rows ||
-      !count || !seg || !segcnt || !rstd || !xn)
+  const bool defer = (gate_mode & SF_GATE_DEFER_COMPACT) != 0;
+  if (!hp || !ffn || !src_prev || !par || !ln_w || !hidden_out || !rec || !rstd || !xn)
     return SF_ERR_ARG;
+  if (!defer && (!f || !src || !rows || !count || !seg || !segcnt)) return SF_ERR_ARG;
   if (hidden_out == hp) return SF_ERR_ARG;
   const int chk = check_gate_args(B1, N, D, bucket, gate_mode);
   if (chk != SF_OK) return chk;
@@ -354,8 +316,9 @@ extern "C" int sf_fold_gate_residual(const uint16_t* hp, const uint16_t* ffn,
   // the row kernel reads src_prev; only the compaction after it writes src
   launch_rows_mode<true>(D, hp, ffn, src_prev, par, ln_w, B1, N, delta, eps, gate_mode, hidden_out,
                         rec, rstd, xn, st);
-  hipLaunchKernelGGL(sf_gate_compact_kernel, dim3(1), dim3(1024), 0, st, rec, par, B1, N, bucket,
-                     f, src, rows, count, seg, segcnt, slot);
+  if (!defer)
+    hipLaunchKernelGGL(sf_gate_compact_kernel, dim3(1), dim3(1024), 0, st, rec, par, B1, N,
+                       bucket, f, src, rows, count, seg, segcnt, slot);
   return sf_launch_status();
 }
 

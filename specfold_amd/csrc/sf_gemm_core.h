@@ -18,6 +18,7 @@
 #pragma once
 
 #include "sf_common.h"
+#include "sf_compact.h"
 #include "sf_index.h"
 
 namespace sfg {
@@ -239,26 +240,52 @@ struct Epi {
   const uint16_t* res;  // residual (kResid), row stride ldo
 };
 
+// GATED: the A rows are the fold gate's compaction of rec (B1 x N flags), done
+// by every workgroup in its prologue (gate_compact) instead of read from a rows
+// table; workgroup 0 also writes the compaction's outputs `out` for the kernels
+// after this one.
+constexpr int kGateMaxRows = 1024;
+struct GateIn {
+  const int8_t* rec;
+  const int32_t* par;
+  int B1, N;
+  GateOut out;
+};
+
 // C = A[rows] . W^T on packed weights, stream-K over (tile, stage) units; WN column
 // tiles of 16 per wave (kSilu: WN = 2 = the gate and the up tile of the same 16
 // output columns).  All M <= MB rows in one pass over the weights (more rows:
 // one pass per MB rows).  Grid: plan_grid workgroups.
 // part: fp32 partial slots [slot][mcap][N] ([slot][mcap][2N] for kSilu).
-template <int WN, int MODE, int MB>
+// GATED: rows and the count come from the compaction of gate.rec (mcap = bucket).
+template <int WN, int MODE, int MB, bool GATED = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void gemm_sk_kernel(const uint16_t* __restrict__ A, const int32_t* __restrict__ a_rows, int lda,
                     const int32_t* __restrict__ count_p, int m_static, int mcap,
                     const uint16_t* __restrict__ W0, const uint16_t* __restrict__ W1, int K, int N,
-                    Plan plan, float* __restrict__ part, Epi ep) {
+                    Plan plan, float* __restrict__ part, Epi ep, GateIn gate) {
   constexpr int kMT = MB / 16;    // max m tiles of this kernel
   using St = Stage<MB, WN>;
   constexpr int R = St::kRing;
   __shared__ sf_u32x4 ring[R * St::kWords];
   __shared__ int rows_s[MB];
+  __shared__ int s_grows[GATED ? kGateMaxRows : 1];      // the compacted rows
+  __shared__ int s_gtot[GATED ? kGateMaxRows / 64 : 1];
+  int M;
+  if constexpr (GATED) {
+    // the ring's memory is free until the main loop: the compaction's scratch
+    static_assert(2 * kGateMaxRows * 4 <= R * St::kWords * 16, "gate scratch");
+    int* s_f = reinterpret_cast<int*>(ring);
+    const int total = gate_compact<kThreads, kGateMaxRows / kThreads>(
+        gate.rec, gate.par, gate.B1, gate.N, mcap, s_f, s_f + kGateMaxRows, s_gtot, s_grows,
+        blockIdx.x == 0, gate.out);
+    M = sf_imin(total, mcap);
+  } else {
+    M = count_p ? sf_imin(*count_p, mcap) : m_static;
+  }
   Ring<MB, WN> rg;
 #pragma unroll
   for (int j = 0; j < 8; ++j) rg.slot[j] = ring + (j < R ? j : 0) * St::kWords;
-  const int M = count_p ? sf_imin(*count_p, mcap) : m_static;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = tid >> 6;
@@ -272,7 +299,7 @@ void gemm_sk_kernel(const uint16_t* __restrict__ A, const int32_t* __restrict__ 
   __syncthreads();  // the previous pass's last readers of the row table are done
   if (tid < MB) {
     const int r = m0 + sf_imin(tid, mrows - 1);
-    rows_s[tid] = a_rows ? a_rows[r] : r;
+    rows_s[tid] = GATED ? s_grows[r] : (a_rows ? a_rows[r] : r);
   }
   __syncthreads();
   for (int u = g * plan.U; u < u_end;) {
@@ -388,18 +415,18 @@ void gemm_sk_kernel(const uint16_t* __restrict__ A, const int32_t* __restrict__ 
 
 // One pass over the weights for every row: the row block MB is the smallest of
 // 64 / 128 / 256 that holds mcap rows (A ring 8 / 8 / 4 stages, 64 / 128 / 128 KB).
-template <int WN, int MODE>
+template <int WN, int MODE, bool GATED = false>
 inline void launch_sk(const Plan& p, const uint16_t* A, const int32_t* a_rows, int lda,
                       const int32_t* count_p, int m_static, int mcap, const uint16_t* W0,
                       const uint16_t* W1, int K, int N, float* part, const Epi& ep,
-                      hipStream_t st) {
+                      hipStream_t st, const GateIn& gate = GateIn{}) {
   const dim3 grid(plan_grid(p));
   if (row_block(mcap) == 64)
-    hipLaunchKernelGGL((gemm_sk_kernel<WN, MODE, 64>), grid, dim3(kThreads), 0, st, A, a_rows, lda,
-                       count_p, m_static, mcap, W0, W1, K, N, p, part, ep);
+    hipLaunchKernelGGL((gemm_sk_kernel<WN, MODE, 64, GATED>), grid, dim3(kThreads), 0, st, A,
+                       a_rows, lda, count_p, m_static, mcap, W0, W1, K, N, p, part, ep, gate);
   else
-    hipLaunchKernelGGL((gemm_sk_kernel<WN, MODE, 128>), grid, dim3(kThreads), 0, st, A, a_rows,
-                       lda, count_p, m_static, mcap, W0, W1, K, N, p, part, ep);
+    hipLaunchKernelGGL((gemm_sk_kernel<WN, MODE, 128, GATED>), grid, dim3(kThreads), 0, st, A,
+                       a_rows, lda, count_p, m_static, mcap, W0, W1, K, N, p, part, ep, gate);
 }
 
 }  // namespace sfg

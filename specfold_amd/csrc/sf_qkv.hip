@@ -146,3 +146,48 @@ extern "C" int sf_qkv_rope_branches(const uint16_t* xn, const int32_t* rows,
                      N, H, Hkv, q_buf, kv_buf);
   return sf_launch_status();
 }
+
+// sf_qkv_rope (pos0_per_branch = 0) or sf_qkv_rope_branches (1) with the fold
+// gate's compaction in the GEMM's prologue, for a gate launched with
+// SF_GATE_DEFER_COMPACT: every GEMM workgroup compacts rec for its own A rows (one
+// launch fewer per layer), and workgroup 0 writes f, src, rows, count, seg, segcnt
+// and slot (may be NULL) as sf_fold_gate documents them, for the epilogue and the
+// kernels after it.  No counterpart in the reference (its gate and its QKV
+// projection are separate launches).
+extern "C" int sf_qkv_rope_gated(const uint16_t* xn, const int8_t* rec, const int32_t* par,
+                                 int B1, int N, int bucket, int32_t* f, int32_t* src,
+                                 int32_t* rows, int32_t* count, int32_t* seg, int32_t* segcnt,
+                                 int32_t* slot, const uint16_t* w_qkv, const uint16_t* b_qkv,
+                                 const uint16_t* cos_tab, const uint16_t* sin_tab,
+                                 const int32_t* pos0, int pos0_per_branch, int table_rows,
+                                 const float* q_scale, int D, int H, int Hkv, int hd,
+                                 uint16_t* q_buf, uint16_t* kv_buf, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+  if (!xn || !rec || !par || !f || !src || !rows || !count || !seg || !segcnt || !w_qkv ||
+      !cos_tab || !sin_tab || !q_buf || !kv_buf || !workspace || (pos0_per_branch && !pos0))
+    return SF_ERR_ARG;
+  if (hd != 128 || H < 1 || Hkv < 1 || H % Hkv != 0) return SF_ERR_SHAPE;
+  if (D < kKC || D % kKC != 0) return SF_ERR_SHAPE;
+  if (B1 < 1 || B1 > 64 || N < 1 || B1 * N > kGateMaxRows) return SF_ERR_SHAPE;
+  if (bucket < 1 || bucket > B1 * N) return SF_ERR_SHAPE;
+  if (!pos0) table_rows = N;
+  if (table_rows < N) return SF_ERR_SHAPE;
+  const int n_qkv = (H + 2 * Hkv) * hd;
+  if (workspace_bytes < sf_qkv_workspace_bytes(bucket, D, n_qkv)) return SF_ERR_WORKSPACE;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const Plan p = make_plan(n_qkv / 128, D / kKC);
+  float* part = reinterpret_cast<float*>(workspace);
+  const GateIn gate{rec, par, B1, N, GateOut{f, src, rows, count, seg, segcnt, slot}};
+  launch_sk<1, kPart, true>(p, xn, nullptr, D, nullptr, 0, bucket, w_qkv, nullptr, D, n_qkv, part,
+                            Epi{}, st, gate);
+  dim3 g2(min(bucket, 128), (H + 2 * Hkv + 3) / 4);
+  if (pos0_per_branch)
+    hipLaunchKernelGGL(sf_qkv_epilogue_kernel<true>, g2, dim3(256), 0, st, part, p, bucket, n_qkv,
+                       rows, count, b_qkv, cos_tab, sin_tab, pos0, table_rows, q_scale, N, H, Hkv,
+                       q_buf, kv_buf);
+  else
+    hipLaunchKernelGGL(sf_qkv_epilogue_kernel<false>, g2, dim3(256), 0, st, part, p, bucket,
+                       n_qkv, rows, count, b_qkv, cos_tab, sin_tab, pos0, table_rows, q_scale, N,
+                       H, Hkv, q_buf, kv_buf);
+  return sf_launch_status();
+}

@@ -235,6 +235,9 @@ class FoldedVerifyEngine:
         self.eps = float(rms_eps if rms_eps is not None else
                          getattr(cfg, "rms_norm_eps", 1e-6))
         self.gate_mode = gate_mode
+        # the gate's compaction runs in the QKV GEMM's prologue (one launch fewer per
+        # layer); False: the gate's own compaction kernel, then sf_qkv_rope
+        self.gated_qkv = True
         # Weights of the HIP GEMMs, packed once into the fragment-major layout the
         # weight-streaming kernels read (the reference packs W_qkv / W_gu once too,
         # fastdllm_v2_folded.py:77-87).  The module tree keeps its own tensors.
@@ -540,6 +543,9 @@ class FoldedVerifyEngine:
         base = self.base
         par = buf.par
         gate_mode = self.gate_mode
+        if self.gated_qkv:
+            # the compaction runs in the QKV GEMM's prologue (sf_qkv_rope_gated)
+            gate_mode |= _lib.SF_GATE_DEFER_COMPACT
         if batch is None:
             _lib.parent_map(tokens, par)          # on the device: no host round trip
         else:
@@ -572,7 +578,15 @@ class FoldedVerifyEngine:
                                         buf.src, buf.rows, count, buf.seg, segcnt, buf.slot,
                                         buf.rstd, buf.xn)
             w_qkv, b_qkv = self._packed[li]
-            if batch is None:
+            if self.gated_qkv:
+                # compaction (rows, count, src, seg, slot) + QKV + bias + RoPE
+                _lib.qkv_rope_gated(
+                    buf.xn, buf.rec, par, B1, N, bucket, buf.f, buf.src, buf.rows, count, buf.seg,
+                    segcnt, buf.slot, w_qkv, b_qkv, cos, sin,
+                    q_scale if batch is None else batch.q_scale_rows, D, H, Hkv, hd, buf.q_buf,
+                    buf.kv_buf, buf.ws_qkv, pos0=pos0 if batch is None else None,
+                    pos0_branch=None if batch is None else batch.pos0_branch)
+            elif batch is None:
                 _lib.qkv_rope(buf.xn, buf.rows, count, bucket, BN, w_qkv, b_qkv, cos, sin,
                               q_scale, N, D, H, Hkv, hd, buf.q_buf, buf.kv_buf, buf.ws_qkv,
                               pos0=pos0)
@@ -759,10 +773,13 @@ class FoldedVerifyEngine:
                                            device=self.device)
         scratch, normed, logits = shared["scratch"], shared["normed"], shared["logits"]
 
+        gate_mode = self.gate_mode | (_lib.SF_GATE_DEFER_COMPACT if self.gated_qkv else 0)
+
         def gate():
-            # the fused gate of a layer after the first (residual update + gate + compaction)
+            # the fused gate of a layer after the first (residual update + gate; the
+            # compaction too unless the QKV launcher runs it)
             _lib.fold_gate_residual(buf.hp, buf.ffn, buf.src, st["par"], lyr.input_layernorm.weight,
-                                    B1, N, D, bucket, st["delta"], self.eps, self.gate_mode,
+                                    B1, N, D, bucket, st["delta"], self.eps, gate_mode,
                                     scratch, buf.rec, buf.f, buf.src, buf.rows, count, buf.seg,
                                     segcnt, buf.slot, buf.rstd, buf.xn)
 
@@ -770,9 +787,15 @@ class FoldedVerifyEngine:
         pos0 = cache.length_dev if _device_cache(cache) else buf.pos0
 
         def qkv():
-            _lib.qkv_rope(buf.xn, buf.rows, count, bucket, BN, w_qkv, b_qkv, cos, sin,
-                          st["q_scale"], N, D, H, Hkv, hd, buf.q_buf, buf.kv_buf, buf.ws_qkv,
-                          pos0=pos0)
+            if self.gated_qkv:
+                _lib.qkv_rope_gated(buf.xn, buf.rec, st["par"], B1, N, bucket, buf.f, buf.src,
+                                    buf.rows, count, buf.seg, segcnt, buf.slot, w_qkv, b_qkv,
+                                    cos, sin, st["q_scale"], D, H, Hkv, hd, buf.q_buf,
+                                    buf.kv_buf, buf.ws_qkv, pos0=pos0)
+            else:
+                _lib.qkv_rope(buf.xn, buf.rows, count, bucket, BN, w_qkv, b_qkv, cos, sin,
+                              st["q_scale"], N, D, H, Hkv, hd, buf.q_buf, buf.kv_buf, buf.ws_qkv,
+                              pos0=pos0)
 
         def attn():
             self._attention(buf, cache, li, count, bucket, B1, N)

@@ -4,6 +4,9 @@ same inputs, bit for bit:
 * sf_fold_gate_residual  == sf_residual_gather_add then sf_fold_gate
 * sf_residual_post_norm  == bf16 add (torch) then sf_rows_rmsnorm of the recomputed rows
 * sf_residual_rmsnorm    == sf_residual_gather_add then sf_rows_rmsnorm of every row
+* sf_fold_gate(SF_GATE_DEFER_COMPACT) + sf_qkv_rope_gated
+                         == sf_fold_gate then sf_qkv_rope (or sf_qkv_rope_branches):
+                            every compaction output and the q/kv tables
 
 (each unfused step is itself checked against the reference semantics in
 test_gpu_gate.py / test_gpu_gemm.py)."""
@@ -123,3 +126,79 @@ def test_residual_rmsnorm_matches_unfused(D, seed):
     torch.cuda.synchronize()
     assert torch.equal(h, h_ref)
     assert torch.equal(out, out_ref)
+
+
+@pytest.mark.parametrize("D,H,Hkv,bucket,branches,seed", [
+    (3584, 28, 4, 256, False, 0),    # the 7B verify step
+    (1536, 12, 2, 40, False, 1),     # an overflowing bucket (count > bucket)
+    (3584, 28, 4, 256, True, 2),     # a batched step's per-branch positions and q scales
+])
+def test_qkv_rope_gated_matches_unfused(D, H, Hkv, bucket, branches, seed):
+    g = torch.Generator().manual_seed(seed)
+    parents = TREE_PARENTS
+    B1, N, hd = len(parents), 32, 128
+    BN = B1 * N
+    nq = (H + 2 * Hkv) * hd
+    hidden = perturbed_hidden(parents, N, D, g).reshape(BN, D).cuda()
+    par = torch.tensor([0] + [int(p) for p in parents[1:]], **I32)
+    ln_w = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).cuda()
+    w = (0.02 * torch.randn(nq, D, generator=g)).to(torch.bfloat16).cuda()
+    wp = _lib.pack_weight(w)
+    b = (0.1 * torch.randn(nq, generator=g)).to(torch.bfloat16).cuda()
+    T = 4096
+    ang = torch.arange(T, dtype=torch.float32)[:, None] * (1e-4 ** (torch.arange(64) / 64))
+    cos = torch.cat([ang.cos(), ang.cos()], 1).to(torch.bfloat16).cuda()
+    sin = torch.cat([ang.sin(), ang.sin()], 1).to(torch.bfloat16).cuda()
+    if branches:
+        pos = torch.randint(0, T - N, (B1,), generator=g, dtype=torch.int32).cuda()
+        q_scale = (1 + 0.1 * torch.rand(BN, generator=g)).cuda()
+    else:
+        pos = torch.tensor([1500], **I32)
+        q_scale = (1 + 0.1 * torch.rand(N, generator=g)).cuda()
+    mode, delta = _lib.SF_GATE_MODEL_DTYPE, 0.1
+    ws = torch.zeros(_lib.qkv_workspace_bytes(bucket, D, nq), dtype=torch.uint8, device="cuda")
+
+    def tables():
+        return (torch.full(((BN + 1) * H * hd,), 7.0, dtype=torch.bfloat16, device="cuda"),
+                torch.full(((BN + 1) * 2 * Hkv * hd,), 7.0, dtype=torch.bfloat16, device="cuda"))
+
+    u = gate_buffers(B1, N, D, bucket)
+    _lib.fold_gate(hidden, par, ln_w, B1, N, bucket, delta, 1e-6, mode, u["rec"], u["f"],
+                   u["src"], u["rows"], u["count"], u["seg"], u["segcnt"], u["rstd"], u["xn"],
+                   slot=u["slot"])
+    q_u, kv_u = tables()
+    if branches:
+        _lib.qkv_rope_branches(u["xn"], u["rows"], u["count"], bucket, BN, wp, b, cos, sin,
+                               q_scale, N, D, H, Hkv, hd, q_u, kv_u, ws, pos)
+    else:
+        _lib.qkv_rope(u["xn"], u["rows"], u["count"], bucket, BN, wp, b, cos, sin, q_scale, N, D,
+                      H, Hkv, hd, q_u, kv_u, ws, pos0=pos)
+
+    fz = gate_buffers(B1, N, D, bucket)
+    _lib.fold_gate(hidden, par, ln_w, B1, N, bucket, delta, 1e-6,
+                   mode | _lib.SF_GATE_DEFER_COMPACT, fz["rec"], fz["f"], fz["src"], fz["rows"],
+                   fz["count"], fz["seg"], fz["segcnt"], fz["rstd"], fz["xn"], slot=fz["slot"])
+    torch.cuda.synchronize()
+    # the deferred gate leaves the compaction's outputs alone
+    assert int(fz["count"][0]) == 0 and int(fz["rows"][0]) == -7
+    q_f, kv_f = tables()
+    _lib.qkv_rope_gated(fz["xn"], fz["rec"], par, B1, N, bucket, fz["f"], fz["src"], fz["rows"],
+                        fz["count"], fz["seg"], fz["segcnt"], fz["slot"], wp, b, cos, sin,
+                        q_scale, D, H, Hkv, hd, q_f, kv_f, ws,
+                        pos0=None if branches else pos, pos0_branch=pos if branches else None)
+    torch.cuda.synchronize()
+    for k in ("rec", "f", "src", "rows", "count", "segcnt", "slot", "rstd"):
+        assert torch.equal(fz[k], u[k]), k
+    for bb in range(B1):
+        c = int(u["segcnt"][bb])
+        assert torch.equal(fz["seg"][bb * N:bb * N + c], u["seg"][bb * N:bb * N + c])
+    count = int(u["count"][0])
+    assert N < count < BN
+    if bucket < count:
+        assert int(fz["count"][0]) == count   # the count of an overflow, rows cut at bucket
+    assert torch.equal(q_f, q_u) and torch.equal(kv_f, kv_u)
+    rows = u["rows"][:min(count, bucket)].long()
+    assert torch.equal(fz["xn"][rows], u["xn"][rows])
+    # the projection was written (not the fill) for the recomputed rows
+    assert not torch.equal(q_f.view(BN + 1, H * hd)[rows], torch.full_like(
+        q_f.view(BN + 1, H * hd)[rows], 7.0))
