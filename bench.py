@@ -190,7 +190,8 @@ PMC_KERNELS = {
     # the head: the whole rounds' 256-column kernel, then (where V leaves a partial
     # round) the 128-column one
     "lm_head": ("head_kernel<8, 1,", "?head_kernel<8, 2,"),
-    "gate": ("sf_gate_rows_kernel", "sf_gate_compact_kernel"),
+    # the compaction runs in the gated QKV GEMM unless the engine's gated_qkv is off
+    "gate": ("sf_gate_rows_kernel", "?sf_gate_compact_kernel"),
 }
 
 
@@ -455,10 +456,10 @@ def kernel_table(w, eng, B1, N, kernel_iters):
 
 # The engine's calls into the library per entry point of the kernel table (the
 # entry points launched by FoldedVerifyEngine._run_layers and its head).
-IN_STEP_CALLS = {"gate": "fold_gate_residual", "qkv": "qkv_rope", "attn": "attn_rows",
-                 "o_proj": "o_proj_post_norm", "gate_up": "ffn_gate_up",
-                 "down": "ffn_down_scatter", "final_norm": "residual_rmsnorm",
-                 "lm_head": "head_logits"}
+IN_STEP_CALLS = {"gate": ("fold_gate_residual",), "qkv": ("qkv_rope", "qkv_rope_gated"),
+                 "attn": ("attn_rows",), "o_proj": ("o_proj_post_norm",),
+                 "gate_up": ("ffn_gate_up",), "down": ("ffn_down_scatter",),
+                 "final_norm": ("residual_rmsnorm",), "lm_head": ("head_logits",)}
 
 
 def in_step_times(run_step, reps: int = 3) -> dict:
@@ -473,18 +474,19 @@ def in_step_times(run_step, reps: int = 3) -> dict:
     from specfold_amd import _lib
     spans = {k: [] for k in IN_STEP_CALLS}
     saved = {}
-    for name, fn in IN_STEP_CALLS.items():
-        orig = getattr(_lib, fn)
-        saved[fn] = orig
+    for name, fns in IN_STEP_CALLS.items():
+        for fn in fns:
+            orig = getattr(_lib, fn)
+            saved[fn] = orig
 
-        def wrapped(*a, _orig=orig, _name=name, **k):
-            s = torch.cuda.Event(enable_timing=True)
-            e = torch.cuda.Event(enable_timing=True)
-            s.record()
-            _orig(*a, **k)
-            e.record()
-            spans[_name].append((s, e))
-        setattr(_lib, fn, wrapped)
+            def wrapped(*a, _orig=orig, _name=name, **k):
+                s = torch.cuda.Event(enable_timing=True)
+                e = torch.cuda.Event(enable_timing=True)
+                s.record()
+                _orig(*a, **k)
+                e.record()
+                spans[_name].append((s, e))
+            setattr(_lib, fn, wrapped)
     empty = []
     try:
         for _ in range(reps):
