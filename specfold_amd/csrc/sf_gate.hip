@@ -12,7 +12,8 @@
 
 namespace {
 
-constexpr int kGateWaves = 4;  // one wave per flat row, 4 rows per workgroup
+constexpr int kGateWaves = 1;  // one wave per flat row and workgroup (the rows spread over
+                                // the CUs: 5.4-5.8 against 6.5-6.7 us with 4 rows per workgroup)
 constexpr int kMaxVecPerLane = 16;  // 16 x 8 bf16 x 64 lanes = 8192 columns
 
 // One wave per flat row r = b*N + n: three fp32 sums over D (x^2, residual^2,
@@ -22,7 +23,7 @@ constexpr int kMaxVecPerLane = 16;  // 16 x 8 bf16 x 64 lanes = 8192 columns
 // fastdllm_v2_folded.py:218), for the row and for its parent row, and x[r] is
 // written to hidden_out.  `par` may be NULL (every row its own parent).
 template <int VPL, bool RESID, bool ROOTS>
-__global__ __launch_bounds__(256) void sf_gate_rows_kernel(
+__global__ __launch_bounds__(kGateWaves * 64) void sf_gate_rows_kernel(
     const uint16_t* __restrict__ hidden, const uint16_t* __restrict__ ffn,
     const int32_t* __restrict__ src_prev, const int32_t* __restrict__ par,
     const uint16_t* __restrict__ ln_w, int B1, int N, int D, float delta, float eps, int mode,
@@ -168,8 +169,9 @@ void launch_rows(const uint16_t* hidden, const uint16_t* ffn, const int32_t* src
                  uint16_t* xn, hipStream_t st) {
   const int BN = B1 * N;
   dim3 grid((BN + kGateWaves - 1) / kGateWaves);
-  hipLaunchKernelGGL((sf_gate_rows_kernel<VPL, RESID, ROOTS>), grid, dim3(256), 0, st, hidden, ffn,
-                     src_prev, par, ln_w, B1, N, D, delta, eps, mode, hidden_out, rec, rstd, xn);
+  hipLaunchKernelGGL((sf_gate_rows_kernel<VPL, RESID, ROOTS>), grid, dim3(kGateWaves * 64), 0, st,
+                     hidden, ffn, src_prev, par, ln_w, B1, N, D, delta, eps, mode, hidden_out, rec,
+                     rstd, xn);
 }
 
 template <bool RESID, bool ROOTS>
