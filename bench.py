@@ -783,6 +783,27 @@ def main(argv=None) -> int:
             lat.append(s.elapsed_time(e))
     verify_ms = statistics.median(lat)
     counts = gen.last_stats.counts
+    # the same step as the decode loop runs it: the head only on the rows the loop
+    # reads (a small block and the next one: the generator's head_rows window)
+    win_ms = None
+    if hasattr(gen, "head_rows") and w.family == "fastdllm":
+        sbs = gen.small_block_size
+        gen.head_rows = (0, min(2 * sbs, w.block))
+        lat_w = []
+        try:
+            for i in range(args.verify_iters + 3):
+                s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                s.record()
+                gen._batched_block_forward(batched, cache)
+                e.record()
+                e.synchronize()
+                if i >= 3:
+                    lat_w.append(s.elapsed_time(e))
+        finally:
+            gen.head_rows = None
+        win_ms = statistics.median(lat_w)
+        print(f"[bench] verify step with the decode window's head rows (2 small blocks) "
+              f"median {win_ms:.3f} ms", file=sys.stderr, flush=True)
     R = round(sum(counts) / len(counts))
     B1, N = batched.shape
     fold_ratio_step = 1 - (sum(counts) - len(counts) * N) / ((B1 - 1) * N * len(counts))
@@ -874,6 +895,7 @@ def main(argv=None) -> int:
                    "lockstep": lockstep,
                    "parallelism": "none (1 GPU)"},
         "verify_step_ms": round(verify_ms, 4),
+        "verify_step_ms_decode_window": None if win_ms is None else round(win_ms, 4),
         "verify_step_batched": batched_step,
         "verify_step_prefix": P,
         "verify_recomputed_rows_mean": R,

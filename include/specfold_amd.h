@@ -75,7 +75,8 @@ const char* sf_status_string(int status);
  * 10: sf_head_logits (the head with the Fast-dLLM shift); sf_lm_head runs on it.
  * 11: attention merges each recomputed row's prefix partials in the kernel that
  *     attends its rows: the workspace holds the range partials only; B1 <= 64.
- * 12: SF_GATE_DEFER_COMPACT and sf_qkv_rope_gated (the compaction in the QKV GEMM). */
+ * 12: SF_GATE_DEFER_COMPACT and sf_qkv_rope_gated (the compaction in the QKV GEMM).
+ * 13: sf_head_logits_rows (the head for the rows a decode step reads). */
 int sf_abi_version(void);
 
 /*
@@ -361,6 +362,21 @@ int sf_lm_head(const uint16_t* x, int M, const uint16_t* w, int D, int V, uint16
  */
 int sf_head_logits(const uint16_t* x, int M, const uint16_t* w, int D, int V, int shift_n,
                    uint16_t* logits, long long ld_out, void* stream);
+/* sf_head_logits for a row window: of every N-row block of x (M % N == 0), only the
+ * logits rows of positions [row_lo, row_lo + row_n) are computed and written (the
+ * other rows of logits are left as they are); shift != 0: position n's logits come
+ * from x row n - 1 of its block (n > 0) or n itself (n = 0), as above.  The rows a
+ * decode step reads (the reference loop slices the small block of the main
+ * branch and, on a later draft hit, of a cached draft's logits,
+ * specfold/generate/fastdllm_v2_generation.py:610-651), so the head does the work
+ * of those rows only: at most 128 of them take a pass with half the X bytes and
+ * MFMAs per column.  Each row's values equal the full call's bit for bit.
+ * sf_head_logits(shift_n) is this with N = shift_n (M without shift), the whole
+ * block.  Limits: as sf_head_logits, with 0 <= row_lo, row_n >= 1,
+ * row_lo + row_n <= N. */
+int sf_head_logits_rows(const uint16_t* x, int M, const uint16_t* w, int D, int V, int N,
+                        int shift, int row_lo, int row_n, uint16_t* logits, long long ld_out,
+                        void* stream);
 
 /* ---- greedy decoding statistics of logits rows ----------------------------------
  * Replaces, at temperature 0, the top-p sampler of the reference decode loop

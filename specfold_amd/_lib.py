@@ -71,6 +71,7 @@ SIGNATURES = {
     "sf_residual_gather_add": (_i, [_vp, _vp, _vp, _i, _i, _i, _vp, _vp]),
     "sf_lm_head": (_i, [_vp, _i, _vp, _i, _i, _vp, _vp]),
     "sf_head_logits": (_i, [_vp, _i, _vp, _i, _i, _i, _vp, _ll, _vp]),
+    "sf_head_logits_rows": (_i, [_vp, _i, _vp, _i, _i, _i, _i, _i, _i, _vp, _ll, _vp]),
     "sf_logit_stats_workspace_bytes": (ctypes.c_size_t, [_i]),
     "sf_parent_map": (_i, [_vp, _i, _i, _vp, _vp, _vp]),
     "sf_logit_stats": (_i, [_vp, _i, _i, _ll, _f] + [_vp] * 7 + [_vp, ctypes.c_size_t, _vp]),
@@ -571,6 +572,23 @@ def head_logits(x, M, w, D, V, logits, shift_n: int = 0, stream=None) -> None:
     st = load().sf_head_logits(_ptr(x), M, _ptr(w), D, V, int(shift_n), _ptr(logits), ld,
                                _stream(stream))
     _check(st, "sf_head_logits")
+
+
+def head_logits_rows(x, M, w, D, V, logits, N: int, shift: bool, row_lo: int, row_n: int,
+                     stream=None) -> None:
+    """The head for a row window: of every N-row block of x [M, D], the logits rows
+    of positions [row_lo, row_lo + row_n) (Fast-dLLM's shift with ``shift``: row n
+    from x row n - 1, row 0 from itself); the other rows of ``logits`` are not
+    written (sf_head_logits_rows)."""
+    _need(x, "x", torch.bfloat16, min_numel=M * D)
+    _need(w, "w", torch.bfloat16, numel=V * D)
+    ld = logits.stride(0) if logits.dim() == 2 else V
+    if logits.dtype != torch.bfloat16 or logits.stride(-1) != 1 or \
+            logits.storage_offset() + (M - 1) * ld + V > logits.untyped_storage().nbytes() // 2:
+        raise ValueError(f"logits must be bf16 rows of stride {ld} holding {M} x {V}")
+    st = load().sf_head_logits_rows(_ptr(x), M, _ptr(w), D, V, int(N), 1 if shift else 0,
+                                    int(row_lo), int(row_n), _ptr(logits), ld, _stream(stream))
+    _check(st, "sf_head_logits_rows")
 
 
 class LogitStats:

@@ -39,35 +39,56 @@ namespace {
 
 using namespace sfg;
 
-constexpr int kHRows = 256;                  // rows per pass: 16 m tiles of 16
-constexpr int kHMT = kHRows / 16;
-constexpr int kHStageWords = 2 * kHMT * 64;  // 16-byte words of X per stage (32 KB)
+// Rows of a launch: output row r (r < Mo, the launch's rows in order) is row
+// b*N + n of the logits, b = r / W, n = lo + r % W: every N-row block's positions
+// [lo, lo + W); its input row is b*N + n - 1 under Fast-dLLM's shift (n > 0), else
+// b*N + n.  The whole block (lo = 0, W = N) gives every row; N = Mo, no shift: the
+// plain product.
+struct HeadRows {
+  int N, lo, W, shift;
+};
+SF_DEV int head_out_row(int r, const HeadRows& hr) {
+  const int b = r / hr.W;
+  return b * hr.N + hr.lo + (r - b * hr.W);
+}
+SF_DEV int head_in_row(int r, const HeadRows& hr) {
+  const int b = r / hr.W;
+  const int n = hr.lo + (r - b * hr.W);
+  return b * hr.N + ((hr.shift && n > 0) ? n - 1 : n);
+}
 
 // A workgroup of NW waves = RG row groups x NW / RG column groups of WN 16-column
-// tiles; TN columns per workgroup tile; a ring of R 64-K stages (X in LDS, each
-// wave's weight fragments in VGPRs), R - 1 of them in flight.
-template <int NW, int RG, int WN, int R>
+// tiles over a pass of HR rows (256 or 128); TN columns per workgroup tile; a ring
+// of R 64-K stages (X in LDS, each wave's weight fragments in VGPRs), R - 1 of
+// them in flight.
+template <int NW, int RG, int WN, int R, int HR>
 struct HeadShape {
   static constexpr int kRing = R;
+  static constexpr int kRows = HR;                 // rows per pass
+  static constexpr int kMT = HR / 16;              // m tiles per pass
+  static constexpr int kStageWords = 2 * kMT * 64; // 16-byte words of X per stage
   static constexpr int kCG = NW / RG;              // column groups
-  static constexpr int kNMT = kHMT / RG;           // m tiles per wave
+  static constexpr int kNMT = kMT / RG;            // m tiles per wave
   static constexpr int kTN = kCG * WN * 16;        // columns of a tile
-  static constexpr int kDA = 2 * kHMT / NW;        // X copies per wave per stage
+  static constexpr int kDA = 2 * kMT / NW;         // X copies per wave per stage
   static constexpr int kDB = 2 * WN;               // weight loads per wave per stage
-  static_assert(kDA * NW == 2 * kHMT, "the X copies of a stage divide over the waves");
+  static_assert(kDA * NW == 2 * kMT, "the X copies of a stage divide over the waves");
   // X fragments read (and waited for) FG m tiles at a time: 4 where the
   // accumulators leave no room for 8
-  static constexpr int kFG = kNMT * WN >= 32 ? 4 : 8;
+  static constexpr int kFG = kNMT * WN >= 32 ? 4 : (kNMT < 8 ? kNMT : 8);
   static_assert(kNMT % kFG == 0, "whole fragment groups");
 };
-// The whole rounds: 4 waves (one per SIMD, 512 registers each: 256 accumulators,
-// three 64-K stages of weight fragments) x 64 columns over all 256 rows -- each
-// weight byte loaded by one wave, 64 KB of weights in flight per CU.
-using HeadMain = HeadShape<8, 1, 2, 3>;
+// Passes of 256 rows.  The whole rounds: 8 waves x 32 columns over all 256 rows
+// -- each weight byte loaded by one wave, 64 KB of weights in flight per CU.
+using HeadMain = HeadShape<8, 1, 2, 3, 256>;
 // The partial last round: 8 waves = 2 row groups x 4 column groups of 32 columns
 // (each weight block loaded by both row groups), 128-column tiles spread over
 // twice as many CUs.
-using HeadTail = HeadShape<8, 2, 2, 4>;
+using HeadTail = HeadShape<8, 2, 2, 4, 256>;
+// Passes of at most 128 rows (a row window of the block): the same tiles with half
+// the X bytes and MFMAs per column, and a ring one stage deeper.
+using HeadMain128 = HeadShape<8, 1, 2, 4, 128>;
+using HeadTail128 = HeadShape<8, 2, 2, 4, 128>;
 
 // The X fragments of FG consecutive m tiles (1 KB apart) from LDS byte address a,
 // without waiting (sf_lds_read16 with compile-time offsets).
@@ -89,25 +110,17 @@ SF_DEV void head_stages(int sb, int S, F& f) {
   }
 }
 
-// Output row of block row m_glob, or -1: shift_n = 0 stores every row in place;
-// shift_n = N > 0 (Fast-dLLM) moves row (b, n) of each N-row block to (b, n + 1)
-// and drops (b, N - 1); (b, 0) is also stored in place (`second`).
-SF_DEV int head_row(int m_glob, int shift_n, bool second) {
-  if (shift_n == 0) return second ? -1 : m_glob;
-  const int n = m_glob % shift_n;
-  if (second) return n == 0 ? m_glob : -1;
-  return n == shift_n - 1 ? -1 : m_glob + 1;
-}
-
-// One pass of at most 256 rows over the column tiles t0 + blockIdx.x of TN
-// columns.  X: this pass's rows (row stride K); m0: the pass's first row in the
-// block (for the shift); W: packed [V, K]; out: row stride ldo, indexed by block
-// row.
-template <int NW, int RG, int WN, int R>
+// One pass of at most HR rows (the launch's output rows [m0, m0 + HR) of Mo, in
+// the row map hr) over the column tiles t0 + blockIdx.x of TN columns.  X: the
+// input rows (row stride K); W: packed [V, K]; out: row stride ldo.
+template <int NW, int RG, int WN, int R, int HR>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(8 / NW, 8 / NW)))
-void head_kernel(const uint16_t* __restrict__ X, int M, int m0, const uint16_t* __restrict__ W,
-                 int K, int t0, int shift_n, uint16_t* __restrict__ out, long long ldo) {
-  using Sh = HeadShape<NW, RG, WN, R>;
+void head_kernel(const uint16_t* __restrict__ X, int Mo, int m0, HeadRows hr,
+                 const uint16_t* __restrict__ W, int K, int t0, uint16_t* __restrict__ out,
+                 long long ldo) {
+  using Sh = HeadShape<NW, RG, WN, R, HR>;
+  constexpr int kHMT = Sh::kMT;
+  constexpr int kHStageWords = Sh::kStageWords;
   constexpr int kHDA = Sh::kDA;
   constexpr int kHDB = Sh::kDB;
   constexpr int kHWN = WN;
@@ -127,16 +140,17 @@ void head_kernel(const uint16_t* __restrict__ X, int M, int m0, const uint16_t* 
   const int S = K / kKC;
   const int slast = S - 1;
 
-  // X copies: copy q = wv + NW*j is (chunk q / 16, m tile q % 16); lane L brings
-  // row L/4 of the tile (rows past M re-read row M - 1), unit a_copy_unit(L)
+  // X copies: copy q = wv + NW*j is (chunk q / kHMT, m tile q % kHMT); lane L
+  // brings pass row L/4 of the tile (rows past Mo re-read the last one), unit
+  // a_copy_unit(L), from its input row
   const uint16_t* asrc[kHDA];
   int adst[kHDA];
 #pragma unroll
   for (int j = 0; j < kHDA; ++j) {
     const int q = wv + NW * j;
     const int ch = q / kHMT, mt = q - ch * kHMT;
-    const int r = sf_imin(mt * 16 + (lane >> 2), M - 1);
-    asrc[j] = X + (size_t)r * K + ch * 32 + a_copy_unit(lane) * 8;
+    const int r = sf_imin(m0 + mt * 16 + (lane >> 2), Mo - 1);
+    asrc[j] = X + (size_t)head_in_row(r, hr) * K + ch * 32 + a_copy_unit(lane) * 8;
     adst[j] = (ch * kHMT + mt) * 64;
   }
   // this lane's weight streams: 16-column tiles t*TN/16 + cg*WN + tt
@@ -223,27 +237,22 @@ void head_kernel(const uint16_t* __restrict__ X, int M, int m0, const uint16_t* 
   // drain the clamped re-issues past the last stage before the workgroup exits
   sf_wait_vm_barrier<0>();
 
-  // lane: row rg*128*(RG-1) + 16 i + lane%16 of the pass, columns col0 + 16 tt .. +4
+  // lane: row (rg*NMT + i)*16 + lane%16 of the pass, columns col0 + 16 tt .. +4
   const int col0 = t * TN + cg * kHWN * 16 + (lane >> 4) * 4;
 #pragma unroll
   for (int i = 0; i < NMT; ++i) {
-    const int row = (rg * NMT + i) * 16 + (lane & 15);
-    if (row < M) {
+    const int row = m0 + (rg * NMT + i) * 16 + (lane & 15);
+    if (row < Mo) {
       sf_u32x2 v[kHWN];
 #pragma unroll
       for (int tt = 0; tt < kHWN; ++tt) {
         v[tt][0] = sf_pack2(acc[i][tt][0], acc[i][tt][1]);
         v[tt][1] = sf_pack2(acc[i][tt][2], acc[i][tt][3]);
       }
+      const size_t orow = (size_t)head_out_row(row, hr);
 #pragma unroll
-      for (int second = 0; second < 2; ++second) {
-        const int orow = head_row(m0 + row, shift_n, second != 0);
-        if (orow >= 0) {
-#pragma unroll
-          for (int tt = 0; tt < kHWN; ++tt)
-            *reinterpret_cast<sf_u32x2*>(out + (size_t)orow * ldo + col0 + tt * 16) = v[tt];
-        }
-      }
+      for (int tt = 0; tt < kHWN; ++tt)
+        *reinterpret_cast<sf_u32x2*>(out + orow * ldo + col0 + tt * 16) = v[tt];
     }
   }
 }
@@ -252,40 +261,57 @@ bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0;
 
 }  // namespace
 
-extern "C" int sf_head_logits(const uint16_t* x, int M, const uint16_t* w, int D, int V,
-                              int shift_n, uint16_t* logits, long long ld_out, void* stream);
+namespace {
 
-extern "C" int sf_lm_head(const uint16_t* x, int M, const uint16_t* w, int D, int V,
-                          uint16_t* logits, void* stream) {
-  return sf_head_logits(x, M, w, D, V, 0, logits, V, stream);
+// Whole rounds of the main shape's tiles (one per CU), the rest in the tail shape's
+// (the partial last round spread over up to twice the CUs); passes of Main::kRows.
+template <class Main, class Tail>
+void head_launch(const uint16_t* x, int Mo, const HeadRows& hr, const uint16_t* w, int D, int V,
+                 uint16_t* logits, long long ld_out, hipStream_t st) {
+  constexpr int kCUs = 256;
+  const int t_main = V / Main::kTN;
+  const int n_main = (t_main / kCUs) * kCUs;
+  const int n_rest = (V - n_main * Main::kTN) / Tail::kTN;
+  for (int m0 = 0; m0 < Mo; m0 += Main::kRows) {
+    if (n_main)
+      hipLaunchKernelGGL((head_kernel<8, 1, 2, Main::kRing, Main::kRows>), dim3(n_main),
+                         dim3(8 * 64), 0, st, x, Mo, m0, hr, w, D, 0, logits, ld_out);
+    if (n_rest)
+      hipLaunchKernelGGL((head_kernel<8, 2, 2, Tail::kRing, Tail::kRows>), dim3(n_rest),
+                         dim3(8 * 64), 0, st, x, Mo, m0, hr, w, D,
+                         n_main * (Main::kTN / Tail::kTN), logits, ld_out);
+  }
+}
+
+}  // namespace
+
+extern "C" int sf_head_logits_rows(const uint16_t* x, int M, const uint16_t* w, int D, int V,
+                                   int N, int shift, int row_lo, int row_n, uint16_t* logits,
+                                   long long ld_out, void* stream) {
+  if (!x || !w || !logits) return SF_ERR_ARG;
+  if (M < 1 || M > 1024 || D < kKC || D % kKC || V < HeadTail::kTN || V % HeadTail::kTN ||
+      ld_out < V || ld_out % 4 || !aligned16(x) || !aligned16(w) ||
+      reinterpret_cast<uintptr_t>(logits) % 8)
+    return SF_ERR_SHAPE;
+  if (N < 1 || M % N || row_lo < 0 || row_n < 1 || row_lo + row_n > N) return SF_ERR_SHAPE;
+  const HeadRows hr{N, row_lo, row_n, shift ? 1 : 0};
+  const int Mo = (M / N) * row_n;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (Mo <= HeadMain128::kRows)
+    head_launch<HeadMain128, HeadTail128>(x, Mo, hr, w, D, V, logits, ld_out, st);
+  else
+    head_launch<HeadMain, HeadTail>(x, Mo, hr, w, D, V, logits, ld_out, st);
+  return sf_launch_status();
 }
 
 extern "C" int sf_head_logits(const uint16_t* x, int M, const uint16_t* w, int D, int V,
                               int shift_n, uint16_t* logits, long long ld_out, void* stream) {
-  if (!x || !w || !logits) return SF_ERR_ARG;
-  if (M < 1 || M > 1024 || D < kKC || D % kKC || V < HeadTail::kTN || V % HeadTail::kTN ||
-      ld_out < V ||
-      ld_out % 4 || !aligned16(x) || !aligned16(w) || reinterpret_cast<uintptr_t>(logits) % 8)
-    return SF_ERR_SHAPE;
-  if (shift_n < 0 || shift_n == 1 || (shift_n > 0 && M % shift_n)) return SF_ERR_SHAPE;
+  if (M < 1 || shift_n < 0 || shift_n == 1 || (shift_n > 0 && M % shift_n)) return SF_ERR_SHAPE;
+  const int N = shift_n > 0 ? shift_n : M;
+  return sf_head_logits_rows(x, M, w, D, V, N, shift_n > 0, 0, N, logits, ld_out, stream);
+}
 
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  // whole rounds of 256-column tiles (one per CU), the rest in 128-column tiles
-  // (the partial last round spread over up to twice the CUs)
-  constexpr int kCUs = 256;
-  const int t_main = V / HeadMain::kTN;
-  const int n_main = (t_main / kCUs) * kCUs;
-  const int n_rest = (V - n_main * HeadMain::kTN) / HeadTail::kTN;
-  for (int m0 = 0; m0 < M; m0 += kHRows) {
-    const int mb = sf_imin(kHRows, M - m0);
-    const uint16_t* xp = x + (size_t)m0 * D;
-    if (n_main)
-      hipLaunchKernelGGL((head_kernel<8, 1, 2, 3>), dim3(n_main), dim3(8 * 64), 0, st, xp, mb,
-                         m0, w, D, 0, shift_n, logits, ld_out);
-    if (n_rest)
-      hipLaunchKernelGGL((head_kernel<8, 2, 2, 4>), dim3(n_rest), dim3(8 * 64), 0, st, xp, mb,
-                         m0, w, D, n_main * (HeadMain::kTN / HeadTail::kTN), shift_n, logits,
-                         ld_out);
-  }
-  return sf_launch_status();
+extern "C" int sf_lm_head(const uint16_t* x, int M, const uint16_t* w, int D, int V,
+                          uint16_t* logits, void* stream) {
+  return sf_head_logits(x, M, w, D, V, 0, logits, V, stream);
 }

@@ -277,17 +277,24 @@ class FoldedVerifyEngine:
         self._mirror: Optional[ContiguousMirror] = None   # reference-style caches
 
     def lm_head(self, x: torch.Tensor, out: Optional[torch.Tensor] = None,
-                shift_n: int = 0) -> torch.Tensor:
+                shift_n: int = 0, rows: Optional[Tuple[int, int, int]] = None) -> torch.Tensor:
         """logits [M, V] = x . Wlm^T for every row of x [M, D] (sf_head_logits on the
         packed head weights; ``out``: an [M, V_pad] bf16 buffer, else a fresh one).
         shift_n = N: x holds blocks of N rows and the result is Fast-dLLM's shifted
         logits (row (b, n) takes row (b, n - 1)'s logits, row (b, 0) its own;
         fastdllm_v2_generation.py:121-126), written so by the head's stores.  A view of
-        V columns (rows of V_pad elements, contiguous when V % 128 == 0)."""
+        V columns (rows of V_pad elements, contiguous when V % 128 == 0).
+        ``rows`` = (N, lo, n): only positions [lo, lo + n) of every N-row block are
+        computed (the rest of ``out`` is not written): the rows a decode step reads."""
         M = x.shape[0]
         if out is None:
             out = torch.empty(M, self.V_pad, dtype=torch.bfloat16, device=self.device)
-        _lib.head_logits(x, M, self._packed_head, self.D, self.V_pad, out, shift_n=shift_n)
+        if rows is None:
+            _lib.head_logits(x, M, self._packed_head, self.D, self.V_pad, out, shift_n=shift_n)
+        else:
+            blk, lo, n = rows
+            _lib.head_logits_rows(x, M, self._packed_head, self.D, self.V_pad, out, blk,
+                                  shift_n > 0, lo, n)
         return out[:, :self.V]
 
     @staticmethod
@@ -332,10 +339,14 @@ class FoldedVerifyEngine:
                 trace: Optional[list] = None,
                 teacher: Optional[Dict[int, torch.Tensor]] = None,
                 stats: Optional[StepStats] = None,
-                causal: bool = False, shift: bool = False) -> Optional[torch.Tensor]:
+                causal: bool = False, shift: bool = False,
+                head_rows: Optional[Tuple[int, int]] = None) -> Optional[torch.Tensor]:
         """Verify step -> logits [B1, N, V] (unshifted, or with ``shift`` Fast-dLLM's
         shifted logits, fastdllm_v2_generation.py:121-126, from the head's stores), or
-        None if not compute_logits.
+        None if not compute_logits.  ``head_rows`` = (lo, n): only positions
+        [lo, lo + n) of every branch get logits (the rest of the returned tensor is
+        not written): the rows a decode step reads, so the head computes a fraction
+        of its rows.
 
         batched_input  [B1, N] int64 on the model's device; row 0 = main branch.
         cache          PagedKVCache, a reference-style per-layer (k, v) cache, or None.
@@ -397,13 +408,15 @@ class FoldedVerifyEngine:
                            bucket, BN)
             return self.forward(batched_input, cache, delta, bucket=BN,
                                 compute_logits=compute_logits, q_scale=q_scale, trace=trace,
-                                teacher=teacher, stats=stats, causal=causal, shift=shift)
+                                teacher=teacher, stats=stats, causal=causal, shift=shift,
+                                head_rows=head_rows)
         self.last_hidden = hidden
         self._last = dict(B1=B1, N=N, bucket=bucket, cache=cache, par=buf.par, q_scale=qs,
                           hidden=hidden, delta=delta, shift=shift)
         if not compute_logits:
             return None
-        return self.lm_head(buf.final, shift_n=N if shift else 0).view(B1, N, self.V)
+        rows = None if head_rows is None else (N, int(head_rows[0]), int(head_rows[1]))
+        return self.lm_head(buf.final, shift_n=N if shift else 0, rows=rows).view(B1, N, self.V)
 
     @torch.no_grad()
     def forward_batched(self, blocks: List[torch.Tensor], caches: list, delta: float = 0.1,

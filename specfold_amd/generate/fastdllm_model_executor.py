@@ -109,14 +109,17 @@ class FastDLLMModelExecutor:
             eng.gate_mode = prev_mode
         return SimpleNamespace(logits=logits, past_key_values=past_key_values)
 
-    def forward_shifted(self, input_seq: torch.Tensor, past_key_values=None) -> torch.Tensor:
+    def forward_shifted(self, input_seq: torch.Tensor, past_key_values=None,
+                        head_rows=None) -> torch.Tensor:
         """Dense block forward -> Fast-dLLM's shifted logits [B, L, V] (the
         generator's _shift_logits of ``forward(...).logits``, fastdllm_v2_generation.py:
-        121-126, 151-186), shifted by the head kernel's stores instead of a copy."""
+        121-126, 151-186), shifted by the head kernel's stores instead of a copy.
+        ``head_rows`` = (lo, n): only those positions get logits (the engine's)."""
         eng = self.engine
         prev_mode, eng.gate_mode = eng.gate_mode, _lib.SF_GATE_ALL
         try:
-            return eng.forward(input_seq.to(self.device), past_key_values, delta=0.0, shift=True)
+            return eng.forward(input_seq.to(self.device), past_key_values, delta=0.0, shift=True,
+                               head_rows=head_rows)
         finally:
             eng.gate_mode = prev_mode
 

@@ -108,7 +108,8 @@ class SpecFoldHIPFastDLLMV2Generation(FastDLLMV2SpeculativeGeneration):
         prev_mode, eng.gate_mode = eng.gate_mode, self.gate_mode
         try:
             logits = eng.forward(batched_input, past_key_values, delta=self.delta, bucket=bucket,
-                                 stats=stats, shift=True)
+                                 stats=stats, shift=True,
+                                 head_rows=self.head_rows)
         finally:
             eng.gate_mode = prev_mode
         # fold counters stay on the device (no host sync per step)

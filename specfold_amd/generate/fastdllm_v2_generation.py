@@ -56,6 +56,10 @@ class FastDLLMV2SpeculativeGeneration:
         # decode statistics of the last generate call
         self.last_model_calls = 0
         self.last_commits: List[int] = []
+        # (lo, n): the positions of every branch whose logits the decode step reads,
+        # set by the loop around each verify forward (None: every row); the verify
+        # step's head computes only those rows
+        self.head_rows = None
 
     # -- helpers with the reference's names ------------------------------------------
     def _shift_logits(self, logits: torch.Tensor) -> torch.Tensor:
@@ -104,7 +108,8 @@ class FastDLLMV2SpeculativeGeneration:
         executor with ``forward_shifted`` returns them shifted by its head's stores."""
         ex = self.model_executor
         if hasattr(ex, "forward_shifted"):
-            return ex.forward_shifted(batched_input, past_key_values)
+            return ex.forward_shifted(batched_input, past_key_values,
+                                      head_rows=self.head_rows)
         out = ex.forward(batched_input, past_key_values=past_key_values,
                          use_cache=True, update_past_key_values=False)
         return self._shift_logits(out.logits)
@@ -314,7 +319,15 @@ class FastDLLMV2SpeculativeGeneration:
                                     raise RuntimeError(
                                         "a deferred forward needs its logits via send()")
                             else:
-                                logits = self._batched_block_forward(batched, st["cache"])
+                                # the rows this forward's logits are read at: the small
+                                # block (main branch, drafts) and the next one (a draft
+                                # that fills this small block is taken at the next one's
+                                # first step, :599-616); the head computes only those
+                                self.head_rows = (s0, min(s1 + sbs, bl) - s0)
+                                try:
+                                    logits = self._batched_block_forward(batched, st["cache"])
+                                finally:
+                                    self.head_rows = None
                             st["model_calls"] += 1
                             main_logits = logits[0:1]
                             for i, d in enumerate(draft_blocks):

@@ -137,6 +137,43 @@ def test_lm_head_rows(M):
     close_bf16(logits, mm64(x, w), atol=acc_bound(x, w))
 
 
+@pytest.mark.parametrize("B1,N,lo,n,shift", [
+    (8, 32, 0, 16, True),      # the first small block and the next: a 128-row pass
+    (8, 32, 8, 16, True),
+    (8, 32, 24, 8, True),      # the last small block: 64 rows
+    (8, 32, 4, 24, False),     # 192 rows: a 256-row pass, unshifted
+    (5, 32, 0, 32, True),      # the whole block of 160 rows through the window path
+    (8, 64, 16, 32, True),     # 256 rows of 64-row blocks
+])
+def test_head_logits_rows_window(B1, N, lo, n, shift):
+    """sf_head_logits_rows: the window's rows equal the whole head's bit for bit
+    (shifted or not), every other row and the padding columns stay untouched;
+    V spans whole rounds of 256-column tiles plus a 128-column tail."""
+    g = torch.Generator().manual_seed(B1 * 100 + lo + n)
+    M, D, V = B1 * N, 1536, 256 * 256 + 384
+    x, w = rnd(M, D, gen=g), rnd(V, D, std=0.02, gen=g)
+    wp = packed(w)
+    full = torch.full((M, V + 8), 7.0, dtype=torch.bfloat16, device="cuda")
+    _lib.head_logits(x, M, wp, D, V, full, shift_n=N if shift else 0)
+    win = torch.full((M, V + 8), 7.0, dtype=torch.bfloat16, device="cuda")
+    _lib.head_logits_rows(x, M, wp, D, V, win, N, shift, lo, n)
+    torch.cuda.synchronize()
+    inside = torch.zeros(B1, N, dtype=torch.bool)
+    inside[:, lo:lo + n] = True
+    inside = inside.reshape(M).cuda()
+    assert torch.equal(win[inside], full[inside])
+    assert torch.all(win[~inside] == 7.0)
+    assert torch.all(win[:, V:] == 7.0)
+    # and the whole head against the float64 product (its shift: row n from n - 1),
+    # on the first main-round columns and the tail tile's
+    src = torch.arange(M, device="cuda")
+    if shift:
+        pos = src % N
+        src = torch.where(pos > 0, src - 1, src)
+    cols = torch.cat([torch.arange(0, 512), torch.arange(V - 384, V)]).cuda()
+    close_bf16(full[:, cols], mm64(x[src], w[cols]), atol=acc_bound(x[src], w[cols]))
+
+
 @pytest.mark.parametrize("count,D,I,bucket", [(1, 1536, 8960, 256), (39, 1536, 8960, 256),
                                                (117, 1536, 8960, 256), (130, 1536, 8960, 256),
                                                (256, 1536, 8960, 256), (39, 3584, 18944, 256),

@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_host_side_validation_without_gpu():
     lib = _lib.load()
-    assert lib.sf_abi_version() == 12
+    assert lib.sf_abi_version() == 13
     assert lib.sf_status_string(1).decode() == "shape outside kernel limits"
     # NULL pointers and bad shapes are rejected before any launch
     assert lib.sf_fold_gate(*([None] * 3), 8, 32, 64, 256, 0.1, 1e-6, 0, *([None] * 11)) == 2
