@@ -154,16 +154,41 @@ __global__ __launch_bounds__(kPrnThreads) void part_residual_norm_kernel(
   int v[VPT];
 #pragma unroll
   for (int i = 0; i < VPT; ++i) v[i] = min(tid + i * kPrnThreads, nvec - 1);
+  // the row's x, norm weights and its first four K-range slots in one round of
+  // loads (clamped slots, added in slot order below), further slots four at a time
+  constexpr int kSl = 4;
   sf_u32x4 xv[VPT], wv[VPT];
   sf_f32x4 y[VPT][2];
+  sf_f32x4 a0[kSl][VPT][2];
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
     xv[i] = xr[v[i]];
     wv[i] = zn ? reinterpret_cast<const sf_u32x4*>(w)[v[i]] : sf_u32x4{0u, 0u, 0u, 0u};
-    y[i][0] = sf_handoff_load(pr + 2 * v[i]);
-    y[i][1] = sf_handoff_load(pr + 2 * v[i] + 1);
   }
-  for (int s0 = 1; s0 < ks; s0 += 4) {
+#pragma unroll
+  for (int j = 0; j < kSl; ++j) {
+    const size_t o = (size_t)min(j, ks - 1) * st4;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      a0[j][i][0] = sf_handoff_load(pr + o + 2 * v[i]);
+      a0[j][i][1] = sf_handoff_load(pr + o + 2 * v[i] + 1);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    y[i][0] = a0[0][i][0];
+    y[i][1] = a0[0][i][1];
+  }
+#pragma unroll
+  for (int j = 1; j < kSl; ++j)
+    if (j < ks) {
+#pragma unroll
+      for (int i = 0; i < VPT; ++i) {
+        y[i][0] += a0[j][i][0];
+        y[i][1] += a0[j][i][1];
+      }
+    }
+  for (int s0 = kSl; s0 < ks; s0 += 4) {
     sf_f32x4 a[4][VPT][2];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -272,7 +297,7 @@ __global__ __launch_bounds__(256) void down_fixup_kernel(const float* __restrict
   const size_t stride = (size_t)mcap * N;
   const int c = t * 128 + (threadIdx.x & 31) * 4;
   const int row = rows[m];
-  const sf_f32x4 y = sum_slots<sf_f32x4>(part + (size_t)m * N + c, stride, nsl);
+  const sf_f32x4 y = sum_slots<sf_f32x4, 12>(part + (size_t)m * N + c, stride, nsl);
   sf_u32x2 o;
   o[0] = sf_pack2(y[0], y[1]);
   o[1] = sf_pack2(y[2], y[3]);

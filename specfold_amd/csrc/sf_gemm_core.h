@@ -206,12 +206,20 @@ SF_DEV void tile_to_lds(float* x, const sf_f32x4 (&acc)[MB / 16][WN], int nmt) {
 // (Plan, make_plan, make_plan_whole, plan_grid, plan_slots, tile_first,
 // tile_last, plan_range_end, plan_piece and part_bytes: sf_index.h.)
 
-// sum_{j < n} p[j * stride .. +T] in slot order (deterministic).  Loads go out four
-// at a time from clamped addresses with no branch in between.
-template <typename T>
+// sum_{j < n} p[j * stride .. +T] in slot order (deterministic).  The first MAXN
+// slots' loads all go out at once (clamped addresses, no branch in between: one
+// round of loads for up to MAXN contributors), further ones four at a time.
+template <typename T, int MAXN = 8>
 SF_DEV T sum_slots(const float* p, size_t stride, int n) {
-  T acc = sf_handoff_load(reinterpret_cast<const T*>(p));
-  for (int s0 = 1; s0 < n; s0 += 4) {
+  T v0[MAXN];
+#pragma unroll
+  for (int j = 0; j < MAXN; ++j)
+    v0[j] = sf_handoff_load(reinterpret_cast<const T*>(p + (size_t)min(j, n - 1) * stride));
+  T acc = v0[0];
+#pragma unroll
+  for (int j = 1; j < MAXN; ++j)
+    if (j < n) acc += v0[j];
+  for (int s0 = MAXN; s0 < n; s0 += 4) {
     T v[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j)

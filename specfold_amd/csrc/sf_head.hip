@@ -63,6 +63,9 @@ SF_DEV int head_in_row(int r, const HeadRows& hr) {
 // them in flight.
 template <int NW, int RG, int WN, int R, int HR>
 struct HeadShape {
+  static constexpr int kNW = NW;
+  static constexpr int kRG = RG;
+  static constexpr int kWN = WN;
   static constexpr int kRing = R;
   static constexpr int kRows = HR;                 // rows per pass
   static constexpr int kMT = HR / 16;              // m tiles per pass
@@ -274,11 +277,12 @@ void head_launch(const uint16_t* x, int Mo, const HeadRows& hr, const uint16_t* 
   const int n_rest = (V - n_main * Main::kTN) / Tail::kTN;
   for (int m0 = 0; m0 < Mo; m0 += Main::kRows) {
     if (n_main)
-      hipLaunchKernelGGL((head_kernel<8, 1, 2, Main::kRing, Main::kRows>), dim3(n_main),
-                         dim3(8 * 64), 0, st, x, Mo, m0, hr, w, D, 0, logits, ld_out);
+      hipLaunchKernelGGL((head_kernel<Main::kNW, Main::kRG, Main::kWN, Main::kRing, Main::kRows>),
+                         dim3(n_main), dim3(Main::kNW * 64), 0, st, x, Mo, m0, hr, w, D, 0, logits,
+                         ld_out);
     if (n_rest)
-      hipLaunchKernelGGL((head_kernel<8, 2, 2, Tail::kRing, Tail::kRows>), dim3(n_rest),
-                         dim3(8 * 64), 0, st, x, Mo, m0, hr, w, D,
+      hipLaunchKernelGGL((head_kernel<Tail::kNW, Tail::kRG, Tail::kWN, Tail::kRing, Tail::kRows>),
+                         dim3(n_rest), dim3(Tail::kNW * 64), 0, st, x, Mo, m0, hr, w, D,
                          n_main * (Main::kTN / Tail::kTN), logits, ld_out);
   }
 }

@@ -30,7 +30,8 @@ def _build(tmp_path_factory, extra=()):
     d = tmp_path_factory.mktemp("gemm_sim")
     # copies, so the sources' quoted includes of sf_common.h resolve to the
     # simulator's host header instead of the HIP one next to the originals
-    for f in ("sf_ffn.hip", "sf_qkv.hip", "sf_head.hip", "sf_gemm_core.h", "sf_gemm_rows.h"):
+    for f in ("sf_ffn.hip", "sf_qkv.hip", "sf_head.hip", "sf_gemm_core.h", "sf_gemm_rows.h",
+              "sf_compact.h"):
         (d / f).write_text((CSRC / f).read_text())
     flags = ["-std=c++20", "-O2", "-Wno-unknown-attributes", "-Wno-psabi", f"-I{SIM}",
              f"-I{ROOT / 'include'}", f"-I{CSRC}", *extra]
