@@ -518,8 +518,11 @@ SF_DEV void row_kv_issue(const uint16_t* __restrict__ kv_buf, const int* s_src, 
   }
 }
 
+// NB = 32: two workgroups per CU (<= 128 VGPRs, 72 KB of LDS each), so a launch of
+// more (row, kv head) items than CUs (cfg5: 39 x 8) runs in one round
 template <bool FOLDED, int NB>
-__global__ __launch_bounds__(kRowsThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+__global__ __launch_bounds__(kRowsThreads)
+__attribute__((amdgpu_waves_per_eu(NB == 32 ? 4 : 2, NB == 32 ? 4 : 2))) void
 sf_attn_rows_kernel(
     const uint16_t* __restrict__ q_buf, const uint16_t* __restrict__ kv_buf,
     const int32_t* __restrict__ src, const int32_t* __restrict__ rows,
