@@ -179,7 +179,7 @@ SF_DEV void prefix_item(const uint16_t* __restrict__ q_buf, const uint16_t* __re
     }
   };
 #pragma unroll
-  for (int j = 0; j < kRing - 1; ++j) issue(c0 + j, ring + j * kSlotBytes);
+  for (int j = 0; j < kRing - 2; ++j) issue(c0 + j, ring + j * kSlotBytes);
 
   // Q^T operands: lane holds q[query][ds*32 + grp*8 .. +8] of its query in each of
   // the two 16-query tiles.  They complete (with the first copies) before the loop,
@@ -221,8 +221,57 @@ SF_DEV void prefix_item(const uint16_t* __restrict__ q_buf, const uint16_t* __re
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) acc[qs][dt] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](int c, const uint8_t* slot) {
-    const sf_lds_off base = sf_lds_addr(slot);
+  // Each chunk's P^T parts are carried into the next chunk's step, whose P.V MFMAs
+  // for them (V^T read again from the carried chunk's slot, which the copies leave
+  // alone until the step after) run beside that chunk's softmax arithmetic: the
+  // wave's instruction stream interleaves them.  Before the first chunk the parts
+  // are zero, so its step adds exact zeros.
+  sf_bf16x8 pb[2][kPParts];
+#pragma unroll
+  for (int qs = 0; qs < 2; ++qs)
+#pragma unroll
+    for (int pp = 0; pp < kPParts; ++pp) pb[qs][pp] = sf_as_bf16x8(sf_u32x4{0u, 0u, 0u, 0u});
+
+  // the V^T operands of the slot at `base` (32 keys x 16 dims per dim tile: two
+  // transposing reads each); complete after sf_lds_reads_done
+  auto read_vt = [&](sf_lds_off base, sf_u32x2 (&vf)[16]) {
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const sf_lds_off va = base + vlane + (uint32_t)(((dt ^ vsw) & 7) * 32);
+      vf[2 * dt] = sf_lds_read8_tr<0>(va);
+      vf[2 * dt + 1] = sf_lds_read8_tr<16 * kRowBytes>(va);
+    }
+  };
+  // O^T += V^T P^T over the wave's 32 keys of the carried chunk (each acc tile takes
+  // the smallest P part first)
+  auto add_pv = [&](const sf_u32x2 (&vf)[16]) {
+#pragma unroll
+    for (int pp = kPParts - 1; pp >= 0; --pp)
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const sf_u32x4 vw = {vf[2 * dt][0], vf[2 * dt][1], vf[2 * dt + 1][0], vf[2 * dt + 1][1]};
+#pragma unroll
+        for (int qs = 0; qs < 2; ++qs)
+          acc[qs][dt] = sf_mfma16x16x32(sf_as_bf16x8(vw), pb[qs][pp], acc[qs][dt]);
+      }
+  };
+
+  // chunk c in the slot at `base`; the carried chunk's slot at `vbase`
+  // a rescale of acc decided by a step, applied at the start of the next (after the
+  // P.V that step added, before the one the next adds)
+  bool resc_prev = false;
+  float alpha_prev[2] = {1.f, 1.f};
+  auto rescale = [&]() {
+    if (resc_prev) {
+#pragma unroll
+      for (int qs = 0; qs < 2; ++qs)
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) acc[qs][dt] = acc[qs][dt] * alpha_prev[qs];
+    }
+  };
+
+  auto step = [&](int c, sf_lds_off base, sf_lds_off vbase) {
+    rescale();
     sf_u32x4 kf[8];   // [t * 4 + ds]
 #pragma unroll
     for (int ds = 0; ds < 4; ++ds) {
@@ -231,19 +280,31 @@ SF_DEV void prefix_item(const uint16_t* __restrict__ q_buf, const uint16_t* __re
     }
     sf_lds_reads_done(kf);
 
-    // S^T tiles [t][qs] (raw dot products)
+    // S^T tiles [t][qs] (raw dot products; four independent accumulations)
+    sf_f32x4 sa[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int qs = 0; qs < 2; ++qs) sa[t][qs] = sf_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ds = 0; ds < 4; ++ds)
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int qs = 0; qs < 2; ++qs)
+          sa[t][qs] = sf_mfma16x16x32(sf_as_bf16x8(kf[t * 4 + ds]), sf_as_bf16x8(qf[qs][ds]), sa[t][qs]);
     float s[2][2][4];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int qs = 0; qs < 2; ++qs) {
-        sf_f32x4 a = {0.f, 0.f, 0.f, 0.f};
+      for (int qs = 0; qs < 2; ++qs)
 #pragma unroll
-        for (int ds = 0; ds < 4; ++ds)
-          a = sf_mfma16x16x32(sf_as_bf16x8(kf[t * 4 + ds]), sf_as_bf16x8(qf[qs][ds]), a);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) s[t][qs][i] = a[i];
-      }
+        for (int i = 0; i < 4; ++i) s[t][qs][i] = sa[t][qs][i];
+    // the carried chunk's V^T, once the K fragments are consumed (no scheduling
+    // across this point: the two operand sets are never live together)
+    __builtin_amdgcn_sched_barrier(0);
+    sf_u32x2 vf[16];
+    read_vt(vbase, vf);
     const int kbase = c * kChunk + kh * 32 + grp * 4;  // key of s[0][.][0] of this lane
     if (kbase + 16 + 3 >= P) {  // a partial last chunk: keys past the prefix
 #pragma unroll
@@ -255,12 +316,10 @@ SF_DEV void prefix_item(const uint16_t* __restrict__ q_buf, const uint16_t* __re
             if (kbase + 16 * t + i >= P) s[t][qs][i] = -INFINITY;
     }
 
-    // online softmax per query (base 2, scores pre-scaled by log2(e) * scaling),
-    // then the V^T operand reads, whose latency the exponentials cover.  m_hi is
-    // kept per lane (the maximum of the lane's own keys) and checked against the
-    // reference per lane; only a rescale takes the maximum over the query's four
+    // online softmax per query (base 2, scores pre-scaled by log2(e) * scaling).
+    // m_hi is kept per lane (the maximum of the lane's own keys) and checked against
+    // the reference per lane; only a rescale takes the maximum over the query's four
     // lane groups (shuffles), so most chunks need no cross-lane step
-    float m_use[2];
     bool need = false;
 #pragma unroll
     for (int qs = 0; qs < 2; ++qs) {
@@ -271,9 +330,12 @@ SF_DEV void prefix_item(const uint16_t* __restrict__ q_buf, const uint16_t* __re
         for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[t][qs][i]);
       mx *= scale_log2;
       m_hi[qs] = fmaxf(m_hi[qs], mx);
-      need = need || mx > m_ref[qs] + kLazy;   // m_ref -inf: any finite key
+      need = need | (mx > m_ref[qs] + kLazy);   // m_ref -inf: any finite key
     }
-    // wave-uniform: rescale every query of the wave to its running maximum
+    // wave-uniform: move every query of the wave's reference to its running
+    // maximum.  acc is rescaled at the start of the next step, after the carried
+    // chunk's P.V (its P is against the old reference) has been added: the same
+    // acc * alpha + P.V sequence, one chunk later.
     const bool resc = __ballot(need) != 0;
     float alpha[2] = {1.f, 1.f};
     if (resc) {
@@ -289,79 +351,63 @@ SF_DEV void prefix_item(const uint16_t* __restrict__ q_buf, const uint16_t* __re
         m_ref[qs] = mx;
       }
     }
+    float m_use[2];
 #pragma unroll
     for (int qs = 0; qs < 2; ++qs) m_use[qs] = m_ref[qs] == -INFINITY ? 0.f : m_ref[qs];
-    sf_u32x2 vf[16];  // [dt * 2 + t]
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const sf_lds_off va = base + vlane + (uint32_t)(((dt ^ vsw) & 7) * 32);
-      vf[2 * dt] = sf_lds_read8_tr<0>(va);
-      vf[2 * dt + 1] = sf_lds_read8_tr<16 * kRowBytes>(va);
-    }
-    float lsum[2] = {0.f, 0.f};
-#pragma unroll
-    for (int qs = 0; qs < 2; ++qs) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          s[t][qs][i] = __builtin_amdgcn_exp2f(fmaf(s[t][qs][i], scale_log2, -m_use[qs]));
-          lsum[qs] += s[t][qs][i];
-        }
-      if (resc) {
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) acc[qs][dt] = acc[qs][dt] * alpha[qs];
-      }
-    }
-    // the exponentials and rescales are done before the wait for the V^T reads
-    // (an empty asm that takes them in keeps the compiler from sinking them past it)
-#pragma unroll
-    for (int qs = 0; qs < 2; ++qs) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sf_pin(s[t][qs][i]);
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) sf_pin(acc[qs][dt]);
-    }
     sf_lds_reads_done(vf);
-    // l is kept per lane (its own keys' terms; alpha is the same for the query's
-    // four lane groups) and summed over them when the range is done
-#pragma unroll
-    for (int qs = 0; qs < 2; ++qs) l_run[qs] = l_run[qs] * alpha[qs] + lsum[qs];
-
-    // O^T += V^T P^T over the wave's 32 keys (smallest P part first)
-    sf_bf16x8 pb[2][kPParts];
+    add_pv(vf);
+    float lsum[2] = {0.f, 0.f};
 #pragma unroll
     for (int qs = 0; qs < 2; ++qs) {
       float p2[2][4];
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) p2[t][i] = s[t][qs][i];
+        for (int i = 0; i < 4; ++i) {
+          p2[t][i] = __builtin_amdgcn_exp2f(fmaf(s[t][qs][i], scale_log2, -m_use[qs]));
+          lsum[qs] += p2[t][i];
+        }
       pv_parts<kPParts>(p2, pb[qs]);
     }
+    // l is kept per lane (its own keys' terms; alpha is the same for the query's
+    // four lane groups) and summed over them when the range is done
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const sf_u32x4 vw = {vf[2 * dt][0], vf[2 * dt][1], vf[2 * dt + 1][0], vf[2 * dt + 1][1]};
-      const sf_bf16x8 va = sf_as_bf16x8(vw);
+    for (int qs = 0; qs < 2; ++qs) l_run[qs] = l_run[qs] * alpha[qs] + lsum[qs];
+    // one MFMA of the carried P.V, then three VALU operations (the exponentials and
+    // the P parts of this chunk), and so on: the matrix core and the VALU work side
+    // by side within the wave
 #pragma unroll
-      for (int qs = 0; qs < 2; ++qs)
-#pragma unroll
-        for (int pp = kPParts - 1; pp >= 0; --pp)
-          acc[qs][dt] = sf_mfma16x16x32(va, pb[qs][pp], acc[qs][dt]);
+    for (int i = 0; i < 16 * kPParts; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x402, 3, 0);
     }
+    resc_prev = resc;
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) alpha_prev[qs] = alpha[qs];
   };
 
-  // ---- the ring: chunk k of the range in slot k % kRing --------------------------------
+  // ---- the ring: chunk k of the range in slot k % kRing, copied kAhead chunks
+  // ahead; its slot is rewritten kRing - kAhead steps later (step k + 1 still reads
+  // its V^T) --------------------------------------------------------------------------
+  constexpr int kAhead = kRing - 2;
   const int nck = c1 - c0;
 #pragma unroll 1
   for (int k = 0; k < nck; ++k) {
     // chunk k has landed (each wave's copies complete in issue order), and every
-    // wave is done with the slot the next issue overwrites (chunk k - 1's)
-    sf_wait_vm_barrier<(kRing - 2) * kCopiesPerChunk>();
-    issue(c0 + k + kRing - 1, ring + ((k + kRing - 1) % kRing) * kSlotBytes);
-    compute(c0 + k, ring + (k % kRing) * kSlotBytes);
+    // wave is done with the slot the next issue overwrites (chunk k - 2's)
+    sf_wait_vm_barrier<(kAhead - 1) * kCopiesPerChunk>();
+    issue(c0 + k + kAhead, ring + ((k + kAhead) % kRing) * kSlotBytes);
+    // (the first step's zero P parts take chunk 0's own V^T: landed, finite values,
+    // where the carried slot would hold stale LDS bytes, possibly NaN patterns)
+    const sf_lds_off cur = sf_lds_addr(ring + (k % kRing) * kSlotBytes);
+    step(c0 + k, cur, k == 0 ? cur : sf_lds_addr(ring + ((k + kRing - 1) % kRing) * kSlotBytes));
+  }
+  {  // the last chunk's P.V
+    rescale();
+    sf_u32x2 vf[16];
+    read_vt(sf_lds_addr(ring + ((nck + kRing - 1) % kRing) * kSlotBytes), vf);
+    sf_lds_reads_done(vf);
+    add_pv(vf);
   }
   // drain the clamped re-issues past the range end before the ring is reused
   sf_wait_vm_barrier<0>();

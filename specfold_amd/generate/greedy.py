@@ -62,7 +62,7 @@ def vocab_rank(st: _lib.LogitStats, pos: torch.Tensor, rank: int) -> Optional[to
     the statistics do not carry that rank."""
     if rank >= TOP_K:
         return None
-    return st.top_idx.index_select(0, pos)[:, rank].long()
+    return st.top_idx[pos, rank].long()
 
 
 class DraftIndex:
@@ -105,8 +105,12 @@ def draft_states(x: torch.Tensor, conf: torch.Tensor, st: _lib.LogitStats, ij_se
     if ix.max_rank >= TOP_K:
         return None
     positions = torch.cat([torch.topk(conf, k=k).indices for k in ix.ks])
-    pos = positions.index_select(0, ix.g_idx)
-    toks = st.top_idx.index_select(0, pos).gather(1, ix.v_idx.unsqueeze(1)).squeeze(1).long()
+    # advanced indexing (one gather kernel per dtype) rather than index_select,
+    # whose kernel variant changes with the index count (16 or fewer, or more): a
+    # step whose node set first crossed that line paid a one-off kernel load of
+    # tens of milliseconds inside the decode loop
+    pos = positions[ix.g_idx]
+    toks = st.top_idx[pos, ix.v_idx].long()
     states = x.unsqueeze(0).repeat(ix.n, 1)
     states.index_put_((ix.node_idx, pos + offset), toks)
     return states

@@ -25,11 +25,15 @@ static uint16_t bf(float f) { return sim_f_to_bf16(f); }
 static double fb(uint16_t b) { return (double)sim_bf16_to_f(b); }
 
 int main(int argc, char** argv) {
-  if (argc != 10 && argc != 11) {
-    fprintf(stderr, "usage: attn_sim P page_size B1 N H Hkv R causal seed [folded]\n");
+  if (argc < 10 || argc > 12) {
+    fprintf(stderr, "usage: attn_sim P page_size B1 N H Hkv R causal seed [folded [ramp]]\n");
     return 2;
   }
-  const int folded = argc == 11 ? atoi(argv[10]) : 0;
+  const int folded = argc >= 11 ? atoi(argv[10]) : 0;
+  // ramp = 1: prefix keys scaled by 1 + 3 p / P, so the scores' maximum climbs along
+  // the prefix and the online softmax moves its reference in later chunks too;
+  // ramp = 2: the last 40 keys scaled 3x more, so it moves in the last chunk as well
+  const int ramp = argc >= 12 ? atoi(argv[11]) : 0;
   const int P = atoi(argv[1]), ps = atoi(argv[2]), B1 = atoi(argv[3]), N = atoi(argv[4]);
   const int H = atoi(argv[5]), Hkv = atoi(argv[6]), causal = atoi(argv[8]);
   int R = atoi(argv[7]);
@@ -83,6 +87,14 @@ int main(int argc, char** argv) {
   std::vector<int32_t> table(npages);
   for (int i = 0; i < npages; ++i) table[i] = i;
   std::shuffle(table.begin(), table.end(), rng);
+  if (ramp)
+    for (int p = 0; p < P; ++p)
+      for (int h = 0; h < Hkv; ++h)
+        for (int d = 0; d < hd; ++d) {
+          uint16_t& x = pk[(size_t)table[p / ps] * page_stride + (size_t)h * head_stride +
+                           (size_t)(p % ps) * hd + d];
+          x = bf((float)(fb(x) * (1.0 + 3.0 * p / P) * (ramp == 2 && p >= P - 40 ? 3.0 : 1.0)));
+        }
   auto pkey = [&](const std::vector<uint16_t>& a, int h, int p, int d) {
     return fb(a[(size_t)table[p / ps] * page_stride + (size_t)h * head_stride + (size_t)(p % ps) * hd + d]);
   };

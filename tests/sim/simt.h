@@ -152,6 +152,9 @@ inline int max(int a, int b) { return a > b ? a : b; }
 inline long long min(long long a, long long b) { return a < b ? a : b; }
 inline float sim_exp2f(float x) { return std::exp2(x); }
 #define __builtin_amdgcn_exp2f(x) sim_exp2f(x)
+// scheduling hints: no effect on what a kernel computes
+#define __builtin_amdgcn_sched_group_barrier(mask, size, id) ((void)0)
+#define __builtin_amdgcn_sched_barrier(mask) ((void)0)
 
 // fp32 -> fp16 rounded toward zero (v_cvt_pkrtz_f16_f32), two at a time
 typedef _Float16 sim_half2 __attribute__((ext_vector_type(2)));

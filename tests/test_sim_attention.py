@@ -25,8 +25,7 @@ CSRC = ROOT / "specfold_amd" / "csrc"
 CLANG = Path("/opt/rocm/llvm/bin/clang++")
 
 
-@pytest.fixture(scope="module")
-def attn_sim(tmp_path_factory):
+def _build_sim(tmp_path_factory, defines=()):
     cxx = str(CLANG) if CLANG.exists() else shutil.which("clang++")
     if cxx is None:
         pytest.skip("no clang++ (the simulator needs clang's vector extensions)")
@@ -36,12 +35,24 @@ def attn_sim(tmp_path_factory):
     src = d / "sf_attn.hip"
     src.write_text((CSRC / "sf_attn.hip").read_text())
     exe = d / "attn_sim"
-    r = subprocess.run([cxx, "-std=c++20", "-O2", "-Wno-unknown-attributes", f"-I{SIM}",
+    r = subprocess.run([cxx, "-std=c++20", "-O2", "-Wno-unknown-attributes", *defines, f"-I{SIM}",
                         f"-I{ROOT / 'include'}", f"-I{CSRC}", f'-DKERNEL_SRC="{src}"',
                         str(SIM / "attn_sim.cpp"), "-o", str(exe), "-lpthread"],
                        capture_output=True, text=True)
     assert r.returncode == 0, r.stderr[-4000:]
     return exe
+
+
+@pytest.fixture(scope="module")
+def attn_sim(tmp_path_factory):
+    return _build_sim(tmp_path_factory)
+
+
+@pytest.fixture(scope="module")
+def attn_sim_one_range(tmp_path_factory):
+    # a work-item target of 1: every (query tile, kv head) item takes the whole
+    # prefix as one chunk range, so the prefix kernel's LDS ring wraps many times
+    return _build_sim(tmp_path_factory, ("-DSFA_ITEMS_TARGET=1",))
 
 
 CASES = [
@@ -68,5 +79,28 @@ CASES = [
 def test_attention_kernels_in_simulator(attn_sim, case):
     r = subprocess.run([str(attn_sim), *map(str, case)], capture_output=True, text=True,
                        timeout=600)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
+
+
+# Long chunk ranges (11 and 18 chunks per item, the ring of four slots wrapping, a
+# partial last chunk) with prefix keys scaled up along the prefix (ramp 1), and
+# their last keys more (ramp 2), so the softmax reference moves in later chunks and
+# in the last: the deferred rescale and the P.V carried from one chunk's step into
+# the next.
+RANGE_CASES = [
+    # P, page size, B1, N, H, Hkv, R, causal, seed, folded, ramp
+    (700, 16, 2, 8, 4, 2, 6, 0, 31, 0, 1),
+    (1100, 32, 3, 8, 8, 2, 0, 0, 32, 1, 2),
+    (700, 16, 2, 8, 4, 2, 6, 0, 33, 0, 0),
+    (1000, 16, 2, 8, 4, 2, 5, 0, 34, 0, 2),
+]
+
+
+@pytest.mark.parametrize("case", RANGE_CASES, ids=lambda c: "P%d_ps%d_R%d_folded%d_ramp%d" % (
+    c[0], c[1], c[6], c[9], c[10]))
+def test_attention_long_ranges_in_simulator(attn_sim_one_range, case):
+    r = subprocess.run([str(attn_sim_one_range), *map(str, case)], capture_output=True,
+                       text=True, timeout=600)
     print(r.stdout)
     assert r.returncode == 0, r.stdout + r.stderr
