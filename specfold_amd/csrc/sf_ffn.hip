@@ -362,6 +362,13 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 // units over all of K (cfg3: 1184 units, 5 each over 237 workgroups), so no tile
 // is shared -- no partial slots, no fix-up launch -- and every CU streams the same
 // share of the weights.  Narrower outputs are dealt out stream-K.
+// FFN down (128-column tiles over D, K = I): each tile cut into whole K ranges
+// (split plan) while the tiles are fewer than the grid; stream-K otherwise.
+Plan down_plan(int N, int K) {
+  const int T = N / 128, S = K / kKC;
+  return T < SFG_GRID ? make_plan_split(T, S) : make_plan(T, S);
+}
+
 Plan gate_up_plan(int I, int S) {
   const int nu = I / 16;
   if (nu >= 2 * SFG_GRID && nu <= 8 * SFG_GRID)
@@ -373,7 +380,7 @@ Plan gate_up_plan(int I, int S) {
 
 extern "C" size_t sf_gemm_workspace_bytes(int mcap, int N, int K) {
   if (mcap < 1 || N < 128 || N % 128 || K < kKC || K % kKC) return 0;
-  const size_t b = part_bytes(make_plan(N / 128, K / kKC), mcap, N);
+  const size_t b = part_bytes(down_plan(N, K), mcap, N);
   return b < 256 ? 256 : b;
 }
 
@@ -525,7 +532,7 @@ extern "C" int sf_ffn_down_scatter(const uint16_t* act, const int32_t* count, in
   if (bucket < 1 || bucket > 1024 || I % kKC || D % 128) return SF_ERR_SHAPE;
   if (workspace_bytes < sf_gemm_workspace_bytes(bucket, D, I)) return SF_ERR_WORKSPACE;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  const Plan p = make_plan(D / 128, I / kKC);
+  const Plan p = down_plan(D, I);
   float* part = reinterpret_cast<float*>(workspace);
   Epi ep{};
   ep.rows = rows;

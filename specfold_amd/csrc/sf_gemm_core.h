@@ -310,7 +310,7 @@ void gemm_sk_kernel(const uint16_t* __restrict__ A, const int32_t* __restrict__ 
     rows_s[tid] = GATED ? s_grows[r] : (a_rows ? a_rows[r] : r);
   }
   __syncthreads();
-  for (int u = g * plan.U; u < u_end;) {
+  for (int u = plan_range_begin(g, plan); u < u_end;) {
     const Piece pc = plan_piece(u, u_end, plan);
     const int t = pc.t;
     const int sa = pc.sa;

@@ -80,6 +80,7 @@ struct Plan {
   int S;       // K stages
   int U;       // units per workgroup
   int NU = 0;  // > 0: column-spread plan (below) over NU column units of 16
+  int KS = 0;  // > 0: split plan (below), KS workgroups per tile
 };
 
 // Balanced plan over SFG_GRID workgroups.
@@ -105,23 +106,49 @@ SF_IDX int spread_workgroups(int nu, int grid) {
   const int k = (nu + grid - 1) / grid;
   return (nu + k - 1) / k;
 }
+// Split plan: each of the T tiles is cut into KS ranges of whole K stages (range
+// j: [split_begin(j), split_begin(j + 1))), one workgroup each, so T·KS workgroups
+// each hold a single piece -- no range crosses a tile, so no workgroup pays a
+// second ring fill and epilogue (the stream-K ranges that straddle two tiles
+// finish last) -- and range j of a tile goes to partial slot j.  KS is the most
+// that keeps T·KS within the grid.
+inline Plan make_plan_split(int T, int S) {
+  int ks = SFG_GRID / T;
+  ks = ks < 1 ? 1 : (ks > S ? S : ks);
+  return Plan{T, S, (S + ks - 1) / ks, 0, ks};
+}
+SF_IDX int split_begin(int j, const Plan& p) { return (int)((long long)j * p.S / p.KS); }
+
 inline int plan_grid(const Plan& p) {
+  if (p.KS) return p.T * p.KS;
   return (int)(((long long)p.T * p.S + p.U - 1) / p.U);
 }
 // Upper bound of contributors (slots) per tile.
-inline int plan_slots(const Plan& p) { return p.U >= p.S ? 2 : (p.S + p.U - 1) / p.U + 1; }
+inline int plan_slots(const Plan& p) {
+  if (p.KS) return p.KS;
+  return p.U >= p.S ? 2 : (p.S + p.U - 1) / p.U + 1;
+}
 
 // First and last workgroup holding units of tile t; a piece of tile t computed by
 // workgroup g goes to partial slot g - tile_first(t).
 SF_IDX int tile_first(int t, const Plan& p) {
+  if (p.KS) return t * p.KS;
   return (int)((long long)t * p.S / p.U);
 }
 SF_IDX int tile_last(int t, const Plan& p) {
+  if (p.KS) return t * p.KS + p.KS - 1;
   return (int)(((long long)(t + 1) * p.S - 1) / p.U);
 }
 
-// Workgroup g's units are [g·U, plan_range_end(g)).
+// Workgroup g's units are [plan_range_begin(g), plan_range_end(g)) in tile-major
+// unit order (unit t·S + s): [g·U, min((g + 1)·U, T·S)) for stream-K and the
+// spread plan, range g % KS of tile g / KS for a split plan.
+SF_IDX int plan_range_begin(int g, const Plan& p) {
+  if (p.KS) return (g / p.KS) * p.S + split_begin(g % p.KS, p);
+  return g * p.U;
+}
 SF_IDX int plan_range_end(int g, const Plan& p) {
+  if (p.KS) return (g / p.KS) * p.S + split_begin(g % p.KS + 1, p);
   const int total = p.T * p.S;
   return sf_imin((g + 1) * p.U, total);
 }

@@ -60,9 +60,11 @@ static int walk_plan(const sfg::Plan& p, bool whole) {
   int max_slot = -1;
   for (int g = 0; g < grid; ++g) {
     const int u_end = sfg::plan_range_end(g, p);
-    CHECK((long long)g * p.U < u_end, "empty range g=%d T=%d S=%d U=%d", g, p.T, p.S, p.U);
-    int last_t = -1;
-    for (int u = g * p.U; u < u_end;) {
+    const int u_begin = sfg::plan_range_begin(g, p);
+    CHECK(u_begin < u_end, "empty range g=%d T=%d S=%d U=%d KS=%d", g, p.T, p.S, p.U, p.KS);
+    int last_t = -1, pieces = 0;
+    for (int u = u_begin; u < u_end;) {
+      ++pieces;
       const sfg::Piece pc = sfg::plan_piece(u, u_end, p);
       CHECK(pc.t >= 0 && pc.t < p.T && pc.sa >= 0 && pc.sa < pc.sb && pc.sb <= p.S,
             "piece t=%d sa=%d sb=%d", pc.t, pc.sa, pc.sb);
@@ -84,6 +86,8 @@ static int walk_plan(const sfg::Plan& p, bool whole) {
       ++cnt[pc.t];
       u += pc.sb - pc.sa;
     }
+    // a split plan's workgroup holds exactly one piece
+    if (p.KS) CHECK(pieces == 1, "split plan g=%d: %d pieces", g, pieces);
   }
   for (long long u = 0; u < total; ++u) CHECK(seen[u], "unit %lld never done", u);
   for (int t = 0; t < p.T; ++t) {
@@ -110,7 +114,14 @@ static void check_plans() {
       const sfg::Plan w = sfg::make_plan_whole(T, S);
       CHECK(sfg::plan_grid(w) == T, "whole grid");
       walk_plan(w, true);
-      plans += 2;
+      // split plan: T·KS workgroups within the grid, KS = min(S, grid / T) ranges per
+      // tile (whole tiles once T reaches the grid's size / 2)
+      const sfg::Plan sp = sfg::make_plan_split(T, S);
+      CHECK(sfg::plan_grid(sp) <= SFG_GRID && sp.KS >= 1 && sp.KS <= S, "split grid %d",
+            sfg::plan_grid(sp));
+      const int ss = walk_plan(sp, sp.KS == 1);
+      CHECK(ss == sp.KS - 1, "split plan slots %d of %d", ss + 1, sp.KS);
+      plans += 3;
     }
   // column-spread plans (gate/up): over T workgroups, workgroup t's units
   // [spread_begin(t), spread_begin(t + 1)) -- 1..8 of them, one per wave, waves past
@@ -171,8 +182,9 @@ static void check_plans() {
       const int qs = walk_plan(q, false);
       const size_t need_q = (size_t)(qs + 1) * mcap * s.nqkv * sizeof(float);
       CHECK(f_qkv_ws(mcap, s.D, s.nqkv) >= need_q, "qkv workspace D=%d", s.D);
-      // down: 128-column tiles over D, K = I
-      const sfg::Plan d = sfg::make_plan(s.D / 128, s.I / 64);
+      // down: 128-column tiles over D, K = I, each tile cut into whole K ranges
+      const sfg::Plan d = s.D / 128 < SFG_GRID ? sfg::make_plan_split(s.D / 128, s.I / 64)
+                                                : sfg::make_plan(s.D / 128, s.I / 64);
       const int ds = walk_plan(d, false);
       CHECK(f_gemm_ws(mcap, s.D, s.I) >= (size_t)(ds + 1) * mcap * s.D * sizeof(float),
             "down workspace D=%d I=%d", s.D, s.I);
