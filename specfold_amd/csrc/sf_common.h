@@ -170,6 +170,12 @@ SF_DEV sf_lds_off sf_lds_addr(const void* p) {
   return (sf_lds_off)(uintptr_t)(const sf_lds_void*)p;
 }
 
+// 16 bytes of a read-once stream (weights) into a register, with the non-temporal
+// hint: the lines are not kept in L2 for reuse.
+SF_DEV sf_u32x4 sf_stream_load16(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const sf_u32x4*>(p));
+}
+
 // fp32 hand-offs (partial sums one kernel writes and the next reads once) with the
 // non-temporal (streaming) hint, so their lines are not kept dirty in L2 for reuse:
 // left there, the next weight-streaming kernel pays their write-back while it

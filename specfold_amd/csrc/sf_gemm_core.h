@@ -30,14 +30,25 @@ constexpr int kThreads = 512; // 8 waves
 // the two 32-K chunks of the MB/16 A m tiles (1 KB per (chunk, m tile)), then
 // every wave's WN weight fragments of its chunk (1 KB each, in lane order: the
 // packed layout).  Sizes in 16-byte words.  The ring holds as many stages as fit
-// kLdsBudget, at most 8.
+// kLdsBudget, at most SFG_RING_MAX.
+// kWReg (one weight tile per wave: down, QKV): the weights skip LDS -- each lane
+// loads the 16-byte fragment its MFMA takes straight into a VGPR ring of the same
+// depth -- and a stage in LDS is the A rows alone.  A direct global->LDS copy
+// stream runs at ~5.5 TB/s on MI355X against ~6.5 TB/s for the same stream through
+// VGPRs (measured with the A copies and the per-stage barrier kept).  gate/up (two
+// tiles per wave) keeps its weights on the LDS path: the register ring (3 stages,
+// all the VGPRs allow) measured faster at one shape and slower at three.
 template <int MB, int WN>
 struct Stage {
+  static constexpr bool kWReg = WN == 1;
   static constexpr int kA = 2 * (MB / 16) * 64;   // words of A per stage
-  static constexpr int kW = 8 * WN * 2 * 64;      // words of weights per stage
+  static constexpr int kW = kWReg ? 0 : 8 * WN * 2 * 64;   // words of weights per stage
   static constexpr int kWords = kA + kW;
+  // kWReg: 4 stages (3 in flight: the register stream's rate, and what the kernels'
+  // scalar registers allow without spilling)
+  static constexpr int kRingMax = kWReg ? 4 : SFG_RING_MAX;
   static constexpr int kRing =
-      kLdsBudget / (kWords * 16) < SFG_RING_MAX ? kLdsBudget / (kWords * 16) : SFG_RING_MAX;
+      kLdsBudget / (kWords * 16) < kRingMax ? kLdsBudget / (kWords * 16) : kRingMax;
 };
 
 // The fragments are read from the ring by sf_lds_read16, which the compiler does
@@ -99,6 +110,7 @@ SF_DEV void mainloop(const uint16_t* __restrict__ A, int lda, int mrows, const i
   static_assert(R >= 3, "the ring needs three stages");
   constexpr int kMT = MB / 16;
   constexpr int DPW = (2 * NMT + 7) / 8;
+  constexpr bool kWR = St::kWReg;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = tid >> 6;
@@ -116,50 +128,73 @@ SF_DEV void mainloop(const uint16_t* __restrict__ A, int lda, int mrows, const i
     adst[j] = (ch * kMT + mt) * 64;
   }
   const int wdst = St::kA + wv * WN * 128;   // this wave's weights: [tile][chunk][1 KB]
-  auto issue = [&](int s, sf_u32x4* slot) {
+  // kWR: this lane's weight fragments of the stages in flight, [ring slot][tile][chunk]
+  sf_u32x4 wreg[kWR ? R : 1][WN][2];
+  // stage s into ring slot j (j a constant once the loops below are unrolled)
+  auto issue = [&](int s, int j) {
     const int sc = sf_imin(s, slast);
+    sf_u32x4* slot = rg.slot[j];
 #pragma unroll
-    for (int j = 0; j < DPW; ++j) sf_lds_dma16(asrc[j] + sc * kKC, slot + adst[j]);
+    for (int d = 0; d < DPW; ++d) sf_lds_dma16(asrc[d] + sc * kKC, slot + adst[d]);
 #pragma unroll
     for (int t = 0; t < WN; ++t)
 #pragma unroll
-      for (int c = 0; c < 2; ++c)
-        sf_lds_dma16(wact ? wsrc[t] + (size_t)weight_chunk(sc, c) * kKsStride
-                          : asrc[0] + sc * kKC,
-                     slot + wdst + (t * 2 + c) * 64);
+      for (int c = 0; c < 2; ++c) {
+        if constexpr (kWR)
+          wreg[j][t][c] = sf_stream_load16(wsrc[t] + (size_t)weight_chunk(sc, c) * kKsStride);
+        else
+          sf_lds_dma16(wact ? wsrc[t] + (size_t)weight_chunk(sc, c) * kKsStride
+                            : asrc[0] + sc * kKC,
+                       slot + wdst + (t * 2 + c) * 64);
+      }
   };
 #pragma unroll
-  for (int j = 0; j < R - 1; ++j) issue(s0 + j, rg.slot[j]);
+  for (int j = 0; j < R - 1; ++j) issue(s0 + j, j);
 
   // this lane's A fragment in chunk c of a stage: word a_read_word(lane) of tile
   // (c, mt); its weight fragment: word `lane` of block (tile t, chunk c)
   const sf_lds_off a_byte = (sf_lds_off)a_read_word(lane) * 16;
   const sf_lds_off w_byte = (sf_lds_off)(wdst + lane) * 16;
+  // the fragment reads and MFMAs of the stage in ring slot j
+  auto compute = [&](int j) {
+    const sf_lds_off base = sf_lds_addr(rg.slot[j]);
+    if (!kWR && !wact) return;   // wave-uniform: no operand reads or MFMAs for dropped results
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      constexpr int kLW = kWR ? 0 : WN;   // weight fragments read from LDS
+      sf_u32x4 f[NMT + kLW];
+      lds_fragments<NMT, kLW>(f, base + a_byte + c * kMT * 1024, base + w_byte + c * 1024);
+      sf_lds_reads_done(f);
+#pragma unroll
+      for (int mt = 0; mt < NMT; ++mt)
+#pragma unroll
+        for (int t = 0; t < WN; ++t) {
+          const sf_u32x4 w = kWR ? wreg[kWR ? j : 0][t][c] : f[kWR ? 0 : NMT + t];
+          acc[mt][t] = sf_mfma16x16x32(sf_as_bf16x8(f[mt]), sf_as_bf16x8(w), acc[mt][t]);
+        }
+    }
+  };
+  // whole groups of R stages with no branch inside (the compiler's own waits for
+  // the weight registers then stay exact across the loop): stage sb + j in slot j
+  // -- wait for it, issue stage sb + j + R - 1 into slot j - 1, compute.  The last
+  // (s1 - s0) % R < R stages were all issued by then: one wait for every copy,
+  // then their fragment reads and MFMAs.
+  int sb = s0;
 #pragma unroll 1
-  for (int sb = s0; sb < s1; sb += R) {
+  for (; sb + R <= s1; sb += R) {
 #pragma unroll
     for (int j = 0; j < R; ++j) {
-      if (sb + j < s1) {  // wave-uniform; no break, so the ring indices stay static
-        sf_wait_vm_barrier<(R - 2) * (DPW + 2 * WN)>();
-        issue(sb + j + R - 1, rg.slot[(j + R - 1) % R]);
-        const sf_lds_off base = sf_lds_addr(rg.slot[j]);
-        if (!wact) continue;   // wave-uniform: no operand reads or MFMAs for dropped results
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          sf_u32x4 f[NMT + WN];
-          lds_fragments<NMT, WN>(f, base + a_byte + c * kMT * 1024, base + w_byte + c * 1024);
-          sf_lds_reads_done(f);
-#pragma unroll
-          for (int mt = 0; mt < NMT; ++mt)
-#pragma unroll
-            for (int t = 0; t < WN; ++t)
-              acc[mt][t] =
-                  sf_mfma16x16x32(sf_as_bf16x8(f[mt]), sf_as_bf16x8(f[NMT + t]), acc[mt][t]);
-        }
-      }
+      sf_wait_vm_barrier<(R - 2) * (DPW + 2 * WN)>();
+      issue(sb + j + R - 1, (j + R - 1) % R);
+      compute(j);
     }
   }
-  // drain the clamped re-issues past the last stage before the LDS is reused
+  sf_wait_vm_barrier<0>();
+#pragma unroll
+  for (int j = 0; j < R - 1; ++j)
+    if (sb + j < s1) compute(j);   // wave-uniform
+  // every wave is done with the ring before the LDS is reused (the copies past the
+  // last stage -- clamped re-reads of it -- were waited for above)
   sf_wait_vm_barrier<0>();
 }
 
@@ -275,14 +310,17 @@ void gemm_sk_kernel(const uint16_t* __restrict__ A, const int32_t* __restrict__ 
   constexpr int kMT = MB / 16;    // max m tiles of this kernel
   using St = Stage<MB, WN>;
   constexpr int R = St::kRing;
-  __shared__ sf_u32x4 ring[R * St::kWords];
+  // the ring, whose memory then holds each piece's fp32 tile for the epilogue
+  constexpr int kTileWords = TileLds<WN, MB, MODE == kSilu>::kFloats / 4;
+  constexpr int kRingWords = R * St::kWords > kTileWords ? R * St::kWords : kTileWords;
+  __shared__ sf_u32x4 ring[kRingWords];
   __shared__ int rows_s[MB];
   __shared__ int s_grows[GATED ? kGateMaxRows : 1];      // the compacted rows
   __shared__ int s_gtot[GATED ? kGateMaxRows / 64 : 1];
   int M;
   if constexpr (GATED) {
     // the ring's memory is free until the main loop: the compaction's scratch
-    static_assert(2 * kGateMaxRows * 4 <= R * St::kWords * 16, "gate scratch");
+    static_assert(2 * kGateMaxRows * 4 <= kRingWords * 16, "gate scratch");
     int* s_f = reinterpret_cast<int*>(ring);
     const int total = gate_compact<kThreads, kGateMaxRows / kThreads>(
         gate.rec, gate.par, gate.B1, gate.N, mcap, s_f, s_f + kGateMaxRows, s_gtot, s_grows,
@@ -357,7 +395,7 @@ void gemm_sk_kernel(const uint16_t* __restrict__ A, const int32_t* __restrict__ 
     // columns of a row: epilogue, vector stores
     constexpr bool kS = MODE == kSilu;
     float* tl = reinterpret_cast<float*>(ring);
-    static_assert(TileLds<WN, MB, kS>::kFloats * 4 <= R * St::kWords * 16, "tile LDS");
+    static_assert(TileLds<WN, MB, kS>::kFloats * 4 <= kRingWords * 16, "tile LDS");
     tile_to_lds<WN, MB, kS>(tl, acc, nmt);
     __syncthreads();
     u += sb - sa;

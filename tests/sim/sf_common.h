@@ -63,6 +63,7 @@ SF_DEV void sf_wait_vm_barrier() {
 }
 
 SF_DEV void sf_lds_barrier() { __syncthreads(); }
+SF_DEV sf_u32x4 sf_stream_load16(const void* p) { return *reinterpret_cast<const sf_u32x4*>(p); }
 template <typename T>
 SF_DEV void sf_handoff_store(T* p, T v) { *p = v; }
 template <typename T>
