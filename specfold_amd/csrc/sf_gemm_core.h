@@ -97,10 +97,10 @@ SF_DEV void lds_fragments(sf_u32x4 (&f)[NMT + WN], sf_lds_off a_addr, sf_lds_off
 // re-read the last row, which keeps every count exact; the loop drains them at
 // its end.
 // A wave with no columns of its own (wact false: a column-spread workgroup with
-// fewer units than waves) issues the same number of copies (the waits count them),
-// but re-reads its first A copy (L2-resident) into its own weight slots instead of
-// weight bytes, and reads no fragments and issues no MFMAs (its results are
-// dropped), which leaves the LDS and the matrix cores of its SIMD to the others.
+// fewer units than waves) issues only its share of the A copies (and waits for
+// its own count of them), reads no fragments and issues no MFMAs (its results are
+// dropped), which leaves the copy path, the LDS and the matrix cores of its CU to
+// the others.
 template <int WN, int NMT, int MB>
 SF_DEV void mainloop(const uint16_t* __restrict__ A, int lda, int mrows, const int* rows,
                      const uint16_t* const (&wsrc)[WN], int s0, int s1, const Ring<MB, WN>& rg,
@@ -142,9 +142,8 @@ SF_DEV void mainloop(const uint16_t* __restrict__ A, int lda, int mrows, const i
       for (int c = 0; c < 2; ++c) {
         if constexpr (kWR)
           wreg[j][t][c] = sf_stream_load16(wsrc[t] + (size_t)weight_chunk(sc, c) * kKsStride);
-        else
-          sf_lds_dma16(wact ? wsrc[t] + (size_t)weight_chunk(sc, c) * kKsStride
-                            : asrc[0] + sc * kKC,
+        else if (wact)   // wave-uniform: a wave with no unit copies no weights
+          sf_lds_dma16(wsrc[t] + (size_t)weight_chunk(sc, c) * kKsStride,
                        slot + wdst + (t * 2 + c) * 64);
       }
   };
@@ -184,7 +183,11 @@ SF_DEV void mainloop(const uint16_t* __restrict__ A, int lda, int mrows, const i
   for (; sb + R <= s1; sb += R) {
 #pragma unroll
     for (int j = 0; j < R; ++j) {
-      sf_wait_vm_barrier<(R - 2) * (DPW + 2 * WN)>();
+      // a wave with no unit (column-spread plan) issues only its A copies
+      if (kWR || wact)
+        sf_wait_vm_barrier<(R - 2) * (DPW + 2 * WN)>();
+      else
+        sf_wait_vm_barrier<(R - 2) * DPW>();
       issue(sb + j + R - 1, (j + R - 1) % R);
       compute(j);
     }
