@@ -20,9 +20,12 @@
 //  * conf = bf16(1 / Zn) (the greedy token's probability), conf_full =
 //    bf16(1 / Z) (the maximum of the bf16 softmax).
 //
-// Two kernels.  Slice: many workgroups per row count every token into a
-// 65536-bin histogram of its bf16 bit pattern (integer atomics) and reduce their
-// slice's top-8.  Finish: one workgroup per row merges the slice candidates and
+// Two kernels.  Slice: several workgroups per row count their tokens into a
+// 65536-bin histogram of the bf16 bit pattern in LDS (two 16-bit counts per
+// 32-bit word), add its nonzero bins into the row's histogram in memory (integer
+// atomics: one per distinct value of the slice instead of one per token, which on
+// logits clustered over a few hundred bf16 values contended in L2), and reduce
+// their slice's top-8.  Finish: one workgroup per row merges the slice candidates and
 // walks the histogram in descending value order: masses are count(v) * e(v) and
 // count(v) * p(v), summed in a fixed order (deterministic), which gives Z, the
 // cut and Zn from exact counts; it then clears the histogram for the next call.
@@ -35,10 +38,11 @@
 namespace {
 
 constexpr int kTop = 8;
-constexpr int kSliceThreads = 256;
+constexpr int kSliceThreads = 512;
 constexpr int kFinishThreads = 1024;
 constexpr int kKeys = 65536;
-constexpr int kMaxSlices = 64;
+constexpr int kMaxSlices = 32;
+constexpr int kMaxSliceTokens = 65535;   // a slice's counts fit 16 bits
 
 // order key of a bf16 bit pattern: larger value -> larger key
 SF_DEV uint32_t bf16_key(uint32_t b) { return (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u); }
@@ -104,12 +108,45 @@ SF_DEV void block_top8(float (&tv)[kTop], int (&ti)[kTop], float (&bv)[kTop], in
   }
 }
 
+// Prefix sums over the workgroup's threads in thread order (a shuffle scan per
+// wave, then the wave totals in order; deterministic): returns the exclusive
+// prefix, with the inclusive one in `incl` (the next thread's exclusive prefix,
+// bit for bit) and the workgroup total in `total`.  s_w: NT / 64 floats of LDS.
+template <int NT>
+SF_DEV float block_scan(float x, float* s_w, float& incl, float& total) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  float in = x;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float y = __shfl_up(in, o, 64);
+    if (lane >= o) in += y;
+  }
+  float ex = __shfl_up(in, 1, 64);
+  if (lane == 0) ex = 0.f;
+  if (lane == 63) s_w[wv] = in;
+  __syncthreads();
+  float base = 0.f, tot = 0.f;
+#pragma unroll
+  for (int w = 0; w < NT / 64; ++w) {
+    if (w < wv) base += s_w[w];
+    tot += s_w[w];
+  }
+  __syncthreads();
+  incl = base + in;
+  total = tot;
+  return base + ex;
+}
+
 // grid (S, M): slice s of row m counts its tokens into hist[m] and writes its top-8
 __global__ __launch_bounds__(kSliceThreads) void sf_logit_slice_kernel(
     const uint16_t* __restrict__ logits, long long ld, int V, uint32_t* __restrict__ hist,
     float* __restrict__ cand_v, int32_t* __restrict__ cand_i) {
+  __shared__ sf_u32x4 s_hist4[kKeys / 8];   // key 2i: low half of word i, 2i + 1: high half
   __shared__ float s_v[kSliceThreads / 64];
   __shared__ int s_i[kSliceThreads / 64];
+  uint32_t* s_hist = reinterpret_cast<uint32_t*>(s_hist4);
+  for (int i = threadIdx.x; i < kKeys / 8; i += kSliceThreads) s_hist4[i] = sf_u32x4{0u, 0u, 0u, 0u};
+  __syncthreads();
   const int S = gridDim.x, s = blockIdx.x, row = blockIdx.y;
   const uint16_t* x = logits + (long long)row * ld;
   uint32_t* h = hist + (size_t)row * kKeys;
@@ -129,7 +166,8 @@ __global__ __launch_bounds__(kSliceThreads) void sf_logit_slice_kernel(
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const uint32_t bits = (e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xffffu);
-      atomicAdd(&h[bf16_key(bits)], 1u);
+      const uint32_t key = bf16_key(bits);
+      atomicAdd(&s_hist[key >> 1], (key & 1u) ? 0x10000u : 1u);
       const float f = __uint_as_float(bits << 16);
       const int idx = vi * 8 + e;
       // indices ascend within a thread: a strict comparison keeps the lowest index
@@ -150,6 +188,16 @@ __global__ __launch_bounds__(kSliceThreads) void sf_logit_slice_kernel(
             kmin = k;
           }
       }
+    }
+  }
+  // the slice's counts into the row's histogram: its nonzero bins only
+  __syncthreads();
+  for (int i = threadIdx.x; i < kKeys / 8; i += kSliceThreads) {
+    const sf_u32x4 w = s_hist4[i];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (w[q] & 0xffffu) atomicAdd(&h[8 * i + 2 * q], w[q] & 0xffffu);
+      if (w[q] >> 16) atomicAdd(&h[8 * i + 2 * q + 1], w[q] >> 16);
     }
   }
   float bv[kTop];
@@ -174,7 +222,6 @@ __global__ __launch_bounds__(kFinishThreads) void sf_logit_finish_kernel(
     int32_t* __restrict__ greedy_tok, float* __restrict__ conf, float* __restrict__ conf_full) {
   __shared__ float s_v[kFinishThreads / 64];
   __shared__ int s_i[kFinishThreads / 64];
-  __shared__ float s_part[kFinishThreads];
   __shared__ float s_cutf[2];  // Z, Zn
   const int tid = threadIdx.x, row = blockIdx.x;
   uint32_t* h = hist + (size_t)row * kKeys;
@@ -213,41 +260,18 @@ __global__ __launch_bounds__(kFinishThreads) void sf_logit_finish_kernel(
     return acc;
   };
   const float part = stretch_sum([&](float v) { return expf(v - lmax); });
-  s_part[tid] = part;
-  __syncthreads();
-  // sequential prefix over the stretches (fixed order; Z is its total)
-  if (tid == 0) {
-    float cum = 0.f;
-    for (int t = 0; t < kFinishThreads; ++t) {
-      const float before = cum;
-      cum += s_part[t];
-      s_part[t] = before;
-    }
-    s_cutf[0] = cum;
-  }
-  __syncthreads();
-  const float z = s_cutf[0];
-  const float excl_e = s_part[tid];
+  // prefix over the stretches in descending key order (fixed order; Z is the total)
+  float z, incl_e;
+  const float excl_e = block_scan<kFinishThreads>(part, s_v, incl_e, z);
   const float part_p = stretch_sum([&](float v) { return sf_rbf(expf(v - lmax) / z); });
-  __syncthreads();
-  s_part[tid] = part_p;
-  __syncthreads();
-  if (tid == 0) {
-    float cum = 0.f;
-    for (int t = 0; t < kFinishThreads; ++t) {
-      const float before = cum;
-      cum += s_part[t];
-      s_part[t] = before;
-    }
-    s_cutf[1] = z;  // the nucleus mass when nothing is cut
-  }
+  float incl_p, tot_p;
+  const float excl_p = block_scan<kFinishThreads>(part_p, s_v, incl_p, tot_p);
+  if (tid == 0) s_cutf[1] = z;  // the nucleus mass when nothing is cut
   __syncthreads();
   // The reference drops sorted token i >= 1 when bf16(cumsum_{j<i} p_j) > top_p:
   // the kept tokens run up to and including the first one whose cumulative
   // probability crosses.  Exactly one stretch holds the crossing (monotone sums).
   auto crosses = [&](float cum) { return sf_rbf(cum) > top_p; };
-  const float excl_p = s_part[tid];
-  const float incl_p = tid + 1 < kFinishThreads ? s_part[tid + 1] : excl_p + part_p;
   if (!crosses(excl_p) && crosses(incl_p)) {
     float cp = excl_p, ce = excl_e;
     float zc = -1.f;
@@ -330,10 +354,17 @@ __global__ __launch_bounds__(kFinishThreads) void sf_logit_finish_kernel(
   }
 }
 
-int slices_for(int M) { return max(1, min(kMaxSlices, 512 / M)); }
+// Slices per row: about 256 workgroups in all, at most kMaxSlices, and enough
+// that no slice counts more than kMaxSliceTokens tokens (V <= kMaxSlices * that).
+int slices_for(int M, int V) {
+  const int need = (V + kMaxSliceTokens - 1) / kMaxSliceTokens;
+  return max(need, max(1, min(kMaxSlices, 256 / M)));
+}
 
-// Rows the allocation-free entry point takes; with S = slices_for(M) slices per
-// row, M * S <= 512 for every M <= 64, so the candidates fit in 512 * 8 pairs.
+// Rows the allocation-free entry point takes; with S = slices_for(M, V) slices per
+// row, M * S <= 256 for every M <= 64 and V <= 4 * 65535 (a call whose larger
+// vocabulary needs more than the 512 candidate lists is refused), so the
+// candidates fit in 512 * 8 pairs.
 constexpr int kNoAllocMaxRows = 64;
 constexpr size_t kNoAllocHistBytes = (size_t)kNoAllocMaxRows * kKeys * 4;
 constexpr size_t kNoAllocBytes = kNoAllocHistBytes + (size_t)512 * kTop * 8;
@@ -346,7 +377,7 @@ __global__ __launch_bounds__(256) void sf_zero_kernel(sf_u32x4* __restrict__ p, 
 int launch_stats(const uint16_t* logits, int M, int V, long long ld, float top_p, int32_t* top_idx,
                  float* top_val, float* zfull, float* znuc, int32_t* greedy_tok, float* conf,
                  float* conf_full, uint32_t* hist, void* cand, hipStream_t st) {
-  const int S = slices_for(M);
+  const int S = slices_for(M, V);
   float* cand_v = reinterpret_cast<float*>(cand);
   int32_t* cand_i = reinterpret_cast<int32_t*>(cand_v + (size_t)M * S * kTop);
   hipLaunchKernelGGL(sf_logit_slice_kernel, dim3(S, M), dim3(kSliceThreads), 0, st, logits, ld, V,
@@ -364,6 +395,7 @@ int check_stats_args(const uint16_t* logits, int M, int V, long long ld, float t
   if (!logits || !top_idx || !top_val || !zfull || !znuc || !greedy_tok || !conf || !conf_full)
     return SF_ERR_ARG;
   if (M < 1 || V < kTop || V % 8 != 0 || ld < V || ld % 8 != 0) return SF_ERR_SHAPE;
+  if (V > kMaxSlices * kMaxSliceTokens) return SF_ERR_SHAPE;
   if (reinterpret_cast<uintptr_t>(logits) % 16 != 0 || !(top_p > 0.0f)) return SF_ERR_ARG;
   return SF_OK;
 }
@@ -412,8 +444,8 @@ int scratch_for_current_device(hipStream_t st, void** out) {
 
 extern "C" size_t sf_logit_stats_workspace_bytes(int M) {
   if (M < 1) return 0;
-  const int S = slices_for(M);
-  return (size_t)M * kKeys * 4 + (size_t)M * S * kTop * 8;
+  // candidates for the most slices any V takes (kMaxSlices)
+  return (size_t)M * kKeys * 4 + (size_t)M * kMaxSlices * kTop * 8;
 }
 
 extern "C" int sf_logit_stats(const uint16_t* logits, int M, int V, long long ld, float top_p,
@@ -440,7 +472,8 @@ extern "C" int sf_logit_stats_noalloc(const uint16_t* logits, int M, int V, long
   const int a = check_stats_args(logits, M, V, ld, top_p, top_idx, top_val, zfull, znuc,
                                  greedy_tok, conf, conf_full);
   if (a != SF_OK) return a;
-  if (M > kNoAllocMaxRows || (size_t)M * slices_for(M) * kTop * 8 > kNoAllocBytes - kNoAllocHistBytes)
+  if (M > kNoAllocMaxRows ||
+      (size_t)M * slices_for(M, V) * kTop * 8 > kNoAllocBytes - kNoAllocHistBytes)
     return SF_ERR_SCRATCH;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   void* ws = nullptr;

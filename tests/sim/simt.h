@@ -114,6 +114,15 @@ inline float __shfl_xor(float v, int mask, int width = 64) {
   return out;
 }
 
+// __shfl_up: lane l reads lane l - delta; lanes below delta keep their own value
+inline float __shfl_up(float v, unsigned delta, int width = 64) {
+  (void)width;
+  float out;
+  const int src = sim_lane() >= (int)delta ? sim_lane() - (int)delta : sim_lane();
+  sim_wave_exchange(&v, 4, [&](const uint8_t* b) { memcpy(&out, b + src * 128, 4); });
+  return out;
+}
+
 inline unsigned long long __ballot(int pred) {
   const int mine = pred != 0;
   unsigned long long m = 0;
