@@ -42,7 +42,8 @@ constexpr int kSliceThreads = 512;
 constexpr int kFinishThreads = 1024;
 constexpr int kKeys = 65536;
 constexpr int kMaxSlices = 32;
-constexpr int kMaxSliceTokens = 65535;   // a slice's counts fit 16 bits
+constexpr int kMaxSliceTokens = 65535;   // a slice's counts and token places fit 16 bits
+static_assert(kMaxSlices <= 64, "one wave merges the slices' lists");
 
 // order key of a bf16 bit pattern: larger value -> larger key
 SF_DEV uint32_t bf16_key(uint32_t b) { return (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u); }
@@ -82,29 +83,38 @@ SF_DEV void block_best(float& v, int& i, float* s_v, int* s_i) {
   __syncthreads();
 }
 
-// Top-8 of a block from per-thread lists (8 rounds, each removing the winner).
-template <int NT>
-SF_DEV void block_top8(float (&tv)[kTop], int (&ti)[kTop], float (&bv)[kTop], int (&bi)[kTop],
-                       float* s_v, int* s_i) {
+// Ordering key of a bf16 logit for the top-8: larger value -> larger key, both
+// zeros equal (as in a float comparison), NaN 0 (below every value, equal to an
+// empty slot, so never taken).
+SF_DEV uint32_t rank_key(uint32_t b) {
+  const uint32_t a = b & 0x7fffu;
+  if (a > 0x7f80u) return 0u;
+  return bf16_key(a == 0u ? 0u : b);
+}
+
+template <typename K>
+SF_DEV K wave_max(K x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const K y = __shfl_xor(x, o, 64);
+    x = x > y ? x : y;
+  }
+  return x;
+}
+
+// Top-8 of a wave from per-lane lists of L keys in descending order (nonzero keys
+// distinct, 0 = empty): 8 rounds of a wave maximum, the winning lane popping its
+// list's head.  Every lane gets the 8 in `out`, largest first.
+template <int L, typename K>
+SF_DEV void wave_top8(K (&l)[L], K (&out)[kTop]) {
 #pragma unroll
   for (int r = 0; r < kTop; ++r) {
-    float v = -INFINITY;
-    int i = 0x7fffffff;
+    const K w = wave_max(l[0]);
+    out[r] = w;
+    const bool pop = l[0] == w;
 #pragma unroll
-    for (int k = 0; k < kTop; ++k)
-      if (better(tv[k], ti[k], v, i)) {
-        v = tv[k];
-        i = ti[k];
-      }
-    block_best<NT>(v, i, s_v, s_i);
-    bv[r] = v;
-    bi[r] = i;
-#pragma unroll
-    for (int k = 0; k < kTop; ++k)
-      if (ti[k] == i) {
-        tv[k] = -INFINITY;
-        ti[k] = 0x7fffffff;
-      }
+    for (int k = 0; k + 1 < L; ++k) l[k] = pop ? l[k + 1] : l[k];
+    l[L - 1] = pop ? K(0) : l[L - 1];
   }
 }
 
@@ -137,13 +147,15 @@ SF_DEV float block_scan(float x, float* s_w, float& incl, float& total) {
   return base + ex;
 }
 
-// grid (S, M): slice s of row m counts its tokens into hist[m] and writes its top-8
+// grid (S, M): slice s of row m counts its tokens into hist[m] and writes its
+// top-8 as keys (rank_key(value) << 16 | 0xffff - token's place in the slice:
+// larger = higher value, then lower index; 0 = none) to cand[m][s][0..7].
 __global__ __launch_bounds__(kSliceThreads) void sf_logit_slice_kernel(
     const uint16_t* __restrict__ logits, long long ld, int V, uint32_t* __restrict__ hist,
-    float* __restrict__ cand_v, int32_t* __restrict__ cand_i) {
+    uint32_t* __restrict__ cand) {
+  static_assert(kSliceThreads / 64 * kTop == 64, "one wave merges the waves' lists");
   __shared__ sf_u32x4 s_hist4[kKeys / 8];   // key 2i: low half of word i, 2i + 1: high half
-  __shared__ float s_v[kSliceThreads / 64];
-  __shared__ int s_i[kSliceThreads / 64];
+  __shared__ uint32_t s_top[kSliceThreads / 64 * kTop];
   uint32_t* s_hist = reinterpret_cast<uint32_t*>(s_hist4);
   for (int i = threadIdx.x; i < kKeys / 8; i += kSliceThreads) s_hist4[i] = sf_u32x4{0u, 0u, 0u, 0u};
   __syncthreads();
@@ -152,15 +164,11 @@ __global__ __launch_bounds__(kSliceThreads) void sf_logit_slice_kernel(
   uint32_t* h = hist + (size_t)row * kKeys;
   const int nvec = V >> 3;
   const int v0 = (int)((long long)nvec * s / S), v1 = (int)((long long)nvec * (s + 1) / S);
-  float tv[kTop];
-  int ti[kTop];
+  // the thread's top-8 keys in descending order: each token passes down the list
+  // in a compare-exchange chain (branch-free; the slice has at most 65535 tokens)
+  uint32_t top[kTop];
 #pragma unroll
-  for (int k = 0; k < kTop; ++k) {
-    tv[k] = -INFINITY;
-    ti[k] = 0x7fffffff;
-  }
-  float tmin = -INFINITY;
-  int kmin = 0;
+  for (int k = 0; k < kTop; ++k) top[k] = 0u;
   for (int vi = v0 + threadIdx.x; vi < v1; vi += kSliceThreads) {
     const sf_u32x4 w = *reinterpret_cast<const sf_u32x4*>(x + (size_t)vi * 8);
 #pragma unroll
@@ -168,25 +176,13 @@ __global__ __launch_bounds__(kSliceThreads) void sf_logit_slice_kernel(
       const uint32_t bits = (e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xffffu);
       const uint32_t key = bf16_key(bits);
       atomicAdd(&s_hist[key >> 1], (key & 1u) ? 0x10000u : 1u);
-      const float f = __uint_as_float(bits << 16);
-      const int idx = vi * 8 + e;
-      // indices ascend within a thread: a strict comparison keeps the lowest index
-      // among equal values (an empty slot, index INT_MAX, always loses)
-      if (better(f, idx, tmin, ti[kmin])) {
+      const uint32_t rk = rank_key(bits);
+      uint32_t c = rk ? (rk << 16) | (0xffffu - (uint32_t)((vi - v0) * 8 + e)) : 0u;
 #pragma unroll
-        for (int k = 0; k < kTop; ++k)
-          if (k == kmin) {
-            tv[k] = f;
-            ti[k] = idx;
-          }
-        tmin = tv[0];
-        kmin = 0;
-#pragma unroll
-        for (int k = 1; k < kTop; ++k)
-          if (better(tmin, ti[kmin], tv[k], ti[k])) {
-            tmin = tv[k];
-            kmin = k;
-          }
+      for (int k = 0; k < kTop; ++k) {
+        const uint32_t hi = max(top[k], c);
+        c = min(top[k], c);
+        top[k] = hi;
       }
     }
   }
@@ -200,15 +196,24 @@ __global__ __launch_bounds__(kSliceThreads) void sf_logit_slice_kernel(
       if (w[q] >> 16) atomicAdd(&h[8 * i + 2 * q + 1], w[q] >> 16);
     }
   }
-  float bv[kTop];
-  int bi[kTop];
-  block_top8<kSliceThreads>(tv, ti, bv, bi, s_v, s_i);
-  if (threadIdx.x == 0) {
-    const size_t o = ((size_t)row * S + s) * kTop;
+  // the slice's top-8: each wave's, then wave 0 merges the waves' 8 x 8
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  uint32_t wt[kTop];
+  wave_top8<kTop>(top, wt);
+  if (lane == 0) {
 #pragma unroll
-    for (int r = 0; r < kTop; ++r) {
-      cand_v[o + r] = bv[r];
-      cand_i[o + r] = bi[r];
+    for (int r = 0; r < kTop; ++r) s_top[wv * kTop + r] = wt[r];
+  }
+  __syncthreads();
+  if (wv == 0) {
+    uint32_t one[1] = {s_top[lane]};
+    uint32_t bt[kTop];
+    wave_top8<1>(one, bt);
+    if (lane < kTop) {
+      uint32_t b = bt[0];
+#pragma unroll
+      for (int r = 1; r < kTop; ++r) b = r == lane ? bt[r] : b;
+      cand[((size_t)row * S + s) * kTop + lane] = b;
     }
   }
 }
@@ -216,29 +221,53 @@ __global__ __launch_bounds__(kSliceThreads) void sf_logit_slice_kernel(
 // one workgroup per row
 __global__ __launch_bounds__(kFinishThreads) void sf_logit_finish_kernel(
     const uint16_t* __restrict__ logits, long long ld, int V, int S, float top_p,
-    uint32_t* __restrict__ hist, const float* __restrict__ cand_v,
-    const int32_t* __restrict__ cand_i, int32_t* __restrict__ top_idx,
+    uint32_t* __restrict__ hist, const uint32_t* __restrict__ cand, int32_t* __restrict__ top_idx,
     float* __restrict__ top_val, float* __restrict__ zfull, float* __restrict__ znuc,
     int32_t* __restrict__ greedy_tok, float* __restrict__ conf, float* __restrict__ conf_full) {
   __shared__ float s_v[kFinishThreads / 64];
   __shared__ int s_i[kFinishThreads / 64];
+  __shared__ float s_bv[kTop];
+  __shared__ int s_bi[kTop];
   __shared__ float s_cutf[2];  // Z, Zn
   const int tid = threadIdx.x, row = blockIdx.x;
   uint32_t* h = hist + (size_t)row * kKeys;
 
-  // ---- merge the slices' top-8 lists (at most 64 x 8 = 512 candidates) -------------
-  float tv[kTop];
-  int ti[kTop];
+  // ---- merge the slices' top-8 lists (S <= 64): lane s of wave 0 takes slice s's ----
+  // list, keyed (rank << 32 | 0xffff - s << 16 | 0xffff - place): ties go to the
+  // lower slice, then the lower place, i.e. the lower token index
+  if (tid < 64) {
+    uint64_t l[kTop];
 #pragma unroll
-  for (int k = 0; k < kTop; ++k) {
-    const int c = tid * kTop + k;
-    const bool ok = tid < S;  // thread t takes slice t's list
-    tv[k] = ok ? cand_v[(size_t)row * S * kTop + c] : -INFINITY;
-    ti[k] = ok ? cand_i[(size_t)row * S * kTop + c] : 0x7fffffff;
+    for (int k = 0; k < kTop; ++k) {
+      const uint32_t c = tid < S ? cand[((size_t)row * S + tid) * kTop + k] : 0u;
+      l[k] = c ? ((uint64_t)(c >> 16) << 32) | ((uint64_t)(0xffffu - tid) << 16) | (c & 0xffffu)
+               : 0ull;
+    }
+    uint64_t b[kTop];
+    wave_top8<kTop>(l, b);
+    if (tid < kTop) {
+      uint64_t w = b[0];
+#pragma unroll
+      for (int r = 1; r < kTop; ++r) w = r == tid ? b[r] : w;
+      float v = -INFINITY;
+      int i = 0x7fffffff;
+      if (w) {
+        const int s = 0xffff - (int)((w >> 16) & 0xffffu);
+        i = (int)((long long)(V >> 3) * s / S) * 8 + (0xffff - (int)(w & 0xffffu));
+        v = __uint_as_float((uint32_t)logits[(long long)row * ld + i] << 16);
+      }
+      s_bv[tid] = v;
+      s_bi[tid] = i;
+    }
   }
+  __syncthreads();
   float bv[kTop];
   int bi[kTop];
-  block_top8<kFinishThreads>(tv, ti, bv, bi, s_v, s_i);
+#pragma unroll
+  for (int r = 0; r < kTop; ++r) {
+    bv[r] = s_bv[r];
+    bi[r] = s_bi[r];
+  }
   const float lmax = bv[0];
 
   // ---- histogram walk: thread t owns keys 65535 - 64t - j, j = 0..63 (descending) --
@@ -273,26 +302,47 @@ __global__ __launch_bounds__(kFinishThreads) void sf_logit_finish_kernel(
   // probability crosses.  Exactly one stretch holds the crossing (monotone sums).
   auto crosses = [&](float cum) { return sf_rbf(cum) > top_p; };
   if (!crosses(excl_p) && crosses(incl_p)) {
+    // the walk down the stretch to the first key whose mass crosses, in two halves
+    // of 32 counts, each read in one round of loads (count of key kb - j in
+    // cnt[j - 32 * half])
     float cp = excl_p, ce = excl_e;
-    float zc = -1.f;
-    for (int j = 0; j < 64 && zc < 0.f; ++j) {
-      const uint32_t c = h[kb - j];
-      if (!c) continue;
-      const float e = expf(key_value(kb - j) - lmax);
-      const float pj = sf_rbf(e / z);
-      if (crosses(cp + (float)c * pj)) {
-        // fewest tokens of this value whose cumulative probability crosses
-        uint32_t lo = 1, hi = c;
-        while (lo < hi) {
-          const uint32_t mid = (lo + hi) >> 1;
-          if (crosses(cp + (float)mid * pj)) hi = mid; else lo = mid + 1;
-        }
-        zc = ce + (float)lo * e;
+    bool found = false;
+    uint32_t cx = 0;
+    float ex = 0.f, px = 0.f, cpx = 0.f, cex = 0.f;
+    for (int half = 0; half < 2 && !found; ++half) {
+      uint32_t cnt[32];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const sf_u32x4 w = hv[15 - 8 * half - q];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) cnt[4 * q + 3 - r] = w[r];
       }
-      cp += (float)c * pj;
-      ce += (float)c * e;
+#pragma unroll
+      for (int jj = 0; jj < 32; ++jj) {
+        const int j = 32 * half + jj;
+        const uint32_t c = cnt[jj];
+        if (!found && c) {
+          const float e = expf(key_value(kb - j) - lmax);
+          const float pj = sf_rbf(e / z);
+          if (crosses(cp + (float)c * pj)) {
+            found = true;
+            cx = c; ex = e; px = pj; cpx = cp; cex = ce;
+          }
+          cp += (float)c * pj;
+          ce += (float)c * e;
+        }
+      }
     }
-    if (zc < 0.f) zc = ce;  // rounding kept the crossing out of reach: whole stretch
+    float zc = ce;  // rounding kept the crossing out of reach: whole stretch
+    if (found) {
+      // fewest tokens of the crossing value whose cumulative probability crosses
+      uint32_t lo = 1, hi = cx;
+      while (lo < hi) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (crosses(cpx + (float)mid * px)) hi = mid; else lo = mid + 1;
+      }
+      zc = cex + (float)lo * ex;
+    }
     s_cutf[1] = zc;
   }
   __syncthreads();
@@ -364,10 +414,10 @@ int slices_for(int M, int V) {
 // Rows the allocation-free entry point takes; with S = slices_for(M, V) slices per
 // row, M * S <= 256 for every M <= 64 and V <= 4 * 65535 (a call whose larger
 // vocabulary needs more than the 512 candidate lists is refused), so the
-// candidates fit in 512 * 8 pairs.
+// candidates fit in 512 * 8 keys.
 constexpr int kNoAllocMaxRows = 64;
 constexpr size_t kNoAllocHistBytes = (size_t)kNoAllocMaxRows * kKeys * 4;
-constexpr size_t kNoAllocBytes = kNoAllocHistBytes + (size_t)512 * kTop * 8;
+constexpr size_t kNoAllocBytes = kNoAllocHistBytes + (size_t)512 * kTop * 4;
 
 __global__ __launch_bounds__(256) void sf_zero_kernel(sf_u32x4* __restrict__ p, size_t n16) {
   for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (size_t)gridDim.x * 256)
@@ -378,12 +428,11 @@ int launch_stats(const uint16_t* logits, int M, int V, long long ld, float top_p
                  float* top_val, float* zfull, float* znuc, int32_t* greedy_tok, float* conf,
                  float* conf_full, uint32_t* hist, void* cand, hipStream_t st) {
   const int S = slices_for(M, V);
-  float* cand_v = reinterpret_cast<float*>(cand);
-  int32_t* cand_i = reinterpret_cast<int32_t*>(cand_v + (size_t)M * S * kTop);
+  uint32_t* cand_k = reinterpret_cast<uint32_t*>(cand);
   hipLaunchKernelGGL(sf_logit_slice_kernel, dim3(S, M), dim3(kSliceThreads), 0, st, logits, ld, V,
-                     hist, cand_v, cand_i);
+                     hist, cand_k);
   hipLaunchKernelGGL(sf_logit_finish_kernel, dim3(M), dim3(kFinishThreads), 0, st, logits, ld, V,
-                     S, top_p, hist, cand_v, cand_i, top_idx, top_val, zfull, znuc, greedy_tok,
+                     S, top_p, hist, cand_k, top_idx, top_val, zfull, znuc, greedy_tok,
                      conf, conf_full);
   return sf_launch_status();
 }
@@ -445,7 +494,7 @@ int scratch_for_current_device(hipStream_t st, void** out) {
 extern "C" size_t sf_logit_stats_workspace_bytes(int M) {
   if (M < 1) return 0;
   // candidates for the most slices any V takes (kMaxSlices)
-  return (size_t)M * kKeys * 4 + (size_t)M * kMaxSlices * kTop * 8;
+  return (size_t)M * kKeys * 4 + (size_t)M * kMaxSlices * kTop * 4;
 }
 
 extern "C" int sf_logit_stats(const uint16_t* logits, int M, int V, long long ld, float top_p,
@@ -473,7 +522,7 @@ extern "C" int sf_logit_stats_noalloc(const uint16_t* logits, int M, int V, long
                                  greedy_tok, conf, conf_full);
   if (a != SF_OK) return a;
   if (M > kNoAllocMaxRows ||
-      (size_t)M * slices_for(M, V) * kTop * 8 > kNoAllocBytes - kNoAllocHistBytes)
+      (size_t)M * slices_for(M, V) * kTop * 4 > kNoAllocBytes - kNoAllocHistBytes)
     return SF_ERR_SCRATCH;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   void* ws = nullptr;

@@ -114,6 +114,31 @@ inline float __shfl_xor(float v, int mask, int width = 64) {
   return out;
 }
 
+inline unsigned __shfl_xor(unsigned v, int mask, int width = 64) {
+  (void)width;
+  unsigned out;
+  sim_wave_exchange(&v, 4, [&](const uint8_t* b) { memcpy(&out, b + ((sim_lane() ^ mask) & 63) * 128, 4); });
+  return out;
+}
+
+template <typename T>
+inline T sim_shfl_xor(T v, int mask) {
+  T out;
+  sim_wave_exchange(&v, sizeof(T), [&](const uint8_t* b) {
+    memcpy(&out, b + ((sim_lane() ^ mask) & 63) * 128, sizeof(T));
+  });
+  return out;
+}
+inline int __shfl_xor(int v, int mask, int width = 64) { (void)width; return sim_shfl_xor(v, mask); }
+inline unsigned long __shfl_xor(unsigned long v, int mask, int width = 64) {
+  (void)width;
+  return sim_shfl_xor(v, mask);
+}
+inline unsigned long long __shfl_xor(unsigned long long v, int mask, int width = 64) {
+  (void)width;
+  return sim_shfl_xor(v, mask);
+}
+
 // __shfl_up: lane l reads lane l - delta; lanes below delta keep their own value
 inline float __shfl_up(float v, unsigned delta, int width = 64) {
   (void)width;
@@ -159,6 +184,8 @@ inline float sim_f16_to_f(uint16_t h) {
 inline int min(int a, int b) { return a < b ? a : b; }
 inline int max(int a, int b) { return a > b ? a : b; }
 inline long long min(long long a, long long b) { return a < b ? a : b; }
+inline unsigned min(unsigned a, unsigned b) { return a < b ? a : b; }
+inline unsigned max(unsigned a, unsigned b) { return a > b ? a : b; }
 inline float sim_exp2f(float x) { return std::exp2(x); }
 #define __builtin_amdgcn_exp2f(x) sim_exp2f(x)
 // scheduling hints: no effect on what a kernel computes
