@@ -169,6 +169,17 @@ int main(int argc, char** argv) {
         for (int c = 0; c < D; ++c) touched += ffn[(size_t)r * D + c] != 0x1234;
     printf("  %-22s %s\n", "down: other rows", touched ? "OVERWRITTEN" : "untouched");
     ok &= cd.report() && touched == 0;
+    // the shared tiles' arrival counters are left zero: a second call on the same
+    // workspace writes the same rows again, bit for bit
+    std::vector<uint16_t> ffn2((size_t)BN * D, 0x1234);
+    if (sf_ffn_down_scatter(act_in.data(), &cnt, bucket, rows.data(), pd.data(), I, D, ffn2.data(),
+                            ws.data(), ws.size() * 4, nullptr)) {
+      fprintf(stderr, "sf_ffn_down_scatter failed\n");
+      return 1;
+    }
+    const bool same = ffn2 == ffn;
+    printf("  %-22s %s\n", "down: repeat call", same ? "identical" : "DIFFERENT");
+    ok &= same;
   }
 
   // ---- o_proj + residual and lm_head over M static rows -----------------------------------
