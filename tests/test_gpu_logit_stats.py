@@ -119,6 +119,36 @@ def test_ties_lowest_index():
     assert st.greedy_tok.tolist() == [40, 100, 20]
 
 
+def top8_order(row):
+    """The 8 (index, value) pairs of a row by value descending, then index ascending
+    (both zeros equal, as in a float comparison)."""
+    v = row.float().tolist()
+    idx = sorted(range(len(v)), key=lambda i: (-v[i], i))[:8]
+    return idx, [v[i] for i in idx]
+
+
+def test_top8_signed_zeros_and_infinities():
+    """Top-8 order on ties the packed order keys must get right: +0 and -0 tie (lower
+    index first), and -inf entries fill the list behind the finite values in index
+    order."""
+    V = 152064
+    a = torch.full((V,), -30.0)
+    a[[500, 9000, 300, 150000]] = torch.tensor([3.0, 2.0, 2.0, 1.0])
+    a[[77, 12, 40000, 5]] = torch.tensor([0.0, -0.0, 0.0, -0.0])
+    b = torch.full((V,), float("-inf"))
+    b[[1000, 20, 70000]] = torch.tensor([1.0, 0.5, 0.5])
+    logits = torch.stack([a, b]).to(torch.bfloat16)
+    st = _lib.logit_stats(logits.cuda(), top_p=0.95)
+    torch.cuda.synchronize()
+    for r in range(2):
+        idx, val = top8_order(logits[r])
+        assert st.top_idx[r].tolist() == idx, r
+        assert st.top_val[r].tolist() == val, r
+    assert st.top_idx[0].tolist() == [500, 300, 9000, 150000, 5, 12, 77, 40000]
+    assert st.top_idx[1].tolist() == [1000, 20, 70000, 0, 1, 2, 3, 4]
+    assert st.greedy_tok.tolist() == [500, 1000]
+
+
 def test_flat_row():
     """Every logit equal: the greedy token is index 0 (the nucleus size of such a
     row depends on how the running sum of equal probabilities rounds, so only the

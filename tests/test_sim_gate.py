@@ -264,6 +264,29 @@ def test_logit_stats(sim, M, V, scale, top_p):
         assert torch.equal(getattr(st, f), getattr(st2, f)), f
 
 
+def test_logit_stats_top8_ties(sim):
+    """The packed order keys of the top-8: +0 and -0 tie (lower index first), -inf
+    entries follow the finite values in index order, ties across slices go to the
+    lower index (tests/test_gpu_logit_stats.py has the same rows at V = 152064)."""
+    from tests.test_gpu_logit_stats import top8_order
+    V = 24576
+    a = torch.full((V,), -30.0)
+    a[[500, 9000, 300, 20000]] = torch.tensor([3.0, 2.0, 2.0, 1.0])
+    a[[77, 12, 16000, 5]] = torch.tensor([0.0, -0.0, 0.0, -0.0])
+    b = torch.full((V,), float("-inf"))
+    b[[1000, 20, 17000]] = torch.tensor([1.0, 0.5, 0.5])
+    c = torch.full((V,), 2.0)   # every token tied: the first 8 indices
+    logits = torch.stack([a, b, c]).to(torch.bfloat16)
+    st, _ = sim_logit_stats(sim, logits, 0.95)
+    for r in range(3):
+        idx, val = top8_order(logits[r])
+        assert st.top_idx[r].tolist() == idx, r
+        assert st.top_val[r].tolist() == val, r
+    assert st.top_idx[0].tolist() == [500, 300, 9000, 20000, 5, 12, 77, 16000]
+    assert st.top_idx[1].tolist() == [1000, 20, 17000, 0, 1, 2, 3, 4]
+    assert st.top_idx[2].tolist() == list(range(8))
+
+
 def test_logit_stats_noalloc_sequence(sim):
     """sf_logit_stats_noalloc over calls of changing row count (more, fewer, more
     again) gives exactly the workspace entry point's statistics every time: its
