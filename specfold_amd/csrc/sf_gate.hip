@@ -35,40 +35,42 @@ __global__ __launch_bounds__(kGateWaves * 64) void sf_gate_rows_kernel(
   if (r >= BN) return;
   const int b = r / N;
   const int n = r - b * N;
+  // Two rounds of loads.  (1) The parent, every branch's source at position n
+  // (lane l: branch l; B1 <= 64), the row and the norm weights; (2) the parent row
+  // and the FFN rows of the row's and the parent's sources, whose ids come from
+  // round 1 by shuffles instead of a further round through memory.  Addresses are
+  // clamped and nothing branches, so each round costs one memory latency.
   int p = par ? par[b] : b;
+  const int src_n = RESID ? src_prev[min(lane, B1 - 1) * N + n] : 0;
+  const int nvec = D >> 3;
+  const sf_u32x4* xrow = reinterpret_cast<const sf_u32x4*>(hidden + (size_t)r * D);
+  const sf_u32x4* wrow = reinterpret_cast<const sf_u32x4*>(ln_w);
+  sf_u32x4 xv[VPL], pv[VPL], wv[VPL];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) xv[i] = xrow[min(lane + i * 64, nvec - 1)];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) wv[i] = wrow[min(lane + i * 64, nvec - 1)];
   p = p < 0 ? 0 : (p >= B1 ? B1 - 1 : p);
   // a draft row is gated against its parent's; the root branch (branch 0, or with
   // ROOTS every branch that is its own parent: the main branch of each sequence
   // of a batched step) is always recomputed
   const bool draft = (ROOTS ? p != b : b > 0) && mode != SF_GATE_ALL;
   const int pr = p * N + n;
-
-  const int nvec = D >> 3;
-  const sf_u32x4* xrow = reinterpret_cast<const sf_u32x4*>(hidden + (size_t)r * D);
   const sf_u32x4* prow = reinterpret_cast<const sf_u32x4*>(hidden + (size_t)pr * D);
-  const sf_u32x4* wrow = reinterpret_cast<const sf_u32x4*>(ln_w);
-
-  // Every load of the rows and the norm weight is issued before the first use
-  // (clamped addresses, no branches), so the wave pays one memory latency per
-  // dependent step instead of one per vector.
-  sf_u32x4 xv[VPL], pv[VPL], wv[VPL];
   sf_u32x4 fx[RESID ? VPL : 1], fp[RESID ? VPL : 1];
   if (RESID) {
-    const sf_u32x4* fxrow =
-        reinterpret_cast<const sf_u32x4*>(ffn + (size_t)(src_prev[r] * N + n) * D);
-    const sf_u32x4* fprow =
-        reinterpret_cast<const sf_u32x4*>(ffn + (size_t)(src_prev[pr] * N + n) * D);
+    // src_prev[b*N + n] and src_prev[p*N + n]
+    const int s_r = __shfl(src_n, b, 64);
+    const int s_p = __shfl(src_n, p, 64);
+    const sf_u32x4* fxrow = reinterpret_cast<const sf_u32x4*>(ffn + (size_t)(s_r * N + n) * D);
+    const sf_u32x4* fprow = reinterpret_cast<const sf_u32x4*>(ffn + (size_t)(s_p * N + n) * D);
 #pragma unroll
     for (int i = 0; i < VPL; ++i) fx[i] = fxrow[min(lane + i * 64, nvec - 1)];
 #pragma unroll
     for (int i = 0; i < VPL; ++i) fp[i] = fprow[min(lane + i * 64, nvec - 1)];
   }
 #pragma unroll
-  for (int i = 0; i < VPL; ++i) xv[i] = xrow[min(lane + i * 64, nvec - 1)];
-#pragma unroll
   for (int i = 0; i < VPL; ++i) pv[i] = prow[min(lane + i * 64, nvec - 1)];
-#pragma unroll
-  for (int i = 0; i < VPL; ++i) wv[i] = wrow[min(lane + i * 64, nvec - 1)];
   if (RESID) {
     // h = bf16(hp + ffn), the layer input, kept as packed bf16
     sf_u32x4* hout = reinterpret_cast<sf_u32x4*>(hidden_out + (size_t)r * D);

@@ -107,6 +107,13 @@ inline float __shfl(float v, int src, int width = 64) {
   return out;
 }
 
+inline int __shfl(int v, int src, int width = 64) {
+  (void)width;
+  int out;
+  sim_wave_exchange(&v, 4, [&](const uint8_t* b) { memcpy(&out, b + (src & 63) * 128, 4); });
+  return out;
+}
+
 inline float __shfl_xor(float v, int mask, int width = 64) {
   (void)width;
   float out;
