@@ -202,7 +202,8 @@ int sf_qkv_rope_gated(const uint16_t* xn, const int8_t* rec, const int32_t* par,
  * whole prefix) — the causal forward the NLD generator commits blocks with
  * (specfold/generate/nld_generation.py:300-310, use_causal_mask=True); used
  * with every row recomputed.
- * Writes o32, o_bf, m_tab, z_tab for the rows listed in rows[0:min(count,bucket)].
+ * Writes o32, o_bf, m_tab, z_tab for the rows listed in rows[0:min(count,bucket)];
+ * o32, m_tab and z_tab may be NULL (not written: o_proj reads o_bf only).
  * prefix_len (optional, device int32[1]): the prefix length, read on the device;
  * P is then the capacity the grid and workspace are sized for (so one captured
  * graph serves a growing cache).  With prefix_len NULL, P is the length.

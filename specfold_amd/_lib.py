@@ -326,13 +326,24 @@ def attn_workspace_bytes(bucket: int, H: int, P: int) -> int:
     return int(load().sf_attn_workspace_bytes(bucket, H, P))
 
 
+def _need_attn_outputs(BN, H, hd, o32, o_bf, m_tab, z_tab):
+    """o_bf is required; o32, m_tab and z_tab may be None (not written)."""
+    if o32 is not None:
+        _need(o32, "o32", torch.float32, min_numel=BN * H * hd)
+    _need(o_bf, "o_bf", torch.bfloat16, min_numel=BN * H * hd)
+    for nm, t in (("m_tab", m_tab), ("z_tab", z_tab)):
+        if t is not None:
+            _need(t, nm, torch.float32, min_numel=BN * H, align=4)
+
+
 def attn_prefix_block(q_buf, kv_buf, prefix_k, prefix_v, page_table, P, page_size, page_stride,
                       head_stride, src, rows, count, bucket, B1, N, H, Hkv, hd, scaling,
                       o32, o_bf, m_tab, z_tab, workspace, prefix_len=None, stream=None,
                       block_causal: bool = False) -> None:
     """prefix_len: optional device int32[1] holding the prefix length; P is then
     the capacity (grid / workspace size).  block_causal: block position n sees the
-    block keys j <= n only (a causal block commit; every row recomputed)."""
+    block keys j <= n only (a causal block commit; every row recomputed).  o32, m_tab
+    and z_tab may be None (not written)."""
     BN = B1 * N
     _need(q_buf, "q_buf", torch.bfloat16, min_numel=(BN + 1) * H * hd)
     _need(kv_buf, "kv_buf", torch.bfloat16, min_numel=(BN + 1) * 2 * Hkv * hd)
@@ -345,10 +356,7 @@ def attn_prefix_block(q_buf, kv_buf, prefix_k, prefix_v, page_table, P, page_siz
     _need(src, "src", torch.int32, min_numel=BN, align=4)
     _need(rows, "rows", torch.int32, min_numel=bucket, align=4)
     _need(count, "count", torch.int32, min_numel=1, align=4)
-    _need(o32, "o32", torch.float32, min_numel=BN * H * hd)
-    _need(o_bf, "o_bf", torch.bfloat16, min_numel=BN * H * hd)
-    _need(m_tab, "m_tab", torch.float32, min_numel=BN * H, align=4)
-    _need(z_tab, "z_tab", torch.float32, min_numel=BN * H, align=4)
+    _need_attn_outputs(BN, H, hd, o32, o_bf, m_tab, z_tab)
     _need(workspace, "workspace", torch.uint8, min_numel=attn_workspace_bytes(bucket, H, P),
           align=256)
     if prefix_len is not None:
@@ -369,7 +377,7 @@ def attn_rows(q_buf, kv_buf, prefix_k, prefix_v, page_table, P, page_size, page_
     """Attention of every row of branches [b_first, b_first + b_count): recomputed
     rows as attn_prefix_block, folded rows from their source row's query over the
     prefix and their own branch's block keys (sf_attn_rows: attention + chain
-    correction in one call)."""
+    correction in one call).  o32, m_tab and z_tab may be None (not written)."""
     BN = B1 * N
     _need(q_buf, "q_buf", torch.bfloat16, min_numel=(BN + 1) * H * hd)
     _need(kv_buf, "kv_buf", torch.bfloat16, min_numel=(BN + 1) * 2 * Hkv * hd)
@@ -382,10 +390,7 @@ def attn_rows(q_buf, kv_buf, prefix_k, prefix_v, page_table, P, page_size, page_
     _need(src, "src", torch.int32, min_numel=BN, align=4)
     _need(rows, "rows", torch.int32, min_numel=bucket, align=4)
     _need(count, "count", torch.int32, min_numel=1, align=4)
-    _need(o32, "o32", torch.float32, min_numel=BN * H * hd)
-    _need(o_bf, "o_bf", torch.bfloat16, min_numel=BN * H * hd)
-    _need(m_tab, "m_tab", torch.float32, min_numel=BN * H, align=4)
-    _need(z_tab, "z_tab", torch.float32, min_numel=BN * H, align=4)
+    _need_attn_outputs(BN, H, hd, o32, o_bf, m_tab, z_tab)
     _need(workspace, "workspace", torch.uint8, min_numel=attn_workspace_bytes(bucket, H, P),
           align=256)
     if prefix_len is not None:

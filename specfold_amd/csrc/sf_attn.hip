@@ -779,7 +779,7 @@ sf_attn_rows_kernel(
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
         const sf_f32x4 o = acc[dt] * inv;
-        *reinterpret_cast<sf_f32x4*>(o32 + off + dt * 16) = o;
+        if (o32) *reinterpret_cast<sf_f32x4*>(o32 + off + dt * 16) = o;   // (kernel argument)
         sf_u32x2 w;
         w[0] = sf_pack2(o[0], o[1]);
         w[1] = sf_pack2(o[2], o[3]);
@@ -787,8 +787,8 @@ sf_attn_rows_kernel(
       }
       if (grp == 0) {
         // the natural-base max the scores were measured from
-        m_tab[(size_t)ro * H + hq] = m_new * 0.69314718055994530942f;
-        z_tab[(size_t)ro * H + hq] = l_new;
+        if (m_tab) m_tab[(size_t)ro * H + hq] = m_new * 0.69314718055994530942f;
+        if (z_tab) z_tab[(size_t)ro * H + hq] = l_new;
       }
     }
     // the next row of this wave (its V copies overwrite the region: the reads of
@@ -817,8 +817,8 @@ int attention(bool folded, const uint16_t* q_buf, const uint16_t* kv_buf,
               const int32_t* prefix_len, int block_causal, float* o32, uint16_t* o_bf,
               float* m_tab, float* z_tab, void* workspace, size_t workspace_bytes,
               hipStream_t st) {
-  if (!q_buf || !kv_buf || !src || !rows || !count || !o32 || !o_bf || !m_tab || !z_tab)
-    return SF_ERR_ARG;
+  // o32, m_tab and z_tab may be NULL (not written): o_proj reads o_bf only
+  if (!q_buf || !kv_buf || !src || !rows || !count || !o_bf) return SF_ERR_ARG;
   if (hd != kHD || H < 1 || Hkv < 1 || H % Hkv != 0 || H / Hkv > kMaxG) return SF_ERR_SHAPE;
   if (N < 1 || N > kMaxN || B1 < 1 || bucket < 1 || bucket > B1 * N) return SF_ERR_SHAPE;
   // the rows kernel stages src in a kMaxBucket-entry LDS table and finds a row's

@@ -613,14 +613,15 @@ class FoldedVerifyEngine:
             # rows over [prefix ; own block], the folded rows from their source row's
             # query over their own branch's keys (what the chain correction computes)
             if batch is None:
-                self._attention(buf, cache, li, count, bucket, B1, N, causal=causal)
+                self._attention(buf, cache, li, count, bucket, B1, N, causal=causal,
+                                side=trace is not None)
             else:
                 # each sequence's rows over its own prefix: the compacted rows are
                 # ascending, so sequence s owns a contiguous run of them
                 rows_s, count_s = batch.split_rows(buf.rows, count, bucket, N)
                 for si, c in enumerate(batch.caches):
                     self._attention(buf, c, li, count_s[si:si + 1], bucket, B1, N,
-                                    rows=rows_s[si],
+                                    rows=rows_s[si], side=trace is not None,
                                     branches=(batch.offsets[si], batch.sizes[si]))
 
             # o_proj for every row (fastdllm_v2_folded.py:207-209) in one pass over Wo,
@@ -656,9 +657,12 @@ class FoldedVerifyEngine:
 
     def _attention(self, buf: _Buffers, cache, li: int, count, bucket: int, B1: int, N: int,
                    causal: bool = False, rows: Optional[torch.Tensor] = None,
-                   branches: Optional[Tuple[int, int]] = None):
+                   branches: Optional[Tuple[int, int]] = None, side: bool = False):
         """Every row of the branches (first, count) (default: all): sf_attn_rows; a
-        causal forward (every row recomputed) takes sf_attn_prefix_block."""
+        causal forward (every row recomputed) takes sf_attn_prefix_block.  side: also
+        write the fp32 output and the softmax state (m, Z) (a traced step); o_proj
+        reads only the bf16 output."""
+        o32, m_tab, z_tab = (buf.o32, buf.m_tab, buf.z_tab) if side else (None, None, None)
         pv = prefix_view(cache, li)
         if pv is None:
             P_arg, plen = 0, None
@@ -672,14 +676,14 @@ class FoldedVerifyEngine:
         rows = buf.rows if rows is None else rows
         if causal:
             _lib.attn_prefix_block(buf.q_buf, buf.kv_buf, *view, buf.src, rows, count, bucket, B1,
-                                   N, self.H, self.Hkv, self.hd, self.scaling, buf.o32, buf.o_bf,
-                                   buf.m_tab, buf.z_tab, buf.ws_attn, prefix_len=plen,
+                                   N, self.H, self.Hkv, self.hd, self.scaling, o32, buf.o_bf,
+                                   m_tab, z_tab, buf.ws_attn, prefix_len=plen,
                                    block_causal=True)
         else:
             b0, nb = branches if branches is not None else (0, B1)
             _lib.attn_rows(buf.q_buf, buf.kv_buf, *view, buf.src, rows, count, bucket, B1, N,
-                           b0, nb, self.H, self.Hkv, self.hd, self.scaling, buf.o32, buf.o_bf,
-                           buf.m_tab, buf.z_tab, buf.ws_attn, prefix_len=plen)
+                           b0, nb, self.H, self.Hkv, self.hd, self.scaling, o32, buf.o_bf,
+                           m_tab, z_tab, buf.ws_attn, prefix_len=plen)
 
     @staticmethod
     def _cache_key(cache):
