@@ -783,7 +783,7 @@ sf_attn_rows_kernel(
         sf_u32x2 w;
         w[0] = sf_pack2(o[0], o[1]);
         w[1] = sf_pack2(o[2], o[3]);
-        *reinterpret_cast<sf_u32x2*>(o_bf + off + dt * 16) = w;
+        sf_handoff_store(reinterpret_cast<sf_u32x2*>(o_bf + off + dt * 16), w);
       }
       if (grp == 0) {
         // the natural-base max the scores were measured from

@@ -223,7 +223,7 @@ __global__ __launch_bounds__(kPrnThreads) void part_residual_norm_kernel(
       hv[i][j] = sf_pack2(a[2 * j] + y0, a[2 * j + 1] + y1);
     }
     if (tid + i * kPrnThreads < nvec) {
-      hrow[tid + i * kPrnThreads] = hv[i];
+      sf_handoff_store(&hrow[tid + i * kPrnThreads], hv[i]);
       float h[8];
       sf_unpack8(hv[i], h);
 #pragma unroll
@@ -250,7 +250,7 @@ __global__ __launch_bounds__(kPrnThreads) void part_residual_norm_kernel(
 #pragma unroll
       for (int j = 0; j < 4; ++j)
         o[j] = sf_pack2(g[2 * j] * sf_rbf(f[2 * j] * inv), g[2 * j + 1] * sf_rbf(f[2 * j + 1] * inv));
-      orow[idx] = o;
+      sf_handoff_store(&orow[idx], o);
     }
   }
 }

@@ -86,7 +86,7 @@ __global__ __launch_bounds__(kGateWaves * 64) void sf_gate_rows_kernel(
         xv[i][j] = sf_pack2(a[2 * j] + c[2 * j], a[2 * j + 1] + c[2 * j + 1]);
         pv[i][j] = sf_pack2(e[2 * j] + g[2 * j], e[2 * j + 1] + g[2 * j + 1]);
       }
-      if (lane + i * 64 < nvec) hout[lane + i * 64] = xv[i];
+      if (lane + i * 64 < nvec) sf_handoff_store(&hout[lane + i * 64], xv[i]);
     }
   }
 
@@ -146,7 +146,7 @@ __global__ __launch_bounds__(kGateWaves * 64) void sf_gate_rows_kernel(
         const float c = sf_rbf(wf[2 * j + 1] * sf_rbf(xf[2 * j + 1] * inv));
         o[j] = sf_pack2(a, c);
       }
-      out[idx] = o;
+      sf_handoff_store(&out[idx], o);
     }
   }
 }
