@@ -301,7 +301,7 @@ __global__ __launch_bounds__(256) void down_fixup_kernel(const float* __restrict
   sf_u32x2 o;
   o[0] = sf_pack2(y[0], y[1]);
   o[1] = sf_pack2(y[2], y[3]);
-  *reinterpret_cast<sf_u32x2*>(out + (size_t)row * N + c) = o;
+  sf_handoff_store(reinterpret_cast<sf_u32x2*>(out + (size_t)row * N + c), o);
 }
 
 // Fix-up of the gate/up GEMM: a 128-column tile computed by several workgroups has
@@ -333,7 +333,7 @@ __global__ __launch_bounds__(256) void silu_fixup_kernel(const float* __restrict
     sf_u32x2 o;
     o[0] = sf_pack2(r[0], r[1]);
     o[1] = sf_pack2(r[2], r[3]);
-    *reinterpret_cast<sf_u32x2*>(act + (size_t)m * I + c) = o;
+    sf_handoff_store(reinterpret_cast<sf_u32x2*>(act + (size_t)m * I + c), o);
   }
 }
 

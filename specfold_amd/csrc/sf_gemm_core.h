@@ -432,7 +432,7 @@ void gemm_sk_kernel(const uint16_t* __restrict__ A, const int32_t* __restrict__ 
           sf_u32x2 o;
           o[0] = sf_pack2(r[0], r[1]);
           o[1] = sf_pack2(r[2], r[3]);
-          *reinterpret_cast<sf_u32x2*>(ep.out + (size_t)(m0 + m) * ep.ldo + c0 + c) = o;
+          sf_handoff_store(reinterpret_cast<sf_u32x2*>(ep.out + (size_t)(m0 + m) * ep.ldo + c0 + c), o);
         }
       } else {
         float r[4];
@@ -454,7 +454,7 @@ void gemm_sk_kernel(const uint16_t* __restrict__ A, const int32_t* __restrict__ 
         sf_u32x2 ov;
         ov[0] = sf_pack2(r[0], r[1]);
         ov[1] = sf_pack2(r[2], r[3]);
-        *reinterpret_cast<sf_u32x2*>(ep.out + o) = ov;
+        sf_handoff_store(reinterpret_cast<sf_u32x2*>(ep.out + o), ov);
       }
     }
     __syncthreads();  // the tile LDS is the next piece's ring

@@ -255,7 +255,7 @@ void head_kernel(const uint16_t* __restrict__ X, int Mo, int m0, HeadRows hr,
       const size_t orow = (size_t)head_out_row(row, hr);
 #pragma unroll
       for (int tt = 0; tt < kHWN; ++tt)
-        *reinterpret_cast<sf_u32x2*>(out + orow * ldo + col0 + tt * 16) = v[tt];
+        sf_handoff_store(reinterpret_cast<sf_u32x2*>(out + orow * ldo + col0 + tt * 16), v[tt]);
     }
   }
 }
