@@ -397,8 +397,8 @@ int sf_head_logits_rows(const uint16_t* x, int M, const uint16_t* w, int D, int 
  * workspace: sf_logit_stats_workspace_bytes(M) bytes, zero before the first call:
  * its first M * 65536 32-bit counters are value histograms that every call leaves
  * zero again; the rest is scratch each call overwrites before reading.
- * Limits: V % 8 == 0, ld % 8 == 0, 16-byte aligned logits, 0 < top_p (top_p >= 1
- * keeps every token).
+ * Limits: 8 <= V <= 2096896 (32 slices of at most 8191 8-token vectors), V % 8 == 0,
+ * ld % 8 == 0, 16-byte aligned logits, 0 < top_p (top_p >= 1 keeps every token).
  */
 size_t sf_logit_stats_workspace_bytes(int M);
 int sf_logit_stats(const uint16_t* logits, int M, int V, long long ld, float top_p,

@@ -382,3 +382,26 @@ inline int prefix_launch_grid(int qmax, int nch, int Hkv) {
 }
 
 }  // namespace sfa
+
+// ---------------------------------------------------------------------------
+// Greedy statistics (sf_logits.hip): the slices of a logits row
+// ---------------------------------------------------------------------------
+namespace sfl {
+
+constexpr int kMaxSlices = 32;          // slices per row: one wave merges their lists
+constexpr int kMaxSliceVectors = 8191;  // 8-token vectors per slice: <= 65528 tokens,
+                                        // so a slice's 16-bit counts and places fit
+constexpr int kMaxVocab = kMaxSlices * kMaxSliceVectors * 8;   // 2,096,896 tokens
+
+// Slices per row of V tokens (V % 8 == 0) for M rows: about 256 workgroups in
+// all, at most kMaxSlices, and enough that no slice holds more than
+// kMaxSliceVectors vectors (V <= kMaxVocab).
+inline int slices_for(int M, int V) {
+  const int nvec = V / 8;
+  const int need = (nvec + kMaxSliceVectors - 1) / kMaxSliceVectors;
+  return sf_imax(need, sf_imax(1, sf_imin(kMaxSlices, 256 / M)));
+}
+// Slice s of S holds the vectors [slice_begin(s), slice_begin(s + 1)) of nvec.
+SF_IDX int slice_begin(int s, int nvec, int S) { return (int)((long long)nvec * s / S); }
+
+}  // namespace sfl

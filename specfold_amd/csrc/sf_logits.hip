@@ -34,6 +34,7 @@
 #include <mutex>
 
 #include "sf_common.h"
+#include "sf_index.h"
 
 namespace {
 
@@ -41,9 +42,10 @@ constexpr int kTop = 8;
 constexpr int kSliceThreads = 512;
 constexpr int kFinishThreads = 1024;
 constexpr int kKeys = 65536;
-constexpr int kMaxSlices = 32;
-constexpr int kMaxSliceTokens = 65535;   // a slice's counts and token places fit 16 bits
+using sfl::kMaxSlices;
+using sfl::slices_for;
 static_assert(kMaxSlices <= 64, "one wave merges the slices' lists");
+static_assert(sfl::kMaxSliceVectors * 8 <= 65535, "a slice's counts and token places fit 16 bits");
 
 // order key of a bf16 bit pattern: larger value -> larger key
 SF_DEV uint32_t bf16_key(uint32_t b) { return (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u); }
@@ -163,7 +165,7 @@ __global__ __launch_bounds__(kSliceThreads) void sf_logit_slice_kernel(
   const uint16_t* x = logits + (long long)row * ld;
   uint32_t* h = hist + (size_t)row * kKeys;
   const int nvec = V >> 3;
-  const int v0 = (int)((long long)nvec * s / S), v1 = (int)((long long)nvec * (s + 1) / S);
+  const int v0 = sfl::slice_begin(s, nvec, S), v1 = sfl::slice_begin(s + 1, nvec, S);
   // the thread's top-8 keys in descending order: each token passes down the list
   // in a compare-exchange chain (branch-free; the slice has at most 65535 tokens)
   uint32_t top[kTop];
@@ -253,7 +255,7 @@ __global__ __launch_bounds__(kFinishThreads) void sf_logit_finish_kernel(
       int i = 0x7fffffff;
       if (w) {
         const int s = 0xffff - (int)((w >> 16) & 0xffffu);
-        i = (int)((long long)(V >> 3) * s / S) * 8 + (0xffff - (int)(w & 0xffffu));
+        i = sfl::slice_begin(s, V >> 3, S) * 8 + (0xffff - (int)(w & 0xffffu));
         v = __uint_as_float((uint32_t)logits[(long long)row * ld + i] << 16);
       }
       s_bv[tid] = v;
@@ -404,15 +406,8 @@ __global__ __launch_bounds__(kFinishThreads) void sf_logit_finish_kernel(
   }
 }
 
-// Slices per row: about 256 workgroups in all, at most kMaxSlices, and enough
-// that no slice counts more than kMaxSliceTokens tokens (V <= kMaxSlices * that).
-int slices_for(int M, int V) {
-  const int need = (V + kMaxSliceTokens - 1) / kMaxSliceTokens;
-  return max(need, max(1, min(kMaxSlices, 256 / M)));
-}
-
 // Rows the allocation-free entry point takes; with S = slices_for(M, V) slices per
-// row, M * S <= 256 for every M <= 64 and V <= 4 * 65535 (a call whose larger
+// row (sf_index.h), M * S <= 256 for every M <= 64 and V <= 4 * 65528 (a call whose larger
 // vocabulary needs more than the 512 candidate lists is refused), so the
 // candidates fit in 512 * 8 keys.
 constexpr int kNoAllocMaxRows = 64;
@@ -444,7 +439,7 @@ int check_stats_args(const uint16_t* logits, int M, int V, long long ld, float t
   if (!logits || !top_idx || !top_val || !zfull || !znuc || !greedy_tok || !conf || !conf_full)
     return SF_ERR_ARG;
   if (M < 1 || V < kTop || V % 8 != 0 || ld < V || ld % 8 != 0) return SF_ERR_SHAPE;
-  if (V > kMaxSlices * kMaxSliceTokens) return SF_ERR_SHAPE;
+  if (V > sfl::kMaxVocab) return SF_ERR_SHAPE;
   if (reinterpret_cast<uintptr_t>(logits) % 16 != 0 || !(top_p > 0.0f)) return SF_ERR_ARG;
   return SF_OK;
 }

@@ -648,6 +648,36 @@ static void check_attention_grid() {
   printf("attention grids: %lld shapes\n", n);
 }
 
+// Greedy statistics: for every vector count a row can have (V <= kMaxVocab) and
+// every minimum slice count M's share of 256 workgroups gives, the slices tile the
+// row's vectors exactly, number at most kMaxSlices, and none holds more than
+// kMaxSliceVectors vectors (its 16-bit counts and token places fit); V beyond
+// kMaxVocab needs more slices than one wave merges.
+static void check_logit_slices() {
+  long long n = 0;
+  const int nmax = sfl::kMaxVocab / 8;
+  for (int M : {1, 2, 3, 5, 7, 8, 9, 16, 31, 32, 33, 64, 85, 86, 127, 128, 129, 255, 256, 257,
+                512, 1024}) {
+    for (int nvec = 1; nvec <= nmax; ++nvec) {
+      const int S = sfl::slices_for(M, nvec * 8);
+      CHECK(S >= 1 && S <= sfl::kMaxSlices, "slice count");
+      CHECK(sfl::slice_begin(0, nvec, S) == 0 && sfl::slice_begin(S, nvec, S) == nvec,
+            "slices cover the row");
+      int big = 0;
+      for (int s = 0; s < S; ++s) {
+        const int len = sfl::slice_begin(s + 1, nvec, S) - sfl::slice_begin(s, nvec, S);
+        CHECK(len >= 0, "slice order");
+        big = len > big ? len : big;
+      }
+      CHECK(big <= sfl::kMaxSliceVectors, "M %d, %d vectors: a slice of %d", M, nvec, big);
+      ++n;
+    }
+  }
+  for (int M : {1, 64, 1024})
+    CHECK(sfl::slices_for(M, sfl::kMaxVocab + 8) > sfl::kMaxSlices, "past the vocabulary cap");
+  printf("logit slices: %lld shapes\n", n);
+}
+
 int main(int argc, char** argv) {
   if (argc != 2) {
     fprintf(stderr, "usage: index_check <libspecfold_amd.so>\n");
@@ -673,6 +703,7 @@ int main(int argc, char** argv) {
   check_lds_paths();
   check_page_addressing();
   check_attention_grid();
+  check_logit_slices();
   printf("OK (%lld checks)\n", g_checks);
   return 0;
 }
