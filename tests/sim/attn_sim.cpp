@@ -171,8 +171,25 @@ int main(int argc, char** argv) {
   printf("P=%d ps=%d B1=%d N=%d H=%d/%d R=%d causal=%d folded=%d: O max abs err %.3g (|O| max "
          "%.3g), m %.3g, Z rel %.3g\n", P, ps, B1, N, H, Hkv, R, causal, folded, err_o, max_o,
          err_m, err_z);
-  const bool ok = err_o <= 2e-4 * std::max(1.0, max_o) && err_m <= 1e-4 && err_z <= 1e-4 &&
-                  std::isfinite(err_o) && std::isfinite(err_m) && std::isfinite(err_z);
+  bool ok = err_o <= 2e-4 * std::max(1.0, max_o) && err_m <= 1e-4 && err_z <= 1e-4 &&
+            std::isfinite(err_o) && std::isfinite(err_m) && std::isfinite(err_z);
+  // without the optional outputs (fp32 O, m, Z: NULL) the bf16 output is the same
+  std::vector<uint16_t> obf2((size_t)BN * H * hd);
+  const int st2 =
+      folded ? sf_attn_rows(q.data(), kv.data(), pk.data(), pv.data(), table.data(), P, ps,
+                            page_stride, head_stride, src.data(), rows.data(), &count, bucket, B1,
+                            N, 0, B1, H, Hkv, hd, scaling, &plen, nullptr, obf2.data(), nullptr,
+                            nullptr, ws_al, wsb, nullptr)
+             : sf_attn_prefix_block(q.data(), kv.data(), pk.data(), pv.data(), table.data(), P,
+                                    ps, page_stride, head_stride, src.data(), rows.data(), &count,
+                                    bucket, B1, N, H, Hkv, hd, scaling, &plen, causal, nullptr,
+                                    obf2.data(), nullptr, nullptr, ws_al, wsb, nullptr);
+  bool same = st2 == 0;
+  for (size_t k = 0; k < out_rows.size() && same; ++k)
+    for (int e = 0; e < H * hd; ++e)
+      same &= obf2[(size_t)out_rows[k] * H * hd + e] == obf[(size_t)out_rows[k] * H * hd + e];
+  printf("  without fp32 O / m / Z: bf16 output %s\n", same ? "identical" : "DIFFERENT");
+  ok &= same;
   if (!ok) printf("FAIL\n");
   return ok ? 0 : 1;
 }
