@@ -129,15 +129,16 @@ __global__ __launch_bounds__(256) void residual_post_norm_kernel(
 }
 
 // The o_proj residual from the all-rows GEMM's KS fp32 partial slots, one
-// 256-thread workgroup per flat row r: y = bf16(sum_s part[s][r]) in slot order,
+// 512-thread workgroup per flat row r: y = bf16(sum_s part[s][r]) in slot order,
 // hp[r] = bf16(x[r] + y) (fastdllm_v2_folded.py:207-209), and with zn given, for a
 // recomputed row (slot[r] >= 0), zn[slot[r]] = bf16(w * bf16(hp[r] * rstd))
-// (:211-212).  Thread t takes vectors of 8 t, t + 256, ... (VPT of them); every
-// load of the row (x, the norm weights, up to 4 slots of partials) is in flight
-// at once, so a row costs one memory round trip per 4 slots.  hp stays in
-// registers for the norm; the sum of squares is reduced per wave, then over the
-// 4 waves in wave order.
-constexpr int kPrnThreads = 256;
+// (:211-212).  Thread t takes vectors of 8 t, t + 512, ... (VPT of them: one at
+// D = 3584, against two with 256 threads, which measured ~0.5 us slower per
+// launch); every load of the row (x, the norm weights, up to 4 slots of partials)
+// is in flight at once, so a row costs one memory round trip per 4 slots.  hp
+// stays in registers for the norm; the sum of squares is reduced per wave, then
+// over the 8 waves in wave order.
+constexpr int kPrnThreads = 512;
 template <int VPT>
 __global__ __launch_bounds__(kPrnThreads) void part_residual_norm_kernel(
     const float* __restrict__ part, int ks, size_t stride, const uint16_t* __restrict__ x,
