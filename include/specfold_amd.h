@@ -76,7 +76,8 @@ const char* sf_status_string(int status);
  * 11: attention merges each recomputed row's prefix partials in the kernel that
  *     attends its rows: the workspace holds the range partials only; B1 <= 64.
  * 12: SF_GATE_DEFER_COMPACT and sf_qkv_rope_gated (the compaction in the QKV GEMM).
- * 13: sf_head_logits_rows (the head for the rows a decode step reads). */
+ * 13: sf_head_logits_rows (the head for the rows a decode step reads).
+ * 14: sf_decode_facts; sf_attn_rows / sf_attn_prefix_block take NULL o32, m_tab, z_tab. */
 int sf_abi_version(void);
 
 /*
@@ -426,6 +427,32 @@ int sf_logit_stats_noalloc_max_rows(void);
 int sf_logit_stats_noalloc(const uint16_t* logits, int M, int V, long long ld, float top_p,
                            int32_t* top_idx, float* top_val, float* zfull, float* znuc,
                            int32_t* greedy_tok, float* conf, float* conf_full, void* stream);
+
+/* ---- one decode-loop iteration's decisions and loop facts -----------------------
+ * Replaces, for one sequence, the Fast-dLLM loop's torch sequence after a small
+ * block's sampling (specfold/generate/fastdllm_v2_generation.py:660-700: the
+ * threshold-or-argmax unmask of the small block and its write into the token
+ * state) and the loop's reads of the token state that follow (stop token with no
+ * mask before it, masked counts, draft-cache hit, committed count), in one launch.
+ * x_t: int64 [L] token state (batch one); the block is its last bl tokens and the
+ * tail x_t[plen:] its last L - plen (1 .. bl).  conf (bf16 [sbs], the small
+ * block's probabilities), x_1 (int64 [sbs], its sampled tokens), threshold (the
+ * loop's threshold rounded to bf16, as torch compares a bf16 tensor with it):
+ * with conf given, column k of the small block at block offset s0 is unmasked
+ * when it is masked and conf[k] > threshold or k is the first maximum of conf over
+ * the masked columns; unmask[k] = 1 then, and x_t takes x_1[k].  conf NULL: no
+ * decision, the facts only.  states: n_states (<= 16) device pointers to cached
+ * draft states (int64 [bl] each, host array).  facts (int64, out): [stop, block
+ * masked count, each small block's masked count (bl / sbs of them), the first
+ * state equal to the block or -1 (only when n_states > 0), the unmasked count
+ * (only with conf)] -- the torch form's values exactly.
+ * Limits: 1 <= bl <= 64, bl % sbs == 0, L - bl <= plen < L.  No counterpart in
+ * the reference as a kernel (its loop runs these as separate torch ops).
+ */
+int sf_decode_facts(int64_t* x_t, int L, int plen, int bl, int sbs, int s0, long long mask_id,
+                    long long stop_id, const uint16_t* conf, const int64_t* x_1, float threshold,
+                    const int64_t* const* states, int n_states, int8_t* unmask, int64_t* facts,
+                    void* stream);
 
 #ifdef __cplusplus
 }

@@ -72,6 +72,8 @@ SIGNATURES = {
     "sf_lm_head": (_i, [_vp, _i, _vp, _i, _i, _vp, _vp]),
     "sf_head_logits": (_i, [_vp, _i, _vp, _i, _i, _i, _vp, _ll, _vp]),
     "sf_head_logits_rows": (_i, [_vp, _i, _vp, _i, _i, _i, _i, _i, _i, _vp, _ll, _vp]),
+    "sf_decode_facts": (_i, [_vp, _i, _i, _i, _i, _i, _ll, _ll, _vp, _vp, _f, _vp, _i, _vp, _vp,
+                             _vp]),
     "sf_logit_stats_workspace_bytes": (ctypes.c_size_t, [_i]),
     "sf_parent_map": (_i, [_vp, _i, _i, _vp, _vp, _vp]),
     "sf_logit_stats": (_i, [_vp, _i, _i, _ll, _f] + [_vp] * 7 + [_vp, ctypes.c_size_t, _vp]),
@@ -577,6 +579,32 @@ def head_logits(x, M, w, D, V, logits, shift_n: int = 0, stream=None) -> None:
     st = load().sf_head_logits(_ptr(x), M, _ptr(w), D, V, int(shift_n), _ptr(logits), ld,
                                _stream(stream))
     _check(st, "sf_head_logits")
+
+
+def decode_facts(x_t, plen: int, bl: int, sbs: int, s0: int, mask_id: int, stop_id: int,
+                 conf, x_1, threshold_bf16: float, states, unmask, facts, stream=None) -> int:
+    """sf_decode_facts on the token state x_t (int64 [1, L] or [L], contiguous):
+    with conf (bf16 [sbs]) the small block at block offset s0 is decided and
+    written (x_1 int64 [sbs], unmask int8 [sbs] out), then the loop facts go to
+    facts (int64, at least 4 + bl // sbs).  states: cached draft states (int64
+    [bl] each, contiguous).  Returns the number of facts written."""
+    _need(x_t, "x_t", torch.int64, align=8)
+    L = x_t.numel()
+    _need(facts, "facts", torch.int64, min_numel=4 + bl // sbs, align=8)
+    if conf is not None:
+        _need(conf, "conf", torch.bfloat16, min_numel=sbs, align=2)
+        _need(x_1, "x_1", torch.int64, min_numel=sbs, align=8)
+        _need(unmask, "unmask", torch.int8, min_numel=sbs, align=1)
+    ptrs = (ctypes.c_void_p * max(1, len(states)))()
+    for i, t in enumerate(states):
+        _need(t, "state", torch.int64, min_numel=bl, align=8)
+        ptrs[i] = t.data_ptr()
+    st = load().sf_decode_facts(_ptr(x_t), L, plen, bl, sbs, s0, int(mask_id), int(stop_id),
+                                _ptr(conf), _ptr(x_1), float(threshold_bf16),
+                                ctypes.cast(ptrs, ctypes.c_void_p), len(states), _ptr(unmask),
+                                _ptr(facts), _stream(stream))
+    _check(st, "sf_decode_facts")
+    return 2 + bl // sbs + (1 if states else 0) + (1 if conf is not None else 0)
 
 
 def head_logits_rows(x, M, w, D, V, logits, N: int, shift: bool, row_lo: int, row_n: int,

@@ -272,7 +272,7 @@ __global__ __launch_bounds__(64) void sf_parent_map_kernel(const int64_t* __rest
 
 }  // namespace
 
-extern "C" int sf_abi_version(void) { return 13; }
+extern "C" int sf_abi_version(void) { return 14; }
 
 extern "C" int sf_parent_map(const int64_t* tokens, int B1, int N, int32_t* par, int32_t* counts,
                              void* stream) {

@@ -18,6 +18,7 @@ from typing import Dict, List, Optional, Tuple
 
 import torch
 
+from specfold_amd import _lib
 from specfold_amd.generate import greedy
 
 logger = logging.getLogger(__name__)
@@ -224,13 +225,47 @@ class FastDLLMV2SpeculativeGeneration:
         if unmask is not None:
             parts.append(unmask.sum().reshape(1))
         v = torch.cat([t.to(torch.long) for t in parts]).tolist()
-        n_small = bl // sbs
+        return self._facts_dict(v, bool(called), unmask is not None)
+
+    def _facts_dict(self, v, has_called: bool, has_unmask: bool) -> Dict:
+        n_small = self.block_length // self.small_block_size
         out = {"stop": bool(v[0]), "block_masks": v[1], "small": v[2:2 + n_small]}
         k = 2 + n_small
-        out["hit"] = v[k] if called else -1
-        k += 1 if called else 0
-        out["n"] = v[k] if unmask is not None else None
+        out["hit"] = v[k] if has_called else -1
+        k += 1 if has_called else 0
+        out["n"] = v[k] if has_unmask else None
         return out
+
+    def _decide(self, x_t: torch.Tensor, plen: int, called, s0: int, x_1: torch.Tensor,
+                conf: torch.Tensor, small_mask: torch.Tensor):
+        """The small block's unmask decision (:660-700: a masked position is committed
+        when its probability passes the threshold or it is the most confident one),
+        its write into x_t, and the loop facts after it -> (unmask [1, sbs] bool,
+        facts).  On a GPU token state of one sequence with bf16 probabilities this is
+        one sf_decode_facts launch; otherwise the torch sequence."""
+        bl, sbs = self.block_length, self.small_block_size
+        if (x_t.is_cuda and x_t.shape[0] == 1 and x_t.is_contiguous() and bl <= 64
+                and conf.dtype == torch.bfloat16 and len(called) <= 16):
+            buf = getattr(self, "_facts_buf", None)
+            if buf is None or buf.device != x_t.device:
+                buf = self._facts_buf = torch.empty(64 + 4, dtype=torch.int64, device=x_t.device)
+                # torch compares a bf16 tensor with a float in bf16
+                self._thr_bf16 = float(torch.tensor(self.threshold, dtype=torch.bfloat16))
+            unmask8 = torch.empty(sbs, dtype=torch.int8, device=x_t.device)
+            n = _lib.decode_facts(x_t, plen, bl, sbs, s0, self.mask_id, self.stop_token,
+                                  conf.reshape(-1), x_1.reshape(-1).contiguous(), self._thr_bf16,
+                                  [st for st, _ in called], unmask8, buf)
+            facts = self._facts_dict(buf[:n].tolist(), bool(called), True)
+            return unmask8.view(torch.bool).unsqueeze(0), facts
+        conf = torch.where(small_mask, conf, -torch.inf)
+        # the reference's unmask[arange, argmax] = True, as a compare with the argmax
+        # column (an index_put_ of a host scalar syncs)
+        best = conf.argmax(dim=-1, keepdim=True)
+        cols = torch.arange(conf.shape[-1], device=self.device)
+        unmask = ((conf > self.threshold) | (cols == best)) & small_mask
+        region = x_t[:, x_t.shape[1] - bl + s0: x_t.shape[1] - bl + s0 + sbs]
+        region.copy_(torch.where(unmask, x_1, region))
+        return unmask, self._loop_facts(x_t, plen, called, unmask)
 
     @torch.no_grad()
     def decode_steps(self, prompt_ids: torch.Tensor, defer_forward: bool = False):
@@ -341,15 +376,8 @@ class FastDLLMV2SpeculativeGeneration:
                                     n_masked=facts["small"][sb])
                                 st["drafts_computed"] += len(draft_blocks)
                             kind = "verify"
-                        conf = torch.where(small_mask, conf, -torch.inf)
-                        # the reference's unmask[arange, argmax] = True, as a compare with
-                        # the argmax column (an index_put_ of a host scalar syncs)
-                        best = conf.argmax(dim=-1, keepdim=True)
-                        cols = torch.arange(conf.shape[-1], device=self.device)
-                        unmask = ((conf > self.threshold) | (cols == best)) & small_mask
-                        region = x_t[:, x_t.shape[1] - bl + s0: x_t.shape[1] - bl + s1]
-                        region.copy_(torch.where(unmask, x_1, region))
-                        facts = self._loop_facts(x_t, plen, called, unmask)
+                        unmask, facts = self._decide(x_t, plen, called, s0, x_1, conf,
+                                                     small_mask)
                         n = facts["n"]
                         self.last_commits.append(n)
                         # the decision itself rides along (device tensors, no sync):

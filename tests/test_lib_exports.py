@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_host_side_validation_without_gpu():
     lib = _lib.load()
-    assert lib.sf_abi_version() == 13
+    assert lib.sf_abi_version() == 14
     assert lib.sf_status_string(1).decode() == "shape outside kernel limits"
     # NULL pointers and bad shapes are rejected before any launch
     assert lib.sf_fold_gate(*([None] * 3), 8, 32, 64, 256, 0.1, 1e-6, 0, *([None] * 11)) == 2
@@ -58,6 +58,13 @@ def test_host_side_validation_without_gpu():
     assert lib.sf_logit_stats(fake, 8, 152063, 152064, 0.95, *outs, fake, 1 << 30, None) == 1
     assert lib.sf_logit_stats_workspace_bytes(8) >= 8 * 65536 * 4
     assert lib.sf_parent_map(None, 8, 32, fake, None, None) == 2
+    # the decode step's facts: the tail must lie inside the block (L - bl <= plen < L)
+    assert lib.sf_decode_facts(fake, 64, 64, 32, 8, 0, 1, 2, None, None, 0.9, None, 0, None,
+                               fake, None) == 1
+    assert lib.sf_decode_facts(fake, 64, 40, 65, 5, 0, 1, 2, None, None, 0.9, None, 0, None,
+                               fake, None) == 1
+    assert lib.sf_decode_facts(None, 64, 40, 32, 8, 0, 1, 2, None, None, 0.9, None, 0, None,
+                               fake, None) == 2
     assert lib.sf_parent_map(fake, 65, 32, fake, None, None) == 1
     # attention: the rows kernel stages src in a 1024-entry LDS table and finds a
     # row's branches with one 64-lane ballot, so a bucket or a step beyond 1024 rows,
