@@ -33,6 +33,8 @@ once per step when a bucket below B1*N could overflow.
 
 from __future__ import annotations
 
+import contextlib
+import gc
 import logging
 from dataclasses import dataclass, field
 from typing import Dict, List, Optional, Tuple
@@ -41,6 +43,26 @@ import torch
 
 from specfold_amd import _lib
 from specfold_amd.kv_cache import ContiguousMirror, PagedKVCache, cache_length, prefix_view
+
+
+@contextlib.contextmanager
+def _capturing(graph: "torch.cuda.CUDAGraph"):
+    """torch.cuda.graph(graph) with the garbage collector held off.
+
+    A collection inside the capture may free an unreachable CUDAGraph (an engine
+    dropped in a reference cycle still holds its graphs), and destroying a graph
+    while a stream captures is refused by HIP and aborts the process.  The cycles
+    are collected first, outside the capture."""
+    gc.collect()
+    was = gc.isenabled()
+    gc.disable()
+    try:
+        with torch.cuda.graph(graph):
+            yield
+    finally:
+        if was:
+            gc.enable()
+
 
 logger = logging.getLogger(__name__)
 
@@ -526,7 +548,7 @@ class FoldedVerifyEngine:
                 self._run_layers(buf, static_tok, None, delta, bucket, batch=batch)
             torch.cuda.current_stream().wait_stream(side)
             graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph):
+            with _capturing(graph):
                 out = self._run_layers(buf, static_tok, None, delta, bucket, batch=batch)
             entry = (graph, static_tok, out, batch)
             while len(self._graphs) >= self.max_graphs:
@@ -749,7 +771,7 @@ class FoldedVerifyEngine:
                                  causal=causal)
             torch.cuda.current_stream().wait_stream(side)
             graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph):
+            with _capturing(graph):
                 out = self._run_layers(buf, static_tok, cache, delta, bucket, q_scale=qs,
                                        causal=causal)
             entry = (graph, static_tok, out)
